@@ -1,0 +1,286 @@
+/*
+ * ORACLE ONLY (test infrastructure): CPU restatement of speculative acceptance
+ * sampling, emulating the fp32 reduction order of the GPU kernel exactly, so
+ * accept counts and tokens can be compared bit for bit given identical logits
+ * and uniforms. Must be built with -ffp-contract=off.
+ *
+ * Rule (Leviathan et al. 2023; Chen et al. 2023), generalising the reference's
+ * greedy-draft case (engine/speculative.py:74-81, where q is one-hot):
+ *   z = logits * inv_temp, p = softmax(z_target), q = softmax(z_draft)
+ *   for i < k: accept draft d_i iff u_i * q_i(d_i) < p_i(d_i)
+ *   first rejection at n: token ~ max(0, p_n - q_n); all accepted: token ~ p_k.
+ * Written without division: with e = exp(z - max), S = sum e,
+ *   accept iff u * e_q(d) * S_p < e_p(d) * S_q,
+ *   residual weight w_j = max(0, e_p(j) * S_q - e_q(j) * S_p),
+ *   bonus weight w_j = e_p(j).
+ * One-hot q (no draft logits): e_q = [j == d], S_q = 1.
+ * Greedy (reference sampler.greedy, engine/speculative.py:75-77): accept iff
+ * argmax(target_i) == d_i (first maximal index), token = argmax of row n.
+ *
+ * Reduction order (shared with the kernel): a row is cut into parts of 8192;
+ * in a part, logical thread t (0..255) owns elements
+ *   base + 4*(t + 256*i) + e,  i = 0..7, e = 0..3  (in that order),
+ * summed sequentially; thread sums combine with an xor butterfly over each
+ * 64-lane wave (32,16,8,4,2,1) and then ((w0 + w1) + w2) + w3.
+ * Parts combine as m = max m_p, S = sum_p S_p * exp(m_p - m) left to right.
+ * Inverse-CDF sampling walks the same order: parts, then threads, then elements,
+ * with running fp32 prefix sums; when rounding leaves the walk without a hit, the
+ * last positive weight of the scope is taken.
+ */
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "oracle.h"
+
+#define PART 8192
+#define NT 256
+#define NI 8
+
+/* exp(x): Cody-Waite reduction x = n*ln2 + r (ln2 split hi/lo), Taylor series of
+ * degree 7 for e^r in Horner form with fmaf, scaled by 2^n; 0 below -86. */
+float orc_expf(float x) {
+  if (!(x >= -86.0f)) return 0.0f;
+  if (x > 88.0f) return INFINITY;
+  const float n = rintf(x * 1.44269504f);
+  float r = fmaf(n, -0.693145751953125f, x);
+  r = fmaf(n, -1.428606765330187e-06f, r);
+  float p = 1.0f / 5040.0f;
+  p = fmaf(p, r, 1.0f / 720.0f);
+  p = fmaf(p, r, 1.0f / 120.0f);
+  p = fmaf(p, r, 1.0f / 24.0f);
+  p = fmaf(p, r, 1.0f / 6.0f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int e = (int)n;
+  uint32_t bits = (uint32_t)(e + 127) << 23;
+  float scale;
+  memcpy(&scale, &bits, 4);
+  return p * scale;
+}
+
+static int nparts(int V) { return (V + PART - 1) / PART; }
+
+/* element j of logical thread t, slot s = 4*i + e, in part p; -1 if past V */
+static inline int elem(int V, int p, int t, int s) {
+  const int i = s >> 2, e = s & 3;
+  const int j = p * PART + 4 * (t + NT * i) + e;
+  const int end = (p + 1) * PART < V ? (p + 1) * PART : V;
+  return j < end ? j : -1;
+}
+
+static float block_sum(const float* tsum) {
+  float w[4];
+  for (int wv = 0; wv < 4; ++wv) {
+    float v[64], nv[64];
+    for (int l = 0; l < 64; ++l) v[l] = tsum[wv * 64 + l];
+    for (int o = 32; o >= 1; o >>= 1) {
+      for (int l = 0; l < 64; ++l) nv[l] = v[l] + v[l ^ o];
+      memcpy(v, nv, sizeof(v));
+    }
+    w[wv] = v[0];
+  }
+  return ((w[0] + w[1]) + w[2]) + w[3];
+}
+
+typedef struct { float m, s; } rowstat;
+
+static rowstat row_stats(const float* row, int V, float inv_temp) {
+  const int P = nparts(V);
+  float mp[4096], sp[4096];
+  for (int p = 0; p < P; ++p) {
+    float m = -INFINITY;
+    for (int t = 0; t < NT; ++t)
+      for (int s = 0; s < 4 * NI; ++s) {
+        const int j = elem(V, p, t, s);
+        if (j >= 0) {
+          const float z = row[j] * inv_temp;
+          if (z > m) m = z;
+        }
+      }
+    float ts[NT];
+    for (int t = 0; t < NT; ++t) {
+      float acc = 0.0f;
+      for (int s = 0; s < 4 * NI; ++s) {
+        const int j = elem(V, p, t, s);
+        if (j >= 0) acc = acc + orc_expf(row[j] * inv_temp - m);
+      }
+      ts[t] = acc;
+    }
+    mp[p] = m;
+    sp[p] = block_sum(ts);
+  }
+  rowstat r;
+  float m = -INFINITY;
+  for (int p = 0; p < P; ++p)
+    if (mp[p] > m) m = mp[p];
+  float s = 0.0f;
+  for (int p = 0; p < P; ++p) s = s + sp[p] * orc_expf(mp[p] - m);
+  r.m = m;
+  r.s = s;
+  return r;
+}
+
+/* first index of the maximum of row (greedy) */
+static int row_argmax(const float* row, int V) {
+  int bj = 0;
+  float bv = row[0];
+  for (int j = 1; j < V; ++j)
+    if (row[j] > bv) {
+      bv = row[j];
+      bj = j;
+    }
+  return bj;
+}
+
+/* sampling weight of element j */
+typedef struct {
+  const float* tp; /* target row */
+  const float* tq; /* draft row or NULL */
+  int d;           /* draft id (one-hot q when tq == NULL) */
+  int mode;        /* 0 = residual, 1 = plain p */
+  float inv_temp;
+  rowstat sp, sq;
+} wctx;
+
+static inline float weight(const wctx* c, int j) {
+  const float ep = orc_expf(c->tp[j] * c->inv_temp - c->sp.m);
+  if (c->mode == 1) return ep;
+  float eq, Sq;
+  if (c->tq) {
+    eq = orc_expf(c->tq[j] * c->inv_temp - c->sq.m);
+    Sq = c->sq.s;
+  } else {
+    eq = (j == c->d) ? 1.0f : 0.0f;
+    Sq = 1.0f;
+  }
+  const float r = ep * Sq - eq * c->sp.s;
+  return r > 0.0f ? r : 0.0f;
+}
+
+static int sample(const wctx* c, int V, float u) {
+  const int P = nparts(V);
+  float* T = (float*)malloc(sizeof(float) * (size_t)P * NT);
+  float* Wp = (float*)malloc(sizeof(float) * (size_t)P);
+  for (int p = 0; p < P; ++p) {
+    for (int t = 0; t < NT; ++t) {
+      float acc = 0.0f;
+      for (int s = 0; s < 4 * NI; ++s) {
+        const int j = elem(V, p, t, s);
+        if (j >= 0) acc = acc + weight(c, j);
+      }
+      T[(size_t)p * NT + t] = acc;
+    }
+    Wp[p] = block_sum(T + (size_t)p * NT);
+  }
+  float W = 0.0f;
+  for (int p = 0; p < P; ++p) W = W + Wp[p];
+  int result = -1;
+  if (W > 0.0f) {
+    const float th = u * W;
+    float cacc = 0.0f;
+    int ps = -1;
+    for (int p = 0; p < P; ++p) {
+      const float nx = cacc + Wp[p];
+      if (nx > th) { ps = p; break; }
+      cacc = nx;
+    }
+    int fallback = 0;
+    if (ps < 0) {
+      for (int p = P - 1; p >= 0; --p)
+        if (Wp[p] > 0.0f) { ps = p; break; }
+      fallback = 1;
+    }
+    int ts = -1;
+    if (!fallback) {
+      for (int t = 0; t < NT; ++t) {
+        const float nx = cacc + T[(size_t)ps * NT + t];
+        if (nx > th) { ts = t; break; }
+        cacc = nx;
+      }
+    }
+    if (ts < 0) {
+      for (int t = NT - 1; t >= 0; --t)
+        if (T[(size_t)ps * NT + t] > 0.0f) { ts = t; break; }
+      fallback = 1;
+    }
+    if (!fallback) {
+      for (int s = 0; s < 4 * NI; ++s) {
+        const int j = elem(V, ps, ts, s);
+        if (j < 0) break;
+        cacc = cacc + weight(c, j);
+        if (cacc > th) { result = j; break; }
+      }
+    }
+    if (result < 0) {
+      for (int s = 4 * NI - 1; s >= 0; --s) {
+        const int j = elem(V, ps, ts, s);
+        if (j >= 0 && weight(c, j) > 0.0f) { result = j; break; }
+      }
+    }
+  }
+  free(T);
+  free(Wp);
+  return result;
+}
+
+void orc_spec_accept(const float* target, const float* draft, const int32_t* draft_ids,
+                     const float* u_accept, const float* u_sample, float inv_temp,
+                     int32_t* n_accept, int32_t* out_token, int S, int k, int V, int threads) {
+  const int greedy = !(inv_temp > 0.0f);
+#pragma omp parallel for schedule(dynamic) num_threads(threads > 0 ? threads : 1)
+  for (int st = 0; st < S; ++st) {
+    const float* tgt = target + (size_t)st * (k + 1) * V;
+    const float* drf = draft ? draft + (size_t)st * k * V : NULL;
+    const int32_t* d = draft_ids + (size_t)st * k;
+    int n = k, tok = -1;
+    if (greedy) {
+      for (int i = 0; i < k; ++i) {
+        const int am = row_argmax(tgt + (size_t)i * V, V);
+        if (am != d[i]) { n = i; tok = am; break; }
+      }
+      if (n == k) tok = row_argmax(tgt + (size_t)k * V, V);
+    } else {
+      rowstat rp[64], rq[64];
+      for (int i = 0; i <= k; ++i) rp[i] = row_stats(tgt + (size_t)i * V, V, inv_temp);
+      if (drf)
+        for (int i = 0; i < k; ++i) rq[i] = row_stats(drf + (size_t)i * V, V, inv_temp);
+      for (int i = 0; i < k; ++i) {
+        const int di = d[i];
+        const float ep = orc_expf(tgt[(size_t)i * V + di] * inv_temp - rp[i].m);
+        float eq = 1.0f, Sq = 1.0f;
+        if (drf) {
+          eq = orc_expf(drf[(size_t)i * V + di] * inv_temp - rq[i].m);
+          Sq = rq[i].s;
+        }
+        const float lhs = u_accept[(size_t)st * k + i] * eq * rp[i].s;
+        const float rhs = ep * Sq;
+        if (!(lhs < rhs)) { n = i; break; }
+      }
+      wctx c;
+      c.inv_temp = inv_temp;
+      c.sp = rp[n];
+      if (n < k) {
+        c.tp = tgt + (size_t)n * V;
+        c.tq = drf ? drf + (size_t)n * V : NULL;
+        c.d = d[n];
+        c.mode = 0;
+        if (drf) c.sq = rq[n];
+        tok = sample(&c, V, u_sample[st]);
+        if (tok < 0) { /* residual vanished in fp32: fall back to p_n */
+          c.mode = 1;
+          tok = sample(&c, V, u_sample[st]);
+        }
+      } else {
+        c.tp = tgt + (size_t)k * V;
+        c.tq = NULL;
+        c.d = -1;
+        c.mode = 1;
+        tok = sample(&c, V, u_sample[st]);
+      }
+    }
+    n_accept[st] = n;
+    out_token[st] = tok;
+  }
+}

@@ -1,0 +1,108 @@
+// Shared device/host helpers for the qvex HIP kernels (gfx950, wave64).
+//
+// bf16 values cross the C ABI as raw uint16_t bit patterns; kernels widen them
+// to fp32 with a shift and narrow with round-to-nearest-even.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+#include "../../include/qvex.h"
+
+#define QVEX_WAVE 64
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (nontemporal: the data is used once).
+__device__ __forceinline__ u32x4 load_nt16(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// ---------------------------------------------------------------- bf16
+
+__device__ __forceinline__ float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+// fp32 -> bf16, round to nearest even; NaN stays NaN (quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+// ---------------------------------------------------------------- wave reductions (DPP)
+//
+// Sum over the 64 lanes of a wave. Row (16-lane) sums use row_shr, then
+// row_bcast15/31 carry partials across rows; the full sum lands in lane 63.
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf, bool BOUND_CTRL = false>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, BANK_MASK, BOUND_CTRL));
+}
+
+// DPP control codes (GCN3+ encoding).
+#define DPP_ROW_SHR(n) (0x110 + (n))
+#define DPP_ROW_BCAST15 0x142
+#define DPP_ROW_BCAST31 0x143
+
+// After this, lane 63 holds the wave total (other lanes hold partials).
+__device__ __forceinline__ float wave_sum_to_lane63(float v) {
+  v += dpp_f<DPP_ROW_SHR(1), 0xf, 0xf, true>(v);   // bound_ctrl: out-of-row source reads 0
+  v += dpp_f<DPP_ROW_SHR(2), 0xf, 0xf, true>(v);
+  v += dpp_f<DPP_ROW_SHR(4), 0xf, 0xf, true>(v);
+  v += dpp_f<DPP_ROW_SHR(8), 0xf, 0xf, true>(v);
+  v += dpp_f<DPP_ROW_BCAST15, 0xa, 0xf, false>(v);  // rows 1,3 get lane 15 of rows 0,2
+  v += dpp_f<DPP_ROW_BCAST31, 0xc, 0xf, false>(v);  // rows 2,3 get lane 31
+  return v;
+}
+
+// Sum broadcast to every lane, via xor butterflies (ds_swizzle / bpermute).
+__device__ __forceinline__ float wave_allsum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_allmax(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// ---------------------------------------------------------------- host-side error plumbing
+
+namespace qvex {
+
+void set_error(const char* fmt, ...);
+int fail(int code, const char* fmt, ...);
+
+}  // namespace qvex
+
+#define QVEX_CHECK_ARG(cond, ...)                                  \
+  do {                                                             \
+    if (!(cond)) return qvex::fail(QVEX_EINVAL, __VA_ARGS__);      \
+  } while (0)
+
+#define QVEX_CHECK_LAUNCH(name)                                                      \
+  do {                                                                               \
+    hipError_t _e = hipGetLastError();                                               \
+    if (_e != hipSuccess)                                                            \
+      return qvex::fail(QVEX_EHIP, "%s: launch failed: %s", name, hipGetErrorString(_e)); \
+  } while (0)
+
+#define QVEX_HIP(call, name)                                                         \
+  do {                                                                               \
+    hipError_t _e = (call);                                                          \
+    if (_e != hipSuccess)                                                            \
+      return qvex::fail(QVEX_EHIP, "%s: %s", name, hipGetErrorString(_e));           \
+  } while (0)
+
+static inline bool qvex_aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }

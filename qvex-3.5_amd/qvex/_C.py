@@ -1,0 +1,63 @@
+"""ctypes binding of libqvex.so (the C ABI declared in include/qvex.h).
+
+The library is loaded from this directory; there is no fallback: every op of
+the package raises if the HIP library is missing or fails.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libqvex.so"
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+U64 = ctypes.c_uint64
+F = ctypes.c_float
+
+# name -> argtypes (all return int status)
+SIGNATURES: dict[str, list] = {
+    "qvex_qmv_w4g64": [P, P, P, P, P, I, I, I, P],
+    "qvex_qmv_w4g64_tiled": [P, P, P, P, P, I, I, I, I, I, P],
+    "qvex_read_roof": [P, U64, P, I, P],
+    "qvex_gdn_recurrent": [P, P, P, P, P, P, P, P, P, I, P, I, I, I, I, I, I, P],
+    "qvex_gdn_recurrent_ring": [P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, I, I, P],
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+class QvexError(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise QvexError(f"{LIB_PATH} is not built: run `python -m qvex.build` "
+                            "(or __graft_entry__.build()) first")
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.qvex_last_error.restype = ctypes.c_char_p
+        L.qvex_last_error.argtypes = []
+        L.qvex_abi_version.restype = I
+        L.qvex_abi_version.argtypes = []
+        for name, args in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = I
+        _lib = L
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point and raise QvexError with the library's message on failure."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        msg = lib().qvex_last_error().decode(errors="replace")
+        raise QvexError(f"{name} failed (status {rc}): {msg}")
+
+
+def exported_symbols() -> list[str]:
+    return ["qvex_last_error", "qvex_abi_version", *SIGNATURES]

@@ -1,0 +1,61 @@
+"""The C ABI library loads, exports every declared symbol, and rejects bad
+arguments on the host before any GPU work (CPU only)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from qvex import _C
+
+REPO = Path(__file__).resolve().parent.parent
+
+
+def declared_symbols():
+    names = []
+    for h in sorted((REPO / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names += re.findall(r"\b(qvex_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_header_declares_symbols():
+    assert "qvex_qmv_w4g64" in declared_symbols()
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _C.lib()
+    missing = [n for n in declared_symbols() if not hasattr(lib, n)]
+    assert not missing, f"libqvex.so lacks {missing}"
+
+
+def test_bindings_cover_header():
+    assert set(declared_symbols()) <= set(_C.exported_symbols())
+
+
+def test_abi_version():
+    assert _C.lib().qvex_abi_version() >= 1
+
+
+@pytest.mark.parametrize("M,N,K", [(0, 16, 64), (9, 16, 64), (1, 0, 64), (1, 16, 96), (1, 16, 0)])
+def test_qmv_rejects_bad_shapes(M, N, K):
+    buf = ctypes.create_string_buffer(1 << 16)
+    p = ctypes.addressof(buf)
+    p16 = (p + 15) // 16 * 16
+    with pytest.raises(_C.QvexError, match="qvex_qmv_w4g64"):
+        _C.call("qvex_qmv_w4g64", p16, p16, p16, p16, p16, M, N, K, None)
+
+
+def test_qmv_rejects_misaligned_pointer():
+    buf = ctypes.create_string_buffer(1 << 12)
+    p16 = (ctypes.addressof(buf) + 15) // 16 * 16
+    with pytest.raises(_C.QvexError, match="16-byte"):
+        _C.call("qvex_qmv_w4g64", p16 + 2, p16, p16, p16, p16, 1, 16, 64, None)
+
+
+def test_qmv_rejects_unknown_tile():
+    buf = ctypes.create_string_buffer(1 << 12)
+    p16 = (ctypes.addressof(buf) + 15) // 16 * 16
+    with pytest.raises(_C.QvexError, match="tile"):
+        _C.call("qvex_qmv_w4g64_tiled", p16, p16, p16, p16, p16, 1, 16, 64, 3, 1, None)
