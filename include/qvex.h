@@ -99,6 +99,32 @@ int qvex_gdn_recurrent_ring(const uint16_t* q, const uint16_t* k, const uint16_t
                             const int32_t* cur_slot, uint16_t* y, int B, int T, int Hk,
                             int Hv, int Dk, int Dv, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Fused speculative acceptance sampling for S independent verify steps.
+ *
+ * target: fp32 [S, k+1, V] logits of the verify rows; draft: fp32 [S, k, V]
+ * logits of the draft distribution, or NULL when the drafts are greedy (q is
+ * one-hot at the draft id); draft_ids: int32 [S, k]; u_accept: fp32 [S, k];
+ * u_sample: fp32 [S]; inv_temp = 1/temperature (<= 0 selects greedy: accept iff
+ * argmax matches, token = argmax). With z = logits * inv_temp, p = softmax(z):
+ *   accept d_i iff u_i * q_i(d_i) < p_i(d_i)  (evaluated division-free);
+ *   n_accept[s] = index of the first rejection (k if none);
+ *   out_token[s] ~ max(0, p_n - q_n) at the first rejection, else ~ p_k.
+ * The reduction order is fixed (see csrc/spec.hip), so results are
+ * reproducible bit for bit given identical logits and uniforms. Requires
+ * V % 4 == 0, V <= 1,179,648, k <= 32; workspace of
+ * qvex_spec_accept_workspace_bytes(S, k, V, draft != NULL) bytes.
+ *
+ * Replaces the accept/resample/bonus block of decode()
+ * (engine/speculative.py:74-81) with Sampler.scores/pick at temperature only
+ * (engine/sampler.py:30-58; top-k/top-p filtering is not applied).
+ * ------------------------------------------------------------------------ */
+uint64_t qvex_spec_accept_workspace_bytes(int S, int k, int V, int has_draft);
+int qvex_spec_accept(const float* target, const float* draft, const int32_t* draft_ids,
+                     const float* u_accept, const float* u_sample, float inv_temp,
+                     int32_t* n_accept, int32_t* out_token, int S, int k, int V,
+                     void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* Pure streaming read of `bytes` bytes (multiple of 16) from `buf`, folding
  * them into `sink` (64 uint32 words). Measures the achievable HBM read rate;
  * the counterpart of read_roof (experiments/native/qmv_spike.mm:21-32). */

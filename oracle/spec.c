@@ -13,7 +13,8 @@
  *   accept iff u * e_q(d) * S_p < e_p(d) * S_q,
  *   residual weight w_j = max(0, e_p(j) * S_q - e_q(j) * S_p),
  *   bonus weight w_j = e_p(j).
- * One-hot q (no draft logits): e_q = [j == d], S_q = 1.
+ * One-hot q (no draft logits): e_q = [j == d], S_q = 1. A draft id outside
+ * [0, V) is rejected. NaN logits are not supported.
  * Greedy (reference sampler.greedy, engine/speculative.py:75-77): accept iff
  * argmax(target_i) == d_i (first maximal index), token = argmax of row n.
  *
@@ -38,9 +39,10 @@
 #define NI 8
 
 /* exp(x): Cody-Waite reduction x = n*ln2 + r (ln2 split hi/lo), Taylor series of
- * degree 7 for e^r in Horner form with fmaf, scaled by 2^n; 0 below -86. */
+ * degree 7 for e^r in Horner form with fmaf, scaled by 2^n; 0 below -69 (keeps
+ * every product formed with it in the normal range). */
 float orc_expf(float x) {
-  if (!(x >= -86.0f)) return 0.0f;
+  if (!(x >= -69.0f)) return 0.0f;
   if (x > 88.0f) return INFINITY;
   const float n = rintf(x * 1.44269504f);
   float r = fmaf(n, -0.693145751953125f, x);
@@ -70,6 +72,9 @@ static inline int elem(int V, int p, int t, int s) {
   return j < end ? j : -1;
 }
 
+/* first element of logical thread t in part p is past the end: the thread owns nothing */
+static inline int thread_empty(int V, int p, int t) { return elem(V, p, t, 0) < 0; }
+
 static float block_sum(const float* tsum) {
   float w[4];
   for (int wv = 0; wv < 4; ++wv) {
@@ -91,21 +96,20 @@ static rowstat row_stats(const float* row, int V, float inv_temp) {
   float mp[4096], sp[4096];
   for (int p = 0; p < P; ++p) {
     float m = -INFINITY;
-    for (int t = 0; t < NT; ++t)
-      for (int s = 0; s < 4 * NI; ++s) {
-        const int j = elem(V, p, t, s);
-        if (j >= 0) {
-          const float z = row[j] * inv_temp;
-          if (z > m) m = z;
-        }
-      }
+    const int b0 = p * PART, e0 = (p + 1) * PART < V ? (p + 1) * PART : V;
+    for (int j = b0; j < e0; ++j) {
+      const float z = row[j] * inv_temp;
+      if (z > m) m = z;
+    }
     float ts[NT];
     for (int t = 0; t < NT; ++t) {
       float acc = 0.0f;
-      for (int s = 0; s < 4 * NI; ++s) {
-        const int j = elem(V, p, t, s);
-        if (j >= 0) acc = acc + orc_expf(row[j] * inv_temp - m);
-      }
+      if (!thread_empty(V, p, t))
+        for (int s = 0; s < 4 * NI; ++s) {
+          const int j = elem(V, p, t, s);
+          if (j < 0) break;
+          acc = acc + orc_expf(row[j] * inv_temp - m);
+        }
       ts[t] = acc;
     }
     mp[p] = m;
@@ -166,10 +170,12 @@ static int sample(const wctx* c, int V, float u) {
   for (int p = 0; p < P; ++p) {
     for (int t = 0; t < NT; ++t) {
       float acc = 0.0f;
-      for (int s = 0; s < 4 * NI; ++s) {
-        const int j = elem(V, p, t, s);
-        if (j >= 0) acc = acc + weight(c, j);
-      }
+      if (!thread_empty(V, p, t))
+        for (int s = 0; s < 4 * NI; ++s) {
+          const int j = elem(V, p, t, s);
+          if (j < 0) break;
+          acc = acc + weight(c, j);
+        }
       T[(size_t)p * NT + t] = acc;
     }
     Wp[p] = block_sum(T + (size_t)p * NT);
@@ -248,6 +254,7 @@ void orc_spec_accept(const float* target, const float* draft, const int32_t* dra
         for (int i = 0; i < k; ++i) rq[i] = row_stats(drf + (size_t)i * V, V, inv_temp);
       for (int i = 0; i < k; ++i) {
         const int di = d[i];
+        if (di < 0 || di >= V) { n = i; break; } /* an out-of-range draft is rejected */
         const float ep = orc_expf(tgt[(size_t)i * V + di] * inv_temp - rp[i].m);
         float eq = 1.0f, Sq = 1.0f;
         if (drf) {

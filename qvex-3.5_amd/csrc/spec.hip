@@ -1,0 +1,416 @@
+// Fused speculative acceptance sampling over the vocabulary.
+//
+// Reference: engine/speculative.py:74-81 (greedy draft: accept iff U < p(draft),
+// resample from p with the draft masked; bonus from the last row) and
+// engine/sampler.py:30-58 (temperature softmax, argmax when greedy). Generalised
+// to k drafts sampled from a draft distribution q (Leviathan et al. 2023; Chen et
+// al. 2023): accept d_i iff u_i * q_i(d_i) < p_i(d_i); at the first rejection n
+// sample from max(0, p_n - q_n); if all k pass, sample the bonus from p_k.
+// Without draft logits q is one-hot at d_i, which is the reference's rule.
+//
+// Division-free form, with e = exp(z - max), S = sum(e), z = logits * inv_temp:
+//   accept iff (u * e_q(d)) * S_p < e_p(d) * S_q
+//   residual weight w_j = max(0, e_p(j) * S_q - e_q(j) * S_p);  bonus w_j = e_p(j)
+// Every value is fp32 and the reduction order is fixed, so a CPU emulation
+// reproduces accept counts and tokens bit for bit (this unit is built with
+// -ffp-contract=off):
+//   * a row is cut into parts of 8192; thread t of a 256-thread block owns the
+//     elements base + 4*(t + 256*i) + e (i = 0..7, e = 0..3), summed in that order;
+//   * thread sums combine by an xor butterfly (32..1) per wave, then
+//     ((w0 + w1) + w2) + w3 over the 4 waves;
+//   * parts combine as m = max m_p, S = sum_p S_p * exp(m_p - m), left to right;
+//   * inverse-CDF sampling walks parts, then threads, then elements with running
+//     fp32 prefix sums; if rounding leaves the walk without a hit, the last
+//     positive weight of the scope is taken.
+//
+// Kernel 1 (grid parts x rows) makes one pass over every logit row of every step
+// and leaves (m_p, S_p) per part: the single HBM pass over (2k+1) x V floats.
+// Kernel 2 (one block per step) combines parts, runs the k accept tests on
+// gathered elements, and makes the one sampling pass over the row(s) it needs.
+#include "qvex_common.h"
+
+namespace {
+
+constexpr int PART = 8192;
+constexpr int NT = 256;
+constexpr int NI = 8;   // float4 loads per thread per part
+
+// exp(x): Cody-Waite reduction x = n*ln2 + r with ln2 split in hi/lo parts,
+// degree-7 Taylor polynomial for e^r (|r| <= ln2/2) in Horner form with fmaf,
+// scaled by 2^n built in the exponent field. Returns 0 below -69 so every
+// product formed with it stays in the normal range.
+__device__ __forceinline__ float qx_expf(float x) {
+  if (!(x >= -69.0f)) return 0.0f;
+  if (x > 88.0f) return __builtin_inff();
+  const float n = rintf(x * 1.44269504f);
+  float r = fmaf(n, -0.693145751953125f, x);
+  r = fmaf(n, -1.428606765330187e-06f, r);
+  float p = 1.0f / 5040.0f;
+  p = fmaf(p, r, 1.0f / 720.0f);
+  p = fmaf(p, r, 1.0f / 120.0f);
+  p = fmaf(p, r, 1.0f / 24.0f);
+  p = fmaf(p, r, 1.0f / 6.0f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const int e = (int)n;
+  return p * __uint_as_float((uint32_t)(e + 127) << 23);
+}
+
+__device__ __forceinline__ float wave_bfly_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = v + __shfl_xor(v, o, 64);
+  return v;
+}
+
+// ((w0 + w1) + w2) + w3 of the four wave sums; result valid in every thread.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_bfly_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_allmax(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+struct SpecArgs {
+  const float* target;    // [S, k+1, V]
+  const float* draft;     // [S, k, V] or nullptr
+  const int32_t* ids;     // [S, k]
+  const float* u_acc;     // [S, k]
+  const float* u_smp;     // [S]
+  float inv_temp;
+  int greedy;
+  int32_t* n_accept;      // [S]
+  int32_t* out_token;     // [S]
+  float* ws;              // [S * rps, P, 2]
+  int S, k, V, P, rps;    // rps = rows per step
+};
+
+__device__ __forceinline__ const float* row_ptr(const SpecArgs& a, int step, int i) {
+  if (i <= a.k) return a.target + ((long)step * (a.k + 1) + i) * a.V;
+  return a.draft + ((long)step * a.k + (i - a.k - 1)) * a.V;
+}
+
+// ---------------------------------------------------------------- kernel 1: part statistics
+
+__global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
+  __shared__ float red[4];
+  __shared__ int redi[4];
+  const int p = blockIdx.x;
+  const int row = blockIdx.y;
+  const int step = row / a.rps, i = row % a.rps;
+  const float* src = row_ptr(a, step, i);
+  const int base = p * PART;
+  const int end = min(a.V, base + PART);
+  const int t = threadIdx.x;
+
+  float x[NI][4];
+  bool ok[NI];
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const int j = base + 4 * (t + NT * it);
+    ok[it] = j < end;
+    if (ok[it]) {
+      const u32x4 v = load_nt16(src + j);
+      x[it][0] = __uint_as_float(v.x);
+      x[it][1] = __uint_as_float(v.y);
+      x[it][2] = __uint_as_float(v.z);
+      x[it][3] = __uint_as_float(v.w);
+    }
+  }
+  float* out = a.ws + ((long)row * a.P + p) * 2;
+  if (a.greedy) {
+    // first index of the maximum raw logit within the part
+    float bv = -__builtin_inff();
+    int bj = 0x7fffffff;
+#pragma unroll
+    for (int it = 0; it < NI; ++it)
+      if (ok[it]) {
+        const int j = base + 4 * (t + NT * it);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (x[it][e] > bv || (x[it][e] == bv && j + e < bj)) { bv = x[it][e]; bj = j + e; }
+      }
+    const float m = block_max(bv, red);
+    int cand = (bv == m) ? bj : 0x7fffffff;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) cand = min(cand, __shfl_xor(cand, o, 64));
+    __syncthreads();
+    if ((t & 63) == 0) redi[t >> 6] = cand;
+    __syncthreads();
+    if (t == 0) {
+      out[0] = m;
+      out[1] = __int_as_float(min(min(redi[0], redi[1]), min(redi[2], redi[3])));
+    }
+    return;
+  }
+  float z[NI][4];
+#pragma unroll
+  for (int it = 0; it < NI; ++it)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) z[it][e] = x[it][e] * a.inv_temp;
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int it = 0; it < NI; ++it)
+    if (ok[it]) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) m = fmaxf(m, z[it][e]);
+    }
+  m = block_max(m, red);
+  float acc = 0.0f;
+#pragma unroll
+  for (int it = 0; it < NI; ++it)
+    if (ok[it]) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = acc + qx_expf(z[it][e] - m);
+    }
+  const float s = block_sum(acc, red);
+  if (t == 0) {
+    out[0] = m;
+    out[1] = s;
+  }
+}
+
+// ---------------------------------------------------------------- kernel 2: accept + sample
+
+struct WCtx {
+  const float* tp;
+  const float* tq;
+  int d;
+  int mode;   // 0 residual, 1 plain p
+  float inv_temp, mp, sp, mq, sq;
+};
+
+__device__ __forceinline__ float weight(const WCtx& c, int j) {
+  const float ep = qx_expf(c.tp[j] * c.inv_temp - c.mp);
+  if (c.mode == 1) return ep;
+  float eq, Sq;
+  if (c.tq) {
+    eq = qx_expf(c.tq[j] * c.inv_temp - c.mq);
+    Sq = c.sq;
+  } else {
+    eq = (j == c.d) ? 1.0f : 0.0f;
+    Sq = 1.0f;
+  }
+  const float t1 = ep * Sq;
+  const float t2 = eq * c.sp;
+  const float r = t1 - t2;
+  return r > 0.0f ? r : 0.0f;
+}
+
+// Inverse-CDF draw over the fixed order; returns -1 when every weight is 0.
+__device__ int sample_pass(const WCtx& c, int V, int P, float u, float* Tpt, float* Wp, float* red) {
+  const int t = threadIdx.x;
+  for (int p = 0; p < P; ++p) {
+    const int base = p * PART, end = min(V, base + PART);
+    float acc = 0.0f;
+#pragma unroll
+    for (int it = 0; it < NI; ++it) {
+      const int j = base + 4 * (t + NT * it);
+      if (j < end) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = acc + weight(c, j + e);
+      }
+    }
+    Tpt[p * NT + t] = acc;
+    const float w = block_sum(acc, red);
+    if (t == 0) Wp[p] = w;
+  }
+  __syncthreads();
+  __shared__ int result;
+  if (t == 0) {
+    float W = 0.0f;
+    for (int p = 0; p < P; ++p) W = W + Wp[p];
+    int res = -1;
+    if (W > 0.0f) {
+      const float th = u * W;
+      float cacc = 0.0f;
+      int ps = -1;
+      for (int p = 0; p < P; ++p) {
+        const float nx = cacc + Wp[p];
+        if (nx > th) { ps = p; break; }
+        cacc = nx;
+      }
+      bool fallback = false;
+      if (ps < 0) {
+        for (int p = P - 1; p >= 0; --p)
+          if (Wp[p] > 0.0f) { ps = p; break; }
+        fallback = true;
+      }
+      int ts = -1;
+      if (!fallback) {
+        for (int tt = 0; tt < NT; ++tt) {
+          const float nx = cacc + Tpt[ps * NT + tt];
+          if (nx > th) { ts = tt; break; }
+          cacc = nx;
+        }
+      }
+      if (ts < 0) {
+        for (int tt = NT - 1; tt >= 0; --tt)
+          if (Tpt[ps * NT + tt] > 0.0f) { ts = tt; break; }
+        fallback = true;
+      }
+      const int base = ps * PART, end = min(V, base + PART);
+      if (!fallback) {
+        for (int s = 0; s < 4 * NI; ++s) {
+          const int j = base + 4 * (ts + NT * (s >> 2)) + (s & 3);
+          if (j >= end) break;
+          cacc = cacc + weight(c, j);
+          if (cacc > th) { res = j; break; }
+        }
+      }
+      if (res < 0) {
+        for (int s = 4 * NI - 1; s >= 0; --s) {
+          const int j = base + 4 * (ts + NT * (s >> 2)) + (s & 3);
+          if (j < end && weight(c, j) > 0.0f) { res = j; break; }
+        }
+      }
+    }
+    result = res;
+  }
+  __syncthreads();
+  return result;
+}
+
+__global__ __launch_bounds__(NT) void spec_accept_kernel(SpecArgs a) {
+  extern __shared__ float smem[];
+  float* Tpt = smem;                       // [P][NT]
+  float* Wp = smem + a.P * NT;             // [P]
+  float* rm = Wp + a.P;                    // [rps] row max (or argmax as int bits)
+  float* rs = rm + a.rps;                  // [rps] row sum
+  __shared__ float red[4];
+  __shared__ int s_n, s_tok;
+  const int step = blockIdx.x;
+  const int t = threadIdx.x;
+  const int k = a.k;
+
+  if (t < a.rps) {
+    const float* w = a.ws + ((long)step * a.rps + t) * a.P * 2;
+    if (a.greedy) {
+      float bv = w[0];
+      int bj = __float_as_int(w[1]);
+      for (int p = 1; p < a.P; ++p)
+        if (w[2 * p] > bv) { bv = w[2 * p]; bj = __float_as_int(w[2 * p + 1]); }
+      rm[t] = __int_as_float(bj);
+    } else {
+      float m = -__builtin_inff();
+      for (int p = 0; p < a.P; ++p) m = fmaxf(m, w[2 * p]);
+      float s = 0.0f;
+      for (int p = 0; p < a.P; ++p) s = s + w[2 * p + 1] * qx_expf(w[2 * p] - m);
+      rm[t] = m;
+      rs[t] = s;
+    }
+  }
+  __syncthreads();
+  if (t == 0) {
+    const int32_t* d = a.ids + (long)step * k;
+    int n = k, tok = -1;
+    if (a.greedy) {
+      for (int i = 0; i < k; ++i) {
+        const int am = __float_as_int(rm[i]);
+        if (am != d[i]) { n = i; tok = am; break; }
+      }
+      if (n == k) tok = __float_as_int(rm[k]);
+    } else {
+      for (int i = 0; i < k; ++i) {
+        const int di = d[i];
+        if (di < 0 || di >= a.V) { n = i; break; }
+        const float ep = qx_expf(row_ptr(a, step, i)[di] * a.inv_temp - rm[i]);
+        float eq = 1.0f, Sq = 1.0f;
+        if (a.draft) {
+          eq = qx_expf(row_ptr(a, step, k + 1 + i)[di] * a.inv_temp - rm[k + 1 + i]);
+          Sq = rs[k + 1 + i];
+        }
+        const float lhs = a.u_acc[(long)step * k + i] * eq * rs[i];
+        const float rhs = ep * Sq;
+        if (!(lhs < rhs)) { n = i; break; }
+      }
+    }
+    s_n = n;
+    s_tok = tok;
+  }
+  __syncthreads();
+  const int n = s_n;
+  int tok = s_tok;
+  if (!a.greedy) {
+    WCtx c;
+    c.inv_temp = a.inv_temp;
+    c.tp = row_ptr(a, step, n);
+    c.mp = rm[n];
+    c.sp = rs[n];
+    const float u = a.u_smp[step];
+    if (n < k) {
+      c.tq = a.draft ? row_ptr(a, step, k + 1 + n) : nullptr;
+      c.d = a.ids[(long)step * k + n];
+      c.mode = 0;
+      c.mq = a.draft ? rm[k + 1 + n] : 0.0f;
+      c.sq = a.draft ? rs[k + 1 + n] : 1.0f;
+      tok = sample_pass(c, a.V, a.P, u, Tpt, Wp, red);
+      if (tok < 0) {
+        c.mode = 1;
+        tok = sample_pass(c, a.V, a.P, u, Tpt, Wp, red);
+      }
+    } else {
+      c.tq = nullptr;
+      c.d = -1;
+      c.mode = 1;
+      c.mq = 0.0f;
+      c.sq = 1.0f;
+      tok = sample_pass(c, a.V, a.P, u, Tpt, Wp, red);
+    }
+  }
+  if (t == 0) {
+    a.n_accept[step] = n;
+    a.out_token[step] = tok;
+  }
+}
+
+int nparts(int V) { return (V + PART - 1) / PART; }
+
+}  // namespace
+
+extern "C" uint64_t qvex_spec_accept_workspace_bytes(int S, int k, int V, int has_draft) {
+  if (S < 1 || k < 0 || V < 1) return 0;
+  const int rps = (k + 1) + (has_draft ? k : 0);
+  return (uint64_t)S * rps * nparts(V) * 2 * sizeof(float);
+}
+
+extern "C" int qvex_spec_accept(const float* target, const float* draft, const int32_t* draft_ids,
+                                const float* u_accept, const float* u_sample, float inv_temp,
+                                int32_t* n_accept, int32_t* out_token, int S, int k, int V,
+                                void* workspace, uint64_t workspace_bytes, void* stream) {
+  QVEX_CHECK_ARG(S >= 1 && k >= 0 && k <= 32, "qvex_spec_accept: S=%d k=%d (need S >= 1, 0 <= k <= 32)", S, k);
+  QVEX_CHECK_ARG(V >= 4 && V % 4 == 0, "qvex_spec_accept: V=%d must be a positive multiple of 4", V);
+  QVEX_CHECK_ARG(target && n_accept && out_token && workspace, "qvex_spec_accept: null pointer");
+  QVEX_CHECK_ARG(k == 0 || (draft_ids && u_accept), "qvex_spec_accept: draft_ids/u_accept required for k > 0");
+  QVEX_CHECK_ARG(qvex_aligned(target, 16) && (!draft || qvex_aligned(draft, 16)),
+                 "qvex_spec_accept: logits must be 16-byte aligned");
+  const int greedy = !(inv_temp > 0.0f);
+  QVEX_CHECK_ARG(greedy || u_sample, "qvex_spec_accept: u_sample required when sampling");
+  const int P = nparts(V);
+  const int rps = (k + 1) + (draft ? k : 0);
+  const uint64_t need = (uint64_t)S * rps * P * 2 * sizeof(float);
+  QVEX_CHECK_ARG(workspace_bytes >= need, "qvex_spec_accept: workspace %llu bytes < %llu needed",
+                 (unsigned long long)workspace_bytes, (unsigned long long)need);
+  const size_t lds = ((size_t)P * NT + P + 2 * rps) * sizeof(float);
+  QVEX_CHECK_ARG(lds <= 150 * 1024, "qvex_spec_accept: V=%d too large for the LDS sampling table", V);
+  QVEX_CHECK_ARG((long)S * rps <= 65535, "qvex_spec_accept: S*rows=%ld exceeds the grid limit", (long)S * rps);
+  SpecArgs a{target, draft, draft_ids, u_accept, u_sample, inv_temp, greedy, n_accept, out_token,
+             (float*)workspace, S, k, V, P, rps};
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(spec_rowstats_kernel, dim3(P, S * rps), dim3(NT), 0, st, a);
+  QVEX_CHECK_LAUNCH("qvex_spec_accept/rowstats");
+  hipLaunchKernelGGL(spec_accept_kernel, dim3(S), dim3(NT), lds, st, a);
+  QVEX_CHECK_LAUNCH("qvex_spec_accept/accept");
+  return QVEX_OK;
+}

@@ -23,6 +23,7 @@ SIGNATURES: dict[str, list] = {
     "qvex_read_roof": [P, U64, P, I, P],
     "qvex_gdn_recurrent": [P, P, P, P, P, P, P, P, P, I, P, I, I, I, I, I, I, P],
     "qvex_gdn_recurrent_ring": [P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, I, I, P],
+    "qvex_spec_accept": [P, P, P, P, P, F, P, P, I, I, I, P, U64, P],
 }
 
 _lib: ctypes.CDLL | None = None
@@ -43,6 +44,8 @@ def lib() -> ctypes.CDLL:
         L.qvex_last_error.argtypes = []
         L.qvex_abi_version.restype = I
         L.qvex_abi_version.argtypes = []
+        L.qvex_spec_accept_workspace_bytes.restype = U64
+        L.qvex_spec_accept_workspace_bytes.argtypes = [I, I, I, I]
         for name, args in SIGNATURES.items():
             fn = getattr(L, name)
             fn.argtypes = args
@@ -60,4 +63,4 @@ def call(name: str, *args) -> None:
 
 
 def exported_symbols() -> list[str]:
-    return ["qvex_last_error", "qvex_abi_version", *SIGNATURES]
+    return ["qvex_last_error", "qvex_abi_version", "qvex_spec_accept_workspace_bytes", *SIGNATURES]

@@ -82,3 +82,113 @@ def read_roof(buf: torch.Tensor, sink: torch.Tensor, blocks: int = 4096) -> None
     """Stream-read every byte of buf (HBM roof probe, experiments/native/qmv_spike.mm:21-32)."""
     nbytes = buf.numel() * buf.element_size()
     _C.call("qvex_read_roof", _ptr(buf), nbytes, _ptr(sink), int(blocks), _stream())
+
+
+# ---------------------------------------------------------------- Gated DeltaNet
+
+def _gdn_check(q, k, v, a, b, A_log, dt_bias):
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (a, "a"), (b, "b"), (dt_bias, "dt_bias")):
+        _check(t, n, torch.bfloat16)
+    _check(A_log, "A_log", torch.float32, 1)
+    B, T, Hk, Dk = k.shape
+    Hv, Dv = v.shape[2:]
+    if q.shape != k.shape or v.shape[:2] != (B, T) or a.shape != (B, T, Hv) or b.shape != (B, T, Hv):
+        raise _C.QvexError(f"gated_delta shape mismatch: q {tuple(q.shape)} k {tuple(k.shape)} "
+                           f"v {tuple(v.shape)} a {tuple(a.shape)} b {tuple(b.shape)}")
+    if A_log.shape != (Hv,) or dt_bias.shape != (Hv,):
+        raise _C.QvexError("A_log and dt_bias must have shape [Hv]")
+    return B, T, Hk, Hv, Dk, Dv
+
+
+def gated_delta_snapshots(q, k, v, a, b, A_log, dt_bias, state, snapshots=None, y=None):
+    """Recurrent Gated DeltaNet over T tokens, keeping the state after every token.
+
+    q, k [B,T,Hk,Dk], v [B,T,Hv,Dv], a, b [B,T,Hv] bf16; A_log fp32 [Hv];
+    dt_bias bf16 [Hv]; state fp32 [B,Hv,Dv,Dk] (may be a slot of `snapshots`).
+    Returns (y [B,T,Hv,Dv] bf16, snapshots fp32 [T,B,Hv,Dv,Dk]); snapshots[t] is
+    the state after token t, so rolling back to L kept tokens is snapshots[L-1]."""
+    B, T, Hk, Hv, Dk, Dv = _gdn_check(q, k, v, a, b, A_log, dt_bias)
+    _check(state, "state", torch.float32)
+    if state.shape != (B, Hv, Dv, Dk):
+        raise _C.QvexError(f"state must be [B,Hv,Dv,Dk]=({B},{Hv},{Dv},{Dk})")
+    if snapshots is None:
+        snapshots = torch.empty((T, B, Hv, Dv, Dk), dtype=torch.float32, device=q.device)
+    if y is None:
+        y = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=q.device)
+    _C.call("qvex_gdn_recurrent", _ptr(q), _ptr(k), _ptr(v), _ptr(a), _ptr(b), _ptr(A_log),
+            _ptr(dt_bias), _ptr(state), _ptr(snapshots), 1, _ptr(y), B, T, Hk, Hv, Dk, Dv, _stream())
+    return y, snapshots
+
+
+def gated_delta(q, k, v, a, b, A_log, dt_bias, state, keep_mid=False):
+    """Mirror of engine/kernels.py:92-116: returns y, the new state and, with
+    keep_mid, the state before the last token."""
+    B, T, Hk, Hv, Dk, Dv = _gdn_check(q, k, v, a, b, A_log, dt_bias)
+    if keep_mid:
+        y, snaps = gated_delta_snapshots(q, k, v, a, b, A_log, dt_bias, state)
+        mid = snaps[T - 2] if T >= 2 else state.clone()
+        return y, snaps[T - 1], mid
+    _check(state, "state", torch.float32)
+    out = torch.empty((1, B, Hv, Dv, Dk), dtype=torch.float32, device=q.device)
+    y = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=q.device)
+    _C.call("qvex_gdn_recurrent", _ptr(q), _ptr(k), _ptr(v), _ptr(a), _ptr(b), _ptr(A_log),
+            _ptr(dt_bias), _ptr(state), _ptr(out), 0, _ptr(y), B, T, Hk, Hv, Dk, Dv, _stream())
+    return y, out[0]
+
+
+def gated_delta_ring(q, k, v, a, b, A_log, dt_bias, ring, cur_slot, y=None):
+    """Ring-buffer form: state read from ring[cur_slot], the state after token t
+    written to ring[(cur_slot + 1 + t) % n_slots]; cur_slot is a device int32."""
+    B, T, Hk, Hv, Dk, Dv = _gdn_check(q, k, v, a, b, A_log, dt_bias)
+    _check(ring, "ring", torch.float32)
+    _check(cur_slot, "cur_slot", torch.int32)
+    if y is None:
+        y = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=q.device)
+    _C.call("qvex_gdn_recurrent_ring", _ptr(q), _ptr(k), _ptr(v), _ptr(a), _ptr(b), _ptr(A_log),
+            _ptr(dt_bias), _ptr(ring), ring.shape[0], _ptr(cur_slot), _ptr(y), B, T, Hk, Hv, Dk, Dv,
+            _stream())
+    return y
+
+
+# ---------------------------------------------------------------- speculative acceptance
+
+def spec_workspace(S: int, k: int, V: int, has_draft: bool, device) -> torch.Tensor:
+    n = int(_C.lib().qvex_spec_accept_workspace_bytes(S, k, V, int(has_draft)))
+    return torch.empty((max(n, 4) + 3) // 4, dtype=torch.float32, device=device)
+
+
+def spec_accept(target: torch.Tensor, draft: torch.Tensor | None, draft_ids: torch.Tensor,
+                u_accept: torch.Tensor, u_sample: torch.Tensor, temperature: float,
+                n_accept: torch.Tensor | None = None, out_token: torch.Tensor | None = None,
+                workspace: torch.Tensor | None = None):
+    """Fused accept / residual-resample / bonus sampling for S verify steps.
+
+    target fp32 [S,k+1,V]; draft fp32 [S,k,V] or None (greedy one-hot drafts, the
+    reference's rule, engine/speculative.py:79-80); draft_ids int32 [S,k];
+    u_accept fp32 [S,k]; u_sample fp32 [S]; temperature <= 0 means greedy.
+    Returns (n_accept int32 [S], out_token int32 [S]) on the device."""
+    _check(target, "target", torch.float32, 3)
+    S, k1, V = target.shape
+    k = k1 - 1
+    if draft is not None:
+        _check(draft, "draft", torch.float32, 3)
+        if draft.shape != (S, k, V):
+            raise _C.QvexError(f"draft must be [S,k,V]=({S},{k},{V})")
+    _check(draft_ids, "draft_ids", torch.int32)
+    _check(u_accept, "u_accept", torch.float32)
+    _check(u_sample, "u_sample", torch.float32)
+    if draft_ids.numel() != S * k or u_accept.numel() != S * k or u_sample.numel() != S:
+        raise _C.QvexError("draft_ids/u_accept must hold S*k values and u_sample S values")
+    import numpy as np
+    inv_temp = float(np.float32(1.0) / np.float32(temperature)) if temperature > 0 else 0.0
+    dev = target.device
+    if n_accept is None:
+        n_accept = torch.empty(S, dtype=torch.int32, device=dev)
+    if out_token is None:
+        out_token = torch.empty(S, dtype=torch.int32, device=dev)
+    if workspace is None:
+        workspace = spec_workspace(S, k, V, draft is not None, dev)
+    _C.call("qvex_spec_accept", _ptr(target), _ptr(draft) if draft is not None else None,
+            _ptr(draft_ids), _ptr(u_accept), _ptr(u_sample), inv_temp, _ptr(n_accept),
+            _ptr(out_token), S, k, V, _ptr(workspace), workspace.numel() * 4, _stream())
+    return n_accept, out_token
