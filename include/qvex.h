@@ -63,6 +63,14 @@ int qvex_qmv_w4g64_tiled(const uint16_t* x, const uint32_t* w, const uint16_t* s
                          const uint16_t* biases, uint16_t* y, int M, int N, int K,
                          int rows_per_wave, int k_split, void* stream);
 
+/* Same product through the MFMA form of the kernel (16-row tiles, block-
+ * diagonal activation operand): tiles_per_wave in {1,2,4} 16-row tiles per
+ * wave, wave_ksplit in {1,2,4} waves of a block splitting K. Requires
+ * K % 256 == 0 for M <= 4 and K % 128 == 0 for M <= 8. */
+int qvex_qmv_w4g64_mfma(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
+                        const uint16_t* biases, uint16_t* y, int M, int N, int K,
+                        int tiles_per_wave, int wave_ksplit, void* stream);
+
 /* ------------------------------------------------------------------------
  * Gated DeltaNet recurrence (verify form), one state snapshot per token.
  *

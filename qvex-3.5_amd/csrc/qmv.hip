@@ -31,13 +31,21 @@ constexpr uint32_t kMagic = 0x43004300u;   // bf16 pair (128.0, 128.0)
 constexpr uint32_t kNib = 0x000F000Fu;
 constexpr uint32_t kOnes = 0x3f803f80u;    // bf16 pair (1.0, 1.0)
 
-// (a & mask) | magic as one VOP3 op. gfx9 VOP3 takes no literal operand, so the
-// compiler would otherwise split it into two VOP2 ops with literals; the mask
-// rides in an SGPR and the magic in a VGPR (one constant-bus read).
+// (a & mask) | magic. gfx9 VOP3 takes no literal operand, so with both constants
+// as literals the compiler splits this into two VOP2 ops; callers make the mask
+// an opaque SGPR value and the magic an opaque VGPR value (see opaque_sgpr /
+// opaque_vgpr), which lets it select one v_and_or_b32 (one constant-bus read)
+// while the hazard recognizer still sees every instruction.
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t magic) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(magic));
-  return r;
+  return (a & mask) | magic;
+}
+__device__ __forceinline__ uint32_t opaque_sgpr(uint32_t v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+__device__ __forceinline__ uint32_t opaque_vgpr(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
 }
 
 // Chunk = 32 consecutive k of one row = 4 uint32 words = 16 bytes.
@@ -49,6 +57,8 @@ __global__ __launch_bounds__(256) void qmv_w4g64_kernel(
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     uint16_t* __restrict__ y, int N, int K) {
   constexpr int RG = 4 / KS;
+  // chunks per lane whose weight loads are issued together (2 measured no faster)
+  constexpr int U = 1;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int rg = wave / KS;
@@ -57,9 +67,9 @@ __global__ __launch_bounds__(256) void qmv_w4g64_kernel(
 
   const int nchunk = K >> 5;
   const int KW = K >> 3;   // words per row
-  uint32_t magic = kMagic;
-  asm volatile("" : "+v"(magic));   // keep the magic constant in a VGPR
   const int G = K >> 6;    // groups per row
+  const uint32_t magic = opaque_vgpr(kMagic);
+  const uint32_t nib = opaque_sgpr(kNib);
 
   float acc[R][M];
 #pragma unroll
@@ -67,31 +77,35 @@ __global__ __launch_bounds__(256) void qmv_w4g64_kernel(
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
 
-  for (int cbase = ws * 64; cbase < nchunk; cbase += 64 * KS) {
-    const int c = cbase + lane;
-    if (c < nchunk) {
-      // weights first: they are the long-latency stream
-      u32x4 wv[R];
-      uint32_t sb[R][2];
+  for (int cbase = ws * 64; cbase < nchunk; cbase += 64 * KS * U) {
+    // weights first: they are the long-latency stream; rows past N re-read
+    // row N-1 (never stored), chunks past K are skipped
+    u32x4 wv[U][R];
+    uint32_t sb[U][R][2];
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int row = row0 + r;
-        if (row < N) {
-          wv[r] = load_nt16(w + (size_t)row * KW + (size_t)c * 4);
-          sb[r][0] = scales[(size_t)row * G + (c >> 1)];
-          sb[r][1] = biases[(size_t)row * G + (c >> 1)];
-        } else {
-          wv[r] = u32x4{0, 0, 0, 0};
-          sb[r][0] = sb[r][1] = 0;
+    for (int u = 0; u < U; ++u) {
+      const int c = cbase + u * 64 * KS + lane;
+      if (c < nchunk) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int row = min(row0 + r, N - 1);
+          wv[u][r] = load_nt16(w + (size_t)row * KW + (size_t)c * 4);
+          sb[u][r][0] = scales[(size_t)row * G + (c >> 1)];
+          sb[u][r][1] = biases[(size_t)row * G + (c >> 1)];
         }
       }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = cbase + u * 64 * KS + lane;
+      if (c >= nchunk) continue;
       // x chunk of every activation row, permuted into (x_j, x_{j+4}) pairs
       uint32_t xp[M][16];
       float xs[M];
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         const uint16_t* xr = x + (size_t)m * K + (size_t)c * 32;
-        float s = 0.0f;
+        float sum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const u32x4 v = load16(xr + 8 * i);
@@ -99,26 +113,26 @@ __global__ __launch_bounds__(256) void qmv_w4g64_kernel(
           xp[m][4 * i + 1] = (v.x >> 16) | (v.z & 0xffff0000u);
           xp[m][4 * i + 2] = (v.y & 0xffffu) | (v.w << 16);
           xp[m][4 * i + 3] = (v.y >> 16) | (v.w & 0xffff0000u);
-          s = dot2(v.x, kOnes, s);
-          s = dot2(v.y, kOnes, s);
-          s = dot2(v.z, kOnes, s);
-          s = dot2(v.w, kOnes, s);
+          sum = dot2(v.x, kOnes, sum);
+          sum = dot2(v.y, kOnes, sum);
+          sum = dot2(v.z, kOnes, sum);
+          sum = dot2(v.w, kOnes, sum);
         }
-        xs[m] = s;
+        xs[m] = sum;
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const uint32_t ws4[4] = {wv[r].x, wv[r].y, wv[r].z, wv[r].w};
+        const uint32_t ws4[4] = {wv[u][r].x, wv[u][r].y, wv[u][r].z, wv[u][r].w};
         float d[M];
 #pragma unroll
         for (int m = 0; m < M; ++m) d[m] = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint32_t wd = ws4[i];
-          const uint32_t p0 = and_or(wd, kNib, magic);
-          const uint32_t p1 = and_or(wd >> 4, kNib, magic);
-          const uint32_t p2 = and_or(wd >> 8, kNib, magic);
-          const uint32_t p3 = and_or(wd >> 12, kNib, magic);
+          const uint32_t p0 = and_or(wd, nib, magic);
+          const uint32_t p1 = and_or(wd >> 4, nib, magic);
+          const uint32_t p2 = and_or(wd >> 8, nib, magic);
+          const uint32_t p3 = and_or(wd >> 12, nib, magic);
 #pragma unroll
           for (int m = 0; m < M; ++m) {
             d[m] = dot2(p0, xp[m][4 * i + 0], d[m]);
@@ -127,8 +141,8 @@ __global__ __launch_bounds__(256) void qmv_w4g64_kernel(
             d[m] = dot2(p3, xp[m][4 * i + 3], d[m]);
           }
         }
-        const float sc = bf16_to_f32((uint16_t)sb[r][0]);
-        const float bi = bf16_to_f32((uint16_t)sb[r][1]);
+        const float sc = bf16_to_f32((uint16_t)sb[u][r][0]);
+        const float bi = bf16_to_f32((uint16_t)sb[u][r][1]);
         const float bo = fmaf(-128.0f, sc, bi);
 #pragma unroll
         for (int m = 0; m < M; ++m) acc[r][m] = fmaf(sc, d[m], fmaf(bo, xs[m], acc[r][m]));
@@ -169,6 +183,223 @@ __global__ __launch_bounds__(256) void qmv_w4g64_kernel(
       for (int j = 0; j < KS; ++j) s += red[rg * KS + j][lane];
       const int row = row0 + r;
       if (row < N) y[(size_t)m * N + row] = f32_to_bf16(s);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- MFMA variant
+//
+// At M > 1 the VALU form above spends 16*M dot2 ops per 16 weight bytes and
+// becomes issue-bound well below the HBM roof. This variant keeps the same
+// one-op nibble dequant (bf16 128+q pairs) but hands the products to
+// v_mfma_f32_16x16x32_bf16, so the VALU work per weight word is fixed (dequant +
+// a group fold) whatever M is.
+//
+// Layout trick: one MFMA covers 16 weight rows (the 16 output columns j) and 4
+// k-chunks of 8 (the lane groups c = lane/16). Chunk c carries the words of
+// group g0 + c/CPG of each row, and the activation operand is block-diagonal:
+// A row i = (group i/MP, activation row i%MP) is non-zero only in the chunks of
+// its own group. The 16x16 accumulator then holds one group's partial dot
+// product per (row, activation row) - exactly what the per-group scale/bias
+// fold needs - and lane l's four accumulators belong to the weight row and
+// group this lane itself loaded, so the fold reads one scale and one bias.
+//   MP = 4 (M <= 4): 4 groups per set, 8 MFMA steps, 32 B of weights per lane;
+//   MP = 8 (M <= 8): 2 groups per set, 4 MFMA steps, 16 B of weights per lane.
+// Group sums of x (for the bias term) are computed once per block into LDS.
+// TN 16-row tiles per wave; WS waves of a block split the group sets of the
+// same tiles and combine through LDS. Weight loads of the next group set are
+// issued before the current one is computed (two register buffers).
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  u32x4 v = {a, b, c, d};
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+template <int MP, int TN, int WS>
+__global__ __launch_bounds__(256) void qmv_mfma_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
+    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
+    uint16_t* __restrict__ y, int M, int N, int K) {
+  constexpr int GPM = 16 / MP;     // groups per set
+  constexpr int CPG = 4 / GPM;     // k-chunks (lane groups) per group
+  constexpr int NS = 8 / CPG;      // MFMA steps per set = words per lane per set
+  constexpr int NL = NS / 4;       // 16-byte weight loads per lane per set
+  constexpr int RG = 4 / WS;       // row groups per block
+  extern __shared__ float smem[];
+  float* Xs = smem;                // [G][MP] group sums of x
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rg = wave / WS, ws = wave % WS;
+  const int G = K >> 6;
+  const int KW = K >> 3;
+  const int GS = G / GPM;
+
+  for (int idx = threadIdx.x; idx < G * MP; idx += 256) {
+    const int g = idx / MP, m = idx % MP;
+    float sum = 0.0f;
+    if (m < M) {
+      const uint16_t* xp = x + (size_t)m * K + g * 64;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const u32x4 v = load16(xp + 8 * i);
+        sum = dot2(v.x, kOnes, sum);
+        sum = dot2(v.y, kOnes, sum);
+        sum = dot2(v.z, kOnes, sum);
+        sum = dot2(v.w, kOnes, sum);
+      }
+    }
+    Xs[idx] = sum;
+  }
+  __syncthreads();
+
+  const uint32_t magic = opaque_vgpr(kMagic);
+  const uint32_t nib = opaque_sgpr(kNib);
+
+  const int c = lane >> 4, i16 = lane & 15;
+  const int cg = c / CPG;                 // group (within the set) of chunk c
+  const int cw = (c % CPG) * NS;          // first word (within the group) of chunk c
+  const bool part = (i16 / MP) == cg && (i16 % MP) < M;
+  const int am = i16 % MP;                // activation row fed by this lane
+  const int fm0 = (4 * c) % MP;           // activation row of accumulator 0
+  const int tile0 = (blockIdx.x * RG + rg) * TN;
+
+  float acc[TN][4];
+#pragma unroll
+  for (int t = 0; t < TN; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
+
+  uint32_t A[NS][4];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) A[s][0] = A[s][1] = A[s][2] = A[s][3] = 0u;
+
+  u32x4 wb[2][TN][NL];
+  uint32_t sbuf[2][TN][2];
+
+  auto load_set = [&](int buf, int gs) {
+    const int g = gs * GPM + cg;
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      // rows past N re-read row N-1; their sums are never stored
+      const int n = min((tile0 + t) * 16 + i16, N - 1);
+      const uint32_t* wp = w + (size_t)n * KW + g * 8 + cw;
+#pragma unroll
+      for (int q = 0; q < NL; ++q) wb[buf][t][q] = load_nt16(wp + 4 * q);
+      sbuf[buf][t][0] = scales[(size_t)n * G + g];
+      sbuf[buf][t][1] = biases[(size_t)n * G + g];
+    }
+  };
+
+  auto build_a = [&](int gs) {
+    const int g = gs * GPM + cg;
+    if (part) {
+      const uint16_t* xp = x + (size_t)am * K + g * 64 + cw * 8;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const u32x4 v = load16(xp + 8 * s);
+        A[s][0] = (v.x & 0xffffu) | (v.z << 16);
+        A[s][1] = (v.x >> 16) | (v.z & 0xffff0000u);
+        A[s][2] = (v.y & 0xffffu) | (v.w << 16);
+        A[s][3] = (v.y >> 16) | (v.w & 0xffff0000u);
+      }
+    }
+  };
+
+  auto compute_set = [&](int buf, int gs) {
+    const int g = gs * GPM + cg;
+    float Xf[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Xf[r] = Xs[g * MP + fm0 + r];
+    // tiles interleaved inside each step: TN independent accumulation chains
+    f32x4_t C[TN];
+#pragma unroll
+    for (int t = 0; t < TN; ++t) C[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const bf16x8_t a = as_bf16x8(A[s][0], A[s][1], A[s][2], A[s][3]);
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        const u32x4 wv = wb[buf][t][s / 4];
+        const uint32_t wd = (s % 4 == 0) ? wv.x : (s % 4 == 1) ? wv.y : (s % 4 == 2) ? wv.z : wv.w;
+        const bf16x8_t b = as_bf16x8(and_or(wd, nib, magic), and_or(wd >> 4, nib, magic),
+                                     and_or(wd >> 8, nib, magic), and_or(wd >> 12, nib, magic));
+        C[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, C[t], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      const float sc = bf16_to_f32((uint16_t)sbuf[buf][t][0]);
+      const float bi = bf16_to_f32((uint16_t)sbuf[buf][t][1]);
+      const float bo = fmaf(-128.0f, sc, bi);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(sc, C[t][r], fmaf(bo, Xf[r], acc[t][r]));
+    }
+  };
+
+  // Memory order per step: activation loads of this set, then the weight
+  // prefetch of the next set, then compute; the in-order vmcnt wait for the
+  // activations then leaves the prefetch in flight.
+  int gs = ws;
+  if (gs < GS) load_set(0, gs);
+  while (gs < GS) {
+    const int g1 = gs + WS;
+    build_a(gs);
+    if (g1 < GS) load_set(1, g1);
+    compute_set(0, gs);
+    if (g1 >= GS) break;
+    const int g2 = g1 + WS;
+    build_a(g1);
+    if (g2 < GS) load_set(0, g2);
+    compute_set(1, g1);
+    gs = g2;
+  }
+
+  // combine the lane groups that share an activation row
+#pragma unroll
+  for (int t = 0; t < TN; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = acc[t][r];
+      if constexpr (MP == 4) v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      acc[t][r] = v;
+    }
+  constexpr int LIVE = 16 * (MP / 4);     // lanes holding distinct (row, m) sums
+  if constexpr (WS > 1) {
+    float* red = smem + G * MP;           // [4 waves][TN][4][LIVE]
+    if (lane < LIVE) {
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[((wave * TN + t) * 4 + r) * LIVE + lane] = acc[t][r];
+    }
+    __syncthreads();
+    if (ws != 0) return;
+    if (lane < LIVE) {
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = 0.0f;
+#pragma unroll
+          for (int j = 0; j < WS; ++j) v += red[(((rg * WS + j) * TN + t) * 4 + r) * LIVE + lane];
+          acc[t][r] = v;
+        }
+    }
+  }
+  if (lane < LIVE) {
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      const int n = (tile0 + t) * 16 + i16;
+      if (n < N) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = fm0 + r;
+          if (m < M) y[(size_t)m * N + n] = f32_to_bf16(acc[t][r]);
+        }
+      }
     }
   }
 }
@@ -223,6 +454,52 @@ qmv_fn pick(int M, int r, int ks) {
   return nullptr;
 }
 
+typedef void (*qmv_mfma_fn)(const uint16_t*, const uint32_t*, const uint16_t*, const uint16_t*,
+                            uint16_t*, int, int, int);
+
+template <int MP, int TN>
+qmv_mfma_fn pick_mfma_ws(int ws) {
+  switch (ws) {
+    case 1: return qmv_mfma_kernel<MP, TN, 1>;
+    case 2: return qmv_mfma_kernel<MP, TN, 2>;
+    case 4: return qmv_mfma_kernel<MP, TN, 4>;
+  }
+  return nullptr;
+}
+
+template <int MP>
+qmv_mfma_fn pick_mfma_tn(int tn, int ws) {
+  switch (tn) {
+    case 1: return pick_mfma_ws<MP, 1>(ws);
+    case 2: return pick_mfma_ws<MP, 2>(ws);
+    case 4: return pick_mfma_ws<MP, 4>(ws);
+  }
+  return nullptr;
+}
+
+int launch_mfma(const uint16_t* x, const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                uint16_t* y, int M, int N, int K, int TN, int WS, hipStream_t stream) {
+  QVEX_CHECK_ARG(M >= 1 && M <= 8, "qvex_qmv_w4g64: M=%d outside 1..8", M);
+  QVEX_CHECK_ARG(N >= 1, "qvex_qmv_w4g64: N=%d", N);
+  const int MP = M <= 4 ? 4 : 8;
+  const int set_k = 64 * (16 / MP);
+  QVEX_CHECK_ARG(K >= set_k && K % set_k == 0, "qvex_qmv_w4g64 (mfma): K=%d must be a multiple of %d", K, set_k);
+  QVEX_CHECK_ARG(x && w && scales && biases && y, "qvex_qmv_w4g64: null pointer");
+  QVEX_CHECK_ARG(qvex_aligned(x, 16) && qvex_aligned(w, 16), "qvex_qmv_w4g64: x and w must be 16-byte aligned");
+  QVEX_CHECK_ARG(qvex_aligned(scales, 2) && qvex_aligned(biases, 2) && qvex_aligned(y, 2),
+                 "qvex_qmv_w4g64: scales/biases/y must be 2-byte aligned");
+  qmv_mfma_fn fn = MP == 4 ? pick_mfma_tn<4>(TN, WS) : pick_mfma_tn<8>(TN, WS);
+  QVEX_CHECK_ARG(fn != nullptr, "qvex_qmv_w4g64 (mfma): unsupported tile TN=%d WS=%d", TN, WS);
+  const int G = K / 64;
+  const size_t lds = (size_t)G * MP * sizeof(float) + (WS > 1 ? (size_t)4 * TN * 4 * 16 * (MP / 4) * sizeof(float) : 0);
+  QVEX_CHECK_ARG(lds <= 64 * 1024, "qvex_qmv_w4g64 (mfma): K=%d needs %zu bytes of LDS", K, lds);
+  const int rows_per_block = 16 * TN * (4 / WS);
+  const int blocks = (N + rows_per_block - 1) / rows_per_block;
+  hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, stream, x, w, scales, biases, y, M, N, K);
+  QVEX_CHECK_LAUNCH("qvex_qmv_w4g64 (mfma)");
+  return QVEX_OK;
+}
+
 // Default tile: rows per wave shrink as M grows (x pairs cost 16*M VGPRs);
 // K is split across waves when the row groups alone cannot fill 256 CUs.
 void default_tile(int M, int N, int K, int* R, int* KS) {
@@ -266,6 +543,12 @@ extern "C" int qvex_qmv_w4g64_tiled(const uint16_t* x, const uint32_t* w, const 
                                     const uint16_t* biases, uint16_t* y, int M, int N, int K,
                                     int rows_per_wave, int k_split, void* stream) {
   return launch(x, w, scales, biases, y, M, N, K, rows_per_wave, k_split, (hipStream_t)stream);
+}
+
+extern "C" int qvex_qmv_w4g64_mfma(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
+                                   const uint16_t* biases, uint16_t* y, int M, int N, int K,
+                                   int tiles_per_wave, int wave_ksplit, void* stream) {
+  return launch_mfma(x, w, scales, biases, y, M, N, K, tiles_per_wave, wave_ksplit, (hipStream_t)stream);
 }
 
 extern "C" int qvex_read_roof(const void* buf, uint64_t bytes, uint32_t* sink, int blocks, void* stream) {

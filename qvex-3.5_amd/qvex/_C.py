@@ -21,6 +21,7 @@ SIGNATURES: dict[str, list] = {
     "qvex_qmv_w4g64": [P, P, P, P, P, I, I, I, P],
     "qvex_qmv_w4g64_tiled": [P, P, P, P, P, I, I, I, I, I, P],
     "qvex_read_roof": [P, U64, P, I, P],
+    "qvex_qmv_w4g64_mfma": [P, P, P, P, P, I, I, I, I, I, P],
     "qvex_gdn_recurrent": [P, P, P, P, P, P, P, P, P, I, P, I, I, I, I, I, I, P],
     "qvex_gdn_recurrent_ring": [P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, I, I, P],
     "qvex_spec_accept": [P, P, P, P, P, F, P, P, I, I, I, P, U64, P],

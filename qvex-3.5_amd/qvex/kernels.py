@@ -62,7 +62,10 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
     _check(out, "out", torch.bfloat16)
     if out.numel() != M * N:
         raise _C.QvexError("out has the wrong size")
-    if tile is None:
+    if tile is not None and tile[0] == "mfma":
+        _C.call("qvex_qmv_w4g64_mfma", _ptr(x2), _ptr(w), _ptr(scales), _ptr(biases), _ptr(out),
+                M, N, K, int(tile[1]), int(tile[2]), _stream())
+    elif tile is None:
         _C.call("qvex_qmv_w4g64", _ptr(x2), _ptr(w), _ptr(scales), _ptr(biases), _ptr(out),
                 M, N, K, _stream())
     else:

@@ -12,6 +12,7 @@ import oracle
 from qvex import kernels, synth
 
 TILES = [(r, ks) for r in (1, 2, 4, 8) for ks in (1, 2, 4)]
+MFMA_TILES = [("mfma", tn, ws) for tn in (1, 2, 4) for ws in (1, 2, 4)]
 
 
 def to_dev(a, dtype):
@@ -133,3 +134,26 @@ def test_closed_forms():
     want = (xi.astype(np.int64) @ oracle.unpack_w4(w, K).astype(np.int64).T).astype(np.float64)
     # integers up to ~2^14 round to bf16; compare after the same rounding
     assert np.array_equal(got, oracle.bf16_to_f32(oracle.bf16_bits(want.astype(np.float32))))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tile", MFMA_TILES)
+@pytest.mark.parametrize("M", [1, 3, 4, 5, 8])
+def test_mfma_tiles(tile, M):
+    N, K = 531, 2304
+    w, s, b = synth.qmv_weights(N, K, seed=16, tag=M)
+    x = synth.qmv_x(M, K, seed=16, tag=M)
+    check(x, w, s, b, run(x, w, s, b, tile=tile))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 4, 5])
+@pytest.mark.parametrize("shape", [(12288, 4096), (4096, 12288), (248320, 4096)])
+def test_mfma_model_shapes(M, shape):
+    N, K = shape
+    w, s, b = synth.qmv_weights(N, K, seed=synth.SEED_SKINNY, tag=N)
+    x = synth.qmv_x(M, K, seed=synth.SEED_SKINNY, tag=M)
+    y = run(x, w, s, b, tile=("mfma", 2, 1))
+    rows = np.unique(np.concatenate([np.arange(32), np.arange(N - 32, N),
+                                     np.random.default_rng(N).choice(N, 1024, replace=False)]))
+    check(x, w, s, b, y, rows=rows)
