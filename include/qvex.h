@@ -96,16 +96,17 @@ int qvex_gdn_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                        int Dv, void* stream);
 
 /* Ring form of qvex_gdn_recurrent for stream/graph replay: ring is
- * fp32 [n_slots,B,Hv,Dv,Dk]; the state is read from slot c = *cur_slot (a device
- * int32) and the state after token t goes to slot (c + 1 + t) % n_slots.
- * Committing L accepted tokens is then cur_slot = (c + L) % n_slots, a device-side
- * update (see qvex_commit_step). Requires n_slots >= T + 1. Same reference
- * interface as qvex_gdn_recurrent. */
+ * fp32 [n_slots,B,Hv,Dv,Dk]; with c = *cur_slot mod n_slots (cur_slot a device
+ * int32, typically the layer's token count), the state is read from slot c and
+ * the state after token t goes to slot (c + 1 + t) % n_slots (every token when
+ * snap_every != 0, else only the last). Keeping L tokens then means advancing
+ * the counter by L: no state is copied. Requires n_slots >= T + 1 with
+ * snapshots. Same reference interface as qvex_gdn_recurrent. */
 int qvex_gdn_recurrent_ring(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                             const uint16_t* a, const uint16_t* b, const float* A_log,
                             const uint16_t* dt_bias, float* ring, int n_slots,
-                            const int32_t* cur_slot, uint16_t* y, int B, int T, int Hk,
-                            int Hv, int Dk, int Dv, void* stream);
+                            const int32_t* cur_slot, int snap_every, uint16_t* y, int B, int T,
+                            int Hk, int Hv, int Dk, int Dv, void* stream);
 
 /* ------------------------------------------------------------------------
  * Fused speculative acceptance sampling for S independent verify steps.
@@ -132,6 +133,83 @@ int qvex_spec_accept(const float* target, const float* draft, const int32_t* dra
                      const float* u_accept, const float* u_sample, float inv_temp,
                      int32_t* n_accept, int32_t* out_token, int S, int k, int V,
                      void* workspace, uint64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Verify-forward glue (Qwen3.5 hybrid stack, engine/model.py). bf16 storage,
+ * fp32 arithmetic, one bf16 rounding per output.
+ * ------------------------------------------------------------------------ */
+
+/* out[l, :] = dequant(w[ids[l], :]) (QEmbedding.__call__, engine/model.py:126-130);
+ * ids outside [0, V) are clamped. w uint32 [V, H/8]; scales/biases bf16 [V, H/64]. */
+int qvex_embed_w4g64(const int32_t* ids, int L, const uint32_t* w, const uint16_t* scales,
+                     const uint16_t* biases, int V, int H, uint16_t* out, void* stream);
+
+/* out[r] = w * (x[r] * rsqrt(mean(x[r]^2) + eps)) * scale, w optional (NULL = 1)
+ * (mx.fast.rms_norm at engine/model.py:218-219, 276-277, 314-316, 335; the
+ * weightless q/k scaling of engine/model.py:275-277 uses scale). Strides in
+ * elements, even. */
+int qvex_rmsnorm(const uint16_t* x, long x_stride, const uint16_t* w, uint16_t* out,
+                 long out_stride, int R, int D, float eps, float scale, void* stream);
+
+/* h = bf16(x + delta); out = rms_norm(h) * w: the residual add and the next
+ * pre-norm of Layer.__call__ (engine/model.py:313-316) in one pass. [R, D]. */
+int qvex_add_rmsnorm(const uint16_t* x, const uint16_t* delta, uint16_t* h_out,
+                     const uint16_t* w, uint16_t* out, int R, int D, float eps, void* stream);
+
+/* GatedDeltaNet input stage (engine/model.py:259-277). The conv input history
+ * is a ring of ring_rows rows [ring_rows, C] keyed by the layer's token count
+ * p = *pos (device int32): the conv state is rows p-K+1 .. p-1 (mod ring_rows),
+ * token t is stored at row p + t, so keeping L tokens is p += L and rollback
+ * copies nothing (generalises RecurrentCache.conv/conv_prev, engine/model.py:
+ * 179-193). Computes causal depthwise conv (conv_w [C, K]) + SiLU; q, k heads
+ * of 128 rms-normalised (no weight, eps) times q_scale / k_scale; v; and the b, a
+ * gate inputs copied from proj[:, ab_offset : ab_offset + 2*Hv] into [T, Hv].
+ * Requires ring_rows >= T + K - 1. */
+int qvex_gdn_conv_qk(const uint16_t* proj, long p_stride, uint16_t* conv_ring, int ring_rows,
+                     const int32_t* pos, const uint16_t* conv_w, int kernel_size, uint16_t* q,
+                     uint16_t* k, uint16_t* v, uint16_t* a_out, uint16_t* b_out, int T, int C,
+                     int key_dim, int Hv, int ab_offset, float q_scale, float k_scale, float eps,
+                     void* stream);
+
+/* counters[i] += n_accept[0] + extra for i < n: advances every cache counter
+ * past the kept verify tokens on the device (the commit half of decode()'s
+ * accept/rollback, engine/speculative.py:85-101), so a captured cycle needs no
+ * host round trip. */
+int qvex_commit_step(int32_t* counters, int n, const int32_t* n_accept, int extra, void* stream);
+
+/* out = silu(z) * rms_norm(y, w) per head row of D (_gated_rmsnorm,
+ * engine/model.py:138-143); y [R, D], z rows of `heads` heads with z_stride. */
+int qvex_gated_rmsnorm(const uint16_t* y, const uint16_t* z, long z_stride, int heads,
+                       const uint16_t* w, uint16_t* out, int R, int D, float eps, void* stream);
+
+/* out[l, i] = silu(gu[l, i]) * gu[l, I + i] (MLP with the fused gate_up,
+ * engine/model.py:133-135, 300-302). */
+int qvex_swiglu(const uint16_t* gu, uint16_t* out, int L, int I, void* stream);
+
+/* fp32 copy of bf16 values (Sampler.scores' astype(float32), engine/sampler.py:151). */
+int qvex_bf16_to_f32(const uint16_t* in, float* out, long n, void* stream);
+
+/* Attention input stage (engine/model.py:213-226): q and k rms-normalised per
+ * head with q_norm / k_norm, NeoX-form RoPE on the first rot_dim dims at
+ * positions *pos0 + l (pos0 a device int32), q written to q_out [L, Hq, D],
+ * k and v appended to k_cache / v_cache [Hkv, cap, D] at those positions
+ * (KVCache.update, engine/model.py:156-170). proj row = [Hq x (q | gate) | Hkv
+ * x k | Hkv x v]. */
+int qvex_attn_qk_rope(const uint16_t* proj, long p_stride, const uint16_t* q_norm,
+                      const uint16_t* k_norm, const int32_t* pos0, int L, int Hq, int Hkv, int D,
+                      int rot_dim, float theta, float eps, uint16_t* q_out, uint16_t* k_cache,
+                      uint16_t* v_cache, int cap, void* stream);
+
+/* Causal GQA attention of L queries over the cache (query l sees keys
+ * 0 .. *pos0 + l), scale 1/sqrt(D), output times sigmoid(gate) from the q_proj
+ * rows: mx.fast.scaled_dot_product_attention + o * sigmoid(gate)
+ * (engine/model.py:228-232). Split-K over keys_per_split keys per block;
+ * max_keys bounds *pos0 + L. workspace: qvex_attn_workspace_bytes(). */
+uint64_t qvex_attn_workspace_bytes(int L, int Hq, int Hkv, int D, int max_keys, int keys_per_split);
+int qvex_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                   const int32_t* pos0, int L, int Hq, int Hkv, int D, int cap, int max_keys,
+                   int keys_per_split, const uint16_t* gate, long gate_stride, uint16_t* out,
+                   void* workspace, uint64_t workspace_bytes, void* stream);
 
 /* Pure streaming read of `bytes` bytes (multiple of 16) from `buf`, folding
  * them into `sink` (64 uint32 words). Measures the achievable HBM read rate;

@@ -133,9 +133,13 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(GdnArgs p) {
         if (l16 == 0) p.y[(((long)bi * T + t) * p.Hv + hv) * p.Dv + dv] = f32_to_bf16(o);
 
         long slot = -1;
-        if (p.slot_ptr) slot = (cur + 1 + t) % p.n_slots;
-        else if (p.snap_every) slot = t;
-        else if (t == T - 1) slot = 0;
+        if (p.slot_ptr) {
+          if (p.snap_every || t == T - 1) slot = (cur + 1 + t) % p.n_slots;
+        } else if (p.snap_every) {
+          slot = t;
+        } else if (t == T - 1) {
+          slot = 0;
+        }
         if (slot >= 0) {
           float* dst = p.s_out + slot * p.slot_stride + row_off;
           u32x4 o0, o1;
@@ -187,15 +191,16 @@ extern "C" int qvex_gdn_recurrent(const uint16_t* q, const uint16_t* k, const ui
 extern "C" int qvex_gdn_recurrent_ring(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                        const uint16_t* a, const uint16_t* b, const float* A_log,
                                        const uint16_t* dt_bias, float* ring, int n_slots,
-                                       const int32_t* cur_slot, uint16_t* y, int B, int T, int Hk,
-                                       int Hv, int Dk, int Dv, void* stream) {
+                                       const int32_t* cur_slot, int snap_every, uint16_t* y, int B, int T,
+                                       int Hk, int Hv, int Dk, int Dv, void* stream) {
   if (int rc = check_common("qvex_gdn_recurrent_ring", B, T, Hk, Hv, Dk, Dv)) return rc;
   QVEX_CHECK_ARG(q && k && v && a && b && A_log && dt_bias && ring && cur_slot && y,
                  "qvex_gdn_recurrent_ring: null pointer");
-  QVEX_CHECK_ARG(n_slots >= T + 1, "qvex_gdn_recurrent_ring: n_slots=%d must be >= T+1=%d", n_slots, T + 1);
+  QVEX_CHECK_ARG(n_slots >= 2 && (!snap_every || n_slots >= T + 1),
+                 "qvex_gdn_recurrent_ring: n_slots=%d must be >= T+1=%d with snapshots (>= 2 without)", n_slots, T + 1);
   QVEX_CHECK_ARG(qvex_aligned(q, 16) && qvex_aligned(k, 16) && qvex_aligned(ring, 16),
                  "qvex_gdn_recurrent_ring: q, k, ring must be 16-byte aligned");
   GdnArgs p{q, k, v, a, b, A_log, dt_bias, ring, ring, cur_slot,
-            (long)B * Hv * Dv * Dk, n_slots, 1, y, B, T, Hk, Hv, Dv};
+            (long)B * Hv * Dv * Dk, n_slots, snap_every ? 1 : 0, y, B, T, Hk, Hv, Dv};
   return launch(p, (hipStream_t)stream);
 }

@@ -1,0 +1,594 @@
+// Verify-forward glue kernels of the Qwen3.5 hybrid layer stack.
+//
+// Reference (engine/model.py): QEmbedding (121-130), mx.fast.rms_norm
+// (218-219, 276-277, 314-316, 335), _swiglu (133-135), _gated_rmsnorm (138-143),
+// GatedDeltaNet conv1d + SiLU + q/k norms (257-277), Attention q/k norm +
+// partial RoPE + KV append + SDPA + sigmoid gate (210-232). All arithmetic is
+// fp32 with bf16 storage; each kernel rounds its outputs to bf16 once.
+//
+// Layout: activations are row-major [rows, features] bf16; KV caches are
+// [Hkv, cap, D] bf16 per layer (one contiguous key run per kv head); the
+// GDN conv input window [3 + T, C] is kept per call so that the conv state
+// after L accepted tokens is rows L..L+2 of it (a pointer pick on rollback).
+#include "qvex_common.h"
+
+#include <math.h>
+
+#include <algorithm>
+
+namespace {
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// ---------------------------------------------------------------- embedding gather + dequant
+
+// out[l, k] = bf16(s[id, k/64] * q[id, k] + b[id, k/64]); one block per token.
+__global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ ids, const uint32_t* __restrict__ w,
+                                                    const uint16_t* __restrict__ sc, const uint16_t* __restrict__ bi,
+                                                    uint16_t* __restrict__ out, int V, int H) {
+  const int l = blockIdx.x;
+  int id = ids[l];
+  id = id < 0 ? 0 : (id >= V ? V - 1 : id);
+  const int KW = H / 8, G = H / 64;
+  const uint32_t* wr = w + (size_t)id * KW;
+  for (int wi = threadIdx.x; wi < KW; wi += blockDim.x) {
+    const uint32_t word = wr[wi];
+    const int g = wi / 8;
+    const float s = bf16_to_f32(sc[(size_t)id * G + g]);
+    const float b = bf16_to_f32(bi[(size_t)id * G + g]);
+    u32x4 o;
+    uint32_t pk[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float v0 = fmaf(s, (float)((word >> (8 * j)) & 0xF), b);
+      const float v1 = fmaf(s, (float)((word >> (8 * j + 4)) & 0xF), b);
+      pk[j] = pack_bf16x2(v0, v1);
+    }
+    o.x = pk[0]; o.y = pk[1]; o.z = pk[2]; o.w = pk[3];
+    *reinterpret_cast<u32x4*>(out + (size_t)l * H + wi * 8) = o;
+  }
+}
+
+// ---------------------------------------------------------------- RMSNorm family
+//
+// One wave per row. y = w * (x * rsqrt(mean(x^2) + eps)) * scale (w optional).
+
+template <bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x, long x_stride,
+                                                      const uint16_t* __restrict__ delta, long d_stride,
+                                                      uint16_t* __restrict__ h_out, long h_stride,
+                                                      const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
+                                                      long o_stride, int R, int D, float eps, float scale) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= R) return;
+  const uint16_t* xr = x + row * x_stride;
+  float ss = 0.0f;
+  // D % 2 == 0 is checked on the host; each lane walks pairs
+  for (int i = 2 * lane; i < D; i += 128) {
+    const uint32_t p = *reinterpret_cast<const uint32_t*>(xr + i);
+    float a = bf16_lo(p), b = bf16_hi(p);
+    if constexpr (ADD) {
+      const uint32_t dp = *reinterpret_cast<const uint32_t*>(delta + row * d_stride + i);
+      a = bf16_to_f32(f32_to_bf16(a + bf16_lo(dp)));
+      b = bf16_to_f32(f32_to_bf16(b + bf16_hi(dp)));
+      *reinterpret_cast<uint32_t*>(h_out + row * h_stride + i) = pack_bf16x2(a, b);
+    }
+    ss = fmaf(a, a, fmaf(b, b, ss));
+  }
+  ss = wave_allsum(ss);
+  const float inv = rsqrtf(ss / (float)D + eps);
+  for (int i = 2 * lane; i < D; i += 128) {
+    uint32_t p;
+    if constexpr (ADD) p = *reinterpret_cast<const uint32_t*>(h_out + row * h_stride + i);
+    else p = *reinterpret_cast<const uint32_t*>(xr + i);
+    float a = bf16_lo(p) * inv, b = bf16_hi(p) * inv;
+    if (w) {
+      const uint32_t wp = *reinterpret_cast<const uint32_t*>(w + i);
+      a = bf16_lo(wp) * a;
+      b = bf16_hi(wp) * b;
+    }
+    *reinterpret_cast<uint32_t*>(out + row * o_stride + i) = pack_bf16x2(a * scale, b * scale);
+  }
+}
+
+// ---------------------------------------------------------------- GDN: conv1d + SiLU + q/k norm
+//
+// The conv input history is a ring of R rows per layer keyed by the token count
+// p = *pos: the state is rows (p-3, p-2, p-1) mod R, new token t goes to row
+// (p + t) mod R. Window row j of token t is ring[(p + t - (K-1) + j) mod R] for
+// t + j < K-1, else proj[t + j - (K-1)]. Keeping L tokens is p += L, so rollback
+// moves no data. conv[t, c] = sum_j window[t + j, c] * cw[c, j]
+// (cross-correlation, MLX conv1d with groups = C); silu; q and k heads
+// rms-normalised (no weight, eps) and scaled; b, a copied out of the
+// projection row into contiguous [T, Hv] arrays.
+// Grid (T, C / 512); block 256 = 4 waves; each wave owns one 128-channel head
+// with 2 channels per lane, so the head's norm is one wave reduction.
+__global__ __launch_bounds__(256) void conv_silu_qk_kernel(
+    const uint16_t* __restrict__ proj, long p_stride, uint16_t* __restrict__ ring, int R,
+    const int32_t* __restrict__ pos, const uint16_t* __restrict__ cw, int KC, uint16_t* __restrict__ q,
+    uint16_t* __restrict__ k, uint16_t* __restrict__ v, uint16_t* __restrict__ a_out,
+    uint16_t* __restrict__ b_out, int T, int C, int key_dim, int Hv, int ab_off, float q_scale,
+    float k_scale, float eps) {
+  const int t = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int head = blockIdx.y * 4 + wave;      // 128-channel head index over C
+  const int c0 = head * 128 + 2 * lane;
+  if (c0 >= C) return;
+  const int W = KC - 1;  // state rows
+  const long p0 = *pos;
+  float acc0 = 0.0f, acc1 = 0.0f;
+  for (int j = 0; j < KC; ++j) {
+    const int r = t + j;   // window row
+    uint32_t p;
+    if (r < W) {
+      long rr = (p0 + r - W) % R;
+      if (rr < 0) rr += R;
+      p = *reinterpret_cast<const uint32_t*>(ring + rr * C + c0);
+    } else {
+      p = *reinterpret_cast<const uint32_t*>(proj + (size_t)(r - W) * p_stride + c0);
+    }
+    acc0 = fmaf(bf16_lo(p), bf16_to_f32(cw[(size_t)c0 * KC + j]), acc0);
+    acc1 = fmaf(bf16_hi(p), bf16_to_f32(cw[(size_t)(c0 + 1) * KC + j]), acc1);
+  }
+  {
+    long rr = (p0 + t) % R;
+    if (rr < 0) rr += R;
+    *reinterpret_cast<uint32_t*>(ring + rr * C + c0) =
+        *reinterpret_cast<const uint32_t*>(proj + (size_t)t * p_stride + c0);
+  }
+  float s0 = silu(acc0), s1 = silu(acc1);
+  if (c0 < 2 * key_dim) {
+    // q or k head: weightless RMSNorm over the 128 channels, then the scale
+    float ss = wave_allsum(s0 * s0 + s1 * s1);
+    const float inv = rsqrtf(ss / 128.0f + eps);
+    const bool isq = c0 < key_dim;
+    const float sc = isq ? q_scale : k_scale;
+    s0 = s0 * inv * sc;
+    s1 = s1 * inv * sc;
+    uint16_t* dst = isq ? q + (size_t)t * key_dim + c0 : k + (size_t)t * key_dim + (c0 - key_dim);
+    *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2(s0, s1);
+  } else {
+    const int vd = C - 2 * key_dim;
+    *reinterpret_cast<uint32_t*>(v + (size_t)t * vd + (c0 - 2 * key_dim)) = pack_bf16x2(s0, s1);
+  }
+  if (blockIdx.y == 0 && threadIdx.x < Hv) {
+    b_out[(size_t)t * Hv + threadIdx.x] = proj[(size_t)t * p_stride + ab_off + threadIdx.x];
+    a_out[(size_t)t * Hv + threadIdx.x] = proj[(size_t)t * p_stride + ab_off + Hv + threadIdx.x];
+  }
+}
+
+// ---------------------------------------------------------------- gated RMSNorm
+// out = bf16(silu(z) * bf16(w * (y * rsqrt(mean(y^2) + eps)))), rows of D = 128.
+__global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const uint16_t* __restrict__ y,
+                                                            const uint16_t* __restrict__ z, long z_stride,
+                                                            int heads, const uint16_t* __restrict__ w,
+                                                            uint16_t* __restrict__ out, int R, int D, float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= R) return;
+  const int t = row / heads, h = row % heads;
+  const uint16_t* yr = y + (size_t)row * D;
+  const uint16_t* zr = z + (size_t)t * z_stride + (size_t)h * D;
+  float ss = 0.0f;
+  for (int i = 2 * lane; i < D; i += 128) {
+    const uint32_t p = *reinterpret_cast<const uint32_t*>(yr + i);
+    ss = fmaf(bf16_lo(p), bf16_lo(p), fmaf(bf16_hi(p), bf16_hi(p), ss));
+  }
+  ss = wave_allsum(ss);
+  const float inv = rsqrtf(ss / (float)D + eps);
+  for (int i = 2 * lane; i < D; i += 128) {
+    const uint32_t p = *reinterpret_cast<const uint32_t*>(yr + i);
+    const uint32_t wp = *reinterpret_cast<const uint32_t*>(w + i);
+    const uint32_t zp = *reinterpret_cast<const uint32_t*>(zr + i);
+    const float n0 = bf16_to_f32(f32_to_bf16(bf16_lo(wp) * (bf16_lo(p) * inv)));
+    const float n1 = bf16_to_f32(f32_to_bf16(bf16_hi(wp) * (bf16_hi(p) * inv)));
+    const float z0 = bf16_lo(zp), z1 = bf16_hi(zp);
+    *reinterpret_cast<uint32_t*>(out + (size_t)row * D + i) = pack_bf16x2(silu(z0) * n0, silu(z1) * n1);
+  }
+}
+
+// ---------------------------------------------------------------- SwiGLU
+// out[l, i] = silu(gu[l, i]) * gu[l, I + i]
+__global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ out,
+                                                     int L, int I) {
+  const long n2 = (long)L * I / 2;
+  for (long p = (long)blockIdx.x * blockDim.x + threadIdx.x; p < n2; p += (long)gridDim.x * blockDim.x) {
+    const long e = 2 * p;
+    const int l = (int)(e / I), i = (int)(e % I);
+    const uint32_t g = *reinterpret_cast<const uint32_t*>(gu + (size_t)l * 2 * I + i);
+    const uint32_t u = *reinterpret_cast<const uint32_t*>(gu + (size_t)l * 2 * I + I + i);
+    *reinterpret_cast<uint32_t*>(out + e) =
+        pack_bf16x2(silu(bf16_lo(g)) * bf16_lo(u), silu(bf16_hi(g)) * bf16_hi(u));
+  }
+}
+
+__global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t* __restrict__ in, float* __restrict__ out,
+                                                          long n) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
+    out[i] = bf16_to_f32(in[i]);
+}
+
+// ---------------------------------------------------------------- attention: q/k norm + partial RoPE + KV append
+//
+// proj row l = [Hq x (q D | gate D) | Hkv x k D | Hkv x v D]. One wave per
+// (token, head); lane holds elements lane + 64 i. RoPE (NeoX form, the
+// non-traditional mx.fast.rope): for i < rot/2, (x_i, x_{i+rot/2}) rotated by
+// pos * theta^(-2i/rot); dims >= rot pass through. pos = *pos0 + l.
+__global__ __launch_bounds__(64) void qk_norm_rope_kernel(
+    const uint16_t* __restrict__ proj, long p_stride, const uint16_t* __restrict__ q_norm,
+    const uint16_t* __restrict__ k_norm, const int32_t* __restrict__ pos0, int Hq, int Hkv, int D,
+    int rot, float theta, float eps, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
+    uint16_t* __restrict__ v_cache, int cap) {
+  const int l = blockIdx.x, h = blockIdx.y;  // h < Hq: query head; else kv head h - Hq
+  const int lane = threadIdx.x;
+  const int pos = *pos0 + l;
+  const bool isq = h < Hq;
+  const int kh = h - Hq;
+  const uint16_t* src = isq ? proj + (size_t)l * p_stride + (size_t)h * 2 * D
+                            : proj + (size_t)l * p_stride + (size_t)Hq * 2 * D + (size_t)kh * D;
+  const uint16_t* nw = isq ? q_norm : k_norm;
+  const int per = D / 64;  // elements per lane (D % 64 == 0)
+  float x[8];
+  float ss = 0.0f;
+  for (int i = 0; i < per; ++i) {
+    x[i] = bf16_to_f32(src[lane + 64 * i]);
+    ss = fmaf(x[i], x[i], ss);
+  }
+  ss = wave_allsum(ss);
+  const float inv = rsqrtf(ss / (float)D + eps);
+  for (int i = 0; i < per; ++i) x[i] = bf16_to_f32(f32_to_bf16(bf16_to_f32(nw[lane + 64 * i]) * (x[i] * inv)));
+  // rotary part lives in element slot 0 (lane < 64 <= rot requires rot <= 64)
+  const int half = rot / 2;
+  if (rot > 0) {
+    const float partner = __shfl_xor(x[0], half, 64);
+    if (lane < rot) {
+      const int i = lane % half;
+      const float inv_freq = powf(theta, -2.0f * (float)i / (float)rot);
+      float sn, cs;
+      sincosf((float)pos * inv_freq, &sn, &cs);
+      x[0] = lane < half ? x[0] * cs - partner * sn : partner * sn + x[0] * cs;
+    }
+  }
+  if (isq) {
+    uint16_t* dst = q_out + ((size_t)l * Hq + h) * D;
+    for (int i = 0; i < per; ++i) dst[lane + 64 * i] = f32_to_bf16(x[i]);
+  } else if (pos >= 0 && pos < cap) {
+    uint16_t* kd = k_cache + ((size_t)kh * cap + pos) * D;
+    uint16_t* vd = v_cache + ((size_t)kh * cap + pos) * D;
+    const uint16_t* vs = proj + (size_t)l * p_stride + (size_t)Hq * 2 * D + (size_t)Hkv * D + (size_t)kh * D;
+    for (int i = 0; i < per; ++i) {
+      kd[lane + 64 * i] = f32_to_bf16(x[i]);
+      vd[lane + 64 * i] = vs[lane + 64 * i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------- attention: split-K over the cache
+//
+// Block = (kv head, query tile, key split). The tile's rows are GQ query heads x
+// QT query positions (GQ = Hq / Hkv); row r = (head g = r / QT, position
+// lq = r % QT). Query l attends keys [0, *pos0 + l]. Keys are processed 64 at a
+// time: lane j scores key j against every row (q rows staged in LDS as fp32),
+// the tile's softmax runs online per row, and P.V is accumulated with lanes
+// over head dims. Partials (m, l, o[D]) go to the workspace; the combine
+// kernel merges splits, normalises, applies sigmoid(gate) and writes bf16.
+constexpr int ATT_KT = 64;
+
+template <int D, int ROWS>
+__global__ __launch_bounds__(256) void attn_partial_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
+    const int32_t* __restrict__ pos0, int L, int Hq, int Hkv, int cap, int QT, int keys_per_split,
+    float scale, float* __restrict__ ws) {
+  constexpr int PER = D / 64;
+  const int kh = blockIdx.x;
+  const int tile = blockIdx.y;
+  const int split = blockIdx.z;
+  const int GQ = Hq / Hkv;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __shared__ float qs[ROWS][D];
+  __shared__ float ps[4][ROWS][ATT_KT];
+  const int p0 = *pos0;
+  const int rows = GQ * QT;
+  // stage q rows (fp32, pre-scaled)
+  for (int idx = threadIdx.x; idx < ROWS * D; idx += 256) {
+    const int r = idx / D, d = idx % D;
+    float val = 0.0f;
+    if (r < rows) {
+      const int g = r / QT, lq = tile * QT + r % QT;
+      if (lq < L) val = bf16_to_f32(q[((size_t)lq * Hq + kh * GQ + g) * D + d]) * scale;
+    }
+    qs[r][d] = val;
+  }
+  __syncthreads();
+  const int kend_tile = p0 + min(L, (tile + 1) * QT);      // exclusive bound over the tile's rows
+  const int k_lo = split * keys_per_split;
+  const int k_hi = min(k_lo + keys_per_split, kend_tile);
+  // each wave takes key blocks k_lo + (wave + 4 i) * 64
+  float m_r[ROWS], l_r[ROWS], o_r[ROWS][PER];
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+    m_r[r] = -INFINITY;
+    l_r[r] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) o_r[r][e] = 0.0f;
+  }
+  for (int kb = k_lo + wave * ATT_KT; kb < k_hi; kb += 4 * ATT_KT) {
+    const int key = kb + lane;
+    const bool kv = key < k_hi;
+    float sc[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) sc[r] = 0.0f;
+    if (kv) {
+      const uint16_t* kp = k_cache + ((size_t)kh * cap + key) * D;
+      for (int d = 0; d < D; d += 8) {
+        const u32x4 kk = load16(kp + d);
+        const float kf[8] = {bf16_lo(kk.x), bf16_hi(kk.x), bf16_lo(kk.y), bf16_hi(kk.y),
+                             bf16_lo(kk.z), bf16_hi(kk.z), bf16_lo(kk.w), bf16_hi(kk.w)};
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sc[r] = fmaf(qs[r][d + e], kf[e], sc[r]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      const int lq = tile * QT + r % QT;
+      const bool ok = kv && r < rows && lq < L && key <= p0 + lq;
+      const float s = ok ? sc[r] : -INFINITY;
+      const float mt = wave_allmax(s);
+      const float mnew = fmaxf(m_r[r], mt);
+      const float p = ok ? expf(s - mnew) : 0.0f;
+      const float corr = (m_r[r] == -INFINITY) ? 0.0f : expf(m_r[r] - mnew);
+      l_r[r] = l_r[r] * corr + wave_allsum(p);
+      m_r[r] = mnew;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) o_r[r][e] *= corr;
+      ps[wave][r][lane] = p;
+    }
+    // P.V: lane owns dims lane + 64 e
+    const int nk = min(ATT_KT, k_hi - kb);
+    for (int j = 0; j < nk; ++j) {
+      const uint16_t* vp = v_cache + ((size_t)kh * cap + kb + j) * D;
+      float vf[PER];
+#pragma unroll
+      for (int e = 0; e < PER; ++e) vf[e] = bf16_to_f32(vp[lane + 64 * e]);
+#pragma unroll
+      for (int r = 0; r < ROWS; ++r) {
+        const float p = ps[wave][r][j];
+#pragma unroll
+        for (int e = 0; e < PER; ++e) o_r[r][e] = fmaf(p, vf[e], o_r[r][e]);
+      }
+    }
+  }
+  // merge the 4 waves through LDS, then write the block's partial per row
+  __shared__ float mw[4][ROWS], lw[4][ROWS];
+  if (lane == 0)
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) { mw[wave][r] = m_r[r]; lw[wave][r] = l_r[r]; }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+    float m = fmaxf(fmaxf(mw[0][r], mw[1][r]), fmaxf(mw[2][r], mw[3][r]));
+    float lsum = 0.0f;
+    float c[4];
+#pragma unroll
+    for (int wv = 0; wv < 4; ++wv) {
+      c[wv] = (mw[wv][r] == -INFINITY) ? 0.0f : expf(mw[wv][r] - m);
+      lsum += lw[wv][r] * c[wv];
+    }
+    // o: sum over waves via atomic-free staged adds in LDS (ps reused as [D])
+    __syncthreads();
+    float* acc = &ps[0][0][0];  // 4*ROWS*64 floats >= D floats
+    for (int e = 0; e < PER; ++e)
+      if (wave == 0) acc[lane + 64 * e] = o_r[r][e] * c[0];
+    __syncthreads();
+    for (int wv = 1; wv < 4; ++wv) {
+      if (wave == wv)
+        for (int e = 0; e < PER; ++e) acc[lane + 64 * e] += o_r[r][e] * c[wv];
+      __syncthreads();
+    }
+    if (r < rows) {
+      float* dst = ws + ((((size_t)kh * gridDim.y + tile) * gridDim.z + split) * ROWS + r) * (D + 2);
+      if (threadIdx.x == 0) { dst[0] = m; dst[1] = lsum; }
+      for (int d = threadIdx.x; d < D; d += 256) dst[2 + d] = acc[d];
+    }
+    __syncthreads();
+  }
+}
+
+// out[lq, (kh*GQ + g)*D + d] = bf16(sigmoid(gate) * sum_s o_s e^{m_s-m} / sum_s l_s e^{m_s-m})
+template <int D, int ROWS>
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ ws, int nsplit, int ntile,
+                                                           int L, int Hq, int Hkv, int QT,
+                                                           const uint16_t* __restrict__ gate, long g_stride,
+                                                           uint16_t* __restrict__ out) {
+  const int kh = blockIdx.x, tile = blockIdx.y, r = blockIdx.z;
+  const int GQ = Hq / Hkv;
+  if (r >= GQ * QT) return;
+  const int g = r / QT, lq = tile * QT + r % QT;
+  if (lq >= L) return;
+  const int h = kh * GQ + g;
+  float m = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) {
+    const float* p = ws + ((((size_t)kh * ntile + tile) * nsplit + s) * ROWS + r) * (D + 2);
+    m = fmaxf(m, p[0]);
+  }
+  float lsum = 0.0f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float* p = ws + ((((size_t)kh * ntile + tile) * nsplit + s) * ROWS + r) * (D + 2);
+    if (p[0] != -INFINITY) lsum += p[1] * expf(p[0] - m);
+  }
+  const float invl = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float o = 0.0f;
+    for (int s = 0; s < nsplit; ++s) {
+      const float* p = ws + ((((size_t)kh * ntile + tile) * nsplit + s) * ROWS + r) * (D + 2);
+      if (p[0] != -INFINITY) o = fmaf(p[2 + d], expf(p[0] - m), o);
+    }
+    const float gt = bf16_to_f32(gate[(size_t)lq * g_stride + (size_t)h * 2 * D + D + d]);
+    out[(size_t)lq * Hq * D + (size_t)h * D + d] = f32_to_bf16(o * invl * sigmoidf_(gt));
+  }
+}
+
+// counters[i] += n_accept[0] + 1 for every i (advance all caches past the kept tokens)
+__global__ void commit_kernel(int32_t* __restrict__ counters, int n, const int32_t* __restrict__ n_accept,
+                              int extra) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) counters[i] += n_accept[0] + extra;
+}
+
+}  // namespace
+
+// ================================================================ C ABI
+
+extern "C" int qvex_embed_w4g64(const int32_t* ids, int L, const uint32_t* w, const uint16_t* scales,
+                                const uint16_t* biases, int V, int H, uint16_t* out, void* stream) {
+  QVEX_CHECK_ARG(ids && w && scales && biases && out, "qvex_embed_w4g64: null pointer");
+  QVEX_CHECK_ARG(L >= 1 && V >= 1 && H >= 64 && H % 64 == 0, "qvex_embed_w4g64: L=%d V=%d H=%d", L, V, H);
+  QVEX_CHECK_ARG(qvex_aligned(out, 16) && qvex_aligned(w, 4), "qvex_embed_w4g64: out must be 16-byte aligned");
+  hipLaunchKernelGGL(embed_kernel, dim3(L), dim3(256), 0, (hipStream_t)stream, ids, w, scales, biases, out, V, H);
+  QVEX_CHECK_LAUNCH("qvex_embed_w4g64");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_rmsnorm(const uint16_t* x, long x_stride, const uint16_t* w, uint16_t* out, long out_stride,
+                            int R, int D, float eps, float scale, void* stream) {
+  QVEX_CHECK_ARG(x && out, "qvex_rmsnorm: null pointer");
+  QVEX_CHECK_ARG(R >= 1 && D >= 2 && D % 2 == 0 && x_stride >= D && out_stride >= D && x_stride % 2 == 0 &&
+                     out_stride % 2 == 0,
+                 "qvex_rmsnorm: R=%d D=%d strides %ld/%ld", R, D, x_stride, out_stride);
+  hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3((R + 3) / 4), dim3(256), 0, (hipStream_t)stream, x, x_stride,
+                     (const uint16_t*)nullptr, 0L, (uint16_t*)nullptr, 0L, w, out, out_stride, R, D, eps, scale);
+  QVEX_CHECK_LAUNCH("qvex_rmsnorm");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_add_rmsnorm(const uint16_t* x, const uint16_t* delta, uint16_t* h_out, const uint16_t* w,
+                                uint16_t* out, int R, int D, float eps, void* stream) {
+  QVEX_CHECK_ARG(x && delta && h_out && out, "qvex_add_rmsnorm: null pointer");
+  QVEX_CHECK_ARG(R >= 1 && D >= 2 && D % 2 == 0, "qvex_add_rmsnorm: R=%d D=%d", R, D);
+  hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3((R + 3) / 4), dim3(256), 0, (hipStream_t)stream, x, (long)D, delta,
+                     (long)D, h_out, (long)D, w, out, (long)D, R, D, eps, 1.0f);
+  QVEX_CHECK_LAUNCH("qvex_add_rmsnorm");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_gdn_conv_qk(const uint16_t* proj, long p_stride, uint16_t* conv_ring, int ring_rows,
+                                const int32_t* pos, const uint16_t* conv_w, int kernel_size, uint16_t* q,
+                                uint16_t* k, uint16_t* v, uint16_t* a_out, uint16_t* b_out, int T, int C,
+                                int key_dim, int Hv, int ab_offset, float q_scale, float k_scale, float eps,
+                                void* stream) {
+  QVEX_CHECK_ARG(proj && conv_ring && pos && conv_w && q && k && v && a_out && b_out,
+                 "qvex_gdn_conv_qk: null pointer");
+  QVEX_CHECK_ARG(T >= 1 && kernel_size >= 2 && C % 512 == 0 && key_dim % 128 == 0 && 2 * key_dim < C &&
+                     Hv >= 1 && Hv <= 256 && ab_offset + 2 * Hv <= p_stride,
+                 "qvex_gdn_conv_qk: T=%d K=%d C=%d key_dim=%d Hv=%d", T, kernel_size, C, key_dim, Hv);
+  QVEX_CHECK_ARG(ring_rows >= T + kernel_size - 1, "qvex_gdn_conv_qk: ring_rows=%d < T + K - 1 = %d", ring_rows,
+                 T + kernel_size - 1);
+  hipLaunchKernelGGL(conv_silu_qk_kernel, dim3(T, C / 512), dim3(256), 0, (hipStream_t)stream, proj, p_stride,
+                     conv_ring, ring_rows, pos, conv_w, kernel_size, q, k, v, a_out, b_out, T, C, key_dim, Hv,
+                     ab_offset, q_scale, k_scale, eps);
+  QVEX_CHECK_LAUNCH("qvex_gdn_conv_qk");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_gated_rmsnorm(const uint16_t* y, const uint16_t* z, long z_stride, int heads, const uint16_t* w,
+                                  uint16_t* out, int R, int D, float eps, void* stream) {
+  QVEX_CHECK_ARG(y && z && w && out, "qvex_gated_rmsnorm: null pointer");
+  QVEX_CHECK_ARG(R >= 1 && D >= 2 && D % 2 == 0 && heads >= 1 && R % heads == 0, "qvex_gated_rmsnorm: R=%d D=%d", R, D);
+  hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3((R + 3) / 4), dim3(256), 0, (hipStream_t)stream, y, z, z_stride,
+                     heads, w, out, R, D, eps);
+  QVEX_CHECK_LAUNCH("qvex_gated_rmsnorm");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_swiglu(const uint16_t* gu, uint16_t* out, int L, int I, void* stream) {
+  QVEX_CHECK_ARG(gu && out && L >= 1 && I >= 2 && I % 2 == 0, "qvex_swiglu: L=%d I=%d", L, I);
+  const long n2 = (long)L * I / 2;
+  const int blocks = (int)std::min<long>((n2 + 255) / 256, 4096);
+  hipLaunchKernelGGL(swiglu_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, gu, out, L, I);
+  QVEX_CHECK_LAUNCH("qvex_swiglu");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_bf16_to_f32(const uint16_t* in, float* out, long n, void* stream) {
+  QVEX_CHECK_ARG(in && out && n >= 1, "qvex_bf16_to_f32: n=%ld", n);
+  const int blocks = (int)std::min<long>((n + 255) / 256, 8192);
+  hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, in, out, n);
+  QVEX_CHECK_LAUNCH("qvex_bf16_to_f32");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_attn_qk_rope(const uint16_t* proj, long p_stride, const uint16_t* q_norm, const uint16_t* k_norm,
+                                 const int32_t* pos0, int L, int Hq, int Hkv, int D, int rot_dim, float theta,
+                                 float eps, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, int cap,
+                                 void* stream) {
+  QVEX_CHECK_ARG(proj && q_norm && k_norm && pos0 && q_out && k_cache && v_cache, "qvex_attn_qk_rope: null pointer");
+  QVEX_CHECK_ARG(L >= 1 && Hq >= 1 && Hkv >= 1 && Hq % Hkv == 0 && D % 64 == 0 && D <= 512 && rot_dim >= 0 &&
+                     rot_dim <= 64 && rot_dim % 2 == 0 && cap >= 1,
+                 "qvex_attn_qk_rope: L=%d Hq=%d Hkv=%d D=%d rot=%d", L, Hq, Hkv, D, rot_dim);
+  QVEX_CHECK_ARG(p_stride >= (long)Hq * 2 * D + 2L * Hkv * D, "qvex_attn_qk_rope: p_stride too small");
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(L, Hq + Hkv), dim3(64), 0, (hipStream_t)stream, proj, p_stride,
+                     q_norm, k_norm, pos0, Hq, Hkv, D, rot_dim, theta, eps, q_out, k_cache, v_cache, cap);
+  QVEX_CHECK_LAUNCH("qvex_attn_qk_rope");
+  return QVEX_OK;
+}
+
+namespace {
+constexpr int ATT_ROWS = 16;
+}
+
+extern "C" uint64_t qvex_attn_workspace_bytes(int L, int Hq, int Hkv, int D, int max_keys, int keys_per_split) {
+  if (L < 1 || Hkv < 1 || Hq % Hkv || keys_per_split < 1) return 0;
+  const int GQ = Hq / Hkv;
+  const int QT = ATT_ROWS / GQ < 1 ? 1 : ATT_ROWS / GQ;
+  const int ntile = (L + QT - 1) / QT;
+  const int nsplit = (max_keys + keys_per_split - 1) / keys_per_split;
+  return (uint64_t)Hkv * ntile * nsplit * ATT_ROWS * (D + 2) * sizeof(float);
+}
+
+extern "C" int qvex_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                              const int32_t* pos0, int L, int Hq, int Hkv, int D, int cap, int max_keys,
+                              int keys_per_split, const uint16_t* gate, long gate_stride, uint16_t* out,
+                              void* workspace, uint64_t workspace_bytes, void* stream) {
+  QVEX_CHECK_ARG(q && k_cache && v_cache && pos0 && gate && out && workspace, "qvex_attention: null pointer");
+  QVEX_CHECK_ARG(L >= 1 && Hkv >= 1 && Hq % Hkv == 0 && Hq / Hkv <= ATT_ROWS, "qvex_attention: Hq=%d Hkv=%d", Hq, Hkv);
+  QVEX_CHECK_ARG(D == 256 || D == 128, "qvex_attention: D=%d (128 or 256 supported)", D);
+  QVEX_CHECK_ARG(max_keys >= 1 && max_keys <= cap && keys_per_split >= ATT_KT && keys_per_split % ATT_KT == 0,
+                 "qvex_attention: max_keys=%d cap=%d keys_per_split=%d", max_keys, cap, keys_per_split);
+  const uint64_t need = qvex_attn_workspace_bytes(L, Hq, Hkv, D, max_keys, keys_per_split);
+  QVEX_CHECK_ARG(workspace_bytes >= need, "qvex_attention: workspace %llu < %llu bytes",
+                 (unsigned long long)workspace_bytes, (unsigned long long)need);
+  const int GQ = Hq / Hkv;
+  const int QT = ATT_ROWS / GQ;
+  const int ntile = (L + QT - 1) / QT;
+  const int nsplit = (max_keys + keys_per_split - 1) / keys_per_split;
+  QVEX_CHECK_ARG(ntile <= 65535 && nsplit <= 65535, "qvex_attention: grid too large");
+  const float scale = 1.0f / sqrtf((float)D);
+  hipStream_t st = (hipStream_t)stream;
+  if (D == 256) {
+    hipLaunchKernelGGL((attn_partial_kernel<256, ATT_ROWS>), dim3(Hkv, ntile, nsplit), dim3(256), 0, st, q, k_cache,
+                       v_cache, pos0, L, Hq, Hkv, cap, QT, keys_per_split, scale, (float*)workspace);
+    QVEX_CHECK_LAUNCH("qvex_attention/partial");
+    hipLaunchKernelGGL((attn_combine_kernel<256, ATT_ROWS>), dim3(Hkv, ntile, ATT_ROWS), dim3(256), 0, st,
+                       (const float*)workspace, nsplit, ntile, L, Hq, Hkv, QT, gate, gate_stride, out);
+  } else {
+    hipLaunchKernelGGL((attn_partial_kernel<128, ATT_ROWS>), dim3(Hkv, ntile, nsplit), dim3(256), 0, st, q, k_cache,
+                       v_cache, pos0, L, Hq, Hkv, cap, QT, keys_per_split, scale, (float*)workspace);
+    QVEX_CHECK_LAUNCH("qvex_attention/partial");
+    hipLaunchKernelGGL((attn_combine_kernel<128, ATT_ROWS>), dim3(Hkv, ntile, ATT_ROWS), dim3(256), 0, st,
+                       (const float*)workspace, nsplit, ntile, L, Hq, Hkv, QT, gate, gate_stride, out);
+  }
+  QVEX_CHECK_LAUNCH("qvex_attention/combine");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_commit_step(int32_t* counters, int n, const int32_t* n_accept, int extra, void* stream) {
+  QVEX_CHECK_ARG(counters && n_accept && n >= 1, "qvex_commit_step: null pointer or n=%d", n);
+  hipLaunchKernelGGL(commit_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, counters, n, n_accept,
+                     extra);
+  QVEX_CHECK_LAUNCH("qvex_commit_step");
+  return QVEX_OK;
+}

@@ -500,14 +500,15 @@ int launch_mfma(const uint16_t* x, const uint32_t* w, const uint16_t* scales, co
   return QVEX_OK;
 }
 
-// Default tile: rows per wave shrink as M grows (x pairs cost 16*M VGPRs);
-// K is split across waves when the row groups alone cannot fill 256 CUs.
+// Default tile: rows per wave shrink as M grows (x pairs cost 16*M VGPRs); the
+// K split depends on (N, K) only, so a row's summation order - and its bits -
+// do not change with the number of activation rows.
 void default_tile(int M, int N, int K, int* R, int* KS) {
-  int r = M <= 2 ? 4 : (M <= 4 ? 4 : 2);
+  const int r = M <= 4 ? 4 : 2;
   const int nchunk = K / 32;
   int ks = 1;
   const long target_waves = 4096;  // 16 waves per CU on 256 CUs
-  while (ks < 4 && (long)((N + r - 1) / r) * ks < target_waves && nchunk >= 64 * ks * 2) ks *= 2;
+  while (ks < 4 && (long)((N + 3) / 4) * ks < target_waves && nchunk >= 64 * ks * 2) ks *= 2;
   *R = r;
   *KS = ks;
 }

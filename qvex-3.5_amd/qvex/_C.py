@@ -15,6 +15,7 @@ P = ctypes.c_void_p
 I = ctypes.c_int
 U64 = ctypes.c_uint64
 F = ctypes.c_float
+LNG = ctypes.c_long
 
 # name -> argtypes (all return int status)
 SIGNATURES: dict[str, list] = {
@@ -23,8 +24,18 @@ SIGNATURES: dict[str, list] = {
     "qvex_read_roof": [P, U64, P, I, P],
     "qvex_qmv_w4g64_mfma": [P, P, P, P, P, I, I, I, I, I, P],
     "qvex_gdn_recurrent": [P, P, P, P, P, P, P, P, P, I, P, I, I, I, I, I, I, P],
-    "qvex_gdn_recurrent_ring": [P, P, P, P, P, P, P, P, I, P, P, I, I, I, I, I, I, P],
+    "qvex_gdn_recurrent_ring": [P, P, P, P, P, P, P, P, I, P, I, P, I, I, I, I, I, I, P],
     "qvex_spec_accept": [P, P, P, P, P, F, P, P, I, I, I, P, U64, P],
+    "qvex_embed_w4g64": [P, I, P, P, P, I, I, P, P],
+    "qvex_rmsnorm": [P, LNG, P, P, LNG, I, I, F, F, P],
+    "qvex_add_rmsnorm": [P, P, P, P, P, I, I, F, P],
+    "qvex_gdn_conv_qk": [P, LNG, P, I, P, P, I, P, P, P, P, P, I, I, I, I, I, F, F, F, P],
+    "qvex_commit_step": [P, I, P, I, P],
+    "qvex_gated_rmsnorm": [P, P, LNG, I, P, P, I, I, F, P],
+    "qvex_swiglu": [P, P, I, I, P],
+    "qvex_bf16_to_f32": [P, P, LNG, P],
+    "qvex_attn_qk_rope": [P, LNG, P, P, P, I, I, I, I, I, F, F, P, P, P, I, P],
+    "qvex_attention": [P, P, P, P, I, I, I, I, I, I, I, P, LNG, P, P, U64, P],
 }
 
 _lib: ctypes.CDLL | None = None
@@ -47,6 +58,8 @@ def lib() -> ctypes.CDLL:
         L.qvex_abi_version.argtypes = []
         L.qvex_spec_accept_workspace_bytes.restype = U64
         L.qvex_spec_accept_workspace_bytes.argtypes = [I, I, I, I]
+        L.qvex_attn_workspace_bytes.restype = U64
+        L.qvex_attn_workspace_bytes.argtypes = [I, I, I, I, I, I]
         for name, args in SIGNATURES.items():
             fn = getattr(L, name)
             fn.argtypes = args
@@ -64,4 +77,5 @@ def call(name: str, *args) -> None:
 
 
 def exported_symbols() -> list[str]:
-    return ["qvex_last_error", "qvex_abi_version", "qvex_spec_accept_workspace_bytes", *SIGNATURES]
+    return ["qvex_last_error", "qvex_abi_version", "qvex_spec_accept_workspace_bytes",
+            "qvex_attn_workspace_bytes", *SIGNATURES]

@@ -139,17 +139,18 @@ def gated_delta(q, k, v, a, b, A_log, dt_bias, state, keep_mid=False):
     return y, out[0]
 
 
-def gated_delta_ring(q, k, v, a, b, A_log, dt_bias, ring, cur_slot, y=None):
-    """Ring-buffer form: state read from ring[cur_slot], the state after token t
-    written to ring[(cur_slot + 1 + t) % n_slots]; cur_slot is a device int32."""
+def gated_delta_ring(q, k, v, a, b, A_log, dt_bias, ring, cur_slot, y=None, snap_every=True):
+    """Ring-buffer form: with c = cur_slot mod n_slots (cur_slot a device int32),
+    the state is read from ring[c] and the state after token t is written to
+    ring[(c + 1 + t) % n_slots] (only the last token's unless snap_every)."""
     B, T, Hk, Hv, Dk, Dv = _gdn_check(q, k, v, a, b, A_log, dt_bias)
     _check(ring, "ring", torch.float32)
     _check(cur_slot, "cur_slot", torch.int32)
     if y is None:
         y = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=q.device)
     _C.call("qvex_gdn_recurrent_ring", _ptr(q), _ptr(k), _ptr(v), _ptr(a), _ptr(b), _ptr(A_log),
-            _ptr(dt_bias), _ptr(ring), ring.shape[0], _ptr(cur_slot), _ptr(y), B, T, Hk, Hv, Dk, Dv,
-            _stream())
+            _ptr(dt_bias), _ptr(ring), ring.shape[0], _ptr(cur_slot), int(bool(snap_every)), _ptr(y),
+            B, T, Hk, Hv, Dk, Dv, _stream())
     return y
 
 

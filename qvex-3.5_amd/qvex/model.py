@@ -1,0 +1,539 @@
+"""Qwen3.5 hybrid stack (dense, text-only) on the qvex HIP kernels.
+
+Mirror of engine/model.py: Config, QLinear, QEmbedding, KVCache,
+RecurrentCache, Attention, GatedDeltaNet, MLP, Layer, Qwen35 keep the
+reference's names, call signatures and cache API (make_cache, rollback(n),
+state(), offset). Every op runs in libqvex.so; torch only holds device memory.
+
+MI355X-specific state layout (what makes rollback free):
+  * every cache of a model shares one device int32 table ``CacheCounters``:
+    entry i is layer i's token count, which all position-dependent kernels read
+    on the device (RoPE position / KV append slot, conv-ring row, DeltaNet
+    ring slot);
+  * KVCache: bf16 [Hkv, cap, D] preallocated to the context capacity;
+  * RecurrentCache: conv history ring [R, conv_dim] bf16 (R >= max verify
+    width + K - 1) and a DeltaNet state ring [S, Hv, Dv, Dk] fp32 with a state
+    snapshot per verify token;
+  so rollback(n) is ``offset -= n`` for every cache kind, any n <= the last
+  call's width (the reference allows n = 1 for recurrent caches only,
+  engine/model.py:189-193).
+"""
+
+from __future__ import annotations
+
+import json
+import math
+from dataclasses import dataclass, field
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from . import _C, kernels
+from .kernels import _ptr, _stream
+
+QMV_MAX_ROWS = 8
+
+
+# ---------------------------------------------------------------- config
+
+@dataclass
+class Config:
+    hidden_size: int
+    intermediate_size: int
+    num_hidden_layers: int
+    num_attention_heads: int
+    num_key_value_heads: int
+    head_dim: int
+    linear_num_key_heads: int
+    linear_num_value_heads: int
+    linear_key_head_dim: int
+    linear_value_head_dim: int
+    linear_conv_kernel_dim: int
+    full_attention_interval: int
+    rms_norm_eps: float
+    vocab_size: int
+    rope_theta: float
+    rotary_dim: int
+    group_size: int
+    bits: int
+    quant: dict = field(default_factory=dict)
+
+    @classmethod
+    def from_file(cls, path: Path) -> "Config":
+        """Same parsing as engine/model.py:39-66 (text_config, rope_parameters,
+        quantization overrides with the language_model. prefix stripped)."""
+        raw = json.loads(Path(path).read_text())
+        t = raw.get("text_config", raw)
+        rope = t.get("rope_parameters") or {}
+        q = raw.get("quantization") or raw.get("quantization_config") or {}
+        head_dim = t.get("head_dim") or t["hidden_size"] // t["num_attention_heads"]
+        return cls(
+            hidden_size=t["hidden_size"], intermediate_size=t["intermediate_size"],
+            num_hidden_layers=t["num_hidden_layers"], num_attention_heads=t["num_attention_heads"],
+            num_key_value_heads=t["num_key_value_heads"], head_dim=head_dim,
+            linear_num_key_heads=t["linear_num_key_heads"], linear_num_value_heads=t["linear_num_value_heads"],
+            linear_key_head_dim=t["linear_key_head_dim"], linear_value_head_dim=t["linear_value_head_dim"],
+            linear_conv_kernel_dim=t["linear_conv_kernel_dim"],
+            full_attention_interval=t.get("full_attention_interval", 4),
+            rms_norm_eps=t["rms_norm_eps"], vocab_size=t["vocab_size"],
+            rope_theta=rope.get("rope_theta", t.get("rope_theta", 10_000_000)),
+            rotary_dim=int(head_dim * rope.get("partial_rotary_factor", 0.25)),
+            group_size=q.get("group_size", 64), bits=q.get("bits", 4),
+            quant={k.removeprefix("language_model."): v for k, v in q.items() if isinstance(v, dict)},
+        )
+
+    @classmethod
+    def qwen35_9b(cls) -> "Config":
+        """Qwen3.5-9B text shape: 32 layers (every 4th full attention), hidden 4096,
+        MLP 12288, vocab 248320, GDN 16 key / 32 value heads of 128, attention 16 q /
+        4 kv heads of 256, conv kernel 4, partial rotary 64 of 256."""
+        return cls(hidden_size=4096, intermediate_size=12288, num_hidden_layers=32,
+                   num_attention_heads=16, num_key_value_heads=4, head_dim=256,
+                   linear_num_key_heads=16, linear_num_value_heads=32, linear_key_head_dim=128,
+                   linear_value_head_dim=128, linear_conv_kernel_dim=4, full_attention_interval=4,
+                   rms_norm_eps=1e-6, vocab_size=248320, rope_theta=10_000_000.0, rotary_dim=64,
+                   group_size=64, bits=4)
+
+    @classmethod
+    def tiny(cls, layers: int = 4, vocab: int = 4096) -> "Config":
+        """Small shape with the same head geometry rules, for parity tests."""
+        return cls(hidden_size=512, intermediate_size=1024, num_hidden_layers=layers,
+                   num_attention_heads=4, num_key_value_heads=2, head_dim=128,
+                   linear_num_key_heads=2, linear_num_value_heads=4, linear_key_head_dim=128,
+                   linear_value_head_dim=128, linear_conv_kernel_dim=4, full_attention_interval=4,
+                   rms_norm_eps=1e-6, vocab_size=vocab, rope_theta=10_000_000.0, rotary_dim=32,
+                   group_size=64, bits=4)
+
+    def qparams(self, module: str) -> tuple[int, int]:
+        o = self.quant.get(module, {})
+        return o.get("group_size", self.group_size), o.get("bits", self.bits)
+
+    def is_linear(self, i: int) -> bool:
+        return (i + 1) % self.full_attention_interval != 0
+
+
+# ---------------------------------------------------------------- building blocks
+
+class QLinear:
+    """Affine-quantized linear layer, y = x @ dequant(W)^T (engine/model.py:80-104).
+
+    w: int32 [N, K/8] (uint32 words), scales, biases: bf16 [N, K/64]."""
+
+    def __init__(self, w, scales, biases, group_size=64, bits=4):
+        if group_size != 64 or bits != 4:
+            raise _C.QvexError(f"QLinear: only 4-bit group-64 weights are implemented (got {bits}/{group_size})")
+        self.w, self.scales, self.biases = w, scales, biases
+        self.group_size, self.bits = group_size, bits
+        self.N = w.shape[0]
+        self.K = w.shape[1] * 8
+
+    def __call__(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, self.K)
+        M = x2.shape[0]
+        if out is None:
+            out = torch.empty((M, self.N), dtype=torch.bfloat16, device=x.device)
+        o2 = out.view(M, self.N)
+        for m0 in range(0, M, QMV_MAX_ROWS):
+            m1 = min(M, m0 + QMV_MAX_ROWS)
+            kernels.quantized_matmul(x2[m0:m1], self.w, self.scales, self.biases, out=o2[m0:m1])
+        return out.view(*lead, self.N)
+
+    @staticmethod
+    def fuse(layers: list["QLinear"]) -> "QLinear":
+        """Stack output rows of layers sharing the input (lossless, engine/model.py:93-104)."""
+        l0 = layers[0]
+        assert all((l.group_size, l.bits) == (l0.group_size, l0.bits) for l in layers), \
+            "fused layers must share the quantization (bits, group size)"
+        return QLinear(torch.cat([l.w for l in layers]), torch.cat([l.scales for l in layers]),
+                       torch.cat([l.biases for l in layers]), l0.group_size, l0.bits)
+
+
+class QEmbedding:
+    """Quantized embedding rows, dequantized on gather (engine/model.py:121-130)."""
+
+    def __init__(self, w, scales, biases, group_size=64, bits=4):
+        self.w, self.scales, self.biases = w, scales, biases
+        self.group_size, self.bits = group_size, bits
+        self.V, self.H = w.shape[0], w.shape[1] * 8
+
+    def __call__(self, ids: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        ids1 = ids.reshape(-1).to(torch.int32).contiguous()
+        L = ids1.numel()
+        if out is None:
+            out = torch.empty((L, self.H), dtype=torch.bfloat16, device=ids.device)
+        _C.call("qvex_embed_w4g64", _ptr(ids1), L, _ptr(self.w), _ptr(self.scales), _ptr(self.biases),
+                self.V, self.H, _ptr(out), _stream())
+        return out
+
+
+def rms_norm(x: torch.Tensor, w: torch.Tensor | None, eps: float, out=None, scale: float = 1.0):
+    """mx.fast.rms_norm over the last dim (weight optional)."""
+    D = x.shape[-1]
+    x2 = x.reshape(-1, D)
+    if out is None:
+        out = torch.empty_like(x2)
+    o2 = out.reshape(-1, out.shape[-1]) if out.dim() > 1 else out
+    _C.call("qvex_rmsnorm", _ptr(x2), x2.stride(0), _ptr(w) if w is not None else None, _ptr(o2),
+            o2.stride(0), x2.shape[0], D, float(eps), float(scale), _stream())
+    return out
+
+
+def add_rms_norm(x, delta, w, eps, h_out=None, out=None):
+    """h = x + delta (bf16), n = rms_norm(h) * w; returns (h, n)."""
+    R, D = x.reshape(-1, x.shape[-1]).shape
+    h_out = torch.empty_like(x) if h_out is None else h_out
+    out = torch.empty_like(x) if out is None else out
+    _C.call("qvex_add_rmsnorm", _ptr(x), _ptr(delta), _ptr(h_out), _ptr(w), _ptr(out), R, D, float(eps), _stream())
+    return h_out, out
+
+
+# ---------------------------------------------------------------- caches
+
+class CacheCounters:
+    """Device int32 table of per-cache token counts (one entry per cache), with a
+    host mirror. Kernels read the device copy; ``sync()`` uploads host edits."""
+
+    def __init__(self, n: int, device):
+        self.host = np.zeros(n, np.int32)
+        self.dev = torch.zeros(n, dtype=torch.int32, device=device)
+        self.dirty = False
+
+    def get(self, i: int) -> int:
+        return int(self.host[i])
+
+    def set(self, i: int, v: int) -> None:
+        self.host[i] = v
+        self.dirty = True
+
+    def sync(self) -> None:
+        if self.dirty:
+            # from pageable memory: the runtime stages the bytes before returning,
+            # so later host edits cannot race the copy
+            self.dev.copy_(torch.from_numpy(self.host.copy()))
+            self.dirty = False
+
+    def ptr(self, i: int) -> int:
+        return self.dev.data_ptr() + 4 * i
+
+
+class KVCache:
+    """bf16 K/V [Hkv, cap, D], preallocated (engine/model.py:149-176 grows in
+    256-token steps instead). rollback(n) is offset -= n."""
+
+    step = 256
+
+    def __init__(self, counters: CacheCounters | None = None, index: int = 0, *, n_kv: int = 0,
+                 head_dim: int = 0, capacity: int = 0, device=None):
+        if counters is None:
+            counters = CacheCounters(1, device)
+            index = 0
+        self.counters, self.index = counters, index
+        self.capacity = int(math.ceil(max(capacity, 1) / self.step) * self.step)
+        self.k = torch.zeros((n_kv, self.capacity, head_dim), dtype=torch.bfloat16, device=device)
+        self.v = torch.zeros_like(self.k)
+
+    @property
+    def offset(self) -> int:
+        return self.counters.get(self.index)
+
+    @offset.setter
+    def offset(self, v: int) -> None:
+        self.counters.set(self.index, v)
+
+    def state(self):
+        return [self.k, self.v]
+
+    def rollback(self, n=1):
+        self.offset -= n  # entries past offset are overwritten by the next append
+
+
+class RecurrentCache:
+    """GDN caches: conv history ring and DeltaNet state ring, both indexed by
+    the layer's token count, so ``rollback(n)`` (n <= last call width) only
+    moves the counter. ``conv``/``ssm`` give the current state like the
+    reference's fields (engine/model.py:179-193)."""
+
+    def __init__(self, counters: CacheCounters, index: int, *, conv_dim: int, kernel: int, hv: int,
+                 dv: int, dk: int, max_width: int, device, prefill_width: int = 64):
+        self.counters, self.index = counters, index
+        self.kernel = kernel
+        self.ring_rows = max(max_width, prefill_width) + kernel - 1
+        self.conv_ring = torch.zeros((self.ring_rows, conv_dim), dtype=torch.bfloat16, device=device)
+        self.n_slots = max_width + 1
+        self.ssm_ring = torch.zeros((self.n_slots, 1, hv, dv, dk), dtype=torch.float32, device=device)
+        self.last_width = 0
+
+    @property
+    def offset(self) -> int:
+        return self.counters.get(self.index)
+
+    @offset.setter
+    def offset(self, v: int) -> None:
+        self.counters.set(self.index, v)
+
+    @property
+    def ssm(self) -> torch.Tensor:
+        return self.ssm_ring[self.offset % self.n_slots]
+
+    @property
+    def conv(self) -> torch.Tensor:
+        p, W, R = self.offset, self.kernel - 1, self.ring_rows
+        rows = [(p - W + j) % R for j in range(W)]
+        return self.conv_ring[rows]
+
+    def state(self):
+        return [self.conv_ring, self.ssm_ring]
+
+    def rollback(self, n=1):
+        if n > self.last_width:
+            raise _C.QvexError(f"RecurrentCache.rollback({n}): only the last {self.last_width} tokens are kept")
+        self.offset -= n
+        self.last_width -= n
+
+
+class LayerCaches(list):
+    """The list returned by make_cache(): one cache per layer, sharing counters."""
+
+    def __init__(self, items, counters):
+        super().__init__(items)
+        self.counters = counters
+
+
+# ---------------------------------------------------------------- layers
+
+class Attention:
+    """Gated full attention (engine/model.py:199-232) with q/k/v projections fused
+    into one quantized matmul (lossless, like the reference's in_proj fusion)."""
+
+    def __init__(self, cfg: Config, p: dict):
+        self.cfg = cfg
+        self.n_heads, self.n_kv = cfg.num_attention_heads, cfg.num_key_value_heads
+        self.head_dim = cfg.head_dim
+        self.qkv_proj = QLinear.fuse([p["q_proj"], p["k_proj"], p["v_proj"]])
+        self.o_proj = p["o_proj"]
+        self.q_norm, self.k_norm = p["q_norm"], p["k_norm"]
+        self._ws = None
+
+    def _workspace(self, L, cap, kps, device):
+        need = int(_C.lib().qvex_attn_workspace_bytes(L, self.n_heads, self.n_kv, self.head_dim, cap, kps))
+        if self._ws is None or self._ws.numel() * 4 < need:
+            self._ws = torch.empty((need + 3) // 4, dtype=torch.float32, device=device)
+        return self._ws
+
+    def __call__(self, x, cache: KVCache):
+        L = x.shape[0]
+        cfg = self.cfg
+        H, Hkv, D = self.n_heads, self.n_kv, self.head_dim
+        proj = self.qkv_proj(x)                                   # [L, H*2D + 2*Hkv*D]
+        q = torch.empty((L, H, D), dtype=torch.bfloat16, device=x.device)
+        pos = cache.counters.ptr(cache.index)
+        _C.call("qvex_attn_qk_rope", _ptr(proj), proj.stride(0), _ptr(self.q_norm), _ptr(self.k_norm), pos,
+                L, H, Hkv, D, cfg.rotary_dim, float(cfg.rope_theta), float(cfg.rms_norm_eps), _ptr(q),
+                _ptr(cache.k), _ptr(cache.v), cache.capacity, _stream())
+        max_keys = min(cache.capacity, cache.offset + L)
+        kps = 256 if L <= 8 else cache.capacity
+        kps = max(64, (kps + 63) // 64 * 64)
+        ws = self._workspace(L, max_keys, kps, x.device)
+        o = torch.empty((L, H * D), dtype=torch.bfloat16, device=x.device)
+        _C.call("qvex_attention", _ptr(q), _ptr(cache.k), _ptr(cache.v), pos, L, H, Hkv, D, cache.capacity,
+                max_keys, kps, _ptr(proj), proj.stride(0), _ptr(o), _ptr(ws), ws.numel() * 4, _stream())
+        cache.offset += L
+        return self.o_proj(o)
+
+
+class GatedDeltaNet:
+    """Gated DeltaNet block (engine/model.py:235-291)."""
+
+    def __init__(self, cfg: Config, p: dict):
+        self.cfg = cfg
+        self.hk, self.hv = cfg.linear_num_key_heads, cfg.linear_num_value_heads
+        self.dk, self.dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
+        self.key_dim, self.value_dim = self.hk * self.dk, self.hv * self.dv
+        self.conv_dim = 2 * self.key_dim + self.value_dim
+        self.K = cfg.linear_conv_kernel_dim
+        self.in_proj = QLinear.fuse([p["in_proj_qkv"], p["in_proj_z"], p["in_proj_b"], p["in_proj_a"]])
+        self.conv_w = p["conv1d"]          # bf16 [conv_dim, K]
+        self.A_log, self.dt_bias = p["A_log"], p["dt_bias"]
+        self.norm_w = p["norm"]
+        self.out_proj = p["out_proj"]
+
+    def __call__(self, x, cache: RecurrentCache, keep_prev=False):
+        S = x.shape[0]
+        dev = x.device
+        proj = self.in_proj(x)                                    # [S, conv | z | b | a]
+        q = torch.empty((1, S, self.hk, self.dk), dtype=torch.bfloat16, device=dev)
+        k = torch.empty_like(q)
+        v = torch.empty((1, S, self.hv, self.dv), dtype=torch.bfloat16, device=dev)
+        a = torch.empty((1, S, self.hv), dtype=torch.bfloat16, device=dev)
+        b = torch.empty_like(a)
+        inv = self.dk ** -0.5
+        pos = cache.counters.ptr(cache.index)
+        ab_off = self.conv_dim + self.value_dim
+        _C.call("qvex_gdn_conv_qk", _ptr(proj), proj.stride(0), _ptr(cache.conv_ring), cache.ring_rows, pos,
+                _ptr(self.conv_w), self.K, _ptr(q), _ptr(k), _ptr(v), _ptr(a), _ptr(b), S, self.conv_dim,
+                self.key_dim, self.hv, ab_off, float(inv * inv), float(inv), 1e-6, _stream())
+        snap = S <= cache.n_slots - 1
+        y = kernels.gated_delta_ring(q, k, v, a, b, self.A_log, self.dt_bias, cache.ssm_ring,
+                                     cache.counters.dev[cache.index:cache.index + 1], snap_every=snap)
+        cache.offset += S
+        cache.last_width = S if snap else 0
+        z = proj[:, self.conv_dim:self.conv_dim + self.value_dim]
+        g = torch.empty((S, self.value_dim), dtype=torch.bfloat16, device=dev)
+        _C.call("qvex_gated_rmsnorm", _ptr(y), _ptr(proj) + 2 * self.conv_dim, proj.stride(0), self.hv,
+                _ptr(self.norm_w), _ptr(g), S * self.hv, self.dv, float(self.cfg.rms_norm_eps), _stream())
+        return self.out_proj(g)
+
+
+class MLP:
+    def __init__(self, p: dict):
+        self.gate_up = QLinear.fuse([p["gate_proj"], p["up_proj"]])
+        self.down = p["down_proj"]
+        self.hidden = p["gate_proj"].N
+
+    def __call__(self, x):
+        gu = self.gate_up(x)
+        L = gu.shape[0]
+        h = torch.empty((L, self.hidden), dtype=torch.bfloat16, device=x.device)
+        _C.call("qvex_swiglu", _ptr(gu), _ptr(h), L, self.hidden, _stream())
+        return self.down(h)
+
+
+class Layer:
+    def __init__(self, cfg: Config, i: int, p: dict):
+        self.linear = cfg.is_linear(i)
+        self.mixer = GatedDeltaNet(cfg, p["linear_attn"]) if self.linear else Attention(cfg, p["self_attn"])
+        self.mlp = MLP(p["mlp"])
+        self.ln1, self.ln2 = p["input_layernorm"], p["post_attention_layernorm"]
+        self.eps = cfg.rms_norm_eps
+
+    def __call__(self, x, cache, keep_prev=False, normed=None):
+        """x [L, H] residual stream. Returns the new residual stream."""
+        n = normed if normed is not None else rms_norm(x, self.ln1, self.eps)
+        d = self.mixer(n, cache, keep_prev) if self.linear else self.mixer(n, cache)
+        h, n2 = add_rms_norm(x, d, self.ln2, self.eps)
+        m = self.mlp(n2)
+        return h, m
+
+
+class Qwen35:
+    """Forward of the hybrid stack (engine/model.py:319-336) for batch 1."""
+
+    def __init__(self, cfg: Config, embed: QEmbedding, layers: list[Layer], norm, lm_head: QLinear,
+                 max_context: int = 8192, max_width: int = 8):
+        self.cfg = cfg
+        self.embed, self.layers, self.norm, self.lm_head = embed, layers, norm, lm_head
+        self.max_context, self.max_width = max_context, max_width
+
+    def make_cache(self, max_context: int | None = None, max_width: int | None = None):
+        cfg = self.cfg
+        dev = self.norm.device
+        cap = max_context or self.max_context
+        width = max_width or self.max_width
+        counters = CacheCounters(len(self.layers), dev)
+        caches = []
+        for i, l in enumerate(self.layers):
+            if l.linear:
+                caches.append(RecurrentCache(counters, i, conv_dim=l.mixer.conv_dim, kernel=l.mixer.K,
+                                             hv=l.mixer.hv, dv=l.mixer.dv, dk=l.mixer.dk,
+                                             max_width=width, device=dev))
+            else:
+                caches.append(KVCache(counters, i, n_kv=cfg.num_key_value_heads, head_dim=cfg.head_dim,
+                                      capacity=cap, device=dev))
+        return LayerCaches(caches, counters)
+
+    def __call__(self, ids, cache, last_only=True, return_hidden=False, keep_prev=False):
+        """ids: [1, L] int -> logits [1, L or 1, V] bf16 (and pre-norm hidden [1, L, H])."""
+        ids = torch.as_tensor(ids, device=self.norm.device).reshape(-1)
+        L = ids.numel()
+        counters = cache.counters
+        # chunk long inputs so every call fits the conv rings (prefill)
+        step = L
+        for c in cache:
+            if isinstance(c, RecurrentCache):
+                step = min(step, c.ring_rows - c.kernel + 1)
+        if L > step:
+            outs, hs = [], []
+            for s0 in range(0, L, step):
+                r = self(ids[s0:s0 + step].reshape(1, -1), cache, last_only=last_only and s0 + step >= L,
+                         return_hidden=return_hidden, keep_prev=keep_prev)
+                if return_hidden:
+                    outs.append(r[0]); hs.append(r[1])
+                else:
+                    outs.append(r)
+            logits = outs[-1] if last_only else torch.cat(outs, dim=1)
+            return (logits, torch.cat(hs, dim=1)) if return_hidden else logits
+        counters.sync()
+        x = self.embed(ids)
+        eps = self.cfg.rms_norm_eps
+        n = rms_norm(x, self.layers[0].ln1, eps)
+        for i, (layer, c) in enumerate(zip(self.layers, cache)):
+            h, m = layer(x, c, keep_prev, normed=n)
+            nxt = self.layers[i + 1].ln1 if i + 1 < len(self.layers) else self.norm
+            x, n = add_rms_norm(h, m, nxt, eps)
+        hidden = x
+        if last_only:
+            n = n[-1:]
+        logits = self.lm_head(n)
+        logits = logits.view(1, -1, self.cfg.vocab_size)
+        return (logits, hidden.view(1, L, -1)) if return_hidden else logits
+
+
+# ---------------------------------------------------------------- random init in the MLX layout
+
+def _rand_qlinear(N, K, gen, scale, device) -> QLinear:
+    """Random 4-bit group-64 weights: codes uniform on 0..15, scales ~ U(0.5, 1.5) * scale,
+    biases = -8 * scale (zero-mean dequantized weights)."""
+    w = torch.randint(-2**31, 2**31, (N, K // 8), generator=gen, device=device, dtype=torch.int64)
+    w = w.to(torch.int32)
+    s = (torch.rand((N, K // 64), generator=gen, device=device) + 0.5) * scale
+    s = s.to(torch.bfloat16)
+    b = (-8.0 * s.float()).to(torch.bfloat16)
+    return QLinear(w, s, b)
+
+
+def random_model(cfg: Config, seed: int = 1004, device="cuda", max_context: int = 8192,
+                 max_width: int = 8, lm_head_scale: float = 2.0) -> Qwen35:
+    """Random-init model of the given shape with weights generated directly in the
+    MLX 4-bit layout on the device (no checkpoint). Linear scales are chosen so a
+    unit-RMS input gives a unit-RMS output (dequantized w has variance 21.25 s^2)."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    H, I = cfg.hidden_size, cfg.intermediate_size
+
+    def lin(N, K, gain=1.0):
+        return _rand_qlinear(N, K, gen, gain / math.sqrt(21.25 * K), device)
+
+    def ones(n):
+        return (1.0 + 0.1 * torch.randn(n, generator=gen, device=device)).to(torch.bfloat16)
+
+    layers = []
+    for i in range(cfg.num_hidden_layers):
+        p = {"input_layernorm": ones(H), "post_attention_layernorm": ones(H),
+             "mlp": {"gate_proj": lin(I, H), "up_proj": lin(I, H), "down_proj": lin(H, I, 0.5)}}
+        if cfg.is_linear(i):
+            kd = cfg.linear_num_key_heads * cfg.linear_key_head_dim
+            vd = cfg.linear_num_value_heads * cfg.linear_value_head_dim
+            conv_dim = 2 * kd + vd
+            hv = cfg.linear_num_value_heads
+            p["linear_attn"] = {
+                "in_proj_qkv": lin(conv_dim, H), "in_proj_z": lin(vd, H),
+                "in_proj_b": lin(hv, H), "in_proj_a": lin(hv, H), "out_proj": lin(H, vd, 0.5),
+                "conv1d": (0.5 * torch.randn((conv_dim, cfg.linear_conv_kernel_dim), generator=gen,
+                                             device=device)).to(torch.bfloat16),
+                "A_log": (0.5 * torch.randn(hv, generator=gen, device=device)).float(),
+                "dt_bias": (0.5 * torch.randn(hv, generator=gen, device=device)).to(torch.bfloat16),
+                "norm": ones(cfg.linear_value_head_dim),
+            }
+        else:
+            D, Hq, Hkv = cfg.head_dim, cfg.num_attention_heads, cfg.num_key_value_heads
+            p["self_attn"] = {"q_proj": lin(Hq * 2 * D, H), "k_proj": lin(Hkv * D, H),
+                              "v_proj": lin(Hkv * D, H), "o_proj": lin(H, Hq * D, 0.5),
+                              "q_norm": ones(D), "k_norm": ones(D)}
+        layers.append(Layer(cfg, i, p))
+    V = cfg.vocab_size
+    e = _rand_qlinear(V, H, gen, 1.0 / math.sqrt(21.25), device)
+    embed = QEmbedding(e.w, e.scales, e.biases)
+    lm_head = lin(V, H, lm_head_scale)
+    return Qwen35(cfg, embed, layers, ones(H), lm_head, max_context=max_context, max_width=max_width)

@@ -1,0 +1,89 @@
+"""Multi-token prediction (MTP) head of Qwen3.5 as the draft model
+(mirror of engine/mtp.py).
+
+    x = fc([rms(embed(tok_{i+1})), rms(h_i)]) -> attention + MLP block -> norm -> lm_head
+
+It shares embed_tokens and lm_head with the main model; its attention layer keeps
+its own KV cache. For k > 1 drafts the head is chained on its own output: draft
+step j + 1 takes (hidden after the MTP block at step j, draft token j), a
+convention of this implementation (the reference drafts one token).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _C
+from .kernels import _ptr, _stream
+from .model import Attention, KVCache, Layer, MLP, QLinear, Qwen35, _rand_qlinear, add_rms_norm, rms_norm
+
+
+class MTPHead:
+    def __init__(self, model: Qwen35, w: dict, group_size: int = 64, bits: int = 4, hidden_mode: str = "pre"):
+        cfg = model.cfg
+        self.model = model
+        self.eps = cfg.rms_norm_eps
+        self.hidden_mode = hidden_mode  # "pre": raw last-layer output, "post": after the final norm
+        self.fc = w["fc"]
+        self.norm_emb, self.norm_hid, self.norm_out = w["norm_emb"], w["norm_hid"], w["norm_out"]
+        layer = Layer.__new__(Layer)
+        layer.linear = False
+        layer.eps = cfg.rms_norm_eps
+        layer.ln1, layer.ln2 = w["ln1"], w["ln2"]
+        layer.mixer = Attention(cfg, w["attn"])
+        layer.mlp = MLP(w["mlp"])
+        self.layer = layer
+
+    def make_cache(self, max_context: int | None = None) -> KVCache:
+        cfg = self.model.cfg
+        return KVCache(None, 0, n_kv=cfg.num_key_value_heads, head_dim=cfg.head_dim,
+                       capacity=max_context or self.model.max_context, device=self.model.norm.device)
+
+    def __call__(self, hidden, next_ids, cache: KVCache, last_only=True, return_hidden=False):
+        """hidden [1, T, H] (main model, pre-norm) and next_ids [1, T] -> logits
+        [1, 1 or T, V] (engine/mtp.py:58-68); with return_hidden also the block
+        output [1, T, H] before the final norm (what a chained draft step takes)."""
+        H = self.model.cfg.hidden_size
+        h = hidden.reshape(-1, H)
+        ids = torch.as_tensor(next_ids, device=h.device).reshape(-1)
+        T = ids.numel()
+        if self.hidden_mode == "post":
+            h = rms_norm(h, self.model.norm, self.eps)
+        cache.counters.sync()
+        e = self.model.embed(ids)
+        x_in = torch.empty((T, 2 * H), dtype=torch.bfloat16, device=h.device)
+        rms_norm(e, self.norm_emb, self.eps, out=x_in[:, :H])
+        rms_norm(h, self.norm_hid, self.eps, out=x_in[:, H:])
+        x = self.fc(x_in)
+        n = rms_norm(x, self.layer.ln1, self.eps)
+        hh, m = self.layer(x, cache, normed=n)
+        out, n_out = add_rms_norm(hh, m, self.norm_out, self.eps)
+        if last_only:
+            n_out = n_out[-1:]
+        logits = self.model.lm_head(n_out).view(1, -1, self.model.cfg.vocab_size)
+        return (logits, out.view(1, T, H)) if return_hidden else logits
+
+
+def random_mtp(model: Qwen35, seed: int = 2004) -> MTPHead:
+    """Random-init MTP head (fc 2H -> H plus one full-attention layer) in the MLX 4-bit layout."""
+    cfg = model.cfg
+    dev = model.norm.device
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    H, I, D = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
+    Hq, Hkv = cfg.num_attention_heads, cfg.num_key_value_heads
+
+    def lin(N, K, gain=1.0):
+        return _rand_qlinear(N, K, gen, gain / math.sqrt(21.25 * K), dev)
+
+    def ones(n):
+        return (1.0 + 0.1 * torch.randn(n, generator=gen, device=dev)).to(torch.bfloat16)
+
+    w = {"fc": lin(H, 2 * H), "norm_emb": ones(H), "norm_hid": ones(H), "norm_out": ones(H),
+         "ln1": ones(H), "ln2": ones(H),
+         "attn": {"q_proj": lin(Hq * 2 * D, H), "k_proj": lin(Hkv * D, H), "v_proj": lin(Hkv * D, H),
+                  "o_proj": lin(H, Hq * D, 0.5), "q_norm": ones(D), "k_norm": ones(D)},
+         "mlp": {"gate_proj": lin(I, H), "up_proj": lin(I, H), "down_proj": lin(H, I, 0.5)}}
+    return MTPHead(model, w)

@@ -1,0 +1,117 @@
+"""Verify forward, rollback and MTP decode on a small random-init model (GPU).
+
+Forward parity vs the numpy restatement of engine/model.py (oracle/model.py):
+logits within 0.15 absolute (unit-scale logits, bf16 rounding points of the
+fused kernels differ from the reference's per-op roundings). Rollback and
+speculative-vs-plain checks are bit-exact: every kernel computes a row the
+same way whatever the number of rows in the call.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.model import OracleModel
+from qvex.model import Config, random_model
+from qvex.mtp import random_mtp
+from qvex.sampler import Sampler, SamplingParams
+from qvex.speculative import decode, mtp_prefill
+
+DEV = "cuda:0"
+LOGIT_TOL = 0.15
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    torch.manual_seed(0)
+    cfg = Config.tiny(layers=4, vocab=4096)
+    m = random_model(cfg, seed=7, device=DEV, max_context=1024, max_width=8)
+    return m
+
+
+def prompt(n, V, seed=3):
+    return np.random.default_rng(seed).integers(0, V, size=n).astype(np.int32)
+
+
+def f32(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.gpu
+def test_prefill_and_verify_match_oracle(tiny):
+    V = tiny.cfg.vocab_size
+    ids = prompt(13, V)
+    cache = tiny.make_cache()
+    logits, hidden = tiny(torch.from_numpy(ids).reshape(1, -1), cache, return_hidden=True)
+    orc = OracleModel(tiny)
+    ol, oh = orc.forward(ids, last_only=True)
+    d = np.abs(f32(logits[0]) - ol).max()
+    dh = np.abs(f32(hidden[0]) - oh).max() / (np.abs(oh).max() + 1e-6)
+    print(f"prefill: max|dlogit|={d:.4f} rel|dhidden|={dh:.4f} argmax {int(f32(logits[0]).argmax())} vs {int(ol.argmax())}")
+    assert d < LOGIT_TOL
+    ver = prompt(4, V, seed=5)
+    logits4 = tiny(torch.from_numpy(ver).reshape(1, -1), cache, last_only=False)
+    ol4, _ = orc.forward(ver, last_only=False)
+    d4 = np.abs(f32(logits4[0]) - ol4).max()
+    print(f"verify: max|dlogit|={d4:.4f}")
+    assert d4 < LOGIT_TOL
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [0, 1, 2, 3])
+def test_rollback_equals_prefix_run(tiny, n):
+    """tests/rollback_test.py generalised: verify [a,b,c,d], keep n + 1 tokens,
+    then feed e; logits equal the sequential run a..(n tokens), e bit for bit."""
+    V = tiny.cfg.vocab_size
+    ids = prompt(11, V, seed=21)
+    ver = prompt(4, V, seed=22)
+    e = prompt(1, V, seed=23)
+    c1 = tiny.make_cache()
+    tiny(torch.from_numpy(ids).reshape(1, -1), c1)
+    tiny(torch.from_numpy(ver).reshape(1, -1), c1, last_only=False, keep_prev=True)
+    for c in c1:
+        c.rollback(3 - n)
+    l1 = tiny(torch.from_numpy(e).reshape(1, -1), c1)
+    c2 = tiny.make_cache()
+    tiny(torch.from_numpy(ids).reshape(1, -1), c2)
+    for t in ver[: n + 1]:
+        tiny(torch.tensor([[int(t)]]), c2)
+    l2 = tiny(torch.from_numpy(e).reshape(1, -1), c2)
+    torch.cuda.synchronize()
+    assert torch.equal(l1.view(torch.int16), l2.view(torch.int16))
+    assert [c.offset for c in c1] == [c.offset for c in c2]
+
+
+def run_decode(model, mtp, k, temp, n_tokens, use_mtp=True, seed=0):
+    V = model.cfg.vocab_size
+    ids = torch.from_numpy(prompt(17, V, seed=31)).reshape(1, -1)
+    cache, mc = model.make_cache(), mtp.make_cache()
+    logits, hidden = model(ids, cache, return_hidden=True)
+    last_h = mtp_prefill(mtp, mc, hidden, ids.to(DEV), None)
+    s = Sampler(SamplingParams(temperature=temp, top_k=0, top_p=1.0, seed=seed), V)
+    stats, out = {}, []
+    for t in decode(model, s, cache, logits[0, -1], last_h, mtp if use_mtp else None, mc, stats=stats, k=k):
+        out.append(t)
+        if len(out) >= n_tokens:
+            break
+    return out, stats
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("k", [1, 3])
+def test_mtp_greedy_equals_plain_greedy(tiny, k):
+    """tests/mtp_teacher.py: greedy speculative decoding emits the main model's
+    greedy tokens (here exactly, rows being bit-identical)."""
+    mtp = random_mtp(tiny, seed=9)
+    spec, st = run_decode(tiny, mtp, k, 0.0, 24)
+    plain, _ = run_decode(tiny, mtp, k, 0.0, 24, use_mtp=False)
+    print("cycles", st["cycles"], "accepted", st["accepted"])
+    assert spec == plain
+
+
+@pytest.mark.gpu
+def test_sampled_decode(tiny):
+    mtp = random_mtp(tiny, seed=11)
+    out, st = run_decode(tiny, mtp, 3, 0.7, 40, seed=5)
+    assert len(out) == 40 and all(0 <= t < tiny.cfg.vocab_size for t in out)
+    assert st["emitted"] >= 40 and st["cycles"] >= 1
