@@ -146,13 +146,14 @@ int qvex_embed_w4g64(const int32_t* ids, int L, const uint32_t* w, const uint16_
 
 /* out[r] = w * (x[r] * rsqrt(mean(x[r]^2) + eps)) * scale, w optional (NULL = 1)
  * (mx.fast.rms_norm at engine/model.py:218-219, 276-277, 314-316, 335; the
- * weightless q/k scaling of engine/model.py:275-277 uses scale). Strides in
- * elements, even. */
+ * weightless q/k scaling of engine/model.py:275-277 uses scale). D % 8 == 0,
+ * D <= 8192; strides in elements, multiples of 8; pointers 16-byte aligned. */
 int qvex_rmsnorm(const uint16_t* x, long x_stride, const uint16_t* w, uint16_t* out,
                  long out_stride, int R, int D, float eps, float scale, void* stream);
 
 /* h = bf16(x + delta); out = rms_norm(h) * w: the residual add and the next
- * pre-norm of Layer.__call__ (engine/model.py:313-316) in one pass. [R, D]. */
+ * pre-norm of Layer.__call__ (engine/model.py:313-316) in one pass. [R, D],
+ * D % 8 == 0, D <= 8192, pointers 16-byte aligned. */
 int qvex_add_rmsnorm(const uint16_t* x, const uint16_t* delta, uint16_t* h_out,
                      const uint16_t* w, uint16_t* out, int R, int D, float eps, void* stream);
 

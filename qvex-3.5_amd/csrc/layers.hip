@@ -52,7 +52,31 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ 
 
 // ---------------------------------------------------------------- RMSNorm family
 //
-// One wave per row. y = w * (x * rsqrt(mean(x^2) + eps)) * scale (w optional).
+// One 256-thread block per row; thread t holds the 8-element chunks t, t+256,
+// ... of the row in registers (16-byte loads), so the row is read once and the
+// reduction is one wave butterfly plus 4 LDS slots.
+// y = w * (x * rsqrt(mean(x^2) + eps)) * scale (w optional); with ADD the row is
+// first h = bf16(x + delta), stored, and normalised.
+constexpr int RMS_MAXC = 4;   // chunks of 8 per thread: D <= 8192
+
+__device__ __forceinline__ void unpack8(const u32x4 v, float* f) {
+  f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x); f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
+  f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
+}
+
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  u32x4 v;
+  v.x = pack_bf16x2(f[0], f[1]); v.y = pack_bf16x2(f[2], f[3]);
+  v.z = pack_bf16x2(f[4], f[5]); v.w = pack_bf16x2(f[6], f[7]);
+  return v;
+}
+
+__device__ __forceinline__ float block_allsum256(float v, float* red) {
+  v = wave_allsum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
 
 template <bool ADD>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x, long x_stride,
@@ -60,36 +84,46 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
                                                       uint16_t* __restrict__ h_out, long h_stride,
                                                       const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
                                                       long o_stride, int R, int D, float eps, float scale) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= R) return;
+  __shared__ float red[4];
+  const int row = blockIdx.x;
+  const int t = threadIdx.x;
   const uint16_t* xr = x + row * x_stride;
+  float v[RMS_MAXC][8];
   float ss = 0.0f;
-  // D % 2 == 0 is checked on the host; each lane walks pairs
-  for (int i = 2 * lane; i < D; i += 128) {
-    const uint32_t p = *reinterpret_cast<const uint32_t*>(xr + i);
-    float a = bf16_lo(p), b = bf16_hi(p);
-    if constexpr (ADD) {
-      const uint32_t dp = *reinterpret_cast<const uint32_t*>(delta + row * d_stride + i);
-      a = bf16_to_f32(f32_to_bf16(a + bf16_lo(dp)));
-      b = bf16_to_f32(f32_to_bf16(b + bf16_hi(dp)));
-      *reinterpret_cast<uint32_t*>(h_out + row * h_stride + i) = pack_bf16x2(a, b);
+#pragma unroll
+  for (int c = 0; c < RMS_MAXC; ++c) {
+    const int i = (t + 256 * c) * 8;
+    if (i < D) {
+      unpack8(load16(xr + i), v[c]);
+      if constexpr (ADD) {
+        float d[8];
+        unpack8(load16(delta + row * d_stride + i), d);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[c][e] = bf16_to_f32(f32_to_bf16(v[c][e] + d[e]));
+        *reinterpret_cast<u32x4*>(h_out + row * h_stride + i) = pack8(v[c]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(v[c][e], v[c][e], ss);
     }
-    ss = fmaf(a, a, fmaf(b, b, ss));
   }
-  ss = wave_allsum(ss);
+  ss = block_allsum256(ss, red);
   const float inv = rsqrtf(ss / (float)D + eps);
-  for (int i = 2 * lane; i < D; i += 128) {
-    uint32_t p;
-    if constexpr (ADD) p = *reinterpret_cast<const uint32_t*>(h_out + row * h_stride + i);
-    else p = *reinterpret_cast<const uint32_t*>(xr + i);
-    float a = bf16_lo(p) * inv, b = bf16_hi(p) * inv;
-    if (w) {
-      const uint32_t wp = *reinterpret_cast<const uint32_t*>(w + i);
-      a = bf16_lo(wp) * a;
-      b = bf16_hi(wp) * b;
+#pragma unroll
+  for (int c = 0; c < RMS_MAXC; ++c) {
+    const int i = (t + 256 * c) * 8;
+    if (i < D) {
+      float o[8];
+      if (w) {
+        float wf[8];
+        unpack8(load16(w + i), wf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = wf[e] * (v[c][e] * inv) * scale;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (v[c][e] * inv) * scale;
+      }
+      *reinterpret_cast<u32x4*>(out + row * o_stride + i) = pack8(o);
     }
-    *reinterpret_cast<uint32_t*>(out + row * o_stride + i) = pack_bf16x2(a * scale, b * scale);
   }
 }
 
@@ -456,10 +490,13 @@ extern "C" int qvex_embed_w4g64(const int32_t* ids, int L, const uint32_t* w, co
 extern "C" int qvex_rmsnorm(const uint16_t* x, long x_stride, const uint16_t* w, uint16_t* out, long out_stride,
                             int R, int D, float eps, float scale, void* stream) {
   QVEX_CHECK_ARG(x && out, "qvex_rmsnorm: null pointer");
-  QVEX_CHECK_ARG(R >= 1 && D >= 2 && D % 2 == 0 && x_stride >= D && out_stride >= D && x_stride % 2 == 0 &&
-                     out_stride % 2 == 0,
-                 "qvex_rmsnorm: R=%d D=%d strides %ld/%ld", R, D, x_stride, out_stride);
-  hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3((R + 3) / 4), dim3(256), 0, (hipStream_t)stream, x, x_stride,
+  QVEX_CHECK_ARG(R >= 1 && D >= 8 && D % 8 == 0 && D <= 256 * 8 * RMS_MAXC && x_stride >= D && out_stride >= D &&
+                     x_stride % 8 == 0 && out_stride % 8 == 0,
+                 "qvex_rmsnorm: R=%d D=%d strides %ld/%ld (D %% 8 == 0, D <= 8192, strides %% 8 == 0)", R, D,
+                 x_stride, out_stride);
+  QVEX_CHECK_ARG(qvex_aligned(x, 16) && qvex_aligned(out, 16) && (!w || qvex_aligned(w, 16)),
+                 "qvex_rmsnorm: x, w, out must be 16-byte aligned");
+  hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(R), dim3(256), 0, (hipStream_t)stream, x, x_stride,
                      (const uint16_t*)nullptr, 0L, (uint16_t*)nullptr, 0L, w, out, out_stride, R, D, eps, scale);
   QVEX_CHECK_LAUNCH("qvex_rmsnorm");
   return QVEX_OK;
@@ -468,9 +505,12 @@ extern "C" int qvex_rmsnorm(const uint16_t* x, long x_stride, const uint16_t* w,
 extern "C" int qvex_add_rmsnorm(const uint16_t* x, const uint16_t* delta, uint16_t* h_out, const uint16_t* w,
                                 uint16_t* out, int R, int D, float eps, void* stream) {
   QVEX_CHECK_ARG(x && delta && h_out && out, "qvex_add_rmsnorm: null pointer");
-  QVEX_CHECK_ARG(R >= 1 && D >= 2 && D % 2 == 0, "qvex_add_rmsnorm: R=%d D=%d", R, D);
-  hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3((R + 3) / 4), dim3(256), 0, (hipStream_t)stream, x, (long)D, delta,
-                     (long)D, h_out, (long)D, w, out, (long)D, R, D, eps, 1.0f);
+  QVEX_CHECK_ARG(R >= 1 && D >= 8 && D % 8 == 0 && D <= 256 * 8 * RMS_MAXC, "qvex_add_rmsnorm: R=%d D=%d", R, D);
+  QVEX_CHECK_ARG(qvex_aligned(x, 16) && qvex_aligned(delta, 16) && qvex_aligned(h_out, 16) && qvex_aligned(out, 16) &&
+                     (!w || qvex_aligned(w, 16)),
+                 "qvex_add_rmsnorm: pointers must be 16-byte aligned");
+  hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3(R), dim3(256), 0, (hipStream_t)stream, x, (long)D, delta, (long)D,
+                     h_out, (long)D, w, out, (long)D, R, D, eps, 1.0f);
   QVEX_CHECK_LAUNCH("qvex_add_rmsnorm");
   return QVEX_OK;
 }

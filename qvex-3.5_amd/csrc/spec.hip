@@ -25,8 +25,10 @@
 //
 // Kernel 1 (grid parts x rows) makes one pass over every logit row of every step
 // and leaves (m_p, S_p) per part: the single HBM pass over (2k+1) x V floats.
-// Kernel 2 (one block per step) combines parts, runs the k accept tests on
-// gathered elements, and makes the one sampling pass over the row(s) it needs.
+// Kernel 2 (grid parts x steps) combines parts, runs the k accept tests on
+// gathered elements and makes the sampling weights' thread and part sums over
+// the one or two rows the draw needs, every part in its own block.
+// Kernel 3 (one block per step) walks the stored sums to the drawn token.
 #include "qvex_common.h"
 
 namespace {
@@ -282,33 +284,49 @@ __device__ int sample_pass(const WCtx& c, int V, int P, float u, float* Tpt, flo
   return result;
 }
 
-__global__ __launch_bounds__(NT) void spec_accept_kernel(SpecArgs a) {
-  extern __shared__ float smem[];
-  float* Tpt = smem;                       // [P][NT]
-  float* Wp = smem + a.P * NT;             // [P]
-  float* rm = Wp + a.P;                    // [rps] row max (or argmax as int bits)
-  float* rs = rm + a.rps;                  // [rps] row sum
+// Workspace after the row statistics: per step T[P][NT] thread sums of the
+// sampling row, W[P] part sums and a decision record (n, mode, stats).
+struct SpecWs {
+  float* T;     // [S][P][NT]
+  float* W;     // [S][P]
+  float* dec;   // [S][8]: n, token (greedy), mp, sp, mq, sq
+};
+
+__device__ __forceinline__ SpecWs spec_ws(const SpecArgs& a) {
+  SpecWs w;
+  w.T = a.ws + (long)a.S * a.rps * a.P * 2;
+  w.W = w.T + (long)a.S * a.P * NT;
+  w.dec = w.W + (long)a.S * a.P;
+  return w;
+}
+
+// Kernel 2 (grid parts x steps): every block combines the step's row statistics
+// and runs the k accept tests (a few gathers), then block p makes the thread and
+// part sums of the sampling weights over part p of the sampling row.
+__global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
+  __shared__ float rm[80], rs[80];
   __shared__ float red[4];
   __shared__ int s_n, s_tok;
-  const int step = blockIdx.x;
+  const int p = blockIdx.x, step = blockIdx.y;
   const int t = threadIdx.x;
   const int k = a.k;
+  const SpecWs W = spec_ws(a);
 
   if (t < a.rps) {
     const float* w = a.ws + ((long)step * a.rps + t) * a.P * 2;
     if (a.greedy) {
       float bv = w[0];
       int bj = __float_as_int(w[1]);
-      for (int p = 1; p < a.P; ++p)
-        if (w[2 * p] > bv) { bv = w[2 * p]; bj = __float_as_int(w[2 * p + 1]); }
+      for (int q = 1; q < a.P; ++q)
+        if (w[2 * q] > bv) { bv = w[2 * q]; bj = __float_as_int(w[2 * q + 1]); }
       rm[t] = __int_as_float(bj);
     } else {
       float m = -__builtin_inff();
-      for (int p = 0; p < a.P; ++p) m = fmaxf(m, w[2 * p]);
-      float s = 0.0f;
-      for (int p = 0; p < a.P; ++p) s = s + w[2 * p + 1] * qx_expf(w[2 * p] - m);
+      for (int q = 0; q < a.P; ++q) m = fmaxf(m, w[2 * q]);
+      float sum = 0.0f;
+      for (int q = 0; q < a.P; ++q) sum = sum + w[2 * q + 1] * qx_expf(w[2 * q] - m);
       rm[t] = m;
-      rs[t] = s;
+      rs[t] = sum;
     }
   }
   __syncthreads();
@@ -341,33 +359,134 @@ __global__ __launch_bounds__(NT) void spec_accept_kernel(SpecArgs a) {
   }
   __syncthreads();
   const int n = s_n;
-  int tok = s_tok;
-  if (!a.greedy) {
-    WCtx c;
-    c.inv_temp = a.inv_temp;
-    c.tp = row_ptr(a, step, n);
-    c.mp = rm[n];
-    c.sp = rs[n];
-    const float u = a.u_smp[step];
-    if (n < k) {
-      c.tq = a.draft ? row_ptr(a, step, k + 1 + n) : nullptr;
-      c.d = a.ids[(long)step * k + n];
-      c.mode = 0;
-      c.mq = a.draft ? rm[k + 1 + n] : 0.0f;
-      c.sq = a.draft ? rs[k + 1 + n] : 1.0f;
-      tok = sample_pass(c, a.V, a.P, u, Tpt, Wp, red);
-      if (tok < 0) {
-        c.mode = 1;
-        tok = sample_pass(c, a.V, a.P, u, Tpt, Wp, red);
-      }
-    } else {
-      c.tq = nullptr;
-      c.d = -1;
-      c.mode = 1;
-      c.mq = 0.0f;
-      c.sq = 1.0f;
-      tok = sample_pass(c, a.V, a.P, u, Tpt, Wp, red);
+  if (a.greedy) {
+    if (p == 0 && t == 0) {
+      a.n_accept[step] = n;
+      a.out_token[step] = s_tok;
     }
+    return;
+  }
+  WCtx c;
+  c.inv_temp = a.inv_temp;
+  c.tp = row_ptr(a, step, n);
+  c.mp = rm[n];
+  c.sp = rs[n];
+  if (n < k) {
+    c.tq = a.draft ? row_ptr(a, step, k + 1 + n) : nullptr;
+    c.d = a.ids[(long)step * k + n];
+    c.mode = 0;
+    c.mq = a.draft ? rm[k + 1 + n] : 0.0f;
+    c.sq = a.draft ? rs[k + 1 + n] : 1.0f;
+  } else {
+    c.tq = nullptr;
+    c.d = -1;
+    c.mode = 1;
+    c.mq = 0.0f;
+    c.sq = 1.0f;
+  }
+  const int base = p * PART, end = min(a.V, base + PART);
+  float acc = 0.0f;
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const int j = base + 4 * (t + NT * it);
+    if (j < end) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = acc + weight(c, j + e);
+    }
+  }
+  W.T[((long)step * a.P + p) * NT + t] = acc;
+  const float wp = block_sum(acc, red);
+  if (t == 0) {
+    W.W[(long)step * a.P + p] = wp;
+    if (p == 0) {
+      float* dd = W.dec + (long)step * 8;
+      dd[0] = __int_as_float(n);
+      dd[1] = __int_as_float(c.d);
+      dd[2] = c.mp; dd[3] = c.sp; dd[4] = c.mq; dd[5] = c.sq;
+    }
+  }
+}
+
+// Kernel 3 (one block per step): inverse-CDF walk over the stored part and
+// thread sums; the last 32 weights are recomputed for the element walk. If the
+// residual vanished in fp32 the block falls back to sampling p_n itself.
+__global__ __launch_bounds__(NT) void spec_sample_kernel(SpecArgs a) {
+  extern __shared__ float smem[];
+  float* Tpt = smem;              // [P][NT] (fallback pass only)
+  float* Wp = smem + a.P * NT;    // [P]
+  __shared__ float red[4];
+  __shared__ int s_tok;
+  const int step = blockIdx.x;
+  const int t = threadIdx.x;
+  const int k = a.k;
+  const SpecWs W = spec_ws(a);
+  const float* dd = W.dec + (long)step * 8;
+  const int n = __float_as_int(dd[0]);
+  WCtx c;
+  c.inv_temp = a.inv_temp;
+  c.tp = row_ptr(a, step, n);
+  c.d = __float_as_int(dd[1]);
+  c.mp = dd[2]; c.sp = dd[3]; c.mq = dd[4]; c.sq = dd[5];
+  c.tq = (n < k && a.draft) ? row_ptr(a, step, k + 1 + n) : nullptr;
+  c.mode = n < k ? 0 : 1;
+  const float u = a.u_smp[step];
+  if (t == 0) {
+    const float* Ws = W.W + (long)step * a.P;
+    const float* Ts = W.T + (long)step * a.P * NT;
+    float Wt = 0.0f;
+    for (int p = 0; p < a.P; ++p) Wt = Wt + Ws[p];
+    int res = -1;
+    if (Wt > 0.0f) {
+      const float th = u * Wt;
+      float cacc = 0.0f;
+      int ps = -1;
+      for (int p = 0; p < a.P; ++p) {
+        const float nx = cacc + Ws[p];
+        if (nx > th) { ps = p; break; }
+        cacc = nx;
+      }
+      bool fallback = false;
+      if (ps < 0) {
+        for (int p = a.P - 1; p >= 0; --p)
+          if (Ws[p] > 0.0f) { ps = p; break; }
+        fallback = true;
+      }
+      int ts = -1;
+      if (!fallback) {
+        for (int tt = 0; tt < NT; ++tt) {
+          const float nx = cacc + Ts[ps * NT + tt];
+          if (nx > th) { ts = tt; break; }
+          cacc = nx;
+        }
+      }
+      if (ts < 0) {
+        for (int tt = NT - 1; tt >= 0; --tt)
+          if (Ts[ps * NT + tt] > 0.0f) { ts = tt; break; }
+        fallback = true;
+      }
+      const int base = ps * PART, end = min(a.V, base + PART);
+      if (!fallback) {
+        for (int s = 0; s < 4 * NI; ++s) {
+          const int j = base + 4 * (ts + NT * (s >> 2)) + (s & 3);
+          if (j >= end) break;
+          cacc = cacc + weight(c, j);
+          if (cacc > th) { res = j; break; }
+        }
+      }
+      if (res < 0) {
+        for (int s = 4 * NI - 1; s >= 0; --s) {
+          const int j = base + 4 * (ts + NT * (s >> 2)) + (s & 3);
+          if (j < end && weight(c, j) > 0.0f) { res = j; break; }
+        }
+      }
+    }
+    s_tok = res;
+  }
+  __syncthreads();
+  int tok = s_tok;
+  if (tok < 0 && c.mode == 0) {     // residual vanished: sample p_n
+    c.mode = 1;
+    tok = sample_pass(c, a.V, a.P, u, Tpt, Wp, red);
   }
   if (t == 0) {
     a.n_accept[step] = n;
@@ -379,10 +498,14 @@ int nparts(int V) { return (V + PART - 1) / PART; }
 
 }  // namespace
 
+uint64_t ws_floats(int S, int rps, int P) {
+  return (uint64_t)S * rps * P * 2 + (uint64_t)S * P * NT + (uint64_t)S * P + (uint64_t)S * 8;
+}
+
 extern "C" uint64_t qvex_spec_accept_workspace_bytes(int S, int k, int V, int has_draft) {
   if (S < 1 || k < 0 || V < 1) return 0;
   const int rps = (k + 1) + (has_draft ? k : 0);
-  return (uint64_t)S * rps * nparts(V) * 2 * sizeof(float);
+  return ws_floats(S, rps, nparts(V)) * sizeof(float);
 }
 
 extern "C" int qvex_spec_accept(const float* target, const float* draft, const int32_t* draft_ids,
@@ -399,18 +522,23 @@ extern "C" int qvex_spec_accept(const float* target, const float* draft, const i
   QVEX_CHECK_ARG(greedy || u_sample, "qvex_spec_accept: u_sample required when sampling");
   const int P = nparts(V);
   const int rps = (k + 1) + (draft ? k : 0);
-  const uint64_t need = (uint64_t)S * rps * P * 2 * sizeof(float);
+  const uint64_t need = ws_floats(S, rps, P) * sizeof(float);
   QVEX_CHECK_ARG(workspace_bytes >= need, "qvex_spec_accept: workspace %llu bytes < %llu needed",
                  (unsigned long long)workspace_bytes, (unsigned long long)need);
   const size_t lds = ((size_t)P * NT + P + 2 * rps) * sizeof(float);
   QVEX_CHECK_ARG(lds <= 150 * 1024, "qvex_spec_accept: V=%d too large for the LDS sampling table", V);
   QVEX_CHECK_ARG((long)S * rps <= 65535, "qvex_spec_accept: S*rows=%ld exceeds the grid limit", (long)S * rps);
+  QVEX_CHECK_ARG(rps <= 80, "qvex_spec_accept: k=%d too large", k);
   SpecArgs a{target, draft, draft_ids, u_accept, u_sample, inv_temp, greedy, n_accept, out_token,
              (float*)workspace, S, k, V, P, rps};
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(spec_rowstats_kernel, dim3(P, S * rps), dim3(NT), 0, st, a);
   QVEX_CHECK_LAUNCH("qvex_spec_accept/rowstats");
-  hipLaunchKernelGGL(spec_accept_kernel, dim3(S), dim3(NT), lds, st, a);
-  QVEX_CHECK_LAUNCH("qvex_spec_accept/accept");
+  hipLaunchKernelGGL(spec_decide_kernel, dim3(P, S), dim3(NT), 0, st, a);
+  QVEX_CHECK_LAUNCH("qvex_spec_accept/decide");
+  if (!greedy) {
+    hipLaunchKernelGGL(spec_sample_kernel, dim3(S), dim3(NT), lds, st, a);
+    QVEX_CHECK_LAUNCH("qvex_spec_accept/sample");
+  }
   return QVEX_OK;
 }

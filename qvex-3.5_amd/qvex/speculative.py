@@ -63,61 +63,87 @@ def _argmax(logits_row):
     return tok
 
 
+class MTPDecoder:
+    """One object per generation: holds the pending (hidden, token) pairs and
+    runs whole MTP cycles (draft k, verify k + 1, accept, rollback) or plain
+    steps. decode() wraps it in the reference's generator API; benchmarks call
+    cycle() directly."""
+
+    def __init__(self, model: Qwen35, sampler: Sampler, cache, first_logits, last_hidden=None,
+                 mtp: MTPHead | None = None, mtp_cache=None, k: int = 1, stats: dict | None = None):
+        self.model, self.sampler, self.cache = model, sampler, cache
+        self.mtp, self.mtp_cache, self.k = mtp, mtp_cache, k
+        self.stats = stats if stats is not None else {}
+        for key in ("cycles", "accepted", "plain", "emitted"):
+            self.stats.setdefault(key, 0)
+        self.feed = sampler.pick(first_logits.reshape(1, -1))        # int32 [1] on the device
+        self.pend_h = [last_hidden] if mtp is not None else []
+        self.pend_ids = [self.feed.reshape(1, 1)] if mtp is not None else []
+        self.first = int(self.feed.item())
+        self.stats["emitted"] += 1
+
+    def can_speculate(self) -> bool:
+        return self.mtp is not None and bool(self.pend_h)
+
+    def cycle(self) -> list[int]:
+        """One MTP cycle; returns the emitted tokens (n accepted drafts + 1)."""
+        k, model, sampler, cache = self.k, self.model, self.sampler, self.cache
+        h_in = self.pend_h[0] if len(self.pend_h) == 1 else torch.cat(self.pend_h, dim=1)
+        id_in = self.pend_ids[0] if len(self.pend_ids) == 1 else torch.cat(self.pend_ids, dim=1)
+        drafts = draft_tokens(self.mtp, self.mtp_cache, h_in, id_in, k)
+        ids = torch.cat([self.feed.reshape(1), drafts]).reshape(1, k + 1)
+        logits, hidden = model(ids, cache, last_only=False, return_hidden=True, keep_prev=True)
+        n_t, tok_t = sampler.accept(logits[0], drafts)
+        vals = torch.cat([n_t, tok_t, drafts]).tolist()                 # the one host sync
+        n, tok = int(vals[0]), int(vals[1])
+        self.stats["cycles"] += 1
+        self.stats["accepted"] += n
+        if n < k:
+            for c in cache:
+                c.rollback(k - n)
+        emitted = [int(t) for t in vals[2:2 + n]] + [tok]
+        tok_dev = tok_t.reshape(1, 1)
+        self.pend_h = [hidden[:, : n + 1]]
+        self.pend_ids = [torch.cat([drafts[:n].reshape(1, n), tok_dev], dim=1) if n else tok_dev]
+        self.feed = tok_t
+        self.stats["emitted"] += len(emitted)
+        return emitted
+
+    def plain(self, forced_token: int | None = None) -> int:
+        """One non-speculative step (engine/speculative.py:103-118)."""
+        model, dev = self.model, self.model.norm.device
+        if self.mtp is not None:
+            logits, hidden = model(self.feed.reshape(1, 1), self.cache, return_hidden=True)
+        else:
+            logits, hidden = model(self.feed.reshape(1, 1), self.cache), None
+        if forced_token is not None:
+            t = torch.tensor([forced_token], dtype=torch.int32, device=dev)
+        else:
+            t = self.sampler.pick(logits[0, -1:])
+        self.stats["plain"] += 1
+        if self.mtp is not None:
+            self.pend_h.append(hidden)
+            self.pend_ids.append(t.reshape(1, 1))
+            if len(self.pend_h) > MAX_PENDING:
+                self.pend_h, self.pend_ids = self.pend_h[-MAX_PENDING:], self.pend_ids[-MAX_PENDING:]
+        self.feed = t
+        self.stats["emitted"] += 1
+        return int(t.item())
+
+
 def decode(model: Qwen35, sampler: Sampler, cache, first_logits, last_hidden=None,
            mtp: MTPHead | None = None, mtp_cache=None,
            use_mtp: Callable[[], bool] = lambda: True, stats: dict | None = None,
            forced: list[int] | None = None, k: int = 1):
     """Generator of token ids (engine/speculative.py:44-118). stats gets 'cycles',
-    'accepted' (accepted drafts), 'plain' and 'emitted'."""
+    'accepted' (accepted drafts), 'plain' and 'emitted'. forced: tokens emitted
+    next, in order, instead of sampled ones (plain steps only)."""
     forced = forced if forced is not None else []
-    stats = stats if stats is not None else {}
-    for key in ("cycles", "accepted", "plain", "emitted"):
-        stats.setdefault(key, 0)
-    dev = model.norm.device
-
-    feed = sampler.pick(first_logits.reshape(1, -1))            # int32 [1]
-    pend_h = [last_hidden] if mtp is not None else []
-    pend_ids = [feed.reshape(1, 1)] if mtp is not None else []
-    stats["emitted"] += 1
-    yield int(feed.item())
-
+    dec = MTPDecoder(model, sampler, cache, first_logits, last_hidden, mtp, mtp_cache, k, stats)
+    yield dec.first
     while True:
-        if mtp is not None and pend_h and not forced and use_mtp():
-            h_in = pend_h[0] if len(pend_h) == 1 else torch.cat(pend_h, dim=1)
-            id_in = pend_ids[0] if len(pend_ids) == 1 else torch.cat(pend_ids, dim=1)
-            drafts = draft_tokens(mtp, mtp_cache, h_in, id_in, k)
-            ids = torch.cat([feed.reshape(1), drafts]).reshape(1, k + 1)
-            logits, hidden = model(ids, cache, last_only=False, return_hidden=True, keep_prev=True)
-            n_t, tok_t = sampler.accept(logits[0], drafts)
-            n, tok = (int(v) for v in torch.cat([n_t, tok_t]).tolist())   # the one host sync
-            stats["cycles"] += 1
-            stats["accepted"] += n
-            if n < k:
-                for c in cache:
-                    c.rollback(k - n)
-            emitted = [int(t) for t in drafts[:n].tolist()] + [tok]
-            tok_dev = tok_t.reshape(1, 1)
-            pend_h = [hidden[:, : n + 1]]
-            pend_ids = [torch.cat([drafts[:n].reshape(1, n), tok_dev], dim=1) if n else tok_dev]
-            feed = tok_t
-            for t in emitted:
-                stats["emitted"] += 1
+        if dec.can_speculate() and not forced and use_mtp():
+            for t in dec.cycle():
                 yield t
         else:
-            if mtp is not None:
-                logits, hidden = model(feed.reshape(1, 1), cache, return_hidden=True)
-            else:
-                logits, hidden = model(feed.reshape(1, 1), cache), None
-            if forced:
-                t = torch.tensor([forced.pop(0)], dtype=torch.int32, device=dev)
-            else:
-                t = sampler.pick(logits[0, -1:])
-            stats["plain"] += 1
-            if mtp is not None:
-                pend_h.append(hidden)
-                pend_ids.append(t.reshape(1, 1))
-                if len(pend_h) > MAX_PENDING:
-                    pend_h, pend_ids = pend_h[-MAX_PENDING:], pend_ids[-MAX_PENDING:]
-            feed = t
-            stats["emitted"] += 1
-            yield int(t.item())
+            yield dec.plain(forced.pop(0) if forced else None)
