@@ -87,13 +87,38 @@ def qmv_time(M, N, K, iters=None, tile=None, seed_tag=0):
     return best, algo
 
 
+def read_roof_calibration(nbytes=28344320 // 16 * 16, copies=24, reps=3):
+    """Stream-read `copies` distinct buffers of nbytes with qvex_read_roof: a
+    kernel of known traffic, for scaling PMC byte counters (FETCH_SIZE)."""
+    import torch
+    from qvex import kernels
+    buf = torch.empty(copies * nbytes // 4, dtype=torch.int32, device="cuda:0").random_()
+    sink = torch.zeros(64, dtype=torch.int32, device="cuda:0")
+    for _ in range(reps):
+        for c in range(copies):
+            kernels.read_roof(buf[c * nbytes // 4:(c + 1) * nbytes // 4], sink, 2048)
+    torch.cuda.synchronize()
+    return nbytes
+
+
+PROFILE = REPO / "profiles" / "qmv_gemv_12288x4096_m1.json"
+
+
 def roofline_qmv0():
     us, algo = qmv_time(1, 12288, 4096)
     ach = algo / (us * 1e-6) / 1e9
-    return {"kernel": "qvex_qmv_w4g64 (M=1, N=12288, K=4096)", "bound": "hbm",
-            "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
-            "algorithmic_bytes_per_launch": int(algo), "avg_launch_us": round(us, 3)}
+    out = {"kernel": "qvex_qmv_w4g64 (M=1, N=12288, K=4096)", "bound": "hbm",
+           "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+           "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
+           "algorithmic_bytes_per_launch": int(algo), "avg_launch_us": round(us, 3)}
+    # HBM bytes per launch come from rocprofv3 FETCH_SIZE/WRITE_SIZE passes of this
+    # same command (calibrated on a read of known size), kept in profiles/
+    if PROFILE.exists():
+        prof = json.loads(PROFILE.read_text())
+        out["traffic"] = prof["traffic_bytes_per_launch"]
+        out["traffic_source"] = f"{PROFILE.relative_to(REPO)} ({prof['calibration']})"
+        out["rocprof_avg_launch_us"] = prof["avg_us"]
+    return out
 
 
 def qmv_shapes():
@@ -246,6 +271,7 @@ def main():
     log("qmv roofline")
     line["roofline"] = roofline_qmv0()
     if args.workload == "qmv":
+        line["read_roof_calibration_bytes"] = read_roof_calibration()
         line.update({"value": line["roofline"]["achieved"], "unit": "GB/s",
                      "ms_per_step": line["roofline"]["avg_launch_us"] / 1e3,
                      "config": {"workload": "4-bit group-64 GEMV, x bf16 [1,4096], W [12288,4096]"}})
