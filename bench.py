@@ -8,7 +8,8 @@ Gated DeltaNet + 8 gated attention, hidden 4096, MLP 12288, vocab 248320, 4-bit
 group-64 MLX-layout weights) with an MTP draft head sharing the lm_head. A
 4096-token prompt of seeded uniform ids is prefilled (untimed), then W warmup
 cycles run, then exactly K timed MTP cycles (draft k=3 greedy, verify 4 tokens,
-accept at T=0.7, roll back). value = tokens emitted in the timed cycles / time.
+accept at T=0.7, roll back; the cycle is captured once as a HIP graph and
+replayed). value = tokens emitted in the timed cycles / time.
 
 Every line also carries:
   roofline: the 4-bit GEMV of 12288 x 4096 (one M=1 qmv), timed with HIP events
@@ -183,7 +184,7 @@ def run_e2e(args):
     from qvex.model import Config, random_model
     from qvex.mtp import random_mtp
     from qvex.sampler import Sampler, SamplingParams
-    from qvex.speculative import MTPDecoder, mtp_prefill
+    from qvex.speculative import GraphedMTPCycle, MTPDecoder, mtp_prefill
     from qvex import synth
 
     cfg = Config.qwen35_9b()
@@ -206,14 +207,20 @@ def run_e2e(args):
     sampler = Sampler(SamplingParams(temperature=args.temperature, top_k=0, top_p=1.0, seed=synth.SEED_E2E), cfg.vocab_size)
     stats = {}
     dec = MTPDecoder(model, sampler, cache, logits[0, -1], last_h, mtp, mcache, k=args.k, stats=stats)
+    runner = dec
+    if not args.eager:
+        dec.cycle()                        # one eager cycle, then capture the cycle as a HIP graph
+        t0 = time.perf_counter()
+        runner = GraphedMTPCycle(dec)
+        log(f"cycle captured as a HIP graph in {time.perf_counter() - t0:.2f}s")
     for _ in range(args.warmup):
-        dec.cycle()
+        runner.cycle()
     torch.cuda.synchronize()
     e0 = stats["emitted"]
     a0, c0 = stats["accepted"], stats["cycles"]
     t0 = time.perf_counter()
     for i in range(args.steps):
-        dec.cycle()
+        runner.cycle()
         if (i + 1) % 64 == 0:
             log(f"cycle {i + 1}/{args.steps}")
     torch.cuda.synchronize()
@@ -237,6 +244,7 @@ def main():
     ap.add_argument("--temperature", type=float, default=0.7)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-shapes", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="launch every kernel from Python (no HIP graph)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (collectives are out of scope); "
@@ -260,7 +268,7 @@ def main():
                                       "+ 8 gated attention, hidden 4096, MLP 12288, vocab 248320), 4-bit g64 "
                                       "weights, MTP head drafting k=3, T=0.7, 4096-token prompt",
                           "k": args.k, "prompt_tokens": args.prompt, "temperature": args.temperature,
-                          "cycles_timed": args.steps}
+                          "cycles_timed": args.steps, "hip_graph": not args.eager}
         line["tokens_per_cycle"] = round(res["tokens_per_cycle"], 4)
         line["acceptance"] = round(res["acceptance"], 4)
         line["prefill_s"] = round(res["prefill_s"], 2)

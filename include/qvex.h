@@ -193,9 +193,9 @@ int qvex_bf16_to_f32(const uint16_t* in, float* out, long n, void* stream);
 /* Attention input stage (engine/model.py:213-226): q and k rms-normalised per
  * head with q_norm / k_norm, NeoX-form RoPE on the first rot_dim dims at
  * positions *pos0 + l (pos0 a device int32), q written to q_out [L, Hq, D],
- * k and v appended to k_cache / v_cache [Hkv, cap, D] at those positions
- * (KVCache.update, engine/model.py:156-170). proj row = [Hq x (q | gate) | Hkv
- * x k | Hkv x v]. */
+ * k appended to k_cache [Hkv, cap, D] and v to the dim-major v_cache
+ * [Hkv, D, cap] at those positions (KVCache.update, engine/model.py:156-170).
+ * proj row = [Hq x (q | gate) | Hkv x k | Hkv x v]. */
 int qvex_attn_qk_rope(const uint16_t* proj, long p_stride, const uint16_t* q_norm,
                       const uint16_t* k_norm, const int32_t* pos0, int L, int Hq, int Hkv, int D,
                       int rot_dim, float theta, float eps, uint16_t* q_out, uint16_t* k_cache,
@@ -211,6 +211,30 @@ int qvex_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v
                    const int32_t* pos0, int L, int Hq, int Hkv, int D, int cap, int max_keys,
                    int keys_per_split, const uint16_t* gate, long gate_stride, uint16_t* out,
                    void* workspace, uint64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Device-side cycle bookkeeping (host side of decode(),
+ * engine/speculative.py:82-102), so a whole MTP cycle can be captured once in a
+ * HIP graph and replayed with one host synchronisation.
+ * ------------------------------------------------------------------------ */
+
+/* dst[0:H) = src[clamp(*idx, 0, rows-1) * row_stride + 0:H): the row of the
+ * last valid pending pair, selected on the device. */
+int qvex_gather_row(const uint16_t* src, long row_stride, const int32_t* idx, int rows,
+                    uint16_t* dst, int H, void* stream);
+
+/* ids = [*feed, drafts[0] .. drafts[k-1]]: the verify input. */
+int qvex_assemble_ids(const int32_t* feed, const int32_t* drafts, int k, int32_t* ids, void* stream);
+
+/* After the accept: pend_ids = [d_0 .. d_{n-1}, token, 0 ...] (k + 1 slots),
+ * *feed = token, *n_prev = n, out = [n, token, d_0 .. d_{k-1}] for the host. */
+int qvex_cycle_finish(const int32_t* drafts, int k, const int32_t* n_accept, const int32_t* token,
+                      int32_t* pend_ids, int32_t* feed, int32_t* n_prev, int32_t* out, void* stream);
+
+/* out[0:width) = table[*counter mod rows]; then *counter += 1 (the cycle's
+ * uniforms from a pre-drawn table). */
+int qvex_next_uniforms(const float* table, int rows, int width, int32_t* counter, float* out,
+                       void* stream);
 
 /* Pure streaming read of `bytes` bytes (multiple of 16) from `buf`, folding
  * them into `sink` (64 uint32 words). Measures the achievable HBM read rate;

@@ -1,0 +1,90 @@
+// Device-side bookkeeping of one MTP cycle, so the whole cycle (draft k, verify
+// k + 1, accept, commit) can be captured once in a HIP graph and replayed with a
+// single host synchronisation. Every quantity that varies between cycles - the
+// accepted count, the drawn token, the pending (hidden, token) pairs of the MTP
+// head, the uniforms' position - lives in device memory read by these kernels.
+//
+// Reference: the host-side bookkeeping of decode() (engine/speculative.py:82-102):
+// mx.eval + accept.item(), pend_h / pend_ids, feed.
+#include "qvex_common.h"
+
+namespace {
+
+__global__ void gather_row_kernel(const uint16_t* __restrict__ src, long row_stride, const int32_t* __restrict__ idx,
+                                  int rows, uint16_t* __restrict__ dst, int H) {
+  int r = *idx;
+  r = r < 0 ? 0 : (r >= rows ? rows - 1 : r);
+  const uint16_t* s = src + (long)r * row_stride;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < H; i += gridDim.x * blockDim.x) dst[i] = s[i];
+}
+
+// ids[0] = *feed, ids[1 + i] = drafts[i]
+__global__ void assemble_ids_kernel(const int32_t* __restrict__ feed, const int32_t* __restrict__ drafts, int k,
+                                    int32_t* __restrict__ ids) {
+  const int i = threadIdx.x;
+  if (i == 0) ids[0] = *feed;
+  else if (i <= k) ids[i] = drafts[i - 1];
+}
+
+// After the accept: pending ids [d_0 .. d_{n-1}, tok, 0 ...] (k + 1 slots),
+// feed = tok, n_prev = n, out = [n, tok, d_0 .. d_{k-1}] for the host.
+__global__ void cycle_finish_kernel(const int32_t* __restrict__ drafts, int k, const int32_t* __restrict__ n_ptr,
+                                    const int32_t* __restrict__ tok_ptr, int32_t* __restrict__ pend_ids,
+                                    int32_t* __restrict__ feed, int32_t* __restrict__ n_prev, int32_t* __restrict__ out) {
+  const int i = threadIdx.x;
+  const int n = *n_ptr, tok = *tok_ptr;
+  if (i <= k) pend_ids[i] = i < n ? drafts[i] : (i == n ? tok : 0);
+  if (i < k) out[2 + i] = drafts[i];
+  if (i == 0) {
+    *feed = tok;
+    *n_prev = n;
+    out[0] = n;
+    out[1] = tok;
+  }
+}
+
+// out[0 .. width) = table[*counter % rows]; then ++*counter
+__global__ void next_uniforms_kernel(const float* __restrict__ table, int rows, int width, int32_t* __restrict__ counter,
+                                     float* __restrict__ out) {
+  const int r = ((*counter % rows) + rows) % rows;
+  const int i = threadIdx.x;
+  if (i < width) out[i] = table[(long)r * width + i];
+  __syncthreads();
+  if (i == 0) *counter += 1;
+}
+
+}  // namespace
+
+extern "C" int qvex_gather_row(const uint16_t* src, long row_stride, const int32_t* idx, int rows, uint16_t* dst,
+                               int H, void* stream) {
+  QVEX_CHECK_ARG(src && idx && dst && rows >= 1 && H >= 1 && row_stride >= H, "qvex_gather_row: bad arguments");
+  hipLaunchKernelGGL(gather_row_kernel, dim3((H + 255) / 256), dim3(256), 0, (hipStream_t)stream, src, row_stride,
+                     idx, rows, dst, H);
+  QVEX_CHECK_LAUNCH("qvex_gather_row");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_assemble_ids(const int32_t* feed, const int32_t* drafts, int k, int32_t* ids, void* stream) {
+  QVEX_CHECK_ARG(feed && ids && (k == 0 || drafts) && k >= 0 && k < 256, "qvex_assemble_ids: bad arguments");
+  hipLaunchKernelGGL(assemble_ids_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, feed, drafts, k, ids);
+  QVEX_CHECK_LAUNCH("qvex_assemble_ids");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_cycle_finish(const int32_t* drafts, int k, const int32_t* n_accept, const int32_t* token,
+                                 int32_t* pend_ids, int32_t* feed, int32_t* n_prev, int32_t* out, void* stream) {
+  QVEX_CHECK_ARG(drafts && n_accept && token && pend_ids && feed && n_prev && out && k >= 1 && k < 255,
+                 "qvex_cycle_finish: bad arguments");
+  hipLaunchKernelGGL(cycle_finish_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, drafts, k, n_accept, token,
+                     pend_ids, feed, n_prev, out);
+  QVEX_CHECK_LAUNCH("qvex_cycle_finish");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_next_uniforms(const float* table, int rows, int width, int32_t* counter, float* out,
+                                  void* stream) {
+  QVEX_CHECK_ARG(table && counter && out && rows >= 1 && width >= 1 && width <= 256, "qvex_next_uniforms: bad arguments");
+  hipLaunchKernelGGL(next_uniforms_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, table, rows, width, counter, out);
+  QVEX_CHECK_LAUNCH("qvex_next_uniforms");
+  return QVEX_OK;
+}

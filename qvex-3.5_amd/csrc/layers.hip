@@ -289,146 +289,170 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
     uint16_t* dst = q_out + ((size_t)l * Hq + h) * D;
     for (int i = 0; i < per; ++i) dst[lane + 64 * i] = f32_to_bf16(x[i]);
   } else if (pos >= 0 && pos < cap) {
+    // K key-major [Hkv, cap, D]; V dim-major [Hkv, D, cap] (the P.V MFMA reads
+    // 8 consecutive keys of one dim per lane)
     uint16_t* kd = k_cache + ((size_t)kh * cap + pos) * D;
-    uint16_t* vd = v_cache + ((size_t)kh * cap + pos) * D;
     const uint16_t* vs = proj + (size_t)l * p_stride + (size_t)Hq * 2 * D + (size_t)Hkv * D + (size_t)kh * D;
     for (int i = 0; i < per; ++i) {
       kd[lane + 64 * i] = f32_to_bf16(x[i]);
-      vd[lane + 64 * i] = vs[lane + 64 * i];
+      v_cache[((size_t)kh * D + lane + 64 * i) * cap + pos] = vs[lane + 64 * i];
     }
   }
 }
 
-// ---------------------------------------------------------------- attention: split-K over the cache
+// ---------------------------------------------------------------- attention: split-K over the cache (MFMA)
 //
-// Block = (kv head, query tile, key split). The tile's rows are GQ query heads x
-// QT query positions (GQ = Hq / Hkv); row r = (head g = r / QT, position
-// lq = r % QT). Query l attends keys [0, *pos0 + l]. Keys are processed 64 at a
-// time: lane j scores key j against every row (q rows staged in LDS as fp32),
-// the tile's softmax runs online per row, and P.V is accumulated with lanes
-// over head dims. Partials (m, l, o[D]) go to the workspace; the combine
-// kernel merges splits, normalises, applies sigmoid(gate) and writes bf16.
-constexpr int ATT_KT = 64;
+// One wave per (kv head, query tile, key split). The tile's 16 rows are GQ query
+// heads x QT positions (row r = head r / QT, position tile*QT + r % QT); query l
+// sees keys [0, *pos0 + l]. For each 16-key block:
+//   S[16 x 16] = Q[16 x D] K^T with v_mfma_f32_16x16x32_bf16 (D/32 steps; lane l
+//   holds Q row l%16 dims 8(l/16).. and key l%16 of the block, same dims);
+//   the accumulator puts rows 4(l/16)+r in lane l at key l%16, so row max / sum
+//   are 16-lane DPP reductions; online softmax rescales O in place;
+//   P (bf16) goes through 1 KB of LDS into the A layout, and O[16 x D] += P V
+//   with V stored dim-major, so lane l reads 8 consecutive keys of dim l%16.
+// Partials (m, l, O) per row go to the workspace; attn_combine merges splits.
+typedef __bf16 att_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float att_f32x4 __attribute__((ext_vector_type(4)));
 
-template <int D, int ROWS>
-__global__ __launch_bounds__(256) void attn_partial_kernel(
+template <int CTRL>
+__device__ __forceinline__ float dpp_row16(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_row16<0xB1>(v));
+  v = fmaxf(v, dpp_row16<0x4E>(v));
+  v = fmaxf(v, dpp_row16<0x124>(v));
+  v = fmaxf(v, dpp_row16<0x128>(v));
+  return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_row16<0xB1>(v);
+  v += dpp_row16<0x4E>(v);
+  v += dpp_row16<0x124>(v);
+  v += dpp_row16<0x128>(v);
+  return v;
+}
+
+__device__ __forceinline__ att_bf16x8 as_att8(const u32x4 v) { return __builtin_bit_cast(att_bf16x8, v); }
+
+template <int D>
+__global__ __launch_bounds__(64) void attn_mfma_partial_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
-    const int32_t* __restrict__ pos0, int L, int Hq, int Hkv, int cap, int QT, int keys_per_split,
-    float scale, float* __restrict__ ws) {
-  constexpr int PER = D / 64;
-  const int kh = blockIdx.x;
-  const int tile = blockIdx.y;
-  const int split = blockIdx.z;
+    const int32_t* __restrict__ pos0, int L, int Hq, int Hkv, int cap, int QT, int keys_per_split, float scale,
+    float* __restrict__ ws) {
+  constexpr int KS = D / 32;     // MFMA steps over head dims
+  constexpr int NT = D / 16;     // 16-dim output tiles of O
+  const int kh = blockIdx.x, tile = blockIdx.y, split = blockIdx.z;
+  const int lane = threadIdx.x;
+  const int li = lane & 15, lg = lane >> 4;
   const int GQ = Hq / Hkv;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  __shared__ float qs[ROWS][D];
-  __shared__ float ps[4][ROWS][ATT_KT];
   const int p0 = *pos0;
-  const int rows = GQ * QT;
-  // stage q rows (fp32, pre-scaled)
-  for (int idx = threadIdx.x; idx < ROWS * D; idx += 256) {
-    const int r = idx / D, d = idx % D;
-    float val = 0.0f;
-    if (r < rows) {
-      const int g = r / QT, lq = tile * QT + r % QT;
-      if (lq < L) val = bf16_to_f32(q[((size_t)lq * Hq + kh * GQ + g) * D + d]) * scale;
-    }
-    qs[r][d] = val;
+  __shared__ uint32_t ps[16][17];  // P tile, bf16 pairs [row][key pair], padded
+
+  // A operand: Q row li, dims step*32 + 8*lg .. +7 (the 1/sqrt(D) scale is applied to the scores)
+  u32x4 qa[KS];
+  {
+    const int g = li / QT, lq = tile * QT + li % QT;
+    const bool ok = g < GQ && lq < L;
+    const uint16_t* qp = q + ((size_t)(ok ? lq : 0) * Hq + kh * GQ + (ok ? g : 0)) * D + 8 * lg;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qa[s] = ok ? load16(qp + 32 * s) : u32x4{0, 0, 0, 0};
   }
-  __syncthreads();
-  const int kend_tile = p0 + min(L, (tile + 1) * QT);      // exclusive bound over the tile's rows
+  // the 4 rows this lane owns in accumulator layout: r = 4*lg + j
+  int rlim[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 4 * lg + j;
+    const int g = r / QT, lq = tile * QT + r % QT;
+    rlim[j] = (g < GQ && lq < L) ? p0 + lq : -1;     // last visible key, -1 = dead row
+  }
+  const int kend_tile = p0 + min(L, (tile + 1) * QT);
   const int k_lo = split * keys_per_split;
   const int k_hi = min(k_lo + keys_per_split, kend_tile);
-  // each wave takes key blocks k_lo + (wave + 4 i) * 64
-  float m_r[ROWS], l_r[ROWS], o_r[ROWS][PER];
+
+  float m_r[4], l_r[4];
+  att_f32x4 o[NT];
 #pragma unroll
-  for (int r = 0; r < ROWS; ++r) {
-    m_r[r] = -INFINITY;
-    l_r[r] = 0.0f;
+  for (int j = 0; j < 4; ++j) { m_r[j] = -INFINITY; l_r[j] = 0.0f; }
 #pragma unroll
-    for (int e = 0; e < PER; ++e) o_r[r][e] = 0.0f;
-  }
-  for (int kb = k_lo + wave * ATT_KT; kb < k_hi; kb += 4 * ATT_KT) {
-    const int key = kb + lane;
-    const bool kv = key < k_hi;
-    float sc[ROWS];
+  for (int t = 0; t < NT; ++t) o[t] = att_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const uint16_t* kbase = k_cache + (size_t)kh * cap * D;
+  const uint16_t* vbase = v_cache + (size_t)kh * D * cap;
+  for (int kb = k_lo; kb < k_hi; kb += 32) {
+    // two 16-key score tiles
+    att_f32x4 sc[2];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) sc[r] = 0.0f;
-    if (kv) {
-      const uint16_t* kp = k_cache + ((size_t)kh * cap + key) * D;
-      for (int d = 0; d < D; d += 8) {
-        const u32x4 kk = load16(kp + d);
-        const float kf[8] = {bf16_lo(kk.x), bf16_hi(kk.x), bf16_lo(kk.y), bf16_hi(kk.y),
-                             bf16_lo(kk.z), bf16_hi(kk.z), bf16_lo(kk.w), bf16_hi(kk.w)};
+    for (int h = 0; h < 2; ++h) {
+      const int key = min(kb + 16 * h + li, cap - 1);
+      const uint16_t* kp = kbase + (size_t)key * D + 8 * lg;
+      att_f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r)
+      for (int s = 0; s < KS; ++s)
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_att8(qa[s]), as_att8(load16(kp + 32 * s)), c, 0, 0, 0);
+      sc[h] = c;
+    }
+    // online softmax per row (row = 4*lg + j, keys across the 16 lanes of the group)
+    float p[2][4];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) sc[r] = fmaf(qs[r][d + e], kf[e], sc[r]);
+    for (int j = 0; j < 4; ++j) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int key = kb + 16 * h + li;
+        const bool vis = key < k_hi && key <= rlim[j];
+        sc[h][j] = vis ? sc[h][j] * scale : -INFINITY;
+        mx = fmaxf(mx, sc[h][j]);
       }
-    }
+      mx = row16_max(mx);
+      const float mnew = fmaxf(m_r[j], mx);
+      const float corr = (mnew == -INFINITY) ? 1.0f : expf(m_r[j] - mnew);
+      float sum = 0.0f;
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) {
-      const int lq = tile * QT + r % QT;
-      const bool ok = kv && r < rows && lq < L && key <= p0 + lq;
-      const float s = ok ? sc[r] : -INFINITY;
-      const float mt = wave_allmax(s);
-      const float mnew = fmaxf(m_r[r], mt);
-      const float p = ok ? expf(s - mnew) : 0.0f;
-      const float corr = (m_r[r] == -INFINITY) ? 0.0f : expf(m_r[r] - mnew);
-      l_r[r] = l_r[r] * corr + wave_allsum(p);
-      m_r[r] = mnew;
-#pragma unroll
-      for (int e = 0; e < PER; ++e) o_r[r][e] *= corr;
-      ps[wave][r][lane] = p;
-    }
-    // P.V: lane owns dims lane + 64 e
-    const int nk = min(ATT_KT, k_hi - kb);
-    for (int j = 0; j < nk; ++j) {
-      const uint16_t* vp = v_cache + ((size_t)kh * cap + kb + j) * D;
-      float vf[PER];
-#pragma unroll
-      for (int e = 0; e < PER; ++e) vf[e] = bf16_to_f32(vp[lane + 64 * e]);
-#pragma unroll
-      for (int r = 0; r < ROWS; ++r) {
-        const float p = ps[wave][r][j];
-#pragma unroll
-        for (int e = 0; e < PER; ++e) o_r[r][e] = fmaf(p, vf[e], o_r[r][e]);
+      for (int h = 0; h < 2; ++h) {
+        p[h][j] = (sc[h][j] == -INFINITY) ? 0.0f : expf(sc[h][j] - mnew);
+        sum += p[h][j];
       }
+      l_r[j] = l_r[j] * corr + row16_sum(sum);
+      m_r[j] = mnew;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) o[t][j] *= corr;
+    }
+    // P to the A layout through LDS: ps[row][key/2] holds bf16 pairs
+    {
+      uint16_t* ps16 = reinterpret_cast<uint16_t*>(&ps[0][0]);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ps16[(4 * lg + j) * 34 + 16 * h + li] = f32_to_bf16(p[h][j]);
+    }
+    __syncthreads();
+    u32x4 pa;
+    {
+      const uint16_t* ps16 = reinterpret_cast<const uint16_t*>(&ps[0][0]) + li * 34 + 8 * lg;
+      pa.x = (uint32_t)ps16[0] | ((uint32_t)ps16[1] << 16);
+      pa.y = (uint32_t)ps16[2] | ((uint32_t)ps16[3] << 16);
+      pa.z = (uint32_t)ps16[4] | ((uint32_t)ps16[5] << 16);
+      pa.w = (uint32_t)ps16[6] | ((uint32_t)ps16[7] << 16);
+    }
+    __syncthreads();
+    // O += P V: B operand = keys kb + 8*lg .. +7 of dim t*16 + li (dim-major V)
+    const int kv0 = min(kb + 8 * lg, cap - 8);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const u32x4 vb = load16(vbase + (size_t)(t * 16 + li) * cap + kv0);
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_att8(pa), as_att8(vb), o[t], 0, 0, 0);
     }
   }
-  // merge the 4 waves through LDS, then write the block's partial per row
-  __shared__ float mw[4][ROWS], lw[4][ROWS];
-  if (lane == 0)
+  // partials: lane (lg, li) holds rows 4*lg + j at dims t*16 + li
+  float* wsb = ws + (((size_t)kh * gridDim.y + tile) * gridDim.z + split) * 16 * (D + 2);
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) { mw[wave][r] = m_r[r]; lw[wave][r] = l_r[r]; }
-  __syncthreads();
+  for (int j = 0; j < 4; ++j) {
+    float* dst = wsb + (size_t)(4 * lg + j) * (D + 2);
+    if (li == 0) { dst[0] = m_r[j]; dst[1] = l_r[j]; }
 #pragma unroll
-  for (int r = 0; r < ROWS; ++r) {
-    float m = fmaxf(fmaxf(mw[0][r], mw[1][r]), fmaxf(mw[2][r], mw[3][r]));
-    float lsum = 0.0f;
-    float c[4];
-#pragma unroll
-    for (int wv = 0; wv < 4; ++wv) {
-      c[wv] = (mw[wv][r] == -INFINITY) ? 0.0f : expf(mw[wv][r] - m);
-      lsum += lw[wv][r] * c[wv];
-    }
-    // o: sum over waves via atomic-free staged adds in LDS (ps reused as [D])
-    __syncthreads();
-    float* acc = &ps[0][0][0];  // 4*ROWS*64 floats >= D floats
-    for (int e = 0; e < PER; ++e)
-      if (wave == 0) acc[lane + 64 * e] = o_r[r][e] * c[0];
-    __syncthreads();
-    for (int wv = 1; wv < 4; ++wv) {
-      if (wave == wv)
-        for (int e = 0; e < PER; ++e) acc[lane + 64 * e] += o_r[r][e] * c[wv];
-      __syncthreads();
-    }
-    if (r < rows) {
-      float* dst = ws + ((((size_t)kh * gridDim.y + tile) * gridDim.z + split) * ROWS + r) * (D + 2);
-      if (threadIdx.x == 0) { dst[0] = m; dst[1] = lsum; }
-      for (int d = threadIdx.x; d < D; d += 256) dst[2 + d] = acc[d];
-    }
-    __syncthreads();
+    for (int t = 0; t < NT; ++t) dst[2 + t * 16 + li] = o[t][j];
   }
 }
 
@@ -596,8 +620,10 @@ extern "C" int qvex_attention(const uint16_t* q, const uint16_t* k_cache, const 
   QVEX_CHECK_ARG(q && k_cache && v_cache && pos0 && gate && out && workspace, "qvex_attention: null pointer");
   QVEX_CHECK_ARG(L >= 1 && Hkv >= 1 && Hq % Hkv == 0 && Hq / Hkv <= ATT_ROWS, "qvex_attention: Hq=%d Hkv=%d", Hq, Hkv);
   QVEX_CHECK_ARG(D == 256 || D == 128, "qvex_attention: D=%d (128 or 256 supported)", D);
-  QVEX_CHECK_ARG(max_keys >= 1 && max_keys <= cap && keys_per_split >= ATT_KT && keys_per_split % ATT_KT == 0,
-                 "qvex_attention: max_keys=%d cap=%d keys_per_split=%d", max_keys, cap, keys_per_split);
+  QVEX_CHECK_ARG(max_keys >= 1 && max_keys <= cap && keys_per_split >= 32 && keys_per_split % 32 == 0 &&
+                     cap % 8 == 0 && cap >= 32,
+                 "qvex_attention: max_keys=%d cap=%d keys_per_split=%d (multiples of 32, cap %% 8 == 0)", max_keys,
+                 cap, keys_per_split);
   const uint64_t need = qvex_attn_workspace_bytes(L, Hq, Hkv, D, max_keys, keys_per_split);
   QVEX_CHECK_ARG(workspace_bytes >= need, "qvex_attention: workspace %llu < %llu bytes",
                  (unsigned long long)workspace_bytes, (unsigned long long)need);
@@ -609,13 +635,13 @@ extern "C" int qvex_attention(const uint16_t* q, const uint16_t* k_cache, const 
   const float scale = 1.0f / sqrtf((float)D);
   hipStream_t st = (hipStream_t)stream;
   if (D == 256) {
-    hipLaunchKernelGGL((attn_partial_kernel<256, ATT_ROWS>), dim3(Hkv, ntile, nsplit), dim3(256), 0, st, q, k_cache,
+    hipLaunchKernelGGL((attn_mfma_partial_kernel<256>), dim3(Hkv, ntile, nsplit), dim3(64), 0, st, q, k_cache,
                        v_cache, pos0, L, Hq, Hkv, cap, QT, keys_per_split, scale, (float*)workspace);
     QVEX_CHECK_LAUNCH("qvex_attention/partial");
     hipLaunchKernelGGL((attn_combine_kernel<256, ATT_ROWS>), dim3(Hkv, ntile, ATT_ROWS), dim3(256), 0, st,
                        (const float*)workspace, nsplit, ntile, L, Hq, Hkv, QT, gate, gate_stride, out);
   } else {
-    hipLaunchKernelGGL((attn_partial_kernel<128, ATT_ROWS>), dim3(Hkv, ntile, nsplit), dim3(256), 0, st, q, k_cache,
+    hipLaunchKernelGGL((attn_mfma_partial_kernel<128>), dim3(Hkv, ntile, nsplit), dim3(64), 0, st, q, k_cache,
                        v_cache, pos0, L, Hq, Hkv, cap, QT, keys_per_split, scale, (float*)workspace);
     QVEX_CHECK_LAUNCH("qvex_attention/partial");
     hipLaunchKernelGGL((attn_combine_kernel<128, ATT_ROWS>), dim3(Hkv, ntile, ATT_ROWS), dim3(256), 0, st,

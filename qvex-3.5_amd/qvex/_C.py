@@ -31,6 +31,10 @@ SIGNATURES: dict[str, list] = {
     "qvex_add_rmsnorm": [P, P, P, P, P, I, I, F, P],
     "qvex_gdn_conv_qk": [P, LNG, P, I, P, P, I, P, P, P, P, P, I, I, I, I, I, F, F, F, P],
     "qvex_commit_step": [P, I, P, I, P],
+    "qvex_gather_row": [P, LNG, P, I, P, I, P],
+    "qvex_assemble_ids": [P, P, I, P, P],
+    "qvex_cycle_finish": [P, I, P, P, P, P, P, P, P],
+    "qvex_next_uniforms": [P, I, I, P, P, P],
     "qvex_gated_rmsnorm": [P, P, LNG, I, P, P, I, I, F, P],
     "qvex_swiglu": [P, P, I, I, P],
     "qvex_bf16_to_f32": [P, P, LNG, P],

@@ -199,6 +199,9 @@ class CacheCounters:
         self.host = np.zeros(n, np.int32)
         self.dev = torch.zeros(n, dtype=torch.int32, device=device)
         self.dirty = False
+        # in graph mode the device table is authoritative (advanced by captured
+        # commit kernels) and the host mirror is kept by the replaying code
+        self.graph_mode = False
 
     def get(self, i: int) -> int:
         return int(self.host[i])
@@ -208,6 +211,8 @@ class CacheCounters:
         self.dirty = True
 
     def sync(self) -> None:
+        if self.graph_mode:
+            return
         if self.dirty:
             # from pageable memory: the runtime stages the bytes before returning,
             # so later host edits cannot race the copy
@@ -219,7 +224,8 @@ class CacheCounters:
 
 
 class KVCache:
-    """bf16 K/V [Hkv, cap, D], preallocated (engine/model.py:149-176 grows in
+    """bf16 K [Hkv, cap, D] and V [Hkv, D, cap] (dim-major, what the P.V MFMA
+    reads), preallocated (engine/model.py:149-176 grows [B, H, cap, D] arrays in
     256-token steps instead). rollback(n) is offset -= n."""
 
     step = 256
@@ -232,7 +238,7 @@ class KVCache:
         self.counters, self.index = counters, index
         self.capacity = int(math.ceil(max(capacity, 1) / self.step) * self.step)
         self.k = torch.zeros((n_kv, self.capacity, head_dim), dtype=torch.bfloat16, device=device)
-        self.v = torch.zeros_like(self.k)
+        self.v = torch.zeros((n_kv, head_dim, self.capacity), dtype=torch.bfloat16, device=device)
 
     @property
     def offset(self) -> int:
@@ -332,9 +338,9 @@ class Attention:
         _C.call("qvex_attn_qk_rope", _ptr(proj), proj.stride(0), _ptr(self.q_norm), _ptr(self.k_norm), pos,
                 L, H, Hkv, D, cfg.rotary_dim, float(cfg.rope_theta), float(cfg.rms_norm_eps), _ptr(q),
                 _ptr(cache.k), _ptr(cache.v), cache.capacity, _stream())
-        max_keys = min(cache.capacity, cache.offset + L)
-        kps = 256 if L <= 8 else cache.capacity
-        kps = max(64, (kps + 63) // 64 * 64)
+        # a captured call must work for every later context length: bound by capacity
+        max_keys = cache.capacity if cache.counters.graph_mode else min(cache.capacity, cache.offset + L)
+        kps = 64 if L <= 8 else 512        # keys per wave: verify spreads over ~ctx/64 waves per kv head
         ws = self._workspace(L, max_keys, kps, x.device)
         o = torch.empty((L, H * D), dtype=torch.bfloat16, device=x.device)
         _C.call("qvex_attention", _ptr(q), _ptr(cache.k), _ptr(cache.v), pos, L, H, Hkv, D, cache.capacity,

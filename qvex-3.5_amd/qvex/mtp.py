@@ -41,10 +41,12 @@ class MTPHead:
         return KVCache(None, 0, n_kv=cfg.num_key_value_heads, head_dim=cfg.head_dim,
                        capacity=max_context or self.model.max_context, device=self.model.norm.device)
 
-    def __call__(self, hidden, next_ids, cache: KVCache, last_only=True, return_hidden=False):
+    def __call__(self, hidden, next_ids, cache: KVCache, last_only=True, return_hidden=False, select=None):
         """hidden [1, T, H] (main model, pre-norm) and next_ids [1, T] -> logits
         [1, 1 or T, V] (engine/mtp.py:58-68); with return_hidden also the block
-        output [1, T, H] before the final norm (what a chained draft step takes)."""
+        output [1, T, H] before the final norm (what a chained draft step takes).
+        select: optional device int32 [1] row index; only that row goes through
+        the lm_head (and is returned as the hidden), chosen on the device."""
         H = self.model.cfg.hidden_size
         h = hidden.reshape(-1, H)
         ids = torch.as_tensor(next_ids, device=h.device).reshape(-1)
@@ -60,6 +62,13 @@ class MTPHead:
         n = rms_norm(x, self.layer.ln1, self.eps)
         hh, m = self.layer(x, cache, normed=n)
         out, n_out = add_rms_norm(hh, m, self.norm_out, self.eps)
+        if select is not None:
+            n_sel = torch.empty((1, H), dtype=torch.bfloat16, device=h.device)
+            o_sel = torch.empty((1, H), dtype=torch.bfloat16, device=h.device)
+            _C.call("qvex_gather_row", _ptr(n_out), H, _ptr(select), T, _ptr(n_sel), H, _stream())
+            _C.call("qvex_gather_row", _ptr(out), H, _ptr(select), T, _ptr(o_sel), H, _stream())
+            logits = self.model.lm_head(n_sel).view(1, 1, self.model.cfg.vocab_size)
+            return (logits, o_sel.view(1, 1, H)) if return_hidden else logits
         if last_only:
             n_out = n_out[-1:]
         logits = self.model.lm_head(n_out).view(1, -1, self.model.cfg.vocab_size)

@@ -67,6 +67,17 @@ class Sampler:
         return kernels.spec_accept(t, d, draft_ids.reshape(1, k).to(torch.int32), u[:k].reshape(1, k).contiguous(),
                                    u[k:].contiguous(), self.p.temperature, workspace=self._ws[key])
 
+    def accept_device(self, target: torch.Tensor, draft_ids: torch.Tensor, u: torch.Tensor):
+        """accept() with the k + 1 uniforms given as a device fp32 [k+1] tensor
+        (no host RNG, so the call can be captured in a graph)."""
+        t = to_f32(target).reshape(1, -1, self.V)
+        k = t.shape[1] - 1
+        key = (k, False)
+        if key not in self._ws:
+            self._ws[key] = kernels.spec_workspace(1, k, self.V, False, t.device)
+        return kernels.spec_accept(t, None, draft_ids.reshape(1, k), u[:k].reshape(1, k), u[k:],
+                                   self.p.temperature, workspace=self._ws[key])
+
     def pick(self, logits: torch.Tensor) -> torch.Tensor:
         """One token per row of logits [R, V] (argmax when greedy) -> int32 [R]."""
         t = to_f32(logits).reshape(-1, 1, self.V)

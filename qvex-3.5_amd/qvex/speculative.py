@@ -15,8 +15,11 @@ from __future__ import annotations
 
 from typing import Callable
 
+import numpy as np
 import torch
 
+from . import _C
+from .kernels import _ptr, _stream
 from .model import Qwen35
 from .mtp import MTPHead
 from .sampler import Sampler
@@ -147,3 +150,105 @@ def decode(model: Qwen35, sampler: Sampler, cache, first_logits, last_hidden=Non
                 yield t
         else:
             yield dec.plain(forced.pop(0) if forced else None)
+
+
+class GraphedMTPCycle:
+    """The MTP cycle of MTPDecoder.cycle() captured once as a HIP graph.
+
+    Everything that changes between cycles is device state: the pending
+    (hidden, token) pairs of the MTP head (k + 1 fixed rows, the first n_prev + 1
+    valid), the feed token, the cache counters (advanced by captured commit
+    kernels) and the uniforms (a pre-drawn table read through a device index).
+    The MTP head's first step always runs k + 1 rows and keeps row n_prev on the
+    device; rows past it write KV entries beyond the committed position, which
+    later cycles overwrite. One replay = one cycle; the host reads
+    [n, token, drafts] once and updates its counter mirrors.
+    """
+
+    def __init__(self, dec: MTPDecoder, table_rows: int = 8192):
+        if dec.mtp is None or not dec.pend_h:
+            raise _C.QvexError("GraphedMTPCycle needs an MTPDecoder with an MTP head and pending pairs")
+        self.dec = dec
+        model, mtp, cache, mc, k = dec.model, dec.mtp, dec.cache, dec.mtp_cache, dec.k
+        self.k = k
+        dev = model.norm.device
+        H = model.cfg.hidden_size
+        h_in = dec.pend_h[0] if len(dec.pend_h) == 1 else torch.cat(dec.pend_h, dim=1)
+        id_in = dec.pend_ids[0] if len(dec.pend_ids) == 1 else torch.cat(dec.pend_ids, dim=1)
+        P = h_in.shape[1]
+        if P > k + 1:
+            raise _C.QvexError(f"{P} pending pairs exceed the captured width k + 1 = {k + 1}")
+        self.pend_h = torch.zeros((1, k + 1, H), dtype=torch.bfloat16, device=dev)
+        self.pend_h[:, :P] = h_in
+        self.pend_ids = torch.zeros((1, k + 1), dtype=torch.int32, device=dev)
+        self.pend_ids[:, :P] = id_in.to(torch.int32)
+        self.n_prev = torch.tensor([P - 1], dtype=torch.int32, device=dev)
+        self.n_prev_host = P - 1
+        self.feed = dec.feed.to(torch.int32).reshape(1).clone()
+        self.ids = torch.empty((1, k + 1), dtype=torch.int32, device=dev)
+        self.out = torch.zeros(2 + k, dtype=torch.int32, device=dev)
+        self.zero = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.u_table = torch.from_numpy(dec.sampler.rng.random((table_rows, k + 1), dtype=np.float32)).to(dev)
+        self.u_idx = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.u_buf = torch.empty(k + 1, dtype=torch.float32, device=dev)
+        # device counters must hold the host values before they become authoritative
+        cache.counters.sync()
+        mc.counters.sync()
+        torch.cuda.synchronize()
+        host_main = cache.counters.host.copy()
+        host_mtp = mc.counters.host.copy()
+        widths = [getattr(c, "last_width", None) for c in cache]
+        cache.counters.graph_mode = True
+        mc.counters.graph_mode = True
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._body()
+        cache.counters.host[:] = host_main
+        mc.counters.host[:] = host_mtp
+        for c, w in zip(cache, widths):
+            if w is not None:
+                c.last_width = w
+
+    def _commit(self, counters, n_ptr, extra):
+        _C.call("qvex_commit_step", counters.dev.data_ptr(), counters.dev.numel(), _ptr(n_ptr), int(extra), _stream())
+
+    def _body(self):
+        d = self.dec
+        k, mtp, mc = self.k, d.mtp, d.mtp_cache
+        logits, h = mtp(self.pend_h, self.pend_ids, mc, return_hidden=True, select=self.n_prev)
+        self._commit(mc.counters, self.n_prev, 1)
+        drafts = [_argmax(logits[0, -1])]
+        for _ in range(1, k):
+            logits, h = mtp(h, drafts[-1].reshape(1, 1), mc, last_only=True, return_hidden=True)
+            self._commit(mc.counters, self.zero, 1)
+            drafts.append(_argmax(logits[0, -1]))
+        if k > 1:
+            self._commit(mc.counters, self.zero, -(k - 1))
+        self.drafts = torch.cat(drafts)
+        _C.call("qvex_assemble_ids", _ptr(self.feed), _ptr(self.drafts), k, _ptr(self.ids), _stream())
+        logits, hidden = d.model(self.ids, d.cache, last_only=False, return_hidden=True, keep_prev=True)
+        self.pend_h.copy_(hidden)
+        _C.call("qvex_next_uniforms", _ptr(self.u_table), self.u_table.shape[0], k + 1, _ptr(self.u_idx),
+                _ptr(self.u_buf), _stream())
+        n, tok = d.sampler.accept_device(logits[0], self.drafts, self.u_buf)
+        self._commit(d.cache.counters, n, 1)
+        _C.call("qvex_cycle_finish", _ptr(self.drafts), k, _ptr(n), _ptr(tok), _ptr(self.pend_ids),
+                _ptr(self.feed), _ptr(self.n_prev), _ptr(self.out), _stream())
+
+    def cycle(self) -> list[int]:
+        """Replay one cycle; returns the emitted tokens (n accepted drafts + 1)."""
+        self.graph.replay()
+        vals = self.out.tolist()                       # the one host sync
+        n, tok = int(vals[0]), int(vals[1])
+        d = self.dec
+        for c in d.cache:
+            c.offset += n + 1
+        d.mtp_cache.offset += self.n_prev_host + 1
+        self.n_prev_host = n
+        d.cache.counters.dirty = False
+        d.mtp_cache.counters.dirty = False
+        emitted = [int(t) for t in vals[2:2 + n]] + [tok]
+        d.stats["cycles"] += 1
+        d.stats["accepted"] += n
+        d.stats["emitted"] += len(emitted)
+        return emitted

@@ -115,3 +115,87 @@ def test_sampled_decode(tiny):
     out, st = run_decode(tiny, mtp, 3, 0.7, 40, seed=5)
     assert len(out) == 40 and all(0 <= t < tiny.cfg.vocab_size for t in out)
     assert st["emitted"] >= 40 and st["cycles"] >= 1
+
+
+def flat_head_model(seed=12):
+    """Tiny model whose shared lm_head is exactly zero: every logit is 0, so both
+    the MTP drafts and the verify argmax are token 0 and every draft is accepted."""
+    cfg = Config.tiny(layers=4, vocab=2048)
+    m = random_model(cfg, seed=seed, device=DEV, max_context=1024)
+    m.lm_head.scales.zero_()
+    m.lm_head.biases.zero_()
+    return m
+
+
+def start_decoder(model, mtp, k, temp, seed=0):
+    from qvex.speculative import MTPDecoder
+    V = model.cfg.vocab_size
+    ids = torch.from_numpy(prompt(15, V, seed=41)).reshape(1, -1).to(DEV)
+    cache, mc = model.make_cache(), mtp.make_cache()
+    logits, hidden = model(ids, cache, return_hidden=True)
+    last_h = mtp_prefill(mtp, mc, hidden, ids, None)
+    s = Sampler(SamplingParams(temperature=temp, top_k=0, top_p=1.0, seed=seed), V)
+    return MTPDecoder(model, s, cache, logits[0, -1], last_h, mtp, mc, k=k)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("k", [1, 3])
+@pytest.mark.parametrize("head", ["random", "flat"])
+def test_graphed_cycle_equals_eager(k, head):
+    """The HIP-graph cycle (device-side pending pairs, counters, uniforms) emits
+    the eager cycle's tokens (greedy) and leaves the same cache counters, both
+    when every draft is rejected (random head) and when every draft is accepted
+    (flat head: n = k, k + 1 pending pairs per cycle)."""
+    from qvex.speculative import GraphedMTPCycle
+    m = random_model(Config.tiny(layers=4, vocab=2048), seed=12, device=DEV, max_context=1024) \
+        if head == "random" else flat_head_model()
+    mtp = random_mtp(m, seed=13)
+    eager = start_decoder(m, mtp, k, 0.0)
+    graphed = GraphedMTPCycle(start_decoder(m, mtp, k, 0.0))
+    te, tg = [], []
+    for _ in range(12):
+        te += eager.cycle()
+        tg += graphed.cycle()
+    print(head, "accepted", eager.stats["accepted"], "of", 12 * k, "graphed", graphed.dec.stats["accepted"])
+    assert te == tg
+    assert eager.stats["accepted"] == (0 if head == "random" else 12 * k)
+    assert [c.offset for c in eager.cache] == [c.offset for c in graphed.dec.cache]
+    assert eager.mtp_cache.offset == graphed.dec.mtp_cache.offset
+    assert list(graphed.dec.cache.counters.dev.cpu().numpy()) == [c.offset for c in graphed.dec.cache]
+    assert int(graphed.dec.mtp_cache.counters.dev.cpu()[0]) + graphed.n_prev_host + 1 == \
+        eager.mtp_cache.offset + len(eager.pend_ids[0][0])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [0, 1, 2, 3])
+def test_cycle_finish_bookkeeping(n):
+    from qvex import _C
+    from qvex.kernels import _ptr, _stream
+    k = 3
+    drafts = torch.tensor([11, 22, 33], dtype=torch.int32, device=DEV)
+    n_t = torch.tensor([n], dtype=torch.int32, device=DEV)
+    tok = torch.tensor([99], dtype=torch.int32, device=DEV)
+    pend = torch.full((k + 1,), -1, dtype=torch.int32, device=DEV)
+    feed, nprev = torch.zeros(1, dtype=torch.int32, device=DEV), torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = torch.zeros(k + 2, dtype=torch.int32, device=DEV)
+    _C.call("qvex_cycle_finish", _ptr(drafts), k, _ptr(n_t), _ptr(tok), _ptr(pend), _ptr(feed), _ptr(nprev),
+            _ptr(out), _stream())
+    counters = torch.tensor([5, 7, 9], dtype=torch.int32, device=DEV)
+    _C.call("qvex_commit_step", _ptr(counters), 3, _ptr(n_t), 1, _stream())
+    torch.cuda.synchronize()
+    assert pend.tolist() == [11, 22, 33][:n] + [99] + [0] * (k - n)
+    assert feed.item() == 99 and nprev.item() == n
+    assert out.tolist() == [n, 99, 11, 22, 33]
+    assert counters.tolist() == [5 + n + 1, 7 + n + 1, 9 + n + 1]
+
+
+@pytest.mark.gpu
+def test_graphed_cycle_sampled_runs():
+    from qvex.speculative import GraphedMTPCycle
+    m = flat_head_model(seed=14)
+    mtp = random_mtp(m, seed=15)
+    g = GraphedMTPCycle(start_decoder(m, mtp, 3, 0.7, seed=3))
+    out = []
+    for _ in range(30):
+        out += g.cycle()
+    assert all(0 <= t < m.cfg.vocab_size for t in out)
