@@ -204,8 +204,10 @@ int qvex_attn_qk_rope(const uint16_t* proj, long p_stride, const uint16_t* q_nor
 /* Causal GQA attention of L queries over the cache (query l sees keys
  * 0 .. *pos0 + l), scale 1/sqrt(D), output times sigmoid(gate) from the q_proj
  * rows: mx.fast.scaled_dot_product_attention + o * sigmoid(gate)
- * (engine/model.py:228-232). Split-K over keys_per_split keys per block;
- * max_keys bounds *pos0 + L. workspace: qvex_attn_workspace_bytes(). */
+ * (engine/model.py:228-232). Split-K over keys_per_split keys per block
+ * (a multiple of 128: 4 waves x 32 keys per step); max_keys bounds *pos0 + L,
+ * and only the splits below *pos0 + L do work. D is 128 or 256.
+ * workspace: qvex_attn_workspace_bytes(). */
 uint64_t qvex_attn_workspace_bytes(int L, int Hq, int Hkv, int D, int max_keys, int keys_per_split);
 int qvex_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                    const int32_t* pos0, int L, int Hq, int Hkv, int D, int cap, int max_keys,

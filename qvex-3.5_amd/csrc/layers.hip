@@ -336,19 +336,34 @@ __device__ __forceinline__ float row16_sum(float v) {
 
 __device__ __forceinline__ att_bf16x8 as_att8(const u32x4 v) { return __builtin_bit_cast(att_bf16x8, v); }
 
+// One block of 4 waves per (kv head, 16-row tile, split of keys_per_split keys).
+// Per iteration each wave takes the next 32 keys of the split (the 4 waves cover
+// 128 adjacent keys), loads their K rows and dim-major V columns in one round
+// trip, scores them with MFMA, runs an online softmax per row and accumulates
+// P V with MFMA. The 4 waves' (max, sum, O) are then merged in LDS and written as
+// one partial per block: ws [kv head][tile][split][16 rows][2 + D] = (m, l, O[D]).
 template <int D>
-__global__ __launch_bounds__(64) void attn_mfma_partial_kernel(
+__global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
     const int32_t* __restrict__ pos0, int L, int Hq, int Hkv, int cap, int QT, int keys_per_split, float scale,
     float* __restrict__ ws) {
   constexpr int KS = D / 32;     // MFMA steps over head dims
   constexpr int NT = D / 16;     // 16-dim output tiles of O
+  constexpr int OS = D + 4;      // padded LDS row of the merge buffer
   const int kh = blockIdx.x, tile = blockIdx.y, split = blockIdx.z;
-  const int lane = threadIdx.x;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int li = lane & 15, lg = lane >> 4;
   const int GQ = Hq / Hkv;
   const int p0 = *pos0;
-  __shared__ uint32_t ps[16][17];  // P tile, bf16 pairs [row][key pair], padded
+  const int kend_tile = p0 + min(L, (tile + 1) * QT);
+  const int k_lo = split * keys_per_split;
+  const int k_hi = min(k_lo + keys_per_split, kend_tile);
+  if (k_lo >= k_hi) return;      // split past the visible keys: the combine never reads it
+
+  __shared__ uint32_t ps[4][16][17];     // per-wave P tile, bf16 pairs [row][key pair], padded
+  __shared__ float ob[4][16][OS];        // per-wave O for the merge
+  __shared__ float ml[4][16][2];         // per-wave (m, l)
+  __shared__ float fac[4][16];           // merge factors e^{m_w - m}
 
   // A operand: Q row li, dims step*32 + 8*lg .. +7 (the 1/sqrt(D) scale is applied to the scores)
   u32x4 qa[KS];
@@ -367,9 +382,6 @@ __global__ __launch_bounds__(64) void attn_mfma_partial_kernel(
     const int g = r / QT, lq = tile * QT + r % QT;
     rlim[j] = (g < GQ && lq < L) ? p0 + lq : -1;     // last visible key, -1 = dead row
   }
-  const int kend_tile = p0 + min(L, (tile + 1) * QT);
-  const int k_lo = split * keys_per_split;
-  const int k_hi = min(k_lo + keys_per_split, kend_tile);
 
   float m_r[4], l_r[4];
   att_f32x4 o[NT];
@@ -380,17 +392,28 @@ __global__ __launch_bounds__(64) void attn_mfma_partial_kernel(
 
   const uint16_t* kbase = k_cache + (size_t)kh * cap * D;
   const uint16_t* vbase = v_cache + (size_t)kh * D * cap;
-  for (int kb = k_lo; kb < k_hi; kb += 32) {
-    // two 16-key score tiles
+  const int n_it = (k_hi - k_lo + 127) / 128;          // uniform over the block (LDS barriers below)
+  for (int it = 0; it < n_it; ++it) {
+    const int kb = k_lo + 128 * it + 32 * w;
+    // K rows kb + 16h + li and V columns kb + 8lg .. +7, issued together (clamped in bounds,
+    // keys past k_hi are masked out of the softmax and get P = 0)
+    u32x4 kr[2][KS], vr[NT];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint16_t* kp = kbase + (size_t)min(kb + 16 * h + li, cap - 1) * D + 8 * lg;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) kr[h][s] = load16(kp + 32 * s);
+    }
+    const int kv0 = min(kb + 8 * lg, cap - 8);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) vr[t] = load16(vbase + (size_t)(t * 16 + li) * cap + kv0);
+
     att_f32x4 sc[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int key = min(kb + 16 * h + li, cap - 1);
-      const uint16_t* kp = kbase + (size_t)key * D + 8 * lg;
       att_f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_att8(qa[s]), as_att8(load16(kp + 32 * s)), c, 0, 0, 0);
+      for (int s = 0; s < KS; ++s) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_att8(qa[s]), as_att8(kr[h][s]), c, 0, 0, 0);
       sc[h] = c;
     }
     // online softmax per row (row = 4*lg + j, keys across the 16 lanes of the group)
@@ -419,9 +442,9 @@ __global__ __launch_bounds__(64) void attn_mfma_partial_kernel(
 #pragma unroll
       for (int t = 0; t < NT; ++t) o[t][j] *= corr;
     }
-    // P to the A layout through LDS: ps[row][key/2] holds bf16 pairs
+    // P to the A layout through this wave's LDS tile
     {
-      uint16_t* ps16 = reinterpret_cast<uint16_t*>(&ps[0][0]);
+      uint16_t* ps16 = reinterpret_cast<uint16_t*>(&ps[w][0][0]);
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -430,64 +453,104 @@ __global__ __launch_bounds__(64) void attn_mfma_partial_kernel(
     __syncthreads();
     u32x4 pa;
     {
-      const uint16_t* ps16 = reinterpret_cast<const uint16_t*>(&ps[0][0]) + li * 34 + 8 * lg;
+      const uint16_t* ps16 = reinterpret_cast<const uint16_t*>(&ps[w][0][0]) + li * 34 + 8 * lg;
       pa.x = (uint32_t)ps16[0] | ((uint32_t)ps16[1] << 16);
       pa.y = (uint32_t)ps16[2] | ((uint32_t)ps16[3] << 16);
       pa.z = (uint32_t)ps16[4] | ((uint32_t)ps16[5] << 16);
       pa.w = (uint32_t)ps16[6] | ((uint32_t)ps16[7] << 16);
     }
     __syncthreads();
-    // O += P V: B operand = keys kb + 8*lg .. +7 of dim t*16 + li (dim-major V)
-    const int kv0 = min(kb + 8 * lg, cap - 8);
+    // O += P V: B operand = keys kb + 8*lg .. +7 of dim t*16 + li
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const u32x4 vb = load16(vbase + (size_t)(t * 16 + li) * cap + kv0);
-      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_att8(pa), as_att8(vb), o[t], 0, 0, 0);
-    }
+    for (int t = 0; t < NT; ++t) o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_att8(pa), as_att8(vr[t]), o[t], 0, 0, 0);
   }
-  // partials: lane (lg, li) holds rows 4*lg + j at dims t*16 + li
-  float* wsb = ws + (((size_t)kh * gridDim.y + tile) * gridDim.z + split) * 16 * (D + 2);
+
+  // merge the 4 waves: m = max_w m_w, l = sum_w l_w e^{m_w-m}, O = sum_w O_w e^{m_w-m} (fixed order w = 0..3)
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    float* dst = wsb + (size_t)(4 * lg + j) * (D + 2);
-    if (li == 0) { dst[0] = m_r[j]; dst[1] = l_r[j]; }
+    const int r = 4 * lg + j;
+    if (li == 0) { ml[w][r][0] = m_r[j]; ml[w][r][1] = l_r[j]; }
 #pragma unroll
-    for (int t = 0; t < NT; ++t) dst[2 + t * 16 + li] = o[t][j];
+    for (int t = 0; t < NT; ++t) ob[w][r][t * 16 + li] = o[t][j];
+  }
+  __syncthreads();
+  float* wsb = ws + (((size_t)kh * gridDim.y + tile) * gridDim.z + split) * 16 * (D + 2);
+  if (threadIdx.x < 16) {
+    const int r = threadIdx.x;
+    const float m = fmaxf(fmaxf(ml[0][r][0], ml[1][r][0]), fmaxf(ml[2][r][0], ml[3][r][0]));
+    float l = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float f = ml[v][r][0] == -INFINITY ? 0.0f : expf(ml[v][r][0] - m);
+      fac[v][r] = f;
+      l += ml[v][r][1] * f;
+    }
+    wsb[(size_t)r * (D + 2)] = m;
+    wsb[(size_t)r * (D + 2) + 1] = l;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < 16 * D; e += 256) {
+    const int r = e / D, d = e % D;
+    const float acc = ((ob[0][r][d] * fac[0][r] + ob[1][r][d] * fac[1][r]) + ob[2][r][d] * fac[2][r]) +
+                      ob[3][r][d] * fac[3][r];
+    wsb[(size_t)r * (D + 2) + 2 + d] = acc;
   }
 }
 
 // out[lq, (kh*GQ + g)*D + d] = bf16(sigmoid(gate) * sum_s o_s e^{m_s-m} / sum_s l_s e^{m_s-m})
-template <int D, int ROWS>
-__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ ws, int nsplit, int ntile,
-                                                           int L, int Hq, int Hkv, int QT,
-                                                           const uint16_t* __restrict__ gate, long g_stride,
-                                                           uint16_t* __restrict__ out) {
+// over the splits that hold visible keys (the count follows from the device position).
+// One block of D threads per (kv head, tile, row).
+template <int D>
+__global__ __launch_bounds__(D) void attn_combine_kernel(const float* __restrict__ ws, int nsplit, int ntile,
+                                                         int keys_per_split, const int32_t* __restrict__ pos0,
+                                                         int L, int Hq, int Hkv, int QT,
+                                                         const uint16_t* __restrict__ gate, long g_stride,
+                                                         uint16_t* __restrict__ out) {
+  constexpr int NW = D / 64;
   const int kh = blockIdx.x, tile = blockIdx.y, r = blockIdx.z;
   const int GQ = Hq / Hkv;
   if (r >= GQ * QT) return;
   const int g = r / QT, lq = tile * QT + r % QT;
   if (lq >= L) return;
   const int h = kh * GQ + g;
+  const int kend_tile = *pos0 + min(L, (tile + 1) * QT);
+  const int nact = min(nsplit, (kend_tile + keys_per_split - 1) / keys_per_split);
+  const size_t sstride = (size_t)16 * (D + 2);
+  const float* base = ws + (((size_t)kh * ntile + tile) * nsplit) * sstride + (size_t)r * (D + 2);
+  __shared__ float red[2][NW];
+  const int tid = threadIdx.x, wv = tid >> 6;
+
   float m = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) {
-    const float* p = ws + ((((size_t)kh * ntile + tile) * nsplit + s) * ROWS + r) * (D + 2);
-    m = fmaxf(m, p[0]);
+  for (int s = tid; s < nact; s += D) m = fmaxf(m, base[s * sstride]);
+  m = wave_allmax(m);
+  if ((tid & 63) == 0) red[0][wv] = m;
+  __syncthreads();
+  m = red[0][0];
+#pragma unroll
+  for (int v = 1; v < NW; ++v) m = fmaxf(m, red[0][v]);
+  float l = 0.0f;
+  for (int s = tid; s < nact; s += D) {
+    const float ms = base[s * sstride];
+    if (ms != -INFINITY) l += base[s * sstride + 1] * expf(ms - m);
   }
-  float lsum = 0.0f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float* p = ws + ((((size_t)kh * ntile + tile) * nsplit + s) * ROWS + r) * (D + 2);
-    if (p[0] != -INFINITY) lsum += p[1] * expf(p[0] - m);
+  l = wave_allsum(l);
+  if ((tid & 63) == 0) red[1][wv] = l;
+  __syncthreads();
+  l = red[1][0];
+#pragma unroll
+  for (int v = 1; v < NW; ++v) l += red[1][v];
+  const float invl = l > 0.0f ? 1.0f / l : 0.0f;
+
+  const int d = tid;
+  float o = 0.0f;
+#pragma unroll 4
+  for (int s = 0; s < nact; ++s) {
+    const float ms = base[s * sstride];
+    const float os = base[s * sstride + 2 + d];
+    if (ms != -INFINITY) o = fmaf(os, expf(ms - m), o);
   }
-  const float invl = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float o = 0.0f;
-    for (int s = 0; s < nsplit; ++s) {
-      const float* p = ws + ((((size_t)kh * ntile + tile) * nsplit + s) * ROWS + r) * (D + 2);
-      if (p[0] != -INFINITY) o = fmaf(p[2 + d], expf(p[0] - m), o);
-    }
-    const float gt = bf16_to_f32(gate[(size_t)lq * g_stride + (size_t)h * 2 * D + D + d]);
-    out[(size_t)lq * Hq * D + (size_t)h * D + d] = f32_to_bf16(o * invl * sigmoidf_(gt));
-  }
+  const float gt = bf16_to_f32(gate[(size_t)lq * g_stride + (size_t)h * 2 * D + D + d]);
+  out[(size_t)lq * Hq * D + (size_t)h * D + d] = f32_to_bf16(o * invl * sigmoidf_(gt));
 }
 
 // counters[i] += n_accept[0] + 1 for every i (advance all caches past the kept tokens)
@@ -620,9 +683,9 @@ extern "C" int qvex_attention(const uint16_t* q, const uint16_t* k_cache, const 
   QVEX_CHECK_ARG(q && k_cache && v_cache && pos0 && gate && out && workspace, "qvex_attention: null pointer");
   QVEX_CHECK_ARG(L >= 1 && Hkv >= 1 && Hq % Hkv == 0 && Hq / Hkv <= ATT_ROWS, "qvex_attention: Hq=%d Hkv=%d", Hq, Hkv);
   QVEX_CHECK_ARG(D == 256 || D == 128, "qvex_attention: D=%d (128 or 256 supported)", D);
-  QVEX_CHECK_ARG(max_keys >= 1 && max_keys <= cap && keys_per_split >= 32 && keys_per_split % 32 == 0 &&
+  QVEX_CHECK_ARG(max_keys >= 1 && max_keys <= cap && keys_per_split >= 128 && keys_per_split % 128 == 0 &&
                      cap % 8 == 0 && cap >= 32,
-                 "qvex_attention: max_keys=%d cap=%d keys_per_split=%d (multiples of 32, cap %% 8 == 0)", max_keys,
+                 "qvex_attention: max_keys=%d cap=%d keys_per_split=%d (a multiple of 128; cap %% 8 == 0)", max_keys,
                  cap, keys_per_split);
   const uint64_t need = qvex_attn_workspace_bytes(L, Hq, Hkv, D, max_keys, keys_per_split);
   QVEX_CHECK_ARG(workspace_bytes >= need, "qvex_attention: workspace %llu < %llu bytes",
@@ -634,18 +697,21 @@ extern "C" int qvex_attention(const uint16_t* q, const uint16_t* k_cache, const 
   QVEX_CHECK_ARG(ntile <= 65535 && nsplit <= 65535, "qvex_attention: grid too large");
   const float scale = 1.0f / sqrtf((float)D);
   hipStream_t st = (hipStream_t)stream;
+  const dim3 pgrid(Hkv, ntile, nsplit);
   if (D == 256) {
-    hipLaunchKernelGGL((attn_mfma_partial_kernel<256>), dim3(Hkv, ntile, nsplit), dim3(64), 0, st, q, k_cache,
-                       v_cache, pos0, L, Hq, Hkv, cap, QT, keys_per_split, scale, (float*)workspace);
+    hipLaunchKernelGGL((attn_mfma_partial_kernel<256>), pgrid, dim3(256), 0, st, q, k_cache, v_cache, pos0, L, Hq,
+                       Hkv, cap, QT, keys_per_split, scale, (float*)workspace);
     QVEX_CHECK_LAUNCH("qvex_attention/partial");
-    hipLaunchKernelGGL((attn_combine_kernel<256, ATT_ROWS>), dim3(Hkv, ntile, ATT_ROWS), dim3(256), 0, st,
-                       (const float*)workspace, nsplit, ntile, L, Hq, Hkv, QT, gate, gate_stride, out);
+    hipLaunchKernelGGL((attn_combine_kernel<256>), dim3(Hkv, ntile, ATT_ROWS), dim3(256), 0, st,
+                       (const float*)workspace, nsplit, ntile, keys_per_split, pos0, L, Hq, Hkv, QT, gate,
+                       gate_stride, out);
   } else {
-    hipLaunchKernelGGL((attn_mfma_partial_kernel<128>), dim3(Hkv, ntile, nsplit), dim3(64), 0, st, q, k_cache,
-                       v_cache, pos0, L, Hq, Hkv, cap, QT, keys_per_split, scale, (float*)workspace);
+    hipLaunchKernelGGL((attn_mfma_partial_kernel<128>), pgrid, dim3(256), 0, st, q, k_cache, v_cache, pos0, L, Hq,
+                       Hkv, cap, QT, keys_per_split, scale, (float*)workspace);
     QVEX_CHECK_LAUNCH("qvex_attention/partial");
-    hipLaunchKernelGGL((attn_combine_kernel<128, ATT_ROWS>), dim3(Hkv, ntile, ATT_ROWS), dim3(256), 0, st,
-                       (const float*)workspace, nsplit, ntile, L, Hq, Hkv, QT, gate, gate_stride, out);
+    hipLaunchKernelGGL((attn_combine_kernel<128>), dim3(Hkv, ntile, ATT_ROWS), dim3(128), 0, st,
+                       (const float*)workspace, nsplit, ntile, keys_per_split, pos0, L, Hq, Hkv, QT, gate,
+                       gate_stride, out);
   }
   QVEX_CHECK_LAUNCH("qvex_attention/combine");
   return QVEX_OK;

@@ -340,7 +340,7 @@ class Attention:
                 _ptr(cache.k), _ptr(cache.v), cache.capacity, _stream())
         # a captured call must work for every later context length: bound by capacity
         max_keys = cache.capacity if cache.counters.graph_mode else min(cache.capacity, cache.offset + L)
-        kps = 64 if L <= 8 else 512        # keys per wave: verify spreads over ~ctx/64 waves per kv head
+        kps = 128 if L <= 8 else 512       # keys per 4-wave block: verify spreads ~ctx/32 waves per kv head
         ws = self._workspace(L, max_keys, kps, x.device)
         o = torch.empty((L, H * D), dtype=torch.bfloat16, device=x.device)
         _C.call("qvex_attention", _ptr(q), _ptr(cache.k), _ptr(cache.v), pos, L, H, Hkv, D, cache.capacity,

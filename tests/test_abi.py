@@ -59,3 +59,13 @@ def test_qmv_rejects_unknown_tile():
     p16 = (ctypes.addressof(buf) + 15) // 16 * 16
     with pytest.raises(_C.QvexError, match="tile"):
         _C.call("qvex_qmv_w4g64_tiled", p16, p16, p16, p16, p16, 1, 16, 64, 3, 1, None)
+
+
+@pytest.mark.parametrize("kps,D,err", [(64, 256, "multiple of 128"), (192, 256, "multiple of 128"),
+                                       (128, 64, "128 or 256")])
+def test_attention_rejects_bad_split_or_dim(kps, D, err):
+    buf = ctypes.create_string_buffer(1 << 12)
+    p16 = (ctypes.addressof(buf) + 15) // 16 * 16
+    with pytest.raises(_C.QvexError, match=err):
+        _C.call("qvex_attention", p16, p16, p16, p16, 4, 16, 4, D, 4096, 4096, kps, p16, 2 * D * 16, p16, p16,
+                1 << 40, None)

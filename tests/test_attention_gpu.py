@@ -21,12 +21,15 @@ def tof(t):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("L,Hq,Hkv,D,pos0,kps", [(4, 16, 4, 256, 4348, 64), (1, 16, 4, 256, 700, 64),
-                                                 (4, 16, 4, 256, 0, 64), (64, 16, 4, 256, 300, 512),
-                                                 (8, 4, 2, 128, 77, 32), (3, 4, 2, 128, 31, 64)])
-def test_attention_matches_reference(L, Hq, Hkv, D, pos0, kps):
+@pytest.mark.parametrize("L,Hq,Hkv,D,pos0,kps,spare", [
+    (4, 16, 4, 256, 4348, 128, 0), (1, 16, 4, 256, 700, 128, 0), (4, 16, 4, 256, 0, 128, 0),
+    (64, 16, 4, 256, 300, 512, 0), (4, 16, 4, 256, 4348, 512, 0), (8, 4, 2, 128, 77, 128, 0),
+    (3, 4, 2, 128, 31, 256, 0),
+    # graph-mode sizing: max_keys = capacity, far past the visible keys
+    (4, 16, 4, 256, 1000, 128, 2048), (2, 4, 2, 128, 129, 128, 1024)])
+def test_attention_matches_reference(L, Hq, Hkv, D, pos0, kps, spare):
     g = np.random.default_rng(L * 1000 + pos0)
-    cap = ((pos0 + L + 255) // 256) * 256
+    cap = ((pos0 + L + spare + 255) // 256) * 256
     q = g.standard_normal((L, Hq, D)).astype(np.float32)
     kc = g.standard_normal((Hkv, cap, D)).astype(np.float32)
     vc = g.standard_normal((Hkv, cap, D)).astype(np.float32)
@@ -36,7 +39,7 @@ def test_attention_matches_reference(L, Hq, Hkv, D, pos0, kps):
     gt = bf(gate_rows.reshape(L, -1))
     pos = torch.tensor([pos0], dtype=torch.int32, device=DEV)
     out = torch.empty((L, Hq * D), dtype=torch.bfloat16, device=DEV)
-    max_keys = pos0 + L
+    max_keys = cap if spare else pos0 + L
     need = int(_C.lib().qvex_attn_workspace_bytes(L, Hq, Hkv, D, max_keys, kps))
     ws = torch.empty((need + 3) // 4, dtype=torch.float32, device=DEV)
     _C.call("qvex_attention", _ptr(qt), _ptr(kt), _ptr(vt), _ptr(pos), L, Hq, Hkv, D, cap, max_keys, kps,
