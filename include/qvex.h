@@ -65,11 +65,35 @@ int qvex_qmv_w4g64_tiled(const uint16_t* x, const uint32_t* w, const uint16_t* s
 
 /* Same product through the MFMA form of the kernel (16-row tiles, block-
  * diagonal activation operand): tiles_per_wave in {1,2,4} 16-row tiles per
- * wave, wave_ksplit in {1,2,4} waves of a block splitting K. Requires
+ * wave, wave_ksplit in {1,2,4,8} waves of a block splitting K. Requires
  * K % 256 == 0 for M <= 4 and K % 128 == 0 for M <= 8. */
 int qvex_qmv_w4g64_mfma(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
                         const uint16_t* biases, uint16_t* y, int M, int N, int K,
                         int tiles_per_wave, int wave_ksplit, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Tile-packed weights: the QLinear triplet (engine/model.py:83-85) re-laid
+ * once, at layer construction, as records of (16 rows x 256 k): 2048 bytes of
+ * 4-bit words in the order the MFMA lanes consume them (nibbles reordered so
+ * even k sit in the low half-word) followed by 256 bytes of (scale, bias)
+ * bf16 pairs. Rows past N are zero. K must be a multiple of 256.
+ * qvex_w4g64_packed_bytes() = ceil(N/16) * (K/256) * 2304 (0 if unsupported). */
+uint64_t qvex_w4g64_packed_bytes(int N, int K);
+int qvex_w4g64_pack(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                    int N, int K, void* packed, uint64_t packed_bytes, void* stream);
+
+/* y[M, N] = x[M, K] @ dequant(W)^T from the packed copy, M = 1..4: the product
+ * of mx.quantized_matmul(x, w, scales, biases, transpose=True, group_size=64,
+ * bits=4) in QLinear.__call__ (engine/model.py:87-91), on MFMA with fully
+ * coalesced record loads. The tile depends on (N, K) only, so each output row
+ * is bitwise the same for every M. x, packed 16-byte aligned. */
+int qvex_qmv_w4g64_packed(const uint16_t* x, const void* packed, uint16_t* y, int M, int N,
+                          int K, void* stream);
+/* The same with an explicit tile: tiles_per_wave in {1,2,4} 16-row tiles,
+ * wave_ksplit in {1,2,4,8} waves splitting the 256-k sets. For tile sweeps. */
+int qvex_qmv_w4g64_packed_tiled(const uint16_t* x, const void* packed, uint16_t* y, int M,
+                                int N, int K, int tiles_per_wave, int wave_ksplit,
+                                void* stream);
 
 /* ------------------------------------------------------------------------
  * Gated DeltaNet recurrence (verify form), one state snapshot per token.

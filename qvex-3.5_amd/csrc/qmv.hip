@@ -17,36 +17,9 @@
 //   * cross-lane sums use DPP row_shr / row_bcast (no LDS round trip), and
 //     KS waves can split K for short-N shapes, combining through LDS.
 #include "qvex_common.h"
+#include "w4_dequant.h"
 
 namespace {
-
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
-
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                         __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-
-constexpr uint32_t kMagic = 0x43004300u;   // bf16 pair (128.0, 128.0)
-constexpr uint32_t kNib = 0x000F000Fu;
-constexpr uint32_t kOnes = 0x3f803f80u;    // bf16 pair (1.0, 1.0)
-
-// (a & mask) | magic. gfx9 VOP3 takes no literal operand, so with both constants
-// as literals the compiler splits this into two VOP2 ops; callers make the mask
-// an opaque SGPR value and the magic an opaque VGPR value (see opaque_sgpr /
-// opaque_vgpr), which lets it select one v_and_or_b32 (one constant-bus read)
-// while the hazard recognizer still sees every instruction.
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t magic) {
-  return (a & mask) | magic;
-}
-__device__ __forceinline__ uint32_t opaque_sgpr(uint32_t v) {
-  asm volatile("" : "+s"(v));
-  return v;
-}
-__device__ __forceinline__ uint32_t opaque_vgpr(uint32_t v) {
-  asm volatile("" : "+v"(v));
-  return v;
-}
 
 // Chunk = 32 consecutive k of one row = 4 uint32 words = 16 bytes.
 // Block = 256 threads = 4 waves; KS waves share one row group of R rows and
@@ -195,40 +168,45 @@ __global__ __launch_bounds__(256) void qmv_w4g64_kernel(
 // v_mfma_f32_16x16x32_bf16, so the VALU work per weight word is fixed (dequant +
 // a group fold) whatever M is.
 //
-// Layout trick: one MFMA covers 16 weight rows (the 16 output columns j) and 4
-// k-chunks of 8 (the lane groups c = lane/16). Chunk c carries the words of
-// group g0 + c/CPG of each row, and the activation operand is block-diagonal:
-// A row i = (group i/MP, activation row i%MP) is non-zero only in the chunks of
-// its own group. The 16x16 accumulator then holds one group's partial dot
-// product per (row, activation row) - exactly what the per-group scale/bias
-// fold needs - and lane l's four accumulators belong to the weight row and
-// group this lane itself loaded, so the fold reads one scale and one bias.
-//   MP = 4 (M <= 4): 4 groups per set, 8 MFMA steps, 32 B of weights per lane;
-//   MP = 8 (M <= 8): 2 groups per set, 4 MFMA steps, 16 B of weights per lane.
-// Group sums of x (for the bias term) are computed once per block into LDS.
-// TN 16-row tiles per wave; WS waves of a block split the group sets of the
-// same tiles and combine through LDS. Weight loads of the next group set are
-// issued before the current one is computed (two register buffers).
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ bf16x8_t as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-  u32x4 v = {a, b, c, d};
-  return __builtin_bit_cast(bf16x8_t, v);
+// Layout: one MFMA covers 16 weight rows (the 16 output columns n = lane%16)
+// and 4 k-chunks of 8 (lane groups c = lane/16). A "set" is the span of K that
+// the 4 lane groups cover together: MP = 4 (M <= 4) gives 4 groups per set, one
+// per lane group (8 words = 32 B per lane, 8 MFMA steps); MP = 8 (M <= 8) gives
+// 2 groups per set, each split over two lane groups (4 words, 4 steps). The
+// activation operand is block-diagonal: A row i = (group slot i/MP, activation
+// row i%MP) is non-zero only in the k-chunks of its own group, so the 16x16
+// accumulator holds one group's partial dot product per (slot, activation row)
+// - what the per-group scale/bias fold needs - and lane l's four accumulators
+// belong to weight row l%16 and a single group slot, so the fold reads one
+// scale and one bias. The bias term needs X = sum(x) per (group, activation
+// row): the same A operand times an all-ones B gives it in exactly the fold's
+// lane layout, one extra MFMA per step and no VALU work.
+//
+// Pipelining: a wave walks its group sets (stride WS) with two register
+// buffers; the weights, scales, biases and the activation chunks of set i+1
+// are in flight while set i is computed. TN 16-row tiles share each activation
+// operand; WS waves of a block split the sets of the same tiles and combine
+// through LDS in a fixed order, so results depend on (N, K, TN, WS) only.
+// (x_0..x_7) as bf16 -> A operand pairs (x_0,x_4) (x_1,x_5) (x_2,x_6) (x_3,x_7),
+// matching the order in which and_or() unpacks the nibbles of a word.
+__device__ __forceinline__ bf16x8_t perm_x(const u32x4 v) {
+  return as_bf16x8((v.x & 0xffffu) | (v.z << 16), (v.x >> 16) | (v.z & 0xffff0000u),
+                   (v.y & 0xffffu) | (v.w << 16), (v.y >> 16) | (v.w & 0xffff0000u));
 }
 
+constexpr int mfma_block(int WS) { return WS >= 4 ? 64 * WS : 256; }
+
 template <int MP, int TN, int WS>
-__global__ __launch_bounds__(256) void qmv_mfma_kernel(
+__global__ __launch_bounds__(mfma_block(WS)) void qmv_mfma_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ w,
     const uint16_t* __restrict__ scales, const uint16_t* __restrict__ biases,
     uint16_t* __restrict__ y, int M, int N, int K) {
   constexpr int GPM = 16 / MP;     // groups per set
-  constexpr int CPG = 4 / GPM;     // k-chunks (lane groups) per group
+  constexpr int CPG = 4 / GPM;     // lane groups per group
   constexpr int NS = 8 / CPG;      // MFMA steps per set = words per lane per set
   constexpr int NL = NS / 4;       // 16-byte weight loads per lane per set
-  constexpr int RG = 4 / WS;       // row groups per block
-  extern __shared__ float smem[];
-  float* Xs = smem;                // [G][MP] group sums of x
+  constexpr int RG = mfma_block(WS) / 64 / WS;   // tile groups per block
+  constexpr int LIVE = 16 * (MP / 4);            // lanes holding distinct (row, m) sums
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rg = wave / WS, ws = wave % WS;
@@ -236,33 +214,15 @@ __global__ __launch_bounds__(256) void qmv_mfma_kernel(
   const int KW = K >> 3;
   const int GS = G / GPM;
 
-  for (int idx = threadIdx.x; idx < G * MP; idx += 256) {
-    const int g = idx / MP, m = idx % MP;
-    float sum = 0.0f;
-    if (m < M) {
-      const uint16_t* xp = x + (size_t)m * K + g * 64;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const u32x4 v = load16(xp + 8 * i);
-        sum = dot2(v.x, kOnes, sum);
-        sum = dot2(v.y, kOnes, sum);
-        sum = dot2(v.z, kOnes, sum);
-        sum = dot2(v.w, kOnes, sum);
-      }
-    }
-    Xs[idx] = sum;
-  }
-  __syncthreads();
-
   const uint32_t magic = opaque_vgpr(kMagic);
   const uint32_t nib = opaque_sgpr(kNib);
+  const bf16x8_t ones = as_bf16x8(kOnes, kOnes, kOnes, kOnes);
 
   const int c = lane >> 4, i16 = lane & 15;
-  const int cg = c / CPG;                 // group (within the set) of chunk c
-  const int cw = (c % CPG) * NS;          // first word (within the group) of chunk c
-  const bool part = (i16 / MP) == cg && (i16 % MP) < M;
+  const int cg = c / CPG;                 // group slot of lane group c
+  const int cw = (c % CPG) * NS;          // first word (within the group) of lane group c
+  const bool part = (i16 / MP) == cg && (i16 % MP) < M;   // A row i16 is live in chunk c
   const int am = i16 % MP;                // activation row fed by this lane
-  const int fm0 = (4 * c) % MP;           // activation row of accumulator 0
   const int tile0 = (blockIdx.x * RG + rg) * TN;
 
   float acc[TN][4];
@@ -271,14 +231,11 @@ __global__ __launch_bounds__(256) void qmv_mfma_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
 
-  uint32_t A[NS][4];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) A[s][0] = A[s][1] = A[s][2] = A[s][3] = 0u;
-
   u32x4 wb[2][TN][NL];
   uint32_t sbuf[2][TN][2];
+  u32x4 xb[2][NS];
 
-  auto load_set = [&](int buf, int gs) {
+  auto issue = [&](int buf, int gs) {
     const int g = gs * GPM + cg;
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
@@ -290,35 +247,19 @@ __global__ __launch_bounds__(256) void qmv_mfma_kernel(
       sbuf[buf][t][0] = scales[(size_t)n * G + g];
       sbuf[buf][t][1] = biases[(size_t)n * G + g];
     }
+    const uint16_t* xp = x + (size_t)(part ? am : 0) * K + g * 64 + cw * 8;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) xb[buf][s] = part ? load16(xp + 8 * s) : u32x4{0u, 0u, 0u, 0u};
   };
 
-  auto build_a = [&](int gs) {
-    const int g = gs * GPM + cg;
-    if (part) {
-      const uint16_t* xp = x + (size_t)am * K + g * 64 + cw * 8;
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const u32x4 v = load16(xp + 8 * s);
-        A[s][0] = (v.x & 0xffffu) | (v.z << 16);
-        A[s][1] = (v.x >> 16) | (v.z & 0xffff0000u);
-        A[s][2] = (v.y & 0xffffu) | (v.w << 16);
-        A[s][3] = (v.y >> 16) | (v.w & 0xffff0000u);
-      }
-    }
-  };
-
-  auto compute_set = [&](int buf, int gs) {
-    const int g = gs * GPM + cg;
-    float Xf[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) Xf[r] = Xs[g * MP + fm0 + r];
-    // tiles interleaved inside each step: TN independent accumulation chains
-    f32x4_t C[TN];
+  auto compute = [&](int buf) {
+    f32x4_t C[TN], CX = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int t = 0; t < TN; ++t) C[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      const bf16x8_t a = as_bf16x8(A[s][0], A[s][1], A[s][2], A[s][3]);
+      const bf16x8_t a = perm_x(xb[buf][s]);
+      CX = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, CX, 0, 0, 0);
 #pragma unroll
       for (int t = 0; t < TN; ++t) {
         const u32x4 wv = wb[buf][t][s / 4];
@@ -334,25 +275,20 @@ __global__ __launch_bounds__(256) void qmv_mfma_kernel(
       const float bi = bf16_to_f32((uint16_t)sbuf[buf][t][1]);
       const float bo = fmaf(-128.0f, sc, bi);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(sc, C[t][r], fmaf(bo, Xf[r], acc[t][r]));
+      for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(sc, C[t][r], fmaf(bo, CX[r], acc[t][r]));
     }
   };
 
-  // Memory order per step: activation loads of this set, then the weight
-  // prefetch of the next set, then compute; the in-order vmcnt wait for the
-  // activations then leaves the prefetch in flight.
   int gs = ws;
-  if (gs < GS) load_set(0, gs);
+  if (gs < GS) issue(0, gs);
   while (gs < GS) {
     const int g1 = gs + WS;
-    build_a(gs);
-    if (g1 < GS) load_set(1, g1);
-    compute_set(0, gs);
+    if (g1 < GS) issue(1, g1);
+    compute(0);
     if (g1 >= GS) break;
     const int g2 = g1 + WS;
-    build_a(g1);
-    if (g2 < GS) load_set(0, g2);
-    compute_set(1, g1);
+    if (g2 < GS) issue(0, g2);
+    compute(1);
     gs = g2;
   }
 
@@ -366,14 +302,13 @@ __global__ __launch_bounds__(256) void qmv_mfma_kernel(
       v += __shfl_xor(v, 32, 64);
       acc[t][r] = v;
     }
-  constexpr int LIVE = 16 * (MP / 4);     // lanes holding distinct (row, m) sums
   if constexpr (WS > 1) {
-    float* red = smem + G * MP;           // [4 waves][TN][4][LIVE]
+    __shared__ float red[RG * WS][TN][4][LIVE];
     if (lane < LIVE) {
 #pragma unroll
       for (int t = 0; t < TN; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[((wave * TN + t) * 4 + r) * LIVE + lane] = acc[t][r];
+        for (int r = 0; r < 4; ++r) red[wave][t][r][lane] = acc[t][r];
     }
     __syncthreads();
     if (ws != 0) return;
@@ -384,12 +319,13 @@ __global__ __launch_bounds__(256) void qmv_mfma_kernel(
         for (int r = 0; r < 4; ++r) {
           float v = 0.0f;
 #pragma unroll
-          for (int j = 0; j < WS; ++j) v += red[(((rg * WS + j) * TN + t) * 4 + r) * LIVE + lane];
+          for (int j = 0; j < WS; ++j) v += red[rg * WS + j][t][r][lane];
           acc[t][r] = v;
         }
     }
   }
   if (lane < LIVE) {
+    const int fm0 = (4 * c) % MP;         // activation row of accumulator 0
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
       const int n = (tile0 + t) * 16 + i16;
@@ -463,6 +399,7 @@ qmv_mfma_fn pick_mfma_ws(int ws) {
     case 1: return qmv_mfma_kernel<MP, TN, 1>;
     case 2: return qmv_mfma_kernel<MP, TN, 2>;
     case 4: return qmv_mfma_kernel<MP, TN, 4>;
+    case 8: return qmv_mfma_kernel<MP, TN, 8>;
   }
   return nullptr;
 }
@@ -490,12 +427,10 @@ int launch_mfma(const uint16_t* x, const uint32_t* w, const uint16_t* scales, co
                  "qvex_qmv_w4g64: scales/biases/y must be 2-byte aligned");
   qmv_mfma_fn fn = MP == 4 ? pick_mfma_tn<4>(TN, WS) : pick_mfma_tn<8>(TN, WS);
   QVEX_CHECK_ARG(fn != nullptr, "qvex_qmv_w4g64 (mfma): unsupported tile TN=%d WS=%d", TN, WS);
-  const int G = K / 64;
-  const size_t lds = (size_t)G * MP * sizeof(float) + (WS > 1 ? (size_t)4 * TN * 4 * 16 * (MP / 4) * sizeof(float) : 0);
-  QVEX_CHECK_ARG(lds <= 64 * 1024, "qvex_qmv_w4g64 (mfma): K=%d needs %zu bytes of LDS", K, lds);
-  const int rows_per_block = 16 * TN * (4 / WS);
+  const int threads = WS >= 4 ? 64 * WS : 256;
+  const int rows_per_block = 16 * TN * (threads / 64 / WS);
   const int blocks = (N + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), lds, stream, x, w, scales, biases, y, M, N, K);
+  hipLaunchKernelGGL(fn, dim3(blocks), dim3(threads), 0, stream, x, w, scales, biases, y, M, N, K);
   QVEX_CHECK_LAUNCH("qvex_qmv_w4g64 (mfma)");
   return QVEX_OK;
 }

@@ -1,0 +1,312 @@
+// 4-bit group-64 skinny GEMM (M = 1..4 activation rows) on a tile-packed copy of
+// the MLX weights, for the verify / draft matmuls of the decode cycle.
+//
+// Reference semantics: mx.quantized_matmul(transpose=True, group_size=64, bits=4)
+// in QLinear.__call__ (engine/model.py:87-91); the weights are the QLinear
+// triplet (engine/model.py:83-85), re-laid once when the layer is built.
+//
+// Why a second layout. The MFMA form of the product (block-diagonal activation
+// operand, see the MFMA variant in qmv.hip) needs every lane of a wave to hold a
+// different weight row; in the MLX row-major layout that makes each 16-byte load
+// instruction touch 16 rows (16 cache lines per KiB), and the load path, not HBM,
+// sets the speed. The packed layout stores each (16-row tile, 256-k set) as one
+// record in exactly the order the lanes consume it:
+//
+//   record (tile t, set s), 2304 bytes, records ordered [t][s]:
+//     bytes [0, 2048):    [q = 0..1][lane L = 0..63][4 words]; lane L = 16c + i
+//                         holds words 4q .. 4q+3 of group 4s + c of row 16t + i
+//     bytes [2048, 2304): [lane L] (scale, bias) bf16 pair of that row and group
+//
+//   Each word's nibbles are reordered so that (w >> 4j) & 0x000F000F yields the
+//   codes of k = 2j and 2j + 1 (even k in the low half-word, odd k in the high
+//   half-word); the activations then enter the MFMA in their natural order.
+//   Rows past N are zero (weights, scale and bias) and never stored.
+//
+// A wave reads one record per (tile, set) with two fully coalesced 1 KiB loads
+// plus one 256-byte load; the activation slice of the set (M x 256 bf16) comes in
+// with two more coalesced loads, goes through a wave-private LDS slot and is read
+// back per MFMA step by the 16 lanes whose A rows are live in that k-chunk.
+#include "qvex_common.h"
+#include "w4_dequant.h"
+
+namespace {
+
+constexpr int PK_TILE = 16;
+constexpr int PK_SET = 256;               // k per record = 4 groups
+constexpr int PK_WBYTES = 2048;
+constexpr int PK_RECORD = 2304;
+
+// nibbles q0..q7 at bits 4k  ->  q_{2j} at bits 4j, q_{2j+1} at bits 16 + 4j
+__device__ __forceinline__ uint32_t reorder_nibbles(uint32_t w) {
+  uint32_t r = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    r |= ((w >> (8 * j)) & 0xFu) << (4 * j);
+    r |= ((w >> (8 * j + 4)) & 0xFu) << (16 + 4 * j);
+  }
+  return r;
+}
+
+// one 64-thread block per record
+__global__ __launch_bounds__(64) void pack_kernel(const uint32_t* __restrict__ w,
+                                                  const uint16_t* __restrict__ scales,
+                                                  const uint16_t* __restrict__ biases, int N, int K,
+                                                  uint8_t* __restrict__ packed) {
+  const int GS = K / PK_SET;
+  const int t = blockIdx.x / GS, s = blockIdx.x % GS;
+  const int L = threadIdx.x, c = L >> 4, i = L & 15;
+  const int row = t * PK_TILE + i, g = s * 4 + c;
+  const int KW = K / 8, G = K / 64;
+  uint8_t* rec = packed + (size_t)blockIdx.x * PK_RECORD;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (row < N) {
+      const uint32_t* src = w + (size_t)row * KW + g * 8 + 4 * q;
+      v = u32x4{reorder_nibbles(src[0]), reorder_nibbles(src[1]), reorder_nibbles(src[2]), reorder_nibbles(src[3])};
+    }
+    *reinterpret_cast<u32x4*>(rec + q * 1024 + L * 16) = v;
+  }
+  uint32_t sb = 0;
+  if (row < N) sb = (uint32_t)scales[(size_t)row * G + g] | ((uint32_t)biases[(size_t)row * G + g] << 16);
+  *reinterpret_cast<uint32_t*>(rec + PK_WBYTES + L * 4) = sb;
+}
+
+constexpr int pk_block(int WS) { return WS >= 4 ? 64 * WS : 256; }
+
+// TN 16-row tiles per wave share each activation operand; WS waves of a block
+// split the sets of the same tiles (set ws, ws + WS, ...) and combine through
+// LDS in a fixed order; 4 / WS tile groups per block when WS < 4. Two register
+// buffers: the records and activation slice of the next set are in flight while
+// the current one is computed. Results depend on (N, K, TN, WS) only, never on M.
+template <int TN, int WS>
+__global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t* __restrict__ x,
+                                                                   const uint8_t* __restrict__ packed,
+                                                                   uint16_t* __restrict__ y, int M, int N, int K) {
+  constexpr int NWAVE = pk_block(WS) / 64;
+  constexpr int RG = NWAVE / WS;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rg = wave / WS, ws = wave % WS;
+  const int GS = K / PK_SET;
+  const int tiles = (N + PK_TILE - 1) / PK_TILE;
+  const int c = lane >> 4, i16 = lane & 15;
+  const int am = i16 & 3;
+  const bool part = (i16 >> 2) == c && am < M;   // A row i16 = (group slot i16/4, activation row i16%4)
+  const int tile0 = (blockIdx.x * RG + rg) * TN;
+
+  __shared__ u32x4 xslot[NWAVE][4 * 32];         // per wave: [activation row][32 chunks of 8 bf16]
+  u32x4* slot = xslot[wave];
+
+  const uint32_t magic = opaque_vgpr(kMagic);
+  const uint32_t nib = opaque_sgpr(kNib);
+  const bf16x8_t ones = as_bf16x8(kOnes, kOnes, kOnes, kOnes);
+
+  float acc[TN][4];
+#pragma unroll
+  for (int t = 0; t < TN; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
+
+  u32x4 wb[2][TN][2];
+  uint32_t sb[2][TN];
+  u32x4 xr[2][2];
+
+  // activation slice loader: lane L of load q covers row 2q + L/32, chunk L%32
+  const int xm0 = lane >> 5, xch = lane & 31;
+
+  auto issue = [&](int buf, int gs) {
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      const int tile = min(tile0 + t, tiles - 1);   // tiles past the end re-read the last one, never stored
+      const uint8_t* rec = packed + ((size_t)tile * GS + gs) * PK_RECORD;
+      wb[buf][t][0] = load_nt16(rec + lane * 16);
+      wb[buf][t][1] = load_nt16(rec + 1024 + lane * 16);
+      sb[buf][t] = *reinterpret_cast<const uint32_t*>(rec + PK_WBYTES + lane * 4);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int m = 2 * q + xm0;
+      xr[buf][q] = m < M ? load16(x + (size_t)m * K + (size_t)gs * PK_SET + 8 * xch) : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+
+  auto compute = [&](int buf) {
+    slot[xm0 * 32 + xch] = xr[buf][0];
+    slot[(2 + xm0) * 32 + xch] = xr[buf][1];
+    f32x4_t C[TN], CX = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int t = 0; t < TN; ++t) C[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const u32x4 xa = part ? slot[am * 32 + c * 8 + s] : u32x4{0u, 0u, 0u, 0u};
+      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, xa);
+      CX = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, CX, 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        const u32x4 wv = wb[buf][t][s / 4];
+        const uint32_t wd = (s % 4 == 0) ? wv.x : (s % 4 == 1) ? wv.y : (s % 4 == 2) ? wv.z : wv.w;
+        const bf16x8_t b = as_bf16x8(and_or(wd, nib, magic), and_or(wd >> 4, nib, magic),
+                                     and_or(wd >> 8, nib, magic), and_or(wd >> 12, nib, magic));
+        C[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, C[t], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      const float sc = bf16_to_f32((uint16_t)(sb[buf][t] & 0xffffu));
+      const float bi = bf16_to_f32((uint16_t)(sb[buf][t] >> 16));
+      const float bo = fmaf(-128.0f, sc, bi);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(sc, C[t][r], fmaf(bo, CX[r], acc[t][r]));
+    }
+  };
+
+  int gs = ws;
+  if (gs < GS) issue(0, gs);
+  while (gs < GS) {
+    const int g1 = gs + WS;
+    if (g1 < GS) issue(1, g1);
+    compute(0);
+    if (g1 >= GS) break;
+    const int g2 = g1 + WS;
+    if (g2 < GS) issue(0, g2);
+    compute(1);
+    gs = g2;
+  }
+
+  // lane (c, i16) holds group slot c of row i16: sum the 4 slots
+#pragma unroll
+  for (int t = 0; t < TN; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = acc[t][r];
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      acc[t][r] = v;
+    }
+  if constexpr (WS > 1) {
+    __shared__ float red[NWAVE][TN][4][16];
+    if (lane < 16) {
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][t][r][lane] = acc[t][r];
+    }
+    __syncthreads();
+    if (ws != 0) return;
+    if (lane < 16) {
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = 0.0f;
+#pragma unroll
+          for (int j = 0; j < WS; ++j) v += red[rg * WS + j][t][r][lane];
+          acc[t][r] = v;
+        }
+    }
+  }
+  if (lane < 16) {
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      const int n = (tile0 + t) * PK_TILE + i16;
+      if (n < N) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (r < M) y[(size_t)r * N + n] = f32_to_bf16(acc[t][r]);
+      }
+    }
+  }
+}
+
+typedef void (*qmv_packed_fn)(const uint16_t*, const uint8_t*, uint16_t*, int, int, int);
+
+template <int TN>
+qmv_packed_fn pick_ws(int ws) {
+  switch (ws) {
+    case 1: return qmv_packed_kernel<TN, 1>;
+    case 2: return qmv_packed_kernel<TN, 2>;
+    case 4: return qmv_packed_kernel<TN, 4>;
+    case 8: return qmv_packed_kernel<TN, 8>;
+  }
+  return nullptr;
+}
+
+qmv_packed_fn pick_packed(int tn, int ws) {
+  switch (tn) {
+    case 1: return pick_ws<1>(ws);
+    case 2: return pick_ws<2>(ws);
+    case 4: return pick_ws<4>(ws);
+  }
+  return nullptr;
+}
+
+// Tile choice from (N, K) only, so a row's bits never depend on M. Two tiles per
+// wave once there are enough rows to keep every CU busy; waves split K until the
+// launch holds ~2048 waves (8 per CU), keeping at least 2 sets per wave and at
+// least two waves per tile when K has 8 sets or more (measured on the 9B shapes:
+// gate_up (2,4), down (1,8), in_proj (1,4), o_proj (1,8), lm_head (2,2)).
+void packed_default_tile(int N, int K, int* TN, int* WS) {
+  const long tiles = (N + PK_TILE - 1) / PK_TILE;
+  const int GS = K / PK_SET;
+  const int tn = tiles >= 1024 ? 2 : 1;
+  int ws = GS >= 8 ? 2 : 1;
+  while (ws < 8 && (tiles / tn) * ws < 2048 && GS >= 2 * (ws * 2)) ws *= 2;
+  *TN = tn;
+  *WS = ws;
+}
+
+int launch_packed(const uint16_t* x, const uint8_t* packed, uint16_t* y, int M, int N, int K, int TN, int WS,
+                  hipStream_t stream) {
+  QVEX_CHECK_ARG(x && packed && y, "qvex_qmv_w4g64_packed: null pointer");
+  QVEX_CHECK_ARG(M >= 1 && M <= 4, "qvex_qmv_w4g64_packed: M=%d outside 1..4", M);
+  QVEX_CHECK_ARG(N >= 1 && K >= PK_SET && K % PK_SET == 0,
+                 "qvex_qmv_w4g64_packed: N=%d K=%d (K must be a positive multiple of 256)", N, K);
+  QVEX_CHECK_ARG(qvex_aligned(x, 16) && qvex_aligned(packed, 16) && qvex_aligned(y, 2),
+                 "qvex_qmv_w4g64_packed: x and packed must be 16-byte aligned");
+  qmv_packed_fn fn = pick_packed(TN, WS);
+  QVEX_CHECK_ARG(fn != nullptr, "qvex_qmv_w4g64_packed: unsupported tile TN=%d WS=%d", TN, WS);
+  const int threads = pk_block(WS);
+  const int tiles = (N + PK_TILE - 1) / PK_TILE;
+  const int tiles_per_block = TN * (threads / 64 / WS);
+  const int blocks = (tiles + tiles_per_block - 1) / tiles_per_block;
+  hipLaunchKernelGGL(fn, dim3(blocks), dim3(threads), 0, stream, x, packed, y, M, N, K);
+  QVEX_CHECK_LAUNCH("qvex_qmv_w4g64_packed");
+  return QVEX_OK;
+}
+
+}  // namespace
+
+extern "C" uint64_t qvex_w4g64_packed_bytes(int N, int K) {
+  if (N < 1 || K < PK_SET || K % PK_SET) return 0;
+  return (uint64_t)((N + PK_TILE - 1) / PK_TILE) * (uint64_t)(K / PK_SET) * PK_RECORD;
+}
+
+extern "C" int qvex_w4g64_pack(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int N, int K,
+                               void* packed, uint64_t packed_bytes, void* stream) {
+  QVEX_CHECK_ARG(w && scales && biases && packed, "qvex_w4g64_pack: null pointer");
+  QVEX_CHECK_ARG(N >= 1 && K >= PK_SET && K % PK_SET == 0,
+                 "qvex_w4g64_pack: N=%d K=%d (K must be a positive multiple of 256)", N, K);
+  const uint64_t need = qvex_w4g64_packed_bytes(N, K);
+  QVEX_CHECK_ARG(packed_bytes >= need, "qvex_w4g64_pack: packed buffer %llu < %llu bytes",
+                 (unsigned long long)packed_bytes, (unsigned long long)need);
+  QVEX_CHECK_ARG(qvex_aligned(packed, 16) && qvex_aligned(w, 4) && qvex_aligned(scales, 2) && qvex_aligned(biases, 2),
+                 "qvex_w4g64_pack: packed must be 16-byte aligned");
+  const long records = (long)((N + PK_TILE - 1) / PK_TILE) * (K / PK_SET);
+  QVEX_CHECK_ARG(records <= 0x7fffffffL, "qvex_w4g64_pack: too many records");
+  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)records), dim3(64), 0, (hipStream_t)stream, w, scales, biases, N, K,
+                     (uint8_t*)packed);
+  QVEX_CHECK_LAUNCH("qvex_w4g64_pack");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_qmv_w4g64_packed(const uint16_t* x, const void* packed, uint16_t* y, int M, int N, int K,
+                                     void* stream) {
+  int TN = 1, WS = 1;
+  if (N >= 1 && K >= PK_SET) packed_default_tile(N, K, &TN, &WS);
+  return launch_packed(x, (const uint8_t*)packed, y, M, N, K, TN, WS, (hipStream_t)stream);
+}
+
+extern "C" int qvex_qmv_w4g64_packed_tiled(const uint16_t* x, const void* packed, uint16_t* y, int M, int N, int K,
+                                           int tiles_per_wave, int wave_ksplit, void* stream) {
+  return launch_packed(x, (const uint8_t*)packed, y, M, N, K, tiles_per_wave, wave_ksplit, (hipStream_t)stream);
+}

@@ -23,6 +23,9 @@ SIGNATURES: dict[str, list] = {
     "qvex_qmv_w4g64_tiled": [P, P, P, P, P, I, I, I, I, I, P],
     "qvex_read_roof": [P, U64, P, I, P],
     "qvex_qmv_w4g64_mfma": [P, P, P, P, P, I, I, I, I, I, P],
+    "qvex_w4g64_pack": [P, P, P, I, I, P, U64, P],
+    "qvex_qmv_w4g64_packed": [P, P, P, I, I, I, P],
+    "qvex_qmv_w4g64_packed_tiled": [P, P, P, I, I, I, I, I, P],
     "qvex_gdn_recurrent": [P, P, P, P, P, P, P, P, P, I, P, I, I, I, I, I, I, P],
     "qvex_gdn_recurrent_ring": [P, P, P, P, P, P, P, P, I, P, I, P, I, I, I, I, I, I, P],
     "qvex_spec_accept": [P, P, P, P, P, F, P, P, I, I, I, P, U64, P],
@@ -64,6 +67,8 @@ def lib() -> ctypes.CDLL:
         L.qvex_spec_accept_workspace_bytes.argtypes = [I, I, I, I]
         L.qvex_attn_workspace_bytes.restype = U64
         L.qvex_attn_workspace_bytes.argtypes = [I, I, I, I, I, I]
+        L.qvex_w4g64_packed_bytes.restype = U64
+        L.qvex_w4g64_packed_bytes.argtypes = [I, I]
         for name, args in SIGNATURES.items():
             fn = getattr(L, name)
             fn.argtypes = args
@@ -82,4 +87,4 @@ def call(name: str, *args) -> None:
 
 def exported_symbols() -> list[str]:
     return ["qvex_last_error", "qvex_abi_version", "qvex_spec_accept_workspace_bytes",
-            "qvex_attn_workspace_bytes", *SIGNATURES]
+            "qvex_attn_workspace_bytes", "qvex_w4g64_packed_bytes", *SIGNATURES]

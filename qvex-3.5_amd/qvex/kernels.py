@@ -81,6 +81,48 @@ def qmv_multi(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: to
     return quantized_matmul(x, w, scales, biases)
 
 
+def pack_w4(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) -> torch.Tensor:
+    """Tile-packed copy of a QLinear triplet (engine/model.py:83-85) for
+    quantized_matmul_packed: uint8 [ceil(N/16) * K/256 * 2304]. K % 256 == 0."""
+    _check(w, "w", torch.int32, 2)
+    _check(scales, "scales", torch.bfloat16, 2)
+    _check(biases, "biases", torch.bfloat16, 2)
+    N, K = w.shape[0], w.shape[1] * 8
+    if scales.shape != (N, K // GROUP) or biases.shape != (N, K // GROUP):
+        raise _C.QvexError("pack_w4: scales/biases shape mismatch")
+    nbytes = int(_C.lib().qvex_w4g64_packed_bytes(N, K))
+    if nbytes == 0:
+        raise _C.QvexError(f"pack_w4: K={K} is not a positive multiple of 256")
+    packed = torch.empty(nbytes, dtype=torch.uint8, device=w.device)
+    _C.call("qvex_w4g64_pack", _ptr(w), _ptr(scales), _ptr(biases), N, K, _ptr(packed), nbytes, _stream())
+    return packed
+
+
+def quantized_matmul_packed(x: torch.Tensor, packed: torch.Tensor, N: int, out: torch.Tensor | None = None,
+                            tile: tuple[int, int] | None = None) -> torch.Tensor:
+    """y = x @ dequant(W)^T from pack_w4's copy, x bf16 [..., K] with 1..4 rows
+    (the product of mx.quantized_matmul in QLinear.__call__, engine/model.py:87-91)."""
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    M = x2.shape[0]
+    _check(x2, "x", torch.bfloat16, 2)
+    if packed.dtype != torch.uint8 or not packed.is_contiguous() or packed.device != x.device:
+        raise _C.QvexError("packed must be a contiguous uint8 tensor on the device of x")
+    if packed.numel() != int(_C.lib().qvex_w4g64_packed_bytes(N, K)):
+        raise _C.QvexError(f"packed has {packed.numel()} bytes, not the size of an N={N} K={K} pack")
+    if out is None:
+        out = torch.empty((*x.shape[:-1], N), dtype=torch.bfloat16, device=x.device)
+    _check(out, "out", torch.bfloat16)
+    if out.numel() != M * N:
+        raise _C.QvexError("out has the wrong size")
+    if tile is None:
+        _C.call("qvex_qmv_w4g64_packed", _ptr(x2), _ptr(packed), _ptr(out), M, N, K, _stream())
+    else:
+        _C.call("qvex_qmv_w4g64_packed_tiled", _ptr(x2), _ptr(packed), _ptr(out), M, N, K,
+                int(tile[0]), int(tile[1]), _stream())
+    return out
+
+
 def read_roof(buf: torch.Tensor, sink: torch.Tensor, blocks: int = 4096) -> None:
     """Stream-read every byte of buf (HBM roof probe, experiments/native/qmv_spike.mm:21-32)."""
     nbytes = buf.numel() * buf.element_size()

@@ -118,15 +118,28 @@ class Config:
 class QLinear:
     """Affine-quantized linear layer, y = x @ dequant(W)^T (engine/model.py:80-104).
 
-    w: int32 [N, K/8] (uint32 words), scales, biases: bf16 [N, K/64]."""
+    w: int32 [N, K/8] (uint32 words), scales, biases: bf16 [N, K/64]. When K is
+    a multiple of 256 the layer also keeps the tile-packed copy (pack_w4), built
+    once here, and runs every call of 1..4 rows - decode, MTP drafts, verify of
+    up to 3 drafts - through the MFMA kernel on it; the row bits of that kernel
+    do not depend on the number of rows. Wider calls (prefill) use the
+    MLX-layout kernel in chunks of 8 rows."""
 
-    def __init__(self, w, scales, biases, group_size=64, bits=4):
+    PACKED_MAX_ROWS = 4
+
+    def __init__(self, w, scales, biases, group_size=64, bits=4, pack: bool = True):
         if group_size != 64 or bits != 4:
             raise _C.QvexError(f"QLinear: only 4-bit group-64 weights are implemented (got {bits}/{group_size})")
         self.w, self.scales, self.biases = w, scales, biases
         self.group_size, self.bits = group_size, bits
         self.N = w.shape[0]
         self.K = w.shape[1] * 8
+        self.packed = kernels.pack_w4(w, scales, biases) if pack and self.K % 256 == 0 else None
+
+    def repack(self) -> None:
+        """Rebuild the packed copy after the MLX-layout tensors were edited in place."""
+        if self.packed is not None:
+            self.packed = kernels.pack_w4(self.w, self.scales, self.biases)
 
     def __call__(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         lead = x.shape[:-1]
@@ -135,6 +148,9 @@ class QLinear:
         if out is None:
             out = torch.empty((M, self.N), dtype=torch.bfloat16, device=x.device)
         o2 = out.view(M, self.N)
+        if self.packed is not None and M <= self.PACKED_MAX_ROWS:
+            kernels.quantized_matmul_packed(x2, self.packed, self.N, out=o2)
+            return out.view(*lead, self.N)
         for m0 in range(0, M, QMV_MAX_ROWS):
             m1 = min(M, m0 + QMV_MAX_ROWS)
             kernels.quantized_matmul(x2[m0:m1], self.w, self.scales, self.biases, out=o2[m0:m1])
@@ -488,7 +504,7 @@ class Qwen35:
 
 # ---------------------------------------------------------------- random init in the MLX layout
 
-def _rand_qlinear(N, K, gen, scale, device) -> QLinear:
+def _rand_qlinear(N, K, gen, scale, device, pack: bool = True) -> QLinear:
     """Random 4-bit group-64 weights: codes uniform on 0..15, scales ~ U(0.5, 1.5) * scale,
     biases = -8 * scale (zero-mean dequantized weights)."""
     w = torch.randint(-2**31, 2**31, (N, K // 8), generator=gen, device=device, dtype=torch.int64)
@@ -496,7 +512,7 @@ def _rand_qlinear(N, K, gen, scale, device) -> QLinear:
     s = (torch.rand((N, K // 64), generator=gen, device=device) + 0.5) * scale
     s = s.to(torch.bfloat16)
     b = (-8.0 * s.float()).to(torch.bfloat16)
-    return QLinear(w, s, b)
+    return QLinear(w, s, b, pack=pack)
 
 
 def random_model(cfg: Config, seed: int = 1004, device="cuda", max_context: int = 8192,
@@ -539,7 +555,7 @@ def random_model(cfg: Config, seed: int = 1004, device="cuda", max_context: int 
                               "q_norm": ones(D), "k_norm": ones(D)}
         layers.append(Layer(cfg, i, p))
     V = cfg.vocab_size
-    e = _rand_qlinear(V, H, gen, 1.0 / math.sqrt(21.25), device)
+    e = _rand_qlinear(V, H, gen, 1.0 / math.sqrt(21.25), device, pack=False)
     embed = QEmbedding(e.w, e.scales, e.biases)
     lm_head = lin(V, H, lm_head_scale)
     return Qwen35(cfg, embed, layers, ones(H), lm_head, max_context=max_context, max_width=max_width)

@@ -69,3 +69,21 @@ def test_attention_rejects_bad_split_or_dim(kps, D, err):
     with pytest.raises(_C.QvexError, match=err):
         _C.call("qvex_attention", p16, p16, p16, p16, 4, 16, 4, D, 4096, 4096, kps, p16, 2 * D * 16, p16, p16,
                 1 << 40, None)
+
+
+def test_packed_bytes_and_rejections():
+    lib = _C.lib()
+    assert lib.qvex_w4g64_packed_bytes(16, 256) == 2304
+    assert lib.qvex_w4g64_packed_bytes(17, 512) == 2 * 2 * 2304
+    assert lib.qvex_w4g64_packed_bytes(16, 320) == 0
+    assert lib.qvex_w4g64_packed_bytes(0, 256) == 0
+    buf = ctypes.create_string_buffer(1 << 12)
+    p16 = (ctypes.addressof(buf) + 15) // 16 * 16
+    with pytest.raises(_C.QvexError, match="outside 1..4"):
+        _C.call("qvex_qmv_w4g64_packed", p16, p16, p16, 5, 16, 256, None)
+    with pytest.raises(_C.QvexError, match="multiple of 256"):
+        _C.call("qvex_qmv_w4g64_packed", p16, p16, p16, 1, 16, 320, None)
+    with pytest.raises(_C.QvexError, match="unsupported tile"):
+        _C.call("qvex_qmv_w4g64_packed_tiled", p16, p16, p16, 1, 16, 256, 3, 1, None)
+    with pytest.raises(_C.QvexError, match="packed buffer"):
+        _C.call("qvex_w4g64_pack", p16, p16, p16, 16, 256, p16, 2303, None)

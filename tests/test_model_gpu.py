@@ -124,6 +124,7 @@ def flat_head_model(seed=12):
     m = random_model(cfg, seed=seed, device=DEV, max_context=1024)
     m.lm_head.scales.zero_()
     m.lm_head.biases.zero_()
+    m.lm_head.repack()
     return m
 
 

@@ -12,7 +12,7 @@ import oracle
 from qvex import kernels, synth
 
 TILES = [(r, ks) for r in (1, 2, 4, 8) for ks in (1, 2, 4)]
-MFMA_TILES = [("mfma", tn, ws) for tn in (1, 2, 4) for ws in (1, 2, 4)]
+MFMA_TILES = [("mfma", tn, ws) for tn in (1, 2, 4) for ws in (1, 2, 4, 8)]
 
 
 def to_dev(a, dtype):

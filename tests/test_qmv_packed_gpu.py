@@ -1,0 +1,78 @@
+"""Tile-packed 4-bit qmv (qvex_w4g64_pack + qvex_qmv_w4g64_packed) vs the
+float64 oracle of mx.quantized_matmul (engine/model.py:87-91), same tolerance
+as the MLX-layout kernel: |err| <= 2^-8 |ref| + 2^-14 sum|x||w| (bf16 output
+rounding plus fp32 accumulation)."""
+
+import numpy as np
+import pytest
+import torch
+
+from qvex import kernels, synth
+from test_qmv_gpu import check, to_dev
+
+PACKED_TILES = [(tn, ws) for tn in (1, 2, 4) for ws in (1, 2, 4, 8)]
+
+
+def run_packed(x, w, s, b, tile=None):
+    wd, sd, bd = to_dev(w, torch.int32), to_dev(s, torch.bfloat16), to_dev(b, torch.bfloat16)
+    packed = kernels.pack_w4(wd, sd, bd)
+    y = kernels.quantized_matmul_packed(to_dev(x, torch.bfloat16), packed, w.shape[0], tile=tile)
+    torch.cuda.synchronize()
+    return y.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tile", PACKED_TILES)
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_packed_tiles(tile, M):
+    N, K = 531, 2304                       # ragged last tile, 9 sets
+    w, s, b = synth.qmv_weights(N, K, seed=31, tag=M)
+    x = synth.qmv_x(M, K, seed=31, tag=M)
+    check(x, w, s, b, run_packed(x, w, s, b, tile=tile))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K", [(1, 256), (16, 256), (17, 512), (100, 4096), (4096, 256)])
+def test_packed_edge_shapes(N, K):
+    w, s, b = synth.qmv_weights(N, K, seed=32, tag=N)
+    x = synth.qmv_x(4, K, seed=32, tag=K)
+    check(x, w, s, b, run_packed(x, w, s, b))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 4])
+@pytest.mark.parametrize("shape", [(24576, 4096), (4096, 12288), (12352, 4096), (248320, 4096), (4096, 8192)])
+def test_packed_model_shapes(M, shape):
+    N, K = shape
+    w, s, b = synth.qmv_weights(N, K, seed=synth.SEED_SKINNY, tag=N)
+    x = synth.qmv_x(M, K, seed=synth.SEED_SKINNY, tag=M)
+    y = run_packed(x, w, s, b)
+    rows = np.unique(np.concatenate([np.arange(32), np.arange(N - 32, N),
+                                     np.random.default_rng(N).choice(N, 1024, replace=False)]))
+    check(x, w, s, b, y, rows=rows)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K", [(12352, 4096), (4096, 12288), (248320, 4096)])
+def test_packed_rows_bitwise_independent_of_m(N, K):
+    """Verify (M = k + 1) and plain decode (M = 1) see the same bits for a row."""
+    w, s, b = synth.qmv_weights(N, K, seed=33, tag=N)
+    x4 = synth.qmv_x(4, K, seed=33, tag=K)
+    y4 = run_packed(x4, w, s, b)
+    for m in range(4):
+        y1 = run_packed(x4[m:m + 1], w, s, b)
+        assert np.array_equal(y1[0], y4[m]), f"row {m} differs between M=1 and M=4"
+    y2 = run_packed(x4[1:3], w, s, b)
+    assert np.array_equal(y2, y4[1:3])
+
+
+@pytest.mark.gpu
+def test_packed_matches_mlx_layout_kernel_closely():
+    """Same product as the MLX-layout kernel (different summation order)."""
+    N, K = 2048, 4096
+    w, s, b = synth.qmv_weights(N, K, seed=34)
+    x = synth.qmv_x(4, K, seed=34)
+    from test_qmv_gpu import run
+    a = synth.bf16_to_f32(run_packed(x, w, s, b)).astype(np.float64)
+    c = synth.bf16_to_f32(run(x, w, s, b)).astype(np.float64)
+    assert np.abs(a - c).max() <= 2.0 ** -7 * np.abs(c).max()
