@@ -12,10 +12,14 @@ accept at T=0.7, roll back; the cycle is captured once as a HIP graph and
 replayed). value = tokens emitted in the timed cycles / time.
 
 Every line also carries:
-  roofline: the 4-bit GEMV of 12288 x 4096 (one M=1 qmv), timed with HIP events
-    over back-to-back launches that rotate through >= 600 MB of weight copies
-    (so HBM, not the 256 MB Infinity Cache, serves them); algorithmic bytes
-    0.5625*N*K + 2K + 2N = 28,344,320 per launch;
+  roofline: the dominant kernel of the cycle, the packed 4-bit MFMA qmv on the
+    fused gate/up projection at the 4 verify rows (N=24576, K=4096), timed with
+    HIP events over back-to-back launches that rotate through >= 600 MB of
+    weight copies (so HBM, not the 256 MB Infinity Cache, serves them);
+    algorithmic bytes 0.5625*N*K + 2MK + 2MN = 56,852,480 per launch;
+  qmv_config0: the same for the single 4-bit GEMV of 12288 x 4096 (M=1,
+    28,344,320 bytes per launch);
+  qmv_shapes: the decode cycle's other matmul shapes;
   cpu_baseline: the oracle's C restatement (OpenMP) of the cycle's quantized
     matmuls, timed on this host on one cycle's worth of shapes and scaled to
     tokens per second with the GPU run's tokens per cycle.
@@ -47,9 +51,10 @@ def log(*a):
 
 # ---------------------------------------------------------------- qmv roofline
 
-def qmv_time(M, N, K, iters=None, tile=None, seed_tag=0):
+def qmv_time(M, N, K, iters=None, tile=None, seed_tag=0, packed=False):
     """Average µs per launch of back-to-back qmv launches captured in one HIP graph,
-    rotating over enough weight copies that every launch reads HBM."""
+    rotating over enough weight copies that every launch reads HBM. packed=True
+    times the tile-packed MFMA kernel (what QLinear runs for 1..4 rows)."""
     import torch
     from qvex import kernels, synth
     dev = torch.device("cuda:0")
@@ -64,14 +69,22 @@ def qmv_time(M, N, K, iters=None, tile=None, seed_tag=0):
     W = [wd] + [torch.empty_like(wd).random_() for _ in range(ncopy - 1)]
     S = [sd] + [sd.clone() for _ in range(ncopy - 1)]
     B = [bd] + [bd.clone() for _ in range(ncopy - 1)]
+    if packed:
+        PK = [kernels.pack_w4(W[i], S[i], B[i]) for i in range(ncopy)]
+        del W, S, B
+        W = S = B = None
+        launch = lambda i: kernels.quantized_matmul_packed(xd, PK[i % ncopy], N, out=y, tile=tile)
+    else:
+        PK = None
+        launch = lambda i: kernels.quantized_matmul(xd, W[i % ncopy], S[i % ncopy], B[i % ncopy], out=y, tile=tile)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     iters = iters or max(2 * ncopy, 40)
-    kernels.quantized_matmul(xd, W[0], S[0], B[0], out=y, tile=tile)
+    launch(0)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for i in range(iters):
-            kernels.quantized_matmul(xd, W[i % ncopy], S[i % ncopy], B[i % ncopy], out=y, tile=tile)
+            launch(i)
     g.replay()
     torch.cuda.synchronize()
     best = float("inf")
@@ -82,7 +95,7 @@ def qmv_time(M, N, K, iters=None, tile=None, seed_tag=0):
         e1.record()
         torch.cuda.synchronize()
         best = min(best, e0.elapsed_time(e1) * 1e3 / iters)
-    del g, W, S, B
+    del g, W, S, B, PK
     torch.cuda.empty_cache()
     algo = 0.5625 * N * K + 2 * M * K + 2 * M * N
     return best, algo
@@ -102,36 +115,130 @@ def read_roof_calibration(nbytes=28344320 // 16 * 16, copies=24, reps=3):
     return nbytes
 
 
-PROFILE = REPO / "profiles" / "qmv_gemv_12288x4096_m1.json"
+# Kernels with a roofline entry: (M, N, K, packed, profile summary). "gate_up_m4" is
+# the dominant kernel of the decode cycle (the fused gate/up projection of every
+# layer at the 4 verify rows); "config0" is the single M=1 GEMV of 12288 x 4096.
+ROOF_KERNELS = {
+    "gate_up_m4": (4, 24576, 4096, True, "qmv_packed_24576x4096_m4.json",
+                   "qvex_qmv_w4g64_packed (M=4, N=24576, K=4096; verify gate_up)"),
+    "config0": (1, 12288, 4096, False, "qmv_gemv_12288x4096_m1.json",
+                "qvex_qmv_w4g64 (M=1, N=12288, K=4096)"),
+}
 
 
-def roofline_qmv0():
-    us, algo = qmv_time(1, 12288, 4096)
+def roofline(name):
+    M, N, K, packed, prof_name, label = ROOF_KERNELS[name]
+    us, algo = qmv_time(M, N, K, packed=packed)
     ach = algo / (us * 1e-6) / 1e9
-    out = {"kernel": "qvex_qmv_w4g64 (M=1, N=12288, K=4096)", "bound": "hbm",
+    out = {"kernel": label, "bound": "hbm",
            "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
            "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
            "algorithmic_bytes_per_launch": int(algo), "avg_launch_us": round(us, 3)}
-    # HBM bytes per launch come from rocprofv3 FETCH_SIZE/WRITE_SIZE passes of this
-    # same command (calibrated on a read of known size), kept in profiles/
-    if PROFILE.exists():
-        prof = json.loads(PROFILE.read_text())
-        out["traffic"] = prof["traffic_bytes_per_launch"]
-        out["traffic_source"] = f"{PROFILE.relative_to(REPO)} ({prof['calibration']})"
-        out["rocprof_avg_launch_us"] = prof["avg_us"]
+    # HBM bytes per launch come from rocprofv3 FETCH_SIZE/WRITE_SIZE passes of
+    # `bench.py --workload qmv --qmv NAME` (calibrated on a read of known size), kept in profiles/
+    prof = REPO / "profiles" / prof_name
+    if prof.exists():
+        p = json.loads(prof.read_text())
+        out["traffic"] = p["traffic_bytes_per_launch"]
+        out["traffic_source"] = f"{prof.relative_to(REPO)} ({p['calibration']})"
+        out["rocprof_avg_launch_us"] = p["avg_us"]
     return out
 
 
 def qmv_shapes():
-    """GB/s of the verify-cycle shapes (M=4 verify rows, M=1 draft rows)."""
+    """Config-1 shapes as the decode cycle runs them: the packed MFMA kernel for
+    1..4 rows (M=4 verify, M=1 draft / plain decode), the MLX-layout kernel at M=5."""
     out = {}
-    for name, (M, N, K) in {"lm_head_m1": (1, 248320, 4096), "lm_head_m4": (4, 248320, 4096),
-                            "gate_up_m4": (4, 24576, 4096), "down_m4": (4, 4096, 12288),
-                            "gdn_in_proj_m4": (4, 12352, 4096)}.items():
-        us, algo = qmv_time(M, N, K)
+    shapes = {"lm_head_m1": (1, 248320, 4096), "lm_head_m4": (4, 248320, 4096),
+              "gate_up_m4": (4, 24576, 4096), "down_m4": (4, 4096, 12288),
+              "gdn_in_proj_m4": (4, 12352, 4096), "attn_qkv_m4": (4, 10240, 4096),
+              "o_proj_m4": (4, 4096, 4096), "mtp_fc_m1": (1, 4096, 8192),
+              "gate_up_m5": (5, 24576, 4096)}
+    for name, (M, N, K) in shapes.items():
+        us, algo = qmv_time(M, N, K, packed=M <= 4)
         out[name] = {"us": round(us, 2), "GB/s": round(algo / (us * 1e-6) / 1e9, 1),
-                     "frac": round(algo / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)}
+                     "frac": round(algo / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                     "kernel": "packed" if M <= 4 else "mlx-layout"}
     return out
+
+
+def _event_time(fn, iters, reps=3):
+    """Best-of-reps average µs per call of fn(i), i = 0..iters-1, between HIP events
+    on the current stream (every call launches on that stream)."""
+    import torch
+    fn(0)
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(iters):
+            fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e3 / iters)
+    return best
+
+
+def spec_config3(S=256, k=4, V=248320, temperature=0.7):
+    """Fused accept/resample over S verify steps in one launch (target ~N(0,3) plus
+    +8 spikes, draft = target + N(0,1), uniforms U(0,1)); bytes (2k+1)*V*4 per step.
+    Inputs (2.29 GB) are generated on the device; bit-exactness against the oracle
+    is what the spec tests check on the same rule."""
+    import torch
+    from qvex import kernels
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1003)
+    target = torch.randn((S, k + 1, V), generator=g, device=dev) * 3.0
+    spikes = torch.randint(0, V, (S, k + 1, 3), generator=g, device=dev)
+    target.scatter_add_(2, spikes, torch.full(spikes.shape, 8.0, device=dev))
+    draft = target[:, :k] + torch.randn((S, k, V), generator=g, device=dev)
+    draft_ids = torch.multinomial(torch.softmax(draft.reshape(-1, V) / temperature, -1), 1,
+                                  generator=g).reshape(S, k).to(torch.int32)
+    u_acc = torch.rand((S, k), generator=g, device=dev)
+    u_smp = torch.rand((S,), generator=g, device=dev)
+    ws = kernels.spec_workspace(S, k, V, True, dev)
+    n = torch.empty(S, dtype=torch.int32, device=dev)
+    tok = torch.empty(S, dtype=torch.int32, device=dev)
+    us = _event_time(lambda i: kernels.spec_accept(target, draft, draft_ids, u_acc, u_smp, temperature,
+                                                    n_accept=n, out_token=tok, workspace=ws), 5)
+    nbytes = (2 * k + 1) * V * 4 * S
+    acc = float(n.float().mean())
+    del target, draft, spikes
+    torch.cuda.empty_cache()
+    return {"kernel": "qvex_spec_accept (3 kernels: rowstats, decide, sample)", "steps": S, "k": k, "V": V,
+            "us": round(us, 1), "us_per_step": round(us / S, 3), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4), "bytes": nbytes,
+            "mean_accept": round(acc, 3)}
+
+
+def gdn_config2_verify(T=5, Hk=16, Hv=32, D=128, copies=40):
+    """Gated DeltaNet verify form: T tokens of one layer (Hk=16, Hv=32, d=128) with
+    a state snapshot per token; rotates over `copies` state/snapshot buffers so the
+    2 MiB state is read from HBM; bytes = state + T snapshots + q,k,v,y,a,b."""
+    import torch
+    from qvex import kernels
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1002)
+    bf = torch.bfloat16
+    q = torch.nn.functional.normalize(torch.randn((1, T, Hk, D), generator=g, device=dev), dim=-1).to(bf)
+    kk = torch.nn.functional.normalize(torch.randn((1, T, Hk, D), generator=g, device=dev), dim=-1).to(bf)
+    v = torch.randn((1, T, Hv, D), generator=g, device=dev).to(bf)
+    a = torch.randn((1, T, Hv), generator=g, device=dev).to(bf)
+    b = torch.randn((1, T, Hv), generator=g, device=dev).to(bf)
+    A_log = torch.zeros(Hv, device=dev)
+    dt = torch.zeros(Hv, device=dev, dtype=bf)
+    states = [torch.randn((1, Hv, D, D), generator=g, device=dev) * 0.02 for _ in range(copies)]
+    snaps = [torch.empty((T, 1, Hv, D, D), device=dev) for _ in range(copies)]
+    y = torch.empty((1, T, Hv, D), device=dev, dtype=bf)
+    us = _event_time(lambda i: kernels.gated_delta_snapshots(q, kk, v, a, b, A_log, dt, states[i % copies],
+                                                              snapshots=snaps[i % copies], y=y), 4 * copies)
+    nbytes = (1 + T) * Hv * D * D * 4 + 2 * T * Hk * D * 2 + 2 * T * Hv * D * 2 + 2 * T * Hv * 2
+    return {"kernel": "qvex_gdn_recurrent (T=5, per-token snapshots)", "us": round(us, 2),
+            "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1), "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            "bytes": nbytes}
 
 
 # ---------------------------------------------------------------- CPU baseline
@@ -244,6 +351,8 @@ def main():
     ap.add_argument("--temperature", type=float, default=0.7)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-shapes", action="store_true")
+    ap.add_argument("--qmv", default="config0", choices=sorted(ROOF_KERNELS),
+                    help="kernel timed by --workload qmv")
     ap.add_argument("--eager", action="store_true", help="launch every kernel from Python (no HIP graph)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -276,15 +385,26 @@ def main():
         from qvex.model import Config
         cfg = Config.qwen35_9b()
         res = None
-    log("qmv roofline")
-    line["roofline"] = roofline_qmv0()
     if args.workload == "qmv":
+        # one kernel only (what the rocprofv3 passes under profiles/ run)
+        log(f"qmv roofline {args.qmv}")
+        line["roofline"] = roofline(args.qmv)
         line["read_roof_calibration_bytes"] = read_roof_calibration()
+        M, N, K = ROOF_KERNELS[args.qmv][:3]
         line.update({"value": line["roofline"]["achieved"], "unit": "GB/s",
                      "ms_per_step": line["roofline"]["avg_launch_us"] / 1e3,
-                     "config": {"workload": "4-bit group-64 GEMV, x bf16 [1,4096], W [12288,4096]"}})
+                     "config": {"workload": f"4-bit group-64 qmv, x bf16 [{M},{K}], W [{N},{K}]"}})
+    else:
+        log("qmv roofline (dominant kernel of the cycle)")
+        line["roofline"] = roofline("gate_up_m4")
+        log("qmv roofline (config 0 GEMV)")
+        line["qmv_config0"] = roofline("config0")
     if not args.no_shapes:
+        log("config-1 shapes")
         line["qmv_shapes"] = qmv_shapes()
+        log("config-2 verify (GDN) and config-3 sampler")
+        line["gdn_config2_verify"] = gdn_config2_verify()
+        line["spec_config3"] = spec_config3()
     if not args.no_cpu_baseline:
         log("cpu baseline")
         tpc = res["tokens_per_cycle"] if res else 1.0
