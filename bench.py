@@ -241,6 +241,40 @@ def gdn_config2_verify(T=5, Hk=16, Hv=32, D=128, copies=40):
             "bytes": nbytes}
 
 
+def gdn_config2_prefill(T=4096, Hk=16, Hv=32, D=128, C=64, recurrent=True):
+    """Gated DeltaNet prefill form, T = 4096 tokens of one layer (Hk = 16, Hv = 32,
+    d = 128) through the chunked MFMA kernel (chunk 64); work counted as the
+    canonical chunked FLOPs Hv*(T/C)*(4C^2 Dk + 4C^2 Dv + 6 C Dk Dv) = 21.47 GFLOP.
+    The recurrent kernel on the same input is timed beside it."""
+    import torch
+    from qvex import _C, kernels
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(1002)
+    bf = torch.bfloat16
+    q = torch.nn.functional.normalize(torch.randn((1, T, Hk, D), generator=g, device=dev), dim=-1).to(bf)
+    kk = torch.nn.functional.normalize(torch.randn((1, T, Hk, D), generator=g, device=dev), dim=-1).to(bf)
+    v = torch.randn((1, T, Hv, D), generator=g, device=dev).to(bf)
+    a = torch.randn((1, T, Hv), generator=g, device=dev).to(bf)
+    b = torch.randn((1, T, Hv), generator=g, device=dev).to(bf)
+    A_log = torch.zeros(Hv, device=dev)
+    dt = torch.zeros(Hv, device=dev, dtype=bf)
+    s0 = torch.randn((1, Hv, D, D), generator=g, device=dev) * 0.02
+    s1 = torch.empty_like(s0)
+    y = torch.empty((1, T, Hv, D), device=dev, dtype=bf)
+    ws = torch.empty(int(_C.lib().qvex_gdn_chunked_workspace_bytes(1, T, Hv, D, D, C)), dtype=torch.uint8, device=dev)
+    us = _event_time(lambda i: kernels.gated_delta_chunked(q, kk, v, a, b, A_log, dt, s0, state_out=s1, y=y,
+                                                           workspace=ws), 10)
+    flops = Hv * (T // C) * (4 * C * C * D + 4 * C * C * D + 6 * C * D * D)
+    out = {"kernel": "qvex_gdn_chunked (prep + scan, chunk 64)", "T": T, "us": round(us, 1),
+           "TFLOP/s": round(flops / (us * 1e-6) / 1e12, 2), "frac_of_bf16_peak": round(flops / (us * 1e-6) / 2.5e15, 4),
+           "flops": flops}
+    if recurrent:
+        ur = _event_time(lambda i: kernels.gated_delta(q, kk, v, a, b, A_log, dt, s0), 3)
+        out["recurrent_us"] = round(ur, 1)
+    return out
+
+
 # ---------------------------------------------------------------- CPU baseline
 
 def cycle_shapes(cfg, k):
@@ -345,7 +379,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="e2e", choices=["e2e", "qmv"])
+    ap.add_argument("--workload", default="e2e", choices=["e2e", "qmv", "gdn"])
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--k", type=int, default=3)
     ap.add_argument("--temperature", type=float, default=0.7)
@@ -385,6 +419,14 @@ def main():
         from qvex.model import Config
         cfg = Config.qwen35_9b()
         res = None
+    if args.workload == "gdn":
+        # the chunked prefill kernel only (what the rocprofv3 MFMA passes under profiles/ run)
+        r = gdn_config2_prefill(recurrent=False)
+        line.update({"value": r["TFLOP/s"], "unit": "TFLOP/s", "ms_per_step": r["us"] / 1e3,
+                     "dtype": "bf16 operands, fp32 state", "gdn_config2_prefill": r,
+                     "config": {"workload": "Gated DeltaNet prefill, T=4096, Hk=16, Hv=32, d=128, chunk 64"}})
+        print(json.dumps(line), flush=True)
+        return
     if args.workload == "qmv":
         # one kernel only (what the rocprofv3 passes under profiles/ run)
         log(f"qmv roofline {args.qmv}")
@@ -405,6 +447,8 @@ def main():
         log("config-2 verify (GDN) and config-3 sampler")
         line["gdn_config2_verify"] = gdn_config2_verify()
         line["spec_config3"] = spec_config3()
+        log("config-2 prefill (chunked GDN)")
+        line["gdn_config2_prefill"] = gdn_config2_prefill()
     if not args.no_cpu_baseline:
         log("cpu baseline")
         tpc = res["tokens_per_cycle"] if res else 1.0

@@ -132,6 +132,22 @@ int qvex_gdn_recurrent_ring(const uint16_t* q, const uint16_t* k, const uint16_t
                             const int32_t* cur_slot, int snap_every, uint16_t* y, int B, int T,
                             int Hk, int Hv, int Dk, int Dv, void* stream);
 
+/* Chunked (prefill) form of the same recurrence, chunk = 64 tokens, on MFMA:
+ * gated_delta over a long prompt (engine/kernels.py:92-116 as called by
+ * GatedDeltaNet.__call__ during prefill, engine/model.py:282-286). Phase 1
+ * (all chunks in parallel) builds each chunk's WY form W, U~ and the masked
+ * Q K^T in `workspace`; phase 2 scans the chunks in order with the fp32 state
+ * in registers. state_in fp32 [B,Hv,Dv,Dk] -> state_out (may be the same
+ * buffer), y bf16 [B,T,Hv,Dv]. Dk = Dv = 128, chunk = 64. Operands of the
+ * products are bf16, accumulation fp32. workspace:
+ * qvex_gdn_chunked_workspace_bytes() = B * Hv * ceil(T/64) * 73984 bytes. */
+uint64_t qvex_gdn_chunked_workspace_bytes(int B, int T, int Hv, int Dk, int Dv, int chunk);
+int qvex_gdn_chunked(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* a,
+                     const uint16_t* b, const float* A_log, const uint16_t* dt_bias,
+                     const float* state_in, float* state_out, uint16_t* y, int B, int T, int Hk,
+                     int Hv, int Dk, int Dv, int chunk, void* workspace, uint64_t workspace_bytes,
+                     void* stream);
+
 /* ------------------------------------------------------------------------
  * Fused speculative acceptance sampling for S independent verify steps.
  *

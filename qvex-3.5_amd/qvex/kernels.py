@@ -198,6 +198,29 @@ def gated_delta_ring(q, k, v, a, b, A_log, dt_bias, ring, cur_slot, y=None, snap
 
 # ---------------------------------------------------------------- speculative acceptance
 
+def gated_delta_chunked(q, k, v, a, b, A_log, dt_bias, state, state_out=None, y=None, workspace=None):
+    """Chunked (64-token, MFMA) Gated DeltaNet over a long prefill: the same
+    recurrence as gated_delta (engine/kernels.py:92-116) without per-token
+    snapshots. Shapes as gated_delta_snapshots; returns (y, final state)."""
+    B, T, Hk, Hv, Dk, Dv = _gdn_check(q, k, v, a, b, A_log, dt_bias)
+    _check(state, "state", torch.float32)
+    if state.shape != (B, Hv, Dv, Dk):
+        raise _C.QvexError(f"state must be [B,Hv,Dv,Dk]=({B},{Hv},{Dv},{Dk})")
+    if state_out is None:
+        state_out = torch.empty_like(state)
+    if y is None:
+        y = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=q.device)
+    need = int(_C.lib().qvex_gdn_chunked_workspace_bytes(B, T, Hv, Dk, Dv, 64))
+    if need == 0:
+        raise _C.QvexError(f"gated_delta_chunked: needs Dk = Dv = 128 (got {Dk}, {Dv})")
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    _C.call("qvex_gdn_chunked", _ptr(q), _ptr(k), _ptr(v), _ptr(a), _ptr(b), _ptr(A_log), _ptr(dt_bias),
+            _ptr(state), _ptr(state_out), _ptr(y), B, T, Hk, Hv, Dk, Dv, 64, _ptr(workspace),
+            workspace.numel() * workspace.element_size(), _stream())
+    return y, state_out
+
+
 def spec_workspace(S: int, k: int, V: int, has_draft: bool, device) -> torch.Tensor:
     n = int(_C.lib().qvex_spec_accept_workspace_bytes(S, k, V, int(has_draft)))
     return torch.empty((max(n, 4) + 3) // 4, dtype=torch.float32, device=device)

@@ -1,0 +1,105 @@
+"""Chunked (64-token, MFMA) Gated DeltaNet prefill vs the fp64 oracle and the
+recurrent kernel (GPU).
+
+The chunked form feeds bf16-rounded operands to the matrix cores (the state and
+the per-chunk WY factors are rounded to bf16 where they enter a product;
+accumulation and the carried state stay fp32), so it agrees with the fp32
+recurrence to bf16-product accuracy, not bit for bit. Errors are measured
+relative to the largest magnitude of the reference tensor:
+    y:     max|y - y64| <= Y_TOL * max|y64|
+    state: max|S - S64| <= S_TOL * max|S64|
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from qvex import kernels, synth
+from test_gdn_gpu import bf, dev_inputs, f32, to_np_bf16
+
+Y_TOL = 2e-2
+S_TOL = 2e-2
+
+
+def rel(got, ref):
+    return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def run_chunked(inp, state=None):
+    st = f32(inp["state"] if state is None else state)
+    y, s = kernels.gated_delta_chunked(*dev_inputs(inp), st)
+    torch.cuda.synchronize()
+    return to_np_bf16(y).astype(np.float64), s.cpu().numpy().astype(np.float64)
+
+
+def oracle_f64(inp, state=None):
+    f = synth.bf16_to_f32
+    y, s, _ = oracle.gated_delta_f64(f(inp["q"]), f(inp["k"]), f(inp["v"]), f(inp["a"]), f(inp["b"]),
+                                     inp["A_log"], f(inp["dt_bias"]),
+                                     inp["state"] if state is None else state, snaps=False)
+    return y, s
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T", [1, 5, 63, 64, 65, 200])
+def test_chunked_matches_oracle(T):
+    inp = synth.gdn_inputs(T, seed=71, Hk=4, Hv=8)
+    y, s = run_chunked(inp)
+    y64, s64 = oracle_f64(inp)
+    ey, es = rel(y, y64), rel(s, s64)
+    print(f"T={T}: y rel {ey:.2e}  state rel {es:.2e}")
+    assert ey <= Y_TOL and es <= S_TOL
+
+
+@pytest.mark.gpu
+def test_chunked_config2_prefill():
+    """T = 4096, Hk = 16, Hv = 32: against the recurrent kernel on every head, and
+    against the fp64 oracle on the first GQA head pair (key head 0)."""
+    T = 4096
+    inp = synth.gdn_inputs(T, seed=1002, Hk=16, Hv=32)
+    y, s = run_chunked(inp)
+    yr, sr = kernels.gated_delta(*dev_inputs(inp), f32(inp["state"]))
+    torch.cuda.synchronize()
+    yr, sr = to_np_bf16(yr).astype(np.float64), sr.cpu().numpy().astype(np.float64)
+    ey, es = rel(y, yr), rel(s, sr)
+    print(f"vs recurrent: y rel {ey:.2e}  state rel {es:.2e}")
+    assert ey <= Y_TOL and es <= S_TOL
+    sub = dict(q=inp["q"][:, :, :1], k=inp["k"][:, :, :1], v=inp["v"][:, :, :2], a=inp["a"][:, :, :2],
+               b=inp["b"][:, :, :2], A_log=inp["A_log"][:2], dt_bias=inp["dt_bias"][:2],
+               state=inp["state"][:, :2])
+    y64, s64 = oracle_f64(sub)
+    ey, es = rel(y[:, :, :2], y64), rel(s[:, :2], s64)
+    print(f"vs fp64 oracle (heads 0-1): y rel {ey:.2e}  state rel {es:.2e}")
+    assert ey <= Y_TOL and es <= S_TOL
+
+
+@pytest.mark.gpu
+def test_chunked_composes_across_calls():
+    """Running 130 then 70 tokens from the carried state equals running 200 at once."""
+    inp = synth.gdn_inputs(200, seed=72, Hk=4, Hv=8)
+    y, s = run_chunked(inp)
+    head = {n: (inp[n][:, :130] if n in ("q", "k", "v", "a", "b") else inp[n]) for n in inp}
+    tail = {n: (inp[n][:, 130:] if n in ("q", "k", "v", "a", "b") else inp[n]) for n in inp}
+    y1, s1 = run_chunked(head)
+    y2, s2 = run_chunked(tail, state=s1.astype(np.float32))
+    e = max(rel(np.concatenate([y1, y2], axis=1), y), rel(s2, s))
+    print(f"split vs whole: {e:.2e}")
+    assert e <= Y_TOL
+
+
+@pytest.mark.gpu
+def test_chunked_identity_gates_keep_state():
+    """g = 1 and beta = 0 (a, b = -30): the state is unchanged and y_t = S0 q_t."""
+    inp = synth.gdn_inputs(100, seed=73, Hk=2, Hv=4)
+    inp["a"] = np.full_like(inp["a"], synth.bf16_bits(np.float32(-30.0)))
+    inp["b"] = np.full_like(inp["b"], synth.bf16_bits(np.float32(-30.0)))
+    y, s = run_chunked(inp)
+    assert rel(s, inp["state"].astype(np.float64)) <= 1e-6
+    q = synth.bf16_to_f32(inp["q"]).astype(np.float64)           # [B,T,Hk,D]
+    S0 = inp["state"].astype(np.float64)                          # [B,Hv,Dv,Dk]
+    grp = S0.shape[1] // q.shape[2]
+    ref = np.einsum("bhij,bthj->bthi", S0, np.repeat(q, grp, axis=2))
+    e = rel(y, ref)
+    print(f"y vs S0 q: {e:.2e}")
+    assert e <= Y_TOL
