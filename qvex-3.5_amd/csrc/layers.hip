@@ -341,7 +341,7 @@ __device__ __forceinline__ att_bf16x8 as_att8(const u32x4 v) { return __builtin_
 // 128 adjacent keys), loads their K rows and dim-major V columns in one round
 // trip, scores them with MFMA, runs an online softmax per row and accumulates
 // P V with MFMA. The 4 waves' (max, sum, O) are then merged in LDS and written as
-// one partial per block: ws [kv head][tile][split][16 rows][2 + D] = (m, l, O[D]).
+// one partial per block: ws [kv head][tile][split] = ([16 rows][m, l], [16 rows][O[D]]).
 template <int D>
 __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
@@ -485,28 +485,32 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
       fac[v][r] = f;
       l += ml[v][r][1] * f;
     }
-    wsb[(size_t)r * (D + 2)] = m;
-    wsb[(size_t)r * (D + 2) + 1] = l;
+    wsb[2 * r] = m;
+    wsb[2 * r + 1] = l;
   }
   __syncthreads();
   for (int e = threadIdx.x; e < 16 * D; e += 256) {
     const int r = e / D, d = e % D;
     const float acc = ((ob[0][r][d] * fac[0][r] + ob[1][r][d] * fac[1][r]) + ob[2][r][d] * fac[2][r]) +
                       ob[3][r][d] * fac[3][r];
-    wsb[(size_t)r * (D + 2) + 2 + d] = acc;
+    wsb[32 + (size_t)r * D + d] = acc;
   }
 }
 
 // out[lq, (kh*GQ + g)*D + d] = bf16(sigmoid(gate) * sum_s o_s e^{m_s-m} / sum_s l_s e^{m_s-m})
 // over the splits that hold visible keys (the count follows from the device position).
-// One block of D threads per (kv head, tile, row).
+// One 256-thread block per (kv head, tile, row): NG groups of D/4 threads, thread
+// (g, j) owns dims 4j..4j+3 of splits g, g + NG, ...; every load of a thread is
+// independent of its sums, so the whole row streams in about one round trip. The
+// groups are merged in LDS in a fixed order.
 template <int D>
-__global__ __launch_bounds__(D) void attn_combine_kernel(const float* __restrict__ ws, int nsplit, int ntile,
-                                                         int keys_per_split, const int32_t* __restrict__ pos0,
-                                                         int L, int Hq, int Hkv, int QT,
-                                                         const uint16_t* __restrict__ gate, long g_stride,
-                                                         uint16_t* __restrict__ out) {
-  constexpr int NW = D / 64;
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ ws, int nsplit, int ntile,
+                                                           int keys_per_split, const int32_t* __restrict__ pos0,
+                                                           int L, int Hq, int Hkv, int QT,
+                                                           const uint16_t* __restrict__ gate, long g_stride,
+                                                           uint16_t* __restrict__ out) {
+  constexpr int TPG = D / 4;            // threads per split group
+  constexpr int NG = 256 / TPG;         // split groups
   const int kh = blockIdx.x, tile = blockIdx.y, r = blockIdx.z;
   const int GQ = Hq / Hkv;
   if (r >= GQ * QT) return;
@@ -515,42 +519,51 @@ __global__ __launch_bounds__(D) void attn_combine_kernel(const float* __restrict
   const int h = kh * GQ + g;
   const int kend_tile = *pos0 + min(L, (tile + 1) * QT);
   const int nact = min(nsplit, (kend_tile + keys_per_split - 1) / keys_per_split);
-  const size_t sstride = (size_t)16 * (D + 2);
-  const float* base = ws + (((size_t)kh * ntile + tile) * nsplit) * sstride + (size_t)r * (D + 2);
-  __shared__ float red[2][NW];
+  const size_t rec = (size_t)16 * (D + 2);
+  const float* base = ws + ((size_t)kh * ntile + tile) * nsplit * rec;
+  __shared__ float red[2][4];
+  __shared__ __align__(16) float part[NG][D];
   const int tid = threadIdx.x, wv = tid >> 6;
 
+  // global max and normaliser over the active splits
   float m = -INFINITY;
-  for (int s = tid; s < nact; s += D) m = fmaxf(m, base[s * sstride]);
+  for (int s = tid; s < nact; s += 256) m = fmaxf(m, base[s * rec + 2 * r]);
   m = wave_allmax(m);
   if ((tid & 63) == 0) red[0][wv] = m;
   __syncthreads();
-  m = red[0][0];
-#pragma unroll
-  for (int v = 1; v < NW; ++v) m = fmaxf(m, red[0][v]);
+  m = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
   float l = 0.0f;
-  for (int s = tid; s < nact; s += D) {
-    const float ms = base[s * sstride];
-    if (ms != -INFINITY) l += base[s * sstride + 1] * expf(ms - m);
+  for (int s = tid; s < nact; s += 256) {
+    const float ms = base[s * rec + 2 * r];
+    if (ms != -INFINITY) l += base[s * rec + 2 * r + 1] * expf(ms - m);
   }
   l = wave_allsum(l);
   if ((tid & 63) == 0) red[1][wv] = l;
   __syncthreads();
-  l = red[1][0];
-#pragma unroll
-  for (int v = 1; v < NW; ++v) l += red[1][v];
+  l = ((red[1][0] + red[1][1]) + red[1][2]) + red[1][3];
   const float invl = l > 0.0f ? 1.0f / l : 0.0f;
 
-  const int d = tid;
-  float o = 0.0f;
-#pragma unroll 4
-  for (int s = 0; s < nact; ++s) {
-    const float ms = base[s * sstride];
-    const float os = base[s * sstride + 2 + d];
-    if (ms != -INFINITY) o = fmaf(os, expf(ms - m), o);
+  const int grp = tid / TPG, j = tid % TPG;
+  float4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
+  for (int s = grp; s < nact; s += NG) {
+    const float ms = base[s * rec + 2 * r];
+    const float4 os = *reinterpret_cast<const float4*>(base + s * rec + 32 + (size_t)r * D + 4 * j);
+    const float f = ms == -INFINITY ? 0.0f : expf(ms - m);
+    o.x = fmaf(os.x, f, o.x);
+    o.y = fmaf(os.y, f, o.y);
+    o.z = fmaf(os.z, f, o.z);
+    o.w = fmaf(os.w, f, o.w);
   }
-  const float gt = bf16_to_f32(gate[(size_t)lq * g_stride + (size_t)h * 2 * D + D + d]);
-  out[(size_t)lq * Hq * D + (size_t)h * D + d] = f32_to_bf16(o * invl * sigmoidf_(gt));
+  *reinterpret_cast<float4*>(&part[grp][4 * j]) = o;
+  __syncthreads();
+  for (int d = tid; d < D; d += 256) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NG; ++q) acc += part[q][d];
+    const float gt = bf16_to_f32(gate[(size_t)lq * g_stride + (size_t)h * 2 * D + D + d]);
+    out[(size_t)lq * Hq * D + (size_t)h * D + d] = f32_to_bf16(acc * invl * sigmoidf_(gt));
+  }
 }
 
 // counters[i] += n_accept[0] + 1 for every i (advance all caches past the kept tokens)
@@ -709,7 +722,7 @@ extern "C" int qvex_attention(const uint16_t* q, const uint16_t* k_cache, const 
     hipLaunchKernelGGL((attn_mfma_partial_kernel<128>), pgrid, dim3(256), 0, st, q, k_cache, v_cache, pos0, L, Hq,
                        Hkv, cap, QT, keys_per_split, scale, (float*)workspace);
     QVEX_CHECK_LAUNCH("qvex_attention/partial");
-    hipLaunchKernelGGL((attn_combine_kernel<128>), dim3(Hkv, ntile, ATT_ROWS), dim3(128), 0, st,
+    hipLaunchKernelGGL((attn_combine_kernel<128>), dim3(Hkv, ntile, ATT_ROWS), dim3(256), 0, st,
                        (const float*)workspace, nsplit, ntile, keys_per_split, pos0, L, Hq, Hkv, QT, gate,
                        gate_stride, out);
   }
