@@ -13,10 +13,11 @@ replayed). value = tokens emitted in the timed cycles / time.
 
 Every line also carries:
   roofline: the dominant kernel of the cycle, the packed 4-bit MFMA qmv on the
-    fused gate/up projection at the 4 verify rows (N=24576, K=4096), timed with
-    HIP events over back-to-back launches that rotate through >= 600 MB of
-    weight copies (so HBM, not the 256 MB Infinity Cache, serves them);
-    algorithmic bytes 0.5625*N*K + 2MK + 2MN = 56,852,480 per launch;
+    fused gate/up projection at the 4 verify rows with SwiGLU in its epilogue
+    (N=24576, K=4096), timed with HIP events over back-to-back launches that
+    rotate through >= 600 MB of weight copies (so HBM, not the 256 MB Infinity
+    Cache, serves them); algorithmic bytes 0.5625*N*K + 2MK + 2M(N/2) =
+    56,754,176 per launch;
   qmv_config0: the same for the single 4-bit GEMV of 12288 x 4096 (M=1,
     28,344,320 bytes per launch);
   qmv_shapes: the decode cycle's other matmul shapes;
@@ -51,7 +52,7 @@ def log(*a):
 
 # ---------------------------------------------------------------- qmv roofline
 
-def qmv_time(M, N, K, iters=None, tile=None, seed_tag=0, packed=False):
+def qmv_time(M, N, K, iters=None, tile=None, seed_tag=0, packed=False, swiglu=False):
     """Average µs per launch of back-to-back qmv launches captured in one HIP graph,
     rotating over enough weight copies that every launch reads HBM. packed=True
     times the tile-packed MFMA kernel (what QLinear runs for 1..4 rows)."""
@@ -70,14 +71,14 @@ def qmv_time(M, N, K, iters=None, tile=None, seed_tag=0, packed=False):
     S = [sd] + [sd.clone() for _ in range(ncopy - 1)]
     B = [bd] + [bd.clone() for _ in range(ncopy - 1)]
     if packed:
-        PK = [kernels.pack_w4(W[i], S[i], B[i]) for i in range(ncopy)]
+        PK = [kernels.pack_w4(W[i], S[i], B[i], swiglu=swiglu) for i in range(ncopy)]
         del W, S, B
         W = S = B = None
-        launch = lambda i: kernels.quantized_matmul_packed(xd, PK[i % ncopy], N, out=y, tile=tile)
+        launch = lambda i: kernels.quantized_matmul_packed(xd, PK[i % ncopy], N, out=y, tile=tile, swiglu=swiglu)
     else:
         PK = None
         launch = lambda i: kernels.quantized_matmul(xd, W[i % ncopy], S[i % ncopy], B[i % ncopy], out=y, tile=tile)
-    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    y = torch.empty((M, N // 2 if swiglu else N), dtype=torch.bfloat16, device=dev)
     iters = iters or max(2 * ncopy, 40)
     launch(0)
     torch.cuda.synchronize()
@@ -97,7 +98,7 @@ def qmv_time(M, N, K, iters=None, tile=None, seed_tag=0, packed=False):
         best = min(best, e0.elapsed_time(e1) * 1e3 / iters)
     del g, W, S, B, PK
     torch.cuda.empty_cache()
-    algo = 0.5625 * N * K + 2 * M * K + 2 * M * N
+    algo = 0.5625 * N * K + 2 * M * K + 2 * M * (N // 2 if swiglu else N)
     return best, algo
 
 
@@ -119,8 +120,8 @@ def read_roof_calibration(nbytes=28344320 // 16 * 16, copies=24, reps=3):
 # the dominant kernel of the decode cycle (the fused gate/up projection of every
 # layer at the 4 verify rows); "config0" is the single M=1 GEMV of 12288 x 4096.
 ROOF_KERNELS = {
-    "gate_up_m4": (4, 24576, 4096, True, "qmv_packed_24576x4096_m4.json",
-                   "qvex_qmv_w4g64_packed (M=4, N=24576, K=4096; verify gate_up)"),
+    "gate_up_m4": (4, 24576, 4096, "swiglu", "qmv_packed_swiglu_24576x4096_m4.json",
+                   "qvex_qmv_w4g64_packed_swiglu (M=4, N=24576, K=4096; verify gate_up + SwiGLU)"),
     "config0": (1, 12288, 4096, False, "qmv_gemv_12288x4096_m1.json",
                 "qvex_qmv_w4g64 (M=1, N=12288, K=4096)"),
 }
@@ -128,7 +129,7 @@ ROOF_KERNELS = {
 
 def roofline(name):
     M, N, K, packed, prof_name, label = ROOF_KERNELS[name]
-    us, algo = qmv_time(M, N, K, packed=packed)
+    us, algo = qmv_time(M, N, K, packed=bool(packed), swiglu=packed == "swiglu")
     ach = algo / (us * 1e-6) / 1e9
     out = {"kernel": label, "bound": "hbm",
            "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -150,12 +151,12 @@ def qmv_shapes():
     1..4 rows (M=4 verify, M=1 draft / plain decode), the MLX-layout kernel at M=5."""
     out = {}
     shapes = {"lm_head_m1": (1, 248320, 4096), "lm_head_m4": (4, 248320, 4096),
-              "gate_up_m4": (4, 24576, 4096), "down_m4": (4, 4096, 12288),
+              "gate_up_swiglu_m4": (4, 24576, 4096), "down_m4": (4, 4096, 12288),
               "gdn_in_proj_m4": (4, 12352, 4096), "attn_qkv_m4": (4, 10240, 4096),
               "o_proj_m4": (4, 4096, 4096), "mtp_fc_m1": (1, 4096, 8192),
               "gate_up_m5": (5, 24576, 4096)}
     for name, (M, N, K) in shapes.items():
-        us, algo = qmv_time(M, N, K, packed=M <= 4)
+        us, algo = qmv_time(M, N, K, packed=M <= 4, swiglu="swiglu" in name)
         out[name] = {"us": round(us, 2), "GB/s": round(algo / (us * 1e-6) / 1e9, 1),
                      "frac": round(algo / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
                      "kernel": "packed" if M <= 4 else "mlx-layout"}

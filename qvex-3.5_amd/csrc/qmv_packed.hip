@@ -47,28 +47,43 @@ __device__ __forceinline__ uint32_t reorder_nibbles(uint32_t w) {
   return r;
 }
 
+// Source row of tile row i of tile t. Plain: 16t + i. SwiGLU interleave (the
+// fused gate/up weight, gate rows [0, N/2), up rows [N/2, N)): tile t holds gate
+// rows 8t..8t+7 in its first 8 rows and the matching up rows in its last 8, so
+// one wave ends with both halves of 8 SwiGLU outputs. -1 = past the end (zero).
+__device__ __forceinline__ int pack_src_row(int t, int i, int N, int swiglu) {
+  if (!swiglu) {
+    const int r = t * PK_TILE + i;
+    return r < N ? r : -1;
+  }
+  const int half = N / 2;
+  const int j = 8 * t + (i & 7);
+  return j < half ? (i < 8 ? j : half + j) : -1;
+}
+
 // one 64-thread block per record
 __global__ __launch_bounds__(64) void pack_kernel(const uint32_t* __restrict__ w,
                                                   const uint16_t* __restrict__ scales,
-                                                  const uint16_t* __restrict__ biases, int N, int K,
+                                                  const uint16_t* __restrict__ biases, int N, int K, int swiglu,
                                                   uint8_t* __restrict__ packed) {
   const int GS = K / PK_SET;
   const int t = blockIdx.x / GS, s = blockIdx.x % GS;
   const int L = threadIdx.x, c = L >> 4, i = L & 15;
-  const int row = t * PK_TILE + i, g = s * 4 + c;
+  const int src = pack_src_row(t, i, N, swiglu);
+  const int g = s * 4 + c;
   const int KW = K / 8, G = K / 64;
   uint8_t* rec = packed + (size_t)blockIdx.x * PK_RECORD;
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     u32x4 v = {0u, 0u, 0u, 0u};
-    if (row < N) {
-      const uint32_t* src = w + (size_t)row * KW + g * 8 + 4 * q;
-      v = u32x4{reorder_nibbles(src[0]), reorder_nibbles(src[1]), reorder_nibbles(src[2]), reorder_nibbles(src[3])};
+    if (src >= 0) {
+      const uint32_t* sp = w + (size_t)src * KW + g * 8 + 4 * q;
+      v = u32x4{reorder_nibbles(sp[0]), reorder_nibbles(sp[1]), reorder_nibbles(sp[2]), reorder_nibbles(sp[3])};
     }
     *reinterpret_cast<u32x4*>(rec + q * 1024 + L * 16) = v;
   }
   uint32_t sb = 0;
-  if (row < N) sb = (uint32_t)scales[(size_t)row * G + g] | ((uint32_t)biases[(size_t)row * G + g] << 16);
+  if (src >= 0) sb = (uint32_t)scales[(size_t)src * G + g] | ((uint32_t)biases[(size_t)src * G + g] << 16);
   *reinterpret_cast<uint32_t*>(rec + PK_WBYTES + L * 4) = sb;
 }
 
@@ -79,7 +94,10 @@ constexpr int pk_block(int WS) { return WS >= 4 ? 64 * WS : 256; }
 // LDS in a fixed order; 4 / WS tile groups per block when WS < 4. Two register
 // buffers: the records and activation slice of the next set are in flight while
 // the current one is computed. Results depend on (N, K, TN, WS) only, never on M.
-template <int TN, int WS>
+// SWIGLU: the weight was packed with the gate/up interleave; the epilogue rounds
+// the gate and up products to bf16 (as the unfused pair of calls would) and
+// writes bf16(silu(g) * u) to y [M, N/2].
+template <int TN, int WS, bool SWIGLU>
 __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t* __restrict__ x,
                                                                    const uint8_t* __restrict__ packed,
                                                                    uint16_t* __restrict__ y, int M, int N, int K) {
@@ -205,7 +223,27 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
         }
     }
   }
-  if (lane < 16) {
+  if constexpr (SWIGLU) {
+    // lanes 0-7 hold gate rows, lanes 8-15 the matching up rows. The TN*4*8
+    // outputs are spread over the wave through its (now idle) LDS slot so that
+    // each lane evaluates at most TN/2 of the exp/divide pairs.
+    const int half = N / 2;
+    float* ep = reinterpret_cast<float*>(slot);          // [TN][4][16] floats <= 1 KiB of the 2 KiB slot
+    if (lane < 16) {
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ep[(t * 4 + r) * 16 + lane] = acc[t][r];
+    }
+#pragma unroll
+    for (int o = lane; o < TN * 32; o += 64) {
+      const int t = o >> 5, r = (o >> 3) & 3, i = o & 7;
+      const float gv = bf16_to_f32(f32_to_bf16(ep[(t * 4 + r) * 16 + i]));
+      const float uv = bf16_to_f32(f32_to_bf16(ep[(t * 4 + r) * 16 + 8 + i]));
+      const int j = (tile0 + t) * 8 + i;
+      if (j < half && r < M) y[(size_t)r * half + j] = f32_to_bf16(gv / (1.0f + expf(-gv)) * uv);
+    }
+  } else if (lane < 16) {
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
       const int n = (tile0 + t) * PK_TILE + i16;
@@ -220,22 +258,23 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
 
 typedef void (*qmv_packed_fn)(const uint16_t*, const uint8_t*, uint16_t*, int, int, int);
 
-template <int TN>
+template <int TN, bool SW>
 qmv_packed_fn pick_ws(int ws) {
   switch (ws) {
-    case 1: return qmv_packed_kernel<TN, 1>;
-    case 2: return qmv_packed_kernel<TN, 2>;
-    case 4: return qmv_packed_kernel<TN, 4>;
-    case 8: return qmv_packed_kernel<TN, 8>;
+    case 1: return qmv_packed_kernel<TN, 1, SW>;
+    case 2: return qmv_packed_kernel<TN, 2, SW>;
+    case 4: return qmv_packed_kernel<TN, 4, SW>;
+    case 8: return qmv_packed_kernel<TN, 8, SW>;
   }
   return nullptr;
 }
 
+template <bool SW>
 qmv_packed_fn pick_packed(int tn, int ws) {
   switch (tn) {
-    case 1: return pick_ws<1>(ws);
-    case 2: return pick_ws<2>(ws);
-    case 4: return pick_ws<4>(ws);
+    case 1: return pick_ws<1, SW>(ws);
+    case 2: return pick_ws<2, SW>(ws);
+    case 4: return pick_ws<4, SW>(ws);
   }
   return nullptr;
 }
@@ -256,21 +295,44 @@ void packed_default_tile(int N, int K, int* TN, int* WS) {
 }
 
 int launch_packed(const uint16_t* x, const uint8_t* packed, uint16_t* y, int M, int N, int K, int TN, int WS,
-                  hipStream_t stream) {
-  QVEX_CHECK_ARG(x && packed && y, "qvex_qmv_w4g64_packed: null pointer");
-  QVEX_CHECK_ARG(M >= 1 && M <= 4, "qvex_qmv_w4g64_packed: M=%d outside 1..4", M);
-  QVEX_CHECK_ARG(N >= 1 && K >= PK_SET && K % PK_SET == 0,
-                 "qvex_qmv_w4g64_packed: N=%d K=%d (K must be a positive multiple of 256)", N, K);
+                  bool swiglu, hipStream_t stream) {
+  const char* fn_name = swiglu ? "qvex_qmv_w4g64_packed_swiglu" : "qvex_qmv_w4g64_packed";
+  QVEX_CHECK_ARG(x && packed && y, "%s: null pointer", fn_name);
+  QVEX_CHECK_ARG(M >= 1 && M <= 4, "%s: M=%d outside 1..4", fn_name, M);
+  QVEX_CHECK_ARG(N >= 1 && K >= PK_SET && K % PK_SET == 0, "%s: N=%d K=%d (K must be a positive multiple of 256)",
+                 fn_name, N, K);
+  QVEX_CHECK_ARG(!swiglu || (N % 16 == 0), "%s: N=%d must be a multiple of 16 (gate and up halves of N/2 rows)",
+                 fn_name, N);
   QVEX_CHECK_ARG(qvex_aligned(x, 16) && qvex_aligned(packed, 16) && qvex_aligned(y, 2),
-                 "qvex_qmv_w4g64_packed: x and packed must be 16-byte aligned");
-  qmv_packed_fn fn = pick_packed(TN, WS);
-  QVEX_CHECK_ARG(fn != nullptr, "qvex_qmv_w4g64_packed: unsupported tile TN=%d WS=%d", TN, WS);
+                 "%s: x and packed must be 16-byte aligned", fn_name);
+  qmv_packed_fn fn = swiglu ? pick_packed<true>(TN, WS) : pick_packed<false>(TN, WS);
+  QVEX_CHECK_ARG(fn != nullptr, "%s: unsupported tile TN=%d WS=%d", fn_name, TN, WS);
   const int threads = pk_block(WS);
   const int tiles = (N + PK_TILE - 1) / PK_TILE;
   const int tiles_per_block = TN * (threads / 64 / WS);
   const int blocks = (tiles + tiles_per_block - 1) / tiles_per_block;
   hipLaunchKernelGGL(fn, dim3(blocks), dim3(threads), 0, stream, x, packed, y, M, N, K);
-  QVEX_CHECK_LAUNCH("qvex_qmv_w4g64_packed");
+  QVEX_CHECK_LAUNCH(fn_name);
+  return QVEX_OK;
+}
+
+int pack(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int N, int K, void* packed,
+         uint64_t packed_bytes, int swiglu, hipStream_t stream) {
+  const char* fn_name = swiglu ? "qvex_w4g64_pack_swiglu" : "qvex_w4g64_pack";
+  QVEX_CHECK_ARG(w && scales && biases && packed, "%s: null pointer", fn_name);
+  QVEX_CHECK_ARG(N >= 1 && K >= PK_SET && K % PK_SET == 0, "%s: N=%d K=%d (K must be a positive multiple of 256)",
+                 fn_name, N, K);
+  QVEX_CHECK_ARG(!swiglu || (N % 16 == 0), "%s: N=%d must be a multiple of 16", fn_name, N);
+  const uint64_t need = (uint64_t)((N + PK_TILE - 1) / PK_TILE) * (uint64_t)(K / PK_SET) * PK_RECORD;
+  QVEX_CHECK_ARG(packed_bytes >= need, "%s: packed buffer %llu < %llu bytes", fn_name,
+                 (unsigned long long)packed_bytes, (unsigned long long)need);
+  QVEX_CHECK_ARG(qvex_aligned(packed, 16) && qvex_aligned(w, 4) && qvex_aligned(scales, 2) && qvex_aligned(biases, 2),
+                 "%s: packed must be 16-byte aligned", fn_name);
+  const long records = (long)((N + PK_TILE - 1) / PK_TILE) * (K / PK_SET);
+  QVEX_CHECK_ARG(records <= 0x7fffffffL, "%s: too many records", fn_name);
+  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)records), dim3(64), 0, stream, w, scales, biases, N, K, swiglu,
+                     (uint8_t*)packed);
+  QVEX_CHECK_LAUNCH(fn_name);
   return QVEX_OK;
 }
 
@@ -283,30 +345,30 @@ extern "C" uint64_t qvex_w4g64_packed_bytes(int N, int K) {
 
 extern "C" int qvex_w4g64_pack(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int N, int K,
                                void* packed, uint64_t packed_bytes, void* stream) {
-  QVEX_CHECK_ARG(w && scales && biases && packed, "qvex_w4g64_pack: null pointer");
-  QVEX_CHECK_ARG(N >= 1 && K >= PK_SET && K % PK_SET == 0,
-                 "qvex_w4g64_pack: N=%d K=%d (K must be a positive multiple of 256)", N, K);
-  const uint64_t need = qvex_w4g64_packed_bytes(N, K);
-  QVEX_CHECK_ARG(packed_bytes >= need, "qvex_w4g64_pack: packed buffer %llu < %llu bytes",
-                 (unsigned long long)packed_bytes, (unsigned long long)need);
-  QVEX_CHECK_ARG(qvex_aligned(packed, 16) && qvex_aligned(w, 4) && qvex_aligned(scales, 2) && qvex_aligned(biases, 2),
-                 "qvex_w4g64_pack: packed must be 16-byte aligned");
-  const long records = (long)((N + PK_TILE - 1) / PK_TILE) * (K / PK_SET);
-  QVEX_CHECK_ARG(records <= 0x7fffffffL, "qvex_w4g64_pack: too many records");
-  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)records), dim3(64), 0, (hipStream_t)stream, w, scales, biases, N, K,
-                     (uint8_t*)packed);
-  QVEX_CHECK_LAUNCH("qvex_w4g64_pack");
-  return QVEX_OK;
+  return pack(w, scales, biases, N, K, packed, packed_bytes, 0, (hipStream_t)stream);
+}
+
+extern "C" int qvex_w4g64_pack_swiglu(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int N,
+                                      int K, void* packed, uint64_t packed_bytes, void* stream) {
+  return pack(w, scales, biases, N, K, packed, packed_bytes, 1, (hipStream_t)stream);
 }
 
 extern "C" int qvex_qmv_w4g64_packed(const uint16_t* x, const void* packed, uint16_t* y, int M, int N, int K,
                                      void* stream) {
   int TN = 1, WS = 1;
   if (N >= 1 && K >= PK_SET) packed_default_tile(N, K, &TN, &WS);
-  return launch_packed(x, (const uint8_t*)packed, y, M, N, K, TN, WS, (hipStream_t)stream);
+  return launch_packed(x, (const uint8_t*)packed, y, M, N, K, TN, WS, false, (hipStream_t)stream);
 }
 
 extern "C" int qvex_qmv_w4g64_packed_tiled(const uint16_t* x, const void* packed, uint16_t* y, int M, int N, int K,
                                            int tiles_per_wave, int wave_ksplit, void* stream) {
-  return launch_packed(x, (const uint8_t*)packed, y, M, N, K, tiles_per_wave, wave_ksplit, (hipStream_t)stream);
+  return launch_packed(x, (const uint8_t*)packed, y, M, N, K, tiles_per_wave, wave_ksplit, false,
+                       (hipStream_t)stream);
+}
+
+extern "C" int qvex_qmv_w4g64_packed_swiglu(const uint16_t* x, const void* packed, uint16_t* y, int M, int N, int K,
+                                            void* stream) {
+  int TN = 1, WS = 1;
+  if (N >= 1 && K >= PK_SET) packed_default_tile(N, K, &TN, &WS);
+  return launch_packed(x, (const uint8_t*)packed, y, M, N, K, TN, WS, true, (hipStream_t)stream);
 }

@@ -26,6 +26,8 @@ SIGNATURES: dict[str, list] = {
     "qvex_w4g64_pack": [P, P, P, I, I, P, U64, P],
     "qvex_qmv_w4g64_packed": [P, P, P, I, I, I, P],
     "qvex_qmv_w4g64_packed_tiled": [P, P, P, I, I, I, I, I, P],
+    "qvex_w4g64_pack_swiglu": [P, P, P, I, I, P, U64, P],
+    "qvex_qmv_w4g64_packed_swiglu": [P, P, P, I, I, I, P],
     "qvex_gdn_recurrent": [P, P, P, P, P, P, P, P, P, I, P, I, I, I, I, I, I, P],
     "qvex_gdn_recurrent_ring": [P, P, P, P, P, P, P, P, I, P, I, P, I, I, I, I, I, I, P],
     "qvex_gdn_chunked": [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P, U64, P],

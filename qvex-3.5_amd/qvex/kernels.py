@@ -81,9 +81,11 @@ def qmv_multi(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: to
     return quantized_matmul(x, w, scales, biases)
 
 
-def pack_w4(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) -> torch.Tensor:
+def pack_w4(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, swiglu: bool = False) -> torch.Tensor:
     """Tile-packed copy of a QLinear triplet (engine/model.py:83-85) for
-    quantized_matmul_packed: uint8 [ceil(N/16) * K/256 * 2304]. K % 256 == 0."""
+    quantized_matmul_packed: uint8 [ceil(N/16) * K/256 * 2304]. K % 256 == 0.
+    swiglu=True packs a fused gate/up weight (gate rows first) with the gate/up
+    interleave that quantized_matmul_packed(..., swiglu=True) expects."""
     _check(w, "w", torch.int32, 2)
     _check(scales, "scales", torch.bfloat16, 2)
     _check(biases, "biases", torch.bfloat16, 2)
@@ -94,14 +96,17 @@ def pack_w4(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) -> torc
     if nbytes == 0:
         raise _C.QvexError(f"pack_w4: K={K} is not a positive multiple of 256")
     packed = torch.empty(nbytes, dtype=torch.uint8, device=w.device)
-    _C.call("qvex_w4g64_pack", _ptr(w), _ptr(scales), _ptr(biases), N, K, _ptr(packed), nbytes, _stream())
+    _C.call("qvex_w4g64_pack_swiglu" if swiglu else "qvex_w4g64_pack", _ptr(w), _ptr(scales), _ptr(biases),
+            N, K, _ptr(packed), nbytes, _stream())
     return packed
 
 
 def quantized_matmul_packed(x: torch.Tensor, packed: torch.Tensor, N: int, out: torch.Tensor | None = None,
-                            tile: tuple[int, int] | None = None) -> torch.Tensor:
+                            tile: tuple[int, int] | None = None, swiglu: bool = False) -> torch.Tensor:
     """y = x @ dequant(W)^T from pack_w4's copy, x bf16 [..., K] with 1..4 rows
-    (the product of mx.quantized_matmul in QLinear.__call__, engine/model.py:87-91)."""
+    (the product of mx.quantized_matmul in QLinear.__call__, engine/model.py:87-91).
+    swiglu=True (weight packed with swiglu=True): y [..., N/2] = silu(gate) * up
+    (_swiglu, engine/model.py:134-135)."""
     K = x.shape[-1]
     x2 = x.reshape(-1, K)
     M = x2.shape[0]
@@ -110,12 +115,17 @@ def quantized_matmul_packed(x: torch.Tensor, packed: torch.Tensor, N: int, out: 
         raise _C.QvexError("packed must be a contiguous uint8 tensor on the device of x")
     if packed.numel() != int(_C.lib().qvex_w4g64_packed_bytes(N, K)):
         raise _C.QvexError(f"packed has {packed.numel()} bytes, not the size of an N={N} K={K} pack")
+    NO = N // 2 if swiglu else N
     if out is None:
-        out = torch.empty((*x.shape[:-1], N), dtype=torch.bfloat16, device=x.device)
+        out = torch.empty((*x.shape[:-1], NO), dtype=torch.bfloat16, device=x.device)
     _check(out, "out", torch.bfloat16)
-    if out.numel() != M * N:
+    if out.numel() != M * NO:
         raise _C.QvexError("out has the wrong size")
-    if tile is None:
+    if swiglu:
+        if tile is not None:
+            raise _C.QvexError("the SwiGLU form picks its own tile")
+        _C.call("qvex_qmv_w4g64_packed_swiglu", _ptr(x2), _ptr(packed), _ptr(out), M, N, K, _stream())
+    elif tile is None:
         _C.call("qvex_qmv_w4g64_packed", _ptr(x2), _ptr(packed), _ptr(out), M, N, K, _stream())
     else:
         _C.call("qvex_qmv_w4g64_packed_tiled", _ptr(x2), _ptr(packed), _ptr(out), M, N, K,

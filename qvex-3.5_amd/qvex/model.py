@@ -127,19 +127,36 @@ class QLinear:
 
     PACKED_MAX_ROWS = 4
 
-    def __init__(self, w, scales, biases, group_size=64, bits=4, pack: bool = True):
+    def __init__(self, w, scales, biases, group_size=64, bits=4, pack: bool = True, swiglu: bool = False):
         if group_size != 64 or bits != 4:
             raise _C.QvexError(f"QLinear: only 4-bit group-64 weights are implemented (got {bits}/{group_size})")
         self.w, self.scales, self.biases = w, scales, biases
         self.group_size, self.bits = group_size, bits
         self.N = w.shape[0]
         self.K = w.shape[1] * 8
-        self.packed = kernels.pack_w4(w, scales, biases) if pack and self.K % 256 == 0 else None
+        # swiglu: a fused [gate; up] weight whose packed copy carries the gate/up
+        # interleave; its 1..4-row calls go through swiglu() (SwiGLU fused in)
+        self.swiglu_packed = swiglu and self.N % 16 == 0
+        self.packed = None
+        if pack and self.K % 256 == 0:
+            self.packed = kernels.pack_w4(w, scales, biases, swiglu=self.swiglu_packed)
 
     def repack(self) -> None:
         """Rebuild the packed copy after the MLX-layout tensors were edited in place."""
         if self.packed is not None:
-            self.packed = kernels.pack_w4(self.w, self.scales, self.biases)
+            self.packed = kernels.pack_w4(self.w, self.scales, self.biases, swiglu=self.swiglu_packed)
+
+    def swiglu(self, x: torch.Tensor) -> torch.Tensor:
+        """silu(x W_gate^T) * (x W_up^T) for a fused [gate; up] layer
+        (_swiglu over the split halves, engine/model.py:134-135, 302)."""
+        x2 = x.reshape(-1, self.K)
+        M, I = x2.shape[0], self.N // 2
+        if self.swiglu_packed and self.packed is not None and M <= self.PACKED_MAX_ROWS:
+            return kernels.quantized_matmul_packed(x2, self.packed, self.N, swiglu=True)
+        gu = self(x2)
+        h = torch.empty((M, I), dtype=torch.bfloat16, device=x.device)
+        _C.call("qvex_swiglu", _ptr(gu), _ptr(h), M, I, _stream())
+        return h
 
     def __call__(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         lead = x.shape[:-1]
@@ -148,7 +165,7 @@ class QLinear:
         if out is None:
             out = torch.empty((M, self.N), dtype=torch.bfloat16, device=x.device)
         o2 = out.view(M, self.N)
-        if self.packed is not None and M <= self.PACKED_MAX_ROWS:
+        if self.packed is not None and not self.swiglu_packed and M <= self.PACKED_MAX_ROWS:
             kernels.quantized_matmul_packed(x2, self.packed, self.N, out=o2)
             return out.view(*lead, self.N)
         for m0 in range(0, M, QMV_MAX_ROWS):
@@ -157,13 +174,13 @@ class QLinear:
         return out.view(*lead, self.N)
 
     @staticmethod
-    def fuse(layers: list["QLinear"]) -> "QLinear":
+    def fuse(layers: list["QLinear"], swiglu: bool = False) -> "QLinear":
         """Stack output rows of layers sharing the input (lossless, engine/model.py:93-104)."""
         l0 = layers[0]
         assert all((l.group_size, l.bits) == (l0.group_size, l0.bits) for l in layers), \
             "fused layers must share the quantization (bits, group size)"
         return QLinear(torch.cat([l.w for l in layers]), torch.cat([l.scales for l in layers]),
-                       torch.cat([l.biases for l in layers]), l0.group_size, l0.bits)
+                       torch.cat([l.biases for l in layers]), l0.group_size, l0.bits, swiglu=swiglu)
 
 
 class QEmbedding:
@@ -409,17 +426,16 @@ class GatedDeltaNet:
 
 
 class MLP:
+    """down(silu(gate(x)) * up(x)) (engine/model.py:294-302); for 1..4 rows the
+    SwiGLU is fused into the gate/up product."""
+
     def __init__(self, p: dict):
-        self.gate_up = QLinear.fuse([p["gate_proj"], p["up_proj"]])
+        self.gate_up = QLinear.fuse([p["gate_proj"], p["up_proj"]], swiglu=True)
         self.down = p["down_proj"]
         self.hidden = p["gate_proj"].N
 
     def __call__(self, x):
-        gu = self.gate_up(x)
-        L = gu.shape[0]
-        h = torch.empty((L, self.hidden), dtype=torch.bfloat16, device=x.device)
-        _C.call("qvex_swiglu", _ptr(gu), _ptr(h), L, self.hidden, _stream())
-        return self.down(h)
+        return self.down(self.gate_up.swiglu(x))
 
 
 class Layer:

@@ -87,3 +87,12 @@ def test_packed_bytes_and_rejections():
         _C.call("qvex_qmv_w4g64_packed_tiled", p16, p16, p16, 1, 16, 256, 3, 1, None)
     with pytest.raises(_C.QvexError, match="packed buffer"):
         _C.call("qvex_w4g64_pack", p16, p16, p16, 16, 256, p16, 2303, None)
+
+
+def test_packed_swiglu_rejects_odd_halves():
+    buf = ctypes.create_string_buffer(1 << 16)
+    p16 = (ctypes.addressof(buf) + 15) // 16 * 16
+    with pytest.raises(_C.QvexError, match="multiple of 16"):
+        _C.call("qvex_qmv_w4g64_packed_swiglu", p16, p16, p16, 1, 24, 256, None)
+    with pytest.raises(_C.QvexError, match="multiple of 16"):
+        _C.call("qvex_w4g64_pack_swiglu", p16, p16, p16, 24, 256, p16, 1 << 15, None)

@@ -76,3 +76,22 @@ def test_packed_matches_mlx_layout_kernel_closely():
     a = synth.bf16_to_f32(run_packed(x, w, s, b)).astype(np.float64)
     c = synth.bf16_to_f32(run(x, w, s, b)).astype(np.float64)
     assert np.abs(a - c).max() <= 2.0 ** -7 * np.abs(c).max()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("N,K", [(24576, 4096), (48, 512), (4096, 256)])
+def test_packed_swiglu_equals_product_then_swiglu(M, N, K):
+    """The fused SwiGLU epilogue gives the same bits as the packed product followed by
+    qvex_swiglu (_swiglu of engine/model.py:134-135 on the two bf16 halves)."""
+    from qvex import _C
+    from qvex.kernels import _ptr, _stream
+    w, s, b = synth.qmv_weights(N, K, seed=35, tag=N)
+    x = to_dev(synth.qmv_x(M, K, seed=35, tag=M), torch.bfloat16)
+    wd, sd, bd = to_dev(w, torch.int32), to_dev(s, torch.bfloat16), to_dev(b, torch.bfloat16)
+    gu = kernels.quantized_matmul_packed(x, kernels.pack_w4(wd, sd, bd), N)
+    ref = torch.empty((M, N // 2), dtype=torch.bfloat16, device="cuda:0")
+    _C.call("qvex_swiglu", _ptr(gu), _ptr(ref), M, N // 2, _stream())
+    got = kernels.quantized_matmul_packed(x, kernels.pack_w4(wd, sd, bd, swiglu=True), N, swiglu=True)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
