@@ -11,6 +11,7 @@
 // GDN conv input window [3 + T, C] is kept per call so that the conv state
 // after L accepted tokens is rows L..L+2 of it (a pointer pick on rollback).
 #include "qvex_common.h"
+#include "rms_row.h"
 
 #include <math.h>
 
@@ -52,32 +53,8 @@ __global__ __launch_bounds__(256) void embed_kernel(const int32_t* __restrict__ 
 
 // ---------------------------------------------------------------- RMSNorm family
 //
-// One 256-thread block per row; thread t holds the 8-element chunks t, t+256,
-// ... of the row in registers (16-byte loads), so the row is read once and the
-// reduction is one wave butterfly plus 4 LDS slots.
-// y = w * (x * rsqrt(mean(x^2) + eps)) * scale (w optional); with ADD the row is
+// One 256-thread block per row (rms_row256 in rms_row.h); with ADD the row is
 // first h = bf16(x + delta), stored, and normalised.
-constexpr int RMS_MAXC = 4;   // chunks of 8 per thread: D <= 8192
-
-__device__ __forceinline__ void unpack8(const u32x4 v, float* f) {
-  f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x); f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
-  f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
-}
-
-__device__ __forceinline__ u32x4 pack8(const float* f) {
-  u32x4 v;
-  v.x = pack_bf16x2(f[0], f[1]); v.y = pack_bf16x2(f[2], f[3]);
-  v.z = pack_bf16x2(f[4], f[5]); v.w = pack_bf16x2(f[6], f[7]);
-  return v;
-}
-
-__device__ __forceinline__ float block_allsum256(float v, float* red) {
-  v = wave_allsum(v);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return (red[0] + red[1]) + (red[2] + red[3]);
-}
-
 template <bool ADD>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x, long x_stride,
                                                       const uint16_t* __restrict__ delta, long d_stride,
@@ -86,45 +63,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
                                                       long o_stride, int R, int D, float eps, float scale) {
   __shared__ float red[4];
   const int row = blockIdx.x;
-  const int t = threadIdx.x;
-  const uint16_t* xr = x + row * x_stride;
-  float v[RMS_MAXC][8];
-  float ss = 0.0f;
-#pragma unroll
-  for (int c = 0; c < RMS_MAXC; ++c) {
-    const int i = (t + 256 * c) * 8;
-    if (i < D) {
-      unpack8(load16(xr + i), v[c]);
-      if constexpr (ADD) {
-        float d[8];
-        unpack8(load16(delta + row * d_stride + i), d);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[c][e] = bf16_to_f32(f32_to_bf16(v[c][e] + d[e]));
-        *reinterpret_cast<u32x4*>(h_out + row * h_stride + i) = pack8(v[c]);
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss = fmaf(v[c][e], v[c][e], ss);
-    }
-  }
-  ss = block_allsum256(ss, red);
-  const float inv = rsqrtf(ss / (float)D + eps);
-#pragma unroll
-  for (int c = 0; c < RMS_MAXC; ++c) {
-    const int i = (t + 256 * c) * 8;
-    if (i < D) {
-      float o[8];
-      if (w) {
-        float wf[8];
-        unpack8(load16(w + i), wf);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = wf[e] * (v[c][e] * inv) * scale;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = (v[c][e] * inv) * scale;
-      }
-      *reinterpret_cast<u32x4*>(out + row * o_stride + i) = pack8(o);
-    }
-  }
+  rms_row256<ADD>(x + row * x_stride, ADD ? delta + row * d_stride : nullptr, ADD ? h_out + row * h_stride : nullptr,
+                  w, out + row * o_stride, D, eps, scale, red);
 }
 
 // ---------------------------------------------------------------- GDN: conv1d + SiLU + q/k norm
