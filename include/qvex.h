@@ -184,6 +184,21 @@ int qvex_spec_accept(const float* target, const float* draft, const int32_t* dra
                      int32_t* n_accept, int32_t* out_token, int S, int k, int V,
                      void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* The same with the target rows filtered as Sampler.scores
+ * (engine/sampler.py:30-52): presence penalty x - penalty * s(j), s(j) = 1 for
+ * the tokens of `seen` (fp32 [V], 0/1, or NULL) and, in verify row i, for the
+ * drafts d_0..d_{i-1}; when sampling, top-k (1..64; 0 = off) and top-p
+ * (0 < top_p < 1, applied over the top-k values; top-p without top-k is not
+ * implemented and returns QVEX_ENOTSUP). Greedy scores are only penalised.
+ * Draft logits, when given, are not filtered. Ties at the cutoff are all kept.
+ * workspace: qvex_spec_accept_filtered_workspace_bytes(S, k, V, has_draft, top_k). */
+uint64_t qvex_spec_accept_filtered_workspace_bytes(int S, int k, int V, int has_draft, int top_k);
+int qvex_spec_accept_filtered(const float* target, const float* draft, const int32_t* draft_ids,
+                              const float* u_accept, const float* u_sample, float inv_temp,
+                              const float* seen, float presence_penalty, int top_k, float top_p,
+                              int32_t* n_accept, int32_t* out_token, int S, int k, int V,
+                              void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Verify-forward glue (Qwen3.5 hybrid stack, engine/model.py). bf16 storage,
  * fp32 arithmetic, one bf16 rounding per output.
@@ -287,6 +302,13 @@ int qvex_cycle_finish(const int32_t* drafts, int k, const int32_t* n_accept, con
  * uniforms from a pre-drawn table). */
 int qvex_next_uniforms(const float* table, int rows, int width, int32_t* counter, float* out,
                        void* stream);
+
+/* Presence tracking (Sampler.observe, engine/sampler.py:60-62): seen[ids[q]] = 1
+ * for q < min(max_ids, (n_ptr ? *n_ptr : 0) + n_offset); ids outside [0, V) are
+ * skipped. With n_ptr = the cycle result [n, token, drafts...] and
+ * ids = result + 1, n_offset = 1 it marks the token and the n accepted drafts. */
+int qvex_mark_seen(float* seen, int V, const int32_t* ids, int max_ids, const int32_t* n_ptr,
+                   int n_offset, void* stream);
 
 /* Pure streaming read of `bytes` bytes (multiple of 16) from `buf`, folding
  * them into `sink` (64 uint32 words). Measures the achievable HBM read rate;

@@ -61,10 +61,11 @@ def lib() -> ctypes.CDLL:
         L.orc_gated_delta_f64.argtypes = [P] * 10 + [I] * 6
         L.orc_gated_delta_f32.argtypes = [P] * 10 + [I] * 7
         L.orc_spec_accept.argtypes = [P, P, P, P, P, F, P, P, I, I, I, I]
+        L.orc_spec_accept_filtered.argtypes = [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, I]
         L.orc_expf.argtypes = [F]
         L.orc_expf.restype = F
         for fn in ("orc_qmv_w4g64_f64", "orc_qmv_w4g64_f32", "orc_gated_delta_f64",
-                   "orc_gated_delta_f32", "orc_spec_accept"):
+                   "orc_gated_delta_f32", "orc_spec_accept", "orc_spec_accept_filtered"):
             getattr(L, fn).restype = None
         _lib = L
     return _lib
@@ -185,10 +186,13 @@ def gated_delta_f32(q, k, v, a, b, A_log, dt_bias, state, snaps=False, threads=1
 
 # ---------------------------------------------------------------- speculative acceptance
 
-def spec_accept(target, draft, draft_ids, u_accept, u_sample, inv_temp, threads=1):
+def spec_accept(target, draft, draft_ids, u_accept, u_sample, inv_temp, threads=1, seen=None,
+                presence_penalty=0.0, top_k=0, top_p=1.0):
     """Bit-exact fp32 emulation of the fused acceptance kernel (see oracle/spec.c).
     target [S,k+1,V] fp32, draft [S,k,V] fp32 or None (one-hot greedy draft),
     draft_ids [S,k] int32, u_accept [S,k], u_sample [S]; inv_temp <= 0 = greedy.
+    seen [V] fp32 (0/1) or None, presence_penalty, top_k (0..64), top_p: the
+    target rows are filtered as Sampler.scores (engine/sampler.py:30-52).
     Returns (n_accept [S] int32, out_token [S] int32)."""
     target = np.ascontiguousarray(target, np.float32)
     S, k1, V = target.shape
@@ -199,10 +203,13 @@ def spec_accept(target, draft, draft_ids, u_accept, u_sample, inv_temp, threads=
     draft_ids = np.ascontiguousarray(draft_ids, np.int32).reshape(S, k)
     u_accept = np.ascontiguousarray(u_accept, np.float32).reshape(S, k)
     u_sample = np.ascontiguousarray(u_sample, np.float32).reshape(S)
+    if seen is not None:
+        seen = np.ascontiguousarray(seen, np.float32).reshape(V)
     n = np.empty(S, np.int32)
     tok = np.empty(S, np.int32)
-    lib().orc_spec_accept(_p(target), _p(draft), _p(draft_ids), _p(u_accept), _p(u_sample),
-                          float(np.float32(inv_temp)), _p(n), _p(tok), S, k, V, threads)
+    lib().orc_spec_accept_filtered(_p(target), _p(draft), _p(draft_ids), _p(u_accept), _p(u_sample),
+                                   float(np.float32(inv_temp)), _p(seen), float(np.float32(presence_penalty)),
+                                   int(top_k), float(np.float32(top_p)), _p(n), _p(tok), S, k, V, threads)
     return n, tok
 
 

@@ -46,6 +46,13 @@ void orc_spec_accept(const float* target, const float* draft, const int32_t* dra
                      const float* u_accept, const float* u_sample, float temperature,
                      int32_t* n_accept, int32_t* out_token, int S, int k, int V, int threads);
 
+/* The same with the target rows filtered as Sampler.scores (presence penalty
+ * with `seen` [V] or NULL, top_k in 0..64, top_p; see spec.c). */
+void orc_spec_accept_filtered(const float* target, const float* draft, const int32_t* draft_ids,
+                              const float* u_accept, const float* u_sample, float inv_temp, const float* seen,
+                              float presence_penalty, int top_k, float top_p, int32_t* n_accept,
+                              int32_t* out_token, int S, int k, int V, int threads);
+
 /* exp used by the sampler on both sides (Cody-Waite reduction + Taylor, fmaf). */
 float orc_expf(float x);
 

@@ -18,6 +18,21 @@
  * Greedy (reference sampler.greedy, engine/speculative.py:75-77): accept iff
  * argmax(target_i) == d_i (first maximal index), token = argmax of row n.
  *
+ * Filtering of the target rows (Sampler.scores, engine/sampler.py:30-52):
+ *   presence penalty: x' = x - penalty * s(j), s(j) = 1 for the tokens of
+ *     `seen` and, in verify row i, for the drafts d_0..d_{i-1} that precede it
+ *     (the reference's extra_seen=draft for its bonus row), else seen[j];
+ *   greedy scores are x' (argmax as above); otherwise z = x' * inv_temp;
+ *   top-k (1 <= top_k <= 64): c_0 >= ... >= c_{K-1}, the K largest z (with
+ *     multiplicity); cutoff = c_{K-1};
+ *   top-p (0 < top_p < 1, needs top_k): e_i = exp(c_i - c_0), S = sum e_i in
+ *     order, p_i = e_i / S, running inclusive sums r_i, keep i iff
+ *     (r_i - p_i) < top_p (mx.cumsum(probs) - probs < top_p); cutoff = min kept c_i;
+ *   kept set: z >= cutoff; p(j) = exp(z_j - c_0) / S_p on the kept set with
+ *     S_p = sum_{i: c_i > cutoff} exp(c_i - c_0) + n_eq * exp(cutoff - c_0),
+ *     n_eq = number of tokens of the row with z == cutoff.
+ * Draft rows (draft logits) are never filtered.
+ *
  * Reduction order (shared with the kernel): a row is cut into parts of 8192;
  * in a part, logical thread t (0..255) owns elements
  *   base + 4*(t + 256*i) + e,  i = 0..7, e = 0..3  (in that order),
@@ -89,16 +104,81 @@ static float block_sum(const float* tsum) {
   return ((w[0] + w[1]) + w[2]) + w[3];
 }
 
-typedef struct { float m, s; } rowstat;
+typedef struct { float m, s, cutoff; } rowstat;
 
-static rowstat row_stats(const float* row, int V, float inv_temp) {
+/* sampling-side filter of a target row: penalty inputs and the tokens that
+ * count as seen in this row in addition to `seen` */
+typedef struct {
+  const float* seen; /* [V] or NULL */
+  float pen;
+  const int32_t* extra; /* drafts d_0 .. d_{n_extra-1} */
+  int n_extra;
+} pfilt;
+
+/* penalised logit x - pen * s(j) (no subtraction at all without a penalty) */
+static inline float pen_logit(const float* row, int j, const pfilt* f) {
+  const float x = row[j];
+  if (!f || (!f->seen && f->n_extra == 0) || f->pen == 0.0f) return x;
+  float sj = f->seen ? f->seen[j] : 0.0f;
+  for (int q = 0; q < f->n_extra; ++q)
+    if (f->extra[q] == j) sj = 1.0f;
+  return x - f->pen * sj;
+}
+
+static int cmp_desc(const void* a, const void* b) {
+  const float x = *(const float*)a, y = *(const float*)b;
+  return (x < y) - (x > y);
+}
+
+/* filtered statistics of a target row (top_k >= 1): m = c_0, s = S_p, cutoff */
+static rowstat filtered_stats(const float* row, int V, float inv_temp, const pfilt* f, int top_k, float top_p) {
+  float* z = (float*)malloc(sizeof(float) * (size_t)V);
+  for (int j = 0; j < V; ++j) z[j] = pen_logit(row, j, f) * inv_temp;
+  float* srt = (float*)malloc(sizeof(float) * (size_t)V);
+  memcpy(srt, z, sizeof(float) * (size_t)V);
+  qsort(srt, (size_t)V, sizeof(float), cmp_desc);
+  const int K = top_k;
+  const float c0 = srt[0];
+  float cutoff = srt[K - 1];
+  if (top_p > 0.0f && top_p < 1.0f) {
+    float e[64], S = 0.0f;
+    for (int i = 0; i < K; ++i) {
+      e[i] = orc_expf(srt[i] - c0);
+      S = S + e[i];
+    }
+    float run = 0.0f, mn = INFINITY;
+    for (int i = 0; i < K; ++i) {
+      const float pi = e[i] / S;
+      const float incl = run + pi;
+      if ((incl - pi) < top_p && srt[i] < mn) mn = srt[i];
+      run = incl;
+    }
+    cutoff = mn;
+  }
+  int n_gt = 0;
+  while (n_gt < K && srt[n_gt] > cutoff) ++n_gt;
+  int n_eq = 0;
+  for (int j = 0; j < V; ++j) n_eq += (z[j] == cutoff);
+  float S = 0.0f;
+  for (int i = 0; i < n_gt; ++i) S = S + orc_expf(srt[i] - c0);
+  S = S + (float)n_eq * orc_expf(cutoff - c0);
+  free(z);
+  free(srt);
+  rowstat r;
+  r.m = c0;
+  r.s = S;
+  r.cutoff = cutoff;
+  return r;
+}
+
+static rowstat row_stats(const float* row, int V, float inv_temp, const pfilt* f) {
   const int P = nparts(V);
   float mp[4096], sp[4096];
   for (int p = 0; p < P; ++p) {
     float m = -INFINITY;
     const int b0 = p * PART, e0 = (p + 1) * PART < V ? (p + 1) * PART : V;
     for (int j = b0; j < e0; ++j) {
-      const float z = row[j] * inv_temp;
+      const float z = pen_logit(row, j, f) * inv_temp;
       if (z > m) m = z;
     }
     float ts[NT];
@@ -108,7 +188,7 @@ static rowstat row_stats(const float* row, int V, float inv_temp) {
         for (int s = 0; s < 4 * NI; ++s) {
           const int j = elem(V, p, t, s);
           if (j < 0) break;
-          acc = acc + orc_expf(row[j] * inv_temp - m);
+          acc = acc + orc_expf(pen_logit(row, j, f) * inv_temp - m);
         }
       ts[t] = acc;
     }
@@ -123,18 +203,21 @@ static rowstat row_stats(const float* row, int V, float inv_temp) {
   for (int p = 0; p < P; ++p) s = s + sp[p] * orc_expf(mp[p] - m);
   r.m = m;
   r.s = s;
+  r.cutoff = -INFINITY;
   return r;
 }
 
-/* first index of the maximum of row (greedy) */
-static int row_argmax(const float* row, int V) {
+/* first index of the maximum of the (penalised) row (greedy) */
+static int row_argmax(const float* row, int V, const pfilt* f) {
   int bj = 0;
-  float bv = row[0];
-  for (int j = 1; j < V; ++j)
-    if (row[j] > bv) {
-      bv = row[j];
+  float bv = pen_logit(row, 0, f);
+  for (int j = 1; j < V; ++j) {
+    const float v = pen_logit(row, j, f);
+    if (v > bv) {
+      bv = v;
       bj = j;
     }
+  }
   return bj;
 }
 
@@ -146,10 +229,12 @@ typedef struct {
   int mode;        /* 0 = residual, 1 = plain p */
   float inv_temp;
   rowstat sp, sq;
+  const pfilt* f;  /* penalty of the target row */
 } wctx;
 
 static inline float weight(const wctx* c, int j) {
-  const float ep = orc_expf(c->tp[j] * c->inv_temp - c->sp.m);
+  const float z = pen_logit(c->tp, j, c->f) * c->inv_temp;
+  const float ep = z >= c->sp.cutoff ? orc_expf(z - c->sp.m) : 0.0f;
   if (c->mode == 1) return ep;
   float eq, Sq;
   if (c->tq) {
@@ -231,31 +316,42 @@ static int sample(const wctx* c, int V, float u) {
   return result;
 }
 
-void orc_spec_accept(const float* target, const float* draft, const int32_t* draft_ids,
-                     const float* u_accept, const float* u_sample, float inv_temp,
-                     int32_t* n_accept, int32_t* out_token, int S, int k, int V, int threads) {
+void orc_spec_accept_filtered(const float* target, const float* draft, const int32_t* draft_ids,
+                              const float* u_accept, const float* u_sample, float inv_temp, const float* seen,
+                              float presence_penalty, int top_k, float top_p, int32_t* n_accept,
+                              int32_t* out_token, int S, int k, int V, int threads) {
   const int greedy = !(inv_temp > 0.0f);
 #pragma omp parallel for schedule(dynamic) num_threads(threads > 0 ? threads : 1)
   for (int st = 0; st < S; ++st) {
     const float* tgt = target + (size_t)st * (k + 1) * V;
     const float* drf = draft ? draft + (size_t)st * k * V : NULL;
     const int32_t* d = draft_ids + (size_t)st * k;
+    pfilt pf[65];
+    for (int i = 0; i <= k; ++i) {
+      pf[i].seen = seen;
+      pf[i].pen = presence_penalty;
+      pf[i].extra = d;
+      pf[i].n_extra = i;
+    }
     int n = k, tok = -1;
     if (greedy) {
       for (int i = 0; i < k; ++i) {
-        const int am = row_argmax(tgt + (size_t)i * V, V);
+        const int am = row_argmax(tgt + (size_t)i * V, V, &pf[i]);
         if (am != d[i]) { n = i; tok = am; break; }
       }
-      if (n == k) tok = row_argmax(tgt + (size_t)k * V, V);
+      if (n == k) tok = row_argmax(tgt + (size_t)k * V, V, &pf[k]);
     } else {
-      rowstat rp[64], rq[64];
-      for (int i = 0; i <= k; ++i) rp[i] = row_stats(tgt + (size_t)i * V, V, inv_temp);
+      rowstat rp[65], rq[64];
+      for (int i = 0; i <= k; ++i)
+        rp[i] = top_k > 0 ? filtered_stats(tgt + (size_t)i * V, V, inv_temp, &pf[i], top_k, top_p)
+                          : row_stats(tgt + (size_t)i * V, V, inv_temp, &pf[i]);
       if (drf)
-        for (int i = 0; i < k; ++i) rq[i] = row_stats(drf + (size_t)i * V, V, inv_temp);
+        for (int i = 0; i < k; ++i) rq[i] = row_stats(drf + (size_t)i * V, V, inv_temp, NULL);
       for (int i = 0; i < k; ++i) {
         const int di = d[i];
         if (di < 0 || di >= V) { n = i; break; } /* an out-of-range draft is rejected */
-        const float ep = orc_expf(tgt[(size_t)i * V + di] * inv_temp - rp[i].m);
+        const float zd = pen_logit(tgt + (size_t)i * V, di, &pf[i]) * inv_temp;
+        const float ep = zd >= rp[i].cutoff ? orc_expf(zd - rp[i].m) : 0.0f;
         float eq = 1.0f, Sq = 1.0f;
         if (drf) {
           eq = orc_expf(drf[(size_t)i * V + di] * inv_temp - rq[i].m);
@@ -268,6 +364,7 @@ void orc_spec_accept(const float* target, const float* draft, const int32_t* dra
       wctx c;
       c.inv_temp = inv_temp;
       c.sp = rp[n];
+      c.f = &pf[n];
       if (n < k) {
         c.tp = tgt + (size_t)n * V;
         c.tq = drf ? drf + (size_t)n * V : NULL;
@@ -290,4 +387,11 @@ void orc_spec_accept(const float* target, const float* draft, const int32_t* dra
     n_accept[st] = n;
     out_token[st] = tok;
   }
+}
+
+void orc_spec_accept(const float* target, const float* draft, const int32_t* draft_ids,
+                     const float* u_accept, const float* u_sample, float inv_temp,
+                     int32_t* n_accept, int32_t* out_token, int S, int k, int V, int threads) {
+  orc_spec_accept_filtered(target, draft, draft_ids, u_accept, u_sample, inv_temp, NULL, 0.0f, 0, 1.0f, n_accept,
+                           out_token, S, k, V, threads);
 }

@@ -53,7 +53,26 @@ __global__ void next_uniforms_kernel(const float* __restrict__ table, int rows, 
   if (i == 0) *counter += 1;
 }
 
+// seen[ids[q]] = 1 for q < min(max_ids, (n_ptr ? *n_ptr : 0) + n_offset); ids outside [0, V) skipped
+__global__ void mark_seen_kernel(float* __restrict__ seen, int V, const int32_t* __restrict__ ids, int max_ids,
+                                 const int32_t* __restrict__ n_ptr, int n_offset) {
+  const int cnt = min(max_ids, (n_ptr ? *n_ptr : 0) + n_offset);
+  for (int q = threadIdx.x; q < cnt; q += blockDim.x) {
+    const int id = ids[q];
+    if (id >= 0 && id < V) seen[id] = 1.0f;
+  }
+}
+
 }  // namespace
+
+extern "C" int qvex_mark_seen(float* seen, int V, const int32_t* ids, int max_ids, const int32_t* n_ptr,
+                              int n_offset, void* stream) {
+  QVEX_CHECK_ARG(seen && ids && V >= 1 && max_ids >= 0, "qvex_mark_seen: bad arguments");
+  hipLaunchKernelGGL(mark_seen_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, seen, V, ids, max_ids, n_ptr,
+                     n_offset);
+  QVEX_CHECK_LAUNCH("qvex_mark_seen");
+  return QVEX_OK;
+}
 
 extern "C" int qvex_gather_row(const uint16_t* src, long row_stride, const int32_t* idx, int rows, uint16_t* dst,
                                int H, void* stream) {

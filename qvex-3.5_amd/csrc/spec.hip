@@ -29,6 +29,16 @@
 // gathered elements and makes the sampling weights' thread and part sums over
 // the one or two rows the draw needs, every part in its own block.
 // Kernel 3 (one block per step) walks the stored sums to the drawn token.
+//
+// Filtering of the target rows (Sampler.scores, engine/sampler.py:30-52), when
+// asked for: presence penalty x - pen * s(j) with s(j) = 1 for `seen` tokens and,
+// in verify row i, for the drafts d_0..d_{i-1} before it; top-k (k <= 64) and
+// top-p over the k largest scaled values; everything outside z >= cutoff has
+// probability 0. Kernel 1 then also leaves each part's k largest values (taken
+// one block maximum at a time) and how many of its values equal the k-th; a
+// filter kernel (one block per verify row) merges them into the row's k largest,
+// applies top-p in order and counts the ties at the cutoff exactly, giving
+// (c_0, S_p, cutoff) for kernels 2 and 3, which only add the z >= cutoff test.
 #include "qvex_common.h"
 
 namespace {
@@ -96,11 +106,72 @@ struct SpecArgs {
   int32_t* out_token;     // [S]
   float* ws;              // [S * rps, P, 2]
   int S, k, V, P, rps;    // rps = rows per step
+  const float* seen;      // [V] presence mask or nullptr
+  float pen;              // presence penalty
+  int top_k;              // 0 = off
+  float top_p;            // top-p when 0 < top_p < 1 (needs top_k)
+  float* fws;             // [S * (k+1), P, top_k + 1] part lists + tie counts
+  float* frow;            // [S * (k+1), 4] (c_0, S_p, cutoff)
 };
 
 __device__ __forceinline__ const float* row_ptr(const SpecArgs& a, int step, int i) {
   if (i <= a.k) return a.target + ((long)step * (a.k + 1) + i) * a.V;
   return a.draft + ((long)step * a.k + (i - a.k - 1)) * a.V;
+}
+
+// Presence penalty of a target row at token j: x - pen * s(j), s(j) = 1 for the
+// n_extra drafts that precede the row, else seen[j]; no subtraction at all when
+// there is no penalty (so the unfiltered rule keeps its bits).
+__device__ __forceinline__ float pen_x(const float* seen, float pen, float x, int j, const int32_t* extra,
+                                       int n_extra) {
+  if (pen == 0.0f || (!seen && n_extra == 0)) return x;
+  float sj = seen ? seen[j] : 0.0f;
+  for (int q = 0; q < n_extra; ++q)
+    if (extra[q] == j) sj = 1.0f;
+  return x - pen * sj;
+}
+
+// The K largest of the block's values (with multiplicity) into lst[0..K-1],
+// descending: each round takes the block maximum once (ties: lowest wave, then
+// lowest lane; the winner only rescans its own NS values). get(s) gives the
+// calling thread's s-th value, -inf if it has none.
+template <int NS, typename Get>
+__device__ __forceinline__ void block_topk(Get get, int K, float* lst, float* wmax, int* wwin) {
+  uint32_t taken = 0;
+  float bv = -__builtin_inff();
+  int bs = -1;
+  auto rescan = [&]() {
+    bv = -__builtin_inff();
+    bs = -1;
+#pragma unroll
+    for (int q = 0; q < NS; ++q)
+      if (!((taken >> q) & 1u)) {
+        const float v = get(q);
+        if (v > bv) { bv = v; bs = q; }
+      }
+  };
+  rescan();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int r = 0; r < K; ++r) {
+    const float m = wave_allmax(bv);
+    const unsigned long long msk = __ballot(bv == m);
+    if (lane == 0) {
+      wmax[wave] = m;
+      wwin[wave] = __ffsll(msk) - 1;
+    }
+    __syncthreads();
+    float M = wmax[0];
+    int ww = 0;
+#pragma unroll
+    for (int q = 1; q < 4; ++q)
+      if (wmax[q] > M) { M = wmax[q]; ww = q; }
+    if (threadIdx.x == 0) lst[r] = M;
+    if ((int)threadIdx.x == ww * 64 + wwin[ww] && bs >= 0) {
+      taken |= 1u << bs;
+      rescan();
+    }
+    __syncthreads();
+  }
 }
 
 // ---------------------------------------------------------------- kernel 1: part statistics
@@ -129,6 +200,17 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
       x[it][2] = __uint_as_float(v.z);
       x[it][3] = __uint_as_float(v.w);
     }
+  }
+  const bool tgt = i <= a.k;
+  if (tgt && a.pen != 0.0f) {
+    const int32_t* extra = a.ids + (long)step * a.k;
+#pragma unroll
+    for (int it = 0; it < NI; ++it)
+      if (ok[it]) {
+        const int j = base + 4 * (t + NT * it);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[it][e] = pen_x(a.seen, a.pen, x[it][e], j + e, extra, i);
+      }
   }
   float* out = a.ws + ((long)row * a.P + p) * 2;
   if (a.greedy) {
@@ -181,6 +263,86 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
     out[0] = m;
     out[1] = s;
   }
+  if (tgt && a.top_k > 0) {
+    // this part's top_k largest z and the count of its values equal to the k-th
+    __shared__ float lst[64];
+    __shared__ float wmax[4];
+    __shared__ int wwin[4];
+    const int K = a.top_k;
+    block_topk<4 * NI>([&](int q) { return ok[q >> 2] ? z[q >> 2][q & 3] : -__builtin_inff(); }, K, lst, wmax,
+                       wwin);
+    const float vk = lst[K - 1];
+    float cnt = 0.0f;
+#pragma unroll
+    for (int it = 0; it < NI; ++it)
+      if (ok[it]) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cnt += (z[it][e] == vk) ? 1.0f : 0.0f;
+      }
+    cnt = block_sum(cnt, red);
+    float* L = a.fws + (((long)step * (a.k + 1) + i) * a.P + p) * (K + 1);
+    if (t < K) L[t] = lst[t];
+    if (t == 0) L[K] = cnt;
+  }
+}
+
+// ---------------------------------------------------------------- filter kernel (top-k / top-p)
+
+// One block per verify row: the row's top_k largest values from the parts'
+// lists, the top-p cutoff over them in order (exp(c_i - c_0) / S, running sums
+// r_i, keep iff r_i - p_i < top_p, cutoff = min kept c_i), and
+// S_p = sum_{c_i > cutoff} exp(c_i - c_0) + n_eq * exp(cutoff - c_0) with n_eq the
+// row's count of values equal to the cutoff: a part whose k-th value is the
+// cutoff contributes its tie count, any other part its list entries equal to it
+// (the cutoff is never below a part's k-th value).
+__global__ __launch_bounds__(NT) void spec_filter_kernel(SpecArgs a) {
+  __shared__ float vals[64 * 64];
+  __shared__ float lst[64];
+  __shared__ float wmax[4];
+  __shared__ int wwin[4];
+  const int row = blockIdx.x;           // step * (k + 1) + i
+  const int K = a.top_k, P = a.P;
+  const int n = P * K;
+  const float* L = a.fws + (long)row * P * (K + 1);
+  for (int q = threadIdx.x; q < n; q += NT) vals[q] = L[(q / K) * (K + 1) + q % K];
+  __syncthreads();
+  const int t = threadIdx.x;
+  block_topk<16>([&](int q) { const int v = t + NT * q; return v < n ? vals[v] : -__builtin_inff(); }, K, lst,
+                 wmax, wwin);
+  if (t == 0) {
+    const float c0 = lst[0];
+    float cutoff = lst[K - 1];
+    if (a.top_p > 0.0f && a.top_p < 1.0f) {
+      float Ssum = 0.0f;
+      for (int q = 0; q < K; ++q) Ssum = Ssum + qx_expf(lst[q] - c0);
+      float run = 0.0f, mn = __builtin_inff();
+      for (int q = 0; q < K; ++q) {
+        const float pi = qx_expf(lst[q] - c0) / Ssum;
+        const float incl = run + pi;
+        if ((incl - pi) < a.top_p && lst[q] < mn) mn = lst[q];
+        run = incl;
+      }
+      cutoff = mn;
+    }
+    int n_gt = 0;
+    while (n_gt < K && lst[n_gt] > cutoff) ++n_gt;
+    int n_eq = 0;
+    for (int q = 0; q < P; ++q) {
+      const float* Lp = L + (long)q * (K + 1);
+      if (cutoff == Lp[K - 1]) {
+        n_eq += (int)Lp[K];
+      } else {
+        for (int r = 0; r < K; ++r) n_eq += (Lp[r] == cutoff) ? 1 : 0;
+      }
+    }
+    float S = 0.0f;
+    for (int q = 0; q < n_gt; ++q) S = S + qx_expf(lst[q] - c0);
+    S = S + (float)n_eq * qx_expf(cutoff - c0);
+    float* fr = a.frow + (long)row * 4;
+    fr[0] = c0;
+    fr[1] = S;
+    fr[2] = cutoff;
+  }
 }
 
 // ---------------------------------------------------------------- kernel 2: accept + sample
@@ -191,10 +353,16 @@ struct WCtx {
   int d;
   int mode;   // 0 residual, 1 plain p
   float inv_temp, mp, sp, mq, sq;
+  float cutoff;             // -inf when the target row is not filtered
+  const float* seen;        // presence penalty of the target row
+  float pen;
+  const int32_t* extra;
+  int n_extra;
 };
 
 __device__ __forceinline__ float weight(const WCtx& c, int j) {
-  const float ep = qx_expf(c.tp[j] * c.inv_temp - c.mp);
+  const float z = pen_x(c.seen, c.pen, c.tp[j], j, c.extra, c.n_extra) * c.inv_temp;
+  const float ep = z >= c.cutoff ? qx_expf(z - c.mp) : 0.0f;
   if (c.mode == 1) return ep;
   float eq, Sq;
   if (c.tq) {
@@ -289,7 +457,7 @@ __device__ int sample_pass(const WCtx& c, int V, int P, float u, float* Tpt, flo
 struct SpecWs {
   float* T;     // [S][P][NT]
   float* W;     // [S][P]
-  float* dec;   // [S][8]: n, token (greedy), mp, sp, mq, sq
+  float* dec;   // [S][8]: n, draft id, mp, sp, mq, sq, cutoff
 };
 
 __device__ __forceinline__ SpecWs spec_ws(const SpecArgs& a) {
@@ -304,7 +472,7 @@ __device__ __forceinline__ SpecWs spec_ws(const SpecArgs& a) {
 // and runs the k accept tests (a few gathers), then block p makes the thread and
 // part sums of the sampling weights over part p of the sampling row.
 __global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
-  __shared__ float rm[80], rs[80];
+  __shared__ float rm[80], rs[80], rc[80];
   __shared__ float red[4];
   __shared__ int s_n, s_tok;
   const int p = blockIdx.x, step = blockIdx.y;
@@ -314,7 +482,13 @@ __global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
 
   if (t < a.rps) {
     const float* w = a.ws + ((long)step * a.rps + t) * a.P * 2;
-    if (a.greedy) {
+    rc[t] = -__builtin_inff();
+    if (!a.greedy && a.top_k > 0 && t <= k) {
+      const float* fr = a.frow + ((long)step * (k + 1) + t) * 4;
+      rm[t] = fr[0];
+      rs[t] = fr[1];
+      rc[t] = fr[2];
+    } else if (a.greedy) {
       float bv = w[0];
       int bj = __float_as_int(w[1]);
       for (int q = 1; q < a.P; ++q)
@@ -343,7 +517,8 @@ __global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
       for (int i = 0; i < k; ++i) {
         const int di = d[i];
         if (di < 0 || di >= a.V) { n = i; break; }
-        const float ep = qx_expf(row_ptr(a, step, i)[di] * a.inv_temp - rm[i]);
+        const float zd = pen_x(a.seen, a.pen, row_ptr(a, step, i)[di], di, d, i) * a.inv_temp;
+        const float ep = zd >= rc[i] ? qx_expf(zd - rm[i]) : 0.0f;
         float eq = 1.0f, Sq = 1.0f;
         if (a.draft) {
           eq = qx_expf(row_ptr(a, step, k + 1 + i)[di] * a.inv_temp - rm[k + 1 + i]);
@@ -371,6 +546,11 @@ __global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
   c.tp = row_ptr(a, step, n);
   c.mp = rm[n];
   c.sp = rs[n];
+  c.cutoff = rc[n];
+  c.seen = a.seen;
+  c.pen = a.pen;
+  c.extra = a.ids + (long)step * k;
+  c.n_extra = n;
   if (n < k) {
     c.tq = a.draft ? row_ptr(a, step, k + 1 + n) : nullptr;
     c.d = a.ids[(long)step * k + n];
@@ -403,6 +583,7 @@ __global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
       dd[0] = __int_as_float(n);
       dd[1] = __int_as_float(c.d);
       dd[2] = c.mp; dd[3] = c.sp; dd[4] = c.mq; dd[5] = c.sq;
+      dd[6] = c.cutoff;
     }
   }
 }
@@ -427,6 +608,11 @@ __global__ __launch_bounds__(NT) void spec_sample_kernel(SpecArgs a) {
   c.tp = row_ptr(a, step, n);
   c.d = __float_as_int(dd[1]);
   c.mp = dd[2]; c.sp = dd[3]; c.mq = dd[4]; c.sq = dd[5];
+  c.cutoff = dd[6];
+  c.seen = a.seen;
+  c.pen = a.pen;
+  c.extra = a.ids + (long)step * k;
+  c.n_extra = n;
   c.tq = (n < k && a.draft) ? row_ptr(a, step, k + 1 + n) : nullptr;
   c.mode = n < k ? 0 : 1;
   const float u = a.u_smp[step];
@@ -502,16 +688,27 @@ uint64_t ws_floats(int S, int rps, int P) {
   return (uint64_t)S * rps * P * 2 + (uint64_t)S * P * NT + (uint64_t)S * P + (uint64_t)S * 8;
 }
 
-extern "C" uint64_t qvex_spec_accept_workspace_bytes(int S, int k, int V, int has_draft) {
-  if (S < 1 || k < 0 || V < 1) return 0;
-  const int rps = (k + 1) + (has_draft ? k : 0);
-  return ws_floats(S, rps, nparts(V)) * sizeof(float);
+uint64_t filter_floats(int S, int k, int P, int top_k) {
+  if (top_k <= 0) return 0;
+  return (uint64_t)S * (k + 1) * P * (top_k + 1) + (uint64_t)S * (k + 1) * 4;
 }
 
-extern "C" int qvex_spec_accept(const float* target, const float* draft, const int32_t* draft_ids,
-                                const float* u_accept, const float* u_sample, float inv_temp,
-                                int32_t* n_accept, int32_t* out_token, int S, int k, int V,
-                                void* workspace, uint64_t workspace_bytes, void* stream) {
+extern "C" uint64_t qvex_spec_accept_filtered_workspace_bytes(int S, int k, int V, int has_draft, int top_k) {
+  if (S < 1 || k < 0 || V < 1 || top_k < 0) return 0;
+  const int rps = (k + 1) + (has_draft ? k : 0);
+  const int P = nparts(V);
+  return (ws_floats(S, rps, P) + filter_floats(S, k, P, top_k)) * sizeof(float);
+}
+
+extern "C" uint64_t qvex_spec_accept_workspace_bytes(int S, int k, int V, int has_draft) {
+  return qvex_spec_accept_filtered_workspace_bytes(S, k, V, has_draft, 0);
+}
+
+extern "C" int qvex_spec_accept_filtered(const float* target, const float* draft, const int32_t* draft_ids,
+                                         const float* u_accept, const float* u_sample, float inv_temp,
+                                         const float* seen, float presence_penalty, int top_k, float top_p,
+                                         int32_t* n_accept, int32_t* out_token, int S, int k, int V,
+                                         void* workspace, uint64_t workspace_bytes, void* stream) {
   QVEX_CHECK_ARG(S >= 1 && k >= 0 && k <= 32, "qvex_spec_accept: S=%d k=%d (need S >= 1, 0 <= k <= 32)", S, k);
   QVEX_CHECK_ARG(V >= 4 && V % 4 == 0, "qvex_spec_accept: V=%d must be a positive multiple of 4", V);
   QVEX_CHECK_ARG(target && n_accept && out_token && workspace, "qvex_spec_accept: null pointer");
@@ -520,20 +717,36 @@ extern "C" int qvex_spec_accept(const float* target, const float* draft, const i
                  "qvex_spec_accept: logits must be 16-byte aligned");
   const int greedy = !(inv_temp > 0.0f);
   QVEX_CHECK_ARG(greedy || u_sample, "qvex_spec_accept: u_sample required when sampling");
+  QVEX_CHECK_ARG(top_k >= 0 && top_k <= 64 && top_k <= V, "qvex_spec_accept: top_k=%d must be in 0..64 (and <= V)",
+                 top_k);
+  QVEX_CHECK_ARG(presence_penalty == presence_penalty, "qvex_spec_accept: presence_penalty is NaN");
+  const bool use_p = top_p > 0.0f && top_p < 1.0f;
+  if (!greedy && use_p && top_k == 0)
+    return qvex::fail(QVEX_ENOTSUP, "qvex_spec_accept: top-p over the whole vocabulary (top_k = 0) is not "
+                                    "implemented; give top_k in 1..64");
   const int P = nparts(V);
+  const int kf = greedy ? 0 : top_k;           // greedy scores are not filtered
+  QVEX_CHECK_ARG(kf == 0 || P * kf <= 64 * 64, "qvex_spec_accept: V=%d too large for top_k=%d", V, kf);
   const int rps = (k + 1) + (draft ? k : 0);
-  const uint64_t need = ws_floats(S, rps, P) * sizeof(float);
+  const uint64_t base = ws_floats(S, rps, P);
+  const uint64_t need = (base + filter_floats(S, k, P, kf)) * sizeof(float);
   QVEX_CHECK_ARG(workspace_bytes >= need, "qvex_spec_accept: workspace %llu bytes < %llu needed",
                  (unsigned long long)workspace_bytes, (unsigned long long)need);
   const size_t lds = ((size_t)P * NT + P + 2 * rps) * sizeof(float);
   QVEX_CHECK_ARG(lds <= 150 * 1024, "qvex_spec_accept: V=%d too large for the LDS sampling table", V);
   QVEX_CHECK_ARG((long)S * rps <= 65535, "qvex_spec_accept: S*rows=%ld exceeds the grid limit", (long)S * rps);
   QVEX_CHECK_ARG(rps <= 80, "qvex_spec_accept: k=%d too large", k);
+  float* fws = (float*)workspace + base;
+  float* frow = fws + (uint64_t)S * (k + 1) * P * (kf + 1);
   SpecArgs a{target, draft, draft_ids, u_accept, u_sample, inv_temp, greedy, n_accept, out_token,
-             (float*)workspace, S, k, V, P, rps};
+             (float*)workspace, S, k, V, P, rps, seen, presence_penalty, kf, top_p, fws, frow};
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(spec_rowstats_kernel, dim3(P, S * rps), dim3(NT), 0, st, a);
   QVEX_CHECK_LAUNCH("qvex_spec_accept/rowstats");
+  if (kf > 0) {
+    hipLaunchKernelGGL(spec_filter_kernel, dim3(S * (k + 1)), dim3(NT), 0, st, a);
+    QVEX_CHECK_LAUNCH("qvex_spec_accept/filter");
+  }
   hipLaunchKernelGGL(spec_decide_kernel, dim3(P, S), dim3(NT), 0, st, a);
   QVEX_CHECK_LAUNCH("qvex_spec_accept/decide");
   if (!greedy) {
@@ -541,4 +754,12 @@ extern "C" int qvex_spec_accept(const float* target, const float* draft, const i
     QVEX_CHECK_LAUNCH("qvex_spec_accept/sample");
   }
   return QVEX_OK;
+}
+
+extern "C" int qvex_spec_accept(const float* target, const float* draft, const int32_t* draft_ids,
+                                const float* u_accept, const float* u_sample, float inv_temp,
+                                int32_t* n_accept, int32_t* out_token, int S, int k, int V,
+                                void* workspace, uint64_t workspace_bytes, void* stream) {
+  return qvex_spec_accept_filtered(target, draft, draft_ids, u_accept, u_sample, inv_temp, nullptr, 0.0f, 0, 1.0f,
+                                   n_accept, out_token, S, k, V, workspace, workspace_bytes, stream);
 }

@@ -32,6 +32,8 @@ SIGNATURES: dict[str, list] = {
     "qvex_gdn_recurrent_ring": [P, P, P, P, P, P, P, P, I, P, I, P, I, I, I, I, I, I, P],
     "qvex_gdn_chunked": [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P, U64, P],
     "qvex_spec_accept": [P, P, P, P, P, F, P, P, I, I, I, P, U64, P],
+    "qvex_spec_accept_filtered": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P, U64, P],
+    "qvex_mark_seen": [P, I, P, I, P, I, P],
     "qvex_embed_w4g64": [P, I, P, P, P, I, I, P, P],
     "qvex_rmsnorm": [P, LNG, P, P, LNG, I, I, F, F, P],
     "qvex_add_rmsnorm": [P, P, P, P, P, I, I, F, P],
@@ -72,6 +74,8 @@ def lib() -> ctypes.CDLL:
         L.qvex_attn_workspace_bytes.argtypes = [I, I, I, I, I, I]
         L.qvex_w4g64_packed_bytes.restype = U64
         L.qvex_w4g64_packed_bytes.argtypes = [I, I]
+        L.qvex_spec_accept_filtered_workspace_bytes.restype = U64
+        L.qvex_spec_accept_filtered_workspace_bytes.argtypes = [I, I, I, I, I]
         L.qvex_gdn_chunked_workspace_bytes.restype = U64
         L.qvex_gdn_chunked_workspace_bytes.argtypes = [I, I, I, I, I, I]
         for name, args in SIGNATURES.items():
@@ -93,4 +97,4 @@ def call(name: str, *args) -> None:
 def exported_symbols() -> list[str]:
     return ["qvex_last_error", "qvex_abi_version", "qvex_spec_accept_workspace_bytes",
             "qvex_attn_workspace_bytes", "qvex_w4g64_packed_bytes",
-            "qvex_gdn_chunked_workspace_bytes", *SIGNATURES]
+            "qvex_gdn_chunked_workspace_bytes", "qvex_spec_accept_filtered_workspace_bytes", *SIGNATURES]

@@ -231,20 +231,24 @@ def gated_delta_chunked(q, k, v, a, b, A_log, dt_bias, state, state_out=None, y=
     return y, state_out
 
 
-def spec_workspace(S: int, k: int, V: int, has_draft: bool, device) -> torch.Tensor:
-    n = int(_C.lib().qvex_spec_accept_workspace_bytes(S, k, V, int(has_draft)))
+def spec_workspace(S: int, k: int, V: int, has_draft: bool, device, top_k: int = 0) -> torch.Tensor:
+    n = int(_C.lib().qvex_spec_accept_filtered_workspace_bytes(S, k, V, int(has_draft), int(top_k)))
     return torch.empty((max(n, 4) + 3) // 4, dtype=torch.float32, device=device)
 
 
 def spec_accept(target: torch.Tensor, draft: torch.Tensor | None, draft_ids: torch.Tensor,
                 u_accept: torch.Tensor, u_sample: torch.Tensor, temperature: float,
                 n_accept: torch.Tensor | None = None, out_token: torch.Tensor | None = None,
-                workspace: torch.Tensor | None = None):
+                workspace: torch.Tensor | None = None, seen: torch.Tensor | None = None,
+                presence_penalty: float = 0.0, top_k: int = 0, top_p: float = 1.0):
     """Fused accept / residual-resample / bonus sampling for S verify steps.
 
     target fp32 [S,k+1,V]; draft fp32 [S,k,V] or None (greedy one-hot drafts, the
     reference's rule, engine/speculative.py:79-80); draft_ids int32 [S,k];
     u_accept fp32 [S,k]; u_sample fp32 [S]; temperature <= 0 means greedy.
+    The target rows are scored as Sampler.scores (engine/sampler.py:30-52):
+    presence penalty over `seen` (fp32 [V], 0/1) plus the drafts before each row,
+    then top-k (0..64, 0 = off) and top-p (needs top-k) when sampling.
     Returns (n_accept int32 [S], out_token int32 [S]) on the device."""
     _check(target, "target", torch.float32, 3)
     S, k1, V = target.shape
@@ -265,9 +269,15 @@ def spec_accept(target: torch.Tensor, draft: torch.Tensor | None, draft_ids: tor
         n_accept = torch.empty(S, dtype=torch.int32, device=dev)
     if out_token is None:
         out_token = torch.empty(S, dtype=torch.int32, device=dev)
+    if seen is not None:
+        _check(seen, "seen", torch.float32)
+        if seen.numel() != V:
+            raise _C.QvexError(f"seen must hold V={V} values")
     if workspace is None:
-        workspace = spec_workspace(S, k, V, draft is not None, dev)
-    _C.call("qvex_spec_accept", _ptr(target), _ptr(draft) if draft is not None else None,
-            _ptr(draft_ids), _ptr(u_accept), _ptr(u_sample), inv_temp, _ptr(n_accept),
-            _ptr(out_token), S, k, V, _ptr(workspace), workspace.numel() * 4, _stream())
+        workspace = spec_workspace(S, k, V, draft is not None, dev, top_k)
+    _C.call("qvex_spec_accept_filtered", _ptr(target), _ptr(draft) if draft is not None else None,
+            _ptr(draft_ids), _ptr(u_accept), _ptr(u_sample), inv_temp,
+            _ptr(seen) if seen is not None else None, float(np.float32(presence_penalty)), int(top_k),
+            float(np.float32(top_p)), _ptr(n_accept), _ptr(out_token), S, k, V, _ptr(workspace),
+            workspace.numel() * 4, _stream())
     return n_accept, out_token

@@ -1,12 +1,14 @@
 """Token sampling on the device (mirror of engine/sampler.py).
 
-The fused kernel (qvex_spec_accept) does temperature softmax, the speculative
-accept test, residual resampling and plain sampling in one place. The reference's
-top-k / top-p candidate filtering and presence penalty (engine/sampler.py:30-55)
-are not implemented by it: a Sampler refuses parameters that would need them.
-Uniforms come from a host PCG64 stream seeded by SamplingParams.seed (the
-reference draws them from MLX's generator, engine/speculative.py:79-80), so a
-run is reproducible given the seed.
+The fused kernel (qvex_spec_accept_filtered) scores the target rows as
+Sampler.scores does (presence penalty, temperature, top-k, top-p over the top-k
+candidates), then runs the speculative accept test, residual resampling and
+plain sampling in one place. Top-p over the whole vocabulary (top_k = 0 or
+>= V with top_p < 1) and top_k > 64 are not implemented and raise. Uniforms
+come from a host PCG64 stream seeded by SamplingParams.seed (the reference
+draws them from MLX's generator, engine/speculative.py:79-80), so a run is
+reproducible given the seed. The presence mask lives on the device and is
+updated by observe().
 """
 
 from __future__ import annotations
@@ -30,14 +32,22 @@ class SamplingParams:
 
 
 class Sampler:
+    TOP_K_MAX = 64
+
     def __init__(self, params: SamplingParams, vocab_size: int):
         self.p = params
         self.V = vocab_size
-        if 0 < params.top_k < vocab_size or 0 < params.top_p < 1 or params.presence_penalty:
-            raise NotImplementedError(
-                "the fused sampler implements temperature sampling only: use top_k=0, top_p=1.0, "
-                "presence_penalty=0 (got top_k=%d top_p=%g presence_penalty=%g)"
-                % (params.top_k, params.top_p, params.presence_penalty))
+        tk = params.top_k if 0 < params.top_k < vocab_size else 0
+        tp = params.top_p if 0 < params.top_p < 1 else 1.0
+        if params.temperature > 0:
+            if tp < 1.0 and tk == 0:
+                raise NotImplementedError("top-p over the whole vocabulary (top_k = 0 or >= vocab) is not "
+                                          "implemented; give 1 <= top_k <= %d" % self.TOP_K_MAX)
+            if tk > self.TOP_K_MAX:
+                raise NotImplementedError("top_k > %d is not implemented (got %d)" % (self.TOP_K_MAX, tk))
+        self.top_k = tk if params.temperature > 0 else 0
+        self.top_p = tp
+        self.seen = None            # device fp32 [V] presence mask, made on first use
         self.rng = np.random.Generator(np.random.PCG64(params.seed if params.seed is not None else 0))
         self._ws = {}
 
@@ -45,10 +55,39 @@ class Sampler:
     def greedy(self) -> bool:
         return self.p.temperature <= 0
 
+    def _filter(self, device) -> dict:
+        if self.p.presence_penalty and self.seen is None:
+            self.seen = torch.zeros(self.V, dtype=torch.float32, device=device)
+        return dict(seen=self.seen if self.p.presence_penalty else None,
+                    presence_penalty=float(self.p.presence_penalty), top_k=self.top_k, top_p=self.top_p)
+
+    def _workspace(self, S, k, has_draft, device):
+        key = (S, k, has_draft, self.top_k)
+        if key not in self._ws:
+            self._ws[key] = kernels.spec_workspace(S, k, self.V, has_draft, device, self.top_k)
+        return self._ws[key]
+
     def scores(self, logits: torch.Tensor, extra_seen=None) -> torch.Tensor:
-        """Full-vocab fp32 scores: raw logits (greedy) or logits / temperature."""
-        z = to_f32(logits.reshape(-1))
-        return z if self.greedy else z / self.p.temperature
+        """Full-vocab fp32 scores as engine/sampler.py:30-52: penalised logits
+        (greedy) or filtered log-probs. A convenience mirror of the reference's
+        API; the decode path does this inside the fused kernel."""
+        z = to_f32(logits.reshape(-1)).clone()
+        if self.p.presence_penalty:
+            seen = self._filter(z.device)["seen"].clone()
+            if extra_seen is not None:
+                seen[torch.as_tensor(extra_seen, device=z.device).long().reshape(-1)] = 1.0
+            z = z - self.p.presence_penalty * seen
+        if self.greedy:
+            return z
+        z = z / self.p.temperature
+        cand = torch.topk(z, self.top_k).values if self.top_k else torch.sort(z, descending=True).values
+        cutoff = cand[-1]
+        if self.top_p < 1.0:
+            probs = torch.softmax(cand, dim=0)
+            keep = (torch.cumsum(probs, 0) - probs) < self.top_p
+            cutoff = torch.where(keep, cand, torch.full_like(cand, float("inf"))).min()
+        z = torch.where(z >= cutoff, z, torch.full_like(z, float("-inf")))
+        return z - torch.logsumexp(z, 0)
 
     def _uniforms(self, n: int, device) -> torch.Tensor:
         return torch.from_numpy(self.rng.random(n, dtype=np.float32)).to(device)
@@ -61,22 +100,18 @@ class Sampler:
         k = t.shape[1] - 1
         d = None if draft_logits is None else to_f32(draft_logits).reshape(1, k, self.V)
         u = self._uniforms(k + 1, t.device)
-        key = (k, d is not None)
-        if key not in self._ws:
-            self._ws[key] = kernels.spec_workspace(1, k, self.V, d is not None, t.device)
         return kernels.spec_accept(t, d, draft_ids.reshape(1, k).to(torch.int32), u[:k].reshape(1, k).contiguous(),
-                                   u[k:].contiguous(), self.p.temperature, workspace=self._ws[key])
+                                   u[k:].contiguous(), self.p.temperature,
+                                   workspace=self._workspace(1, k, d is not None, t.device), **self._filter(t.device))
 
     def accept_device(self, target: torch.Tensor, draft_ids: torch.Tensor, u: torch.Tensor):
         """accept() with the k + 1 uniforms given as a device fp32 [k+1] tensor
         (no host RNG, so the call can be captured in a graph)."""
         t = to_f32(target).reshape(1, -1, self.V)
         k = t.shape[1] - 1
-        key = (k, False)
-        if key not in self._ws:
-            self._ws[key] = kernels.spec_workspace(1, k, self.V, False, t.device)
         return kernels.spec_accept(t, None, draft_ids.reshape(1, k), u[:k].reshape(1, k), u[k:],
-                                   self.p.temperature, workspace=self._ws[key])
+                                   self.p.temperature, workspace=self._workspace(1, k, False, t.device),
+                                   **self._filter(t.device))
 
     def pick(self, logits: torch.Tensor) -> torch.Tensor:
         """One token per row of logits [R, V] (argmax when greedy) -> int32 [R]."""
@@ -84,13 +119,34 @@ class Sampler:
         R = t.shape[0]
         empty_i = torch.empty((R, 0), dtype=torch.int32, device=t.device)
         empty_f = torch.empty((R, 0), dtype=torch.float32, device=t.device)
-        _, tok = kernels.spec_accept(t, None, empty_i, empty_f, self._uniforms(R, t.device),
-                                     self.p.temperature)
+        _, tok = kernels.spec_accept(t, None, empty_i, empty_f, self._uniforms(R, t.device), self.p.temperature,
+                                     workspace=self._workspace(R, 0, False, t.device), **self._filter(t.device))
         return tok
 
-    def observe(self, tok):
-        """Presence tracking is not needed without a presence penalty."""
-        return None
+    def observe(self, tok) -> None:
+        """Mark emitted tokens as seen (engine/sampler.py:60-62): an int, a list of
+        ints or a device int32 tensor."""
+        if not self.p.presence_penalty:
+            return
+        if isinstance(tok, torch.Tensor):
+            ids = tok.reshape(-1).to(torch.int32)
+            dev = ids.device
+        else:
+            vals = [int(tok)] if not isinstance(tok, (list, tuple)) else [int(v) for v in tok]
+            dev = self.seen.device if self.seen is not None else torch.device("cuda")
+            ids = torch.tensor(vals, dtype=torch.int32, device=dev)
+        seen = self._filter(dev)["seen"]
+        _C.call("qvex_mark_seen", seen.data_ptr(), self.V, ids.data_ptr(), ids.numel(), None, ids.numel(),
+                kernels._stream())
+
+    def observe_result(self, result: torch.Tensor) -> None:
+        """observe() for a device cycle result [n, token, d_0, ...]: the token and the
+        n accepted drafts (graph-capturable)."""
+        if not self.p.presence_penalty:
+            return
+        seen = self._filter(result.device)["seen"]
+        _C.call("qvex_mark_seen", seen.data_ptr(), self.V, result[1:].data_ptr(), result.numel() - 1,
+                result.data_ptr(), 1, kernels._stream())
 
 
 def to_f32(x: torch.Tensor) -> torch.Tensor:

@@ -80,6 +80,7 @@ class MTPDecoder:
         for key in ("cycles", "accepted", "plain", "emitted"):
             self.stats.setdefault(key, 0)
         self.feed = sampler.pick(first_logits.reshape(1, -1))        # int32 [1] on the device
+        sampler.observe(self.feed)
         self.pend_h = [last_hidden] if mtp is not None else []
         self.pend_ids = [self.feed.reshape(1, 1)] if mtp is not None else []
         self.first = int(self.feed.item())
@@ -105,6 +106,7 @@ class MTPDecoder:
             for c in cache:
                 c.rollback(k - n)
         emitted = [int(t) for t in vals[2:2 + n]] + [tok]
+        sampler.observe(emitted)
         tok_dev = tok_t.reshape(1, 1)
         self.pend_h = [hidden[:, : n + 1]]
         self.pend_ids = [torch.cat([drafts[:n].reshape(1, n), tok_dev], dim=1) if n else tok_dev]
@@ -123,6 +125,7 @@ class MTPDecoder:
             t = torch.tensor([forced_token], dtype=torch.int32, device=dev)
         else:
             t = self.sampler.pick(logits[0, -1:])
+        self.sampler.observe(t)
         self.stats["plain"] += 1
         if self.mtp is not None:
             self.pend_h.append(hidden)
@@ -234,6 +237,7 @@ class GraphedMTPCycle:
         self._commit(d.cache.counters, n, 1)
         _C.call("qvex_cycle_finish", _ptr(self.drafts), k, _ptr(n), _ptr(tok), _ptr(self.pend_ids),
                 _ptr(self.feed), _ptr(self.n_prev), _ptr(self.out), _stream())
+        d.sampler.observe_result(self.out)
 
     def cycle(self) -> list[int]:
         """Replay one cycle; returns the emitted tokens (n accepted drafts + 1)."""

@@ -96,3 +96,17 @@ def test_packed_swiglu_rejects_odd_halves():
         _C.call("qvex_qmv_w4g64_packed_swiglu", p16, p16, p16, 1, 24, 256, None)
     with pytest.raises(_C.QvexError, match="multiple of 16"):
         _C.call("qvex_w4g64_pack_swiglu", p16, p16, p16, 24, 256, p16, 1 << 15, None)
+
+
+def test_spec_filter_argument_rules():
+    buf = ctypes.create_string_buffer(1 << 20)
+    p16 = (ctypes.addressof(buf) + 15) // 16 * 16
+    with pytest.raises(_C.QvexError, match="whole vocabulary"):
+        _C.call("qvex_spec_accept_filtered", p16, None, p16, p16, p16, 1.0, None, 0.0, 0, 0.9, p16, p16,
+                1, 1, 4096, p16, 1 << 19, None)
+    with pytest.raises(_C.QvexError, match="top_k"):
+        _C.call("qvex_spec_accept_filtered", p16, None, p16, p16, p16, 1.0, None, 0.0, 65, 0.9, p16, p16,
+                1, 1, 4096, p16, 1 << 19, None)
+    lib = _C.lib()
+    assert lib.qvex_spec_accept_filtered_workspace_bytes(1, 1, 8192, 0, 20) > \
+        lib.qvex_spec_accept_filtered_workspace_bytes(1, 1, 8192, 0, 0) == lib.qvex_spec_accept_workspace_bytes(1, 1, 8192, 0)

@@ -128,14 +128,16 @@ def flat_head_model(seed=12):
     return m
 
 
-def start_decoder(model, mtp, k, temp, seed=0):
+def start_decoder(model, mtp, k, temp, seed=0, **params):
     from qvex.speculative import MTPDecoder
     V = model.cfg.vocab_size
     ids = torch.from_numpy(prompt(15, V, seed=41)).reshape(1, -1).to(DEV)
     cache, mc = model.make_cache(), mtp.make_cache()
     logits, hidden = model(ids, cache, return_hidden=True)
     last_h = mtp_prefill(mtp, mc, hidden, ids, None)
-    s = Sampler(SamplingParams(temperature=temp, top_k=0, top_p=1.0, seed=seed), V)
+    sp = dict(temperature=temp, top_k=0, top_p=1.0, seed=seed)
+    sp.update(params)
+    s = Sampler(SamplingParams(**sp), V)
     return MTPDecoder(model, s, cache, logits[0, -1], last_h, mtp, mc, k=k)
 
 
@@ -200,3 +202,25 @@ def test_graphed_cycle_sampled_runs():
     for _ in range(30):
         out += g.cycle()
     assert all(0 <= t < m.cfg.vocab_size for t in out)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("head", ["random", "flat"])
+def test_graphed_cycle_equals_eager_reference_sampling(head):
+    """The reference's default sampling (T = 0.6, top-k 20, top-p 0.95) plus a presence
+    penalty: the graph replays emit the eager cycles' tokens (same uniform stream) and
+    leave the same device presence mask."""
+    from qvex.speculative import GraphedMTPCycle
+    m = random_model(Config.tiny(layers=4, vocab=2048), seed=16, device=DEV, max_context=1024) \
+        if head == "random" else flat_head_model(seed=17)
+    mtp = random_mtp(m, seed=18)
+    params = dict(top_k=20, top_p=0.95, presence_penalty=0.5)
+    eager = start_decoder(m, mtp, 3, 0.6, seed=5, **params)
+    graphed = GraphedMTPCycle(start_decoder(m, mtp, 3, 0.6, seed=5, **params))
+    te, tg = [], []
+    for _ in range(10):
+        te += eager.cycle()
+        tg += graphed.cycle()
+    assert te == tg
+    assert torch.equal(eager.sampler.seen, graphed.dec.sampler.seen)
+    assert int(eager.sampler.seen.sum().item()) == len(set(te + [eager.first]))

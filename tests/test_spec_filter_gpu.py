@@ -1,0 +1,83 @@
+"""Fused acceptance with the reference's score filtering (presence penalty, top-k,
+top-p; engine/sampler.py:30-52) vs the fp32-emulation oracle: accept counts and
+tokens identical (GPU)."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from qvex import kernels, synth
+from test_spec_gpu import DEV, assert_same, inv
+
+
+def make_case(S, k, V, seed, bf16=False, draft_logits=False):
+    g = np.random.default_rng(seed)
+    target = (g.standard_normal((S, k + 1, V)) * 3.0).astype(np.float32)
+    for s in range(S):
+        for i in range(k + 1):
+            target[s, i, g.integers(0, V, 3)] += 8.0
+    if bf16:
+        target = synth.bf16_to_f32(synth.bf16_bits(target))          # heavy exact ties
+    ids = np.empty((S, k), np.int32)
+    for s in range(S):
+        for i in range(k):
+            top = np.argsort(-target[s, i])[:40]
+            ids[s, i] = top[0] if g.random() < 0.6 else top[g.integers(1, 40)]
+    draft = (target[:, :k] + g.standard_normal((S, k, V)).astype(np.float32)) if draft_logits else None
+    ua = g.random((S, k)).astype(np.float32)
+    us = g.random(S).astype(np.float32)
+    seen = (g.random(V) < 0.05).astype(np.float32)
+    return target, draft, ids, ua, us, seen
+
+
+def run_both(target, draft, ids, ua, us, T, seen=None, **kw):
+    t = torch.from_numpy(target).to(DEV)
+    d = torch.from_numpy(draft).to(DEV) if draft is not None else None
+    sd = torch.from_numpy(seen).to(DEV) if seen is not None else None
+    n, tok = kernels.spec_accept(t, d, torch.from_numpy(ids).to(DEV), torch.from_numpy(ua).to(DEV),
+                                 torch.from_numpy(us).to(DEV), T, seen=sd, **kw)
+    torch.cuda.synchronize()
+    n_o, tok_o = oracle.spec_accept(target, draft, ids, ua, us, inv(T), threads=16, seen=seen, **kw)
+    return n.cpu().numpy(), tok.cpu().numpy(), n_o, tok_o
+
+
+CASES = [
+    # S, k, V, T, top_k, top_p, penalty, bf16, draft_logits
+    (12, 3, 248320, 0.7, 20, 0.95, 0.0, False, False),     # the reference's defaults
+    (12, 3, 248320, 0.6, 20, 0.95, 1.2, True, False),      # + presence penalty, bf16 ties
+    (16, 2, 50000, 1.0, 8, 1.0, 0.0, True, False),         # top-k only, ties at the k-th value
+    (16, 4, 20000, 0.7, 64, 0.5, 0.5, False, False),       # wide k, tight p
+    (16, 1, 8192, 0.9, 1, 1.0, 0.0, False, False),         # top-1
+    (8, 3, 30000, 0.7, 20, 0.9, 0.8, False, True),         # draft logits (q unfiltered)
+    (24, 0, 248320, 0.7, 20, 0.95, 0.3, True, False),      # plain sampling (k = 0)
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("S,k,V,T,top_k,top_p,pen,bf16,dl", CASES)
+def test_filtered_accept_bit_exact(S, k, V, T, top_k, top_p, pen, bf16, dl):
+    target, draft, ids, ua, us, seen = make_case(S, k, V, seed=S * 7 + k + top_k, bf16=bf16, draft_logits=dl)
+    assert_same(*run_both(target, draft, ids, ua, us, T, seen=seen if pen else None, presence_penalty=pen,
+                          top_k=top_k, top_p=top_p))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("k", [0, 3])
+def test_greedy_presence_penalty_bit_exact(k):
+    target, _, ids, ua, us, seen = make_case(16, k, 248320, seed=90 + k, bf16=True)
+    assert_same(*run_both(target, None, ids, ua, us, 0.0, seen=seen, presence_penalty=2.0))
+
+
+@pytest.mark.gpu
+def test_filtered_tokens_stay_in_the_kept_set():
+    """Every emitted token has a target score >= the row's cutoff (checked on the oracle's
+    restated kept set for k = 0)."""
+    S, V, T = 64, 30000, 0.7
+    target, _, _, _, us, _ = make_case(S, 0, V, seed=95, bf16=True)
+    n, tok, _, _ = run_both(target, None, np.zeros((S, 0), np.int32), np.zeros((S, 0), np.float32), us, T,
+                            top_k=10, top_p=0.8)
+    for s in range(S):
+        z = target[s, 0] * np.float32(inv(T))
+        kth = np.sort(z)[::-1][9]
+        assert z[tok[s]] >= kth
