@@ -8,7 +8,7 @@ Gated DeltaNet + 8 gated attention, hidden 4096, MLP 12288, vocab 248320, 4-bit
 group-64 MLX-layout weights) with an MTP draft head sharing the lm_head. A
 4096-token prompt of seeded uniform ids is prefilled (untimed), then W warmup
 cycles run, then exactly K timed MTP cycles (draft k=3 greedy, verify 4 tokens,
-accept at T=0.7, roll back; the cycle is captured once as a HIP graph and
+accept at T=0.7 with top-k 20 / top-p 0.8 as the reference's MTP benchmark, roll back; the cycle is captured once as a HIP graph and
 replayed). value = tokens emitted in the timed cycles / time.
 
 Every line also carries:
@@ -346,7 +346,9 @@ def run_e2e(args):
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t0
     log(f"prefill {args.prompt} tokens in {prefill_s:.2f}s")
-    sampler = Sampler(SamplingParams(temperature=args.temperature, top_k=0, top_p=1.0, seed=synth.SEED_E2E), cfg.vocab_size)
+    # the reference's MTP benchmark samples with top_k = 20, top_p = 0.8 (bench/mtp_bench.py:39)
+    sampler = Sampler(SamplingParams(temperature=args.temperature, top_k=args.top_k, top_p=args.top_p,
+                                     seed=synth.SEED_E2E), cfg.vocab_size)
     stats = {}
     dec = MTPDecoder(model, sampler, cache, logits[0, -1], last_h, mtp, mcache, k=args.k, stats=stats)
     runner = dec
@@ -384,6 +386,8 @@ def main():
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--k", type=int, default=3)
     ap.add_argument("--temperature", type=float, default=0.7)
+    ap.add_argument("--top-k", type=int, default=20)
+    ap.add_argument("--top-p", type=float, default=0.8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-shapes", action="store_true")
     ap.add_argument("--qmv", default="config0", choices=sorted(ROOF_KERNELS),
@@ -410,8 +414,9 @@ def main():
         line.update({"value": round(res["value"], 2), "unit": "tok/s", "ms_per_step": round(res["ms_per_step"], 3)})
         line["config"] = {"workload": "MTP speculative decode, Qwen3.5-9B shape (32 layers: 24 Gated DeltaNet "
                                       "+ 8 gated attention, hidden 4096, MLP 12288, vocab 248320), 4-bit g64 "
-                                      "weights, MTP head drafting k=3, T=0.7, 4096-token prompt",
+                                      "weights, MTP head drafting k=3, T=0.7 (top-k 20, top-p 0.8), 4096-token prompt",
                           "k": args.k, "prompt_tokens": args.prompt, "temperature": args.temperature,
+                          "top_k": args.top_k, "top_p": args.top_p,
                           "cycles_timed": args.steps, "hip_graph": not args.eager}
         line["tokens_per_cycle"] = round(res["tokens_per_cycle"], 4)
         line["acceptance"] = round(res["acceptance"], 4)

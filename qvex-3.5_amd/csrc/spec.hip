@@ -132,11 +132,12 @@ __device__ __forceinline__ float pen_x(const float* seen, float pen, float x, in
 }
 
 // The K largest of the block's values (with multiplicity) into lst[0..K-1],
-// descending: each round takes the block maximum once (ties: lowest wave, then
-// lowest lane; the winner only rescans its own NS values). get(s) gives the
-// calling thread's s-th value, -inf if it has none.
+// descending. Each wave extracts its own K largest, one wave maximum per round
+// (ties: lowest lane; only the winner rescans its NS values), with no block
+// barrier inside the rounds; thread 0 then merges the four sorted lists. get(s)
+// gives the calling thread's s-th value, -inf if it has none. wl: 4 * K floats.
 template <int NS, typename Get>
-__device__ __forceinline__ void block_topk(Get get, int K, float* lst, float* wmax, int* wwin) {
+__device__ __forceinline__ void block_topk(Get get, int K, float* lst, float* wl) {
   uint32_t taken = 0;
   float bv = -__builtin_inff();
   int bs = -1;
@@ -155,23 +156,27 @@ __device__ __forceinline__ void block_topk(Get get, int K, float* lst, float* wm
   for (int r = 0; r < K; ++r) {
     const float m = wave_allmax(bv);
     const unsigned long long msk = __ballot(bv == m);
-    if (lane == 0) {
-      wmax[wave] = m;
-      wwin[wave] = __ffsll(msk) - 1;
-    }
-    __syncthreads();
-    float M = wmax[0];
-    int ww = 0;
-#pragma unroll
-    for (int q = 1; q < 4; ++q)
-      if (wmax[q] > M) { M = wmax[q]; ww = q; }
-    if (threadIdx.x == 0) lst[r] = M;
-    if ((int)threadIdx.x == ww * 64 + wwin[ww] && bs >= 0) {
+    if (lane == 0) wl[wave * K + r] = m;
+    if (lane == __ffsll(msk) - 1 && bs >= 0) {
       taken |= 1u << bs;
       rescan();
     }
-    __syncthreads();
   }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int h[4] = {0, 0, 0, 0};
+    for (int r = 0; r < K; ++r) {
+      int bw = 0;
+      float best = wl[h[0]];
+      for (int w = 1; w < 4; ++w) {
+        const float v = wl[w * K + h[w]];
+        if (v > best) { best = v; bw = w; }
+      }
+      lst[r] = best;
+      ++h[bw];
+    }
+  }
+  __syncthreads();
 }
 
 // ---------------------------------------------------------------- kernel 1: part statistics
@@ -266,11 +271,9 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
   if (tgt && a.top_k > 0) {
     // this part's top_k largest z and the count of its values equal to the k-th
     __shared__ float lst[64];
-    __shared__ float wmax[4];
-    __shared__ int wwin[4];
+    __shared__ float wl[4 * 64];
     const int K = a.top_k;
-    block_topk<4 * NI>([&](int q) { return ok[q >> 2] ? z[q >> 2][q & 3] : -__builtin_inff(); }, K, lst, wmax,
-                       wwin);
+    block_topk<4 * NI>([&](int q) { return ok[q >> 2] ? z[q >> 2][q & 3] : -__builtin_inff(); }, K, lst, wl);
     const float vk = lst[K - 1];
     float cnt = 0.0f;
 #pragma unroll
@@ -298,8 +301,7 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
 __global__ __launch_bounds__(NT) void spec_filter_kernel(SpecArgs a) {
   __shared__ float vals[64 * 64];
   __shared__ float lst[64];
-  __shared__ float wmax[4];
-  __shared__ int wwin[4];
+  __shared__ float wl[4 * 64];
   const int row = blockIdx.x;           // step * (k + 1) + i
   const int K = a.top_k, P = a.P;
   const int n = P * K;
@@ -307,8 +309,7 @@ __global__ __launch_bounds__(NT) void spec_filter_kernel(SpecArgs a) {
   for (int q = threadIdx.x; q < n; q += NT) vals[q] = L[(q / K) * (K + 1) + q % K];
   __syncthreads();
   const int t = threadIdx.x;
-  block_topk<16>([&](int q) { const int v = t + NT * q; return v < n ? vals[v] : -__builtin_inff(); }, K, lst,
-                 wmax, wwin);
+  block_topk<16>([&](int q) { const int v = t + NT * q; return v < n ? vals[v] : -__builtin_inff(); }, K, lst, wl);
   if (t == 0) {
     const float c0 = lst[0];
     float cutoff = lst[K - 1];
