@@ -71,10 +71,25 @@ __device__ __forceinline__ float wave_allsum(float v) {
   return v;
 }
 
+// DPP move whose disabled or out-of-range lanes keep their own value.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_keep(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Maximum broadcast to every lane: quad swaps, half-row and row mirrors give
+// every lane its row maximum, row_bcast15/31 fold the rows into lane 63, which
+// is read back. A maximum is order-free, so the result equals any other
+// reduction order's (up to the sign of a zero).
 __device__ __forceinline__ float wave_allmax(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp_keep<0xB1>(v));                     // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_keep<0x4E>(v));                     // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_keep<0x141>(v));                    // row_half_mirror
+  v = fmaxf(v, dpp_keep<0x140>(v));                    // row_mirror
+  v = fmaxf(v, dpp_keep<DPP_ROW_BCAST15, 0xa>(v));     // rows 1,3 take rows 0,2
+  v = fmaxf(v, dpp_keep<DPP_ROW_BCAST31, 0xc>(v));     // rows 2,3 take row 1
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // ---------------------------------------------------------------- host-side error plumbing

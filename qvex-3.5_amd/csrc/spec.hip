@@ -131,52 +131,72 @@ __device__ __forceinline__ float pen_x(const float* seen, float pen, float x, in
   return x - pen * sj;
 }
 
-// The K largest of the block's values (with multiplicity) into lst[0..K-1],
-// descending. Each wave extracts its own K largest, one wave maximum per round
-// (ties: lowest lane; only the winner rescans its NS values), with no block
-// barrier inside the rounds; thread 0 then merges the four sorted lists. get(s)
-// gives the calling thread's s-th value, -inf if it has none. wl: 4 * K floats.
-template <int NS, typename Get>
-__device__ __forceinline__ void block_topk(Get get, int K, float* lst, float* wl) {
-  uint32_t taken = 0;
-  float bv = -__builtin_inff();
-  int bs = -1;
-  auto rescan = [&]() {
-    bv = -__builtin_inff();
-    bs = -1;
+// A thread's next two values in (value descending, slot ascending) order after
+// (lv, li): strictly greater values move ahead, so an earlier slot wins a tie.
+// Empty entries are (-inf, NS).
+template <int NS>
+__device__ __forceinline__ void next_two(const float (&v)[NS], float lv, int li, float& b0, int& i0, float& b1,
+                                         int& i1) {
+  b0 = b1 = -__builtin_inff();
+  i0 = i1 = NS;
 #pragma unroll
-    for (int q = 0; q < NS; ++q)
-      if (!((taken >> q) & 1u)) {
-        const float v = get(q);
-        if (v > bv) { bv = v; bs = q; }
-      }
-  };
-  rescan();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int q = 0; q < NS; ++q) {
+    const bool after = v[q] < lv || (v[q] == lv && q > li);
+    const float x = after ? v[q] : -__builtin_inff();
+    const bool c0 = x > b0, c1 = x > b1;
+    b1 = c0 ? b0 : (c1 ? x : b1);
+    i1 = c0 ? i0 : (c1 ? q : i1);
+    b0 = c0 ? x : b0;
+    i0 = c0 ? q : i0;
+  }
+}
+
+// The K largest of the block's values (with multiplicity) into lst[0..K-1],
+// descending; v holds the calling thread's NS values, -inf for none. Each wave
+// extracts its own K largest, one wave maximum per round (ties: lowest lane),
+// with no block barrier inside the rounds; a thread serves its values from a
+// two-entry buffer and rescans its registers only when the buffer runs dry.
+// The four sorted lists are then merged by rank: entry i of wave w lands at
+// i + #(entries of other waves that are larger, or equal and from a lower
+// wave), which is unique. wl: 4 * K floats.
+template <int NS>
+__device__ __forceinline__ void block_topk(const float (&v)[NS], int K, float* lst, float* wl) {
+  float b0, b1;
+  int i0, i1;
+  next_two(v, __builtin_inff(), -1, b0, i0, b1, i1);
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   for (int r = 0; r < K; ++r) {
-    const float m = wave_allmax(bv);
-    const unsigned long long msk = __ballot(bv == m);
+    const float m = wave_allmax(b0);
+    const unsigned long long msk = __ballot(b0 == m);
     if (lane == 0) wl[wave * K + r] = m;
-    if (lane == __ffsll(msk) - 1 && bs >= 0) {
-      taken |= 1u << bs;
-      rescan();
+    if (lane == __ffsll(msk) - 1) {
+      const float lv = b0;
+      const int li = i0;
+      b0 = b1;
+      i0 = i1;
+      b1 = -__builtin_inff();
+      i1 = NS;
+      if (i0 == NS && li < NS) next_two(v, lv, li, b0, i0, b1, i1);
     }
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int h[4] = {0, 0, 0, 0};
-    for (int r = 0; r < K; ++r) {
-      int bw = 0;
-      float best = wl[h[0]];
-      for (int w = 1; w < 4; ++w) {
-        const float v = wl[w * K + h[w]];
-        if (v > best) { best = v; bw = w; }
-      }
-      lst[r] = best;
-      ++h[bw];
+  if (t < 4 * K) {
+    const int w = t / K;
+    const float x = wl[t];
+    int rank = t - w * K;
+    for (int w2 = 0; w2 < 4; ++w2) {
+      if (w2 == w) continue;
+      const float* o = wl + w2 * K;
+#pragma unroll 8
+      for (int j = 0; j < K; ++j) rank += (o[j] > x || (w2 < w && o[j] == x)) ? 1 : 0;
     }
+    if (rank < K) lst[rank] = x;
   }
   __syncthreads();
+}
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
 // ---------------------------------------------------------------- kernel 1: part statistics
@@ -273,7 +293,10 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
     __shared__ float lst[64];
     __shared__ float wl[4 * 64];
     const int K = a.top_k;
-    block_topk<4 * NI>([&](int q) { return ok[q >> 2] ? z[q >> 2][q & 3] : -__builtin_inff(); }, K, lst, wl);
+    float zz[4 * NI];
+#pragma unroll
+    for (int q = 0; q < 4 * NI; ++q) zz[q] = ok[q >> 2] ? z[q >> 2][q & 3] : -__builtin_inff();
+    block_topk(zz, K, lst, wl);
     const float vk = lst[K - 1];
     float cnt = 0.0f;
 #pragma unroll
@@ -299,50 +322,80 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
 // cutoff contributes its tie count, any other part its list entries equal to it
 // (the cutoff is never below a part's k-th value).
 __global__ __launch_bounds__(NT) void spec_filter_kernel(SpecArgs a) {
-  __shared__ float vals[64 * 64];
   __shared__ float lst[64];
   __shared__ float wl[4 * 64];
+  __shared__ float cut_s;
+  __shared__ int neq_s;
   const int row = blockIdx.x;           // step * (k + 1) + i
   const int K = a.top_k, P = a.P;
-  const int n = P * K;
+  const int n = P * K;                  // <= 16 * NT, checked by the host
   const float* L = a.fws + (long)row * P * (K + 1);
-  for (int q = threadIdx.x; q < n; q += NT) vals[q] = L[(q / K) * (K + 1) + q % K];
-  __syncthreads();
   const int t = threadIdx.x;
-  block_topk<16>([&](int q) { const int v = t + NT * q; return v < n ? vals[v] : -__builtin_inff(); }, K, lst, wl);
-  if (t == 0) {
-    const float c0 = lst[0];
+  float v[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int i = t + NT * q;
+    const int pp = i / K;
+    v[q] = i < n ? L[pp * (K + 1) + (i - pp * K)] : -__builtin_inff();
+  }
+  block_topk(v, K, lst, wl);
+  // Wave 0 holds the candidates c_i = lst[i] and e_i = exp(c_i - c_0) one per
+  // lane; the ordered sums run over them with readlane, in index order.
+  const int lane = t & 63;
+  const float c0 = lst[0];
+  const float cl = lane < K ? lst[lane] : -__builtin_inff();
+  const float el = lane < K ? qx_expf(cl - c0) : 0.0f;
+  if (t < 64) {
     float cutoff = lst[K - 1];
     if (a.top_p > 0.0f && a.top_p < 1.0f) {
       float Ssum = 0.0f;
-      for (int q = 0; q < K; ++q) Ssum = Ssum + qx_expf(lst[q] - c0);
+      for (int q = 0; q < K; ++q) Ssum = Ssum + readlane_f(el, q);
+      const float pl = el / Ssum;
       float run = 0.0f, mn = __builtin_inff();
       for (int q = 0; q < K; ++q) {
-        const float pi = qx_expf(lst[q] - c0) / Ssum;
+        const float pi = readlane_f(pl, q);
+        const float cq = readlane_f(cl, q);
         const float incl = run + pi;
-        if ((incl - pi) < a.top_p && lst[q] < mn) mn = lst[q];
+        if ((incl - pi) < a.top_p && cq < mn) mn = cq;
         run = incl;
       }
       cutoff = mn;
     }
-    int n_gt = 0;
-    while (n_gt < K && lst[n_gt] > cutoff) ++n_gt;
-    int n_eq = 0;
-    for (int q = 0; q < P; ++q) {
-      const float* Lp = L + (long)q * (K + 1);
-      if (cutoff == Lp[K - 1]) {
-        n_eq += (int)Lp[K];
-      } else {
-        for (int r = 0; r < K; ++r) n_eq += (Lp[r] == cutoff) ? 1 : 0;
-      }
+    if (t == 0) {
+      cut_s = cutoff;
+      neq_s = 0;
     }
+  }
+  __syncthreads();
+  // Values equal to the cutoff: a part whose K-th value is the cutoff
+  // contributes its tie count (every element of the part equal to that value),
+  // any other part its list entries equal to it. Integer sum, so order-free.
+  const float cutoff = cut_s;
+  int my_eq = 0;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int i = t + NT * q;
+    if (i < n && v[q] == cutoff) {
+      const int pp = i / K;
+      if (L[pp * (K + 1) + K - 1] != cutoff) ++my_eq;
+    }
+  }
+  for (int q = t; q < P; q += NT)
+    if (L[q * (K + 1) + K - 1] == cutoff) my_eq += (int)L[q * (K + 1) + K];
+  if (my_eq) atomicAdd(&neq_s, my_eq);
+  __syncthreads();
+  if (t < 64) {
+    // lst is descending, so the values above the cutoff are a prefix
+    const int n_gt = __popcll(__ballot(lane < K && cl > cutoff));
     float S = 0.0f;
-    for (int q = 0; q < n_gt; ++q) S = S + qx_expf(lst[q] - c0);
-    S = S + (float)n_eq * qx_expf(cutoff - c0);
-    float* fr = a.frow + (long)row * 4;
-    fr[0] = c0;
-    fr[1] = S;
-    fr[2] = cutoff;
+    for (int q = 0; q < n_gt; ++q) S = S + readlane_f(el, q);
+    S = S + (float)neq_s * qx_expf(cutoff - c0);
+    if (t == 0) {
+      float* fr = a.frow + (long)row * 4;
+      fr[0] = c0;
+      fr[1] = S;
+      fr[2] = cutoff;
+    }
   }
 }
 
