@@ -142,6 +142,23 @@ int qvex_gdn_recurrent_ring(const uint16_t* q, const uint16_t* k, const uint16_t
                             const int32_t* cur_slot, int snap_every, uint16_t* y, int B, int T,
                             int Hk, int Hv, int Dk, int Dv, void* stream);
 
+/* The whole GatedDeltaNet mixer between in_proj and out_proj for a verify or
+ * decode step of T <= 8 tokens, one launch (GatedDeltaNet.__call__,
+ * engine/model.py:259-290, with gated_delta from engine/kernels.py:92-116 and
+ * _gated_rmsnorm from engine/model.py:138-143): qvex_gdn_conv_qk, then
+ * qvex_gdn_recurrent_ring, then qvex_gated_rmsnorm, with bitwise the same
+ * outputs, conv ring and state ring as those three calls. proj [T, p_stride]
+ * bf16 holds the conv channels (conv_dim = 2 * key_dim + Hv * 128), z at
+ * z_offset and b, a at ab_offset; `counter` is the layer's token count (conv
+ * ring row and state slot, as in the two ring forms); out bf16 [T, Hv * 128]
+ * is the input of out_proj. B = 1, Dk = Dv = 128, key_dim = Hk * 128. */
+int qvex_gdn_decode_fused(const uint16_t* proj, long p_stride, uint16_t* conv_ring, int ring_rows,
+                          const int32_t* counter, const uint16_t* conv_w, int kernel_size, int conv_dim,
+                          int key_dim, float q_scale, float k_scale, float qk_eps, const float* A_log,
+                          const uint16_t* dt_bias, int z_offset, int ab_offset, float* state_ring,
+                          int n_slots, int snap_every, const uint16_t* norm_w, float norm_eps,
+                          uint16_t* out, int T, int Hk, int Hv, int Dk, int Dv, void* stream);
+
 /* Chunked (prefill) form of the same recurrence, chunk = 64 tokens, on MFMA:
  * gated_delta over a long prompt (engine/kernels.py:92-116 as called by
  * GatedDeltaNet.__call__ during prefill, engine/model.py:282-286). Phase 1

@@ -155,6 +155,201 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(GdnArgs p) {
   }
 }
 
+// ---------------------------------------------------------------- fused decode layer
+//
+// One block of 1024 threads per value head runs the whole GDN mixer between
+// the input and output projections for T <= 8 tokens (engine/model.py:235-291):
+//   1. depthwise conv over the ring window + silu for the head's 128 q, 128 k
+//      and 128 v channels, q/k weightless RMSNorm and scales, and the new
+//      projection rows stored into the conv ring (each channel by one block);
+//   2. the recurrence with a snapshot per token (as gdn_recurrent_kernel);
+//   3. the gated RMSNorm of the head's output rows.
+// Every step keeps the arithmetic and reduction order of conv_silu_qk_kernel,
+// gdn_recurrent_kernel and gated_rmsnorm_kernel (one wave per 128-channel head
+// with 2 channels per lane; one 16-lane DPP row per state row, here two rows
+// per 16 lanes), so the outputs, the conv ring and the state ring are
+// bitwise those of the three-kernel path.
+constexpr int FUSED_TMAX = 8;
+constexpr int FUSED_THREADS = 1024;
+constexpr int FUSED_KC = 4;   // conv taps (Qwen3.5: linear_conv_kernel_dim = 4)
+
+struct GdnFusedArgs {
+  const uint16_t* proj;    // [T, p_stride]: conv channels | z | b | a
+  long p_stride;
+  uint16_t* ring;          // [R, C] conv input history
+  int R;
+  const int32_t* counter;  // the layer's token count (conv ring row and state slot)
+  const uint16_t* cw;      // [C, FUSED_KC]
+  int C, key_dim;
+  float q_scale, k_scale, qk_eps;
+  const float* A_log;
+  const uint16_t* dt_bias;
+  int z_off, ab_off;
+  float* state;            // [n_slots, Hv, 128, 128]
+  int n_slots, snap_every;
+  const uint16_t* norm_w;  // [128]
+  float norm_eps;
+  uint16_t* out;           // [T, Hv * 128]
+  int T, Hk, Hv;
+};
+
+__global__ __launch_bounds__(FUSED_THREADS) void gdn_decode_fused_kernel(GdnFusedArgs p) {
+  __shared__ float qs[FUSED_TMAX][DK], ks[FUSED_TMAX][DK], vs[FUSED_TMAX][DK], ys[FUSED_TMAX][DK];
+  const int hv = blockIdx.x;
+  const int hk = hv / (p.Hv / p.Hk);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int grp = threadIdx.x >> 4, l16 = threadIdx.x & 15;
+  const int T = p.T;
+  const long p0 = *p.counter;
+  const int cur = (int)(((p0 % p.n_slots) + p.n_slots) % p.n_slots);
+  const long slot_stride = (long)p.Hv * DK * DK;
+
+  // state rows grp and grp + 64 of this head, 8 columns per lane
+  long row_off[2];
+  float st[2][8];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    row_off[r] = ((long)hv * DK + grp + 64 * r) * DK + l16 * 8;
+    const float* src = p.state + cur * slot_stride + row_off[r];
+    const u32x4 s0 = load16(src);
+    const u32x4 s1 = load16(src + 4);
+    st[r][0] = __uint_as_float(s0.x); st[r][1] = __uint_as_float(s0.y);
+    st[r][2] = __uint_as_float(s0.z); st[r][3] = __uint_as_float(s0.w);
+    st[r][4] = __uint_as_float(s1.x); st[r][5] = __uint_as_float(s1.y);
+    st[r][6] = __uint_as_float(s1.z); st[r][7] = __uint_as_float(s1.w);
+  }
+
+  // the gate inputs b, a of every token, and this wave's token of z and the
+  // norm weight for step 3, all requested before any of them is needed
+  // per-token decay g and write strength beta, once per block
+  __shared__ float gb_s[2][FUSED_TMAX];
+  if (threadIdx.x < T) {
+    const int t = threadIdx.x;
+    const float A = expf(p.A_log[hv]);
+    const float dt = bf16_to_f32(p.dt_bias[hv]);
+    const float aa = bf16_to_f32(p.proj[(size_t)t * p.p_stride + p.ab_off + p.Hv + hv]);
+    const float bb = bf16_to_f32(p.proj[(size_t)t * p.p_stride + p.ab_off + hv]);
+    const float x = aa + dt;
+    const float sp = x > 20.0f ? x : log1pf(expf(x));
+    gb_s[0][t] = expf(-A * sp);
+    gb_s[1][t] = 1.0f / (1.0f + expf(-bb));
+  }
+  uint32_t zp = 0, wp = 0;
+  if (wave < T) {
+    zp = *reinterpret_cast<const uint32_t*>(p.proj + (size_t)wave * p.p_stride + p.z_off + hv * DK + 2 * lane);
+    wp = *reinterpret_cast<const uint32_t*>(p.norm_w + 2 * lane);
+  }
+
+  // 1. conv + silu (+ q/k norm): one wave per (token, q | k | v head); the
+  // KC = 4 window rows and the lane's two channels' taps (16 bytes) load at once
+  constexpr int W = FUSED_KC - 1;
+  const bool ring_qk = hv % (p.Hv / p.Hk) == 0;
+  for (int task = wave; task < 3 * T; task += FUSED_THREADS / 64) {
+    const int t = task / 3, part = task - 3 * (task / 3);
+    const int cb = part == 0 ? hk * DK : part == 1 ? p.key_dim + hk * DK : 2 * p.key_dim + hv * DK;
+    const int c0 = cb + 2 * lane;
+    uint32_t win[FUSED_KC];
+#pragma unroll
+    for (int j = 0; j < FUSED_KC; ++j) {
+      const int r = t + j;
+      if (r < W) {
+        long rr = (p0 + r - W) % p.R;
+        if (rr < 0) rr += p.R;
+        win[j] = *reinterpret_cast<const uint32_t*>(p.ring + rr * p.C + c0);
+      } else {
+        win[j] = *reinterpret_cast<const uint32_t*>(p.proj + (size_t)(r - W) * p.p_stride + c0);
+      }
+    }
+    const u32x4 taps = load16(p.cw + (size_t)c0 * FUSED_KC);   // c0: x0 x1 x2 x3 | c0+1: x0 x1 x2 x3
+    const float w0[4] = {bf16_lo(taps.x), bf16_hi(taps.x), bf16_lo(taps.y), bf16_hi(taps.y)};
+    const float w1[4] = {bf16_lo(taps.z), bf16_hi(taps.z), bf16_lo(taps.w), bf16_hi(taps.w)};
+    float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < FUSED_KC; ++j) {
+      acc0 = fmaf(bf16_lo(win[j]), w0[j], acc0);
+      acc1 = fmaf(bf16_hi(win[j]), w1[j], acc1);
+    }
+    if (part == 2 || ring_qk) {
+      long rr = (p0 + t) % p.R;
+      if (rr < 0) rr += p.R;
+      *reinterpret_cast<uint32_t*>(p.ring + rr * p.C + c0) = win[W];
+    }
+    float s0 = silu(acc0), s1 = silu(acc1);
+    float* dst = part == 0 ? qs[t] : part == 1 ? ks[t] : vs[t];
+    if (part < 2) {
+      const float ss = wave_allsum(fmaf(s0, s0, s1 * s1));
+      const float inv = rsqrtf(ss / 128.0f + p.qk_eps);
+      const float sc = part == 0 ? p.q_scale : p.k_scale;
+      s0 = s0 * inv * sc;
+      s1 = s1 * inv * sc;
+    }
+    const uint32_t pk = pack_bf16x2(s0, s1);
+    dst[2 * lane] = bf16_lo(pk);
+    dst[2 * lane + 1] = bf16_hi(pk);
+  }
+  __syncthreads();
+
+  // 2. recurrence
+  for (int t = 0; t < T; ++t) {
+    const float g = gb_s[0][t];
+    const float beta = gb_s[1][t];
+    float kk[8], qq[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      kk[i] = ks[t][l16 * 8 + i];
+      qq[i] = qs[t][l16 * 8 + i];
+    }
+    long slot = -1;
+    if (p.snap_every || t == T - 1) slot = (cur + 1 + t) % p.n_slots;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int dv = grp + 64 * r;
+      float kv = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        st[r][i] *= g;
+        kv = fmaf(st[r][i], kk[i], kv);
+      }
+      kv = row16_allsum(kv);
+      const float delta = (vs[t][dv] - kv) * beta;
+      float o = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        st[r][i] = fmaf(kk[i], delta, st[r][i]);
+        o = fmaf(st[r][i], qq[i], o);
+      }
+      o = row16_allsum(o);
+      if (l16 == 0) ys[t][dv] = bf16_to_f32(f32_to_bf16(o));
+      if (slot >= 0) {
+        float* dstp = p.state + slot * slot_stride + row_off[r];
+        u32x4 o0, o1;
+        o0.x = __float_as_uint(st[r][0]); o0.y = __float_as_uint(st[r][1]);
+        o0.z = __float_as_uint(st[r][2]); o0.w = __float_as_uint(st[r][3]);
+        o1.x = __float_as_uint(st[r][4]); o1.y = __float_as_uint(st[r][5]);
+        o1.z = __float_as_uint(st[r][6]); o1.w = __float_as_uint(st[r][7]);
+        *reinterpret_cast<u32x4*>(dstp) = o0;
+        *reinterpret_cast<u32x4*>(dstp + 4) = o1;
+      }
+    }
+  }
+  __syncthreads();
+
+  // 3. gated RMSNorm: one wave per token (T <= 8 < 16 waves), 2 channels per lane
+  if (wave < T) {
+    const int t = wave;
+    const float y0 = ys[t][2 * lane], y1 = ys[t][2 * lane + 1];
+    float ss = 0.0f;
+    ss = fmaf(y0, y0, fmaf(y1, y1, ss));
+    ss = wave_allsum(ss);
+    const float inv = rsqrtf(ss / (float)DK + p.norm_eps);
+    const float n0 = bf16_to_f32(f32_to_bf16(bf16_lo(wp) * (y0 * inv)));
+    const float n1 = bf16_to_f32(f32_to_bf16(bf16_hi(wp) * (y1 * inv)));
+    const float z0 = bf16_lo(zp), z1 = bf16_hi(zp);
+    *reinterpret_cast<uint32_t*>(p.out + (size_t)t * p.Hv * DK + hv * DK + 2 * lane) =
+        pack_bf16x2(silu(z0) * n0, silu(z1) * n1);
+  }
+}
+
 int check_common(const char* fn, int B, int T, int Hk, int Hv, int Dk, int Dv) {
   QVEX_CHECK_ARG(B >= 1 && T >= 1, "%s: B=%d T=%d must be >= 1", fn, B, T);
   QVEX_CHECK_ARG(Hk >= 1 && Hv >= Hk && Hv % Hk == 0, "%s: Hv=%d must be a multiple of Hk=%d", fn, Hv, Hk);
@@ -203,4 +398,41 @@ extern "C" int qvex_gdn_recurrent_ring(const uint16_t* q, const uint16_t* k, con
   GdnArgs p{q, k, v, a, b, A_log, dt_bias, ring, ring, cur_slot,
             (long)B * Hv * Dv * Dk, n_slots, snap_every ? 1 : 0, y, B, T, Hk, Hv, Dv};
   return launch(p, (hipStream_t)stream);
+}
+
+extern "C" int qvex_gdn_decode_fused(const uint16_t* proj, long p_stride, uint16_t* conv_ring, int ring_rows,
+                                     const int32_t* counter, const uint16_t* conv_w, int kernel_size, int conv_dim,
+                                     int key_dim, float q_scale, float k_scale, float qk_eps, const float* A_log,
+                                     const uint16_t* dt_bias, int z_offset, int ab_offset, float* state_ring,
+                                     int n_slots, int snap_every, const uint16_t* norm_w, float norm_eps,
+                                     uint16_t* out, int T, int Hk, int Hv, int Dk, int Dv, void* stream) {
+  QVEX_CHECK_ARG(proj && conv_ring && counter && conv_w && A_log && dt_bias && state_ring && norm_w && out,
+                 "qvex_gdn_decode_fused: null pointer");
+  QVEX_CHECK_ARG(T >= 1 && T <= FUSED_TMAX, "qvex_gdn_decode_fused: T=%d must be in 1..%d", T, FUSED_TMAX);
+  if (Dk != DK || Dv != DK)
+    return qvex::fail(QVEX_ENOTSUP, "qvex_gdn_decode_fused: needs Dk = Dv = 128 (got %d, %d)", Dk, Dv);
+  QVEX_CHECK_ARG(Hk >= 1 && Hv >= Hk && Hv % Hk == 0, "qvex_gdn_decode_fused: Hv=%d must be a multiple of Hk=%d",
+                 Hv, Hk);
+  QVEX_CHECK_ARG(key_dim == Hk * DK && conv_dim == 2 * key_dim + Hv * DK,
+                 "qvex_gdn_decode_fused: conv_dim=%d key_dim=%d do not match Hk=%d Hv=%d", conv_dim, key_dim, Hk, Hv);
+  if (kernel_size != FUSED_KC)
+    return qvex::fail(QVEX_ENOTSUP, "qvex_gdn_decode_fused: needs kernel_size = %d (got %d)", FUSED_KC, kernel_size);
+  QVEX_CHECK_ARG(ring_rows >= T + kernel_size - 1, "qvex_gdn_decode_fused: ring_rows=%d < T + K - 1 = %d",
+                 ring_rows, T + kernel_size - 1);
+  QVEX_CHECK_ARG(n_slots >= 2 && (!snap_every || n_slots >= T + 1),
+                 "qvex_gdn_decode_fused: n_slots=%d must be >= T+1=%d with snapshots (>= 2 without)", n_slots, T + 1);
+  QVEX_CHECK_ARG(p_stride % 2 == 0 && conv_dim <= p_stride && z_offset % 2 == 0 && z_offset + Hv * DK <= p_stride &&
+                     ab_offset >= 0 && ab_offset + 2 * Hv <= p_stride,
+                 "qvex_gdn_decode_fused: p_stride=%ld z_offset=%d ab_offset=%d do not fit the projection row",
+                 p_stride, z_offset, ab_offset);
+  QVEX_CHECK_ARG(qvex_aligned(proj, 4) && qvex_aligned(conv_ring, 4) && qvex_aligned(norm_w, 4) &&
+                     qvex_aligned(out, 4) && qvex_aligned(state_ring, 16) && qvex_aligned(conv_w, 16),
+                 "qvex_gdn_decode_fused: proj, conv_ring, norm_w, out need 4-byte and state_ring, conv_w 16-byte "
+                 "alignment");
+  GdnFusedArgs p{proj, p_stride, conv_ring, ring_rows, counter, conv_w, conv_dim, key_dim,
+                 q_scale, k_scale, qk_eps, A_log, dt_bias, z_offset, ab_offset, state_ring, n_slots,
+                 snap_every ? 1 : 0, norm_w, norm_eps, out, T, Hk, Hv};
+  hipLaunchKernelGGL(gdn_decode_fused_kernel, dim3(Hv), dim3(FUSED_THREADS), 0, (hipStream_t)stream, p);
+  QVEX_CHECK_LAUNCH("qvex_gdn_decode_fused");
+  return QVEX_OK;
 }

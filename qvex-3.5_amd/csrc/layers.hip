@@ -19,7 +19,6 @@
 
 namespace {
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // ---------------------------------------------------------------- embedding gather + dequant
@@ -115,7 +114,7 @@ __global__ __launch_bounds__(256) void conv_silu_qk_kernel(
   float s0 = silu(acc0), s1 = silu(acc1);
   if (c0 < 2 * key_dim) {
     // q or k head: weightless RMSNorm over the 128 channels, then the scale
-    float ss = wave_allsum(s0 * s0 + s1 * s1);
+    float ss = wave_allsum(fmaf(s0, s0, s1 * s1));
     const float inv = rsqrtf(ss / 128.0f + eps);
     const bool isq = c0 < key_dim;
     const float sc = isq ? q_scale : k_scale;

@@ -30,6 +30,7 @@ SIGNATURES: dict[str, list] = {
     "qvex_qmv_w4g64_packed_swiglu": [P, P, P, I, I, I, P],
     "qvex_gdn_recurrent": [P, P, P, P, P, P, P, P, P, I, P, I, I, I, I, I, I, P],
     "qvex_gdn_recurrent_ring": [P, P, P, P, P, P, P, P, I, P, I, P, I, I, I, I, I, I, P],
+    "qvex_gdn_decode_fused": [P, LNG, P, I, P, P, I, I, I, F, F, F, P, P, I, I, P, I, I, P, F, P, I, I, I, I, I, P],
     "qvex_gdn_chunked": [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P, U64, P],
     "qvex_spec_accept": [P, P, P, P, P, F, P, P, I, I, I, P, U64, P],
     "qvex_spec_accept_filtered": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P, U64, P],

@@ -398,10 +398,17 @@ class GatedDeltaNet:
         self.norm_w = p["norm"]
         self.out_proj = p["out_proj"]
 
+    # 1..8 tokens (decode / verify) run the conv, recurrence and gated norm as
+    # one kernel (qvex_gdn_decode_fused, bitwise the three-kernel path)
+    FUSED_MAX_T = 8
+    fused_decode = True
+
     def __call__(self, x, cache: RecurrentCache, keep_prev=False):
         S = x.shape[0]
         dev = x.device
         proj = self.in_proj(x)                                    # [S, conv | z | b | a]
+        if self.fused_decode and S <= self.FUSED_MAX_T and self.dk == 128 and self.dv == 128 and self.K == 4:
+            return self.out_proj(self.mix_fused(proj, cache))
         q = torch.empty((1, S, self.hk, self.dk), dtype=torch.bfloat16, device=dev)
         k = torch.empty_like(q)
         v = torch.empty((1, S, self.hv, self.dv), dtype=torch.bfloat16, device=dev)
@@ -423,6 +430,22 @@ class GatedDeltaNet:
         _C.call("qvex_gated_rmsnorm", _ptr(y), _ptr(proj) + 2 * self.conv_dim, proj.stride(0), self.hv,
                 _ptr(self.norm_w), _ptr(g), S * self.hv, self.dv, float(self.cfg.rms_norm_eps), _stream())
         return self.out_proj(g)
+
+    def mix_fused(self, proj, cache: RecurrentCache):
+        """conv + recurrence + gated norm of S <= 8 rows of in_proj output in one
+        launch; returns the out_proj input [S, value_dim] and advances the cache."""
+        S = proj.shape[0]
+        g = torch.empty((S, self.value_dim), dtype=torch.bfloat16, device=proj.device)
+        inv = self.dk ** -0.5
+        snap = S <= cache.n_slots - 1
+        _C.call("qvex_gdn_decode_fused", _ptr(proj), proj.stride(0), _ptr(cache.conv_ring), cache.ring_rows,
+                cache.counters.ptr(cache.index), _ptr(self.conv_w), self.K, self.conv_dim, self.key_dim,
+                float(inv * inv), float(inv), 1e-6, _ptr(self.A_log), _ptr(self.dt_bias), self.conv_dim,
+                self.conv_dim + self.value_dim, _ptr(cache.ssm_ring), cache.n_slots, int(snap), _ptr(self.norm_w),
+                float(self.cfg.rms_norm_eps), _ptr(g), S, self.hk, self.hv, self.dk, self.dv, _stream())
+        cache.offset += S
+        cache.last_width = S if snap else 0
+        return g
 
 
 class MLP:

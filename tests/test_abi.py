@@ -110,3 +110,28 @@ def test_spec_filter_argument_rules():
     lib = _C.lib()
     assert lib.qvex_spec_accept_filtered_workspace_bytes(1, 1, 8192, 0, 20) > \
         lib.qvex_spec_accept_filtered_workspace_bytes(1, 1, 8192, 0, 0) == lib.qvex_spec_accept_workspace_bytes(1, 1, 8192, 0)
+
+
+def test_gdn_decode_fused_argument_rules():
+    buf = ctypes.create_string_buffer(1 << 12)
+    p = (ctypes.addressof(buf) + 15) // 16 * 16
+    C, kd = 2 * 256 + 512, 256
+
+    def call(T=4, Hk=2, Hv=4, Dk=128, Dv=128, conv_dim=C, key_dim=kd, R=67, n_slots=9, stride=C + 512 + 8):
+        _C.call("qvex_gdn_decode_fused", p, stride, p, R, p, p, 4, conv_dim, key_dim, 1.0, 1.0, 1e-6, p, p, C,
+                C + 512, p, n_slots, 1, p, 1e-6, p, T, Hk, Hv, Dk, Dv, None)
+
+    with pytest.raises(_C.QvexError, match="1..8"):
+        call(T=9)
+    with pytest.raises(_C.QvexError, match="Dk = Dv = 128"):
+        call(Dk=64)
+    with pytest.raises(_C.QvexError, match="multiple of Hk"):
+        call(Hk=3)
+    with pytest.raises(_C.QvexError, match="do not match"):
+        call(conv_dim=C + 128)
+    with pytest.raises(_C.QvexError, match="ring_rows"):
+        call(R=6)
+    with pytest.raises(_C.QvexError, match="n_slots"):
+        call(n_slots=4)
+    with pytest.raises(_C.QvexError, match="projection row"):
+        call(stride=C + 100)
