@@ -99,11 +99,38 @@ int qvex_w4g64_pack_swiglu(const uint32_t* w, const uint16_t* scales, const uint
                            int N, int K, void* packed, uint64_t packed_bytes, void* stream);
 int qvex_qmv_w4g64_packed_swiglu(const uint16_t* x, const void* packed, uint16_t* y, int M,
                                  int N, int K, void* stream);
+/* Residual RMSNorm folded into the products around it (the residual adds and
+ * mx.fast.rms_norm of the decoder layer, engine/model.py:309-317):
+ *
+ * qvex_qmv_w4g64_packed_resid - a product that ends a sub-block (o_proj,
+ *   out_proj, down): delta = bf16(x W^T) as qvex_qmv_w4g64_packed, then
+ *   h = bf16(resid + delta) -> h_out [M, N], u = bf16(h * norm_w) -> u_out
+ *   [M, N] (norm_w: the NEXT norm's weight), and per row r and 16-row tile j
+ *   the sum of h^2 over the tile -> sq_parts[r * ceil(N/16) + j].
+ * qvex_qmv_w4g64_packed_rstd - the product that starts the next sub-block
+ *   (in_proj, qkv, gate_up with swiglu != 0, lm_head) on x = u: output row r is
+ *   scaled by rsqrt(S_r / dim + eps) before rounding, S_r the sum of the row's
+ *   nparts = ceil(dim/16) partials (a multiple of 4, <= 256, i.e. dim <= 4096).
+ *   This equals rms_norm(h) W^T up to where the bf16 roundings fall.
+ * qvex_rms_parts - u and the partials for a residual row no product made
+ *   (the embedding): u = bf16(x * norm_w), sq_parts as above, x [M, D]. */
+int qvex_qmv_w4g64_packed_resid(const uint16_t* x, const void* packed, int M, int N, int K,
+                                const uint16_t* resid, const uint16_t* norm_w, uint16_t* h_out,
+                                uint16_t* u_out, float* sq_parts, void* stream);
+int qvex_qmv_w4g64_packed_rstd(const uint16_t* u, const void* packed, uint16_t* y, int M, int N,
+                               int K, const float* sq_parts, int nparts, int dim, float eps,
+                               int swiglu, void* stream);
+int qvex_rms_parts(const uint16_t* x, const uint16_t* norm_w, uint16_t* u_out, float* sq_parts,
+                   int M, int D, void* stream);
 /* The same with an explicit tile: tiles_per_wave in {1,2,4} 16-row tiles,
- * wave_ksplit in {1,2,4,8} waves splitting the 256-k sets. For tile sweeps. */
+ * wave_ksplit in {1,2,4,8} (16 with one tile) waves splitting the 256-k sets,
+ * and the load pipeline: prefetch_sets = 0 keeps two sets in flight per wave,
+ * 2/4/6/8 issues all of a wave's sets (at least ceil(K/256 / wave_ksplit)) at
+ * once, -1 picks as qvex_qmv_w4g64_packed does. Same bits for every pipeline.
+ * For tile sweeps and tests. */
 int qvex_qmv_w4g64_packed_tiled(const uint16_t* x, const void* packed, uint16_t* y, int M,
                                 int N, int K, int tiles_per_wave, int wave_ksplit,
-                                void* stream);
+                                int prefetch_sets, void* stream);
 
 /* ------------------------------------------------------------------------
  * Gated DeltaNet recurrence (verify form), one state snapshot per token.

@@ -22,20 +22,6 @@ constexpr int DK = 128;
 constexpr int ROWS_PER_BLOCK = 16;
 constexpr int TMAX_PREFETCH = 8;
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_row(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-
-// Sum over the 16 lanes of a DPP row, broadcast to all 16.
-__device__ __forceinline__ float row16_allsum(float v) {
-  v += dpp_row<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_row<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_row<0x124>(v);  // row_ror 4
-  v += dpp_row<0x128>(v);  // row_ror 8
-  return v;
-}
-
 __device__ __forceinline__ void load8_bf16(const uint16_t* p, float* o) {
   const u32x4 v = load16(p);
   o[0] = bf16_lo(v.x); o[1] = bf16_hi(v.x);

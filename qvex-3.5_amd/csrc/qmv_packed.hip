@@ -87,20 +87,48 @@ __global__ __launch_bounds__(64) void pack_kernel(const uint32_t* __restrict__ w
   *reinterpret_cast<uint32_t*>(rec + PK_WBYTES + L * 4) = sb;
 }
 
-constexpr int pk_block(int WS) { return WS >= 4 ? 64 * WS : 256; }
+// Optional epilogues that take the residual RMSNorm out of its own launch
+// (mx.fast.rms_norm after the residual add, engine/model.py:309-317). The norm's
+// per-row scale rsqrt(mean(h^2) + eps) commutes with the product, so:
+//   producer (resid != null): the layer output delta = bf16(x W^T) is added to
+//     the residual stream, h = bf16(resid + delta), and the epilogue writes h,
+//     u = bf16(h * norm_w) (the next norm's weight applied) and, per row and
+//     16-row tile, the partial sum of h^2 (16-lane DPP sum) to sq_parts[r][tile];
+//   consumer (rs_parts != null): x is such a u, and every output row r is scaled
+//     by rsqrt(S_r / rs_dim + rs_eps) before rounding, S_r the sum of the row's
+//     rs_nparts (<= 256, a multiple of 4) partials in a fixed order (lane l adds
+//     parts 4l .. 4l+3, then an xor butterfly over the wave).
+// The product itself is unchanged, so the rows stay independent of M.
+struct PkEpi {
+  const float* rs_parts;
+  int rs_nparts, rs_dim;
+  float rs_eps;
+  const uint16_t* resid;
+  const uint16_t* norm_w;
+  uint16_t* h_out;
+  uint16_t* u_out;
+  float* sq_parts;
+};
+
+constexpr int pk_block(int WS) { return WS >= 4 ? 64 * WS : 256; }   // WS = 16: 1024 threads
 
 // TN 16-row tiles per wave share each activation operand; WS waves of a block
 // split the sets of the same tiles (set ws, ws + WS, ...) and combine through
 // LDS in a fixed order; 4 / WS tile groups per block when WS < 4. Two register
 // buffers: the records and activation slice of the next set are in flight while
-// the current one is computed. Results depend on (N, K, TN, WS) only, never on M.
+// the current one is computed. NP > 0 instead issues the loads of all of a wave's
+// sets (at most NP; indices past the last set are clamped and not computed) before
+// computing any, so a wave with few sets keeps all its bytes in flight; the sets
+// are still computed in the same order. Results depend on (N, K, TN, WS) only,
+// never on M or NP.
 // SWIGLU: the weight was packed with the gate/up interleave; the epilogue rounds
 // the gate and up products to bf16 (as the unfused pair of calls would) and
 // writes bf16(silu(g) * u) to y [M, N/2].
-template <int TN, int WS, bool SWIGLU>
+template <int TN, int WS, int NP, bool SWIGLU>
 __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t* __restrict__ x,
                                                                    const uint8_t* __restrict__ packed,
-                                                                   uint16_t* __restrict__ y, int M, int N, int K) {
+                                                                   uint16_t* __restrict__ y, int M, int N, int K,
+                                                                   PkEpi e) {
   constexpr int NWAVE = pk_block(WS) / 64;
   constexpr int RG = NWAVE / WS;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -125,12 +153,33 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
 
-  u32x4 wb[2][TN][2];
-  uint32_t sb[2][TN];
-  u32x4 xr[2][2];
+  constexpr int NB = NP > 0 ? NP : 2;
+  u32x4 wb[NB][TN][2];
+  uint32_t sb[NB][TN];
+  u32x4 xr[NB][2];
 
   // activation slice loader: lane L of load q covers row 2q + L/32, chunk L%32
   const int xm0 = lane >> 5, xch = lane & 31;
+
+  // epilogue inputs, requested before the weights so their latency hides
+  const bool rs = e.rs_parts != nullptr, prod = e.resid != nullptr;
+  u32x4 rsp[4];
+  if (rs && ws == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      rsp[r] = (r < M && 4 * lane < e.rs_nparts) ? load16(e.rs_parts + (size_t)r * e.rs_nparts + 4 * lane)
+                                                 : u32x4{0u, 0u, 0u, 0u};
+  }
+  uint16_t rsd[TN][4], nw[TN];
+  if (prod && ws == 0 && lane < 16) {
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      const int n = (tile0 + t) * PK_TILE + lane;
+      nw[t] = n < N ? e.norm_w[n] : (uint16_t)0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) rsd[t][r] = (r < M && n < N) ? e.resid[(size_t)r * N + n] : (uint16_t)0;
+    }
+  }
 
   auto issue = [&](int buf, int gs) {
 #pragma unroll
@@ -178,17 +227,26 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
     }
   };
 
-  int gs = ws;
-  if (gs < GS) issue(0, gs);
-  while (gs < GS) {
-    const int g1 = gs + WS;
-    if (g1 < GS) issue(1, g1);
-    compute(0);
-    if (g1 >= GS) break;
-    const int g2 = g1 + WS;
-    if (g2 < GS) issue(0, g2);
-    compute(1);
-    gs = g2;
+  if constexpr (NP == 0) {
+    int gs = ws;
+    if (gs < GS) issue(0, gs);
+    while (gs < GS) {
+      const int g1 = gs + WS;
+      if (g1 < GS) issue(1, g1);
+      compute(0);
+      if (g1 >= GS) break;
+      const int g2 = g1 + WS;
+      if (g2 < GS) issue(0, g2);
+      compute(1);
+      gs = g2;
+    }
+  } else {
+    // the host guarantees ceil(GS / WS) <= NP
+#pragma unroll
+    for (int j = 0; j < NP; ++j) issue(j, min(ws + j * WS, GS - 1));
+#pragma unroll
+    for (int j = 0; j < NP; ++j)
+      if (ws + j * WS < GS) compute(j);
   }
 
   // lane (c, i16) holds group slot c of row i16: sum the 4 slots
@@ -223,6 +281,17 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
         }
     }
   }
+  float rstd[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  if (rs) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = ((__uint_as_float(rsp[r].x) + __uint_as_float(rsp[r].y)) + __uint_as_float(rsp[r].z)) +
+                __uint_as_float(rsp[r].w);
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+      rstd[r] = rsqrtf(v / (float)e.rs_dim + e.rs_eps);
+    }
+  }
   if constexpr (SWIGLU) {
     // lanes 0-7 hold gate rows, lanes 8-15 the matching up rows. The TN*4*8
     // outputs are spread over the wave through its (now idle) LDS slot so that
@@ -233,7 +302,7 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
 #pragma unroll
       for (int t = 0; t < TN; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) ep[(t * 4 + r) * 16 + lane] = acc[t][r];
+        for (int r = 0; r < 4; ++r) ep[(t * 4 + r) * 16 + lane] = rs ? acc[t][r] * rstd[r] : acc[t][r];
     }
 #pragma unroll
     for (int o = lane; o < TN * 32; o += 64) {
@@ -247,36 +316,87 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
       const int n = (tile0 + t) * PK_TILE + i16;
-      if (n < N) {
+      const int tile = tile0 + t;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (r < M) y[(size_t)r * N + n] = f32_to_bf16(acc[t][r]);
+      for (int r = 0; r < 4; ++r) {
+        if (r >= M) continue;
+        const uint16_t d = f32_to_bf16(rs ? acc[t][r] * rstd[r] : acc[t][r]);
+        if (prod) {
+          // lanes 0-15 (one DPP row) are all active here: the tile's sum of h^2
+          const float hv = n < N ? bf16_to_f32(f32_to_bf16(bf16_to_f32(rsd[t][r]) + bf16_to_f32(d))) : 0.0f;
+          const float sq = row16_allsum(hv * hv);
+          if (n < N) {
+            e.h_out[(size_t)r * N + n] = f32_to_bf16(hv);
+            e.u_out[(size_t)r * N + n] = f32_to_bf16(hv * bf16_to_f32(nw[t]));
+          }
+          if (i16 == 0 && tile < tiles) e.sq_parts[(size_t)r * tiles + tile] = sq;
+        }
+        if (y && n < N) y[(size_t)r * N + n] = d;
       }
     }
   }
 }
 
-typedef void (*qmv_packed_fn)(const uint16_t*, const uint8_t*, uint16_t*, int, int, int);
+// The producer epilogue's outputs for a residual row that no product made (the
+// embedding, an MTP input): u = bf16(x * w) and the per-16-column sums of x^2,
+// summed over the 16 lanes of a DPP row exactly as the epilogue does.
+__global__ __launch_bounds__(256) void rms_parts_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                        uint16_t* __restrict__ u, float* __restrict__ parts, int D) {
+  const int r = blockIdx.y;
+  const int tiles = (D + PK_TILE - 1) / PK_TILE;
+  const int tile = blockIdx.x * 16 + (threadIdx.x >> 4), i16 = threadIdx.x & 15;
+  const int n = tile * PK_TILE + i16;
+  const bool ok = tile < tiles && n < D;
+  const float hv = ok ? bf16_to_f32(x[(size_t)r * D + n]) : 0.0f;
+  const float sq = row16_allsum(hv * hv);
+  if (ok) u[(size_t)r * D + n] = f32_to_bf16(hv * bf16_to_f32(w[n]));
+  if (i16 == 0 && tile < tiles) parts[(size_t)r * tiles + tile] = sq;
+}
 
-template <int TN, bool SW>
+typedef void (*qmv_packed_fn)(const uint16_t*, const uint8_t*, uint16_t*, int, int, int, PkEpi);
+
+template <int TN, int NP, bool SW>
 qmv_packed_fn pick_ws(int ws) {
   switch (ws) {
-    case 1: return qmv_packed_kernel<TN, 1, SW>;
-    case 2: return qmv_packed_kernel<TN, 2, SW>;
-    case 4: return qmv_packed_kernel<TN, 4, SW>;
-    case 8: return qmv_packed_kernel<TN, 8, SW>;
+    case 1: return NP == 0 ? qmv_packed_kernel<TN, 1, 0, SW> : nullptr;
+    case 2: return qmv_packed_kernel<TN, 2, NP, SW>;
+    case 4: return qmv_packed_kernel<TN, 4, NP, SW>;
+    case 8: return qmv_packed_kernel<TN, 8, NP, SW>;
+    case 16: return TN == 1 ? qmv_packed_kernel<1, 16, NP, SW> : nullptr;
+  }
+  return nullptr;
+}
+
+template <int NP, bool SW>
+qmv_packed_fn pick_tn(int tn, int ws) {
+  switch (tn) {
+    case 1: return pick_ws<1, NP, SW>(ws);
+    case 2: return NP <= 4 ? pick_ws<2, (NP <= 4 ? NP : 0), SW>(ws) : nullptr;
+    case 4: return NP <= 2 ? pick_ws<4, (NP <= 2 ? NP : 0), SW>(ws) : nullptr;
   }
   return nullptr;
 }
 
 template <bool SW>
-qmv_packed_fn pick_packed(int tn, int ws) {
-  switch (tn) {
-    case 1: return pick_ws<1, SW>(ws);
-    case 2: return pick_ws<2, SW>(ws);
-    case 4: return pick_ws<4, SW>(ws);
+qmv_packed_fn pick_packed(int tn, int ws, int np) {
+  switch (np) {
+    case 0: return pick_tn<0, SW>(tn, ws);
+    case 2: return pick_tn<2, SW>(tn, ws);
+    case 4: return pick_tn<4, SW>(tn, ws);
+    case 6: return pick_tn<6, SW>(tn, ws);
+    case 8: return pick_tn<8, SW>(tn, ws);
   }
   return nullptr;
+}
+
+// Full prefetch when a wave's sets fit: the smallest NP in {2, 4, 6, 8} holding
+// ceil(GS / WS) sets, with at most 8 records (TN * NP) of registers per wave.
+int packed_prefetch_depth(int K, int TN, int WS) {
+  const int S = (K / PK_SET + WS - 1) / WS;
+  if (WS < 2) return 0;
+  for (int np = 2; np <= 8; np += 2)
+    if (S <= np && TN * np <= 8) return np;
+  return 0;
 }
 
 // Tile choice from (N, K) only, so a row's bits never depend on M. Two tiles per
@@ -295,9 +415,11 @@ void packed_default_tile(int N, int K, int* TN, int* WS) {
 }
 
 int launch_packed(const uint16_t* x, const uint8_t* packed, uint16_t* y, int M, int N, int K, int TN, int WS,
-                  bool swiglu, hipStream_t stream) {
-  const char* fn_name = swiglu ? "qvex_qmv_w4g64_packed_swiglu" : "qvex_qmv_w4g64_packed";
-  QVEX_CHECK_ARG(x && packed && y, "%s: null pointer", fn_name);
+                  bool swiglu, int prefetch_sets, const PkEpi& e, hipStream_t stream,
+                  const char* fn_name_override = nullptr) {
+  const char* fn_name =
+      fn_name_override ? fn_name_override : swiglu ? "qvex_qmv_w4g64_packed_swiglu" : "qvex_qmv_w4g64_packed";
+  QVEX_CHECK_ARG(x && packed && (y || e.resid), "%s: null pointer", fn_name);
   QVEX_CHECK_ARG(M >= 1 && M <= 4, "%s: M=%d outside 1..4", fn_name, M);
   QVEX_CHECK_ARG(N >= 1 && K >= PK_SET && K % PK_SET == 0, "%s: N=%d K=%d (K must be a positive multiple of 256)",
                  fn_name, N, K);
@@ -305,13 +427,17 @@ int launch_packed(const uint16_t* x, const uint8_t* packed, uint16_t* y, int M, 
                  fn_name, N);
   QVEX_CHECK_ARG(qvex_aligned(x, 16) && qvex_aligned(packed, 16) && qvex_aligned(y, 2),
                  "%s: x and packed must be 16-byte aligned", fn_name);
-  qmv_packed_fn fn = swiglu ? pick_packed<true>(TN, WS) : pick_packed<false>(TN, WS);
-  QVEX_CHECK_ARG(fn != nullptr, "%s: unsupported tile TN=%d WS=%d", fn_name, TN, WS);
+  const int NP = prefetch_sets < 0 ? packed_prefetch_depth(K, TN, WS) : prefetch_sets;
+  QVEX_CHECK_ARG(NP == 0 || (WS >= 2 && (K / PK_SET + WS - 1) / WS <= NP),
+                 "%s: prefetch_sets=%d must be 0 or hold all ceil(K/256 / WS) = %d sets of a wave", fn_name, NP,
+                 (K / PK_SET + WS - 1) / WS);
+  qmv_packed_fn fn = swiglu ? pick_packed<true>(TN, WS, NP) : pick_packed<false>(TN, WS, NP);
+  QVEX_CHECK_ARG(fn != nullptr, "%s: unsupported tile TN=%d WS=%d prefetch_sets=%d", fn_name, TN, WS, NP);
   const int threads = pk_block(WS);
   const int tiles = (N + PK_TILE - 1) / PK_TILE;
   const int tiles_per_block = TN * (threads / 64 / WS);
   const int blocks = (tiles + tiles_per_block - 1) / tiles_per_block;
-  hipLaunchKernelGGL(fn, dim3(blocks), dim3(threads), 0, stream, x, packed, y, M, N, K);
+  hipLaunchKernelGGL(fn, dim3(blocks), dim3(threads), 0, stream, x, packed, y, M, N, K, e);
   QVEX_CHECK_LAUNCH(fn_name);
   return QVEX_OK;
 }
@@ -357,18 +483,63 @@ extern "C" int qvex_qmv_w4g64_packed(const uint16_t* x, const void* packed, uint
                                      void* stream) {
   int TN = 1, WS = 1;
   if (N >= 1 && K >= PK_SET) packed_default_tile(N, K, &TN, &WS);
-  return launch_packed(x, (const uint8_t*)packed, y, M, N, K, TN, WS, false, (hipStream_t)stream);
+  return launch_packed(x, (const uint8_t*)packed, y, M, N, K, TN, WS, false, -1, PkEpi{}, (hipStream_t)stream);
 }
 
 extern "C" int qvex_qmv_w4g64_packed_tiled(const uint16_t* x, const void* packed, uint16_t* y, int M, int N, int K,
-                                           int tiles_per_wave, int wave_ksplit, void* stream) {
-  return launch_packed(x, (const uint8_t*)packed, y, M, N, K, tiles_per_wave, wave_ksplit, false,
-                       (hipStream_t)stream);
+                                           int tiles_per_wave, int wave_ksplit, int prefetch_sets, void* stream) {
+  return launch_packed(x, (const uint8_t*)packed, y, M, N, K, tiles_per_wave, wave_ksplit, false, prefetch_sets,
+                       PkEpi{}, (hipStream_t)stream);
 }
 
 extern "C" int qvex_qmv_w4g64_packed_swiglu(const uint16_t* x, const void* packed, uint16_t* y, int M, int N, int K,
                                             void* stream) {
   int TN = 1, WS = 1;
   if (N >= 1 && K >= PK_SET) packed_default_tile(N, K, &TN, &WS);
-  return launch_packed(x, (const uint8_t*)packed, y, M, N, K, TN, WS, true, (hipStream_t)stream);
+  return launch_packed(x, (const uint8_t*)packed, y, M, N, K, TN, WS, true, -1, PkEpi{}, (hipStream_t)stream);
+}
+
+extern "C" int qvex_qmv_w4g64_packed_resid(const uint16_t* x, const void* packed, int M, int N, int K,
+                                           const uint16_t* resid, const uint16_t* norm_w, uint16_t* h_out,
+                                           uint16_t* u_out, float* sq_parts, void* stream) {
+  const char* fn = "qvex_qmv_w4g64_packed_resid";
+  QVEX_CHECK_ARG(resid && norm_w && h_out && u_out && sq_parts, "%s: null pointer", fn);
+  int TN = 1, WS = 1;
+  if (N >= 1 && K >= PK_SET) packed_default_tile(N, K, &TN, &WS);
+  PkEpi e{};
+  e.resid = resid;
+  e.norm_w = norm_w;
+  e.h_out = h_out;
+  e.u_out = u_out;
+  e.sq_parts = sq_parts;
+  return launch_packed(x, (const uint8_t*)packed, nullptr, M, N, K, TN, WS, false, -1, e, (hipStream_t)stream, fn);
+}
+
+extern "C" int qvex_qmv_w4g64_packed_rstd(const uint16_t* u, const void* packed, uint16_t* y, int M, int N, int K,
+                                          const float* sq_parts, int nparts, int dim, float eps, int swiglu,
+                                          void* stream) {
+  const char* fn = "qvex_qmv_w4g64_packed_rstd";
+  QVEX_CHECK_ARG(sq_parts && y, "%s: null pointer", fn);
+  QVEX_CHECK_ARG(nparts >= 1 && nparts <= 256 && nparts % 4 == 0 && dim >= 1 && nparts == (dim + PK_TILE - 1) / PK_TILE,
+                 "%s: nparts=%d must be ceil(dim/16) for dim=%d, a multiple of 4 and <= 256", fn, nparts, dim);
+  QVEX_CHECK_ARG(qvex_aligned(sq_parts, 16), "%s: sq_parts must be 16-byte aligned", fn);
+  int TN = 1, WS = 1;
+  if (N >= 1 && K >= PK_SET) packed_default_tile(N, K, &TN, &WS);
+  PkEpi e{};
+  e.rs_parts = sq_parts;
+  e.rs_nparts = nparts;
+  e.rs_dim = dim;
+  e.rs_eps = eps;
+  return launch_packed(u, (const uint8_t*)packed, y, M, N, K, TN, WS, swiglu != 0, -1, e, (hipStream_t)stream, fn);
+}
+
+extern "C" int qvex_rms_parts(const uint16_t* x, const uint16_t* norm_w, uint16_t* u_out, float* sq_parts, int M,
+                              int D, void* stream) {
+  QVEX_CHECK_ARG(x && norm_w && u_out && sq_parts, "qvex_rms_parts: null pointer");
+  QVEX_CHECK_ARG(M >= 1 && D >= 1, "qvex_rms_parts: M=%d D=%d", M, D);
+  const int tiles = (D + PK_TILE - 1) / PK_TILE;
+  hipLaunchKernelGGL(rms_parts_kernel, dim3((tiles + 15) / 16, M), dim3(256), 0, (hipStream_t)stream, x, norm_w,
+                     u_out, sq_parts, D);
+  QVEX_CHECK_LAUNCH("qvex_rms_parts");
+  return QVEX_OK;
 }

@@ -94,6 +94,21 @@ __device__ __forceinline__ float wave_allmax(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 16 lanes of a DPP row (quad swaps, then row rotations by 4 and
+// 8), the same bits in all 16 lanes.
+__device__ __forceinline__ float row16_allsum(float v) {
+  v += dpp_row<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_row<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_row<0x124>(v);  // row_ror 4
+  v += dpp_row<0x128>(v);  // row_ror 8
+  return v;
+}
+
 // ---------------------------------------------------------------- host-side error plumbing
 
 namespace qvex {

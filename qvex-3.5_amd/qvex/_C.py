@@ -25,7 +25,10 @@ SIGNATURES: dict[str, list] = {
     "qvex_qmv_w4g64_mfma": [P, P, P, P, P, I, I, I, I, I, P],
     "qvex_w4g64_pack": [P, P, P, I, I, P, U64, P],
     "qvex_qmv_w4g64_packed": [P, P, P, I, I, I, P],
-    "qvex_qmv_w4g64_packed_tiled": [P, P, P, I, I, I, I, I, P],
+    "qvex_qmv_w4g64_packed_tiled": [P, P, P, I, I, I, I, I, I, P],
+    "qvex_qmv_w4g64_packed_resid": [P, P, I, I, I, P, P, P, P, P, P],
+    "qvex_qmv_w4g64_packed_rstd": [P, P, P, I, I, I, P, I, I, F, I, P],
+    "qvex_rms_parts": [P, P, P, P, I, I, P],
     "qvex_w4g64_pack_swiglu": [P, P, P, I, I, P, U64, P],
     "qvex_qmv_w4g64_packed_swiglu": [P, P, P, I, I, I, P],
     "qvex_gdn_recurrent": [P, P, P, P, P, P, P, P, P, I, P, I, I, I, I, I, I, P],

@@ -102,9 +102,11 @@ def pack_w4(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, swiglu:
 
 
 def quantized_matmul_packed(x: torch.Tensor, packed: torch.Tensor, N: int, out: torch.Tensor | None = None,
-                            tile: tuple[int, int] | None = None, swiglu: bool = False) -> torch.Tensor:
+                            tile: tuple[int, ...] | None = None, swiglu: bool = False) -> torch.Tensor:
     """y = x @ dequant(W)^T from pack_w4's copy, x bf16 [..., K] with 1..4 rows
     (the product of mx.quantized_matmul in QLinear.__call__, engine/model.py:87-91).
+    tile = (tiles_per_wave, wave_ksplit[, prefetch_sets]) forces a tile and load
+    pipeline (prefetch_sets 0 = two-deep, default -1 = automatic).
     swiglu=True (weight packed with swiglu=True): y [..., N/2] = silu(gate) * up
     (_swiglu, engine/model.py:134-135)."""
     K = x.shape[-1]
@@ -129,8 +131,70 @@ def quantized_matmul_packed(x: torch.Tensor, packed: torch.Tensor, N: int, out: 
         _C.call("qvex_qmv_w4g64_packed", _ptr(x2), _ptr(packed), _ptr(out), M, N, K, _stream())
     else:
         _C.call("qvex_qmv_w4g64_packed_tiled", _ptr(x2), _ptr(packed), _ptr(out), M, N, K,
-                int(tile[0]), int(tile[1]), _stream())
+                int(tile[0]), int(tile[1]), int(tile[2]) if len(tile) > 2 else -1, _stream())
     return out
+
+
+def qmv_packed_resid(x: torch.Tensor, packed: torch.Tensor, N: int, resid: torch.Tensor, norm_w: torch.Tensor,
+                     h_out: torch.Tensor | None = None, u_out: torch.Tensor | None = None,
+                     parts: torch.Tensor | None = None):
+    """Product that ends a sub-block, with the residual add and the next norm's
+    inputs in its epilogue: h = bf16(resid + bf16(x W^T)), u = bf16(h * norm_w),
+    parts [M, ceil(N/16)] fp32 sums of h^2 per 16 columns. Returns (h, u, parts)."""
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    M = x2.shape[0]
+    _check(x2, "x", torch.bfloat16, 2)
+    _check(resid, "resid", torch.bfloat16)
+    _check(norm_w, "norm_w", torch.bfloat16)
+    if resid.numel() != M * N or norm_w.numel() != N:
+        raise _C.QvexError(f"resid must hold M*N = {M * N} and norm_w N = {N} values")
+    if packed.numel() != int(_C.lib().qvex_w4g64_packed_bytes(N, K)):
+        raise _C.QvexError(f"packed has {packed.numel()} bytes, not the size of an N={N} K={K} pack")
+    tiles = (N + 15) // 16
+    h_out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device) if h_out is None else h_out
+    u_out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device) if u_out is None else u_out
+    parts = torch.empty((M, tiles), dtype=torch.float32, device=x.device) if parts is None else parts
+    if h_out.numel() != M * N or u_out.numel() != M * N or parts.numel() != M * tiles:
+        raise _C.QvexError("h_out/u_out/parts have the wrong size")
+    _C.call("qvex_qmv_w4g64_packed_resid", _ptr(x2), _ptr(packed), M, N, K, _ptr(resid), _ptr(norm_w),
+            _ptr(h_out), _ptr(u_out), _ptr(parts), _stream())
+    return h_out, u_out, parts
+
+
+def qmv_packed_rstd(u: torch.Tensor, packed: torch.Tensor, N: int, parts: torch.Tensor, eps: float,
+                    out: torch.Tensor | None = None, swiglu: bool = False) -> torch.Tensor:
+    """quantized_matmul_packed of rms_norm(h) given as u = bf16(h * w) and the
+    per-16-column sums of h^2 (qmv_packed_resid / rms_parts); swiglu as there."""
+    K = u.shape[-1]
+    u2 = u.reshape(-1, K)
+    M = u2.shape[0]
+    _check(u2, "u", torch.bfloat16, 2)
+    _check(parts, "parts", torch.float32)
+    nparts = (K + 15) // 16
+    if parts.numel() != M * nparts:
+        raise _C.QvexError(f"parts must hold M * ceil(K/16) = {M * nparts} values")
+    if packed.numel() != int(_C.lib().qvex_w4g64_packed_bytes(N, K)):
+        raise _C.QvexError(f"packed has {packed.numel()} bytes, not the size of an N={N} K={K} pack")
+    NO = N // 2 if swiglu else N
+    out = torch.empty((M, NO), dtype=torch.bfloat16, device=u.device) if out is None else out
+    _check(out, "out", torch.bfloat16)
+    _C.call("qvex_qmv_w4g64_packed_rstd", _ptr(u2), _ptr(packed), _ptr(out), M, N, K, _ptr(parts), nparts, K,
+            float(eps), int(bool(swiglu)), _stream())
+    return out
+
+
+def rms_parts(x: torch.Tensor, w: torch.Tensor, u_out: torch.Tensor | None = None,
+              parts: torch.Tensor | None = None):
+    """u = bf16(x * w) and the per-16-column sums of x^2 of rows x [M, D]."""
+    D = x.shape[-1]
+    x2 = x.reshape(-1, D)
+    M = x2.shape[0]
+    _check(x2, "x", torch.bfloat16, 2)
+    u_out = torch.empty((M, D), dtype=torch.bfloat16, device=x.device) if u_out is None else u_out
+    parts = torch.empty((M, (D + 15) // 16), dtype=torch.float32, device=x.device) if parts is None else parts
+    _C.call("qvex_rms_parts", _ptr(x2), _ptr(w), _ptr(u_out), _ptr(parts), M, D, _stream())
+    return u_out, parts
 
 
 def read_roof(buf: torch.Tensor, sink: torch.Tensor, blocks: int = 4096) -> None:

@@ -146,9 +146,17 @@ class QLinear:
         if self.packed is not None:
             self.packed = kernels.pack_w4(self.w, self.scales, self.biases, swiglu=self.swiglu_packed)
 
-    def swiglu(self, x: torch.Tensor) -> torch.Tensor:
+    def _takes_normed(self, x, M: int) -> bool:
+        return self.packed is not None and M <= self.PACKED_MAX_ROWS and NormedRows.supported(self.K)
+
+    def swiglu(self, x) -> torch.Tensor:
         """silu(x W_gate^T) * (x W_up^T) for a fused [gate; up] layer
         (_swiglu over the split halves, engine/model.py:134-135, 302)."""
+        if isinstance(x, NormedRows):
+            M = x.u.reshape(-1, self.K).shape[0]
+            if self.swiglu_packed and self._takes_normed(x, M):
+                return kernels.qmv_packed_rstd(x.u, self.packed, self.N, x.parts, x.eps, swiglu=True)
+            x = x.materialize()
         x2 = x.reshape(-1, self.K)
         M, I = x2.shape[0], self.N // 2
         if self.swiglu_packed and self.packed is not None and M <= self.PACKED_MAX_ROWS:
@@ -158,7 +166,14 @@ class QLinear:
         _C.call("qvex_swiglu", _ptr(gu), _ptr(h), M, I, _stream())
         return h
 
-    def __call__(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    def __call__(self, x, out: torch.Tensor | None = None) -> torch.Tensor:
+        if isinstance(x, NormedRows):
+            M = x.u.reshape(-1, self.K).shape[0]
+            if not self.swiglu_packed and self._takes_normed(x, M):
+                o = kernels.qmv_packed_rstd(x.u, self.packed, self.N, x.parts, x.eps,
+                                            out=None if out is None else out.view(M, self.N))
+                return o.view(*x.u.shape[:-1], self.N)
+            x = x.materialize()
         lead = x.shape[:-1]
         x2 = x.reshape(-1, self.K)
         M = x2.shape[0]
@@ -172,6 +187,18 @@ class QLinear:
             m1 = min(M, m0 + QMV_MAX_ROWS)
             kernels.quantized_matmul(x2[m0:m1], self.w, self.scales, self.biases, out=o2[m0:m1])
         return out.view(*lead, self.N)
+
+    def residual(self, x: torch.Tensor, resid: torch.Tensor, norm_w: torch.Tensor, eps: float):
+        """h = resid + x W^T and the next norm of h: returns (h, NormedRows) with
+        the add and the norm's inputs in the product's epilogue (1..4 rows), or
+        (h, normalised tensor) through add_rms_norm otherwise."""
+        x2 = x.reshape(-1, self.K)
+        M = x2.shape[0]
+        if (self.packed is not None and not self.swiglu_packed and M <= self.PACKED_MAX_ROWS
+                and NormedRows.supported(self.N)):
+            h, u, parts = kernels.qmv_packed_resid(x2, self.packed, self.N, resid.reshape(M, self.N), norm_w)
+            return h, NormedRows(u, parts, eps)
+        return add_rms_norm(resid.reshape(M, self.N), self(x2), norm_w, eps)
 
     @staticmethod
     def fuse(layers: list["QLinear"], swiglu: bool = False) -> "QLinear":
@@ -220,6 +247,43 @@ def add_rms_norm(x, delta, w, eps, h_out=None, out=None):
     out = torch.empty_like(x) if out is None else out
     _C.call("qvex_add_rmsnorm", _ptr(x), _ptr(delta), _ptr(h_out), _ptr(w), _ptr(out), R, D, float(eps), _stream())
     return h_out, out
+
+
+class NormedRows:
+    """rms_norm(h) * w for 1..4 rows kept unnormalised: u = bf16(h * w) and the
+    fp32 sums of h^2 per 16 columns (written by the product that made h, or by
+    rms_parts). A packed QLinear takes it as input and applies the per-row
+    rsqrt(mean(h^2) + eps) to its outputs, so the norm costs no launch."""
+
+    def __init__(self, u: torch.Tensor, parts: torch.Tensor, eps: float):
+        self.u, self.parts, self.eps = u, parts, eps
+
+    @classmethod
+    def of(cls, x: torch.Tensor, w: torch.Tensor, eps: float) -> "NormedRows":
+        u, parts = kernels.rms_parts(x, w)
+        return cls(u, parts, eps)
+
+    @staticmethod
+    def supported(D: int) -> bool:
+        n = (D + 15) // 16
+        return n % 4 == 0 and n <= 256
+
+    @property
+    def shape(self):
+        return self.u.shape
+
+    @property
+    def device(self):
+        return self.u.device
+
+    def __getitem__(self, rows) -> "NormedRows":
+        return NormedRows(self.u[rows], self.parts[rows], self.eps)
+
+    def materialize(self) -> torch.Tensor:
+        """The normalised rows as a tensor (for a consumer without the packed path)."""
+        D = self.u.shape[-1]
+        ms = self.parts.sum(dim=-1, keepdim=True) / D
+        return (self.u.float() * torch.rsqrt(ms + self.eps)).to(torch.bfloat16)
 
 
 # ---------------------------------------------------------------- caches
@@ -361,7 +425,9 @@ class Attention:
             self._ws = torch.empty((need + 3) // 4, dtype=torch.float32, device=device)
         return self._ws
 
-    def __call__(self, x, cache: KVCache):
+    def __call__(self, x, cache: KVCache, resid=None, norm_w=None, eps=None):
+        """x [L, H] (or NormedRows); with resid the o_proj also adds the residual
+        and prepares the next norm (QLinear.residual)."""
         L = x.shape[0]
         cfg = self.cfg
         H, Hkv, D = self.n_heads, self.n_kv, self.head_dim
@@ -379,6 +445,8 @@ class Attention:
         _C.call("qvex_attention", _ptr(q), _ptr(cache.k), _ptr(cache.v), pos, L, H, Hkv, D, cache.capacity,
                 max_keys, kps, _ptr(proj), proj.stride(0), _ptr(o), _ptr(ws), ws.numel() * 4, _stream())
         cache.offset += L
+        if resid is not None:
+            return self.o_proj.residual(o, resid, norm_w, eps)
         return self.o_proj(o)
 
 
@@ -403,12 +471,19 @@ class GatedDeltaNet:
     FUSED_MAX_T = 8
     fused_decode = True
 
-    def __call__(self, x, cache: RecurrentCache, keep_prev=False):
+    def _out(self, g, resid, norm_w, eps):
+        if resid is not None:
+            return self.out_proj.residual(g, resid, norm_w, eps)
+        return self.out_proj(g)
+
+    def __call__(self, x, cache: RecurrentCache, keep_prev=False, resid=None, norm_w=None, eps=None):
+        """x [S, H] (or NormedRows); with resid the out_proj also adds the residual
+        and prepares the next norm (QLinear.residual)."""
         S = x.shape[0]
         dev = x.device
         proj = self.in_proj(x)                                    # [S, conv | z | b | a]
         if self.fused_decode and S <= self.FUSED_MAX_T and self.dk == 128 and self.dv == 128 and self.K == 4:
-            return self.out_proj(self.mix_fused(proj, cache))
+            return self._out(self.mix_fused(proj, cache), resid, norm_w, eps)
         q = torch.empty((1, S, self.hk, self.dk), dtype=torch.bfloat16, device=dev)
         k = torch.empty_like(q)
         v = torch.empty((1, S, self.hv, self.dv), dtype=torch.bfloat16, device=dev)
@@ -429,7 +504,7 @@ class GatedDeltaNet:
         g = torch.empty((S, self.value_dim), dtype=torch.bfloat16, device=dev)
         _C.call("qvex_gated_rmsnorm", _ptr(y), _ptr(proj) + 2 * self.conv_dim, proj.stride(0), self.hv,
                 _ptr(self.norm_w), _ptr(g), S * self.hv, self.dv, float(self.cfg.rms_norm_eps), _stream())
-        return self.out_proj(g)
+        return self._out(g, resid, norm_w, eps)
 
     def mix_fused(self, proj, cache: RecurrentCache):
         """conv + recurrence + gated norm of S <= 8 rows of in_proj output in one
@@ -469,6 +544,13 @@ class Layer:
         self.ln1, self.ln2 = p["input_layernorm"], p["post_attention_layernorm"]
         self.eps = cfg.rms_norm_eps
 
+    def fused(self, h, st, cache, keep_prev, next_w):
+        """1..4 rows with the norms folded into the products: h the residual stream,
+        st its ln1 norm as NormedRows; returns the new stream and its norm by next_w."""
+        kw = dict(resid=h, norm_w=self.ln2, eps=self.eps)
+        h2, st2 = self.mixer(st, cache, keep_prev, **kw) if self.linear else self.mixer(st, cache, **kw)
+        return self.mlp.down.residual(self.mlp.gate_up.swiglu(st2), h2, next_w, self.eps)
+
     def __call__(self, x, cache, keep_prev=False, normed=None):
         """x [L, H] residual stream. Returns the new residual stream."""
         n = normed if normed is not None else rms_norm(x, self.ln1, self.eps)
@@ -480,6 +562,10 @@ class Layer:
 
 class Qwen35:
     """Forward of the hybrid stack (engine/model.py:319-336) for batch 1."""
+
+    # 1..4-row calls fold every residual RMSNorm into the neighbouring products
+    # (QLinear.residual / NormedRows); False keeps the separate norm kernels
+    fuse_norms = True
 
     def __init__(self, cfg: Config, embed: QEmbedding, layers: list[Layer], norm, lm_head: QLinear,
                  max_context: int = 8192, max_width: int = 8):
@@ -528,6 +614,14 @@ class Qwen35:
         counters.sync()
         x = self.embed(ids)
         eps = self.cfg.rms_norm_eps
+        if self.fuse_norms and L <= QLinear.PACKED_MAX_ROWS and NormedRows.supported(self.cfg.hidden_size):
+            # decode / verify: residual adds and norms ride on the products' epilogues
+            h, st = x, NormedRows.of(x, self.layers[0].ln1, eps)
+            for i, (layer, c) in enumerate(zip(self.layers, cache)):
+                nxt = self.layers[i + 1].ln1 if i + 1 < len(self.layers) else self.norm
+                h, st = layer.fused(h, st, c, keep_prev, nxt)
+            logits = self.lm_head(st[-1:] if last_only else st).view(1, -1, self.cfg.vocab_size)
+            return (logits, h.view(1, L, -1)) if return_hidden else logits
         n = rms_norm(x, self.layers[0].ln1, eps)
         for i, (layer, c) in enumerate(zip(self.layers, cache)):
             h, m = layer(x, c, keep_prev, normed=n)

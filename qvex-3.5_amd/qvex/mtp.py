@@ -17,7 +17,8 @@ import torch
 
 from . import _C
 from .kernels import _ptr, _stream
-from .model import Attention, KVCache, Layer, MLP, QLinear, Qwen35, _rand_qlinear, add_rms_norm, rms_norm
+from .model import (Attention, KVCache, Layer, MLP, NormedRows, QLinear, Qwen35, _rand_qlinear, add_rms_norm,
+                    rms_norm)
 
 
 class MTPHead:
@@ -59,6 +60,17 @@ class MTPHead:
         rms_norm(e, self.norm_emb, self.eps, out=x_in[:, :H])
         rms_norm(h, self.norm_hid, self.eps, out=x_in[:, H:])
         x = self.fc(x_in)
+        V = self.model.cfg.vocab_size
+        if self.model.fuse_norms and T <= QLinear.PACKED_MAX_ROWS and NormedRows.supported(H):
+            # the block's residual norms ride on its products (Layer.fused)
+            out, st = self.layer.fused(x, NormedRows.of(x, self.layer.ln1, self.eps), cache, False, self.norm_out)
+            if select is not None:
+                o_sel = torch.empty((1, H), dtype=torch.bfloat16, device=h.device)
+                _C.call("qvex_gather_row", _ptr(out), H, _ptr(select), T, _ptr(o_sel), H, _stream())
+                logits = self.model.lm_head(NormedRows.of(o_sel, self.norm_out, self.eps)).view(1, 1, V)
+                return (logits, o_sel.view(1, 1, H)) if return_hidden else logits
+            logits = self.model.lm_head(st[-1:] if last_only else st).view(1, -1, V)
+            return (logits, out.view(1, T, H)) if return_hidden else logits
         n = rms_norm(x, self.layer.ln1, self.eps)
         hh, m = self.layer(x, cache, normed=n)
         out, n_out = add_rms_norm(hh, m, self.norm_out, self.eps)

@@ -84,7 +84,7 @@ def test_packed_bytes_and_rejections():
     with pytest.raises(_C.QvexError, match="multiple of 256"):
         _C.call("qvex_qmv_w4g64_packed", p16, p16, p16, 1, 16, 320, None)
     with pytest.raises(_C.QvexError, match="unsupported tile"):
-        _C.call("qvex_qmv_w4g64_packed_tiled", p16, p16, p16, 1, 16, 256, 3, 1, None)
+        _C.call("qvex_qmv_w4g64_packed_tiled", p16, p16, p16, 1, 16, 256, 3, 1, -1, None)
     with pytest.raises(_C.QvexError, match="packed buffer"):
         _C.call("qvex_w4g64_pack", p16, p16, p16, 16, 256, p16, 2303, None)
 
@@ -135,3 +135,18 @@ def test_gdn_decode_fused_argument_rules():
         call(n_slots=4)
     with pytest.raises(_C.QvexError, match="projection row"):
         call(stride=C + 100)
+
+
+def test_resid_norm_products_argument_rules():
+    buf = ctypes.create_string_buffer(1 << 14)
+    p = (ctypes.addressof(buf) + 15) // 16 * 16
+    with pytest.raises(_C.QvexError, match="null pointer"):
+        _C.call("qvex_qmv_w4g64_packed_resid", p, p, 1, 16, 256, None, p, p, p, p, None)
+    with pytest.raises(_C.QvexError, match="outside 1..4"):
+        _C.call("qvex_qmv_w4g64_packed_resid", p, p, 5, 16, 256, p, p, p, p, p, None)
+    with pytest.raises(_C.QvexError, match="ceil\\(dim/16\\)"):
+        _C.call("qvex_qmv_w4g64_packed_rstd", p, p, p, 1, 16, 256, p, 255, 4096, 1e-6, 0, None)
+    with pytest.raises(_C.QvexError, match="ceil\\(dim/16\\)"):
+        _C.call("qvex_qmv_w4g64_packed_rstd", p, p, p, 1, 16, 256, p, 320, 5120, 1e-6, 0, None)
+    with pytest.raises(_C.QvexError, match="16-byte"):
+        _C.call("qvex_qmv_w4g64_packed_rstd", p, p, p, 1, 16, 256, p + 4, 256, 4096, 1e-6, 0, None)

@@ -10,7 +10,7 @@ import torch
 from qvex import kernels, synth
 from test_qmv_gpu import check, to_dev
 
-PACKED_TILES = [(tn, ws) for tn in (1, 2, 4) for ws in (1, 2, 4, 8)]
+PACKED_TILES = [(tn, ws) for tn in (1, 2, 4) for ws in (1, 2, 4, 8)] + [(1, 16)]
 
 
 def run_packed(x, w, s, b, tile=None):
@@ -95,3 +95,41 @@ def test_packed_swiglu_equals_product_then_swiglu(M, N, K):
     got = kernels.quantized_matmul_packed(x, kernels.pack_w4(wd, sd, bd, swiglu=True), N, swiglu=True)
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+def default_tile(N, K):
+    """The tile qvex_qmv_w4g64_packed picks (packed_default_tile)."""
+    tiles, GS = (N + 15) // 16, K // 256
+    tn = 2 if tiles >= 1024 else 1
+    ws = 2 if GS >= 8 else 1
+    while ws < 8 and (tiles // tn) * ws < 2048 and GS >= 2 * (ws * 2):
+        ws *= 2
+    return tn, ws
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 4])
+@pytest.mark.parametrize("N,K", [(4096, 12288), (12352, 4096), (4096, 4096), (24576, 4096), (4096, 8192),
+                                 (531, 2304), (17, 512), (4096, 256), (100, 1280)])
+def test_prefetch_pipeline_equals_double_buffer(M, N, K):
+    """The default entry (all of a wave's sets in flight when they fit) and the
+    explicit-tile entry (two-deep pipeline) with the same tile give the same bits."""
+    w, s, b = synth.qmv_weights(N, K, seed=36, tag=N)
+    x = synth.qmv_x(M, K, seed=36, tag=K)
+    auto = run_packed(x, w, s, b)
+    two = run_packed(x, w, s, b, tile=(*default_tile(N, K), 0))
+    assert np.array_equal(auto, two)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tile", [(1, 16, 2), (1, 16, 4), (1, 16, 0), (1, 8, 8), (2, 4, 4), (1, 2, 8)])
+def test_prefetch_explicit_tiles(tile):
+    N, K = 531, 2304 * 2                   # ragged last tile, 18 sets
+    GS = K // 256
+    if tile[2] and -(-GS // tile[1]) > tile[2]:
+        pytest.skip("the wave's sets do not fit the prefetch depth")
+    w, s, b = synth.qmv_weights(N, K, seed=37, tag=tile[1])
+    x = synth.qmv_x(4, K, seed=37, tag=tile[2])
+    y = run_packed(x, w, s, b, tile=tile)
+    check(x, w, s, b, y)
+    assert np.array_equal(y, run_packed(x, w, s, b, tile=(*tile[:2], 0)))
