@@ -170,16 +170,29 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
       rsp[r] = (r < M && 4 * lane < e.rs_nparts) ? load16(e.rs_parts + (size_t)r * e.rs_nparts + 4 * lane)
                                                  : u32x4{0u, 0u, 0u, 0u};
   }
-  uint16_t rsd[TN][4], nw[TN];
-  if (prod && ws == 0 && lane < 16) {
+  // the plain epilogue gives lane L row L / 16 and column L % 16 of each tile
+  const int er = lane >> 4, ei = lane & 15;
+  uint16_t rsd[TN], nw[TN];
+  if (prod && ws == 0) {
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
-      const int n = (tile0 + t) * PK_TILE + lane;
+      const int n = (tile0 + t) * PK_TILE + ei;
       nw[t] = n < N ? e.norm_w[n] : (uint16_t)0;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) rsd[t][r] = (r < M && n < N) ? e.resid[(size_t)r * N + n] : (uint16_t)0;
+      rsd[t] = (er < M && n < N) ? e.resid[(size_t)er * N + n] : (uint16_t)0;
     }
   }
+  // consumer scale: summed as soon as the partials are in (they were requested
+  // first), off the tail of the kernel; a DPP sum into lane 63, read back
+  float rstd[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  auto compute_rstd = [&]() {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = ((__uint_as_float(rsp[r].x) + __uint_as_float(rsp[r].y)) + __uint_as_float(rsp[r].z)) +
+                __uint_as_float(rsp[r].w);
+      v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_to_lane63(v)), 63));
+      rstd[r] = rsqrtf(v / (float)e.rs_dim + e.rs_eps);
+    }
+  };
 
   auto issue = [&](int buf, int gs) {
 #pragma unroll
@@ -230,9 +243,11 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
   if constexpr (NP == 0) {
     int gs = ws;
     if (gs < GS) issue(0, gs);
+    if (gs < GS && gs + WS < GS) issue(1, gs + WS);
+    if (rs && ws == 0) compute_rstd();
     while (gs < GS) {
       const int g1 = gs + WS;
-      if (g1 < GS) issue(1, g1);
+      if (g1 < GS && gs != ws) issue(1, g1);
       compute(0);
       if (g1 >= GS) break;
       const int g2 = g1 + WS;
@@ -244,6 +259,7 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
     // the host guarantees ceil(GS / WS) <= NP
 #pragma unroll
     for (int j = 0; j < NP; ++j) issue(j, min(ws + j * WS, GS - 1));
+    if (rs && ws == 0) compute_rstd();
 #pragma unroll
     for (int j = 0; j < NP; ++j)
       if (ws + j * WS < GS) compute(j);
@@ -281,17 +297,6 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
         }
     }
   }
-  float rstd[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-  if (rs) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v = ((__uint_as_float(rsp[r].x) + __uint_as_float(rsp[r].y)) + __uint_as_float(rsp[r].z)) +
-                __uint_as_float(rsp[r].w);
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-      rstd[r] = rsqrtf(v / (float)e.rs_dim + e.rs_eps);
-    }
-  }
   if constexpr (SWIGLU) {
     // lanes 0-7 hold gate rows, lanes 8-15 the matching up rows. The TN*4*8
     // outputs are spread over the wave through its (now idle) LDS slot so that
@@ -312,26 +317,34 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
       const int j = (tile0 + t) * 8 + i;
       if (j < half && r < M) y[(size_t)r * half + j] = f32_to_bf16(gv / (1.0f + expf(-gv)) * uv);
     }
-  } else if (lane < 16) {
+  } else {
+    // lanes 0-15 hold row r of tile t in acc[t][r]; spread through the wave's
+    // (idle) LDS slot so that lane L finishes row L / 16, column L % 16
+    float* ep = reinterpret_cast<float*>(slot);          // [TN][4][16] floats <= 1 KiB of the 2 KiB slot
+    if (lane < 16) {
 #pragma unroll
-    for (int t = 0; t < TN; ++t) {
-      const int n = (tile0 + t) * PK_TILE + i16;
-      const int tile = tile0 + t;
+      for (int t = 0; t < TN; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (r >= M) continue;
-        const uint16_t d = f32_to_bf16(rs ? acc[t][r] * rstd[r] : acc[t][r]);
+        for (int r = 0; r < 4; ++r) ep[(t * 4 + r) * 16 + lane] = acc[t][r];
+    }
+    const float rs_r = er == 0 ? rstd[0] : er == 1 ? rstd[1] : er == 2 ? rstd[2] : rstd[3];
+    if (er < M) {                       // whole 16-lane DPP rows
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        const int n = (tile0 + t) * PK_TILE + ei;
+        const int tile = tile0 + t;
+        const float a = ep[(t * 4 + er) * 16 + ei];
+        const uint16_t d = f32_to_bf16(rs ? a * rs_r : a);
         if (prod) {
-          // lanes 0-15 (one DPP row) are all active here: the tile's sum of h^2
-          const float hv = n < N ? bf16_to_f32(f32_to_bf16(bf16_to_f32(rsd[t][r]) + bf16_to_f32(d))) : 0.0f;
+          const float hv = n < N ? bf16_to_f32(f32_to_bf16(bf16_to_f32(rsd[t]) + bf16_to_f32(d))) : 0.0f;
           const float sq = row16_allsum(hv * hv);
           if (n < N) {
-            e.h_out[(size_t)r * N + n] = f32_to_bf16(hv);
-            e.u_out[(size_t)r * N + n] = f32_to_bf16(hv * bf16_to_f32(nw[t]));
+            e.h_out[(size_t)er * N + n] = f32_to_bf16(hv);
+            e.u_out[(size_t)er * N + n] = f32_to_bf16(hv * bf16_to_f32(nw[t]));
           }
-          if (i16 == 0 && tile < tiles) e.sq_parts[(size_t)r * tiles + tile] = sq;
+          if (ei == 0 && tile < tiles) e.sq_parts[(size_t)er * tiles + tile] = sq;
         }
-        if (y && n < N) y[(size_t)r * N + n] = d;
+        if (y && n < N) y[(size_t)er * N + n] = d;
       }
     }
   }
