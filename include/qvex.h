@@ -342,6 +342,20 @@ int qvex_assemble_ids(const int32_t* feed, const int32_t* drafts, int k, int32_t
 int qvex_cycle_finish(const int32_t* drafts, int k, const int32_t* n_accept, const int32_t* token,
                       int32_t* pend_ids, int32_t* feed, int32_t* n_prev, int32_t* out, void* stream);
 
+/* qvex_cycle_finish and the rest of a captured cycle's bookkeeping in one
+ * launch: ids_next[0] = token (the next verify input's first id, the drafts
+ * then being written straight into ids_next[1..k]), main_counters[i] +=
+ * n + main_extra for i < n_main (the verify commit of decode(),
+ * engine/speculative.py:94-101), mtp_counters[i] += mtp_delta (the draft
+ * steps' net advance), and u_out = u_table[*u_counter mod u_rows], then
+ * *u_counter += 1 (the next cycle's uniforms). Null pointers skip a part; every
+ * read happens before any write, so drafts may alias ids_next + 1. */
+int qvex_cycle_finish_ex(const int32_t* drafts, int k, const int32_t* n_accept, const int32_t* token,
+                         int32_t* pend_ids, int32_t* feed, int32_t* n_prev, int32_t* out,
+                         int32_t* ids_next, int32_t* main_counters, int n_main, int main_extra,
+                         int32_t* mtp_counters, int n_mtp, int mtp_delta, const float* u_table,
+                         int u_rows, int u_width, int32_t* u_counter, float* u_out, void* stream);
+
 /* out[0:width) = table[*counter mod rows]; then *counter += 1 (the cycle's
  * uniforms from a pre-drawn table). */
 int qvex_next_uniforms(const float* table, int rows, int width, int32_t* counter, float* out,

@@ -43,6 +43,44 @@ __global__ void cycle_finish_kernel(const int32_t* __restrict__ drafts, int k, c
   }
 }
 
+// cycle_finish plus the rest of the cycle's bookkeeping in the same launch:
+// ids_next[0] = tok (the next verify's first id), main_counters[i] += n + main_extra
+// (the verify commit), mtp_counters[i] += mtp_delta (the draft steps' net
+// advance), and u_out = table[*u_counter % rows], ++*u_counter (the next
+// cycle's uniforms). Null pointers skip a part.
+__global__ void cycle_finish_ex_kernel(const int32_t* __restrict__ drafts, int k, const int32_t* __restrict__ n_ptr,
+                                       const int32_t* __restrict__ tok_ptr, int32_t* __restrict__ pend_ids,
+                                       int32_t* __restrict__ feed, int32_t* __restrict__ n_prev,
+                                       int32_t* __restrict__ out, int32_t* __restrict__ ids_next,
+                                       int32_t* __restrict__ main_counters, int n_main, int main_extra,
+                                       int32_t* __restrict__ mtp_counters, int n_mtp, int mtp_delta,
+                                       const float* __restrict__ table, int rows, int width,
+                                       int32_t* __restrict__ u_counter, float* __restrict__ u_out) {
+  const int i = threadIdx.x;
+  const int n = *n_ptr, tok = *tok_ptr;
+  int32_t d = 0;
+  if (i < k) d = drafts[i];
+  int r = 0;
+  if (u_counter) r = ((*u_counter % rows) + rows) % rows;
+  __syncthreads();                       // every read of ids / the counter before the writes below
+  if (i <= k) pend_ids[i] = i < n ? (i < k ? d : 0) : (i == n ? tok : 0);
+  if (i < k) out[2 + i] = d;
+  if (main_counters)
+    for (int c = i; c < n_main; c += blockDim.x) main_counters[c] += n + main_extra;
+  if (mtp_counters)
+    for (int c = i; c < n_mtp; c += blockDim.x) mtp_counters[c] += mtp_delta;
+  if (u_out && i < width) u_out[i] = table[(long)r * width + i];
+  __syncthreads();
+  if (i == 0) {
+    *feed = tok;
+    *n_prev = n;
+    out[0] = n;
+    out[1] = tok;
+    if (ids_next) ids_next[0] = tok;
+    if (u_counter) *u_counter += 1;
+  }
+}
+
 // out[0 .. width) = table[*counter % rows]; then ++*counter
 __global__ void next_uniforms_kernel(const float* __restrict__ table, int rows, int width, int32_t* __restrict__ counter,
                                      float* __restrict__ out) {
@@ -105,5 +143,22 @@ extern "C" int qvex_next_uniforms(const float* table, int rows, int width, int32
   QVEX_CHECK_ARG(table && counter && out && rows >= 1 && width >= 1 && width <= 256, "qvex_next_uniforms: bad arguments");
   hipLaunchKernelGGL(next_uniforms_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, table, rows, width, counter, out);
   QVEX_CHECK_LAUNCH("qvex_next_uniforms");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_cycle_finish_ex(const int32_t* drafts, int k, const int32_t* n_accept, const int32_t* token,
+                                    int32_t* pend_ids, int32_t* feed, int32_t* n_prev, int32_t* out,
+                                    int32_t* ids_next, int32_t* main_counters, int n_main, int main_extra,
+                                    int32_t* mtp_counters, int n_mtp, int mtp_delta, const float* u_table,
+                                    int u_rows, int u_width, int32_t* u_counter, float* u_out, void* stream) {
+  QVEX_CHECK_ARG(drafts && n_accept && token && pend_ids && feed && n_prev && out && k >= 1 && k < 255,
+                 "qvex_cycle_finish_ex: bad arguments");
+  QVEX_CHECK_ARG((!main_counters || n_main >= 0) && (!mtp_counters || n_mtp >= 0) &&
+                     (!u_out || (u_table && u_counter && u_rows >= 1 && u_width >= 1 && u_width <= 256)),
+                 "qvex_cycle_finish_ex: bad counter or uniform arguments");
+  hipLaunchKernelGGL(cycle_finish_ex_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, drafts, k, n_accept, token,
+                     pend_ids, feed, n_prev, out, ids_next, main_counters, n_main, main_extra, mtp_counters, n_mtp,
+                     mtp_delta, u_table, u_rows, u_width, u_counter, u_out);
+  QVEX_CHECK_LAUNCH("qvex_cycle_finish_ex");
   return QVEX_OK;
 }

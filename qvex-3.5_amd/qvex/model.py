@@ -188,17 +188,20 @@ class QLinear:
             kernels.quantized_matmul(x2[m0:m1], self.w, self.scales, self.biases, out=o2[m0:m1])
         return out.view(*lead, self.N)
 
-    def residual(self, x: torch.Tensor, resid: torch.Tensor, norm_w: torch.Tensor, eps: float):
+    def residual(self, x: torch.Tensor, resid: torch.Tensor, norm_w: torch.Tensor, eps: float,
+                 h_out: torch.Tensor | None = None):
         """h = resid + x W^T and the next norm of h: returns (h, NormedRows) with
         the add and the norm's inputs in the product's epilogue (1..4 rows), or
-        (h, normalised tensor) through add_rms_norm otherwise."""
+        (h, normalised tensor) through add_rms_norm otherwise. h_out: where h goes."""
         x2 = x.reshape(-1, self.K)
         M = x2.shape[0]
+        ho = None if h_out is None else h_out.view(M, self.N)
         if (self.packed is not None and not self.swiglu_packed and M <= self.PACKED_MAX_ROWS
                 and NormedRows.supported(self.N)):
-            h, u, parts = kernels.qmv_packed_resid(x2, self.packed, self.N, resid.reshape(M, self.N), norm_w)
+            h, u, parts = kernels.qmv_packed_resid(x2, self.packed, self.N, resid.reshape(M, self.N), norm_w,
+                                                   h_out=ho)
             return h, NormedRows(u, parts, eps)
-        return add_rms_norm(resid.reshape(M, self.N), self(x2), norm_w, eps)
+        return add_rms_norm(resid.reshape(M, self.N), self(x2), norm_w, eps, h_out=ho)
 
     @staticmethod
     def fuse(layers: list["QLinear"], swiglu: bool = False) -> "QLinear":
@@ -544,12 +547,13 @@ class Layer:
         self.ln1, self.ln2 = p["input_layernorm"], p["post_attention_layernorm"]
         self.eps = cfg.rms_norm_eps
 
-    def fused(self, h, st, cache, keep_prev, next_w):
+    def fused(self, h, st, cache, keep_prev, next_w, h_out=None):
         """1..4 rows with the norms folded into the products: h the residual stream,
-        st its ln1 norm as NormedRows; returns the new stream and its norm by next_w."""
+        st its ln1 norm as NormedRows; returns the new stream (into h_out when
+        given) and its norm by next_w."""
         kw = dict(resid=h, norm_w=self.ln2, eps=self.eps)
         h2, st2 = self.mixer(st, cache, keep_prev, **kw) if self.linear else self.mixer(st, cache, **kw)
-        return self.mlp.down.residual(self.mlp.gate_up.swiglu(st2), h2, next_w, self.eps)
+        return self.mlp.down.residual(self.mlp.gate_up.swiglu(st2), h2, next_w, self.eps, h_out=h_out)
 
     def __call__(self, x, cache, keep_prev=False, normed=None):
         """x [L, H] residual stream. Returns the new residual stream."""
@@ -590,8 +594,9 @@ class Qwen35:
                                       capacity=cap, device=dev))
         return LayerCaches(caches, counters)
 
-    def __call__(self, ids, cache, last_only=True, return_hidden=False, keep_prev=False):
-        """ids: [1, L] int -> logits [1, L or 1, V] bf16 (and pre-norm hidden [1, L, H])."""
+    def __call__(self, ids, cache, last_only=True, return_hidden=False, keep_prev=False, hidden_out=None):
+        """ids: [1, L] int -> logits [1, L or 1, V] bf16 (and pre-norm hidden [1, L, H],
+        written into hidden_out when given)."""
         ids = torch.as_tensor(ids, device=self.norm.device).reshape(-1)
         L = ids.numel()
         counters = cache.counters
@@ -603,8 +608,9 @@ class Qwen35:
         if L > step:
             outs, hs = [], []
             for s0 in range(0, L, step):
+                ho = None if hidden_out is None else hidden_out.view(L, -1)[s0:s0 + step]
                 r = self(ids[s0:s0 + step].reshape(1, -1), cache, last_only=last_only and s0 + step >= L,
-                         return_hidden=return_hidden, keep_prev=keep_prev)
+                         return_hidden=return_hidden, keep_prev=keep_prev, hidden_out=ho)
                 if return_hidden:
                     outs.append(r[0]); hs.append(r[1])
                 else:
@@ -618,8 +624,9 @@ class Qwen35:
             # decode / verify: residual adds and norms ride on the products' epilogues
             h, st = x, NormedRows.of(x, self.layers[0].ln1, eps)
             for i, (layer, c) in enumerate(zip(self.layers, cache)):
-                nxt = self.layers[i + 1].ln1 if i + 1 < len(self.layers) else self.norm
-                h, st = layer.fused(h, st, c, keep_prev, nxt)
+                last = i + 1 == len(self.layers)
+                nxt = self.norm if last else self.layers[i + 1].ln1
+                h, st = layer.fused(h, st, c, keep_prev, nxt, h_out=hidden_out if last else None)
             logits = self.lm_head(st[-1:] if last_only else st).view(1, -1, self.cfg.vocab_size)
             return (logits, h.view(1, L, -1)) if return_hidden else logits
         n = rms_norm(x, self.layers[0].ln1, eps)
@@ -628,6 +635,9 @@ class Qwen35:
             nxt = self.layers[i + 1].ln1 if i + 1 < len(self.layers) else self.norm
             x, n = add_rms_norm(h, m, nxt, eps)
         hidden = x
+        if hidden_out is not None:
+            hidden_out.view(L, -1).copy_(hidden.view(L, -1))
+            hidden = hidden_out
         if last_only:
             n = n[-1:]
         logits = self.lm_head(n)

@@ -56,13 +56,21 @@ def draft_tokens(mtp: MTPHead, mtp_cache, h_in, id_in, k: int):
     return torch.cat(drafts)
 
 
-def _argmax(logits_row):
+_ZERO_U = {}
+
+
+def _argmax(logits_row, out=None):
+    """Greedy token of one logits row (first index of the maximum) -> int32 [1]
+    on the device, written into `out` (an int32 [1] view) when given."""
     from .sampler import to_f32
     from . import kernels
     t = to_f32(logits_row).reshape(1, 1, -1)
-    e_i = torch.empty((1, 0), dtype=torch.int32, device=t.device)
-    e_f = torch.empty((1, 0), dtype=torch.float32, device=t.device)
-    _, tok = kernels.spec_accept(t, None, e_i, e_f, torch.zeros(1, dtype=torch.float32, device=t.device), 0.0)
+    dev = t.device
+    if dev not in _ZERO_U:
+        _ZERO_U[dev] = torch.zeros(1, dtype=torch.float32, device=dev)
+    e_i = torch.empty((1, 0), dtype=torch.int32, device=dev)
+    e_f = torch.empty((1, 0), dtype=torch.float32, device=dev)
+    _, tok = kernels.spec_accept(t, None, e_i, e_f, _ZERO_U[dev], 0.0, out_token=out)
     return tok
 
 
@@ -188,12 +196,19 @@ class GraphedMTPCycle:
         self.n_prev = torch.tensor([P - 1], dtype=torch.int32, device=dev)
         self.n_prev_host = P - 1
         self.feed = dec.feed.to(torch.int32).reshape(1).clone()
+        # verify input [feed, d_0 .. d_{k-1}]: the drafts are written in place and
+        # the finishing kernel stores the next feed in slot 0
         self.ids = torch.empty((1, k + 1), dtype=torch.int32, device=dev)
+        self.ids[:, :1] = self.feed.view(1, 1)
+        self.drafts = self.ids[0, 1:]
         self.out = torch.zeros(2 + k, dtype=torch.int32, device=dev)
         self.zero = torch.zeros(1, dtype=torch.int32, device=dev)
         self.u_table = torch.from_numpy(dec.sampler.rng.random((table_rows, k + 1), dtype=np.float32)).to(dev)
         self.u_idx = torch.zeros(1, dtype=torch.int32, device=dev)
         self.u_buf = torch.empty(k + 1, dtype=torch.float32, device=dev)
+        # the first cycle's uniforms; each replay draws the next cycle's at its end
+        _C.call("qvex_next_uniforms", _ptr(self.u_table), self.u_table.shape[0], k + 1, _ptr(self.u_idx),
+                _ptr(self.u_buf), _stream())
         # device counters must hold the host values before they become authoritative
         cache.counters.sync()
         mc.counters.sync()
@@ -220,23 +235,23 @@ class GraphedMTPCycle:
         k, mtp, mc = self.k, d.mtp, d.mtp_cache
         logits, h = mtp(self.pend_h, self.pend_ids, mc, return_hidden=True, select=self.n_prev)
         self._commit(mc.counters, self.n_prev, 1)
-        drafts = [_argmax(logits[0, -1])]
-        for _ in range(1, k):
-            logits, h = mtp(h, drafts[-1].reshape(1, 1), mc, last_only=True, return_hidden=True)
-            self._commit(mc.counters, self.zero, 1)
-            drafts.append(_argmax(logits[0, -1]))
-        if k > 1:
-            self._commit(mc.counters, self.zero, -(k - 1))
-        self.drafts = torch.cat(drafts)
-        _C.call("qvex_assemble_ids", _ptr(self.feed), _ptr(self.drafts), k, _ptr(self.ids), _stream())
-        logits, hidden = d.model(self.ids, d.cache, last_only=False, return_hidden=True, keep_prev=True)
-        self.pend_h.copy_(hidden)
-        _C.call("qvex_next_uniforms", _ptr(self.u_table), self.u_table.shape[0], k + 1, _ptr(self.u_idx),
-                _ptr(self.u_buf), _stream())
+        _argmax(logits[0, -1], out=self.ids[0, 1:2])
+        for j in range(1, k):
+            logits, h = mtp(h, self.ids[:, j:j + 1], mc, last_only=True, return_hidden=True)
+            if j < k - 1:                        # the last step's advance folds into the finish
+                self._commit(mc.counters, self.zero, 1)
+            _argmax(logits[0, -1], out=self.ids[0, j + 1:j + 2])
+        logits, _ = d.model(self.ids, d.cache, last_only=False, return_hidden=True, keep_prev=True,
+                            hidden_out=self.pend_h)
         n, tok = d.sampler.accept_device(logits[0], self.drafts, self.u_buf)
-        self._commit(d.cache.counters, n, 1)
-        _C.call("qvex_cycle_finish", _ptr(self.drafts), k, _ptr(n), _ptr(tok), _ptr(self.pend_ids),
-                _ptr(self.feed), _ptr(self.n_prev), _ptr(self.out), _stream())
+        # verify commit (+n+1 on every main cache), the k - 1 speculative MTP
+        # entries rolled back (net -(k-2) after the folded last advance), the
+        # next feed and the next cycle's uniforms
+        _C.call("qvex_cycle_finish_ex", _ptr(self.drafts), k, _ptr(n), _ptr(tok), _ptr(self.pend_ids),
+                _ptr(self.feed), _ptr(self.n_prev), _ptr(self.out), _ptr(self.ids),
+                d.cache.counters.dev.data_ptr(), d.cache.counters.dev.numel(), 1,
+                mc.counters.dev.data_ptr(), mc.counters.dev.numel(), -(k - 2) if k > 1 else 0,
+                _ptr(self.u_table), self.u_table.shape[0], k + 1, _ptr(self.u_idx), _ptr(self.u_buf), _stream())
         d.sampler.observe_result(self.out)
 
     def cycle(self) -> list[int]:
