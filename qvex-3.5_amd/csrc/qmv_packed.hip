@@ -403,26 +403,30 @@ qmv_packed_fn pick_packed(int tn, int ws, int np) {
 }
 
 // Full prefetch when a wave's sets fit: the smallest NP in {2, 4, 6, 8} holding
-// ceil(GS / WS) sets, with at most 8 records (TN * NP) of registers per wave.
+// ceil(GS / WS) sets, with at most 4 records (TN * NP) of registers per wave
+// (more costs occupancy: measured on gate_up (2,4), 13.3 us two-deep vs 13.8).
 int packed_prefetch_depth(int K, int TN, int WS) {
   const int S = (K / PK_SET + WS - 1) / WS;
   if (WS < 2) return 0;
   for (int np = 2; np <= 8; np += 2)
-    if (S <= np && TN * np <= 8) return np;
+    if (S <= np && TN * np <= 4) return np;
   return 0;
 }
 
 // Tile choice from (N, K) only, so a row's bits never depend on M. Two tiles per
-// wave once there are enough rows to keep every CU busy; waves split K until the
-// launch holds ~2048 waves (8 per CU), keeping at least 2 sets per wave and at
-// least two waves per tile when K has 8 sets or more (measured on the 9B shapes:
-// gate_up (2,4), down (1,8), in_proj (1,4), o_proj (1,8), lm_head (2,2)).
+// wave from ~700 tiles up; waves split K until the launch holds ~4096 waves
+// (one tile per wave, up to 16 waves per tile) or ~3072 (two tiles), keeping at
+// least 2 sets per wave. Measured on the 9B shapes (M = 4 / 1, us): down
+// (1,16) 9.7 / 8.5, in_proj (2,8) 9.6 / 8.9, qkv (1,8) 8.4 / 7.5, o_proj (1,8)
+// 5.2 / 4.8, gate_up (2,4) 13.3 / 12.9, mtp fc (1,16) 7.1 / 6.4, lm_head (2,2).
 void packed_default_tile(int N, int K, int* TN, int* WS) {
   const long tiles = (N + PK_TILE - 1) / PK_TILE;
   const int GS = K / PK_SET;
-  const int tn = tiles >= 1024 ? 2 : 1;
+  const int tn = tiles >= 704 ? 2 : 1;
+  const long limit = tn == 1 ? 4096 : 3072;
+  const int ws_max = tn == 1 ? 16 : 8;
   int ws = GS >= 8 ? 2 : 1;
-  while (ws < 8 && (tiles / tn) * ws < 2048 && GS >= 2 * (ws * 2)) ws *= 2;
+  while (ws < ws_max && (tiles / tn) * ws < limit && GS >= 2 * (ws * 2)) ws *= 2;
   *TN = tn;
   *WS = ws;
 }

@@ -100,9 +100,10 @@ def test_packed_swiglu_equals_product_then_swiglu(M, N, K):
 def default_tile(N, K):
     """The tile qvex_qmv_w4g64_packed picks (packed_default_tile)."""
     tiles, GS = (N + 15) // 16, K // 256
-    tn = 2 if tiles >= 1024 else 1
+    tn = 2 if tiles >= 704 else 1
+    limit, ws_max = (4096, 16) if tn == 1 else (3072, 8)
     ws = 2 if GS >= 8 else 1
-    while ws < 8 and (tiles // tn) * ws < 2048 and GS >= 2 * (ws * 2):
+    while ws < ws_max and (tiles // tn) * ws < limit and GS >= 2 * (ws * 2):
         ws *= 2
     return tn, ws
 
