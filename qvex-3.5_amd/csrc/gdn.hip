@@ -313,8 +313,8 @@ __global__ __launch_bounds__(FUSED_THREADS) void gdn_decode_fused_kernel(GdnFuse
         o0.z = __float_as_uint(st[r][2]); o0.w = __float_as_uint(st[r][3]);
         o1.x = __float_as_uint(st[r][4]); o1.y = __float_as_uint(st[r][5]);
         o1.z = __float_as_uint(st[r][6]); o1.w = __float_as_uint(st[r][7]);
-        *reinterpret_cast<u32x4*>(dstp) = o0;
-        *reinterpret_cast<u32x4*>(dstp + 4) = o1;
+        __builtin_nontemporal_store(o0, reinterpret_cast<u32x4*>(dstp));
+        __builtin_nontemporal_store(o1, reinterpret_cast<u32x4*>(dstp + 4));
       }
     }
   }
