@@ -242,6 +242,16 @@ int qvex_spec_accept_filtered(const float* target, const float* draft, const int
                               const float* seen, float presence_penalty, int top_k, float top_p,
                               int32_t* n_accept, int32_t* out_token, int S, int k, int V,
                               void* workspace, uint64_t workspace_bytes, void* stream);
+/* The same on bf16 logits as the lm_head writes them (target and draft both
+ * bf16): every value widens exactly to fp32 on load, so the results equal
+ * qvex_spec_accept_filtered on the fp32 copies (Sampler.scores' astype(float32),
+ * engine/sampler.py:151) without making them. */
+int qvex_spec_accept_filtered_bf16(const uint16_t* target, const uint16_t* draft,
+                                   const int32_t* draft_ids, const float* u_accept,
+                                   const float* u_sample, float inv_temp, const float* seen,
+                                   float presence_penalty, int top_k, float top_p,
+                                   int32_t* n_accept, int32_t* out_token, int S, int k, int V,
+                                   void* workspace, uint64_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Verify-forward glue (Qwen3.5 hybrid stack, engine/model.py). bf16 storage,

@@ -14,6 +14,7 @@
 #define QVEX_WAVE 64
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // 16-byte streaming load (nontemporal: the data is used once).
 __device__ __forceinline__ u32x4 load_nt16(const void* p) {

@@ -95,8 +95,8 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 }
 
 struct SpecArgs {
-  const float* target;    // [S, k+1, V]
-  const float* draft;     // [S, k, V] or nullptr
+  const void* target;     // [S, k+1, V] fp32, or bf16 when bf
+  const void* draft;      // [S, k, V] or nullptr, same type
   const int32_t* ids;     // [S, k]
   const float* u_acc;     // [S, k]
   const float* u_smp;     // [S]
@@ -112,11 +112,18 @@ struct SpecArgs {
   float top_p;            // top-p when 0 < top_p < 1 (needs top_k)
   float* fws;             // [S * (k+1), P, top_k + 1] part lists + tie counts
   float* frow;            // [S * (k+1), 4] (c_0, S_p, cutoff)
+  int bf;                 // logits are bf16 (widened exactly to fp32 on load)
 };
 
-__device__ __forceinline__ const float* row_ptr(const SpecArgs& a, int step, int i) {
-  if (i <= a.k) return a.target + ((long)step * (a.k + 1) + i) * a.V;
-  return a.draft + ((long)step * a.k + (i - a.k - 1)) * a.V;
+__device__ __forceinline__ const void* row_ptr(const SpecArgs& a, int step, int i) {
+  const long es = a.bf ? 2 : 4;
+  if (i <= a.k) return (const char*)a.target + ((long)step * (a.k + 1) + i) * a.V * es;
+  return (const char*)a.draft + ((long)step * a.k + (i - a.k - 1)) * a.V * es;
+}
+
+// Logit j of a row as fp32 (bf16 rows widen exactly).
+__device__ __forceinline__ float lg(const void* row, long j, int bf) {
+  return bf ? bf16_to_f32(reinterpret_cast<const uint16_t*>(row)[j]) : reinterpret_cast<const float*>(row)[j];
 }
 
 // Presence penalty of a target row at token j: x - pen * s(j), s(j) = 1 for the
@@ -201,13 +208,14 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
 
 // ---------------------------------------------------------------- kernel 1: part statistics
 
+template <bool BF>
 __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
   __shared__ float red[4];
   __shared__ int redi[4];
   const int p = blockIdx.x;
   const int row = blockIdx.y;
   const int step = row / a.rps, i = row % a.rps;
-  const float* src = row_ptr(a, step, i);
+  const void* src = row_ptr(a, step, i);
   const int base = p * PART;
   const int end = min(a.V, base + PART);
   const int t = threadIdx.x;
@@ -219,11 +227,20 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
     const int j = base + 4 * (t + NT * it);
     ok[it] = j < end;
     if (ok[it]) {
-      const u32x4 v = load_nt16(src + j);
-      x[it][0] = __uint_as_float(v.x);
-      x[it][1] = __uint_as_float(v.y);
-      x[it][2] = __uint_as_float(v.z);
-      x[it][3] = __uint_as_float(v.w);
+      if constexpr (BF) {
+        const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(
+            reinterpret_cast<const uint16_t*>(src) + j));
+        x[it][0] = bf16_lo(v.x);
+        x[it][1] = bf16_hi(v.x);
+        x[it][2] = bf16_lo(v.y);
+        x[it][3] = bf16_hi(v.y);
+      } else {
+        const u32x4 v = load_nt16(reinterpret_cast<const float*>(src) + j);
+        x[it][0] = __uint_as_float(v.x);
+        x[it][1] = __uint_as_float(v.y);
+        x[it][2] = __uint_as_float(v.z);
+        x[it][3] = __uint_as_float(v.w);
+      }
     }
   }
   const bool tgt = i <= a.k;
@@ -402,8 +419,9 @@ __global__ __launch_bounds__(NT) void spec_filter_kernel(SpecArgs a) {
 // ---------------------------------------------------------------- kernel 2: accept + sample
 
 struct WCtx {
-  const float* tp;
-  const float* tq;
+  const void* tp;
+  const void* tq;
+  int bf;
   int d;
   int mode;   // 0 residual, 1 plain p
   float inv_temp, mp, sp, mq, sq;
@@ -415,12 +433,12 @@ struct WCtx {
 };
 
 __device__ __forceinline__ float weight(const WCtx& c, int j) {
-  const float z = pen_x(c.seen, c.pen, c.tp[j], j, c.extra, c.n_extra) * c.inv_temp;
+  const float z = pen_x(c.seen, c.pen, lg(c.tp, j, c.bf), j, c.extra, c.n_extra) * c.inv_temp;
   const float ep = z >= c.cutoff ? qx_expf(z - c.mp) : 0.0f;
   if (c.mode == 1) return ep;
   float eq, Sq;
   if (c.tq) {
-    eq = qx_expf(c.tq[j] * c.inv_temp - c.mq);
+    eq = qx_expf(lg(c.tq, j, c.bf) * c.inv_temp - c.mq);
     Sq = c.sq;
   } else {
     eq = (j == c.d) ? 1.0f : 0.0f;
@@ -571,11 +589,11 @@ __global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
       for (int i = 0; i < k; ++i) {
         const int di = d[i];
         if (di < 0 || di >= a.V) { n = i; break; }
-        const float zd = pen_x(a.seen, a.pen, row_ptr(a, step, i)[di], di, d, i) * a.inv_temp;
+        const float zd = pen_x(a.seen, a.pen, lg(row_ptr(a, step, i), di, a.bf), di, d, i) * a.inv_temp;
         const float ep = zd >= rc[i] ? qx_expf(zd - rm[i]) : 0.0f;
         float eq = 1.0f, Sq = 1.0f;
         if (a.draft) {
-          eq = qx_expf(row_ptr(a, step, k + 1 + i)[di] * a.inv_temp - rm[k + 1 + i]);
+          eq = qx_expf(lg(row_ptr(a, step, k + 1 + i), di, a.bf) * a.inv_temp - rm[k + 1 + i]);
           Sq = rs[k + 1 + i];
         }
         const float lhs = a.u_acc[(long)step * k + i] * eq * rs[i];
@@ -598,6 +616,7 @@ __global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
   WCtx c;
   c.inv_temp = a.inv_temp;
   c.tp = row_ptr(a, step, n);
+  c.bf = a.bf;
   c.mp = rm[n];
   c.sp = rs[n];
   c.cutoff = rc[n];
@@ -660,6 +679,7 @@ __global__ __launch_bounds__(NT) void spec_sample_kernel(SpecArgs a) {
   WCtx c;
   c.inv_temp = a.inv_temp;
   c.tp = row_ptr(a, step, n);
+  c.bf = a.bf;
   c.d = __float_as_int(dd[1]);
   c.mp = dd[2]; c.sp = dd[3]; c.mq = dd[4]; c.sq = dd[5];
   c.cutoff = dd[6];
@@ -758,11 +778,10 @@ extern "C" uint64_t qvex_spec_accept_workspace_bytes(int S, int k, int V, int ha
   return qvex_spec_accept_filtered_workspace_bytes(S, k, V, has_draft, 0);
 }
 
-extern "C" int qvex_spec_accept_filtered(const float* target, const float* draft, const int32_t* draft_ids,
-                                         const float* u_accept, const float* u_sample, float inv_temp,
-                                         const float* seen, float presence_penalty, int top_k, float top_p,
-                                         int32_t* n_accept, int32_t* out_token, int S, int k, int V,
-                                         void* workspace, uint64_t workspace_bytes, void* stream) {
+static int spec_accept_impl(const void* target, const void* draft, int bf, const int32_t* draft_ids,
+                            const float* u_accept, const float* u_sample, float inv_temp, const float* seen,
+                            float presence_penalty, int top_k, float top_p, int32_t* n_accept, int32_t* out_token,
+                            int S, int k, int V, void* workspace, uint64_t workspace_bytes, void* stream) {
   QVEX_CHECK_ARG(S >= 1 && k >= 0 && k <= 32, "qvex_spec_accept: S=%d k=%d (need S >= 1, 0 <= k <= 32)", S, k);
   QVEX_CHECK_ARG(V >= 4 && V % 4 == 0, "qvex_spec_accept: V=%d must be a positive multiple of 4", V);
   QVEX_CHECK_ARG(target && n_accept && out_token && workspace, "qvex_spec_accept: null pointer");
@@ -793,9 +812,12 @@ extern "C" int qvex_spec_accept_filtered(const float* target, const float* draft
   float* fws = (float*)workspace + base;
   float* frow = fws + (uint64_t)S * (k + 1) * P * (kf + 1);
   SpecArgs a{target, draft, draft_ids, u_accept, u_sample, inv_temp, greedy, n_accept, out_token,
-             (float*)workspace, S, k, V, P, rps, seen, presence_penalty, kf, top_p, fws, frow};
+             (float*)workspace, S, k, V, P, rps, seen, presence_penalty, kf, top_p, fws, frow, bf};
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(spec_rowstats_kernel, dim3(P, S * rps), dim3(NT), 0, st, a);
+  if (a.bf)
+    hipLaunchKernelGGL(spec_rowstats_kernel<true>, dim3(P, S * rps), dim3(NT), 0, st, a);
+  else
+    hipLaunchKernelGGL(spec_rowstats_kernel<false>, dim3(P, S * rps), dim3(NT), 0, st, a);
   QVEX_CHECK_LAUNCH("qvex_spec_accept/rowstats");
   if (kf > 0) {
     hipLaunchKernelGGL(spec_filter_kernel, dim3(S * (k + 1)), dim3(NT), 0, st, a);
@@ -808,6 +830,25 @@ extern "C" int qvex_spec_accept_filtered(const float* target, const float* draft
     QVEX_CHECK_LAUNCH("qvex_spec_accept/sample");
   }
   return QVEX_OK;
+}
+
+extern "C" int qvex_spec_accept_filtered(const float* target, const float* draft, const int32_t* draft_ids,
+                                         const float* u_accept, const float* u_sample, float inv_temp,
+                                         const float* seen, float presence_penalty, int top_k, float top_p,
+                                         int32_t* n_accept, int32_t* out_token, int S, int k, int V,
+                                         void* workspace, uint64_t workspace_bytes, void* stream) {
+  return spec_accept_impl(target, draft, 0, draft_ids, u_accept, u_sample, inv_temp, seen, presence_penalty, top_k,
+                          top_p, n_accept, out_token, S, k, V, workspace, workspace_bytes, stream);
+}
+
+extern "C" int qvex_spec_accept_filtered_bf16(const uint16_t* target, const uint16_t* draft,
+                                              const int32_t* draft_ids, const float* u_accept,
+                                              const float* u_sample, float inv_temp, const float* seen,
+                                              float presence_penalty, int top_k, float top_p, int32_t* n_accept,
+                                              int32_t* out_token, int S, int k, int V, void* workspace,
+                                              uint64_t workspace_bytes, void* stream) {
+  return spec_accept_impl(target, draft, 1, draft_ids, u_accept, u_sample, inv_temp, seen, presence_penalty, top_k,
+                          top_p, n_accept, out_token, S, k, V, workspace, workspace_bytes, stream);
 }
 
 extern "C" int qvex_spec_accept(const float* target, const float* draft, const int32_t* draft_ids,

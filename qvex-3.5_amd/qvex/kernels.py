@@ -307,18 +307,22 @@ def spec_accept(target: torch.Tensor, draft: torch.Tensor | None, draft_ids: tor
                 presence_penalty: float = 0.0, top_k: int = 0, top_p: float = 1.0):
     """Fused accept / residual-resample / bonus sampling for S verify steps.
 
-    target fp32 [S,k+1,V]; draft fp32 [S,k,V] or None (greedy one-hot drafts, the
-    reference's rule, engine/speculative.py:79-80); draft_ids int32 [S,k];
+    target fp32 or bf16 [S,k+1,V]; draft [S,k,V] of the same dtype or None (greedy
+    one-hot drafts, the reference's rule, engine/speculative.py:79-80); bf16
+    logits are read as they are (exact widening, same results as their fp32
+    copies); draft_ids int32 [S,k];
     u_accept fp32 [S,k]; u_sample fp32 [S]; temperature <= 0 means greedy.
     The target rows are scored as Sampler.scores (engine/sampler.py:30-52):
     presence penalty over `seen` (fp32 [V], 0/1) plus the drafts before each row,
     then top-k (0..64, 0 = off) and top-p (needs top-k) when sampling.
     Returns (n_accept int32 [S], out_token int32 [S]) on the device."""
-    _check(target, "target", torch.float32, 3)
+    bf = target.dtype == torch.bfloat16
+    ldt = torch.bfloat16 if bf else torch.float32
+    _check(target, "target", ldt, 3)
     S, k1, V = target.shape
     k = k1 - 1
     if draft is not None:
-        _check(draft, "draft", torch.float32, 3)
+        _check(draft, "draft", ldt, 3)
         if draft.shape != (S, k, V):
             raise _C.QvexError(f"draft must be [S,k,V]=({S},{k},{V})")
     _check(draft_ids, "draft_ids", torch.int32)
@@ -339,7 +343,8 @@ def spec_accept(target: torch.Tensor, draft: torch.Tensor | None, draft_ids: tor
             raise _C.QvexError(f"seen must hold V={V} values")
     if workspace is None:
         workspace = spec_workspace(S, k, V, draft is not None, dev, top_k)
-    _C.call("qvex_spec_accept_filtered", _ptr(target), _ptr(draft) if draft is not None else None,
+    _C.call("qvex_spec_accept_filtered_bf16" if bf else "qvex_spec_accept_filtered", _ptr(target),
+            _ptr(draft) if draft is not None else None,
             _ptr(draft_ids), _ptr(u_accept), _ptr(u_sample), inv_temp,
             _ptr(seen) if seen is not None else None, float(np.float32(presence_penalty)), int(top_k),
             float(np.float32(top_p)), _ptr(n_accept), _ptr(out_token), S, k, V, _ptr(workspace),

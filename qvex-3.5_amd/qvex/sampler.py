@@ -106,8 +106,9 @@ class Sampler:
 
     def accept_device(self, target: torch.Tensor, draft_ids: torch.Tensor, u: torch.Tensor):
         """accept() with the k + 1 uniforms given as a device fp32 [k+1] tensor
-        (no host RNG, so the call can be captured in a graph)."""
-        t = to_f32(target).reshape(1, -1, self.V)
+        (no host RNG, so the call can be captured in a graph). bf16 logits are
+        read in place."""
+        t = as_logits(target).reshape(1, -1, self.V)
         k = t.shape[1] - 1
         return kernels.spec_accept(t, None, draft_ids.reshape(1, k), u[:k].reshape(1, k), u[k:],
                                    self.p.temperature, workspace=self._workspace(1, k, False, t.device),
@@ -115,7 +116,7 @@ class Sampler:
 
     def pick(self, logits: torch.Tensor) -> torch.Tensor:
         """One token per row of logits [R, V] (argmax when greedy) -> int32 [R]."""
-        t = to_f32(logits).reshape(-1, 1, self.V)
+        t = as_logits(logits).reshape(-1, 1, self.V)
         R = t.shape[0]
         empty_i = torch.empty((R, 0), dtype=torch.int32, device=t.device)
         empty_f = torch.empty((R, 0), dtype=torch.float32, device=t.device)
@@ -147,6 +148,13 @@ class Sampler:
         seen = self._filter(result.device)["seen"]
         _C.call("qvex_mark_seen", seen.data_ptr(), self.V, result[1:].data_ptr(), result.numel() - 1,
                 result.data_ptr(), 1, kernels._stream())
+
+
+def as_logits(x: torch.Tensor) -> torch.Tensor:
+    """Logits as the accept kernels take them: bf16 or fp32 as they are (contiguous)."""
+    if x.dtype in (torch.bfloat16, torch.float32):
+        return x.contiguous()
+    raise _C.QvexError(f"logits must be bf16 or fp32 (got {x.dtype})")
 
 
 def to_f32(x: torch.Tensor) -> torch.Tensor:

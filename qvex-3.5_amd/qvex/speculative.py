@@ -62,9 +62,9 @@ _ZERO_U = {}
 def _argmax(logits_row, out=None):
     """Greedy token of one logits row (first index of the maximum) -> int32 [1]
     on the device, written into `out` (an int32 [1] view) when given."""
-    from .sampler import to_f32
+    from .sampler import as_logits
     from . import kernels
-    t = to_f32(logits_row).reshape(1, 1, -1)
+    t = as_logits(logits_row).reshape(1, 1, -1)
     dev = t.device
     if dev not in _ZERO_U:
         _ZERO_U[dev] = torch.zeros(1, dtype=torch.float32, device=dev)

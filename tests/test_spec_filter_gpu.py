@@ -81,3 +81,28 @@ def test_filtered_tokens_stay_in_the_kept_set():
         z = target[s, 0] * np.float32(inv(T))
         kth = np.sort(z)[::-1][9]
         assert z[tok[s]] >= kth
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("S,k,V,T,top_k,top_p,pen,dl", [
+    (1, 3, 248320, 0.7, 20, 0.8, 0.0, False),
+    (1, 3, 248320, 0.0, 0, 1.0, 0.0, False),
+    (2, 4, 50000, 1.0, 0, 1.0, 0.5, True),
+    (1, 0, 4096, 0.6, 64, 0.95, 1.5, False),
+    (3, 2, 4100, 0.0, 0, 1.0, 1.0, False),
+])
+def test_bf16_logits_equal_their_fp32_copies(S, k, V, T, top_k, top_p, pen, dl):
+    """qvex_spec_accept_filtered_bf16 on bf16 logits == the fp32 entry on the same
+    values widened (exact), bit for bit in n and token."""
+    target, draft, ids, ua, us, seen = make_case(S, k, V, seed=S * 31 + k + V, bf16=True, draft_logits=dl)
+    if draft is not None:
+        draft = synth.bf16_to_f32(synth.bf16_bits(draft))
+    t32 = torch.from_numpy(target).to(DEV)
+    d32 = torch.from_numpy(draft).to(DEV) if draft is not None else None
+    args = (torch.from_numpy(ids).to(DEV), torch.from_numpy(ua).to(DEV), torch.from_numpy(us).to(DEV), T)
+    kw = dict(seen=torch.from_numpy(seen).to(DEV) if pen else None, presence_penalty=pen, top_k=top_k, top_p=top_p)
+    n1, tok1 = kernels.spec_accept(t32, d32, *args, **kw)
+    n2, tok2 = kernels.spec_accept(t32.to(torch.bfloat16), None if d32 is None else d32.to(torch.bfloat16),
+                                   *args, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(n1, n2) and torch.equal(tok1, tok2)
