@@ -105,13 +105,15 @@ def default_tile(N, K):
     ws = 2 if GS >= 8 else 1
     while ws < ws_max and (tiles // tn) * ws < limit and GS >= 2 * (ws * 2):
         ws *= 2
+    if tiles // tn >= 4096 and GS >= 8 and ws < 4:
+        ws = 4
     return tn, ws
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("M", [1, 4])
 @pytest.mark.parametrize("N,K", [(4096, 12288), (12352, 4096), (4096, 4096), (24576, 4096), (4096, 8192),
-                                 (531, 2304), (17, 512), (4096, 256), (100, 1280)])
+                                 (531, 2304), (17, 512), (4096, 256), (100, 1280), (131072, 2048)])
 def test_prefetch_pipeline_equals_double_buffer(M, N, K):
     """The default entry (all of a wave's sets in flight when they fit) and the
     explicit-tile entry (two-deep pipeline) with the same tile give the same bits."""
