@@ -189,6 +189,9 @@ __global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t* __rest
 // (token, head); lane holds elements lane + 64 i. RoPE (NeoX form, the
 // non-traditional mx.fast.rope): for i < rot/2, (x_i, x_{i+rot/2}) rotated by
 // pos * theta^(-2i/rot); dims >= rot pass through. pos = *pos0 + l.
+// PER = D / 64 elements per lane, a template parameter so that every load of the
+// wave (row, norm weights, the V row) is issued before the first is waited on.
+template <int PER>
 __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
     const uint16_t* __restrict__ proj, long p_stride, const uint16_t* __restrict__ q_norm,
     const uint16_t* __restrict__ k_norm, const int32_t* __restrict__ pos0, int Hq, int Hkv, int D,
@@ -202,16 +205,22 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
   const uint16_t* src = isq ? proj + (size_t)l * p_stride + (size_t)h * 2 * D
                             : proj + (size_t)l * p_stride + (size_t)Hq * 2 * D + (size_t)kh * D;
   const uint16_t* nw = isq ? q_norm : k_norm;
-  const int per = D / 64;  // elements per lane (D % 64 == 0)
-  float x[8];
-  float ss = 0.0f;
-  for (int i = 0; i < per; ++i) {
+  const uint16_t* vs = proj + (size_t)l * p_stride + (size_t)Hq * 2 * D + (size_t)Hkv * D + (size_t)kh * D;
+  float x[PER];
+  uint16_t wv[PER], vv[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
     x[i] = bf16_to_f32(src[lane + 64 * i]);
-    ss = fmaf(x[i], x[i], ss);
+    wv[i] = nw[lane + 64 * i];
+    vv[i] = isq ? (uint16_t)0 : vs[lane + 64 * i];
   }
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) ss = fmaf(x[i], x[i], ss);
   ss = wave_allsum(ss);
   const float inv = rsqrtf(ss / (float)D + eps);
-  for (int i = 0; i < per; ++i) x[i] = bf16_to_f32(f32_to_bf16(bf16_to_f32(nw[lane + 64 * i]) * (x[i] * inv)));
+#pragma unroll
+  for (int i = 0; i < PER; ++i) x[i] = bf16_to_f32(f32_to_bf16(bf16_to_f32(wv[i]) * (x[i] * inv)));
   // rotary part lives in element slot 0 (lane < 64 <= rot requires rot <= 64)
   const int half = rot / 2;
   if (rot > 0) {
@@ -226,15 +235,16 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
   }
   if (isq) {
     uint16_t* dst = q_out + ((size_t)l * Hq + h) * D;
-    for (int i = 0; i < per; ++i) dst[lane + 64 * i] = f32_to_bf16(x[i]);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) dst[lane + 64 * i] = f32_to_bf16(x[i]);
   } else if (pos >= 0 && pos < cap) {
     // K key-major [Hkv, cap, D]; V dim-major [Hkv, D, cap] (the P.V MFMA reads
     // 8 consecutive keys of one dim per lane)
     uint16_t* kd = k_cache + ((size_t)kh * cap + pos) * D;
-    const uint16_t* vs = proj + (size_t)l * p_stride + (size_t)Hq * 2 * D + (size_t)Hkv * D + (size_t)kh * D;
-    for (int i = 0; i < per; ++i) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
       kd[lane + 64 * i] = f32_to_bf16(x[i]);
-      v_cache[((size_t)kh * D + lane + 64 * i) * cap + pos] = vs[lane + 64 * i];
+      v_cache[((size_t)kh * D + lane + 64 * i) * cap + pos] = vv[i];
     }
   }
 }
@@ -609,8 +619,19 @@ extern "C" int qvex_attn_qk_rope(const uint16_t* proj, long p_stride, const uint
                      rot_dim <= 64 && rot_dim % 2 == 0 && cap >= 1,
                  "qvex_attn_qk_rope: L=%d Hq=%d Hkv=%d D=%d rot=%d", L, Hq, Hkv, D, rot_dim);
   QVEX_CHECK_ARG(p_stride >= (long)Hq * 2 * D + 2L * Hkv * D, "qvex_attn_qk_rope: p_stride too small");
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(L, Hq + Hkv), dim3(64), 0, (hipStream_t)stream, proj, p_stride,
-                     q_norm, k_norm, pos0, Hq, Hkv, D, rot_dim, theta, eps, q_out, k_cache, v_cache, cap);
+  decltype(&qk_norm_rope_kernel<1>) fn = nullptr;
+  switch (D / 64) {
+    case 1: fn = qk_norm_rope_kernel<1>; break;
+    case 2: fn = qk_norm_rope_kernel<2>; break;
+    case 3: fn = qk_norm_rope_kernel<3>; break;
+    case 4: fn = qk_norm_rope_kernel<4>; break;
+    case 5: fn = qk_norm_rope_kernel<5>; break;
+    case 6: fn = qk_norm_rope_kernel<6>; break;
+    case 7: fn = qk_norm_rope_kernel<7>; break;
+    case 8: fn = qk_norm_rope_kernel<8>; break;
+  }
+  hipLaunchKernelGGL(fn, dim3(L, Hq + Hkv), dim3(64), 0, (hipStream_t)stream, proj, p_stride, q_norm, k_norm, pos0,
+                     Hq, Hkv, D, rot_dim, theta, eps, q_out, k_cache, v_cache, cap);
   QVEX_CHECK_LAUNCH("qvex_attn_qk_rope");
   return QVEX_OK;
 }
