@@ -122,6 +122,19 @@ int qvex_qmv_w4g64_packed_rstd(const uint16_t* u, const void* packed, uint16_t* 
                                int swiglu, void* stream);
 int qvex_rms_parts(const uint16_t* x, const uint16_t* norm_w, uint16_t* u_out, float* sq_parts,
                    int M, int D, void* stream);
+/* Greedy drafting on the lm_head (the argmax of `_argmax` / Sampler.pick with
+ * temperature 0, engine/sampler.py:30-58, over mx.quantized_matmul's bf16
+ * logits): out_token[r] = the first index of the largest bf16-rounded output
+ * of row r of x W^T, without writing the product. The packed kernel's epilogue
+ * keeps each 16-row tile's (max, first index); a one-block-per-row kernel
+ * takes the first tile holding the row maximum. With sq_parts the rows are
+ * scaled as qvex_qmv_w4g64_packed_rstd does (x = u of the final norm).
+ * workspace: qvex_qmv_w4g64_argmax_workspace_bytes(M, N) = M * ceil(N/16) * 8. */
+uint64_t qvex_qmv_w4g64_argmax_workspace_bytes(int M, int N);
+int qvex_qmv_w4g64_packed_argmax(const uint16_t* x, const void* packed, int M, int N, int K,
+                                 const float* sq_parts, int nparts, int dim, float eps,
+                                 int32_t* out_token, void* workspace, uint64_t workspace_bytes,
+                                 void* stream);
 /* The same with an explicit tile: tiles_per_wave in {1,2,4} 16-row tiles,
  * wave_ksplit in {1,2,4,8} (16 with one tile) waves splitting the 256-k sets,
  * and the load pipeline: prefetch_sets = 0 keeps two sets in flight per wave,

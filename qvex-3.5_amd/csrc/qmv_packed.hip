@@ -87,6 +87,26 @@ __global__ __launch_bounds__(64) void pack_kernel(const uint32_t* __restrict__ w
   *reinterpret_cast<uint32_t*>(rec + PK_WBYTES + L * 4) = sb;
 }
 
+// Max / min over the 16 lanes of a DPP row, the same in all 16 lanes.
+__device__ __forceinline__ float row16_allmax(float v) {
+  v = fmaxf(v, dpp_row<0xB1>(v));
+  v = fmaxf(v, dpp_row<0x4E>(v));
+  v = fmaxf(v, dpp_row<0x124>(v));
+  v = fmaxf(v, dpp_row<0x128>(v));
+  return v;
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_row_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ int row16_allmin(int v) {
+  v = min(v, dpp_row_i<0xB1>(v));
+  v = min(v, dpp_row_i<0x4E>(v));
+  v = min(v, dpp_row_i<0x124>(v));
+  v = min(v, dpp_row_i<0x128>(v));
+  return v;
+}
+
 // Optional epilogues that take the residual RMSNorm out of its own launch
 // (mx.fast.rms_norm after the residual add, engine/model.py:309-317). The norm's
 // per-row scale rsqrt(mean(h^2) + eps) commutes with the product, so:
@@ -99,6 +119,7 @@ __global__ __launch_bounds__(64) void pack_kernel(const uint32_t* __restrict__ w
 //     rs_nparts (<= 256, a multiple of 4) partials in a fixed order (lane l adds
 //     parts 4l .. 4l+3, then an xor butterfly over the wave).
 // The product itself is unchanged, so the rows stay independent of M.
+// An argmax epilogue (greedy drafting on the lm_head) is below.
 struct PkEpi {
   const float* rs_parts;
   int rs_nparts, rs_dim;
@@ -108,6 +129,9 @@ struct PkEpi {
   uint16_t* h_out;
   uint16_t* u_out;
   float* sq_parts;
+  // argmax (am_parts != null): per row r and 16-row tile j, the largest
+  // bf16-rounded output and its first index -> am_parts[(r * tiles + j) * 2 + {0, 1}]
+  float* am_parts;
 };
 
 constexpr int pk_block(int WS) { return WS >= 4 ? 64 * WS : 256; }   // WS = 16: 1024 threads
@@ -345,8 +369,61 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
           if (ei == 0 && tile < tiles) e.sq_parts[(size_t)er * tiles + tile] = sq;
         }
         if (y && n < N) y[(size_t)er * N + n] = d;
+        if (e.am_parts) {
+          // the tile's largest rounded output and its first column (whole DPP rows active)
+          const float v = n < N ? bf16_to_f32(d) : -__builtin_inff();
+          const float m = row16_allmax(v);
+          const int j = row16_allmin(n < N && v == m ? n : 0x7fffffff);
+          if (ei == 0 && tile < tiles) {
+            e.am_parts[((size_t)er * tiles + tile) * 2] = m;
+            e.am_parts[((size_t)er * tiles + tile) * 2 + 1] = __int_as_float(j);
+          }
+        }
       }
     }
+  }
+}
+
+// Row r's first index of its largest output from the per-tile (max, first index)
+// pairs, tiles in index order: thread t takes tiles t + AM_T * i (all its loads
+// issued at once), keeps the largest value and, on a tie, the smaller index;
+// the block then does the same over its threads.
+constexpr int AM_T = 1024;
+constexpr int AM_PER = 16;   // tiles per thread per round: 16384 tiles (262144 outputs) per round
+
+__global__ __launch_bounds__(AM_T) void argmax_parts_kernel(const float* __restrict__ parts, int tiles,
+                                                            int32_t* __restrict__ out) {
+  __shared__ float bvs[AM_T / 64];
+  __shared__ int bjs[AM_T / 64];
+  const int r = blockIdx.x, t = threadIdx.x;
+  const float2* p = reinterpret_cast<const float2*>(parts + (size_t)r * tiles * 2);
+  float bv = -__builtin_inff();
+  int bj = 0x7fffffff;
+  for (int q0 = 0; q0 < tiles; q0 += AM_T * AM_PER) {
+    float2 v[AM_PER];
+#pragma unroll
+    for (int i = 0; i < AM_PER; ++i) {
+      const int q = q0 + t + AM_T * i;
+      v[i] = q < tiles ? p[q] : make_float2(-__builtin_inff(), __int_as_float(0x7fffffff));
+    }
+#pragma unroll
+    for (int i = 0; i < AM_PER; ++i) {
+      const int j = __float_as_int(v[i].y);
+      if (v[i].x > bv || (v[i].x == bv && j < bj)) { bv = v[i].x; bj = j; }
+    }
+  }
+  const float m = wave_allmax(bv);
+  int c = bv == m ? bj : 0x7fffffff;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) c = min(c, __shfl_xor(c, o, 64));
+  if ((t & 63) == 0) { bvs[t >> 6] = m; bjs[t >> 6] = c; }
+  __syncthreads();
+  if (t == 0) {
+    float v = bvs[0];
+    int j = bjs[0];
+    for (int w = 1; w < AM_T / 64; ++w)
+      if (bvs[w] > v || (bvs[w] == v && bjs[w] < j)) { v = bvs[w]; j = bjs[w]; }
+    out[r] = j == 0x7fffffff ? 0 : j;
   }
 }
 
@@ -437,7 +514,7 @@ int launch_packed(const uint16_t* x, const uint8_t* packed, uint16_t* y, int M, 
                   const char* fn_name_override = nullptr) {
   const char* fn_name =
       fn_name_override ? fn_name_override : swiglu ? "qvex_qmv_w4g64_packed_swiglu" : "qvex_qmv_w4g64_packed";
-  QVEX_CHECK_ARG(x && packed && (y || e.resid), "%s: null pointer", fn_name);
+  QVEX_CHECK_ARG(x && packed && (y || e.resid || e.am_parts), "%s: null pointer", fn_name);
   QVEX_CHECK_ARG(M >= 1 && M <= 4, "%s: M=%d outside 1..4", fn_name, M);
   QVEX_CHECK_ARG(N >= 1 && K >= PK_SET && K % PK_SET == 0, "%s: N=%d K=%d (K must be a positive multiple of 256)",
                  fn_name, N, K);
@@ -559,5 +636,42 @@ extern "C" int qvex_rms_parts(const uint16_t* x, const uint16_t* norm_w, uint16_
   hipLaunchKernelGGL(rms_parts_kernel, dim3((tiles + 15) / 16, M), dim3(256), 0, (hipStream_t)stream, x, norm_w,
                      u_out, sq_parts, D);
   QVEX_CHECK_LAUNCH("qvex_rms_parts");
+  return QVEX_OK;
+}
+
+extern "C" uint64_t qvex_qmv_w4g64_argmax_workspace_bytes(int M, int N) {
+  if (M < 1 || N < 1) return 0;
+  return (uint64_t)M * ((N + PK_TILE - 1) / PK_TILE) * 2 * sizeof(float);
+}
+
+extern "C" int qvex_qmv_w4g64_packed_argmax(const uint16_t* x, const void* packed, int M, int N, int K,
+                                            const float* sq_parts, int nparts, int dim, float eps, int32_t* out_token,
+                                            void* workspace, uint64_t workspace_bytes, void* stream) {
+  const char* fn = "qvex_qmv_w4g64_packed_argmax";
+  QVEX_CHECK_ARG(out_token && workspace, "%s: null pointer", fn);
+  QVEX_CHECK_ARG(workspace_bytes >= qvex_qmv_w4g64_argmax_workspace_bytes(M, N),
+                 "%s: workspace %llu bytes < %llu", fn, (unsigned long long)workspace_bytes,
+                 (unsigned long long)qvex_qmv_w4g64_argmax_workspace_bytes(M, N));
+  if (sq_parts) {
+    QVEX_CHECK_ARG(nparts >= 1 && nparts <= 256 && nparts % 4 == 0 && nparts == (dim + PK_TILE - 1) / PK_TILE,
+                   "%s: nparts=%d must be ceil(dim/16) for dim=%d, a multiple of 4 and <= 256", fn, nparts, dim);
+    QVEX_CHECK_ARG(qvex_aligned(sq_parts, 16), "%s: sq_parts must be 16-byte aligned", fn);
+  }
+  int TN = 1, WS = 1;
+  if (N >= 1 && K >= PK_SET) packed_default_tile(N, K, &TN, &WS);
+  PkEpi e{};
+  e.rs_parts = sq_parts;
+  e.rs_nparts = nparts;
+  e.rs_dim = dim;
+  e.rs_eps = eps;
+  e.am_parts = (float*)workspace;
+  // the product itself is launch_packed's; y is not written
+  e.resid = nullptr;
+  if (int rc = launch_packed(x, (const uint8_t*)packed, nullptr, M, N, K, TN, WS, false, -1, e,
+                             (hipStream_t)stream, fn))
+    return rc;
+  hipLaunchKernelGGL(argmax_parts_kernel, dim3(M), dim3(AM_T), 0, (hipStream_t)stream, (const float*)workspace,
+                     (N + PK_TILE - 1) / PK_TILE, out_token);
+  QVEX_CHECK_LAUNCH(fn);
   return QVEX_OK;
 }

@@ -552,27 +552,55 @@ __global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
   const int k = a.k;
   const SpecWs W = spec_ws(a);
 
-  if (t < a.rps) {
-    const float* w = a.ws + ((long)step * a.rps + t) * a.P * 2;
-    rc[t] = -__builtin_inff();
-    if (!a.greedy && a.top_k > 0 && t <= k) {
-      const float* fr = a.frow + ((long)step * (k + 1) + t) * 4;
-      rm[t] = fr[0];
-      rs[t] = fr[1];
-      rc[t] = fr[2];
-    } else if (a.greedy) {
-      float bv = w[0];
-      int bj = __float_as_int(w[1]);
-      for (int q = 1; q < a.P; ++q)
-        if (w[2 * q] > bv) { bv = w[2 * q]; bj = __float_as_int(w[2 * q + 1]); }
-      rm[t] = __int_as_float(bj);
-    } else {
-      float m = -__builtin_inff();
-      for (int q = 0; q < a.P; ++q) m = fmaxf(m, w[2 * q]);
-      float sum = 0.0f;
-      for (int q = 0; q < a.P; ++q) sum = sum + w[2 * q + 1] * qx_expf(w[2 * q] - m);
-      rm[t] = m;
-      rs[t] = sum;
+  // per-row statistics from the parts, one wave per row: lane q holds part q
+  // (parts 64 apart in later rounds). Greedy: the first part holding the row
+  // maximum gives the index (the serial rule "strictly greater replaces");
+  // sampling: m = max, S = sum_q S_q e^{m_q - m} added in part order.
+  {
+    const int lane = t & 63, wave = t >> 6;
+    for (int r = wave; r < a.rps; r += NT / 64) {
+      const float* w = a.ws + ((long)step * a.rps + r) * a.P * 2;
+      float cut = -__builtin_inff(), mr = 0.0f, sr = 0.0f;
+      if (!a.greedy && a.top_k > 0 && r <= k) {
+        const float* fr = a.frow + ((long)step * (k + 1) + r) * 4;
+        mr = fr[0];
+        sr = fr[1];
+        cut = fr[2];
+      } else if (a.greedy) {
+        float bv = -__builtin_inff();
+        int bj = 0;
+        for (int q0 = 0; q0 < a.P; q0 += 64) {
+          const int q = q0 + lane;
+          const float v = q < a.P ? w[2 * q] : -__builtin_inff();
+          const int j = q < a.P ? __float_as_int(w[2 * q + 1]) : 0;
+          const float m = wave_allmax(v);
+          const unsigned long long hit = __ballot(q < a.P && v == m);
+          const int src = __ffsll(hit) - 1;
+          const int jm = __builtin_amdgcn_readlane(j, src);
+          if (q0 == 0 || m > bv) { bv = m; bj = jm; }
+        }
+        mr = __int_as_float(bj);
+      } else {
+        float m = -__builtin_inff();
+        for (int q0 = 0; q0 < a.P; q0 += 64) {
+          const int q = q0 + lane;
+          m = fmaxf(m, wave_allmax(q < a.P ? w[2 * q] : -__builtin_inff()));
+        }
+        float sum = 0.0f;
+        for (int q0 = 0; q0 < a.P; q0 += 64) {
+          const int q = q0 + lane;
+          const float term = q < a.P ? w[2 * q + 1] * qx_expf(w[2 * q] - m) : 0.0f;
+          const int n = min(64, a.P - q0);
+          for (int i = 0; i < n; ++i) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(term), i));
+        }
+        mr = m;
+        sr = sum;
+      }
+      if (lane == 0) {
+        rm[r] = mr;
+        rs[r] = sr;
+        rc[r] = cut;
+      }
     }
   }
   __syncthreads();

@@ -29,6 +29,7 @@ SIGNATURES: dict[str, list] = {
     "qvex_qmv_w4g64_packed_resid": [P, P, I, I, I, P, P, P, P, P, P],
     "qvex_qmv_w4g64_packed_rstd": [P, P, P, I, I, I, P, I, I, F, I, P],
     "qvex_rms_parts": [P, P, P, P, I, I, P],
+    "qvex_qmv_w4g64_packed_argmax": [P, P, I, I, I, P, I, I, F, P, P, U64, P],
     "qvex_w4g64_pack_swiglu": [P, P, P, I, I, P, U64, P],
     "qvex_qmv_w4g64_packed_swiglu": [P, P, P, I, I, I, P],
     "qvex_gdn_recurrent": [P, P, P, P, P, P, P, P, P, I, P, I, I, I, I, I, I, P],
@@ -84,6 +85,8 @@ def lib() -> ctypes.CDLL:
         L.qvex_spec_accept_filtered_workspace_bytes.argtypes = [I, I, I, I, I]
         L.qvex_gdn_chunked_workspace_bytes.restype = U64
         L.qvex_gdn_chunked_workspace_bytes.argtypes = [I, I, I, I, I, I]
+        L.qvex_qmv_w4g64_argmax_workspace_bytes.restype = U64
+        L.qvex_qmv_w4g64_argmax_workspace_bytes.argtypes = [I, I]
         for name, args in SIGNATURES.items():
             fn = getattr(L, name)
             fn.argtypes = args
@@ -103,4 +106,5 @@ def call(name: str, *args) -> None:
 def exported_symbols() -> list[str]:
     return ["qvex_last_error", "qvex_abi_version", "qvex_spec_accept_workspace_bytes",
             "qvex_attn_workspace_bytes", "qvex_w4g64_packed_bytes",
-            "qvex_gdn_chunked_workspace_bytes", "qvex_spec_accept_filtered_workspace_bytes", *SIGNATURES]
+            "qvex_gdn_chunked_workspace_bytes", "qvex_spec_accept_filtered_workspace_bytes",
+            "qvex_qmv_w4g64_argmax_workspace_bytes", *SIGNATURES]

@@ -184,6 +184,36 @@ def qmv_packed_rstd(u: torch.Tensor, packed: torch.Tensor, N: int, parts: torch.
     return out
 
 
+def qmv_packed_argmax(x: torch.Tensor, packed: torch.Tensor, N: int, out: torch.Tensor,
+                      parts: torch.Tensor | None = None, eps: float = 0.0,
+                      workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy token of each row of x W^T (first index of the largest bf16-rounded
+    output, as an argmax over the product's bf16 result) without writing the
+    product: out int32 [M]. With parts, x is NormedRows' u (the rows are scaled
+    by rsqrt(mean(h^2) + eps) as qmv_packed_rstd does)."""
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    M = x2.shape[0]
+    _check(x2, "x", torch.bfloat16, 2)
+    _check(out, "out", torch.int32)
+    if out.numel() != M:
+        raise _C.QvexError(f"out must hold M = {M} values")
+    if packed.numel() != int(_C.lib().qvex_w4g64_packed_bytes(N, K)):
+        raise _C.QvexError(f"packed has {packed.numel()} bytes, not the size of an N={N} K={K} pack")
+    need = int(_C.lib().qvex_qmv_w4g64_argmax_workspace_bytes(M, N))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty((need + 3) // 4, dtype=torch.float32, device=x.device)
+    nparts = (K + 15) // 16
+    if parts is not None:
+        _check(parts, "parts", torch.float32)
+        if parts.numel() != M * nparts:
+            raise _C.QvexError(f"parts must hold M * ceil(K/16) = {M * nparts} values")
+    _C.call("qvex_qmv_w4g64_packed_argmax", _ptr(x2), _ptr(packed), M, N, K,
+            _ptr(parts) if parts is not None else None, nparts, K, float(eps), _ptr(out), _ptr(workspace),
+            workspace.numel() * workspace.element_size(), _stream())
+    return out
+
+
 def rms_parts(x: torch.Tensor, w: torch.Tensor, u_out: torch.Tensor | None = None,
               parts: torch.Tensor | None = None):
     """u = bf16(x * w) and the per-16-column sums of x^2 of rows x [M, D]."""

@@ -188,6 +188,25 @@ class QLinear:
             kernels.quantized_matmul(x2[m0:m1], self.w, self.scales, self.biases, out=o2[m0:m1])
         return out.view(*lead, self.N)
 
+    def argmax(self, x, out: torch.Tensor) -> torch.Tensor:
+        """Greedy token per row of the product (first index of the largest bf16
+        output) into out int32 [M]; x a tensor or NormedRows of 1..4 rows."""
+        if isinstance(x, NormedRows):
+            M = x.u.reshape(-1, self.K).shape[0]
+            if self._takes_normed(x, M) and not self.swiglu_packed:
+                if not hasattr(self, "_am_ws"):
+                    self._am_ws = {}
+                ws = self._am_ws.get(M)
+                if ws is None:
+                    need = int(_C.lib().qvex_qmv_w4g64_argmax_workspace_bytes(M, self.N))
+                    ws = self._am_ws[M] = torch.empty((need + 3) // 4, dtype=torch.float32, device=x.device)
+                return kernels.qmv_packed_argmax(x.u, self.packed, self.N, out, x.parts, x.eps, workspace=ws)
+        from .speculative import _argmax
+        logits = self(x).reshape(-1, self.N)
+        for r in range(logits.shape[0]):
+            _argmax(logits[r], out=out.reshape(-1)[r:r + 1])
+        return out
+
     def residual(self, x: torch.Tensor, resid: torch.Tensor, norm_w: torch.Tensor, eps: float,
                  h_out: torch.Tensor | None = None):
         """h = resid + x W^T and the next norm of h: returns (h, NormedRows) with

@@ -42,12 +42,16 @@ class MTPHead:
         return KVCache(None, 0, n_kv=cfg.num_key_value_heads, head_dim=cfg.head_dim,
                        capacity=max_context or self.model.max_context, device=self.model.norm.device)
 
-    def __call__(self, hidden, next_ids, cache: KVCache, last_only=True, return_hidden=False, select=None):
+    def __call__(self, hidden, next_ids, cache: KVCache, last_only=True, return_hidden=False, select=None,
+                 argmax_out=None):
         """hidden [1, T, H] (main model, pre-norm) and next_ids [1, T] -> logits
         [1, 1 or T, V] (engine/mtp.py:58-68); with return_hidden also the block
         output [1, T, H] before the final norm (what a chained draft step takes).
         select: optional device int32 [1] row index; only that row goes through
-        the lm_head (and is returned as the hidden), chosen on the device."""
+        the lm_head (and is returned as the hidden), chosen on the device.
+        argmax_out: optional int32 [1]; the greedy draft of the (selected or last)
+        row is written there by the lm_head's argmax epilogue and no logits are
+        made (logits returned as None)."""
         H = self.model.cfg.hidden_size
         h = hidden.reshape(-1, H)
         ids = torch.as_tensor(next_ids, device=h.device).reshape(-1)
@@ -67,9 +71,19 @@ class MTPHead:
             if select is not None:
                 o_sel = torch.empty((1, H), dtype=torch.bfloat16, device=h.device)
                 _C.call("qvex_gather_row", _ptr(out), H, _ptr(select), T, _ptr(o_sel), H, _stream())
-                logits = self.model.lm_head(NormedRows.of(o_sel, self.norm_out, self.eps)).view(1, 1, V)
+                st_sel = NormedRows.of(o_sel, self.norm_out, self.eps)
+                if argmax_out is not None:
+                    self.model.lm_head.argmax(st_sel, argmax_out)
+                    return (None, o_sel.view(1, 1, H)) if return_hidden else None
+                logits = self.model.lm_head(st_sel).view(1, 1, V)
                 return (logits, o_sel.view(1, 1, H)) if return_hidden else logits
+            if argmax_out is not None and last_only:
+                self.model.lm_head.argmax(st[-1:], argmax_out)
+                return (None, out.view(1, T, H)) if return_hidden else None
             logits = self.model.lm_head(st[-1:] if last_only else st).view(1, -1, V)
+            if argmax_out is not None:
+                from .speculative import _argmax
+                _argmax(logits[0, -1], out=argmax_out)
             return (logits, out.view(1, T, H)) if return_hidden else logits
         n = rms_norm(x, self.layer.ln1, self.eps)
         hh, m = self.layer(x, cache, normed=n)
@@ -80,10 +94,16 @@ class MTPHead:
             _C.call("qvex_gather_row", _ptr(n_out), H, _ptr(select), T, _ptr(n_sel), H, _stream())
             _C.call("qvex_gather_row", _ptr(out), H, _ptr(select), T, _ptr(o_sel), H, _stream())
             logits = self.model.lm_head(n_sel).view(1, 1, self.model.cfg.vocab_size)
+            if argmax_out is not None:
+                from .speculative import _argmax
+                _argmax(logits[0, -1], out=argmax_out)
             return (logits, o_sel.view(1, 1, H)) if return_hidden else logits
         if last_only:
             n_out = n_out[-1:]
         logits = self.model.lm_head(n_out).view(1, -1, self.model.cfg.vocab_size)
+        if argmax_out is not None:
+            from .speculative import _argmax
+            _argmax(logits[0, -1], out=argmax_out)
         return (logits, out.view(1, T, H)) if return_hidden else logits
 
 

@@ -233,14 +233,15 @@ class GraphedMTPCycle:
     def _body(self):
         d = self.dec
         k, mtp, mc = self.k, d.mtp, d.mtp_cache
-        logits, h = mtp(self.pend_h, self.pend_ids, mc, return_hidden=True, select=self.n_prev)
+        # greedy drafts straight from the MTP lm_head's argmax epilogue into the verify ids
+        _, h = mtp(self.pend_h, self.pend_ids, mc, return_hidden=True, select=self.n_prev,
+                   argmax_out=self.ids[0, 1:2])
         self._commit(mc.counters, self.n_prev, 1)
-        _argmax(logits[0, -1], out=self.ids[0, 1:2])
         for j in range(1, k):
-            logits, h = mtp(h, self.ids[:, j:j + 1], mc, last_only=True, return_hidden=True)
+            _, h = mtp(h, self.ids[:, j:j + 1], mc, last_only=True, return_hidden=True,
+                       argmax_out=self.ids[0, j + 1:j + 2])
             if j < k - 1:                        # the last step's advance folds into the finish
                 self._commit(mc.counters, self.zero, 1)
-            _argmax(logits[0, -1], out=self.ids[0, j + 1:j + 2])
         logits, _ = d.model(self.ids, d.cache, last_only=False, return_hidden=True, keep_prev=True,
                             hidden_out=self.pend_h)
         n, tok = d.sampler.accept_device(logits[0], self.drafts, self.u_buf)

@@ -136,3 +136,36 @@ def test_prefetch_explicit_tiles(tile):
     y = run_packed(x, w, s, b, tile=tile)
     check(x, w, s, b, y)
     assert np.array_equal(y, run_packed(x, w, s, b, tile=(*tile[:2], 0)))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 3, 4])
+@pytest.mark.parametrize("N,K,ties", [(248320, 4096, False), (4096, 512, True), (531, 2304, True), (50000, 1024, False)])
+def test_argmax_epilogue_equals_argmax_of_product(M, N, K, ties):
+    """qvex_qmv_w4g64_packed_argmax == the first index of the maximum of the bf16
+    product (the greedy pick over the lm_head's output), also with exact ties
+    (duplicated weight rows) and with the folded-norm row scale."""
+    from qvex.model import NormedRows
+    w, s, b = synth.qmv_weights(N, K, seed=38, tag=N)
+    if ties:
+        g = np.random.default_rng(N)
+        src = g.integers(0, N, 64)
+        dst = g.integers(0, N, 64)
+        w[dst], s[dst], b[dst] = w[src], s[src], b[src]
+    packed = kernels.pack_w4(to_dev(w, torch.int32), to_dev(s, torch.bfloat16), to_dev(b, torch.bfloat16))
+    x = to_dev(synth.qmv_x(M, K, seed=38, tag=M), torch.bfloat16)
+    out = torch.empty(M, dtype=torch.int32, device="cuda:0")
+    kernels.qmv_packed_argmax(x, packed, N, out)
+    y = kernels.quantized_matmul_packed(x, packed, N).float()
+    want = torch.tensor([int(torch.nonzero(y[r] == y[r].max())[0]) for r in range(M)], dtype=torch.int32)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), want)
+    g = torch.Generator().manual_seed(M)
+    h = (torch.randn(M, K, generator=g) * 2).to(torch.bfloat16).to("cuda:0")
+    nw = (1 + 0.1 * torch.randn(K, generator=g)).to(torch.bfloat16).to("cuda:0")
+    st = NormedRows.of(h, nw, 1e-6)
+    kernels.qmv_packed_argmax(st.u, packed, N, out, st.parts, 1e-6)
+    y2 = kernels.qmv_packed_rstd(st.u, packed, N, st.parts, 1e-6).float()
+    want2 = torch.tensor([int(torch.nonzero(y2[r] == y2[r].max())[0]) for r in range(M)], dtype=torch.int32)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), want2)
