@@ -122,6 +122,19 @@ int qvex_qmv_w4g64_packed_rstd(const uint16_t* u, const void* packed, uint16_t* 
                                int swiglu, void* stream);
 int qvex_rms_parts(const uint16_t* x, const uint16_t* norm_w, uint16_t* u_out, float* sq_parts,
                    int M, int D, void* stream);
+/* out_proj after the split GatedDeltaNet mixer (qvex_gdn_decode_split): the
+ * gated RMSNorm's per-(token, head) scale (_gated_rmsnorm, engine/model.py:
+ * 138-143, before out_proj at engine/model.py:288-290) applied inside the
+ * product. u [M, K] bf16 is silu(z) * w * y per 128-column head, unscaled;
+ * head h's share of row r of u W^T is multiplied in fp32 by
+ * rsqrt(S_rh / 128 + eps), S_rh the sum of the seg_nb (1, 2, 4 or 8) partials
+ * seg_ss[(r * K/128 + h) * seg_nb + b]; then the residual epilogue of
+ * qvex_qmv_w4g64_packed_resid. This equals out_proj(gated_rmsnorm(y, z)) up
+ * to where the bf16 roundings fall. */
+int qvex_qmv_w4g64_packed_gnorm_resid(const uint16_t* u, const void* packed, int M, int N, int K,
+                                      const float* seg_ss, int seg_nb, float seg_eps,
+                                      const uint16_t* resid, const uint16_t* norm_w, uint16_t* h_out,
+                                      uint16_t* u_out, float* sq_parts, void* stream);
 /* Greedy drafting on the lm_head (the argmax of `_argmax` / Sampler.pick with
  * temperature 0, engine/sampler.py:30-58, over mx.quantized_matmul's bf16
  * logits): out_token[r] = the first index of the largest bf16-rounded output
@@ -198,6 +211,22 @@ int qvex_gdn_decode_fused(const uint16_t* proj, long p_stride, uint16_t* conv_ri
                           const uint16_t* dt_bias, int z_offset, int ab_offset, float* state_ring,
                           int n_slots, int snap_every, const uint16_t* norm_w, float norm_eps,
                           uint16_t* out, int T, int Hk, int Hv, int Dk, int Dv, void* stream);
+/* The same mixer with each value head split over blocks_per_head (2, 4 or 8)
+ * workgroups of 128 / blocks_per_head state rows, so that the recurrence
+ * spreads over Hv * blocks_per_head CUs. The gated norm's per-head scale needs
+ * all 128 rows of a head, so it is left to the out_proj
+ * (qvex_qmv_w4g64_packed_gnorm_resid): u_out [T, Hv * 128] bf16 receives
+ * silu(z) * (norm_w * y) with y the bf16 recurrence output, and
+ * ss_parts [T, Hv, blocks_per_head] fp32 each workgroup's sum of y^2. The conv
+ * ring and state ring are bitwise those of qvex_gdn_decode_fused. Same
+ * reference interface as qvex_gdn_decode_fused. */
+int qvex_gdn_decode_split(const uint16_t* proj, long p_stride, uint16_t* conv_ring, int ring_rows,
+                          const int32_t* counter, const uint16_t* conv_w, int kernel_size, int conv_dim,
+                          int key_dim, float q_scale, float k_scale, float qk_eps, const float* A_log,
+                          const uint16_t* dt_bias, int z_offset, int ab_offset, float* state_ring,
+                          int n_slots, int snap_every, const uint16_t* norm_w, uint16_t* u_out,
+                          float* ss_parts, int T, int Hk, int Hv, int Dk, int Dv, int blocks_per_head,
+                          void* stream);
 
 /* Chunked (prefill) form of the same recurrence, chunk = 64 tokens, on MFMA:
  * gated_delta over a long prompt (engine/kernels.py:92-116 as called by

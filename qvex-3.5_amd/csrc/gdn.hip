@@ -159,6 +159,15 @@ constexpr int FUSED_TMAX = 8;
 constexpr int FUSED_THREADS = 1024;
 constexpr int FUSED_KC = 4;   // conv taps (Qwen3.5: linear_conv_kernel_dim = 4)
 
+// (base + d) mod m for 0 <= base < m and -m <= d < m: a 64-bit modulo is a long
+// instruction sequence, so the token count is reduced once per kernel (the ring
+// offsets -3 .. T-1 lie within that range since ring_rows >= T + 3)
+__device__ __forceinline__ int wrap_add(int base, int d, int m) {
+  int r = base + d;
+  r = r < 0 ? r + m : r;
+  return r >= m ? r - m : r;
+}
+
 struct GdnFusedArgs {
   const uint16_t* proj;    // [T, p_stride]: conv channels | z | b | a
   long p_stride;
@@ -188,6 +197,7 @@ __global__ __launch_bounds__(FUSED_THREADS) void gdn_decode_fused_kernel(GdnFuse
   const int T = p.T;
   const long p0 = *p.counter;
   const int cur = (int)(((p0 % p.n_slots) + p.n_slots) % p.n_slots);
+  const int rbase = (int)(((p0 % p.R) + p.R) % p.R);
   const long slot_stride = (long)p.Hv * DK * DK;
 
   // state rows grp and grp + 64 of this head, 8 columns per lane
@@ -239,8 +249,7 @@ __global__ __launch_bounds__(FUSED_THREADS) void gdn_decode_fused_kernel(GdnFuse
     for (int j = 0; j < FUSED_KC; ++j) {
       const int r = t + j;
       if (r < W) {
-        long rr = (p0 + r - W) % p.R;
-        if (rr < 0) rr += p.R;
+        const long rr = wrap_add(rbase, r - W, p.R);
         win[j] = *reinterpret_cast<const uint32_t*>(p.ring + rr * p.C + c0);
       } else {
         win[j] = *reinterpret_cast<const uint32_t*>(p.proj + (size_t)(r - W) * p.p_stride + c0);
@@ -256,8 +265,7 @@ __global__ __launch_bounds__(FUSED_THREADS) void gdn_decode_fused_kernel(GdnFuse
       acc1 = fmaf(bf16_hi(win[j]), w1[j], acc1);
     }
     if (part == 2 || ring_qk) {
-      long rr = (p0 + t) % p.R;
-      if (rr < 0) rr += p.R;
+      const long rr = wrap_add(rbase, t, p.R);
       *reinterpret_cast<uint32_t*>(p.ring + rr * p.C + c0) = win[W];
     }
     float s0 = silu(acc0), s1 = silu(acc1);
@@ -286,7 +294,7 @@ __global__ __launch_bounds__(FUSED_THREADS) void gdn_decode_fused_kernel(GdnFuse
       qq[i] = qs[t][l16 * 8 + i];
     }
     long slot = -1;
-    if (p.snap_every || t == T - 1) slot = (cur + 1 + t) % p.n_slots;
+    if (p.snap_every || t == T - 1) slot = wrap_add(cur, (1 + t) % p.n_slots, p.n_slots);
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int dv = grp + 64 * r;
@@ -333,6 +341,196 @@ __global__ __launch_bounds__(FUSED_THREADS) void gdn_decode_fused_kernel(GdnFuse
     const float z0 = bf16_lo(zp), z1 = bf16_hi(zp);
     *reinterpret_cast<uint32_t*>(p.out + (size_t)t * p.Hv * DK + hv * DK + 2 * lane) =
         pack_bf16x2(silu(z0) * n0, silu(z1) * n1);
+  }
+}
+
+// The mixer with each value head split over NB blocks of 128 / NB state rows
+// (one row per 16-lane DPP row, the arithmetic of gdn_recurrent_kernel), so the
+// recurrence fills NB * Hv CUs. The gated RMSNorm's per-(token, head) scale
+// rsqrt(mean(y^2) + eps) would need all 128 rows of a head; it commutes with the
+// out_proj product, so each block writes instead
+//   u = bf16(silu(z) * (w * y))            (y the bf16 recurrence output)
+//   ss_parts[(t * Hv + head) * NB + b] = the sum of y^2 over its rows,
+// and the out_proj applies the scale to each 128-column segment of its input
+// as it stages it (qvex_qmv_w4g64_packed_resid with a segment scale). The conv
+// ring and state ring are bitwise those of the other forms.
+template <int NB>
+__global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArgs p, float* ss_parts) {
+  constexpr int RB = DK / NB;            // rows per block
+  constexpr int NTH = 16 * RB;           // threads
+  constexpr int NW = NTH / 64;           // waves
+  constexpr int NTASK = (3 * FUSED_TMAX + NW - 1) / NW;   // conv tasks per wave at most
+  __shared__ float qs[FUSED_TMAX][DK], ks[FUSED_TMAX][DK], vs[FUSED_TMAX][RB], ys[FUSED_TMAX][RB];
+  __shared__ float gb_s[2][FUSED_TMAX];
+  const int hv = blockIdx.x / NB, b = blockIdx.x % NB;
+  const int hk = hv / (p.Hv / p.Hk);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int grp = threadIdx.x >> 4, l16 = threadIdx.x & 15;
+  const int dv = b * RB + grp;
+  const int T = p.T;
+  constexpr int W = FUSED_KC - 1;
+
+  // the state row first (it waits on the token count), then this wave's conv
+  // rows from proj, the taps, the gate inputs, z and the norm weight, then the
+  // ring rows
+  const long p0 = *p.counter;
+  const int cur = (int)(((p0 % p.n_slots) + p.n_slots) % p.n_slots);
+  const int rbase = (int)(((p0 % p.R) + p.R) % p.R);
+  const long slot_stride = (long)p.Hv * DK * DK;
+  const long row_off = ((long)hv * DK + dv) * DK + l16 * 8;
+  float st[8];
+  {
+    const float* src = p.state + cur * slot_stride + row_off;
+    const u32x4 s0 = load16(src);
+    const u32x4 s1 = load16(src + 4);
+    st[0] = __uint_as_float(s0.x); st[1] = __uint_as_float(s0.y);
+    st[2] = __uint_as_float(s0.z); st[3] = __uint_as_float(s0.w);
+    st[4] = __uint_as_float(s1.x); st[5] = __uint_as_float(s1.y);
+    st[6] = __uint_as_float(s1.z); st[7] = __uint_as_float(s1.w);
+  }
+  int c0[NTASK];
+  bool act[NTASK];
+  uint32_t win[NTASK][FUSED_KC];
+  u32x4 taps[NTASK];
+#pragma unroll
+  for (int i = 0; i < NTASK; ++i) {
+    const int task = wave + i * NW;
+    const int t = task / 3, part = task - 3 * (task / 3);
+    // q and k: the whole wave (128 channels); v: lanes < RB / 2 (RB channels)
+    act[i] = task < 3 * T && (part < 2 || 2 * lane < RB);
+    const int cb = part == 0 ? hk * DK : part == 1 ? p.key_dim + hk * DK : 2 * p.key_dim + hv * DK + b * RB;
+    c0[i] = cb + (act[i] ? 2 * lane : 0);
+    taps[i] = task < 3 * T ? load16(p.cw + (size_t)c0[i] * FUSED_KC) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < FUSED_KC; ++j)
+      win[i][j] = (task < 3 * T && t + j >= W)
+                      ? *reinterpret_cast<const uint32_t*>(p.proj + (size_t)(t + j - W) * p.p_stride + c0[i])
+                      : 0u;
+  }
+  float ga = 0.0f, gbb = 0.0f, Alog = 0.0f, dtb = 0.0f;
+  if (threadIdx.x < T) {
+    const int t = threadIdx.x;
+    Alog = p.A_log[hv];
+    dtb = bf16_to_f32(p.dt_bias[hv]);
+    ga = bf16_to_f32(p.proj[(size_t)t * p.p_stride + p.ab_off + p.Hv + hv]);
+    gbb = bf16_to_f32(p.proj[(size_t)t * p.p_stride + p.ab_off + hv]);
+  }
+  float zr[FUSED_TMAX];
+  float wr = 0.0f;
+  if (l16 == 0) {
+    wr = bf16_to_f32(p.norm_w[dv]);
+#pragma unroll
+    for (int t = 0; t < FUSED_TMAX; ++t)
+      zr[t] = t < T ? bf16_to_f32(p.proj[(size_t)t * p.p_stride + p.z_off + hv * DK + dv]) : 0.0f;
+  }
+
+#pragma unroll
+  for (int i = 0; i < NTASK; ++i) {
+    const int task = wave + i * NW;
+    const int t = task / 3;
+#pragma unroll
+    for (int j = 0; j < FUSED_KC; ++j)
+      if (task < 3 * T && t + j < W) {
+        const long rr = wrap_add(rbase, t + j - W, p.R);
+        win[i][j] = *reinterpret_cast<const uint32_t*>(p.ring + rr * p.C + c0[i]);
+      }
+  }
+  if (threadIdx.x < T) {
+    const float A = expf(Alog);
+    const float x = ga + dtb;
+    const float sp = x > 20.0f ? x : log1pf(expf(x));
+    gb_s[0][threadIdx.x] = expf(-A * sp);
+    gb_s[1][threadIdx.x] = 1.0f / (1.0f + expf(-gbb));
+  }
+
+  // 1. conv + silu: q and k heads (normed as in conv_silu_qk_kernel) and this
+  // block's RB v channels; the q / k ring rows are written by one block per k head
+  const bool ring_qk = hv % (p.Hv / p.Hk) == 0 && b == 0;
+#pragma unroll
+  for (int i = 0; i < NTASK; ++i) {
+    const int task = wave + i * NW;
+    if (task >= 3 * T) break;                     // uniform over the wave
+    const int t = task / 3, part = task - 3 * (task / 3);
+    const float w0[4] = {bf16_lo(taps[i].x), bf16_hi(taps[i].x), bf16_lo(taps[i].y), bf16_hi(taps[i].y)};
+    const float w1[4] = {bf16_lo(taps[i].z), bf16_hi(taps[i].z), bf16_lo(taps[i].w), bf16_hi(taps[i].w)};
+    float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < FUSED_KC; ++j) {
+      acc0 = fmaf(bf16_lo(win[i][j]), w0[j], acc0);
+      acc1 = fmaf(bf16_hi(win[i][j]), w1[j], acc1);
+    }
+    if (act[i] && (part == 2 || ring_qk)) {
+      const long rr = wrap_add(rbase, t, p.R);
+      *reinterpret_cast<uint32_t*>(p.ring + rr * p.C + c0[i]) = win[i][W];
+    }
+    float s0 = silu(acc0), s1 = silu(acc1);
+    if (part < 2) {
+      const float ss = wave_allsum(fmaf(s0, s0, s1 * s1));
+      const float inv = rsqrtf(ss / 128.0f + p.qk_eps);
+      const float sc = part == 0 ? p.q_scale : p.k_scale;
+      s0 = s0 * inv * sc;
+      s1 = s1 * inv * sc;
+    }
+    const uint32_t pk = pack_bf16x2(s0, s1);
+    if (act[i]) {
+      float* dst = part == 0 ? qs[t] : part == 1 ? ks[t] : vs[t];
+      dst[2 * lane] = bf16_lo(pk);
+      dst[2 * lane + 1] = bf16_hi(pk);
+    }
+  }
+  __syncthreads();
+
+  // 2. recurrence; u of this block's rows to `out`, y to LDS for the sums
+  for (int t = 0; t < T; ++t) {
+    const float g = gb_s[0][t];
+    const float beta = gb_s[1][t];
+    float kk[8], qq[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      kk[i] = ks[t][l16 * 8 + i];
+      qq[i] = qs[t][l16 * 8 + i];
+    }
+    float kv = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      st[i] *= g;
+      kv = fmaf(st[i], kk[i], kv);
+    }
+    kv = row16_allsum(kv);
+    const float delta = (vs[t][grp] - kv) * beta;
+    float o = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      st[i] = fmaf(kk[i], delta, st[i]);
+      o = fmaf(st[i], qq[i], o);
+    }
+    o = row16_allsum(o);
+    if (l16 == 0) {
+      const float y = bf16_to_f32(f32_to_bf16(o));
+      ys[t][grp] = y;
+      float zt = zr[0];
+#pragma unroll
+      for (int i = 1; i < FUSED_TMAX; ++i) zt = t == i ? zr[i] : zt;
+      p.out[(size_t)t * p.Hv * DK + hv * DK + dv] = f32_to_bf16(silu(zt) * (wr * y));
+    }
+    if (p.snap_every || t == T - 1) {
+      float* dstp = p.state + wrap_add(cur, (1 + t) % p.n_slots, p.n_slots) * slot_stride + row_off;
+      u32x4 o0, o1;
+      o0.x = __float_as_uint(st[0]); o0.y = __float_as_uint(st[1]);
+      o0.z = __float_as_uint(st[2]); o0.w = __float_as_uint(st[3]);
+      o1.x = __float_as_uint(st[4]); o1.y = __float_as_uint(st[5]);
+      o1.z = __float_as_uint(st[6]); o1.w = __float_as_uint(st[7]);
+      __builtin_nontemporal_store(o0, reinterpret_cast<u32x4*>(dstp));
+      __builtin_nontemporal_store(o1, reinterpret_cast<u32x4*>(dstp + 4));
+    }
+  }
+  __syncthreads();
+  // 3. per token, the sum of y^2 over this block's rows: one wave per token,
+  // lane r < RB squares row r, a DPP sum over the wave
+  for (int t = wave; t < T; t += NW) {
+    const float y = lane < RB ? ys[t][lane] : 0.0f;
+    const float ss = wave_allsum(y * y);
+    if (lane == 0) ss_parts[((size_t)t * p.Hv + hv) * NB + b] = ss;
   }
 }
 
@@ -420,5 +618,49 @@ extern "C" int qvex_gdn_decode_fused(const uint16_t* proj, long p_stride, uint16
                  snap_every ? 1 : 0, norm_w, norm_eps, out, T, Hk, Hv};
   hipLaunchKernelGGL(gdn_decode_fused_kernel, dim3(Hv), dim3(FUSED_THREADS), 0, (hipStream_t)stream, p);
   QVEX_CHECK_LAUNCH("qvex_gdn_decode_fused");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_gdn_decode_split(const uint16_t* proj, long p_stride, uint16_t* conv_ring, int ring_rows,
+                                     const int32_t* counter, const uint16_t* conv_w, int kernel_size, int conv_dim,
+                                     int key_dim, float q_scale, float k_scale, float qk_eps, const float* A_log,
+                                     const uint16_t* dt_bias, int z_offset, int ab_offset, float* state_ring,
+                                     int n_slots, int snap_every, const uint16_t* norm_w, uint16_t* u_out,
+                                     float* ss_parts, int T, int Hk, int Hv, int Dk, int Dv, int blocks_per_head,
+                                     void* stream) {
+  const char* fn = "qvex_gdn_decode_split";
+  QVEX_CHECK_ARG(proj && conv_ring && counter && conv_w && A_log && dt_bias && state_ring && norm_w && u_out &&
+                     ss_parts,
+                 "%s: null pointer", fn);
+  QVEX_CHECK_ARG(blocks_per_head == 2 || blocks_per_head == 4 || blocks_per_head == 8,
+                 "%s: blocks_per_head=%d must be 2, 4 or 8", fn, blocks_per_head);
+  QVEX_CHECK_ARG(T >= 1 && T <= FUSED_TMAX, "%s: T=%d must be in 1..%d", fn, T, FUSED_TMAX);
+  if (Dk != DK || Dv != DK) return qvex::fail(QVEX_ENOTSUP, "%s: needs Dk = Dv = 128 (got %d, %d)", fn, Dk, Dv);
+  QVEX_CHECK_ARG(Hk >= 1 && Hv >= Hk && Hv % Hk == 0, "%s: Hv=%d must be a multiple of Hk=%d", fn, Hv, Hk);
+  QVEX_CHECK_ARG(key_dim == Hk * DK && conv_dim == 2 * key_dim + Hv * DK,
+                 "%s: conv_dim=%d key_dim=%d do not match Hk=%d Hv=%d", fn, conv_dim, key_dim, Hk, Hv);
+  if (kernel_size != FUSED_KC)
+    return qvex::fail(QVEX_ENOTSUP, "%s: needs kernel_size = %d (got %d)", fn, FUSED_KC, kernel_size);
+  QVEX_CHECK_ARG(ring_rows >= T + kernel_size - 1, "%s: ring_rows=%d < T + K - 1 = %d", fn, ring_rows,
+                 T + kernel_size - 1);
+  QVEX_CHECK_ARG(n_slots >= 2 && (!snap_every || n_slots >= T + 1),
+                 "%s: n_slots=%d must be >= T+1=%d with snapshots (>= 2 without)", fn, n_slots, T + 1);
+  QVEX_CHECK_ARG(p_stride % 2 == 0 && conv_dim <= p_stride && z_offset + Hv * DK <= p_stride && ab_offset >= 0 &&
+                     ab_offset + 2 * Hv <= p_stride,
+                 "%s: p_stride=%ld z_offset=%d ab_offset=%d do not fit the projection row", fn, p_stride, z_offset,
+                 ab_offset);
+  QVEX_CHECK_ARG(qvex_aligned(proj, 4) && qvex_aligned(conv_ring, 4) && qvex_aligned(state_ring, 16) &&
+                     qvex_aligned(conv_w, 16),
+                 "%s: proj, conv_ring need 4-byte and state_ring, conv_w 16-byte alignment", fn);
+  GdnFusedArgs p{proj, p_stride, conv_ring, ring_rows, counter, conv_w, conv_dim, key_dim,
+                 q_scale, k_scale, qk_eps, A_log, dt_bias, z_offset, ab_offset, state_ring, n_slots,
+                 snap_every ? 1 : 0, norm_w, 0.0f, u_out, T, Hk, Hv};
+  const dim3 grid(Hv * blocks_per_head);
+  switch (blocks_per_head) {
+    case 2: hipLaunchKernelGGL(gdn_decode_split_kernel<2>, grid, dim3(1024), 0, (hipStream_t)stream, p, ss_parts); break;
+    case 4: hipLaunchKernelGGL(gdn_decode_split_kernel<4>, grid, dim3(512), 0, (hipStream_t)stream, p, ss_parts); break;
+    case 8: hipLaunchKernelGGL(gdn_decode_split_kernel<8>, grid, dim3(256), 0, (hipStream_t)stream, p, ss_parts); break;
+  }
+  QVEX_CHECK_LAUNCH(fn);
   return QVEX_OK;
 }

@@ -132,6 +132,16 @@ struct PkEpi {
   // argmax (am_parts != null): per row r and 16-row tile j, the largest
   // bf16-rounded output and its first index -> am_parts[(r * tiles + j) * 2 + {0, 1}]
   float* am_parts;
+  // head-segment scale (seg_ss != null; the gated RMSNorm before out_proj,
+  // engine/model.py:285-288): x is u = bf16(silu(z) * w * y) for K / 128 <= 64
+  // heads of 128 columns, and the share of the product over head h of row r is
+  // scaled by rsqrt(S_rh / 128 + seg_eps) in fp32, S_rh the sum of the seg_nb
+  // (1, 2, 4 or 8) partials seg_ss[(r * K / 128 + h) * seg_nb + b] in order.
+  // The block puts the scales in LDS once, while its first weights load; each
+  // lane's 64-column group lies in one head.
+  const float* seg_ss;
+  int seg_nb;
+  float seg_eps;
 };
 
 constexpr int pk_block(int WS) { return WS >= 4 ? 64 * WS : 256; }   // WS = 16: 1024 threads
@@ -145,10 +155,12 @@ constexpr int pk_block(int WS) { return WS >= 4 ? 64 * WS : 256; }   // WS = 16:
 // computing any, so a wave with few sets keeps all its bytes in flight; the sets
 // are still computed in the same order. Results depend on (N, K, TN, WS) only,
 // never on M or NP.
-// SWIGLU: the weight was packed with the gate/up interleave; the epilogue rounds
-// the gate and up products to bf16 (as the unfused pair of calls would) and
-// writes bf16(silu(g) * u) to y [M, N/2].
-template <int TN, int WS, int NP, bool SWIGLU>
+// MODE 1 (SwiGLU): the weight was packed with the gate/up interleave; the
+// epilogue rounds the gate and up products to bf16 (as the unfused pair of calls
+// would) and writes bf16(silu(g) * u) to y [M, N/2]. MODE 2: the head-segment
+// scale of PkEpi (a mode of its own so that the other kernels keep their
+// registers). MODE 0: plain.
+template <int TN, int WS, int NP, int MODE>
 __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t* __restrict__ x,
                                                                    const uint8_t* __restrict__ packed,
                                                                    uint16_t* __restrict__ y, int M, int N, int K,
@@ -181,9 +193,35 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
   u32x4 wb[NB][TN][2];
   uint32_t sb[NB][TN];
   u32x4 xr[NB][2];
+  int sgs[NB];
 
   // activation slice loader: lane L of load q covers row 2q + L/32, chunk L%32
   const int xm0 = lane >> 5, xch = lane & 31;
+  constexpr bool SWIGLU = MODE == 1;
+  constexpr bool seg = MODE == 2;
+
+  // head-segment partials: thread i sums pair (head i / 4, row i % 4)
+  __shared__ __align__(16) float seg_tab[seg ? 256 : 4];
+  const int H = K / 128;
+  float segv[8];
+  if constexpr (seg) {
+    const int sh = threadIdx.x >> 2, sr = threadIdx.x & 3;
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+      segv[b] = (b < e.seg_nb && sh < H && sr < M) ? e.seg_ss[((size_t)sr * H + sh) * e.seg_nb + b] : 0.0f;
+  }
+  auto seg_table = [&]() {
+    if constexpr (seg) {
+      if ((int)threadIdx.x < 4 * H) {
+        float v = segv[0];
+#pragma unroll
+        for (int b = 1; b < 8; ++b)
+          if (b < e.seg_nb) v += segv[b];
+        seg_tab[threadIdx.x] = (int)(threadIdx.x & 3) < M ? rsqrtf(v / 128.0f + e.seg_eps) : 1.0f;
+      }
+      __syncthreads();
+    }
+  };
 
   // epilogue inputs, requested before the weights so their latency hides
   const bool rs = e.rs_parts != nullptr, prod = e.resid != nullptr;
@@ -232,6 +270,7 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
       const int m = 2 * q + xm0;
       xr[buf][q] = m < M ? load16(x + (size_t)m * K + (size_t)gs * PK_SET + 8 * xch) : u32x4{0u, 0u, 0u, 0u};
     }
+    sgs[buf] = gs;
   };
 
   auto compute = [&](int buf) {
@@ -254,6 +293,20 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
         C[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, C[t], 0, 0, 0);
       }
     }
+    if constexpr (seg) {
+      // lane (c, i16) holds group slot c: head 2 gs + c / 2 of rows 0..3
+      const float4 gt = reinterpret_cast<const float4*>(seg_tab)[2 * sgs[buf] + (c >> 1)];
+      const float g[4] = {gt.x, gt.y, gt.z, gt.w};
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        const float sc = bf16_to_f32((uint16_t)(sb[buf][t] & 0xffffu));
+        const float bi = bf16_to_f32((uint16_t)(sb[buf][t] >> 16));
+        const float bo = fmaf(-128.0f, sc, bi);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(g[r], fmaf(sc, C[t][r], bo * CX[r]), acc[t][r]);
+      }
+      return;
+    }
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
       const float sc = bf16_to_f32((uint16_t)(sb[buf][t] & 0xffffu));
@@ -268,6 +321,7 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
     int gs = ws;
     if (gs < GS) issue(0, gs);
     if (gs < GS && gs + WS < GS) issue(1, gs + WS);
+    seg_table();
     if (rs && ws == 0) compute_rstd();
     while (gs < GS) {
       const int g1 = gs + WS;
@@ -283,6 +337,7 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
     // the host guarantees ceil(GS / WS) <= NP
 #pragma unroll
     for (int j = 0; j < NP; ++j) issue(j, min(ws + j * WS, GS - 1));
+    seg_table();
     if (rs && ws == 0) compute_rstd();
 #pragma unroll
     for (int j = 0; j < NP; ++j)
@@ -445,7 +500,7 @@ __global__ __launch_bounds__(256) void rms_parts_kernel(const uint16_t* __restri
 
 typedef void (*qmv_packed_fn)(const uint16_t*, const uint8_t*, uint16_t*, int, int, int, PkEpi);
 
-template <int TN, int NP, bool SW>
+template <int TN, int NP, int SW>
 qmv_packed_fn pick_ws(int ws) {
   switch (ws) {
     case 1: return NP == 0 ? qmv_packed_kernel<TN, 1, 0, SW> : nullptr;
@@ -457,7 +512,7 @@ qmv_packed_fn pick_ws(int ws) {
   return nullptr;
 }
 
-template <int NP, bool SW>
+template <int NP, int SW>
 qmv_packed_fn pick_tn(int tn, int ws) {
   switch (tn) {
     case 1: return pick_ws<1, NP, SW>(ws);
@@ -467,7 +522,7 @@ qmv_packed_fn pick_tn(int tn, int ws) {
   return nullptr;
 }
 
-template <bool SW>
+template <int SW>
 qmv_packed_fn pick_packed(int tn, int ws, int np) {
   switch (np) {
     case 0: return pick_tn<0, SW>(tn, ws);
@@ -526,7 +581,9 @@ int launch_packed(const uint16_t* x, const uint8_t* packed, uint16_t* y, int M, 
   QVEX_CHECK_ARG(NP == 0 || (WS >= 2 && (K / PK_SET + WS - 1) / WS <= NP),
                  "%s: prefetch_sets=%d must be 0 or hold all ceil(K/256 / WS) = %d sets of a wave", fn_name, NP,
                  (K / PK_SET + WS - 1) / WS);
-  qmv_packed_fn fn = swiglu ? pick_packed<true>(TN, WS, NP) : pick_packed<false>(TN, WS, NP);
+  qmv_packed_fn fn = swiglu   ? pick_packed<1>(TN, WS, NP)
+                     : e.seg_ss ? pick_packed<2>(TN, WS, NP)
+                                : pick_packed<0>(TN, WS, NP);
   QVEX_CHECK_ARG(fn != nullptr, "%s: unsupported tile TN=%d WS=%d prefetch_sets=%d", fn_name, TN, WS, NP);
   const int threads = pk_block(WS);
   const int tiles = (N + PK_TILE - 1) / PK_TILE;
@@ -608,6 +665,30 @@ extern "C" int qvex_qmv_w4g64_packed_resid(const uint16_t* x, const void* packed
   e.u_out = u_out;
   e.sq_parts = sq_parts;
   return launch_packed(x, (const uint8_t*)packed, nullptr, M, N, K, TN, WS, false, -1, e, (hipStream_t)stream, fn);
+}
+
+extern "C" int qvex_qmv_w4g64_packed_gnorm_resid(const uint16_t* u, const void* packed, int M, int N, int K,
+                                                 const float* seg_ss, int seg_nb, float seg_eps,
+                                                 const uint16_t* resid, const uint16_t* norm_w, uint16_t* h_out,
+                                                 uint16_t* u_out, float* sq_parts, void* stream) {
+  const char* fn = "qvex_qmv_w4g64_packed_gnorm_resid";
+  QVEX_CHECK_ARG(seg_ss && resid && norm_w && h_out && u_out && sq_parts, "%s: null pointer", fn);
+  QVEX_CHECK_ARG(seg_nb == 1 || seg_nb == 2 || seg_nb == 4 || seg_nb == 8, "%s: seg_nb=%d must be 1, 2, 4 or 8", fn,
+                 seg_nb);
+  QVEX_CHECK_ARG(qvex_aligned(seg_ss, 4), "%s: seg_ss must be 4-byte aligned", fn);
+  QVEX_CHECK_ARG(K <= 64 * 128, "%s: K=%d must be at most 8192 (64 heads of 128)", fn, K);
+  int TN = 1, WS = 1;
+  if (N >= 1 && K >= PK_SET) packed_default_tile(N, K, &TN, &WS);
+  PkEpi e{};
+  e.seg_ss = seg_ss;
+  e.seg_nb = seg_nb;
+  e.seg_eps = seg_eps;
+  e.resid = resid;
+  e.norm_w = norm_w;
+  e.h_out = h_out;
+  e.u_out = u_out;
+  e.sq_parts = sq_parts;
+  return launch_packed(u, (const uint8_t*)packed, nullptr, M, N, K, TN, WS, false, -1, e, (hipStream_t)stream, fn);
 }
 
 extern "C" int qvex_qmv_w4g64_packed_rstd(const uint16_t* u, const void* packed, uint16_t* y, int M, int N, int K,

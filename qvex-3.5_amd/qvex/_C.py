@@ -28,6 +28,7 @@ SIGNATURES: dict[str, list] = {
     "qvex_qmv_w4g64_packed_tiled": [P, P, P, I, I, I, I, I, I, P],
     "qvex_qmv_w4g64_packed_resid": [P, P, I, I, I, P, P, P, P, P, P],
     "qvex_qmv_w4g64_packed_rstd": [P, P, P, I, I, I, P, I, I, F, I, P],
+    "qvex_qmv_w4g64_packed_gnorm_resid": [P, P, I, I, I, P, I, F, P, P, P, P, P, P],
     "qvex_rms_parts": [P, P, P, P, I, I, P],
     "qvex_qmv_w4g64_packed_argmax": [P, P, I, I, I, P, I, I, F, P, P, U64, P],
     "qvex_w4g64_pack_swiglu": [P, P, P, I, I, P, U64, P],
@@ -35,6 +36,7 @@ SIGNATURES: dict[str, list] = {
     "qvex_gdn_recurrent": [P, P, P, P, P, P, P, P, P, I, P, I, I, I, I, I, I, P],
     "qvex_gdn_recurrent_ring": [P, P, P, P, P, P, P, P, I, P, I, P, I, I, I, I, I, I, P],
     "qvex_gdn_decode_fused": [P, LNG, P, I, P, P, I, I, I, F, F, F, P, P, I, I, P, I, I, P, F, P, I, I, I, I, I, P],
+    "qvex_gdn_decode_split": [P, LNG, P, I, P, P, I, I, I, F, F, F, P, P, I, I, P, I, I, P, P, P, I, I, I, I, I, I, P],
     "qvex_gdn_chunked": [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P, U64, P],
     "qvex_spec_accept": [P, P, P, P, P, F, P, P, I, I, I, P, U64, P],
     "qvex_spec_accept_filtered": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P, U64, P],

@@ -162,6 +162,38 @@ def qmv_packed_resid(x: torch.Tensor, packed: torch.Tensor, N: int, resid: torch
     return h_out, u_out, parts
 
 
+def qmv_packed_gnorm_resid(u: torch.Tensor, ss_parts: torch.Tensor, packed: torch.Tensor, N: int, eps: float,
+                           resid: torch.Tensor, norm_w: torch.Tensor, h_out: torch.Tensor | None = None):
+    """out_proj over the gated norm's unscaled input u = bf16(silu(z) * w * y)
+    [M, K] (heads of 128 columns), each head's share of the product scaled by
+    rsqrt(sum(ss_parts[r, head, :]) / 128 + eps) (ss_parts [M, K/128, nb] fp32,
+    nb in 1, 2, 4, 8), then the residual epilogue of qmv_packed_resid.
+    Returns (h, u_next, parts)."""
+    K = u.shape[-1]
+    u2 = u.reshape(-1, K)
+    M = u2.shape[0]
+    _check(u2, "u", torch.bfloat16, 2)
+    _check(ss_parts, "ss_parts", torch.float32)
+    _check(resid, "resid", torch.bfloat16)
+    _check(norm_w, "norm_w", torch.bfloat16)
+    nb = ss_parts.shape[-1]
+    if ss_parts.numel() != M * (K // 128) * nb or K % 128:
+        raise _C.QvexError(f"ss_parts must hold M * K/128 * nb = {M * (K // 128) * nb} values")
+    if resid.numel() != M * N or norm_w.numel() != N:
+        raise _C.QvexError(f"resid must hold M*N = {M * N} and norm_w N = {N} values")
+    if packed.numel() != int(_C.lib().qvex_w4g64_packed_bytes(N, K)):
+        raise _C.QvexError(f"packed has {packed.numel()} bytes, not the size of an N={N} K={K} pack")
+    tiles = (N + 15) // 16
+    h_out = torch.empty((M, N), dtype=torch.bfloat16, device=u.device) if h_out is None else h_out
+    u_out = torch.empty((M, N), dtype=torch.bfloat16, device=u.device)
+    parts = torch.empty((M, tiles), dtype=torch.float32, device=u.device)
+    if h_out.numel() != M * N:
+        raise _C.QvexError("h_out has the wrong size")
+    _C.call("qvex_qmv_w4g64_packed_gnorm_resid", _ptr(u2), _ptr(packed), M, N, K, _ptr(ss_parts), nb, float(eps),
+            _ptr(resid), _ptr(norm_w), _ptr(h_out), _ptr(u_out), _ptr(parts), _stream())
+    return h_out, u_out, parts
+
+
 def qmv_packed_rstd(u: torch.Tensor, packed: torch.Tensor, N: int, parts: torch.Tensor, eps: float,
                     out: torch.Tensor | None = None, swiglu: bool = False) -> torch.Tensor:
     """quantized_matmul_packed of rms_norm(h) given as u = bf16(h * w) and the

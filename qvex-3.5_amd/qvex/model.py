@@ -492,6 +492,10 @@ class GatedDeltaNet:
     # one kernel (qvex_gdn_decode_fused, bitwise the three-kernel path)
     FUSED_MAX_T = 8
     fused_decode = True
+    # with the norms folded (resid given, <= 4 rows) each head is split over this
+    # many workgroups (qvex_gdn_decode_split) and the gated norm's scale moves
+    # into the out_proj; 0 keeps one workgroup per head
+    split_blocks = 4
 
     def _out(self, g, resid, norm_w, eps):
         if resid is not None:
@@ -505,6 +509,13 @@ class GatedDeltaNet:
         dev = x.device
         proj = self.in_proj(x)                                    # [S, conv | z | b | a]
         if self.fused_decode and S <= self.FUSED_MAX_T and self.dk == 128 and self.dv == 128 and self.K == 4:
+            if (self.split_blocks and resid is not None and S <= QLinear.PACKED_MAX_ROWS
+                    and self.out_proj.packed is not None and NormedRows.supported(self.out_proj.N)):
+                u, ss = self.mix_split(proj, cache)
+                h, un, parts = kernels.qmv_packed_gnorm_resid(u, ss, self.out_proj.packed, self.out_proj.N,
+                                                              float(self.cfg.rms_norm_eps), resid.reshape(S, -1),
+                                                              norm_w)
+                return h, NormedRows(un, parts, eps)
             return self._out(self.mix_fused(proj, cache), resid, norm_w, eps)
         q = torch.empty((1, S, self.hk, self.dk), dtype=torch.bfloat16, device=dev)
         k = torch.empty_like(q)
@@ -543,6 +554,25 @@ class GatedDeltaNet:
         cache.offset += S
         cache.last_width = S if snap else 0
         return g
+
+    def mix_split(self, proj, cache: RecurrentCache):
+        """mix_fused over split_blocks workgroups per head: returns the unscaled
+        gated-norm input u [S, value_dim] and the per-workgroup sums of y^2
+        [S, hv, split_blocks] (the out_proj applies the scale)."""
+        S = proj.shape[0]
+        nb = self.split_blocks
+        u = torch.empty((S, self.value_dim), dtype=torch.bfloat16, device=proj.device)
+        ss = torch.empty((S, self.hv, nb), dtype=torch.float32, device=proj.device)
+        inv = self.dk ** -0.5
+        snap = S <= cache.n_slots - 1
+        _C.call("qvex_gdn_decode_split", _ptr(proj), proj.stride(0), _ptr(cache.conv_ring), cache.ring_rows,
+                cache.counters.ptr(cache.index), _ptr(self.conv_w), self.K, self.conv_dim, self.key_dim,
+                float(inv * inv), float(inv), 1e-6, _ptr(self.A_log), _ptr(self.dt_bias), self.conv_dim,
+                self.conv_dim + self.value_dim, _ptr(cache.ssm_ring), cache.n_slots, int(snap), _ptr(self.norm_w),
+                _ptr(u), _ptr(ss), S, self.hk, self.hv, self.dk, self.dv, nb, _stream())
+        cache.offset += S
+        cache.last_width = S if snap else 0
+        return u, ss
 
 
 class MLP:

@@ -137,6 +137,43 @@ def test_gdn_decode_fused_argument_rules():
         call(stride=C + 100)
 
 
+def test_gdn_decode_split_argument_rules():
+    buf = ctypes.create_string_buffer(1 << 12)
+    p = (ctypes.addressof(buf) + 15) // 16 * 16
+    C, kd = 2 * 256 + 512, 256
+
+    def call(T=4, nb=8, Dk=128, n_slots=9, R=67):
+        _C.call("qvex_gdn_decode_split", p, C + 512 + 8, p, R, p, p, 4, C, kd, 1.0, 1.0, 1e-6, p, p, C, C + 512,
+                p, n_slots, 1, p, p, p, T, 2, 4, Dk, 128, nb, None)
+
+    for nb in (0, 1, 3, 16):
+        with pytest.raises(_C.QvexError, match="blocks_per_head"):
+            call(nb=nb)
+    with pytest.raises(_C.QvexError, match="1..8"):
+        call(T=9)
+    with pytest.raises(_C.QvexError, match="Dk = Dv = 128"):
+        call(Dk=64)
+    with pytest.raises(_C.QvexError, match="n_slots"):
+        call(n_slots=4)
+    with pytest.raises(_C.QvexError, match="ring_rows"):
+        call(R=6)
+    with pytest.raises(_C.QvexError, match="null pointer"):
+        _C.call("qvex_gdn_decode_split", p, C + 520, p, 67, p, p, 4, C, kd, 1.0, 1.0, 1e-6, p, p, C, C + 512,
+                p, 9, 1, p, p, None, 4, 2, 4, 128, 128, 8, None)
+
+
+def test_gnorm_resid_argument_rules():
+    buf = ctypes.create_string_buffer(1 << 14)
+    p = (ctypes.addressof(buf) + 15) // 16 * 16
+    for nb in (0, 3, 16):
+        with pytest.raises(_C.QvexError, match="seg_nb"):
+            _C.call("qvex_qmv_w4g64_packed_gnorm_resid", p, p, 1, 16, 256, p, nb, 1e-6, p, p, p, p, p, None)
+    with pytest.raises(_C.QvexError, match="null pointer"):
+        _C.call("qvex_qmv_w4g64_packed_gnorm_resid", p, p, 1, 16, 256, None, 8, 1e-6, p, p, p, p, p, None)
+    with pytest.raises(_C.QvexError, match="outside 1..4"):
+        _C.call("qvex_qmv_w4g64_packed_gnorm_resid", p, p, 5, 16, 256, p, 8, 1e-6, p, p, p, p, p, None)
+
+
 def test_resid_norm_products_argument_rules():
     buf = ctypes.create_string_buffer(1 << 14)
     p = (ctypes.addressof(buf) + 15) // 16 * 16
