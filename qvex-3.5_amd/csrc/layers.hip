@@ -303,17 +303,27 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int li = lane & 15, lg = lane >> 4;
   const int GQ = Hq / Hkv;
-  const int p0 = *pos0;
-  const int kend_tile = p0 + min(L, (tile + 1) * QT);
   const int k_lo = split * keys_per_split;
-  const int k_hi = min(k_lo + keys_per_split, kend_tile);
-  if (k_lo >= k_hi) return;      // split past the visible keys: the combine never reads it
+  const uint16_t* kbase = k_cache + (size_t)kh * cap * D;
+  const uint16_t* vbase = v_cache + (size_t)kh * D * cap;
 
-  __shared__ uint32_t ps[4][16][17];     // per-wave P tile, bf16 pairs [row][key pair], padded
-  __shared__ float ob[4][16][OS];        // per-wave O for the merge
-  __shared__ float ml[4][16][2];         // per-wave (m, l)
-  __shared__ float fac[4][16];           // merge factors e^{m_w - m}
-
+  // K rows kb + 16h + li and V columns kb + 8lg .. +7 of a 128-key window, issued
+  // together (clamped in bounds; keys past k_hi are masked out of the softmax and
+  // get P = 0). The first window does not depend on the device position, so its
+  // loads go out before the position is read.
+  u32x4 kr[2][KS], vr[NT];
+  auto load_kv = [&](int kb) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint16_t* kp = kbase + (size_t)min(kb + 16 * h + li, cap - 1) * D + 8 * lg;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) kr[h][s] = load16(kp + 32 * s);
+    }
+    const int kv0 = min(kb + 8 * lg, cap - 8);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) vr[t] = load16(vbase + (size_t)(t * 16 + li) * cap + kv0);
+  };
+  load_kv(k_lo + 32 * w);
   // A operand: Q row li, dims step*32 + 8*lg .. +7 (the 1/sqrt(D) scale is applied to the scores)
   u32x4 qa[KS];
   {
@@ -323,6 +333,17 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
 #pragma unroll
     for (int s = 0; s < KS; ++s) qa[s] = ok ? load16(qp + 32 * s) : u32x4{0, 0, 0, 0};
   }
+
+  const int p0 = *pos0;
+  const int kend_tile = p0 + min(L, (tile + 1) * QT);
+  const int k_hi = min(k_lo + keys_per_split, kend_tile);
+  if (k_lo >= k_hi) return;      // split past the visible keys: the combine never reads it
+
+  __shared__ uint32_t ps[4][16][17];     // per-wave P tile, bf16 pairs [row][key pair], padded
+  __shared__ float ob[4][16][OS];        // per-wave O for the merge
+  __shared__ float ml[4][16][2];         // per-wave (m, l)
+  __shared__ float fac[4][16];           // merge factors e^{m_w - m}
+
   // the 4 rows this lane owns in accumulator layout: r = 4*lg + j
   int rlim[4];
 #pragma unroll
@@ -339,23 +360,10 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
 #pragma unroll
   for (int t = 0; t < NT; ++t) o[t] = att_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const uint16_t* kbase = k_cache + (size_t)kh * cap * D;
-  const uint16_t* vbase = v_cache + (size_t)kh * D * cap;
   const int n_it = (k_hi - k_lo + 127) / 128;          // uniform over the block (LDS barriers below)
   for (int it = 0; it < n_it; ++it) {
     const int kb = k_lo + 128 * it + 32 * w;
-    // K rows kb + 16h + li and V columns kb + 8lg .. +7, issued together (clamped in bounds,
-    // keys past k_hi are masked out of the softmax and get P = 0)
-    u32x4 kr[2][KS], vr[NT];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint16_t* kp = kbase + (size_t)min(kb + 16 * h + li, cap - 1) * D + 8 * lg;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) kr[h][s] = load16(kp + 32 * s);
-    }
-    const int kv0 = min(kb + 8 * lg, cap - 8);
-#pragma unroll
-    for (int t = 0; t < NT; ++t) vr[t] = load16(vbase + (size_t)(t * 16 + li) * cap + kv0);
+    if (it > 0) load_kv(kb);
 
     att_f32x4 sc[2];
 #pragma unroll
@@ -449,9 +457,13 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
 // out[lq, (kh*GQ + g)*D + d] = bf16(sigmoid(gate) * sum_s o_s e^{m_s-m} / sum_s l_s e^{m_s-m})
 // over the splits that hold visible keys (the count follows from the device position).
 // One 256-thread block per (kv head, tile, row): NG groups of D/4 threads, thread
-// (g, j) owns dims 4j..4j+3 of splits g, g + NG, ...; every load of a thread is
-// independent of its sums, so the whole row streams in about one round trip. The
-// groups are merged in LDS in a fixed order.
+// (g, j) owns dims 4j..4j+3 of splits g, g + NG, ... The gate and the first
+// CB splits of each thread (m, l and its 4 values) are requested before the
+// position is read; splits past the active count are dropped by selects (the
+// workspace may hold anything there). Each thread merges its splits against its
+// own maximum, the groups then merge in LDS in a fixed order. A split whose keys
+// are all invisible to the row (m = -inf) adds nothing, so a row's bits do not
+// depend on the other rows of the call.
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ ws, int nsplit, int ntile,
                                                            int keys_per_split, const int32_t* __restrict__ pos0,
@@ -460,58 +472,81 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
                                                            uint16_t* __restrict__ out) {
   constexpr int TPG = D / 4;            // threads per split group
   constexpr int NG = 256 / TPG;         // split groups
+  constexpr int CB = 8;                 // splits per thread per batch
   const int kh = blockIdx.x, tile = blockIdx.y, r = blockIdx.z;
   const int GQ = Hq / Hkv;
   if (r >= GQ * QT) return;
   const int g = r / QT, lq = tile * QT + r % QT;
   if (lq >= L) return;
   const int h = kh * GQ + g;
-  const int kend_tile = *pos0 + min(L, (tile + 1) * QT);
-  const int nact = min(nsplit, (kend_tile + keys_per_split - 1) / keys_per_split);
   const size_t rec = (size_t)16 * (D + 2);
   const float* base = ws + ((size_t)kh * ntile + tile) * nsplit * rec;
-  __shared__ float red[2][4];
-  __shared__ __align__(16) float part[NG][D];
-  const int tid = threadIdx.x, wv = tid >> 6;
-
-  // global max and normaliser over the active splits
-  float m = -INFINITY;
-  for (int s = tid; s < nact; s += 256) m = fmaxf(m, base[s * rec + 2 * r]);
-  m = wave_allmax(m);
-  if ((tid & 63) == 0) red[0][wv] = m;
-  __syncthreads();
-  m = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-  float l = 0.0f;
-  for (int s = tid; s < nact; s += 256) {
-    const float ms = base[s * rec + 2 * r];
-    if (ms != -INFINITY) l += base[s * rec + 2 * r + 1] * expf(ms - m);
-  }
-  l = wave_allsum(l);
-  if ((tid & 63) == 0) red[1][wv] = l;
-  __syncthreads();
-  l = ((red[1][0] + red[1][1]) + red[1][2]) + red[1][3];
-  const float invl = l > 0.0f ? 1.0f / l : 0.0f;
-
+  const int tid = threadIdx.x;
   const int grp = tid / TPG, j = tid % TPG;
+  __shared__ float gm[NG], gl[NG];
+  __shared__ __align__(16) float part[NG][D];
+
+  const float gt = tid < D ? bf16_to_f32(gate[(size_t)lq * g_stride + (size_t)h * 2 * D + D + tid]) : 0.0f;
+  float ms[CB], ls[CB];
+  float4 os[CB];
+  auto load_batch = [&](int s0, int lim) {
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+      const int s = s0 + grp + NG * i;
+      const bool ok = s < lim;
+      const float* rp = base + (size_t)(ok ? s : 0) * rec;
+      ms[i] = ok ? rp[2 * r] : -INFINITY;
+      ls[i] = ok ? rp[2 * r + 1] : 0.0f;
+      os[i] = ok ? *reinterpret_cast<const float4*>(rp + 32 + (size_t)r * D + 4 * j) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  };
+  load_batch(0, nsplit);
+  const int kend_tile = *pos0 + min(L, (tile + 1) * QT);
+  const int nact = min(nsplit, (kend_tile + keys_per_split - 1) / keys_per_split);
+
+  // this thread's splits, merged against its running maximum
+  float m = -INFINITY, l = 0.0f;
   float4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 8
-  for (int s = grp; s < nact; s += NG) {
-    const float ms = base[s * rec + 2 * r];
-    const float4 os = *reinterpret_cast<const float4*>(base + s * rec + 32 + (size_t)r * D + 4 * j);
-    const float f = ms == -INFINITY ? 0.0f : expf(ms - m);
-    o.x = fmaf(os.x, f, o.x);
-    o.y = fmaf(os.y, f, o.y);
-    o.z = fmaf(os.z, f, o.z);
-    o.w = fmaf(os.w, f, o.w);
+  for (int s0 = 0; s0 < nact; s0 += CB * NG) {
+    if (s0 > 0) load_batch(s0, nact);
+    float mb = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < CB; ++i)
+      if (s0 + grp + NG * i < nact) mb = fmaxf(mb, ms[i]);
+    if (mb == -INFINITY) continue;                  // nothing visible in this batch
+    const float mn = fmaxf(m, mb);
+    const float c = m == -INFINITY ? 0.0f : expf(m - mn);
+    l *= c;
+    o.x *= c; o.y *= c; o.z *= c; o.w *= c;
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+      if (s0 + grp + NG * i < nact && ms[i] != -INFINITY) {
+        const float f = expf(ms[i] - mn);
+        l = fmaf(ls[i], f, l);
+        o.x = fmaf(os[i].x, f, o.x);
+        o.y = fmaf(os[i].y, f, o.y);
+        o.z = fmaf(os[i].z, f, o.z);
+        o.w = fmaf(os[i].w, f, o.w);
+      }
+    }
+    m = mn;
   }
+  if (j == 0) { gm[grp] = m; gl[grp] = l; }
   *reinterpret_cast<float4*>(&part[grp][4 * j]) = o;
   __syncthreads();
-  for (int d = tid; d < D; d += 256) {
-    float acc = 0.0f;
+  if (tid < D) {
+    float mx = gm[0];
 #pragma unroll
-    for (int q = 0; q < NG; ++q) acc += part[q][d];
-    const float gt = bf16_to_f32(gate[(size_t)lq * g_stride + (size_t)h * 2 * D + D + d]);
-    out[(size_t)lq * Hq * D + (size_t)h * D + d] = f32_to_bf16(acc * invl * sigmoidf_(gt));
+    for (int q = 1; q < NG; ++q) mx = fmaxf(mx, gm[q]);
+    float acc = 0.0f, lt = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+      const float f = gm[q] == -INFINITY ? 0.0f : expf(gm[q] - mx);
+      acc = fmaf(part[q][tid], f, acc);
+      lt = fmaf(gl[q], f, lt);
+    }
+    const float invl = lt > 0.0f ? 1.0f / lt : 0.0f;
+    out[(size_t)lq * Hq * D + (size_t)h * D + tid] = f32_to_bf16(acc * invl * sigmoidf_(gt));
   }
 }
 
