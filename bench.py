@@ -9,7 +9,8 @@ group-64 MLX-layout weights) with an MTP draft head sharing the lm_head. A
 4096-token prompt of seeded uniform ids is prefilled (untimed), then W warmup
 cycles run, then exactly K timed MTP cycles (draft k=3 greedy, verify 4 tokens,
 accept at T=0.7 with top-k 20 / top-p 0.8 as the reference's MTP benchmark, roll back; the cycle is captured once as a HIP graph and
-replayed). value = tokens emitted in the timed cycles / time.
+replayed, each cycle launched before the previous cycle's result is read).
+value = tokens emitted in the timed cycles / time.
 
 Every line also carries:
   roofline: the dominant kernel of the cycle, the packed 4-bit MFMA qmv on the
@@ -357,16 +358,22 @@ def run_e2e(args):
         t0 = time.perf_counter()
         runner = GraphedMTPCycle(dec)
         log(f"cycle captured as a HIP graph in {time.perf_counter() - t0:.2f}s")
-    for _ in range(args.warmup):
-        runner.cycle()
+    if args.eager:
+        for _ in range(args.warmup):
+            runner.cycle()
+    else:
+        runner.run(args.warmup)            # graphed: each cycle launched before the previous result is read
     torch.cuda.synchronize()
     e0 = stats["emitted"]
     a0, c0 = stats["accepted"], stats["cycles"]
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        runner.cycle()
-        if (i + 1) % 64 == 0:
-            log(f"cycle {i + 1}/{args.steps}")
+    if args.eager:
+        for i in range(args.steps):
+            runner.cycle()
+            if (i + 1) % 64 == 0:
+                log(f"cycle {i + 1}/{args.steps}")
+    else:
+        runner.run(args.steps)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     emitted = stats["emitted"] - e0

@@ -213,24 +213,32 @@ class GraphedMTPCycle:
         cache.counters.sync()
         mc.counters.sync()
         torch.cuda.synchronize()
-        host_main = cache.counters.host.copy()
-        host_mtp = mc.counters.host.copy()
-        widths = [getattr(c, "last_width", None) for c in cache]
         cache.counters.graph_mode = True
         mc.counters.graph_mode = True
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self._body()
-        cache.counters.host[:] = host_main
-        mc.counters.host[:] = host_mtp
-        for c, w in zip(cache, widths):
+        self.graph = self._capture(self.out)
+        self._pipe = None
+
+    def _capture(self, out, pool=None) -> torch.cuda.CUDAGraph:
+        """Capture one cycle writing its result to `out`; the host mirrors the
+        capture advances are put back (capture runs no kernels)."""
+        d = self.dec
+        host_main = d.cache.counters.host.copy()
+        host_mtp = d.mtp_cache.counters.host.copy()
+        widths = [getattr(c, "last_width", None) for c in d.cache]
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, pool=pool):
+            self._body(out)
+        d.cache.counters.host[:] = host_main
+        d.mtp_cache.counters.host[:] = host_mtp
+        for c, w in zip(d.cache, widths):
             if w is not None:
                 c.last_width = w
+        return g
 
     def _commit(self, counters, n_ptr, extra):
         _C.call("qvex_commit_step", counters.dev.data_ptr(), counters.dev.numel(), _ptr(n_ptr), int(extra), _stream())
 
-    def _body(self):
+    def _body(self, out):
         d = self.dec
         k, mtp, mc = self.k, d.mtp, d.mtp_cache
         # greedy drafts straight from the MTP lm_head's argmax epilogue into the verify ids
@@ -249,16 +257,46 @@ class GraphedMTPCycle:
         # entries rolled back (net -(k-2) after the folded last advance), the
         # next feed and the next cycle's uniforms
         _C.call("qvex_cycle_finish_ex", _ptr(self.drafts), k, _ptr(n), _ptr(tok), _ptr(self.pend_ids),
-                _ptr(self.feed), _ptr(self.n_prev), _ptr(self.out), _ptr(self.ids),
+                _ptr(self.feed), _ptr(self.n_prev), _ptr(out), _ptr(self.ids),
                 d.cache.counters.dev.data_ptr(), d.cache.counters.dev.numel(), 1,
                 mc.counters.dev.data_ptr(), mc.counters.dev.numel(), -(k - 2) if k > 1 else 0,
                 _ptr(self.u_table), self.u_table.shape[0], k + 1, _ptr(self.u_idx), _ptr(self.u_buf), _stream())
-        d.sampler.observe_result(self.out)
+        d.sampler.observe_result(out)
 
     def cycle(self) -> list[int]:
         """Replay one cycle; returns the emitted tokens (n accepted drafts + 1)."""
         self.graph.replay()
-        vals = self.out.tolist()                       # the one host sync
+        return self._account(self.out.tolist())        # the one host sync
+
+    def run(self, n: int) -> list[list[int]]:
+        """n cycles, each launched before the previous one's result is read, so
+        the GPU does not wait on the host between cycles. Two graphs alternate;
+        each writes its result into its own slot of a pinned host buffer, and the
+        host waits on that graph's event rather than on the stream. The next
+        cycle only reads device state, so the token stream and the caches are
+        those of n cycle() calls, and no cycle is in flight on return. Returns
+        each cycle's emitted tokens."""
+        if self._pipe is None:
+            ring = torch.zeros((2, 2 + self.k), dtype=torch.int32, pin_memory=True)
+            graphs = [self._capture(ring[s], pool=self.graph.pool()) for s in range(2)]
+            self._pipe = (ring, graphs, [torch.cuda.Event(), torch.cuda.Event()])
+        ring, graphs, evs = self._pipe
+        res = []
+        if n <= 0:
+            return res
+        graphs[0].replay()
+        evs[0].record()
+        for c in range(n):
+            s = c % 2
+            if c + 1 < n:
+                graphs[1 - s].replay()
+                evs[1 - s].record()
+            evs[s].synchronize()
+            res.append(self._account(ring[s].tolist()))
+        return res
+
+    def _account(self, vals) -> list[int]:
+        """Host mirrors and stats of one finished cycle from its [n, token, drafts]."""
         n, tok = int(vals[0]), int(vals[1])
         d = self.dec
         for c in d.cache:

@@ -224,3 +224,36 @@ def test_graphed_cycle_equals_eager_reference_sampling(head):
     assert te == tg
     assert torch.equal(eager.sampler.seen, graphed.dec.sampler.seen)
     assert int(eager.sampler.seen.sum().item()) == len(set(te + [eager.first]))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("head", ["random", "flat"])
+def test_graphed_run_pipelined_equals_cycles(head):
+    """run(n) launches each cycle before reading the previous one's result (two
+    graphs writing pinned host slots): same tokens, cache counters and presence
+    mask as the same number of cycle() calls, also when the two are mixed."""
+    from qvex.speculative import GraphedMTPCycle
+    m = random_model(Config.tiny(layers=4, vocab=2048), seed=21, device=DEV, max_context=1024) \
+        if head == "random" else flat_head_model(seed=22)
+    mtp = random_mtp(m, seed=23)
+    params = dict(top_k=20, top_p=0.95, presence_penalty=0.5)
+    a = GraphedMTPCycle(start_decoder(m, mtp, 3, 0.6, seed=7, **params))
+    b = GraphedMTPCycle(start_decoder(m, mtp, 3, 0.6, seed=7, **params))
+    ta = []
+    for _ in range(13):
+        ta += a.cycle()
+    tb = []
+    for part in b.run(5):
+        tb += part
+    tb += b.cycle()
+    tb += b.cycle()
+    assert b.run(0) == []
+    for part in b.run(6):
+        tb += part
+    assert ta == tb
+    assert a.dec.stats["cycles"] == b.dec.stats["cycles"] == 13
+    assert [c.offset for c in a.dec.cache] == [c.offset for c in b.dec.cache]
+    assert a.dec.mtp_cache.offset == b.dec.mtp_cache.offset
+    assert torch.equal(a.dec.cache.counters.dev, b.dec.cache.counters.dev)
+    assert torch.equal(a.dec.mtp_cache.counters.dev, b.dec.mtp_cache.counters.dev)
+    assert torch.equal(a.dec.sampler.seen, b.dec.sampler.seen)
