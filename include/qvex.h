@@ -312,6 +312,15 @@ int qvex_embed_w4g64(const int32_t* ids, int L, const uint32_t* w, const uint16_
 int qvex_rmsnorm(const uint16_t* x, long x_stride, const uint16_t* w, uint16_t* out,
                  long out_stride, int R, int D, float eps, float scale, void* stream);
 
+/* Two qvex_rmsnorm calls in one launch: out0 = rms_norm(x0) * w0 and
+ * out1 = rms_norm(x1) * w1, R rows each of width D (same rules as qvex_rmsnorm,
+ * scale 1). The MTP head's input norms (engine/mtp.py:63-65: rms of the
+ * embedding and of the hidden, concatenated): out0, out1 are the two halves of
+ * the fc input row, sharing out_stride. */
+int qvex_rmsnorm_pair(const uint16_t* x0, long x0_stride, const uint16_t* w0, uint16_t* out0,
+                      const uint16_t* x1, long x1_stride, const uint16_t* w1, uint16_t* out1,
+                      long out_stride, int R, int D, float eps, void* stream);
+
 /* h = bf16(x + delta); out = rms_norm(h) * w: the residual add and the next
  * pre-norm of Layer.__call__ (engine/model.py:313-316) in one pass. [R, D],
  * D % 8 == 0, D <= 8192, pointers 16-byte aligned. */

@@ -66,6 +66,22 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
                   w, out + row * o_stride, D, eps, scale, red);
 }
 
+// Two independent row sets in one launch (grid.y selects the set): the MTP
+// head's two input norms, each written into its half of the fc input.
+__global__ __launch_bounds__(256) void rmsnorm_pair_kernel(const uint16_t* __restrict__ x0, long x0_stride,
+                                                           const uint16_t* __restrict__ w0,
+                                                           uint16_t* __restrict__ out0,
+                                                           const uint16_t* __restrict__ x1, long x1_stride,
+                                                           const uint16_t* __restrict__ w1,
+                                                           uint16_t* __restrict__ out1, long o_stride, int D,
+                                                           float eps) {
+  __shared__ float red[4];
+  const int row = blockIdx.x;
+  const bool second = blockIdx.y != 0;
+  rms_row256<false>((second ? x1 : x0) + row * (second ? x1_stride : x0_stride), nullptr, nullptr,
+                    second ? w1 : w0, (second ? out1 : out0) + row * o_stride, D, eps, 1.0f, red);
+}
+
 // ---------------------------------------------------------------- GDN: conv1d + SiLU + q/k norm
 //
 // The conv input history is a ring of R rows per layer keyed by the token count
@@ -583,6 +599,23 @@ extern "C" int qvex_rmsnorm(const uint16_t* x, long x_stride, const uint16_t* w,
   hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3(R), dim3(256), 0, (hipStream_t)stream, x, x_stride,
                      (const uint16_t*)nullptr, 0L, (uint16_t*)nullptr, 0L, w, out, out_stride, R, D, eps, scale);
   QVEX_CHECK_LAUNCH("qvex_rmsnorm");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_rmsnorm_pair(const uint16_t* x0, long x0_stride, const uint16_t* w0, uint16_t* out0,
+                                 const uint16_t* x1, long x1_stride, const uint16_t* w1, uint16_t* out1,
+                                 long out_stride, int R, int D, float eps, void* stream) {
+  QVEX_CHECK_ARG(x0 && x1 && out0 && out1, "qvex_rmsnorm_pair: null pointer");
+  QVEX_CHECK_ARG(R >= 1 && D >= 8 && D % 8 == 0 && D <= 256 * 8 * RMS_MAXC && x0_stride >= D && x1_stride >= D &&
+                     out_stride >= D && x0_stride % 8 == 0 && x1_stride % 8 == 0 && out_stride % 8 == 0,
+                 "qvex_rmsnorm_pair: R=%d D=%d strides %ld/%ld/%ld (D %% 8 == 0, D <= 8192, strides %% 8 == 0)", R,
+                 D, x0_stride, x1_stride, out_stride);
+  QVEX_CHECK_ARG(qvex_aligned(x0, 16) && qvex_aligned(x1, 16) && qvex_aligned(out0, 16) && qvex_aligned(out1, 16) &&
+                     (!w0 || qvex_aligned(w0, 16)) && (!w1 || qvex_aligned(w1, 16)),
+                 "qvex_rmsnorm_pair: pointers must be 16-byte aligned");
+  hipLaunchKernelGGL(rmsnorm_pair_kernel, dim3(R, 2), dim3(256), 0, (hipStream_t)stream, x0, x0_stride, w0, out0,
+                     x1, x1_stride, w1, out1, out_stride, D, eps);
+  QVEX_CHECK_LAUNCH("qvex_rmsnorm_pair");
   return QVEX_OK;
 }
 

@@ -45,6 +45,7 @@ SIGNATURES: dict[str, list] = {
     "qvex_embed_w4g64": [P, I, P, P, P, I, I, P, P],
     "qvex_rmsnorm": [P, LNG, P, P, LNG, I, I, F, F, P],
     "qvex_add_rmsnorm": [P, P, P, P, P, I, I, F, P],
+    "qvex_rmsnorm_pair": [P, LNG, P, P, P, LNG, P, P, LNG, I, I, F, P],
     "qvex_gdn_conv_qk": [P, LNG, P, I, P, P, I, P, P, P, P, P, I, I, I, I, I, F, F, F, P],
     "qvex_commit_step": [P, I, P, I, P],
     "qvex_gather_row": [P, LNG, P, I, P, I, P],

@@ -61,8 +61,9 @@ class MTPHead:
         cache.counters.sync()
         e = self.model.embed(ids)
         x_in = torch.empty((T, 2 * H), dtype=torch.bfloat16, device=h.device)
-        rms_norm(e, self.norm_emb, self.eps, out=x_in[:, :H])
-        rms_norm(h, self.norm_hid, self.eps, out=x_in[:, H:])
+        # [rms(embed) | rms(hidden)] in one launch
+        _C.call("qvex_rmsnorm_pair", _ptr(e), e.stride(0), _ptr(self.norm_emb), _ptr(x_in), _ptr(h), h.stride(0),
+                _ptr(self.norm_hid), _ptr(x_in) + 2 * H, x_in.stride(0), T, H, float(self.eps), _stream())
         x = self.fc(x_in)
         V = self.model.cfg.vocab_size
         if self.model.fuse_norms and T <= QLinear.PACKED_MAX_ROWS and NormedRows.supported(H):

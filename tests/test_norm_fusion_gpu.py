@@ -134,3 +134,31 @@ def test_model_fused_rows_independent_of_width(tiny):
     wide = run(tiny, [ids], True)[0][0]
     narrow = torch.cat([o[0] for o in run(tiny, [[t] for t in ids], True)])
     assert torch.equal(wide, narrow)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("R,D", [(1, 4096), (4, 4096), (3, 512)])
+def test_rmsnorm_pair_equals_two_calls(R, D):
+    """qvex_rmsnorm_pair (the MTP head's two input norms into the halves of the fc
+    input) = two qvex_rmsnorm calls bit for bit, and rms_norm(x) * w in float64
+    within bf16 rounding (engine/mtp.py:63-65)."""
+    from qvex import _C
+    from qvex.kernels import _ptr, _stream
+    from qvex.model import rms_norm
+    g = torch.Generator().manual_seed(R * 7 + D)
+    x0 = (torch.randn(R, D, generator=g) * 3).to(torch.bfloat16).to(DEV)
+    x1 = torch.randn(R, D + 64, generator=g).to(torch.bfloat16).to(DEV)[:, :D]       # strided rows
+    w0 = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(DEV)
+    w1 = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(DEV)
+    pair = torch.empty(R, 2 * D, dtype=torch.bfloat16, device=DEV)
+    _C.call("qvex_rmsnorm_pair", _ptr(x0), x0.stride(0), _ptr(w0), _ptr(pair), _ptr(x1), x1.stride(0), _ptr(w1),
+            _ptr(pair) + 2 * D, pair.stride(0), R, D, EPS, _stream())
+    two = torch.empty_like(pair)
+    rms_norm(x0, w0, EPS, out=two[:, :D])
+    rms_norm(x1, w1, EPS, out=two[:, D:])
+    torch.cuda.synchronize()
+    assert torch.equal(pair.view(torch.int16), two.view(torch.int16))
+    for x, w, o in ((x0, w0, pair[:, :D]), (x1, w1, pair[:, D:])):
+        xx = bf(x)
+        ref = xx / np.sqrt((xx ** 2).mean(-1, keepdims=True) + EPS) * bf(w)
+        assert (np.abs(bf(o) - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-6).all()
