@@ -138,23 +138,34 @@ __device__ __forceinline__ float pen_x(const float* seen, float pen, float x, in
   return x - pen * sj;
 }
 
-// A thread's next two values in (value descending, slot ascending) order after
-// (lv, li): strictly greater values move ahead, so an earlier slot wins a tie.
-// Empty entries are (-inf, NS).
+// A thread's next NB values in (value descending, slot ascending) order after
+// (lv, li), into bv/bi (descending): strictly greater values move ahead, so an
+// earlier slot wins a tie. Empty entries are (-inf, NS).
+constexpr int TOPK_BUF = 4;
 template <int NS>
-__device__ __forceinline__ void next_two(const float (&v)[NS], float lv, int li, float& b0, int& i0, float& b1,
-                                         int& i1) {
-  b0 = b1 = -__builtin_inff();
-  i0 = i1 = NS;
+__device__ __forceinline__ void next_buf(const float (&v)[NS], float lv, int li, float (&bv)[TOPK_BUF],
+                                         int (&bi)[TOPK_BUF]) {
+#pragma unroll
+  for (int e = 0; e < TOPK_BUF; ++e) {
+    bv[e] = -__builtin_inff();
+    bi[e] = NS;
+  }
 #pragma unroll
   for (int q = 0; q < NS; ++q) {
-    const bool after = v[q] < lv || (v[q] == lv && q > li);
+    // bitwise, not short-circuit: a per-element branch here is what the
+    // compiler makes of ||, and a rescan then costs a branch per slot
+    const bool after = (v[q] < lv) | ((v[q] == lv) & (q > li));
     const float x = after ? v[q] : -__builtin_inff();
-    const bool c0 = x > b0, c1 = x > b1;
-    b1 = c0 ? b0 : (c1 ? x : b1);
-    i1 = c0 ? i0 : (c1 ? q : i1);
-    b0 = c0 ? x : b0;
-    i0 = c0 ? q : i0;
+    bool gt[TOPK_BUF];
+#pragma unroll
+    for (int e = 0; e < TOPK_BUF; ++e) gt[e] = x > bv[e];
+#pragma unroll
+    for (int e = TOPK_BUF - 1; e > 0; --e) {
+      bv[e] = gt[e - 1] ? bv[e - 1] : (gt[e] ? x : bv[e]);
+      bi[e] = gt[e - 1] ? bi[e - 1] : (gt[e] ? q : bi[e]);
+    }
+    bv[0] = gt[0] ? x : bv[0];
+    bi[0] = gt[0] ? q : bi[0];
   }
 }
 
@@ -162,28 +173,32 @@ __device__ __forceinline__ void next_two(const float (&v)[NS], float lv, int li,
 // descending; v holds the calling thread's NS values, -inf for none. Each wave
 // extracts its own K largest, one wave maximum per round (ties: lowest lane),
 // with no block barrier inside the rounds; a thread serves its values from a
-// two-entry buffer and rescans its registers only when the buffer runs dry.
+// TOPK_BUF-entry buffer and rescans its registers only when the buffer runs
+// dry (a lane must win TOPK_BUF rounds first).
 // The four sorted lists are then merged by rank: entry i of wave w lands at
 // i + #(entries of other waves that are larger, or equal and from a lower
 // wave), which is unique. wl: 4 * K floats.
 template <int NS>
 __device__ __forceinline__ void block_topk(const float (&v)[NS], int K, float* lst, float* wl) {
-  float b0, b1;
-  int i0, i1;
-  next_two(v, __builtin_inff(), -1, b0, i0, b1, i1);
+  float bv[TOPK_BUF];
+  int bi[TOPK_BUF];
+  next_buf(v, __builtin_inff(), -1, bv, bi);
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   for (int r = 0; r < K; ++r) {
-    const float m = wave_allmax(b0);
-    const unsigned long long msk = __ballot(b0 == m);
+    const float m = wave_allmax(bv[0]);
+    const unsigned long long msk = __ballot(bv[0] == m);
     if (lane == 0) wl[wave * K + r] = m;
     if (lane == __ffsll(msk) - 1) {
-      const float lv = b0;
-      const int li = i0;
-      b0 = b1;
-      i0 = i1;
-      b1 = -__builtin_inff();
-      i1 = NS;
-      if (i0 == NS && li < NS) next_two(v, lv, li, b0, i0, b1, i1);
+      const float lv = bv[0];
+      const int li = bi[0];
+#pragma unroll
+      for (int e = 0; e + 1 < TOPK_BUF; ++e) {
+        bv[e] = bv[e + 1];
+        bi[e] = bi[e + 1];
+      }
+      bv[TOPK_BUF - 1] = -__builtin_inff();
+      bi[TOPK_BUF - 1] = NS;
+      if (bi[0] == NS && li < NS) next_buf(v, lv, li, bv, bi);
     }
   }
   __syncthreads();
