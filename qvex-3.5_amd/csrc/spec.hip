@@ -619,6 +619,29 @@ __global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
     }
   }
   __syncthreads();
+  // the k accept tests, one thread each (their gathers in flight together);
+  // thread 0 then takes the first rejection, as the serial rule does
+  __shared__ int s_ok[32];
+  if (!a.greedy && t < k) {
+    const int i = t;
+    const int32_t* d = a.ids + (long)step * k;
+    const int di = d[i];
+    int ok = 0;
+    if (!(di < 0 || di >= a.V)) {
+      const float zd = pen_x(a.seen, a.pen, lg(row_ptr(a, step, i), di, a.bf), di, d, i) * a.inv_temp;
+      const float ep = zd >= rc[i] ? qx_expf(zd - rm[i]) : 0.0f;
+      float eq = 1.0f, Sq = 1.0f;
+      if (a.draft) {
+        eq = qx_expf(lg(row_ptr(a, step, k + 1 + i), di, a.bf) * a.inv_temp - rm[k + 1 + i]);
+        Sq = rs[k + 1 + i];
+      }
+      const float lhs = a.u_acc[(long)step * k + i] * eq * rs[i];
+      const float rhs = ep * Sq;
+      ok = lhs < rhs ? 1 : 0;
+    }
+    s_ok[i] = ok;
+  }
+  __syncthreads();
   if (t == 0) {
     const int32_t* d = a.ids + (long)step * k;
     int n = k, tok = -1;
@@ -629,20 +652,8 @@ __global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
       }
       if (n == k) tok = __float_as_int(rm[k]);
     } else {
-      for (int i = 0; i < k; ++i) {
-        const int di = d[i];
-        if (di < 0 || di >= a.V) { n = i; break; }
-        const float zd = pen_x(a.seen, a.pen, lg(row_ptr(a, step, i), di, a.bf), di, d, i) * a.inv_temp;
-        const float ep = zd >= rc[i] ? qx_expf(zd - rm[i]) : 0.0f;
-        float eq = 1.0f, Sq = 1.0f;
-        if (a.draft) {
-          eq = qx_expf(lg(row_ptr(a, step, k + 1 + i), di, a.bf) * a.inv_temp - rm[k + 1 + i]);
-          Sq = rs[k + 1 + i];
-        }
-        const float lhs = a.u_acc[(long)step * k + i] * eq * rs[i];
-        const float rhs = ep * Sq;
-        if (!(lhs < rhs)) { n = i; break; }
-      }
+      for (int i = 0; i < k; ++i)
+        if (!s_ok[i]) { n = i; break; }
     }
     s_n = n;
     s_tok = tok;
@@ -733,53 +744,93 @@ __global__ __launch_bounds__(NT) void spec_sample_kernel(SpecArgs a) {
   c.tq = (n < k && a.draft) ? row_ptr(a, step, k + 1 + n) : nullptr;
   c.mode = n < k ? 0 : 1;
   const float u = a.u_smp[step];
+  // The walks are sequential fp32 sums (the fixed order), done by thread 0, but
+  // over values the block first stages in LDS: the part sums, then the chosen
+  // part's thread sums, then the chosen thread's element weights.
+  const float* Ws = W.W + (long)step * a.P;
+  const float* Ts = W.T + (long)step * a.P * NT;
+  float* sT = Tpt;                  // [NT] (Tpt is rebuilt by the fallback pass)
+  float* sW = Wp;                   // [P]
+  __shared__ float sE[4 * NI];
+  __shared__ float s_cacc, s_th, s_Wt;
+  __shared__ int s_ps, s_ts, s_fb;
+  for (int p = t; p < a.P; p += NT) sW[p] = Ws[p];
+  __syncthreads();
   if (t == 0) {
-    const float* Ws = W.W + (long)step * a.P;
-    const float* Ts = W.T + (long)step * a.P * NT;
     float Wt = 0.0f;
-    for (int p = 0; p < a.P; ++p) Wt = Wt + Ws[p];
-    int res = -1;
+    for (int p = 0; p < a.P; ++p) Wt = Wt + sW[p];
+    int ps = -1;
+    bool fallback = false;
+    float cacc = 0.0f, th = 0.0f;
     if (Wt > 0.0f) {
-      const float th = u * Wt;
-      float cacc = 0.0f;
-      int ps = -1;
+      th = u * Wt;
       for (int p = 0; p < a.P; ++p) {
-        const float nx = cacc + Ws[p];
+        const float nx = cacc + sW[p];
         if (nx > th) { ps = p; break; }
         cacc = nx;
       }
-      bool fallback = false;
       if (ps < 0) {
         for (int p = a.P - 1; p >= 0; --p)
-          if (Ws[p] > 0.0f) { ps = p; break; }
+          if (sW[p] > 0.0f) { ps = p; break; }
         fallback = true;
       }
-      int ts = -1;
-      if (!fallback) {
-        for (int tt = 0; tt < NT; ++tt) {
-          const float nx = cacc + Ts[ps * NT + tt];
-          if (nx > th) { ts = tt; break; }
-          cacc = nx;
-        }
+    }
+    s_Wt = Wt;
+    s_th = th;
+    s_cacc = cacc;
+    s_ps = ps;
+    s_fb = fallback ? 1 : 0;
+  }
+  __syncthreads();
+  const int ps = s_ps;
+  if (ps >= 0) sT[t] = Ts[ps * NT + t];
+  __syncthreads();
+  if (t == 0 && ps >= 0) {
+    bool fallback = s_fb != 0;
+    float cacc = s_cacc;
+    const float th = s_th;
+    int ts = -1;
+    if (!fallback) {
+      for (int tt = 0; tt < NT; ++tt) {
+        const float nx = cacc + sT[tt];
+        if (nx > th) { ts = tt; break; }
+        cacc = nx;
       }
-      if (ts < 0) {
-        for (int tt = NT - 1; tt >= 0; --tt)
-          if (Ts[ps * NT + tt] > 0.0f) { ts = tt; break; }
-        fallback = true;
-      }
-      const int base = ps * PART, end = min(a.V, base + PART);
-      if (!fallback) {
-        for (int s = 0; s < 4 * NI; ++s) {
-          const int j = base + 4 * (ts + NT * (s >> 2)) + (s & 3);
+    }
+    if (ts < 0) {
+      for (int tt = NT - 1; tt >= 0; --tt)
+        if (sT[tt] > 0.0f) { ts = tt; break; }
+      fallback = true;
+    }
+    s_ts = ts;
+    s_fb = fallback ? 1 : 0;
+    s_cacc = cacc;
+  }
+  __syncthreads();
+  const int base = ps * PART, end = min(a.V, base + PART);
+  const int ts = ps >= 0 ? s_ts : -1;
+  if (ts >= 0 && t < 4 * NI) {
+    const int j = base + 4 * (ts + NT * (t >> 2)) + (t & 3);
+    sE[t] = j < end ? weight(c, j) : 0.0f;
+  }
+  __syncthreads();
+  if (t == 0) {
+    int res = -1;
+    if (s_Wt > 0.0f && ts >= 0) {
+      const float th = s_th;
+      float cacc = s_cacc;
+      if (!s_fb) {
+        for (int q = 0; q < 4 * NI; ++q) {
+          const int j = base + 4 * (ts + NT * (q >> 2)) + (q & 3);
           if (j >= end) break;
-          cacc = cacc + weight(c, j);
+          cacc = cacc + sE[q];
           if (cacc > th) { res = j; break; }
         }
       }
       if (res < 0) {
-        for (int s = 4 * NI - 1; s >= 0; --s) {
-          const int j = base + 4 * (ts + NT * (s >> 2)) + (s & 3);
-          if (j < end && weight(c, j) > 0.0f) { res = j; break; }
+        for (int q = 4 * NI - 1; q >= 0; --q) {
+          const int j = base + 4 * (ts + NT * (q >> 2)) + (q & 3);
+          if (j < end && sE[q] > 0.0f) { res = j; break; }
         }
       }
     }
