@@ -764,10 +764,19 @@ __global__ __launch_bounds__(NT) void spec_sample_kernel(SpecArgs a) {
     float cacc = 0.0f, th = 0.0f;
     if (Wt > 0.0f) {
       th = u * Wt;
-      for (int p = 0; p < a.P; ++p) {
-        const float nx = cacc + sW[p];
-        if (nx > th) { ps = p; break; }
-        cacc = nx;
+      // eight values per LDS round trip; the adds stay sequential
+      for (int p0 = 0; p0 < a.P && ps < 0; p0 += 8) {
+        float r[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[e] = p0 + e < a.P ? sW[p0 + e] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (ps < 0 && p0 + e < a.P) {
+            const float nx = cacc + r[e];
+            if (nx > th) ps = p0 + e;
+            else cacc = nx;
+          }
+        }
       }
       if (ps < 0) {
         for (int p = a.P - 1; p >= 0; --p)
@@ -791,10 +800,18 @@ __global__ __launch_bounds__(NT) void spec_sample_kernel(SpecArgs a) {
     const float th = s_th;
     int ts = -1;
     if (!fallback) {
-      for (int tt = 0; tt < NT; ++tt) {
-        const float nx = cacc + sT[tt];
-        if (nx > th) { ts = tt; break; }
-        cacc = nx;
+      for (int t0 = 0; t0 < NT && ts < 0; t0 += 8) {
+        float r[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[e] = sT[t0 + e];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (ts < 0) {
+            const float nx = cacc + r[e];
+            if (nx > th) ts = t0 + e;
+            else cacc = nx;
+          }
+        }
       }
     }
     if (ts < 0) {
@@ -820,11 +837,23 @@ __global__ __launch_bounds__(NT) void spec_sample_kernel(SpecArgs a) {
       const float th = s_th;
       float cacc = s_cacc;
       if (!s_fb) {
-        for (int q = 0; q < 4 * NI; ++q) {
-          const int j = base + 4 * (ts + NT * (q >> 2)) + (q & 3);
-          if (j >= end) break;
-          cacc = cacc + sE[q];
-          if (cacc > th) { res = j; break; }
+        bool stop = false;
+        for (int q0 = 0; q0 < 4 * NI && !stop; q0 += 8) {
+          float r[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) r[e] = sE[q0 + e];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int j = base + 4 * (ts + NT * ((q0 + e) >> 2)) + ((q0 + e) & 3);
+            if (!stop) {
+              if (j >= end) {
+                stop = true;
+              } else {
+                cacc = cacc + r[e];
+                if (cacc > th) { res = j; stop = true; }
+              }
+            }
+          }
         }
       }
       if (res < 0) {
