@@ -403,30 +403,18 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArg
     for (int t = 0; t < FUSED_TMAX; ++t)
       zr[t] = t < T ? bf16_to_f32(p.proj[(size_t)t * p.p_stride + p.z_off + hv * DK + dv]) : 0.0f;
   }
-  // 1. conv + silu: q and k heads (128 channels, one wave each, normed as in
-  // conv_silu_qk_kernel) and this block's RB v channels; each task's loads are
-  // issued in its own iteration (issuing every task's loads up front measured
-  // 0.2-0.4 us slower). The q / k ring rows are written by one block per k head.
+  // 1. conv + silu. Two kinds of task, each one wave with all of its loads
+  // issued in its own iteration: a token's q and k heads (lane: channels 2l,
+  // 2l+1 of both, each head normed by its own wave sum as in
+  // conv_silu_qk_kernel), and this block's RB v channels for VTOK tokens at
+  // once (lane: one token and channel pair). T + ceil(T / VTOK) tasks, so a
+  // 4-token verify is one round of loads on 8 waves. The q / k ring rows are
+  // written by one block per k head.
   constexpr int W = FUSED_KC - 1;
+  constexpr int VPT = RB / 2;          // v channel pairs per token
+  constexpr int VTOK = 64 / VPT;       // tokens per v task
   const bool ring_qk = hv % (p.Hv / p.Hk) == 0 && b == 0;
-  for (int task = wave; task < 3 * T; task += NW) {
-    const int t = task / 3, part = task - 3 * (task / 3);
-    // q and k: the whole wave (128 channels); v: lanes < RB / 2 (RB channels)
-    const bool act = part < 2 || 2 * lane < RB;
-    const int cb = part == 0 ? hk * DK : part == 1 ? p.key_dim + hk * DK : 2 * p.key_dim + hv * DK + b * RB;
-    const int c0 = cb + (act ? 2 * lane : 0);
-    uint32_t win[FUSED_KC];
-#pragma unroll
-    for (int j = 0; j < FUSED_KC; ++j) {
-      const int r = t + j;
-      if (r < W) {
-        const long rr = wrap_add(rbase, r - W, p.R);
-        win[j] = *reinterpret_cast<const uint32_t*>(p.ring + rr * p.C + c0);
-      } else {
-        win[j] = *reinterpret_cast<const uint32_t*>(p.proj + (size_t)(r - W) * p.p_stride + c0);
-      }
-    }
-    const u32x4 taps = load16(p.cw + (size_t)c0 * FUSED_KC);
+  auto conv_pair = [&](const uint32_t (&win)[FUSED_KC], const u32x4 taps, float& s0, float& s1) {
     const float w0[4] = {bf16_lo(taps.x), bf16_hi(taps.x), bf16_lo(taps.y), bf16_hi(taps.y)};
     const float w1[4] = {bf16_lo(taps.z), bf16_hi(taps.z), bf16_lo(taps.w), bf16_hi(taps.w)};
     float acc0 = 0.0f, acc1 = 0.0f;
@@ -435,23 +423,69 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArg
       acc0 = fmaf(bf16_lo(win[j]), w0[j], acc0);
       acc1 = fmaf(bf16_hi(win[j]), w1[j], acc1);
     }
-    if (act && (part == 2 || ring_qk)) {
-      const long rr = wrap_add(rbase, t, p.R);
-      *reinterpret_cast<uint32_t*>(p.ring + rr * p.C + c0) = win[W];
-    }
-    float s0 = silu(acc0), s1 = silu(acc1);
-    if (part < 2) {
-      const float ss = wave_allsum(fmaf(s0, s0, s1 * s1));
-      const float inv = rsqrtf(ss / 128.0f + p.qk_eps);
-      const float sc = part == 0 ? p.q_scale : p.k_scale;
-      s0 = s0 * inv * sc;
-      s1 = s1 * inv * sc;
-    }
-    const uint32_t pk = pack_bf16x2(s0, s1);
-    if (act) {
-      float* dst = part == 0 ? qs[t] : part == 1 ? ks[t] : vs[t];
-      dst[2 * lane] = bf16_lo(pk);
-      dst[2 * lane + 1] = bf16_hi(pk);
+    s0 = silu(acc0);
+    s1 = silu(acc1);
+  };
+  const int n_vt = (T + VTOK - 1) / VTOK;
+  for (int task = wave; task < T + n_vt; task += NW) {
+    if (task < T) {                       // uniform over the wave
+      const int t = task;
+      const int cq = hk * DK + 2 * lane, ck = p.key_dim + hk * DK + 2 * lane;
+      uint32_t wq[FUSED_KC], wk[FUSED_KC];
+#pragma unroll
+      for (int j = 0; j < FUSED_KC; ++j) {
+        const int r = t + j;
+        if (r < W) {
+          const long rr = wrap_add(rbase, r - W, p.R);
+          wq[j] = *reinterpret_cast<const uint32_t*>(p.ring + rr * p.C + cq);
+          wk[j] = *reinterpret_cast<const uint32_t*>(p.ring + rr * p.C + ck);
+        } else {
+          wq[j] = *reinterpret_cast<const uint32_t*>(p.proj + (size_t)(r - W) * p.p_stride + cq);
+          wk[j] = *reinterpret_cast<const uint32_t*>(p.proj + (size_t)(r - W) * p.p_stride + ck);
+        }
+      }
+      const u32x4 tq = load16(p.cw + (size_t)cq * FUSED_KC);
+      const u32x4 tk = load16(p.cw + (size_t)ck * FUSED_KC);
+      if (ring_qk) {
+        const long rr = wrap_add(rbase, t, p.R);
+        *reinterpret_cast<uint32_t*>(p.ring + rr * p.C + cq) = wq[W];
+        *reinterpret_cast<uint32_t*>(p.ring + rr * p.C + ck) = wk[W];
+      }
+      float q0, q1, k0, k1;
+      conv_pair(wq, tq, q0, q1);
+      conv_pair(wk, tk, k0, k1);
+      const float iq = rsqrtf(wave_allsum(fmaf(q0, q0, q1 * q1)) / 128.0f + p.qk_eps);
+      const float ik = rsqrtf(wave_allsum(fmaf(k0, k0, k1 * k1)) / 128.0f + p.qk_eps);
+      const uint32_t pq = pack_bf16x2(q0 * iq * p.q_scale, q1 * iq * p.q_scale);
+      const uint32_t pk = pack_bf16x2(k0 * ik * p.k_scale, k1 * ik * p.k_scale);
+      qs[t][2 * lane] = bf16_lo(pq);
+      qs[t][2 * lane + 1] = bf16_hi(pq);
+      ks[t][2 * lane] = bf16_lo(pk);
+      ks[t][2 * lane + 1] = bf16_hi(pk);
+    } else {
+      const int t = (task - T) * VTOK + lane / VPT, cp = lane % VPT;
+      if (t < T) {
+        const int c0 = 2 * p.key_dim + hv * DK + b * RB + 2 * cp;
+        uint32_t win[FUSED_KC];
+#pragma unroll
+        for (int j = 0; j < FUSED_KC; ++j) {
+          const int r = t + j;
+          if (r < W) {
+            const long rr = wrap_add(rbase, r - W, p.R);
+            win[j] = *reinterpret_cast<const uint32_t*>(p.ring + rr * p.C + c0);
+          } else {
+            win[j] = *reinterpret_cast<const uint32_t*>(p.proj + (size_t)(r - W) * p.p_stride + c0);
+          }
+        }
+        const u32x4 taps = load16(p.cw + (size_t)c0 * FUSED_KC);
+        const long rr = wrap_add(rbase, t, p.R);
+        *reinterpret_cast<uint32_t*>(p.ring + rr * p.C + c0) = win[W];
+        float v0, v1;
+        conv_pair(win, taps, v0, v1);
+        const uint32_t pv = pack_bf16x2(v0, v1);
+        vs[t][2 * cp] = bf16_lo(pv);
+        vs[t][2 * cp + 1] = bf16_hi(pv);
+      }
     }
   }
   __syncthreads();
