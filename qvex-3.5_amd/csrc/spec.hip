@@ -363,6 +363,8 @@ __global__ __launch_bounds__(NT) void spec_filter_kernel(SpecArgs a) {
   const int n = P * K;                  // <= 16 * NT, checked by the host
   const float* L = a.fws + (long)row * P * (K + 1);
   const int t = threadIdx.x;
+  // candidate i = t + NT * q in slot q: four slots cover n <= 1024 (the
+  // 9B vocabulary's 31 parts x top-k 20), sixteen the rest; the list is the same
   float v[16];
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
@@ -370,7 +372,12 @@ __global__ __launch_bounds__(NT) void spec_filter_kernel(SpecArgs a) {
     const int pp = i / K;
     v[q] = i < n ? L[pp * (K + 1) + (i - pp * K)] : -__builtin_inff();
   }
-  block_topk(v, K, lst, wl);
+  if (n <= 4 * NT) {
+    const float v4[4] = {v[0], v[1], v[2], v[3]};
+    block_topk(v4, K, lst, wl);
+  } else {
+    block_topk(v, K, lst, wl);
+  }
   // Wave 0 holds the candidates c_i = lst[i] and e_i = exp(c_i - c_0) one per
   // lane; the ordered sums run over them with readlane, in index order.
   const int lane = t & 63;

@@ -51,6 +51,7 @@ CASES = [
     (16, 1, 8192, 0.9, 1, 1.0, 0.0, False, False),         # top-1
     (8, 3, 30000, 0.7, 20, 0.9, 0.8, False, True),         # draft logits (q unfiltered)
     (24, 0, 248320, 0.7, 20, 0.95, 0.3, True, False),      # plain sampling (k = 0)
+    (6, 3, 248320, 0.8, 64, 0.9, 0.0, True, False),        # 31 x 64 candidates: the 16-slot merge
 ]
 
 
