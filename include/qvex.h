@@ -435,6 +435,14 @@ int qvex_mark_seen(float* seen, int V, const int32_t* ids, int max_ids, const in
 int qvex_read_roof(const void* buf, uint64_t bytes, uint32_t* sink, int blocks,
                    void* stream);
 
+/* Dense bf16 copy of an MLX 4-bit group-64 weight: out[n, k] =
+ * bf16(s[n, k/64] * q[n, k] + b[n, k/64]) with the product and sum in fp32
+ * (one rounding). The long (prefill) calls of QLinear (engine/model.py:87-91
+ * with many rows, mx.quantized_matmul's prefill case) then run as a plain
+ * library GEMM on it. out [N, K] bf16, 16-byte aligned; K % 64 == 0. */
+int qvex_w4g64_dequant(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int N, int K,
+                       uint16_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

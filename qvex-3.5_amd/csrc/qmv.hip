@@ -466,7 +466,49 @@ int launch(const uint16_t* x, const uint32_t* w, const uint16_t* scales, const u
   return QVEX_OK;
 }
 
+// W[n, k] = bf16(s * q + b) in fp32 (one rounding), for the dense GEMM of long
+// (prefill) calls. One thread per uint32 word: eight codes of one group, one
+// 16-byte store.
+__global__ __launch_bounds__(256) void dequant_w4g64_kernel(const uint32_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ scales,
+                                                            const uint16_t* __restrict__ biases,
+                                                            uint16_t* __restrict__ out, long words, int K) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= words) return;
+  const int KW = K / 8;
+  const long n = i / KW;
+  const int kw = (int)(i - n * KW);
+  const int g = kw / 8;                       // 64 codes = 8 words per group
+  const float sc = bf16_to_f32(scales[n * (K / 64) + g]);
+  const float bi = bf16_to_f32(biases[n * (K / 64) + g]);
+  const uint32_t wd = w[i];
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float lo = fmaf(sc, (float)((wd >> (8 * j)) & 0xFu), bi);
+    const float hi = fmaf(sc, (float)((wd >> (8 * j + 4)) & 0xFu), bi);
+    o[j] = pack_bf16x2(lo, hi);
+  }
+  u32x4 v;
+  v.x = o[0]; v.y = o[1]; v.z = o[2]; v.w = o[3];
+  *reinterpret_cast<u32x4*>(out + i * 8) = v;
+}
+
 }  // namespace
+
+extern "C" int qvex_w4g64_dequant(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int N, int K,
+                                  uint16_t* out, void* stream) {
+  QVEX_CHECK_ARG(w && scales && biases && out, "qvex_w4g64_dequant: null pointer");
+  QVEX_CHECK_ARG(N >= 1 && K >= 64 && K % 64 == 0, "qvex_w4g64_dequant: N=%d K=%d (K a positive multiple of 64)", N,
+                 K);
+  QVEX_CHECK_ARG(qvex_aligned(out, 16) && qvex_aligned(w, 4), "qvex_w4g64_dequant: out must be 16-byte aligned");
+  const long words = (long)N * (K / 8);
+  QVEX_CHECK_ARG(words / 256 < 0x7fffffffL, "qvex_w4g64_dequant: too large");
+  hipLaunchKernelGGL(dequant_w4g64_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     w, scales, biases, out, words, K);
+  QVEX_CHECK_LAUNCH("qvex_w4g64_dequant");
+  return QVEX_OK;
+}
 
 extern "C" int qvex_qmv_w4g64(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
                               const uint16_t* biases, uint16_t* y, int M, int N, int K, void* stream) {

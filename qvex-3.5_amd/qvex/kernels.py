@@ -101,6 +101,24 @@ def pack_w4(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, swiglu:
     return packed
 
 
+def dequant_w4(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, out: torch.Tensor | None = None):
+    """bf16 [N, K] copy of an MLX 4-bit group-64 weight, bf16(s * q + b) computed
+    in fp32: the operand of the dense GEMM that long (prefill) calls use."""
+    _check(w, "w", torch.int32, 2)
+    _check(scales, "scales", torch.bfloat16, 2)
+    _check(biases, "biases", torch.bfloat16, 2)
+    N, K = w.shape[0], w.shape[1] * 8
+    if scales.shape != (N, K // 64) or biases.shape != (N, K // 64):
+        raise _C.QvexError(f"scales/biases must be [N, K/64] = ({N}, {K // 64})")
+    if out is None:
+        out = torch.empty((N, K), dtype=torch.bfloat16, device=w.device)
+    _check(out, "out", torch.bfloat16, 2)
+    if out.shape != (N, K):
+        raise _C.QvexError(f"out must be [N, K] = ({N}, {K})")
+    _C.call("qvex_w4g64_dequant", _ptr(w), _ptr(scales), _ptr(biases), N, K, _ptr(out), _stream())
+    return out
+
+
 def quantized_matmul_packed(x: torch.Tensor, packed: torch.Tensor, N: int, out: torch.Tensor | None = None,
                             tile: tuple[int, ...] | None = None, swiglu: bool = False) -> torch.Tensor:
     """y = x @ dequant(W)^T from pack_w4's copy, x bf16 [..., K] with 1..4 rows

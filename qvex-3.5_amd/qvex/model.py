@@ -126,6 +126,9 @@ class QLinear:
     MLX-layout kernel in chunks of 8 rows."""
 
     PACKED_MAX_ROWS = 4
+    # calls of at least this many rows (prefill) dequantize the weight to bf16
+    # and run a library GEMM; 0 disables it
+    DENSE_MIN_ROWS = 16
 
     def __init__(self, w, scales, biases, group_size=64, bits=4, pack: bool = True, swiglu: bool = False):
         if group_size != 64 or bits != 4:
@@ -182,6 +185,12 @@ class QLinear:
         o2 = out.view(M, self.N)
         if self.packed is not None and not self.swiglu_packed and M <= self.PACKED_MAX_ROWS:
             kernels.quantized_matmul_packed(x2, self.packed, self.N, out=o2)
+            return out.view(*lead, self.N)
+        if self.DENSE_MIN_ROWS and M >= self.DENSE_MIN_ROWS:
+            # long (prefill) call: the weight dequantized once to bf16, then a
+            # plain 2-D library GEMM (fp32 accumulation) instead of M / 8 GEMVs
+            wd = kernels.dequant_w4(self.w, self.scales, self.biases)
+            torch.mm(x2, wd.t(), out=o2)
             return out.view(*lead, self.N)
         for m0 in range(0, M, QMV_MAX_ROWS):
             m1 = min(M, m0 + QMV_MAX_ROWS)
@@ -492,6 +501,9 @@ class GatedDeltaNet:
     # one kernel (qvex_gdn_decode_fused, bitwise the three-kernel path)
     FUSED_MAX_T = 8
     fused_decode = True
+    # calls of at least this many tokens without snapshots (prefill) use the
+    # chunked recurrence (qvex_gdn_chunked); larger than any ring-snapshot width
+    CHUNKED_MIN_T = 64
     # with the norms folded (resid given, <= 4 rows) each head is split over this
     # many workgroups (qvex_gdn_decode_split) and the gated norm's scale moves
     # into the out_proj; 0 keeps one workgroup per head
@@ -529,8 +541,16 @@ class GatedDeltaNet:
                 _ptr(self.conv_w), self.K, _ptr(q), _ptr(k), _ptr(v), _ptr(a), _ptr(b), S, self.conv_dim,
                 self.key_dim, self.hv, ab_off, float(inv * inv), float(inv), 1e-6, _stream())
         snap = S <= cache.n_slots - 1
-        y = kernels.gated_delta_ring(q, k, v, a, b, self.A_log, self.dt_bias, cache.ssm_ring,
-                                     cache.counters.dev[cache.index:cache.index + 1], snap_every=snap)
+        if not snap and S >= self.CHUNKED_MIN_T and self.dk == 128 and self.dv == 128:
+            # long prefill chunk: the 64-token MFMA form, state read from the
+            # current slot and the final state written to slot (p + S) mod n
+            cur = cache.offset % cache.n_slots
+            nxt = (cache.offset + S) % cache.n_slots
+            y, _ = kernels.gated_delta_chunked(q, k, v, a, b, self.A_log, self.dt_bias, cache.ssm_ring[cur],
+                                               state_out=cache.ssm_ring[nxt])
+        else:
+            y = kernels.gated_delta_ring(q, k, v, a, b, self.A_log, self.dt_bias, cache.ssm_ring,
+                                         cache.counters.dev[cache.index:cache.index + 1], snap_every=snap)
         cache.offset += S
         cache.last_width = S if snap else 0
         z = proj[:, self.conv_dim:self.conv_dim + self.value_dim]
@@ -619,6 +639,9 @@ class Qwen35:
     # 1..4-row calls fold every residual RMSNorm into the neighbouring products
     # (QLinear.residual / NormedRows); False keeps the separate norm kernels
     fuse_norms = True
+    # prompt tokens per forward call of a prefill (engine/engine.py:232-248 runs
+    # 512-token chunks); the conv rings are sized for it
+    prefill_chunk = 512
 
     def __init__(self, cfg: Config, embed: QEmbedding, layers: list[Layer], norm, lm_head: QLinear,
                  max_context: int = 8192, max_width: int = 8):
@@ -637,7 +660,7 @@ class Qwen35:
             if l.linear:
                 caches.append(RecurrentCache(counters, i, conv_dim=l.mixer.conv_dim, kernel=l.mixer.K,
                                              hv=l.mixer.hv, dv=l.mixer.dv, dk=l.mixer.dk,
-                                             max_width=width, device=dev))
+                                             max_width=width, device=dev, prefill_width=self.prefill_chunk))
             else:
                 caches.append(KVCache(counters, i, n_kv=cfg.num_key_value_heads, head_dim=cfg.head_dim,
                                       capacity=cap, device=dev))

@@ -157,3 +157,49 @@ def test_mfma_model_shapes(M, shape):
     rows = np.unique(np.concatenate([np.arange(32), np.arange(N - 32, N),
                                      np.random.default_rng(N).choice(N, 1024, replace=False)]))
     check(x, w, s, b, y, rows=rows)
+
+
+# ---------------------------------------------------------------- dense (prefill) path
+
+def _dequant_np(w, s, b):
+    """bf16(s * q + b) with the product and sum in fp32 (one rounding), in numpy."""
+    N, KW = w.shape
+    K = KW * 8
+    q = np.stack([(w >> (4 * j)) & 0xF for j in range(8)], axis=-1).reshape(N, K).astype(np.float32)
+    sc = np.repeat(synth.bf16_to_f32(s), 64, axis=1).astype(np.float32)
+    bi = np.repeat(synth.bf16_to_f32(b), 64, axis=1).astype(np.float32)
+    prod = (sc.astype(np.float64) * q + bi).astype(np.float32)   # fma: exact product, one rounding
+    return synth.bf16_bits(prod)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K", [(256, 512), (12352, 4096), (64, 12288)])
+def test_dequant_bit_exact(N, K):
+    w, s, b = synth.qmv_weights(N, K, seed=5, tag=N)
+    out = kernels.dequant_w4(to_dev(w, torch.int32), to_dev(s, torch.bfloat16), to_dev(b, torch.bfloat16))
+    torch.cuda.synchronize()
+    got = out.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, _dequant_np(w, s, b))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [16, 100, 512])
+def test_dense_prefill_product(M):
+    """QLinear with M >= DENSE_MIN_ROWS: bf16(x W~^T) with W~ the bf16 dequantized
+    weight and fp32 accumulation: within bf16 output rounding plus 2^-8 of
+    sum |x||w| (weight rounding, accumulation) of the exact affine product."""
+    from qvex.model import QLinear
+    N, K = 1024, 4096
+    w, s, b = synth.qmv_weights(N, K, seed=6, tag=M)
+    lin = QLinear(to_dev(w, torch.int32), to_dev(s, torch.bfloat16), to_dev(b, torch.bfloat16))
+    assert M >= QLinear.DENSE_MIN_ROWS
+    x = synth.qmv_x(M, K, seed=6, tag=M)
+    y = lin(to_dev(x, torch.bfloat16))
+    torch.cuda.synchronize()
+    xf = synth.bf16_to_f32(x).astype(np.float64)
+    q = np.stack([(w >> (4 * j)) & 0xF for j in range(8)], axis=-1).reshape(N, K).astype(np.float64)
+    W = q * np.repeat(synth.bf16_to_f32(s), 64, axis=1) + np.repeat(synth.bf16_to_f32(b), 64, axis=1)
+    ref = xf @ W.T
+    bound = 2.0 ** -8 * np.abs(ref) + 2.0 ** -8 * (np.abs(xf) @ np.abs(W).T)
+    err = np.abs(y.float().cpu().numpy().astype(np.float64) - ref)
+    assert (err <= bound).all(), float((err - bound).max())
