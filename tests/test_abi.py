@@ -187,3 +187,14 @@ def test_resid_norm_products_argument_rules():
         _C.call("qvex_qmv_w4g64_packed_rstd", p, p, p, 1, 16, 256, p, 320, 5120, 1e-6, 0, None)
     with pytest.raises(_C.QvexError, match="16-byte"):
         _C.call("qvex_qmv_w4g64_packed_rstd", p, p, p, 1, 16, 256, p + 4, 256, 4096, 1e-6, 0, None)
+
+
+def test_dequant_argument_rules():
+    buf = ctypes.create_string_buffer(1 << 12)
+    p = (ctypes.addressof(buf) + 15) // 16 * 16
+    with pytest.raises(_C.QvexError, match="multiple of 64"):
+        _C.call("qvex_w4g64_dequant", p, p, p, 4, 96, p, None)
+    with pytest.raises(_C.QvexError, match="null pointer"):
+        _C.call("qvex_w4g64_dequant", p, None, p, 4, 64, p, None)
+    with pytest.raises(_C.QvexError, match="16-byte"):
+        _C.call("qvex_w4g64_dequant", p, p, p, 4, 64, p + 2, None)
