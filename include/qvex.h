@@ -92,9 +92,10 @@ int qvex_qmv_w4g64_packed(const uint16_t* x, const void* packed, uint16_t* y, in
 /* SwiGLU variant for the fused gate/up projection of the MLP (gate rows
  * [0, N/2), up rows [N/2, N), engine/model.py:294-302): pack with the gate/up
  * interleave (each 16-row tile holds 8 gate rows and their 8 up rows), then
- * y[M, N/2] = bf16(silu(g) * u) with g, u the bf16-rounded products, i.e. the
- * same bits as qvex_qmv_w4g64_packed followed by qvex_swiglu (_swiglu,
- * engine/model.py:134-135). N % 16 == 0. */
+ * y[M, N/2] = bf16(silu(g) * u) with g, u the bf16-rounded products, i.e.
+ * qvex_qmv_w4g64_packed followed by qvex_swiglu (_swiglu,
+ * engine/model.py:134-135) up to the order of the per-set fp32 sums (a row
+ * sits in another block of the interleaved pack). N % 16 == 0. */
 int qvex_w4g64_pack_swiglu(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                            int N, int K, void* packed, uint64_t packed_bytes, void* stream);
 int qvex_qmv_w4g64_packed_swiglu(const uint16_t* x, const void* packed, uint16_t* y, int M,

@@ -317,31 +317,35 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
     }
   };
 
+  // this wave's sets ws, ws + WS, ... taken from a block-dependent start, so
+  // the blocks' first activation loads spread over every slice of x instead of
+  // all hitting the same few lines (fixed per tile, so rows stay M-independent;
+  // every load pipeline uses the same order)
+  const int nws = ws < GS ? (GS - ws + WS - 1) / WS : 0;
+  const int rot = nws > 1 ? (int)(blockIdx.x % (unsigned)nws) : 0;
+  auto set_of = [&](int j) { const int jj = j + rot; return ws + (jj >= nws ? jj - nws : jj) * WS; };
   if constexpr (NP == 0) {
-    int gs = ws;
-    if (gs < GS) issue(0, gs);
-    if (gs < GS && gs + WS < GS) issue(1, gs + WS);
+    if (nws > 0) issue(0, set_of(0));
+    if (nws > 1) issue(1, set_of(1));
     seg_table();
     if (rs && ws == 0) compute_rstd();
-    while (gs < GS) {
-      const int g1 = gs + WS;
-      if (g1 < GS && gs != ws) issue(1, g1);
+    int j = 0;
+    while (j < nws) {
+      if (j + 1 < nws && j != 0) issue(1, set_of(j + 1));
       compute(0);
-      if (g1 >= GS) break;
-      const int g2 = g1 + WS;
-      if (g2 < GS) issue(0, g2);
+      if (j + 1 >= nws) break;
+      if (j + 2 < nws) issue(0, set_of(j + 2));
       compute(1);
-      gs = g2;
+      j += 2;
     }
   } else {
-    // the host guarantees ceil(GS / WS) <= NP
 #pragma unroll
-    for (int j = 0; j < NP; ++j) issue(j, min(ws + j * WS, GS - 1));
+    for (int j = 0; j < NP; ++j) issue(j, j < nws ? set_of(j) : GS - 1);
     seg_table();
     if (rs && ws == 0) compute_rstd();
 #pragma unroll
     for (int j = 0; j < NP; ++j)
-      if (ws + j * WS < GS) compute(j);
+      if (j < nws) compute(j);
   }
 
   // lane (c, i16) holds group slot c of row i16: sum the 4 slots

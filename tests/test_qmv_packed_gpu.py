@@ -82,8 +82,11 @@ def test_packed_matches_mlx_layout_kernel_closely():
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
 @pytest.mark.parametrize("N,K", [(24576, 4096), (48, 512), (4096, 256)])
 def test_packed_swiglu_equals_product_then_swiglu(M, N, K):
-    """The fused SwiGLU epilogue gives the same bits as the packed product followed by
-    qvex_swiglu (_swiglu of engine/model.py:134-135 on the two bf16 halves)."""
+    """The fused SwiGLU epilogue matches the packed product followed by qvex_swiglu
+    (_swiglu of engine/model.py:134-135 on the two bf16 halves). A row sits in a
+    different block in the interleaved pack, so the per-set accumulation order,
+    and with it the rounding of g and u, may differ: within two bf16 steps (a
+    wrong interleave is off by far more)."""
     from qvex import _C
     from qvex.kernels import _ptr, _stream
     w, s, b = synth.qmv_weights(N, K, seed=35, tag=N)
@@ -94,7 +97,8 @@ def test_packed_swiglu_equals_product_then_swiglu(M, N, K):
     _C.call("qvex_swiglu", _ptr(gu), _ptr(ref), M, N // 2, _stream())
     got = kernels.quantized_matmul_packed(x, kernels.pack_w4(wd, sd, bd, swiglu=True), N, swiglu=True)
     torch.cuda.synchronize()
-    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    d = (got.float() - ref.float()).abs()
+    assert bool((d <= 2.0 ** -6 * ref.float().abs() + 2.0 ** -10).all()), float(d.max())
 
 
 def default_tile(N, K):
