@@ -167,7 +167,8 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
                                                                    PkEpi e) {
   constexpr int NWAVE = pk_block(WS) / 64;
   constexpr int RG = NWAVE / WS;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wave index is uniform: in an SGPR, the tile / set / record arithmetic is scalar
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rg = wave / WS, ws = wave % WS;
   const int GS = K / PK_SET;
   const int tiles = (N + PK_TILE - 1) / PK_TILE;
@@ -176,12 +177,17 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
   const bool part = (i16 >> 2) == c && am < M;   // A row i16 = (group slot i16/4, activation row i16%4)
   const int tile0 = (blockIdx.x * RG + rg) * TN;
 
-  __shared__ u32x4 xslot[NWAVE][4 * 32];         // per wave: [activation row][32 chunks of 8 bf16]
+  // per wave: [activation row][32 chunks of 8 bf16], then 8 zero chunks that the
+  // lanes outside the block diagonal read in place of x (no predicated reads)
+  __shared__ u32x4 xslot[NWAVE][4 * 32 + 8];
   u32x4* slot = xslot[wave];
+  if (lane < 8) slot[4 * 32 + lane] = u32x4{0u, 0u, 0u, 0u};
+  const u32x4* arow = part ? slot + am * 32 + c * 8 : slot + 4 * 32;
 
   const uint32_t magic = opaque_vgpr(kMagic);
   const uint32_t nib = opaque_sgpr(kNib);
-  const bf16x8_t ones = as_bf16x8(kOnes, kOnes, kOnes, kOnes);
+  // four distinct registers (the compiler would otherwise keep one and copy it per step)
+  const bf16x8_t ones = as_bf16x8(opaque_vgpr(kOnes), opaque_vgpr(kOnes), opaque_vgpr(kOnes), opaque_vgpr(kOnes));
 
   float acc[TN][4];
 #pragma unroll
@@ -265,10 +271,12 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
       wb[buf][t][1] = load_nt16(rec + 1024 + lane * 16);
       sb[buf][t] = *reinterpret_cast<const uint32_t*>(rec + PK_WBYTES + lane * 4);
     }
+    // rows m >= M re-read row M - 1: only the block-diagonal lanes of rows < M
+    // ever read the slot, so no zero fill (and no predicated load) is needed
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      const int m = 2 * q + xm0;
-      xr[buf][q] = m < M ? load16(x + (size_t)m * K + (size_t)gs * PK_SET + 8 * xch) : u32x4{0u, 0u, 0u, 0u};
+      const int m = min(2 * q + xm0, M - 1);
+      xr[buf][q] = load16(x + (size_t)m * K + (size_t)gs * PK_SET + 8 * xch);
     }
     sgs[buf] = gs;
   };
@@ -281,8 +289,7 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
     for (int t = 0; t < TN; ++t) C[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const u32x4 xa = part ? slot[am * 32 + c * 8 + s] : u32x4{0u, 0u, 0u, 0u};
-      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, xa);
+      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, arow[s]);
       CX = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, CX, 0, 0, 0);
 #pragma unroll
       for (int t = 0; t < TN; ++t) {
