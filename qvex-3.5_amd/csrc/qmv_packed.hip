@@ -87,6 +87,15 @@ __global__ __launch_bounds__(64) void pack_kernel(const uint32_t* __restrict__ w
   *reinterpret_cast<uint32_t*>(rec + PK_WBYTES + L * 4) = sb;
 }
 
+// A 64-bit right shift as one v_lshrrev_b64 (the compiler would split it into
+// v_alignbit_b32 + v_lshrrev_b32 when both halves are used separately).
+template <int SH>
+__device__ __forceinline__ uint64_t shr64(uint64_t v) {
+  uint64_t r;
+  asm("v_lshrrev_b64 %0, %1, %2" : "=v"(r) : "i"(SH), "v"(v));
+  return r;
+}
+
 // Max / min over the 16 lanes of a DPP row, the same in all 16 lanes.
 __device__ __forceinline__ float row16_allmax(float v) {
   v = fmaxf(v, dpp_row<0xB1>(v));
@@ -288,16 +297,26 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
 #pragma unroll
     for (int t = 0; t < TN; ++t) C[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, arow[s]);
-      CX = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, CX, 0, 0, 0);
+    for (int s = 0; s < 8; s += 2) {
+      // steps s and s + 1 use adjacent words of a tile: one 64-bit shift moves
+      // both (the bits a word takes from its neighbour fall outside the mask)
+      bf16x8_t b[TN][2];
 #pragma unroll
       for (int t = 0; t < TN; ++t) {
         const u32x4 wv = wb[buf][t][s / 4];
-        const uint32_t wd = (s % 4 == 0) ? wv.x : (s % 4 == 1) ? wv.y : (s % 4 == 2) ? wv.z : wv.w;
-        const bf16x8_t b = as_bf16x8(and_or(wd, nib, magic), and_or(wd >> 4, nib, magic),
-                                     and_or(wd >> 8, nib, magic), and_or(wd >> 12, nib, magic));
-        C[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, C[t], 0, 0, 0);
+        const uint64_t pr = (s % 4 == 0) ? ((uint64_t)wv.y << 32 | wv.x) : ((uint64_t)wv.w << 32 | wv.z);
+        const uint64_t p4 = shr64<4>(pr), p8 = shr64<8>(pr), p12 = shr64<12>(pr);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          b[t][h] = as_bf16x8(and_or((uint32_t)(pr >> (32 * h)), nib, magic), and_or((uint32_t)(p4 >> (32 * h)), nib, magic),
+                              and_or((uint32_t)(p8 >> (32 * h)), nib, magic), and_or((uint32_t)(p12 >> (32 * h)), nib, magic));
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, arow[s + h]);
+        CX = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, CX, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < TN; ++t) C[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[t][h], C[t], 0, 0, 0);
       }
     }
     if constexpr (seg) {
