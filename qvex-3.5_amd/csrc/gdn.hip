@@ -383,25 +383,27 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArg
     st[4] = __uint_as_float(s1.x); st[5] = __uint_as_float(s1.y);
     st[6] = __uint_as_float(s1.z); st[7] = __uint_as_float(s1.w);
   }
+  // the token's decay and beta inputs (threads t < T), converted after the conv
+  // tasks so that no wave waits on them before issuing its conv loads
+  float a_log = 0.0f;
+  uint32_t dt_raw = 0, aa_raw = 0, bb_raw = 0;
   if (threadIdx.x < T) {
     const int t = threadIdx.x;
-    const float A = expf(p.A_log[hv]);
-    const float dt = bf16_to_f32(p.dt_bias[hv]);
-    const float aa = bf16_to_f32(p.proj[(size_t)t * p.p_stride + p.ab_off + p.Hv + hv]);
-    const float bb = bf16_to_f32(p.proj[(size_t)t * p.p_stride + p.ab_off + hv]);
-    const float x = aa + dt;
-    const float sp = x > 20.0f ? x : log1pf(expf(x));
-    gb_s[0][t] = expf(-A * sp);
-    gb_s[1][t] = 1.0f / (1.0f + expf(-bb));
+    a_log = p.A_log[hv];
+    dt_raw = p.dt_bias[hv];
+    aa_raw = p.proj[(size_t)t * p.p_stride + p.ab_off + p.Hv + hv];
+    bb_raw = p.proj[(size_t)t * p.p_stride + p.ab_off + hv];
   }
-  // this row's z for every token and its norm weight (the row's lane 0 uses them)
-  float zr[FUSED_TMAX];
-  float wr = 0.0f;
+  // this row's z for every token and its norm weight (the row's lane 0 uses
+  // them), loaded unconditionally (rows past T re-read row T - 1) into one
+  // register each, so the loads go out together and are first waited for in
+  // the recurrence
+  uint32_t zr[FUSED_TMAX];
+  uint32_t wr_raw = 0;
   if (l16 == 0) {
-    wr = bf16_to_f32(p.norm_w[dv]);
+    wr_raw = p.norm_w[dv];
 #pragma unroll
-    for (int t = 0; t < FUSED_TMAX; ++t)
-      zr[t] = t < T ? bf16_to_f32(p.proj[(size_t)t * p.p_stride + p.z_off + hv * DK + dv]) : 0.0f;
+    for (int t = 0; t < FUSED_TMAX; ++t) zr[t] = p.proj[(size_t)min(t, T - 1) * p.p_stride + p.z_off + hv * DK + dv];
   }
   // 1. conv + silu. Two kinds of task, each one wave with all of its loads
   // issued in its own iteration: a token's q and k heads (lane: channels 2l,
@@ -488,6 +490,17 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArg
       }
     }
   }
+  if (threadIdx.x < T) {
+    const int t = threadIdx.x;
+    // empty asm: keeps the compiler from hoisting these conversions (and the
+    // wait for their loads) back above the conv tasks
+    asm volatile("" : "+v"(a_log), "+v"(dt_raw), "+v"(aa_raw), "+v"(bb_raw));
+    const float A = expf(a_log);
+    const float x = bf16_to_f32((uint16_t)aa_raw) + bf16_to_f32((uint16_t)dt_raw);
+    const float sp = x > 20.0f ? x : log1pf(expf(x));
+    gb_s[0][t] = expf(-A * sp);
+    gb_s[1][t] = 1.0f / (1.0f + expf(-bf16_to_f32((uint16_t)bb_raw)));
+  }
   __syncthreads();
 
   // 2. recurrence; u of this block's rows to `out`, y to LDS for the sums
@@ -518,10 +531,12 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArg
     if (l16 == 0) {
       const float y = bf16_to_f32(f32_to_bf16(o));
       ys[t][grp] = y;
-      float zt = zr[0];
+      uint32_t zb = zr[0];
 #pragma unroll
-      for (int i = 1; i < FUSED_TMAX; ++i) zt = t == i ? zr[i] : zt;
-      p.out[(size_t)t * p.Hv * DK + hv * DK + dv] = f32_to_bf16(silu(zt) * (wr * y));
+      for (int i = 1; i < FUSED_TMAX; ++i) zb = t == i ? zr[i] : zb;
+      asm volatile("" : "+v"(zb), "+v"(wr_raw));
+      const float zt = bf16_to_f32((uint16_t)zb);
+      p.out[(size_t)t * p.Hv * DK + hv * DK + dv] = f32_to_bf16(silu(zt) * (bf16_to_f32((uint16_t)wr_raw) * y));
     }
     if (p.snap_every || t == T - 1) {
       float* dstp = p.state + wrap_add(cur, (1 + t) % p.n_slots, p.n_slots) * slot_stride + row_off;
