@@ -22,6 +22,9 @@ from .model import (Attention, KVCache, Layer, MLP, NormedRows, QLinear, Qwen35,
 
 
 class MTPHead:
+    # the first norm of the block from the fc product's epilogue (False: its own launch)
+    fc_epilogue = True
+
     def __init__(self, model: Qwen35, w: dict, group_size: int = 64, bits: int = 4, hidden_mode: str = "pre"):
         cfg = model.cfg
         self.model = model
@@ -36,6 +39,11 @@ class MTPHead:
         layer.mixer = Attention(cfg, w["attn"])
         layer.mlp = MLP(w["mlp"])
         self.layer = layer
+        # zero residual for the fc product, whose epilogue then leaves the block
+        # input x = bf16(0 + fc(.)) and the first norm's inputs (allocated here,
+        # never inside a graph capture)
+        self._zero = torch.zeros((QLinear.PACKED_MAX_ROWS, cfg.hidden_size), dtype=torch.bfloat16,
+                                 device=model.norm.device)
 
     def make_cache(self, max_context: int | None = None) -> KVCache:
         cfg = self.model.cfg
@@ -64,11 +72,17 @@ class MTPHead:
         # [rms(embed) | rms(hidden)] in one launch
         _C.call("qvex_rmsnorm_pair", _ptr(e), e.stride(0), _ptr(self.norm_emb), _ptr(x_in), _ptr(h), h.stride(0),
                 _ptr(self.norm_hid), _ptr(x_in) + 2 * H, x_in.stride(0), T, H, float(self.eps), _stream())
-        x = self.fc(x_in)
         V = self.model.cfg.vocab_size
         if self.model.fuse_norms and T <= QLinear.PACKED_MAX_ROWS and NormedRows.supported(H):
-            # the block's residual norms ride on its products (Layer.fused)
-            out, st = self.layer.fused(x, NormedRows.of(x, self.layer.ln1, self.eps), cache, False, self.norm_out)
+            # the block's residual norms ride on its products (Layer.fused); the
+            # first one on the fc product, as a residual add onto zero
+            if self.fc_epilogue:
+                x, n1 = self.fc.residual(x_in, self._zero[:T], self.layer.ln1, self.eps)
+            else:
+                x, n1 = self.fc(x_in), None
+            if not isinstance(n1, NormedRows):
+                n1 = NormedRows.of(x, self.layer.ln1, self.eps)
+            out, st = self.layer.fused(x, n1, cache, False, self.norm_out)
             if select is not None:
                 o_sel = torch.empty((1, H), dtype=torch.bfloat16, device=h.device)
                 _C.call("qvex_gather_row", _ptr(out), H, _ptr(select), T, _ptr(o_sel), H, _stream())
@@ -86,6 +100,7 @@ class MTPHead:
                 from .speculative import _argmax
                 _argmax(logits[0, -1], out=argmax_out)
             return (logits, out.view(1, T, H)) if return_hidden else logits
+        x = self.fc(x_in)
         n = rms_norm(x, self.layer.ln1, self.eps)
         hh, m = self.layer(x, cache, normed=n)
         out, n_out = add_rms_norm(hh, m, self.norm_out, self.eps)
