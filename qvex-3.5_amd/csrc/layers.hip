@@ -314,7 +314,6 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
     float* __restrict__ ws) {
   constexpr int KS = D / 32;     // MFMA steps over head dims
   constexpr int NT = D / 16;     // 16-dim output tiles of O
-  constexpr int OS = D + 4;      // padded LDS row of the merge buffer
   const int kh = blockIdx.x, tile = blockIdx.y, split = blockIdx.z;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int li = lane & 15, lg = lane >> 4;
@@ -356,9 +355,9 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
   if (k_lo >= k_hi) return;      // split past the visible keys: the combine never reads it
 
   __shared__ uint32_t ps[4][16][17];     // per-wave P tile, bf16 pairs [row][key pair], padded
-  __shared__ float ob[4][16][OS];        // per-wave O for the merge
+  __shared__ float4 obv[4][NT][4][16];   // per-wave O for the merge: [wave][dim tile][row group][dim] x 4 rows
   __shared__ float ml[4][16][2];         // per-wave (m, l)
-  __shared__ float fac[4][16];           // merge factors e^{m_w - m}
+  __shared__ __align__(16) float fac[4][16];   // merge factors e^{m_w - m}
 
   // the 4 rows this lane owns in accumulator layout: r = 4*lg + j
   int rlim[4];
@@ -438,14 +437,15 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
     for (int t = 0; t < NT; ++t) o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_att8(pa), as_att8(vr[t]), o[t], 0, 0, 0);
   }
 
-  // merge the 4 waves: m = max_w m_w, l = sum_w l_w e^{m_w-m}, O = sum_w O_w e^{m_w-m} (fixed order w = 0..3)
+  // merge the 4 waves: m = max_w m_w, l = sum_w l_w e^{m_w-m}, O = sum_w O_w e^{m_w-m} (fixed order w = 0..3).
+  // A lane's 4 rows of a dim go to LDS as one float4 (16 b128 writes per lane)
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r = 4 * lg + j;
     if (li == 0) { ml[w][r][0] = m_r[j]; ml[w][r][1] = l_r[j]; }
-#pragma unroll
-    for (int t = 0; t < NT; ++t) ob[w][r][t * 16 + li] = o[t][j];
   }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) obv[w][t][lg][li] = make_float4(o[t][0], o[t][1], o[t][2], o[t][3]);
   __syncthreads();
   float* wsb = ws + (((size_t)kh * gridDim.y + tile) * gridDim.z + split) * 16 * (D + 2);
   if (threadIdx.x < 16) {
@@ -462,11 +462,24 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
     wsb[2 * r + 1] = l;
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < 16 * D; e += 256) {
-    const int r = e / D, d = e % D;
-    const float acc = ((ob[0][r][d] * fac[0][r] + ob[1][r][d] * fac[1][r]) + ob[2][r][d] * fac[2][r]) +
-                      ob[3][r][d] * fac[3][r];
-    wsb[32 + (size_t)r * D + d] = acc;
+  // thread (row group rg, dim d): rows 4 rg .. 4 rg + 3 of dim d, one b128 read per wave
+  for (int e = threadIdx.x; e < 4 * D; e += 256) {
+    const int rg = e / D, d = e % D, t = d >> 4, dl = d & 15;
+    float4 ov[4], fv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      ov[v] = obv[v][t][rg][dl];
+      fv[v] = *reinterpret_cast<const float4*>(&fac[v][4 * rg]);
+    }
+    const float a0 = ((ov[0].x * fv[0].x + ov[1].x * fv[1].x) + ov[2].x * fv[2].x) + ov[3].x * fv[3].x;
+    const float a1 = ((ov[0].y * fv[0].y + ov[1].y * fv[1].y) + ov[2].y * fv[2].y) + ov[3].y * fv[3].y;
+    const float a2 = ((ov[0].z * fv[0].z + ov[1].z * fv[1].z) + ov[2].z * fv[2].z) + ov[3].z * fv[3].z;
+    const float a3 = ((ov[0].w * fv[0].w + ov[1].w * fv[1].w) + ov[2].w * fv[2].w) + ov[3].w * fv[3].w;
+    float* op = wsb + 32 + (size_t)(4 * rg) * D + d;
+    op[0] = a0;
+    op[D] = a1;
+    op[2 * D] = a2;
+    op[3 * D] = a3;
   }
 }
 
