@@ -485,24 +485,25 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
 
 // out[lq, (kh*GQ + g)*D + d] = bf16(sigmoid(gate) * sum_s o_s e^{m_s-m} / sum_s l_s e^{m_s-m})
 // over the splits that hold visible keys (the count follows from the device position).
-// One 256-thread block per (kv head, tile, row): NG groups of D/4 threads, thread
-// (g, j) owns dims 4j..4j+3 of splits g, g + NG, ... The gate and the first
-// CB splits of each thread (m, l and its 4 values) are requested before the
-// position is read; splits past the active count are dropped by selects (the
-// workspace may hold anything there). Each thread merges its splits against its
-// own maximum, the groups then merge in LDS in a fixed order. A split whose keys
-// are all invisible to the row (m = -inf) adds nothing, so a row's bits do not
-// depend on the other rows of the call.
-template <int D>
+// One 256-thread block per (kv head, tile, row, slice of D / DS dims): NG groups of
+// D / (4 DS) threads, thread (g, j) owns dims 4j..4j+3 of the slice for splits g,
+// g + NG, ... The gate and the first CB splits of each thread (m, l and its 4
+// values) are requested before the position is read; splits past the active count
+// are dropped by selects (the workspace may hold anything there). Each thread
+// merges its splits against its own maximum, the groups then merge in LDS in a
+// fixed order. A split whose keys are all invisible to the row (m = -inf) adds
+// nothing, so a row's bits do not depend on the other rows of the call.
+template <int D, int DS>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ ws, int nsplit, int ntile,
                                                            int keys_per_split, const int32_t* __restrict__ pos0,
                                                            int L, int Hq, int Hkv, int QT,
                                                            const uint16_t* __restrict__ gate, long g_stride,
                                                            uint16_t* __restrict__ out) {
-  constexpr int TPG = D / 4;            // threads per split group
+  constexpr int DSL = D / DS;           // dims per block
+  constexpr int TPG = DSL / 4;          // threads per split group
   constexpr int NG = 256 / TPG;         // split groups
   constexpr int CB = 8;                 // splits per thread per batch
-  const int kh = blockIdx.x, tile = blockIdx.y, r = blockIdx.z;
+  const int kh = blockIdx.x, tile = blockIdx.y, r = blockIdx.z / DS, ds = blockIdx.z % DS;
   const int GQ = Hq / Hkv;
   if (r >= GQ * QT) return;
   const int g = r / QT, lq = tile * QT + r % QT;
@@ -512,10 +513,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   const float* base = ws + ((size_t)kh * ntile + tile) * nsplit * rec;
   const int tid = threadIdx.x;
   const int grp = tid / TPG, j = tid % TPG;
+  const int d0 = ds * DSL;
   __shared__ float gm[NG], gl[NG];
-  __shared__ __align__(16) float part[NG][D];
+  __shared__ __align__(16) float part[NG][DSL];
 
-  const float gt = tid < D ? bf16_to_f32(gate[(size_t)lq * g_stride + (size_t)h * 2 * D + D + tid]) : 0.0f;
+  const float gt = tid < DSL ? bf16_to_f32(gate[(size_t)lq * g_stride + (size_t)h * 2 * D + D + d0 + tid]) : 0.0f;
   float ms[CB], ls[CB];
   float4 os[CB];
   auto load_batch = [&](int s0, int lim) {
@@ -526,7 +528,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
       const float* rp = base + (size_t)(ok ? s : 0) * rec;
       ms[i] = ok ? rp[2 * r] : -INFINITY;
       ls[i] = ok ? rp[2 * r + 1] : 0.0f;
-      os[i] = ok ? *reinterpret_cast<const float4*>(rp + 32 + (size_t)r * D + 4 * j) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+      os[i] = ok ? *reinterpret_cast<const float4*>(rp + 32 + (size_t)r * D + d0 + 4 * j)
+                 : float4{0.0f, 0.0f, 0.0f, 0.0f};
     }
   };
   load_batch(0, nsplit);
@@ -563,7 +566,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   if (j == 0) { gm[grp] = m; gl[grp] = l; }
   *reinterpret_cast<float4*>(&part[grp][4 * j]) = o;
   __syncthreads();
-  if (tid < D) {
+  if (tid < DSL) {
     float mx = gm[0];
 #pragma unroll
     for (int q = 1; q < NG; ++q) mx = fmaxf(mx, gm[q]);
@@ -575,7 +578,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
       lt = fmaf(gl[q], f, lt);
     }
     const float invl = lt > 0.0f ? 1.0f / lt : 0.0f;
-    out[(size_t)lq * Hq * D + (size_t)h * D + tid] = f32_to_bf16(acc * invl * sigmoidf_(gt));
+    out[(size_t)lq * Hq * D + (size_t)h * D + d0 + tid] = f32_to_bf16(acc * invl * sigmoidf_(gt));
   }
 }
 
@@ -719,6 +722,7 @@ extern "C" int qvex_attn_qk_rope(const uint16_t* proj, long p_stride, const uint
 
 namespace {
 constexpr int ATT_ROWS = 16;
+constexpr int ATT_DSPLIT = 4;   // combine blocks per row, each over D / 4 dims (4 x the blocks in flight)
 }
 
 extern "C" uint64_t qvex_attn_workspace_bytes(int L, int Hq, int Hkv, int D, int max_keys, int keys_per_split) {
@@ -756,14 +760,14 @@ extern "C" int qvex_attention(const uint16_t* q, const uint16_t* k_cache, const 
     hipLaunchKernelGGL((attn_mfma_partial_kernel<256>), pgrid, dim3(256), 0, st, q, k_cache, v_cache, pos0, L, Hq,
                        Hkv, cap, QT, keys_per_split, scale, (float*)workspace);
     QVEX_CHECK_LAUNCH("qvex_attention/partial");
-    hipLaunchKernelGGL((attn_combine_kernel<256>), dim3(Hkv, ntile, ATT_ROWS), dim3(256), 0, st,
+    hipLaunchKernelGGL((attn_combine_kernel<256, ATT_DSPLIT>), dim3(Hkv, ntile, ATT_ROWS * ATT_DSPLIT), dim3(256), 0, st,
                        (const float*)workspace, nsplit, ntile, keys_per_split, pos0, L, Hq, Hkv, QT, gate,
                        gate_stride, out);
   } else {
     hipLaunchKernelGGL((attn_mfma_partial_kernel<128>), pgrid, dim3(256), 0, st, q, k_cache, v_cache, pos0, L, Hq,
                        Hkv, cap, QT, keys_per_split, scale, (float*)workspace);
     QVEX_CHECK_LAUNCH("qvex_attention/partial");
-    hipLaunchKernelGGL((attn_combine_kernel<128>), dim3(Hkv, ntile, ATT_ROWS), dim3(256), 0, st,
+    hipLaunchKernelGGL((attn_combine_kernel<128, ATT_DSPLIT>), dim3(Hkv, ntile, ATT_ROWS * ATT_DSPLIT), dim3(256), 0, st,
                        (const float*)workspace, nsplit, ntile, keys_per_split, pos0, L, Hq, Hkv, QT, gate,
                        gate_stride, out);
   }
