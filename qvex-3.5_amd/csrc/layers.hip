@@ -354,7 +354,7 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
   const int k_hi = min(k_lo + keys_per_split, kend_tile);
   if (k_lo >= k_hi) return;      // split past the visible keys: the combine never reads it
 
-  __shared__ uint32_t ps[4][16][17];     // per-wave P tile, bf16 pairs [row][key pair], padded
+  __shared__ __align__(16) uint32_t ps[4][16][20];   // per-wave P tile, bf16 pairs [row][key pair], 80-byte rows
   __shared__ float4 obv[4][NT][4][16];   // per-wave O for the merge: [wave][dim tile][row group][dim] x 4 rows
   __shared__ float ml[4][16][2];         // per-wave (m, l)
   __shared__ __align__(16) float fac[4][16];   // merge factors e^{m_w - m}
@@ -414,24 +414,17 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
 #pragma unroll
       for (int t = 0; t < NT; ++t) o[t][j] *= corr;
     }
-    // P to the A layout through this wave's LDS tile
+    // P to the A layout through this wave's own LDS tile (in-order LDS within
+    // the wave: no block barrier), read back as one 16-byte row slice
     {
       uint16_t* ps16 = reinterpret_cast<uint16_t*>(&ps[w][0][0]);
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ps16[(4 * lg + j) * 34 + 16 * h + li] = f32_to_bf16(p[h][j]);
+        for (int j = 0; j < 4; ++j) ps16[(4 * lg + j) * 40 + 16 * h + li] = f32_to_bf16(p[h][j]);
     }
-    __syncthreads();
     u32x4 pa;
-    {
-      const uint16_t* ps16 = reinterpret_cast<const uint16_t*>(&ps[w][0][0]) + li * 34 + 8 * lg;
-      pa.x = (uint32_t)ps16[0] | ((uint32_t)ps16[1] << 16);
-      pa.y = (uint32_t)ps16[2] | ((uint32_t)ps16[3] << 16);
-      pa.z = (uint32_t)ps16[4] | ((uint32_t)ps16[5] << 16);
-      pa.w = (uint32_t)ps16[6] | ((uint32_t)ps16[7] << 16);
-    }
-    __syncthreads();
+    __builtin_memcpy(&pa, &ps[w][li][4 * lg], sizeof(pa));   // alias-safe (the tile is written as bf16)
     // O += P V: B operand = keys kb + 8*lg .. +7 of dim t*16 + li
 #pragma unroll
     for (int t = 0; t < NT; ++t) o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_att8(pa), as_att8(vr[t]), o[t], 0, 0, 0);
