@@ -580,7 +580,8 @@ int packed_prefetch_depth(int K, int TN, int WS) {
 // (one tile per wave, up to 16 waves per tile) or ~3072 (two tiles), keeping at
 // least 2 sets per wave. Measured on the 9B shapes (M = 4 / 1, us): down
 // (1,16) 9.7 / 8.5, in_proj (2,8) 9.6 / 8.9, qkv (1,8) 8.4 / 7.5, o_proj (1,8)
-// 5.2 / 4.8, gate_up (2,4) 13.3 / 12.9, mtp fc (1,16) 7.1 / 6.4, lm_head (2,4) 93.5 / 86.0.
+// 5.2 / 4.8, gate_up (2,4) 13.3 / 12.9 (the fused gate/up product takes
+// packed_swiglu_tile), mtp fc (1,16) 7.1 / 6.4, lm_head (2,4) 93.5 / 86.0.
 void packed_default_tile(int N, int K, int* TN, int* WS) {
   const long tiles = (N + PK_TILE - 1) / PK_TILE;
   const int GS = K / PK_SET;
