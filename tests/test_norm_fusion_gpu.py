@@ -137,6 +137,33 @@ def test_model_fused_rows_independent_of_width(tiny):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("T", [1, 3])
+def test_mtp_first_norm_from_fc_epilogue(tiny, T):
+    """The MTP block's first norm inputs from the fc product's residual epilogue
+    (zero residual) give the same bits as fc followed by rms_parts: logits and
+    the block output of a draft step, for T rows."""
+    from qvex.mtp import MTPHead, random_mtp
+    mtp = random_mtp(tiny, seed=23)
+    H, V = tiny.cfg.hidden_size, tiny.cfg.vocab_size
+    g = torch.Generator().manual_seed(29)
+    hidden = (torch.randn(1, T, H, generator=g) * 2).to(torch.bfloat16).to(DEV)
+    ids = torch.randint(0, V, (1, T), generator=g, dtype=torch.int32).to(DEV)
+    outs = []
+    old = MTPHead.fc_epilogue
+    try:
+        for flag in (False, True):
+            MTPHead.fc_epilogue = flag
+            cache = mtp.make_cache()
+            logits, h = mtp(hidden, ids, cache, last_only=False, return_hidden=True)
+            torch.cuda.synchronize()
+            outs.append((logits.float().cpu(), h.float().cpu()))
+    finally:
+        MTPHead.fc_epilogue = old
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1])
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("R,D", [(1, 4096), (4, 4096), (3, 512)])
 def test_rmsnorm_pair_equals_two_calls(R, D):
     """qvex_rmsnorm_pair (the MTP head's two input norms into the halves of the fc
