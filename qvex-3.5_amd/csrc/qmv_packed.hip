@@ -578,10 +578,12 @@ int packed_prefetch_depth(int K, int TN, int WS) {
 // Tile choice from (N, K) only, so a row's bits never depend on M. Two tiles per
 // wave from ~700 tiles up; waves split K until the launch holds ~4096 waves
 // (one tile per wave, up to 16 waves per tile) or ~3072 (two tiles), keeping at
-// least 2 sets per wave. Measured on the 9B shapes (M = 4 / 1, us): down
-// (1,16) 9.7 / 8.5, in_proj (2,8) 9.6 / 8.9, qkv (1,8) 8.4 / 7.5, o_proj (1,8)
-// 5.2 / 4.8, gate_up (2,4) 13.3 / 12.9 (the fused gate/up product takes
-// packed_swiglu_tile), mtp fc (1,16) 7.1 / 6.4, lm_head (2,4) 93.5 / 86.0.
+// least 2 sets per wave; at most 8 waves per tile for K >= 12288 (the MLP down:
+// 512-thread blocks, 9.3 against 9.5 us at (1,16), -9.7 us per decode cycle).
+// Measured on the 9B shapes (M = 4 / 1, us): in_proj (2,8) 9.6 / 8.9, qkv (1,8)
+// 8.4 / 7.5, o_proj (1,8) 5.2 / 4.8, gate_up (2,4) 13.3 / 12.9 (the fused
+// gate/up product takes packed_swiglu_tile), mtp fc (1,16) 7.1 / 6.4, lm_head
+// (2,4) 93.5 / 86.0.
 void packed_default_tile(int N, int K, int* TN, int* WS) {
   const long tiles = (N + PK_TILE - 1) / PK_TILE;
   const int GS = K / PK_SET;
@@ -591,6 +593,7 @@ void packed_default_tile(int N, int K, int* TN, int* WS) {
   int ws = GS >= 8 ? 2 : 1;
   while (ws < ws_max && (tiles / tn) * ws < limit && GS >= 2 * (ws * 2)) ws *= 2;
   if (tiles / tn >= 4096 && GS >= 8 && ws < 4) ws = 4;   // lm_head-wide: 4 sets per wave (86 vs 89.5 us at M=1)
+  if (GS >= 48 && ws > 8) ws = 8;                        // long K (the MLP down): 512-thread blocks
   *TN = tn;
   *WS = ws;
 }

@@ -111,6 +111,8 @@ def default_tile(N, K):
         ws *= 2
     if tiles // tn >= 4096 and GS >= 8 and ws < 4:
         ws = 4
+    if GS >= 48 and ws > 8:
+        ws = 8
     return tn, ws
 
 
