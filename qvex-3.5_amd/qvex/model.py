@@ -441,6 +441,9 @@ class Attention:
     """Gated full attention (engine/model.py:199-232) with q/k/v projections fused
     into one quantized matmul (lossless, like the reference's in_proj fusion)."""
 
+    # keys per split of the decode / verify attention (a multiple of 128)
+    decode_kps = 128
+
     def __init__(self, cfg: Config, p: dict):
         self.cfg = cfg
         self.n_heads, self.n_kv = cfg.num_attention_heads, cfg.num_key_value_heads
@@ -470,7 +473,7 @@ class Attention:
                 _ptr(cache.k), _ptr(cache.v), cache.capacity, _stream())
         # a captured call must work for every later context length: bound by capacity
         max_keys = cache.capacity if cache.counters.graph_mode else min(cache.capacity, cache.offset + L)
-        kps = 128 if L <= 8 else 512       # keys per 4-wave block: verify spreads ~ctx/32 waves per kv head
+        kps = self.decode_kps if L <= 8 else 512   # keys per 4-wave block: verify spreads ~ctx/32 waves per kv head
         ws = self._workspace(L, max_keys, kps, x.device)
         o = torch.empty((L, H * D), dtype=torch.bfloat16, device=x.device)
         _C.call("qvex_attention", _ptr(q), _ptr(cache.k), _ptr(cache.v), pos, L, H, Hkv, D, cache.capacity,
