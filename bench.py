@@ -75,7 +75,10 @@ def qmv_time(M, N, K, iters=None, tile=None, seed_tag=0, packed=False, swiglu=Fa
         PK = [kernels.pack_w4(W[i], S[i], B[i], swiglu=swiglu) for i in range(ncopy)]
         del W, S, B
         W = S = B = None
-        launch = lambda i: kernels.quantized_matmul_packed(xd, PK[i % ncopy], N, out=y, tile=tile, swiglu=swiglu)
+        def launch(i):   # rows in chunks of 4, as QLinear runs 5..15-row calls
+            for m0 in range(0, M, 4):
+                kernels.quantized_matmul_packed(xd[m0:m0 + 4], PK[i % ncopy], N, out=y[m0:m0 + 4], tile=tile,
+                                                swiglu=swiglu)
     else:
         PK = None
         launch = lambda i: kernels.quantized_matmul(xd, W[i % ncopy], S[i % ncopy], B[i % ncopy], out=y, tile=tile)
@@ -149,18 +152,19 @@ def roofline(name):
 
 def qmv_shapes():
     """Config-1 shapes as the decode cycle runs them: the packed MFMA kernel for
-    1..4 rows (M=4 verify, M=1 draft / plain decode), the MLX-layout kernel at M=5."""
+    1..4 rows (M=4 verify, M=1 draft / plain decode), and in chunks of 4 rows for
+    M=5 (a verify of 4 drafts: two launches, 4 + 1 rows)."""
     out = {}
     shapes = {"lm_head_m1": (1, 248320, 4096), "lm_head_m4": (4, 248320, 4096),
               "gate_up_swiglu_m4": (4, 24576, 4096), "down_m4": (4, 4096, 12288),
               "gdn_in_proj_m4": (4, 12352, 4096), "attn_qkv_m4": (4, 10240, 4096),
               "o_proj_m4": (4, 4096, 4096), "mtp_fc_m1": (1, 4096, 8192),
-              "gate_up_m5": (5, 24576, 4096)}
+              "gate_up_swiglu_m5": (5, 24576, 4096)}
     for name, (M, N, K) in shapes.items():
-        us, algo = qmv_time(M, N, K, packed=M <= 4, swiglu="swiglu" in name)
+        us, algo = qmv_time(M, N, K, packed=True, swiglu="swiglu" in name)
         out[name] = {"us": round(us, 2), "GB/s": round(algo / (us * 1e-6) / 1e9, 1),
                      "frac": round(algo / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
-                     "kernel": "packed" if M <= 4 else "mlx-layout"}
+                     "kernel": "packed" if M <= 4 else "packed, chunks of 4 rows"}
     return out
 
 

@@ -122,8 +122,11 @@ class QLinear:
     a multiple of 256 the layer also keeps the tile-packed copy (pack_w4), built
     once here, and runs every call of 1..4 rows - decode, MTP drafts, verify of
     up to 3 drafts - through the MFMA kernel on it; the row bits of that kernel
-    do not depend on the number of rows. Wider calls (prefill) use the
-    MLX-layout kernel in chunks of 8 rows."""
+    do not depend on the number of rows. Calls of 5..DENSE_MIN_ROWS-1 rows
+    (verify of more drafts, short prefill tails) run it on chunks of 4 rows, so
+    their rows have the same bits too; longer calls dequantize once and use a
+    library GEMM. Without a packed copy (K not a multiple of 256) the MLX-layout
+    kernel takes chunks of 8 rows."""
 
     PACKED_MAX_ROWS = 4
     # calls of at least this many rows (prefill) dequantize the weight to bf16
@@ -152,6 +155,10 @@ class QLinear:
     def _takes_normed(self, x, M: int) -> bool:
         return self.packed is not None and M <= self.PACKED_MAX_ROWS and NormedRows.supported(self.K)
 
+    def _packed_chunks(self, M: int) -> bool:
+        """Rows for the packed kernel in chunks of PACKED_MAX_ROWS (M > 4, below the dense GEMM)."""
+        return self.packed is not None and M < max(self.DENSE_MIN_ROWS, self.PACKED_MAX_ROWS + 1)
+
     def swiglu(self, x) -> torch.Tensor:
         """silu(x W_gate^T) * (x W_up^T) for a fused [gate; up] layer
         (_swiglu over the split halves, engine/model.py:134-135, 302)."""
@@ -164,6 +171,12 @@ class QLinear:
         M, I = x2.shape[0], self.N // 2
         if self.swiglu_packed and self.packed is not None and M <= self.PACKED_MAX_ROWS:
             return kernels.quantized_matmul_packed(x2, self.packed, self.N, swiglu=True)
+        if self.swiglu_packed and self._packed_chunks(M):
+            h = torch.empty((M, I), dtype=torch.bfloat16, device=x.device)
+            for m0 in range(0, M, self.PACKED_MAX_ROWS):
+                m1 = min(M, m0 + self.PACKED_MAX_ROWS)
+                kernels.quantized_matmul_packed(x2[m0:m1], self.packed, self.N, out=h[m0:m1], swiglu=True)
+            return h
         gu = self(x2)
         h = torch.empty((M, I), dtype=torch.bfloat16, device=x.device)
         _C.call("qvex_swiglu", _ptr(gu), _ptr(h), M, I, _stream())
@@ -185,6 +198,11 @@ class QLinear:
         o2 = out.view(M, self.N)
         if self.packed is not None and not self.swiglu_packed and M <= self.PACKED_MAX_ROWS:
             kernels.quantized_matmul_packed(x2, self.packed, self.N, out=o2)
+            return out.view(*lead, self.N)
+        if not self.swiglu_packed and self._packed_chunks(M):
+            for m0 in range(0, M, self.PACKED_MAX_ROWS):
+                m1 = min(M, m0 + self.PACKED_MAX_ROWS)
+                kernels.quantized_matmul_packed(x2[m0:m1], self.packed, self.N, out=o2[m0:m1])
             return out.view(*lead, self.N)
         if self.DENSE_MIN_ROWS and M >= self.DENSE_MIN_ROWS:
             # long (prefill) call: the weight dequantized once to bf16, then a

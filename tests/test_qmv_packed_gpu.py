@@ -175,3 +175,30 @@ def test_argmax_epilogue_equals_argmax_of_product(M, N, K, ties):
     want2 = torch.tensor([int(torch.nonzero(y2[r] == y2[r].max())[0]) for r in range(M)], dtype=torch.int32)
     torch.cuda.synchronize()
     assert torch.equal(out.cpu(), want2)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [5, 7, 8, 13])
+@pytest.mark.parametrize("swiglu", [False, True])
+def test_qlinear_rows_5_to_15_equal_single_row_calls(M, swiglu):
+    """QLinear runs 5..15 rows through the packed kernel in chunks of 4: every row
+    has the bits of the same row computed alone (as decode computes it)."""
+    from qvex.model import QLinear
+    N, K = 1024, 2048
+    w, s, b = synth.qmv_weights(N, K, seed=41, tag=M)
+    lin = QLinear(torch.from_numpy(w.view(np.int32)).to("cuda:0"),
+                  torch.from_numpy(s.view(np.int16)).to("cuda:0").view(torch.bfloat16),
+                  torch.from_numpy(b.view(np.int16)).to("cuda:0").view(torch.bfloat16), swiglu=swiglu)
+    assert lin.packed is not None and M < QLinear.DENSE_MIN_ROWS
+    x = torch.from_numpy(synth.qmv_x(M, K, seed=41, tag=M).view(np.int16)).to("cuda:0").view(torch.bfloat16)
+    f = lin.swiglu if swiglu else lin
+    wide = f(x)
+    rows = torch.cat([f(x[r:r + 1]) for r in range(M)])
+    torch.cuda.synchronize()
+    assert torch.equal(wide, rows)
+    # and the values are the product's (plain: against the MLX-layout kernel)
+    if not swiglu:
+        ref = torch.cat([kernels.quantized_matmul(x[m0:m0 + 8], lin.w, lin.scales, lin.biases)
+                         for m0 in range(0, M, 8)]).float()
+        d = (wide.float() - ref).abs()
+        assert float((d / (ref.abs() + 1.0)).max()) < 2e-2
