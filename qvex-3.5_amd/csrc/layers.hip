@@ -274,7 +274,7 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
 //   holds Q row l%16 dims 8(l/16).. and key l%16 of the block, same dims);
 //   the accumulator puts rows 4(l/16)+r in lane l at key l%16, so row max / sum
 //   are 16-lane DPP reductions; online softmax rescales O in place;
-//   P (bf16) goes through 1 KB of LDS into the A layout, and O[16 x D] += P V
+//   P (bf16) goes through the wave's own LDS tile into the A layout, and O[16 x D] += P V
 //   with V stored dim-major, so lane l reads 8 consecutive keys of dim l%16.
 // Partials (m, l, O) per row go to the workspace; attn_combine merges splits.
 typedef __bf16 att_bf16x8 __attribute__((ext_vector_type(8)));

@@ -25,7 +25,8 @@
 // A wave reads one record per (tile, set) with two fully coalesced 1 KiB loads
 // plus one 256-byte load; the activation slice of the set (M x 256 bf16) comes in
 // with two more coalesced loads, goes through a wave-private LDS slot and is read
-// back per MFMA step by the 16 lanes whose A rows are live in that k-chunk.
+// back per MFMA step by the 16 lanes whose A rows are live in that k-chunk (the
+// other lanes read a zeroed area of the slot).
 #include "qvex_common.h"
 #include "w4_dequant.h"
 
