@@ -1,0 +1,101 @@
+"""The caller above the decode generator (engine/engine.py:105-118, 280-366):
+prefill, the MTP policy, forced tokens, stop ids, max_tokens and the run's
+stats, for token ids in and token ids out.
+
+What the reference's Engine adds beyond this - the worker thread and job queue,
+tokenizer and chat template, reasoning budget (which feeds `forced`), thermal
+governor, power telemetry and the HTTP layer - is outside the decode path and
+not reproduced. Without a thermal governor the "auto" MTP mode is "on": the
+reference's auto policy only turns MTP off under a tok/s cap or near the die's
+thermal target (engine/engine.py:112-118).
+"""
+
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _C
+from .model import Qwen35
+from .mtp import MTPHead
+from .sampler import Sampler, SamplingParams
+from .speculative import decode, mtp_prefill
+
+MTP_MODES = ("off", "on", "auto")
+
+
+@dataclass
+class GenerateResult:
+    tokens: list[int]              # emitted ids, the stop token excluded
+    finish_reason: str             # "stop" or "length"
+    stats: dict = field(default_factory=dict)
+
+
+def mtp_policy(mode: str, mtp: MTPHead | None):
+    """use_mtp callable of a mode (engine/engine.py:105-118)."""
+    if mode not in MTP_MODES:
+        raise ValueError(f"unknown MTP mode {mode!r}")
+    if mode != "off" and mode != "auto" and mtp is None:
+        raise ValueError("MTP head not loaded")
+    on = mode != "off" and mtp is not None
+    return lambda: on
+
+
+def generate(model: Qwen35, prompt_ids, params: SamplingParams, mtp: MTPHead | None = None,
+             mtp_mode: str = "auto", k: int = 3, stop_ids=(), forced: list[int] | None = None,
+             max_tokens: int | None = None) -> GenerateResult:
+    """Prefill the prompt (the model runs it in 512-token chunks), hand the last
+    hidden states to the MTP head, then draw tokens through decode() until a
+    stop id or max_tokens (engine/engine.py:280-300). `forced` is shared with the
+    generator: ids appended to it while iterating are emitted next, as the
+    reference's reasoning budget does. A stop id counts in completion_tokens but
+    is not returned. Stats keys follow the reference's (engine/engine.py:340-357)
+    where they apply to this path."""
+    use_mtp = mtp_policy(mtp_mode, mtp)
+    ids = torch.as_tensor(prompt_ids, dtype=torch.int32).reshape(1, -1).to(model.norm.device)
+    if ids.shape[1] < 1:
+        raise _C.QvexError("generate: empty prompt")
+    limit = params.max_tokens if max_tokens is None else max_tokens
+    forced = forced if forced is not None else []
+    stop = set(int(t) for t in stop_ids)
+
+    t_start = time.perf_counter()
+    cache = model.make_cache()
+    mcache = mtp.make_cache() if mtp is not None else None
+    logits, hidden = model(ids, cache, return_hidden=True)
+    last_h = mtp_prefill(mtp, mcache, hidden, ids, None) if mtp is not None else None
+    sampler = Sampler(params, model.cfg.vocab_size)
+    spec: dict = {}
+    tokens = decode(model, sampler, cache, logits[0, -1], last_h, mtp, mcache, use_mtp, spec, forced, k)
+
+    out: list[int] = []
+    n, finish = 0, "length"
+    t_first = None
+    for t in tokens:
+        if t_first is None:
+            t_first = time.perf_counter()
+        n += 1
+        if t in stop:
+            finish = "stop"
+            break
+        out.append(int(t))
+        if n >= limit:
+            break
+    tokens.close()
+    torch.cuda.synchronize()
+    t_end = time.perf_counter()
+    t_first = t_first if t_first is not None else t_end
+    decode_s = t_end - t_first
+    stats = {
+        "prompt_tokens": int(ids.shape[1]),
+        "cached_tokens": 0,
+        "completion_tokens": n,
+        "ttft_s": t_first - t_start,
+        "prefill_tps": ids.shape[1] / (t_first - t_start) if t_first > t_start else None,
+        "decode_tps": n / decode_s if decode_s > 0 else None,
+        "mtp_cycles": spec.get("cycles", 0),
+        "mtp_accepted": spec.get("accepted", 0),
+    }
+    return GenerateResult(out, finish, stats)

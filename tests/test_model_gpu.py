@@ -257,3 +257,54 @@ def test_graphed_run_pipelined_equals_cycles(head):
     assert torch.equal(a.dec.cache.counters.dev, b.dec.cache.counters.dev)
     assert torch.equal(a.dec.mtp_cache.counters.dev, b.dec.mtp_cache.counters.dev)
     assert torch.equal(a.dec.sampler.seen, b.dec.sampler.seen)
+
+
+# ---------------------------------------------------------------- generate() (engine/engine.py:105-118, 280-366)
+
+@pytest.mark.gpu
+def test_generate_mtp_on_equals_off_greedy_and_stats(tiny):
+    """Greedy generation with the MTP policy on emits the tokens of the policy
+    off; stats carry the reference's keys, MTP cycles only when on."""
+    from qvex.engine import generate
+    mtp = random_mtp(tiny, seed=31)
+    prompt = np.random.default_rng(31).integers(0, tiny.cfg.vocab_size, 37).tolist()
+    p = SamplingParams(temperature=0.0, max_tokens=20)
+    on = generate(tiny, prompt, p, mtp, mtp_mode="on", k=3)
+    off = generate(tiny, prompt, p, mtp, mtp_mode="off", k=3)
+    assert on.tokens == off.tokens and len(on.tokens) == 20
+    assert on.finish_reason == off.finish_reason == "length"
+    for key in ("prompt_tokens", "cached_tokens", "completion_tokens", "ttft_s", "prefill_tps", "decode_tps",
+                "mtp_cycles", "mtp_accepted"):
+        assert key in on.stats
+    assert on.stats["prompt_tokens"] == 37 and on.stats["completion_tokens"] == 20
+    assert on.stats["mtp_cycles"] > 0 and off.stats["mtp_cycles"] == 0
+    auto = generate(tiny, prompt, p, None, mtp_mode="auto")       # auto without a head: plain decoding
+    assert auto.tokens == off.tokens and auto.stats["mtp_cycles"] == 0
+
+
+@pytest.mark.gpu
+def test_generate_stop_ids_and_forced_tokens(tiny):
+    """A stop id ends the run (counted, not returned); forced ids are emitted next
+    in order, and ids appended to the list while iterating too."""
+    from qvex.engine import generate
+    mtp = random_mtp(tiny, seed=37)
+    prompt = np.random.default_rng(37).integers(0, tiny.cfg.vocab_size, 20).tolist()
+    p = SamplingParams(temperature=0.0, max_tokens=12)
+    base = generate(tiny, prompt, p, mtp, mtp_mode="on")
+    stop = base.tokens[4]
+    first = base.tokens.index(stop)
+    r = generate(tiny, prompt, p, mtp, mtp_mode="on", stop_ids=[stop])
+    assert r.finish_reason == "stop" and r.tokens == base.tokens[:first]
+    assert r.stats["completion_tokens"] == first + 1
+    f = generate(tiny, prompt, p, mtp, mtp_mode="on", forced=[11, 12, 13])
+    assert f.tokens[0] == base.tokens[0] and f.tokens[1:4] == [11, 12, 13]
+
+
+@pytest.mark.gpu
+def test_generate_policy_errors(tiny):
+    from qvex.engine import generate
+    p = SamplingParams(temperature=0.0, max_tokens=2)
+    with pytest.raises(ValueError):
+        generate(tiny, [1, 2, 3], p, None, mtp_mode="on")
+    with pytest.raises(ValueError):
+        generate(tiny, [1, 2, 3], p, None, mtp_mode="sometimes")
