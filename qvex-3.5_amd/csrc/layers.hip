@@ -326,6 +326,17 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
   // together (clamped in bounds; keys past k_hi are masked out of the softmax and
   // get P = 0). The first window does not depend on the device position, so its
   // loads go out before the position is read.
+  // A operand: Q row li, dims step*32 + 8*lg .. +7 (the 1/sqrt(D) scale is applied
+  // to the scores). Requested first: loads complete in order, so the scores can
+  // start once Q and K are in while the V columns still stream
+  u32x4 qa[KS];
+  {
+    const int g = li / QT, lq = tile * QT + li % QT;
+    const bool ok = g < GQ && lq < L;
+    const uint16_t* qp = q + ((size_t)(ok ? lq : 0) * Hq + kh * GQ + (ok ? g : 0)) * D + 8 * lg;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qa[s] = ok ? load16(qp + 32 * s) : u32x4{0, 0, 0, 0};
+  }
   u32x4 kr[2][KS], vr[NT];
   auto load_kv = [&](int kb) {
 #pragma unroll
@@ -339,15 +350,6 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
     for (int t = 0; t < NT; ++t) vr[t] = load16(vbase + (size_t)(t * 16 + li) * cap + kv0);
   };
   load_kv(k_lo + 32 * w);
-  // A operand: Q row li, dims step*32 + 8*lg .. +7 (the 1/sqrt(D) scale is applied to the scores)
-  u32x4 qa[KS];
-  {
-    const int g = li / QT, lq = tile * QT + li % QT;
-    const bool ok = g < GQ && lq < L;
-    const uint16_t* qp = q + ((size_t)(ok ? lq : 0) * Hq + kh * GQ + (ok ? g : 0)) * D + 8 * lg;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) qa[s] = ok ? load16(qp + 32 * s) : u32x4{0, 0, 0, 0};
-  }
 
   const int p0 = *pos0;
   const int kend_tile = p0 + min(L, (tile + 1) * QT);
