@@ -21,8 +21,6 @@ MI355X-specific state layout (what makes rollback free):
 
 from __future__ import annotations
 
-import contextlib
-
 import json
 import math
 from dataclasses import dataclass, field
@@ -134,23 +132,6 @@ class QLinear:
     # calls of at least this many rows (prefill) dequantize the weight to bf16
     # and run a library GEMM; 0 disables it
     DENSE_MIN_ROWS = 16
-    # bf16 weights kept across the chunks of one prefill (dense_weights_kept)
-    _dense_keep: dict | None = None
-
-    @classmethod
-    @contextlib.contextmanager
-    def dense_weights_kept(cls):
-        """Within the block, each layer's bf16 weight of the dense path is made
-        once and reused (a chunked prefill dequantizes every weight once instead
-        of once per chunk; the model's bf16 size in HBM meanwhile), then freed."""
-        if cls._dense_keep is not None:
-            yield
-            return
-        cls._dense_keep = {}
-        try:
-            yield
-        finally:
-            cls._dense_keep = None
 
     def __init__(self, w, scales, biases, group_size=64, bits=4, pack: bool = True, swiglu: bool = False):
         if group_size != 64 or bits != 4:
@@ -226,12 +207,7 @@ class QLinear:
         if self.DENSE_MIN_ROWS and M >= self.DENSE_MIN_ROWS:
             # long (prefill) call: the weight dequantized once to bf16, then a
             # plain 2-D library GEMM (fp32 accumulation) instead of M / 8 GEMVs
-            keep = QLinear._dense_keep
-            wd = keep.get(id(self)) if keep is not None else None
-            if wd is None:
-                wd = kernels.dequant_w4(self.w, self.scales, self.biases)
-                if keep is not None:
-                    keep[id(self)] = wd
+            wd = kernels.dequant_w4(self.w, self.scales, self.biases)
             torch.mm(x2, wd.t(), out=o2)
             return out.view(*lead, self.N)
         for m0 in range(0, M, QMV_MAX_ROWS):
@@ -724,15 +700,14 @@ class Qwen35:
                 step = min(step, c.ring_rows - c.kernel + 1)
         if L > step:
             outs, hs = [], []
-            with QLinear.dense_weights_kept():
-                for s0 in range(0, L, step):
-                    ho = None if hidden_out is None else hidden_out.view(L, -1)[s0:s0 + step]
-                    r = self(ids[s0:s0 + step].reshape(1, -1), cache, last_only=last_only and s0 + step >= L,
-                             return_hidden=return_hidden, keep_prev=keep_prev, hidden_out=ho)
-                    if return_hidden:
-                        outs.append(r[0]); hs.append(r[1])
-                    else:
-                        outs.append(r)
+            for s0 in range(0, L, step):
+                ho = None if hidden_out is None else hidden_out.view(L, -1)[s0:s0 + step]
+                r = self(ids[s0:s0 + step].reshape(1, -1), cache, last_only=last_only and s0 + step >= L,
+                         return_hidden=return_hidden, keep_prev=keep_prev, hidden_out=ho)
+                if return_hidden:
+                    outs.append(r[0]); hs.append(r[1])
+                else:
+                    outs.append(r)
             logits = outs[-1] if last_only else torch.cat(outs, dim=1)
             return (logits, torch.cat(hs, dim=1)) if return_hidden else logits
         counters.sync()
