@@ -409,19 +409,24 @@ int qvex_cycle_finish(const int32_t* drafts, int k, const int32_t* n_accept, con
  * then being written straight into ids_next[1..k]), main_counters[i] +=
  * n + main_extra for i < n_main (the verify commit of decode(),
  * engine/speculative.py:94-101), mtp_counters[i] += mtp_delta (the draft
- * steps' net advance), and u_out = u_table[*u_counter mod u_rows], then
- * *u_counter += 1 (the next cycle's uniforms). Null pointers skip a part; every
- * read happens before any write, so drafts may alias ids_next + 1. */
+ * steps' net advance), and u_out[0:u_width) = the uniforms of draw event
+ * *u_counter under u_seed (as qvex_philox_uniforms), then *u_counter += 1 (the
+ * next cycle's uniforms). Null pointers skip a part; every read happens before
+ * any write, so drafts may alias ids_next + 1. */
 int qvex_cycle_finish_ex(const int32_t* drafts, int k, const int32_t* n_accept, const int32_t* token,
                          int32_t* pend_ids, int32_t* feed, int32_t* n_prev, int32_t* out,
                          int32_t* ids_next, int32_t* main_counters, int n_main, int main_extra,
-                         int32_t* mtp_counters, int n_mtp, int mtp_delta, const float* u_table,
-                         int u_rows, int u_width, int32_t* u_counter, float* u_out, void* stream);
+                         int32_t* mtp_counters, int n_mtp, int mtp_delta, uint64_t u_seed,
+                         uint64_t* u_counter, int u_width, float* u_out, void* stream);
 
-/* out[0:width) = table[*counter mod rows]; then *counter += 1 (the cycle's
- * uniforms from a pre-drawn table). */
-int qvex_next_uniforms(const float* table, int rows, int width, int32_t* counter, float* out,
-                       void* stream);
+/* The sampler's uniforms (the draws of engine/speculative.py:79-81 and
+ * Sampler.pick's categorical, engine/sampler.py:57-58, which use MLX's
+ * generator): out[i] = u(*counter, i) for i < n (1..256), then *counter += 1,
+ * where draw event c under seed s gives
+ *   u(c, i) = (philox4x32_10({c_lo, c_hi, i / 4, 0}, {s_lo, s_hi})[i % 4] >> 8) * 2^-24
+ * (Philox4x32-10, Salmon et al., SC 2011). counter: one device uint64. The
+ * stream never repeats, and a draw needs no host work, so it can be captured. */
+int qvex_philox_uniforms(uint64_t seed, uint64_t* counter, int n, float* out, void* stream);
 
 /* Presence tracking (Sampler.observe, engine/sampler.py:60-62): seen[ids[q]] = 1
  * for q < min(max_ids, (n_ptr ? *n_ptr : 0) + n_offset); ids outside [0, V) are

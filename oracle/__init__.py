@@ -20,6 +20,8 @@ listed per function below; each is exercised in tests/test_oracle.py.
   - gated_delta_f64: matrix form S_t = g S (I - b k k^T) + b v k^T (a different
     formulation); delta-rule invariants (g = 1, b = 0 keeps S; g = 1, b = 1,
     |k| = 1 gives S k = v); T-step = T one-step calls; golden fixtures.
+  - philox4x32_10 / philox_uniforms: the known-answer vectors published with
+    Philox (Salmon et al. 2011); the uniform law (moments, equidistribution).
   - spec_accept: textbook rule checked by exhaustive enumeration on tiny
     vocabularies, p == q accepts all, p(d) = 0 rejects, greedy limit, chi^2 of
     the emitted-token law; orc_expf within 2 ulp of float64 exp.
@@ -62,6 +64,10 @@ def lib() -> ctypes.CDLL:
         L.orc_gated_delta_f32.argtypes = [P] * 10 + [I] * 7
         L.orc_spec_accept.argtypes = [P, P, P, P, P, F, P, P, I, I, I, I]
         L.orc_spec_accept_filtered.argtypes = [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, I]
+        L.orc_philox4x32_10.argtypes = [P, P, P]
+        L.orc_philox4x32_10.restype = None
+        L.orc_philox_uniforms.argtypes = [ctypes.c_uint64, ctypes.c_uint64, I, P]
+        L.orc_philox_uniforms.restype = None
         L.orc_expf.argtypes = [F]
         L.orc_expf.restype = F
         for fn in ("orc_qmv_w4g64_f64", "orc_qmv_w4g64_f32", "orc_gated_delta_f64",
@@ -211,6 +217,24 @@ def spec_accept(target, draft, draft_ids, u_accept, u_sample, inv_temp, threads=
                                    float(np.float32(inv_temp)), _p(seen), float(np.float32(presence_penalty)),
                                    int(top_k), float(np.float32(top_p)), _p(n), _p(tok), S, k, V, threads)
     return n, tok
+
+
+# ---------------------------------------------------------------- uniforms
+
+def philox4x32_10(ctr, key) -> np.ndarray:
+    """One Philox4x32-10 block (Salmon et al. 2011) of 4 uint32 words."""
+    c = np.ascontiguousarray(ctr, np.uint32).reshape(4)
+    k = np.ascontiguousarray(key, np.uint32).reshape(2)
+    out = np.empty(4, np.uint32)
+    lib().orc_philox4x32_10(_p(c), _p(k), _p(out))
+    return out
+
+
+def philox_uniforms(seed: int, event: int, n: int) -> np.ndarray:
+    """The sampler's n uniforms of draw event `event` (oracle/rng.c)."""
+    out = np.empty(n, np.float32)
+    lib().orc_philox_uniforms(int(seed) & (2**64 - 1), int(event), int(n), _p(out))
+    return out
 
 
 def expf(x: float) -> float:

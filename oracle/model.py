@@ -3,14 +3,23 @@ forward, following engine/model.py:121-336 and engine/mtp.py:58-68 op by op,
 with a bf16 rounding wherever the reference produces a bf16 array.
 
 Weights are read from a qvex model object's tensors (host copies); the oracle
-never calls the HIP library. fp32 arithmetic (float64 for the matmul accumulations).
+never calls the HIP library. fp32 arithmetic (float64 for the matmul
+accumulations, through the C fp64 qmv of liboracle).
+
+Pinning (tests/test_oracle_model.py, CPU): rope against the complex-rotation
+form and its invariants (identity at position 0, norm kept, scores depend only
+on the position difference, dims past rot_dim untouched, the half-split pairing
+of traditional=False); conv1d_window against numpy's correlate and one-hot taps;
+rms_norm against a float64 formula; attention_core against a log-sum-exp form;
+the MTP head (mtp) against the composition of these pinned parts, written out
+separately in the test.
 """
 
 from __future__ import annotations
 
 import numpy as np
 
-from . import bf16_to_f32, round_bf16, dequant_w4_f64, gated_delta_f64
+from . import bf16_bits, bf16_to_f32, round_bf16, dequant_w4_f64, gated_delta_f64, qmv_f64
 
 
 def _np_bf16(t):
@@ -41,10 +50,13 @@ def embed_rows(e, ids):
 
 
 def qlinear(q, x):
-    """y = bf16(x @ dequant(W)^T) (mx.quantized_matmul)."""
+    """y = bf16(x @ dequant(W)^T) (mx.quantized_matmul); x holds bf16 values.
+    The fp64 sum runs in C (one dequantized weight row at a time), so a
+    full-vocabulary lm_head needs no dense copy of the weight."""
     w, s, b = _qweights(q)
-    W = dequant_w4_f64(w, s, b, w.shape[1] * 8)
-    return round_bf16((x.astype(np.float64) @ W.T).astype(np.float32))
+    x2 = np.asarray(x, np.float32).reshape(-1, w.shape[1] * 8)
+    y = qmv_f64(bf16_bits(x2), w, s, b)
+    return round_bf16(y.astype(np.float32)).reshape(*np.shape(x)[:-1], w.shape[0])
 
 
 def rms_norm(x, w, eps):
@@ -59,6 +71,32 @@ def rms_norm(x, w, eps):
 
 def sigmoid(x):
     return 1.0 / (1.0 + np.exp(-x))
+
+
+def conv1d_window(state, x, w):
+    """Causal depthwise conv over [state; x] (engine/model.py:261-269): mx.conv1d
+    with weight [C, K, 1] and groups = C is a cross-correlation, so output row t
+    = sum_j conv_in[t + j] * w[:, j]; tap K - 1 multiplies the current token.
+    state [K-1, C], x [S, C], w [C, K] -> (bf16 conv output [S, C], new state)."""
+    Kw = w.shape[1]
+    conv_in = np.concatenate([state, x], axis=0)
+    S = x.shape[0]
+    acc = np.zeros((S, x.shape[1]), np.float64)
+    for j in range(Kw):
+        acc += conv_in[j:j + S].astype(np.float64) * w[:, j][None, :]
+    return round_bf16(acc.astype(np.float32)), conv_in[-(Kw - 1):].copy()
+
+
+def attention_core(q, K, V, pos0, scale):
+    """Causal softmax attention of L queries at positions pos0.. over S keys
+    (mx.fast.scaled_dot_product_attention with mask="causal" when L > 1):
+    q [L, D], K, V [S, D] -> [L, D] float64."""
+    L, S = q.shape[0], K.shape[0]
+    s = (q.astype(np.float64) @ K.T.astype(np.float64)) * scale
+    s[np.arange(S)[None, :] > (pos0 + np.arange(L))[:, None]] = -np.inf
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    return p @ V.astype(np.float64)
 
 
 def rope(x, pos0, dims, base):
@@ -123,16 +161,10 @@ class OracleModel:
         c["k"] = np.concatenate([c["k"], k], axis=1)
         c["v"] = np.concatenate([c["v"], v], axis=1)
         K, V = c["k"], c["v"]
-        S = K.shape[1]
         rep = H // Hkv
         o = np.zeros((H, L, D), np.float64)
         for h in range(H):
-            s = (q[h].astype(np.float64) @ K[h // rep].T.astype(np.float64)) / np.sqrt(D)
-            mask = np.arange(S)[None, :] > (pos0 + np.arange(L))[:, None]
-            s[mask] = -np.inf
-            p = np.exp(s - s.max(-1, keepdims=True))
-            p /= p.sum(-1, keepdims=True)
-            o[h] = p @ V[h // rep].astype(np.float64)
+            o[h] = attention_core(q[h], K[h // rep], V[h // rep], pos0, 1.0 / np.sqrt(D))
         o = round_bf16(o.astype(np.float32)).transpose(1, 0, 2).reshape(L, H * D)
         og = round_bf16(o * round_bf16(sigmoid(gate.reshape(L, H * D))))
         return qlinear(att.o_proj, og)
@@ -145,13 +177,7 @@ class OracleModel:
         z = proj[:, g.conv_dim:g.conv_dim + g.value_dim]
         b = proj[:, g.conv_dim + g.value_dim:g.conv_dim + g.value_dim + g.hv]
         a = proj[:, g.conv_dim + g.value_dim + g.hv:]
-        conv_in = np.concatenate([c["conv"], qkv], axis=0)
-        c["conv"] = conv_in[-(g.K - 1):].copy()
-        cw = _np(g.conv_w)                              # [C, K]
-        conv = np.zeros((S, g.conv_dim), np.float64)
-        for j in range(g.K):
-            conv += conv_in[j:j + S].astype(np.float64) * cw[:, j][None, :]
-        conv = round_bf16(conv.astype(np.float32))
+        conv, c["conv"] = conv1d_window(c["conv"], qkv, _np(g.conv_w))
         conv = round_bf16(conv * round_bf16(sigmoid(conv)))
         q = conv[:, :g.key_dim].reshape(1, S, g.hk, g.dk)
         k = conv[:, g.key_dim:2 * g.key_dim].reshape(1, S, g.hk, g.dk)
@@ -180,6 +206,27 @@ class OracleModel:
         d = self.gdn(l.mixer, n, c) if l.linear else self.attention(l.mixer, n, c)
         h = round_bf16(x + d)
         return round_bf16(h + self.mlp(l.mlp, rms_norm(h, _np(l.ln2), eps)))
+
+    def new_kv_cache(self):
+        cfg = self.cfg
+        return {"k": np.zeros((cfg.num_key_value_heads, 0, cfg.head_dim), np.float32),
+                "v": np.zeros((cfg.num_key_value_heads, 0, cfg.head_dim), np.float32)}
+
+    def mtp(self, head, hidden, next_ids, cache, last_only=True):
+        """The MTP head (engine/mtp.py:58-68): hidden [T, H] (main model,
+        pre-norm, bf16 values) and next_ids [T] -> (logits [1 or T, V], block
+        output x [T, H] before the final norm). x is what a chained draft step
+        takes as its hidden (k > 1 drafting). cache: new_kv_cache()."""
+        eps = self.cfg.rms_norm_eps
+        h = np.asarray(hidden, np.float32)
+        if head.hidden_mode == "post":
+            h = rms_norm(h, _np(self.m.norm), eps)
+        e = rms_norm(embed_rows(self.m.embed, next_ids), _np(head.norm_emb), eps)
+        hn = rms_norm(h, _np(head.norm_hid), eps)
+        x = qlinear(head.fc, np.concatenate([e, hn], axis=-1))
+        x = self.layer(head.layer, x, cache)
+        xo = x[-1:] if last_only else x
+        return qlinear(self.m.lm_head, rms_norm(xo, _np(head.norm_out), eps)), x
 
     def forward(self, ids, last_only=True):
         """ids [L] -> (logits [L or 1, V] fp32 of bf16 values, pre-norm hidden [L, H])."""

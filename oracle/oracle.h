@@ -47,11 +47,17 @@ void orc_spec_accept(const float* target, const float* draft, const int32_t* dra
                      int32_t* n_accept, int32_t* out_token, int S, int k, int V, int threads);
 
 /* The same with the target rows filtered as Sampler.scores (presence penalty
- * with `seen` [V] or NULL, top_k in 0..64, top_p; see spec.c). */
+ * with `seen` [V] or NULL, top_k (0 or >= V: off), top_p; see spec.c). */
 void orc_spec_accept_filtered(const float* target, const float* draft, const int32_t* draft_ids,
                               const float* u_accept, const float* u_sample, float inv_temp, const float* seen,
                               float presence_penalty, int top_k, float top_p, int32_t* n_accept,
                               int32_t* out_token, int S, int k, int V, int threads);
+
+/* Philox4x32-10 block (Salmon et al. 2011): out = philox(ctr, key). */
+void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+
+/* The sampler's uniforms of draw event `event` (see rng.c): n values in [0, 1). */
+void orc_philox_uniforms(uint64_t seed, uint64_t event, int n, float* out);
 
 /* exp used by the sampler on both sides (Cody-Waite reduction + Taylor, fmaf). */
 float orc_expf(float x);

@@ -28,22 +28,40 @@ static inline uint16_t f2bf(float f) {
   return (uint16_t)(u >> 16);
 }
 
-/* engine/kernels.py:121 (formula), experiments/native/qmv_spike.mm:118-124 (fp64 loop) */
+/* engine/kernels.py:121 (formula), experiments/native/qmv_spike.mm:118-124 (fp64 loop).
+ * Each weight row is dequantized once into fp64 and dotted with every x row in
+ * k order; rows are independent (OpenMP over n), so the result does not depend
+ * on the thread count. */
 void orc_qmv_w4g64_f64(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
                        const uint16_t* biases, double* y, int M, int N, int K) {
   const int KW = K / 8, G = K / 64;
-  for (int m = 0; m < M; ++m) {
+  double* xd = (double*)malloc(sizeof(double) * (size_t)M * K);
+  for (size_t i = 0; i < (size_t)M * K; ++i) xd[i] = (double)bf2f(x[i]);
+#pragma omp parallel
+  {
+    double* wrow = (double*)malloc(sizeof(double) * (size_t)K);
+#pragma omp for schedule(static)
     for (int n = 0; n < N; ++n) {
-      double acc = 0.0;
       for (int k = 0; k < K; ++k) {
         const uint32_t q = (w[(size_t)n * KW + k / 8] >> (4 * (k % 8))) & 0xFu;
         const double s = bf2f(scales[(size_t)n * G + k / 64]);
         const double b = bf2f(biases[(size_t)n * G + k / 64]);
-        acc += (s * (double)q + b) * (double)bf2f(x[(size_t)m * K + k]);
+        wrow[k] = s * (double)q + b;
       }
-      y[(size_t)m * N + n] = acc;
+      /* up to 8 x rows at a time: independent sums, each still in k order */
+      for (int m0 = 0; m0 < M; m0 += 8) {
+        const int mb = M - m0 < 8 ? M - m0 : 8;
+        double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int k = 0; k < K; ++k) {
+          const double wk = wrow[k];
+          for (int j = 0; j < mb; ++j) acc[j] += wk * xd[(size_t)(m0 + j) * K + k];
+        }
+        for (int j = 0; j < mb; ++j) y[(size_t)(m0 + j) * N + n] = acc[j];
+      }
     }
+    free(wrow);
   }
+  free(xd);
 }
 
 /* engine/kernels.py:146-172: per group d = sum q*x, acc += s*d + b*sum(x); fp32 */

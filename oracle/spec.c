@@ -31,6 +31,17 @@
  *   kept set: z >= cutoff; p(j) = exp(z_j - c_0) / S_p on the kept set with
  *     S_p = sum_{i: c_i > cutoff} exp(c_i - c_0) + n_eq * exp(cutoff - c_0),
  *     n_eq = number of tokens of the row with z == cutoff.
+ * Wide form (64 < top_k < V, or top-p with no top-k; top_k >= V means no
+ * top-k, engine/sampler.py:44-47): masses m(z) = trunc(exp(z - c_0) * 2^32)
+ * as uint64 (exact, order-free sums); v_k = the top_k-th largest z (with
+ * multiplicity); S_cand = sum of m over the top_k candidates (z > v_k, plus
+ * top_k - #(z > v_k) copies of m(v_k)), or over the whole row; cutoff = the
+ * smallest row value v >= v_k with M(> v) < top_p * S_cand in double, where
+ * M(> v) = sum of m over z > v (engine/sampler.py:47-50 with exact sums; v_k
+ * itself without top-p); S_p = sum of exp(z - c_0) over z >= cutoff in fp32,
+ * logical thread t of 1024 owning elements 4 (t + 1024 i) + e in (i, e) order,
+ * xor butterflies per 64-thread wave, then the 16 wave sums in order. The
+ * integer parts are computed here by sorting, not by the kernel's radix descent.
  * Draft rows (draft logits) are never filtered.
  *
  * Reduction order (shared with the kernel): a row is cut into parts of 8192;
@@ -162,6 +173,68 @@ static rowstat filtered_stats(const float* row, int V, float inv_temp, const pfi
   float S = 0.0f;
   for (int i = 0; i < n_gt; ++i) S = S + orc_expf(srt[i] - c0);
   S = S + (float)n_eq * orc_expf(cutoff - c0);
+  free(z);
+  free(srt);
+  rowstat r;
+  r.m = c0;
+  r.s = S;
+  r.cutoff = cutoff;
+  return r;
+}
+
+static inline uint64_t fx_mass(float z, float c0) { return (uint64_t)(orc_expf(z - c0) * 4294967296.0f); }
+
+#define WT 1024
+
+/* wide-form statistics of a target row (see the header): m = c_0, s = S_p, cutoff */
+static rowstat wide_stats(const float* row, int V, float inv_temp, const pfilt* f, int K, float top_p) {
+  float* z = (float*)malloc(sizeof(float) * (size_t)V);
+  for (int j = 0; j < V; ++j) z[j] = pen_logit(row, j, f) * inv_temp;
+  float* srt = (float*)malloc(sizeof(float) * (size_t)V);
+  memcpy(srt, z, sizeof(float) * (size_t)V);
+  qsort(srt, (size_t)V, sizeof(float), cmp_desc);
+  const float c0 = srt[0];
+  const float vk = K > 0 ? srt[K - 1] : -INFINITY;
+  float cutoff = vk;
+  if (top_p > 0.0f && top_p < 1.0f) {
+    uint64_t S = 0;
+    if (K > 0) {
+      int n_gt = 0;
+      while (srt[n_gt] > vk) S += fx_mass(srt[n_gt++], c0);
+      S += (uint64_t)(K - n_gt) * fx_mass(vk, c0);
+    } else {
+      for (int j = 0; j < V; ++j) S += fx_mass(srt[j], c0);
+    }
+    const double T = (double)top_p * (double)S;
+    /* walk the distinct values downwards; M = mass of the values above */
+    uint64_t M = 0;
+    int i = 0;
+    cutoff = srt[0];
+    while (i < V && srt[i] >= vk) {
+      const float v = srt[i];
+      if (!((double)M < T)) break;
+      cutoff = v;
+      while (i < V && srt[i] == v) M += fx_mass(srt[i++], c0);
+    }
+  }
+  /* S_p in the kernel's order */
+  float tsum[WT];
+  for (int t = 0; t < WT; ++t) {
+    float acc = 0.0f;
+    for (int j = 4 * t; j < V; j += 4 * WT)
+      for (int e = 0; e < 4; ++e) acc = acc + (z[j + e] >= cutoff ? orc_expf(z[j + e] - c0) : 0.0f);
+    tsum[t] = acc;
+  }
+  float S = 0.0f;
+  for (int w = 0; w < WT / 64; ++w) {
+    float v[64], nv[64];
+    for (int l = 0; l < 64; ++l) v[l] = tsum[w * 64 + l];
+    for (int o = 32; o >= 1; o >>= 1) {
+      for (int l = 0; l < 64; ++l) nv[l] = v[l] + v[l ^ o];
+      memcpy(v, nv, sizeof(v));
+    }
+    S = w == 0 ? v[0] : S + v[0];
+  }
   free(z);
   free(srt);
   rowstat r;
@@ -342,9 +415,14 @@ void orc_spec_accept_filtered(const float* target, const float* draft, const int
       if (n == k) tok = row_argmax(tgt + (size_t)k * V, V, &pf[k]);
     } else {
       rowstat rp[65], rq[64];
-      for (int i = 0; i <= k; ++i)
-        rp[i] = top_k > 0 ? filtered_stats(tgt + (size_t)i * V, V, inv_temp, &pf[i], top_k, top_p)
-                          : row_stats(tgt + (size_t)i * V, V, inv_temp, &pf[i]);
+      const int tk = (top_k > 0 && top_k < V) ? top_k : 0;
+      const int use_p = top_p > 0.0f && top_p < 1.0f;
+      for (int i = 0; i <= k; ++i) {
+        const float* ri = tgt + (size_t)i * V;
+        if (tk >= 1 && tk <= 64) rp[i] = filtered_stats(ri, V, inv_temp, &pf[i], tk, top_p);
+        else if (tk > 64 || use_p) rp[i] = wide_stats(ri, V, inv_temp, &pf[i], tk, top_p);
+        else rp[i] = row_stats(ri, V, inv_temp, &pf[i]);
+      }
       if (drf)
         for (int i = 0; i < k; ++i) rq[i] = row_stats(drf + (size_t)i * V, V, inv_temp, NULL);
       for (int i = 0; i < k; ++i) {

@@ -2,13 +2,50 @@
 // k + 1, accept, commit) can be captured once in a HIP graph and replayed with a
 // single host synchronisation. Every quantity that varies between cycles - the
 // accepted count, the drawn token, the pending (hidden, token) pairs of the MTP
-// head, the uniforms' position - lives in device memory read by these kernels.
+// head, the uniforms' draw counter - lives in device memory read by these kernels.
 //
 // Reference: the host-side bookkeeping of decode() (engine/speculative.py:82-102):
 // mx.eval + accept.item(), pend_h / pend_ids, feed.
+//
+// Uniforms: Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC 2011), a counter-based
+// generator, so a draw needs only (seed, draw counter) and the stream never
+// repeats or runs out: draw event c gives
+//   u(c, i) = (philox({c_lo, c_hi, i / 4, 0}, {seed_lo, seed_hi})[i % 4] >> 8) * 2^-24.
+// The reference draws from MLX's generator (engine/speculative.py:79-81).
 #include "qvex_common.h"
 
 namespace {
+
+__device__ __forceinline__ float philox_uniform(uint64_t seed, uint64_t event, int i) {
+  uint32_t c0 = (uint32_t)event, c1 = (uint32_t)(event >> 32), c2 = (uint32_t)(i >> 2), c3 = 0u;
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    if (r > 0) {
+      k0 += 0x9E3779B9u;
+      k1 += 0xBB67AE85u;
+    }
+    const uint32_t lo0 = 0xD2511F53u * c0, hi0 = __umulhi(0xD2511F53u, c0);
+    const uint32_t lo1 = 0xCD9E8D57u * c2, hi1 = __umulhi(0xCD9E8D57u, c2);
+    const uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+    c0 = n0;
+    c1 = lo1;
+    c2 = n2;
+    c3 = lo0;
+  }
+  const int w = i & 3;
+  const uint32_t x = w == 0 ? c0 : (w == 1 ? c1 : (w == 2 ? c2 : c3));
+  return (float)(x >> 8) * 0x1p-24f;
+}
+
+// out[i] = u(*counter, i) for i < n, then ++*counter
+__global__ void philox_uniforms_kernel(uint64_t seed, uint64_t* __restrict__ counter, int n, float* __restrict__ out) {
+  const uint64_t ev = *counter;
+  const int i = threadIdx.x;
+  if (i < n) out[i] = philox_uniform(seed, ev, i);
+  __syncthreads();                       // every thread has read the counter
+  if (i == 0) *counter = ev + 1;
+}
 
 __global__ void gather_row_kernel(const uint16_t* __restrict__ src, long row_stride, const int32_t* __restrict__ idx,
                                   int rows, uint16_t* __restrict__ dst, int H) {
@@ -46,22 +83,21 @@ __global__ void cycle_finish_kernel(const int32_t* __restrict__ drafts, int k, c
 // cycle_finish plus the rest of the cycle's bookkeeping in the same launch:
 // ids_next[0] = tok (the next verify's first id), main_counters[i] += n + main_extra
 // (the verify commit), mtp_counters[i] += mtp_delta (the draft steps' net
-// advance), and u_out = table[*u_counter % rows], ++*u_counter (the next
-// cycle's uniforms). Null pointers skip a part.
+// advance), and u_out[i] = u(*u_counter, i), ++*u_counter (the next cycle's
+// uniforms). Null pointers skip a part.
 __global__ void cycle_finish_ex_kernel(const int32_t* __restrict__ drafts, int k, const int32_t* __restrict__ n_ptr,
                                        const int32_t* __restrict__ tok_ptr, int32_t* __restrict__ pend_ids,
                                        int32_t* __restrict__ feed, int32_t* __restrict__ n_prev,
                                        int32_t* __restrict__ out, int32_t* __restrict__ ids_next,
                                        int32_t* __restrict__ main_counters, int n_main, int main_extra,
                                        int32_t* __restrict__ mtp_counters, int n_mtp, int mtp_delta,
-                                       const float* __restrict__ table, int rows, int width,
-                                       int32_t* __restrict__ u_counter, float* __restrict__ u_out) {
+                                       uint64_t u_seed, uint64_t* __restrict__ u_counter, int width,
+                                       float* __restrict__ u_out) {
   const int i = threadIdx.x;
   const int n = *n_ptr, tok = *tok_ptr;
   int32_t d = 0;
   if (i < k) d = drafts[i];
-  int r = 0;
-  if (u_counter) r = ((*u_counter % rows) + rows) % rows;
+  const uint64_t ev = u_counter ? *u_counter : 0;
   __syncthreads();                       // every read of ids / the counter before the writes below
   if (i <= k) pend_ids[i] = i < n ? (i < k ? d : 0) : (i == n ? tok : 0);
   if (i < k) out[2 + i] = d;
@@ -69,7 +105,7 @@ __global__ void cycle_finish_ex_kernel(const int32_t* __restrict__ drafts, int k
     for (int c = i; c < n_main; c += blockDim.x) main_counters[c] += n + main_extra;
   if (mtp_counters)
     for (int c = i; c < n_mtp; c += blockDim.x) mtp_counters[c] += mtp_delta;
-  if (u_out && i < width) u_out[i] = table[(long)r * width + i];
+  if (u_out && i < width) u_out[i] = philox_uniform(u_seed, ev, i);
   __syncthreads();
   if (i == 0) {
     *feed = tok;
@@ -77,18 +113,8 @@ __global__ void cycle_finish_ex_kernel(const int32_t* __restrict__ drafts, int k
     out[0] = n;
     out[1] = tok;
     if (ids_next) ids_next[0] = tok;
-    if (u_counter) *u_counter += 1;
+    if (u_counter) *u_counter = ev + 1;
   }
-}
-
-// out[0 .. width) = table[*counter % rows]; then ++*counter
-__global__ void next_uniforms_kernel(const float* __restrict__ table, int rows, int width, int32_t* __restrict__ counter,
-                                     float* __restrict__ out) {
-  const int r = ((*counter % rows) + rows) % rows;
-  const int i = threadIdx.x;
-  if (i < width) out[i] = table[(long)r * width + i];
-  __syncthreads();
-  if (i == 0) *counter += 1;
 }
 
 // seen[ids[q]] = 1 for q < min(max_ids, (n_ptr ? *n_ptr : 0) + n_offset); ids outside [0, V) skipped
@@ -138,27 +164,26 @@ extern "C" int qvex_cycle_finish(const int32_t* drafts, int k, const int32_t* n_
   return QVEX_OK;
 }
 
-extern "C" int qvex_next_uniforms(const float* table, int rows, int width, int32_t* counter, float* out,
-                                  void* stream) {
-  QVEX_CHECK_ARG(table && counter && out && rows >= 1 && width >= 1 && width <= 256, "qvex_next_uniforms: bad arguments");
-  hipLaunchKernelGGL(next_uniforms_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, table, rows, width, counter, out);
-  QVEX_CHECK_LAUNCH("qvex_next_uniforms");
+extern "C" int qvex_philox_uniforms(uint64_t seed, uint64_t* counter, int n, float* out, void* stream) {
+  QVEX_CHECK_ARG(counter && out && n >= 1 && n <= 256, "qvex_philox_uniforms: bad arguments (n=%d, 1..256)", n);
+  hipLaunchKernelGGL(philox_uniforms_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, seed, counter, n, out);
+  QVEX_CHECK_LAUNCH("qvex_philox_uniforms");
   return QVEX_OK;
 }
 
 extern "C" int qvex_cycle_finish_ex(const int32_t* drafts, int k, const int32_t* n_accept, const int32_t* token,
                                     int32_t* pend_ids, int32_t* feed, int32_t* n_prev, int32_t* out,
                                     int32_t* ids_next, int32_t* main_counters, int n_main, int main_extra,
-                                    int32_t* mtp_counters, int n_mtp, int mtp_delta, const float* u_table,
-                                    int u_rows, int u_width, int32_t* u_counter, float* u_out, void* stream) {
+                                    int32_t* mtp_counters, int n_mtp, int mtp_delta, uint64_t u_seed,
+                                    uint64_t* u_counter, int u_width, float* u_out, void* stream) {
   QVEX_CHECK_ARG(drafts && n_accept && token && pend_ids && feed && n_prev && out && k >= 1 && k < 255,
                  "qvex_cycle_finish_ex: bad arguments");
   QVEX_CHECK_ARG((!main_counters || n_main >= 0) && (!mtp_counters || n_mtp >= 0) &&
-                     (!u_out || (u_table && u_counter && u_rows >= 1 && u_width >= 1 && u_width <= 256)),
+                     (!u_out || (u_counter && u_width >= 1 && u_width <= 256)),
                  "qvex_cycle_finish_ex: bad counter or uniform arguments");
   hipLaunchKernelGGL(cycle_finish_ex_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, drafts, k, n_accept, token,
                      pend_ids, feed, n_prev, out, ids_next, main_counters, n_main, main_extra, mtp_counters, n_mtp,
-                     mtp_delta, u_table, u_rows, u_width, u_counter, u_out);
+                     mtp_delta, u_seed, u_counter, u_width, u_out);
   QVEX_CHECK_LAUNCH("qvex_cycle_finish_ex");
   return QVEX_OK;
 }

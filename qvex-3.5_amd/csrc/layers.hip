@@ -237,10 +237,12 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
   const float inv = rsqrtf(ss / (float)D + eps);
 #pragma unroll
   for (int i = 0; i < PER; ++i) x[i] = bf16_to_f32(f32_to_bf16(bf16_to_f32(wv[i]) * (x[i] * inv)));
-  // rotary part lives in element slot 0 (lane < 64 <= rot requires rot <= 64)
+  // rotary part lives in element slot 0 (lane < 64 <= rot requires rot <= 64);
+  // lane i < half pairs with lane i + half (an explicit index: an xor by half
+  // pairs the right lanes only when half is a power of two)
   const int half = rot / 2;
   if (rot > 0) {
-    const float partner = __shfl_xor(x[0], half, 64);
+    const float partner = __shfl(x[0], lane < half ? lane + half : lane - half, 64);
     if (lane < rot) {
       const int i = lane % half;
       const float inv_freq = powf(theta, -2.0f * (float)i / (float)rot);

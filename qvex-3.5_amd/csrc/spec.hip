@@ -32,13 +32,26 @@
 //
 // Filtering of the target rows (Sampler.scores, engine/sampler.py:30-52), when
 // asked for: presence penalty x - pen * s(j) with s(j) = 1 for `seen` tokens and,
-// in verify row i, for the drafts d_0..d_{i-1} before it; top-k (k <= 64) and
-// top-p over the k largest scaled values; everything outside z >= cutoff has
-// probability 0. Kernel 1 then also leaves each part's k largest values (taken
-// one block maximum at a time) and how many of its values equal the k-th; a
-// filter kernel (one block per verify row) merges them into the row's k largest,
-// applies top-p in order and counts the ties at the cutoff exactly, giving
-// (c_0, S_p, cutoff) for kernels 2 and 3, which only add the z >= cutoff test.
+// in verify row i, for the drafts d_0..d_{i-1} before it; top-k and top-p; every
+// token outside z >= cutoff has probability 0. Two forms give (c_0, S_p, cutoff)
+// per target row to kernels 2 and 3, which only add the z >= cutoff test:
+//   * list form (1 <= top_k <= 64, optional top-p over the top-k): kernel 1 also
+//     leaves each part's k largest values (taken one block maximum at a time) and
+//     how many of its values equal the k-th; a filter kernel (one block per
+//     verify row) merges them into the row's k largest, applies top-p in order
+//     and counts the ties at the cutoff exactly;
+//   * wide form (64 < top_k < V, or top-p over the whole vocabulary): one
+//     1024-thread block per verify row finds the k-th largest value exactly by a
+//     radix descent over order-preserving 32-bit keys (11/11/10-bit digits,
+//     counts), and the top-p cutoff by a second descent over fixed-point masses
+//     m(z) = trunc(exp(z - c_0) * 2^32) (uint64, so the sums are exact and
+//     order-free): cutoff = the smallest value v >= v_k with
+//     M(> v) < top_p * S_cand (M(> v) = sum of m over z > v; S_cand = the mass of
+//     the k candidates, the whole row without top-k), the cumulative rule of
+//     engine/sampler.py:47-50 on exact sums. S_p = sum of exp(z - c_0) over
+//     z >= cutoff in fp32, in a fixed order (thread t of 1024 owns elements
+//     4 (t + 1024 i) + e, summed in (i, e) order; xor butterflies per wave, then
+//     the 16 wave sums in wave order).
 #include "qvex_common.h"
 
 namespace {
@@ -108,11 +121,13 @@ struct SpecArgs {
   int S, k, V, P, rps;    // rps = rows per step
   const float* seen;      // [V] presence mask or nullptr
   float pen;              // presence penalty
-  int top_k;              // 0 = off
-  float top_p;            // top-p when 0 < top_p < 1 (needs top_k)
-  float* fws;             // [S * (k+1), P, top_k + 1] part lists + tie counts
+  int top_k;              // list form: 1..64; 0 = off (also in the wide form)
+  float top_p;            // top-p when 0 < top_p < 1
+  float* fws;             // [S * (k+1), P, top_k + 1] part lists + tie counts (list form)
   float* frow;            // [S * (k+1), 4] (c_0, S_p, cutoff)
   int bf;                 // logits are bf16 (widened exactly to fp32 on load)
+  int filt;               // 0: no filter, 1: list form, 2: wide form
+  int wide_k;             // wide form: top-k (0 = off)
 };
 
 __device__ __forceinline__ const void* row_ptr(const SpecArgs& a, int step, int i) {
@@ -320,7 +335,7 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
     out[0] = m;
     out[1] = s;
   }
-  if (tgt && a.top_k > 0) {
+  if (tgt && a.filt == 1) {
     // this part's top_k largest z and the count of its values equal to the k-th
     __shared__ float lst[64];
     __shared__ float wl[4 * 64];
@@ -435,6 +450,236 @@ __global__ __launch_bounds__(NT) void spec_filter_kernel(SpecArgs a) {
       fr[1] = S;
       fr[2] = cutoff;
     }
+  }
+}
+
+// ---------------------------------------------------------------- wide filter (top-k > 64, top-p over the vocabulary)
+
+constexpr int WT = 1024;        // threads of a wide-filter block
+constexpr int WB = 2048;        // buckets per radix level (11-bit digits)
+
+// order-preserving key: a < b as floats iff okey(a) < okey(b) (no NaN)
+__device__ __forceinline__ uint32_t okey(float z) {
+  const uint32_t u = __float_as_uint(z);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float okey_val(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+// fixed-point mass of a value: trunc(exp(z - c0) * 2^32), <= 2^32
+__device__ __forceinline__ uint64_t fx_mass(float z, float c0) {
+  return (uint64_t)(qx_expf(z - c0) * 4294967296.0f);
+}
+
+// The four values of thread t's group i (elements 4 (t + WT i) .. + 3) of a
+// target row as z = penalised logit * inv_temp.
+struct WRow {
+  const void* src;
+  int bf;
+  const float* seen;
+  float pen;
+  const int32_t* extra;
+  int n_extra;
+  float inv_temp;
+};
+
+__device__ __forceinline__ void wide_z4(const WRow& r, int j, float (&z)[4]) {
+  if (r.bf) {
+    const u32x2 v = *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint16_t*>(r.src) + j);
+    z[0] = bf16_lo(v.x);
+    z[1] = bf16_hi(v.x);
+    z[2] = bf16_lo(v.y);
+    z[3] = bf16_hi(v.y);
+  } else {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(r.src) + j);
+    z[0] = __uint_as_float(v.x);
+    z[1] = __uint_as_float(v.y);
+    z[2] = __uint_as_float(v.z);
+    z[3] = __uint_as_float(v.w);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) z[e] = pen_x(r.seen, r.pen, z[e], j + e, r.extra, r.n_extra) * r.inv_temp;
+}
+
+__device__ __forceinline__ uint64_t shfl_down_u64(uint64_t v, int o) {
+  const uint32_t lo = __shfl_down((uint32_t)v, o, 64), hi = __shfl_down((uint32_t)(v >> 32), o, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Exclusive suffix sum over the block's threads: sum of v over threads t' > t.
+__device__ __forceinline__ uint64_t block_suffix_excl(uint64_t v, uint64_t* sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint64_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t y = shfl_down_u64(x, o);
+    if (lane + o < 64) x += y;
+  }
+  __syncthreads();
+  if (lane == 0) sh[wave] = x;
+  __syncthreads();
+  uint64_t hi = 0;
+  for (int w = wave + 1; w < WT / 64; ++w) hi += sh[w];
+  return x - v + hi;
+}
+
+// One block per target row (grid S * (k + 1)): (c_0, S_p, cutoff) into frow.
+__global__ __launch_bounds__(WT) void spec_wide_filter_kernel(SpecArgs a) {
+  __shared__ unsigned long long hmass[WB];
+  __shared__ uint32_t hcnt[WB];
+  __shared__ uint64_t sh[WT / 64];
+  __shared__ float shf[WT / 64];
+  __shared__ int s_pick;
+  __shared__ uint64_t s_val;
+  const int row = blockIdx.x;                   // step * (k + 1) + i
+  const int step = row / (a.k + 1), i = row % (a.k + 1);
+  const int t = threadIdx.x;
+  WRow r;
+  r.src = row_ptr(a, step, i);
+  r.bf = a.bf;
+  r.seen = a.seen;
+  r.pen = a.pen;
+  r.extra = a.ids + (long)step * a.k;
+  r.n_extra = i;
+  r.inv_temp = a.inv_temp;
+  const int V = a.V;
+  // c_0: the maximum of the part maxima kernel 1 left (order-free)
+  const float* pw = a.ws + ((long)step * a.rps + i) * a.P * 2;
+  float c0 = -__builtin_inff();
+  for (int q = 0; q < a.P; ++q) c0 = fmaxf(c0, pw[2 * q]);
+
+  const int shifts[3] = {21, 10, 0};
+  const int widths[3] = {11, 11, 10};
+
+  // ---- k-th largest value (counts): after the descent kk is its key, n_gt the
+  // count of larger values and n_eq the count of values equal to it
+  uint32_t kk = 0;
+  uint32_t n_gt = 0, n_eq = 0;
+  const int K = a.wide_k;
+  if (K > 0) {
+    uint32_t prefix = 0, pmask = 0;
+    uint32_t need = (uint32_t)K;                // rank among the values matching the prefix
+    for (int lv = 0; lv < 3; ++lv) {
+      const int sft = shifts[lv];
+      const uint32_t dmask = (1u << widths[lv]) - 1u;
+      for (int b = t; b < WB; b += WT) hcnt[b] = 0;
+      __syncthreads();
+      for (int j = 4 * t; j < V; j += 4 * WT) {
+        float z[4];
+        wide_z4(r, j, z);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t key = okey(z[e]);
+          if ((key & pmask) == prefix) atomicAdd(&hcnt[(key >> sft) & dmask], 1u);
+        }
+      }
+      __syncthreads();
+      // thread t owns buckets 2t, 2t + 1; the bucket holding the need-th largest
+      const uint32_t c_lo = hcnt[2 * t], c_hi = hcnt[2 * t + 1];
+      const uint64_t above = block_suffix_excl((uint64_t)c_lo + c_hi, sh);
+      if (t == 0) s_pick = -1;
+      __syncthreads();
+      if (above < need && need <= above + c_hi) {
+        s_pick = 2 * t + 1;
+        s_val = above;
+      } else if (above + c_hi < need && need <= above + c_hi + c_lo) {
+        s_pick = 2 * t;
+        s_val = above + c_hi;
+      }
+      __syncthreads();
+      const int bsel = s_pick;
+      need -= (uint32_t)s_val;
+      prefix |= (uint32_t)bsel << sft;
+      pmask |= dmask << sft;
+      if (lv == 2) n_eq = hcnt[bsel];
+      __syncthreads();
+    }
+    kk = prefix;
+    n_gt = (uint32_t)K - need;
+  }
+  const float vk = K > 0 ? okey_val(kk) : -__builtin_inff();
+
+  // ---- top-p cutoff over the candidates (fixed-point masses, exact sums)
+  float cutoff = vk;
+  if (a.top_p > 0.0f && a.top_p < 1.0f) {
+    const uint32_t kmin = K > 0 ? kk : 0u;      // values below v_k are not candidates
+    uint32_t prefix = 0, pmask = 0;
+    uint64_t base = 0;                          // mass of candidates above the prefix's range
+    double T = 0.0;
+    for (int lv = 0; lv < 3; ++lv) {
+      const int sft = shifts[lv];
+      const uint32_t dmask = (1u << widths[lv]) - 1u;
+      for (int b = t; b < WB; b += WT) {
+        hmass[b] = 0;
+        hcnt[b] = 0;
+      }
+      __syncthreads();
+      for (int j = 4 * t; j < V; j += 4 * WT) {
+        float z[4];
+        wide_z4(r, j, z);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t key = okey(z[e]);
+          if (key >= kmin && (key & pmask) == prefix) {
+            const uint32_t b = (key >> sft) & dmask;
+            atomicAdd(&hmass[b], (unsigned long long)fx_mass(z[e], c0));
+            atomicAdd(&hcnt[b], 1u);
+          }
+        }
+      }
+      __syncthreads();
+      const uint64_t m_lo = hmass[2 * t], m_hi = hmass[2 * t + 1];
+      const uint64_t above = block_suffix_excl(m_lo + m_hi, sh);
+      if (lv == 0) {
+        // S_cand: every candidate is in this level's histogram; with top-k the
+        // values equal to v_k count only up to the k candidates
+        uint64_t total = above + m_lo + m_hi;   // thread 0 holds the whole sum
+        if (t == 0) s_val = total;
+        __syncthreads();
+        total = s_val;
+        if (K > 0) {
+          const uint64_t mk = fx_mass(vk, c0);
+          total = total - (uint64_t)n_eq * mk + (uint64_t)(K - n_gt) * mk;
+        }
+        T = (double)a.top_p * (double)total;
+        __syncthreads();
+      }
+      // lowest non-empty bucket whose largest value still has M(> v) < T
+      if (t == 0) s_pick = 0x7fffffff;
+      __syncthreads();
+      if (hcnt[2 * t] && (double)(base + above + m_hi) < T) atomicMin(&s_pick, 2 * t);
+      else if (hcnt[2 * t + 1] && (double)(base + above) < T) atomicMin(&s_pick, 2 * t + 1);
+      __syncthreads();
+      const int bsel = s_pick;
+      if (bsel == 2 * t) s_val = above + m_hi;
+      if (bsel == 2 * t + 1) s_val = above;
+      __syncthreads();
+      base += s_val;
+      prefix |= (uint32_t)bsel << sft;
+      pmask |= dmask << sft;
+      __syncthreads();
+    }
+    cutoff = okey_val(prefix);
+  }
+
+  // ---- S_p = sum of exp(z - c0) over z >= cutoff, fixed order
+  float acc = 0.0f;
+  for (int j = 4 * t; j < V; j += 4 * WT) {
+    float z[4];
+    wide_z4(r, j, z);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc = acc + (z[e] >= cutoff ? qx_expf(z[e] - c0) : 0.0f);
+  }
+  acc = wave_bfly_sum(acc);
+  if ((t & 63) == 0) shf[t >> 6] = acc;
+  __syncthreads();
+  if (t == 0) {
+    float S = shf[0];
+    for (int w = 1; w < WT / 64; ++w) S = S + shf[w];
+    float* fr = a.frow + (long)row * 4;
+    fr[0] = c0;
+    fr[1] = S;
+    fr[2] = cutoff;
   }
 }
 
@@ -583,7 +828,7 @@ __global__ __launch_bounds__(NT) void spec_decide_kernel(SpecArgs a) {
     for (int r = wave; r < a.rps; r += NT / 64) {
       const float* w = a.ws + ((long)step * a.rps + r) * a.P * 2;
       float cut = -__builtin_inff(), mr = 0.0f, sr = 0.0f;
-      if (!a.greedy && a.top_k > 0 && r <= k) {
+      if (!a.greedy && a.filt != 0 && r <= k) {
         const float* fr = a.frow + ((long)step * (k + 1) + r) * 4;
         mr = fr[0];
         sr = fr[1];
@@ -892,9 +1137,11 @@ uint64_t ws_floats(int S, int rps, int P) {
   return (uint64_t)S * rps * P * 2 + (uint64_t)S * P * NT + (uint64_t)S * P + (uint64_t)S * 8;
 }
 
+// list-form part lists (1 <= top_k <= 64) and the per-row (c_0, S_p, cutoff),
+// which every filtered call needs (the wide form keeps no lists)
 uint64_t filter_floats(int S, int k, int P, int top_k) {
-  if (top_k <= 0) return 0;
-  return (uint64_t)S * (k + 1) * P * (top_k + 1) + (uint64_t)S * (k + 1) * 4;
+  const uint64_t lists = (top_k >= 1 && top_k <= 64) ? (uint64_t)S * (k + 1) * P * (top_k + 1) : 0;
+  return lists + (uint64_t)S * (k + 1) * 4;
 }
 
 extern "C" uint64_t qvex_spec_accept_filtered_workspace_bytes(int S, int k, int V, int has_draft, int top_k) {
@@ -920,19 +1167,19 @@ static int spec_accept_impl(const void* target, const void* draft, int bf, const
                  "qvex_spec_accept: logits must be 16-byte aligned");
   const int greedy = !(inv_temp > 0.0f);
   QVEX_CHECK_ARG(greedy || u_sample, "qvex_spec_accept: u_sample required when sampling");
-  QVEX_CHECK_ARG(top_k >= 0 && top_k <= 64 && top_k <= V, "qvex_spec_accept: top_k=%d must be in 0..64 (and <= V)",
-                 top_k);
+  QVEX_CHECK_ARG(top_k >= 0, "qvex_spec_accept: top_k=%d must be >= 0", top_k);
   QVEX_CHECK_ARG(presence_penalty == presence_penalty, "qvex_spec_accept: presence_penalty is NaN");
+  QVEX_CHECK_ARG(top_p == top_p, "qvex_spec_accept: top_p is NaN");
   const bool use_p = top_p > 0.0f && top_p < 1.0f;
-  if (!greedy && use_p && top_k == 0)
-    return qvex::fail(QVEX_ENOTSUP, "qvex_spec_accept: top-p over the whole vocabulary (top_k = 0) is not "
-                                    "implemented; give top_k in 1..64");
   const int P = nparts(V);
-  const int kf = greedy ? 0 : top_k;           // greedy scores are not filtered
+  // engine/sampler.py:44-47: top-k only when 0 < top_k < V; greedy scores are not filtered
+  const int tk = (top_k > 0 && top_k < V) ? top_k : 0;
+  const int filt = greedy ? 0 : (tk >= 1 && tk <= 64 ? 1 : ((tk > 64 || use_p) ? 2 : 0));
+  const int kf = filt == 1 ? tk : 0;           // list-form top-k
   QVEX_CHECK_ARG(kf == 0 || P * kf <= 64 * 64, "qvex_spec_accept: V=%d too large for top_k=%d", V, kf);
   const int rps = (k + 1) + (draft ? k : 0);
   const uint64_t base = ws_floats(S, rps, P);
-  const uint64_t need = (base + filter_floats(S, k, P, kf)) * sizeof(float);
+  const uint64_t need = (base + (filt ? filter_floats(S, k, P, kf) : 0)) * sizeof(float);
   QVEX_CHECK_ARG(workspace_bytes >= need, "qvex_spec_accept: workspace %llu bytes < %llu needed",
                  (unsigned long long)workspace_bytes, (unsigned long long)need);
   const size_t lds = ((size_t)P * NT + P + 2 * rps) * sizeof(float);
@@ -940,18 +1187,22 @@ static int spec_accept_impl(const void* target, const void* draft, int bf, const
   QVEX_CHECK_ARG((long)S * rps <= 65535, "qvex_spec_accept: S*rows=%ld exceeds the grid limit", (long)S * rps);
   QVEX_CHECK_ARG(rps <= 80, "qvex_spec_accept: k=%d too large", k);
   float* fws = (float*)workspace + base;
-  float* frow = fws + (uint64_t)S * (k + 1) * P * (kf + 1);
+  float* frow = fws + (kf > 0 ? (uint64_t)S * (k + 1) * P * (kf + 1) : 0);
   SpecArgs a{target, draft, draft_ids, u_accept, u_sample, inv_temp, greedy, n_accept, out_token,
-             (float*)workspace, S, k, V, P, rps, seen, presence_penalty, kf, top_p, fws, frow, bf};
+             (float*)workspace, S, k, V, P, rps, seen, presence_penalty, kf, use_p ? top_p : 1.0f, fws, frow, bf,
+             filt, filt == 2 ? tk : 0};
   hipStream_t st = (hipStream_t)stream;
   if (a.bf)
     hipLaunchKernelGGL(spec_rowstats_kernel<true>, dim3(P, S * rps), dim3(NT), 0, st, a);
   else
     hipLaunchKernelGGL(spec_rowstats_kernel<false>, dim3(P, S * rps), dim3(NT), 0, st, a);
   QVEX_CHECK_LAUNCH("qvex_spec_accept/rowstats");
-  if (kf > 0) {
+  if (filt == 1) {
     hipLaunchKernelGGL(spec_filter_kernel, dim3(S * (k + 1)), dim3(NT), 0, st, a);
     QVEX_CHECK_LAUNCH("qvex_spec_accept/filter");
+  } else if (filt == 2) {
+    hipLaunchKernelGGL(spec_wide_filter_kernel, dim3(S * (k + 1)), dim3(WT), 0, st, a);
+    QVEX_CHECK_LAUNCH("qvex_spec_accept/wide_filter");
   }
   hipLaunchKernelGGL(spec_decide_kernel, dim3(P, S), dim3(NT), 0, st, a);
   QVEX_CHECK_LAUNCH("qvex_spec_accept/decide");

@@ -51,9 +51,9 @@ SIGNATURES: dict[str, list] = {
     "qvex_commit_step": [P, I, P, I, P],
     "qvex_gather_row": [P, LNG, P, I, P, I, P],
     "qvex_assemble_ids": [P, P, I, P, P],
-    "qvex_cycle_finish_ex": [P, I, P, P, P, P, P, P, P, P, I, I, P, I, I, P, I, I, P, P, P],
+    "qvex_cycle_finish_ex": [P, I, P, P, P, P, P, P, P, P, I, I, P, I, I, U64, P, I, P, P],
     "qvex_cycle_finish": [P, I, P, P, P, P, P, P, P],
-    "qvex_next_uniforms": [P, I, I, P, P, P],
+    "qvex_philox_uniforms": [U64, P, I, P, P],
     "qvex_gated_rmsnorm": [P, P, LNG, I, P, P, I, I, F, P],
     "qvex_swiglu": [P, P, I, I, P],
     "qvex_bf16_to_f32": [P, P, LNG, P],

@@ -43,6 +43,27 @@ def mtp_policy(mode: str, mtp: MTPHead | None):
     return lambda: on
 
 
+def prefill(model: Qwen35, ids, cache, mtp: MTPHead | None = None, mtp_cache=None, last_hidden=None,
+            chunk: int | None = None):
+    """Run a prompt through the model in chunks (engine/engine.py:232-248) and,
+    with an MTP cache, hand each chunk's (hidden, next token) pairs to the MTP
+    head as it goes (mtp_prefill with the previous chunk's last hidden), so the
+    head's attention workspace stays at one chunk's size. ids: [1, L] or [L].
+    Returns (logits of the last token [1, 1, V], last hidden [1, 1, H] or the
+    given last_hidden without an MTP cache)."""
+    ids = torch.as_tensor(ids, dtype=torch.int32).reshape(1, -1).to(model.norm.device)
+    step = chunk or model.prefill_chunk
+    logits = None
+    for i in range(0, ids.shape[1], step):
+        part = ids[:, i:i + step]
+        if mtp_cache is not None:
+            logits, hidden = model(part, cache, return_hidden=True)
+            last_hidden = mtp_prefill(mtp, mtp_cache, hidden, part, last_hidden)
+        else:
+            logits = model(part, cache)
+    return logits, last_hidden
+
+
 def generate(model: Qwen35, prompt_ids, params: SamplingParams, mtp: MTPHead | None = None,
              mtp_mode: str = "auto", k: int = 3, stop_ids=(), forced: list[int] | None = None,
              max_tokens: int | None = None) -> GenerateResult:
@@ -62,10 +83,14 @@ def generate(model: Qwen35, prompt_ids, params: SamplingParams, mtp: MTPHead | N
     stop = set(int(t) for t in stop_ids)
 
     t_start = time.perf_counter()
-    cache = model.make_cache()
-    mcache = mtp.make_cache() if mtp is not None else None
-    logits, hidden = model(ids, cache, return_hidden=True)
-    last_h = mtp_prefill(mtp, mcache, hidden, ids, None) if mtp is not None else None
+    # room for the prompt, every emitted token and the draft/verify tokens past
+    # the last one (the reference's caches grow, engine/model.py:156-170; these
+    # are sized up front)
+    need = ids.shape[1] + limit + 2 * k + 2
+    cap = max(model.max_context, need)
+    cache = model.make_cache(max_context=cap)
+    mcache = mtp.make_cache(max_context=cap) if mtp is not None else None
+    logits, last_h = prefill(model, ids, cache, mtp, mcache)
     sampler = Sampler(params, model.cfg.vocab_size)
     spec: dict = {}
     tokens = decode(model, sampler, cache, logits[0, -1], last_h, mtp, mcache, use_mtp, spec, forced, k)

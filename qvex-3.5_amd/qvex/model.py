@@ -346,17 +346,26 @@ class CacheCounters:
         self.dev = torch.zeros(n, dtype=torch.int32, device=device)
         self.dirty = False
         # in graph mode the device table is authoritative (advanced by captured
-        # commit kernels) and the host mirror is kept by the replaying code
+        # commit kernels) and the host mirror is kept by the replaying code;
+        # host edits are then refused except while a graph is being captured
         self.graph_mode = False
+        self.capturing = False
+
+    def _check_host_edit(self) -> None:
+        if self.graph_mode and not self.capturing:
+            raise _C.QvexError("these caches are driven by a captured cycle (GraphedMTPCycle); release() it "
+                               "before eager calls, rollbacks or offset edits")
 
     def get(self, i: int) -> int:
         return int(self.host[i])
 
     def set(self, i: int, v: int) -> None:
+        self._check_host_edit()
         self.host[i] = v
         self.dirty = True
 
     def sync(self) -> None:
+        self._check_host_edit()
         if self.graph_mode:
             return
         if self.dirty:
@@ -367,6 +376,14 @@ class CacheCounters:
 
     def ptr(self, i: int) -> int:
         return self.dev.data_ptr() + 4 * i
+
+    def clone(self) -> "CacheCounters":
+        self._check_host_edit()
+        c = CacheCounters(len(self.host), self.dev.device)
+        c.host[:] = self.host
+        c.dev.copy_(self.dev)
+        c.dirty = self.dirty
+        return c
 
 
 class KVCache:
@@ -399,6 +416,15 @@ class KVCache:
 
     def rollback(self, n=1):
         self.offset -= n  # entries past offset are overwritten by the next append
+
+    def clone(self, counters: CacheCounters | None = None) -> "KVCache":
+        """A copy of the cache (device tensors copied); counters: the cloned table
+        it indexes (a new one-entry table for a standalone cache)."""
+        c = KVCache.__new__(KVCache)
+        c.counters = counters if counters is not None else self.counters.clone()
+        c.index, c.capacity = self.index, self.capacity
+        c.k, c.v = self.k.clone(), self.v.clone()
+        return c
 
 
 class RecurrentCache:
@@ -439,10 +465,18 @@ class RecurrentCache:
         return [self.conv_ring, self.ssm_ring]
 
     def rollback(self, n=1):
+        self.counters._check_host_edit()
         if n > self.last_width:
             raise _C.QvexError(f"RecurrentCache.rollback({n}): only the last {self.last_width} tokens are kept")
         self.offset -= n
         self.last_width -= n
+
+    def clone(self, counters: CacheCounters) -> "RecurrentCache":
+        c = RecurrentCache.__new__(RecurrentCache)
+        c.__dict__.update(self.__dict__)
+        c.counters = counters
+        c.conv_ring, c.ssm_ring = self.conv_ring.clone(), self.ssm_ring.clone()
+        return c
 
 
 class LayerCaches(list):
@@ -451,6 +485,11 @@ class LayerCaches(list):
     def __init__(self, items, counters):
         super().__init__(items)
         self.counters = counters
+
+    def clone(self) -> "LayerCaches":
+        """A deep copy (device tensors and counters): a prefix to branch from."""
+        counters = self.counters.clone()
+        return LayerCaches([c.clone(counters) for c in self], counters)
 
 
 # ---------------------------------------------------------------- layers
@@ -483,6 +522,11 @@ class Attention:
         L = x.shape[0]
         cfg = self.cfg
         H, Hkv, D = self.n_heads, self.n_kv, self.head_dim
+        if not cache.counters.graph_mode and cache.offset + L > cache.capacity:
+            # the kernels would drop the writes past the capacity; the reference
+            # grows its cache (engine/model.py:156-170), this one is sized up front
+            raise _C.QvexError(f"KV cache full: offset {cache.offset} + {L} tokens > capacity {cache.capacity} "
+                               "(make the cache with a larger max_context)")
         proj = self.qkv_proj(x)                                   # [L, H*2D + 2*Hkv*D]
         q = torch.empty((L, H, D), dtype=torch.bfloat16, device=x.device)
         pos = cache.counters.ptr(cache.index)

@@ -2,13 +2,23 @@
 
 The fused kernel (qvex_spec_accept_filtered) scores the target rows as
 Sampler.scores does (presence penalty, temperature, top-k, top-p over the top-k
-candidates), then runs the speculative accept test, residual resampling and
-plain sampling in one place. Top-p over the whole vocabulary (top_k = 0 or
->= V with top_p < 1) and top_k > 64 are not implemented and raise. Uniforms
-come from a host PCG64 stream seeded by SamplingParams.seed (the reference
-draws them from MLX's generator, engine/speculative.py:79-80), so a run is
-reproducible given the seed. The presence mask lives on the device and is
+candidates or, with top_k = 0 or >= V, over the whole vocabulary), then runs
+the speculative accept test, residual resampling and plain sampling in one
+place.
+
+Uniforms come from a counter-based Philox4x32-10 stream on the device
+(qvex_philox_uniforms): the sampler's seed (SamplingParams.seed, or fresh
+entropy when None, as the reference seeds MLX's generator only when given one,
+engine/sampler.py:25-26) and one device draw counter, advanced once per draw.
+The reference draws from MLX's generator (engine/speculative.py:79-81). Draws
+need no host work, so a captured cycle draws the same stream as eager calls,
+for any number of cycles. The presence mask lives on the device and is
 updated by observe().
+
+API as engine/sampler.py: scores(logits, extra_seen) -> full-vocabulary scores,
+pick(scores) -> argmax (greedy) or a categorical draw from the scores. The
+decode path uses pick_logits(logits), which applies the same filtering inside
+the sampling kernel (no score vector is made).
 """
 
 from __future__ import annotations
@@ -32,23 +42,18 @@ class SamplingParams:
 
 
 class Sampler:
-    TOP_K_MAX = 64
-
     def __init__(self, params: SamplingParams, vocab_size: int):
         self.p = params
         self.V = vocab_size
+        # engine/sampler.py:44-50: top-k when 0 < top_k < V, top-p when 0 < top_p < 1
         tk = params.top_k if 0 < params.top_k < vocab_size else 0
         tp = params.top_p if 0 < params.top_p < 1 else 1.0
-        if params.temperature > 0:
-            if tp < 1.0 and tk == 0:
-                raise NotImplementedError("top-p over the whole vocabulary (top_k = 0 or >= vocab) is not "
-                                          "implemented; give 1 <= top_k <= %d" % self.TOP_K_MAX)
-            if tk > self.TOP_K_MAX:
-                raise NotImplementedError("top_k > %d is not implemented (got %d)" % (self.TOP_K_MAX, tk))
         self.top_k = tk if params.temperature > 0 else 0
         self.top_p = tp
         self.seen = None            # device fp32 [V] presence mask, made on first use
-        self.rng = np.random.Generator(np.random.PCG64(params.seed if params.seed is not None else 0))
+        seed = params.seed if params.seed is not None else np.random.SeedSequence().entropy
+        self.seed = int(seed) & (2**64 - 1)
+        self.u_counter = None       # device uint64 draw counter (int64 storage), made on first use
         self._ws = {}
 
     @property
@@ -61,10 +66,11 @@ class Sampler:
         return dict(seen=self.seen if self.p.presence_penalty else None,
                     presence_penalty=float(self.p.presence_penalty), top_k=self.top_k, top_p=self.top_p)
 
-    def _workspace(self, S, k, has_draft, device):
-        key = (S, k, has_draft, self.top_k)
+    def _workspace(self, S, k, has_draft, device, top_k=None):
+        tk = self.top_k if top_k is None else top_k
+        key = (S, k, has_draft, tk)
         if key not in self._ws:
-            self._ws[key] = kernels.spec_workspace(S, k, self.V, has_draft, device, self.top_k)
+            self._ws[key] = kernels.spec_workspace(S, k, self.V, has_draft, device, tk)
         return self._ws[key]
 
     def scores(self, logits: torch.Tensor, extra_seen=None) -> torch.Tensor:
@@ -89,8 +95,25 @@ class Sampler:
         z = torch.where(z >= cutoff, z, torch.full_like(z, float("-inf")))
         return z - torch.logsumexp(z, 0)
 
+    def counter(self, device) -> torch.Tensor:
+        """The device draw counter (one uint64 in an int64 tensor)."""
+        if self.u_counter is None:
+            self.u_counter = torch.zeros(1, dtype=torch.int64, device=device)
+        return self.u_counter
+
+    def draw_into(self, out: torch.Tensor) -> torch.Tensor:
+        """One draw event: out (device fp32, 1..256 values) = the next uniforms."""
+        if out.dtype != torch.float32 or not out.is_contiguous() or not 1 <= out.numel() <= 256:
+            raise _C.QvexError("draw_into: out must be a contiguous fp32 tensor of 1..256 values")
+        _C.call("qvex_philox_uniforms", self.seed, self.counter(out.device).data_ptr(), out.numel(),
+                out.data_ptr(), kernels._stream())
+        return out
+
     def _uniforms(self, n: int, device) -> torch.Tensor:
-        return torch.from_numpy(self.rng.random(n, dtype=np.float32)).to(device)
+        u = torch.empty(n, dtype=torch.float32, device=device)
+        for i in range(0, n, 256):
+            self.draw_into(u[i:i + 256])
+        return u
 
     def accept(self, target: torch.Tensor, draft_ids: torch.Tensor, draft_logits: torch.Tensor | None = None):
         """target [k+1, V] logits of the verify rows, draft_ids [k] -> device int32
@@ -114,8 +137,22 @@ class Sampler:
                                    self.p.temperature, workspace=self._workspace(1, k, False, t.device),
                                    **self._filter(t.device))
 
-    def pick(self, logits: torch.Tensor) -> torch.Tensor:
-        """One token per row of logits [R, V] (argmax when greedy) -> int32 [R]."""
+    def pick(self, scores: torch.Tensor) -> torch.Tensor:
+        """One token per row of scores [R, V] as made by scores() (engine/sampler.py:
+        57-58): argmax when greedy, else a categorical draw with probabilities
+        proportional to exp(scores) -> int32 [R] on the device."""
+        t = to_f32(scores).reshape(-1, 1, self.V)
+        R = t.shape[0]
+        empty_i = torch.empty((R, 0), dtype=torch.int32, device=t.device)
+        empty_f = torch.empty((R, 0), dtype=torch.float32, device=t.device)
+        _, tok = kernels.spec_accept(t, None, empty_i, empty_f, self._uniforms(R, t.device),
+                                     0.0 if self.greedy else 1.0, workspace=self._workspace(R, 0, False, t.device,
+                                                                                            top_k=0))
+        return tok
+
+    def pick_logits(self, logits: torch.Tensor) -> torch.Tensor:
+        """pick(scores(logits)) in one kernel pass: one token per row of logits
+        [R, V] (penalty, temperature and filters applied inside) -> int32 [R]."""
         t = as_logits(logits).reshape(-1, 1, self.V)
         R = t.shape[0]
         empty_i = torch.empty((R, 0), dtype=torch.int32, device=t.device)

@@ -15,7 +15,6 @@ from __future__ import annotations
 
 from typing import Callable
 
-import numpy as np
 import torch
 
 from . import _C
@@ -87,7 +86,7 @@ class MTPDecoder:
         self.stats = stats if stats is not None else {}
         for key in ("cycles", "accepted", "plain", "emitted"):
             self.stats.setdefault(key, 0)
-        self.feed = sampler.pick(first_logits.reshape(1, -1))        # int32 [1] on the device
+        self.feed = sampler.pick_logits(first_logits.reshape(1, -1))  # int32 [1] on the device
         sampler.observe(self.feed)
         self.pend_h = [last_hidden] if mtp is not None else []
         self.pend_ids = [self.feed.reshape(1, 1)] if mtp is not None else []
@@ -97,8 +96,14 @@ class MTPDecoder:
     def can_speculate(self) -> bool:
         return self.mtp is not None and bool(self.pend_h)
 
+    def _eager(self) -> None:
+        if self.cache.counters.graph_mode or (self.mtp_cache is not None and self.mtp_cache.counters.graph_mode):
+            raise _C.QvexError("this decoder's caches are driven by a GraphedMTPCycle; call its release() "
+                               "before eager steps")
+
     def cycle(self) -> list[int]:
         """One MTP cycle; returns the emitted tokens (n accepted drafts + 1)."""
+        self._eager()
         k, model, sampler, cache = self.k, self.model, self.sampler, self.cache
         h_in = self.pend_h[0] if len(self.pend_h) == 1 else torch.cat(self.pend_h, dim=1)
         id_in = self.pend_ids[0] if len(self.pend_ids) == 1 else torch.cat(self.pend_ids, dim=1)
@@ -124,6 +129,7 @@ class MTPDecoder:
 
     def plain(self, forced_token: int | None = None) -> int:
         """One non-speculative step (engine/speculative.py:103-118)."""
+        self._eager()
         model, dev = self.model, self.model.norm.device
         if self.mtp is not None:
             logits, hidden = model(self.feed.reshape(1, 1), self.cache, return_hidden=True)
@@ -132,7 +138,7 @@ class MTPDecoder:
         if forced_token is not None:
             t = torch.tensor([forced_token], dtype=torch.int32, device=dev)
         else:
-            t = self.sampler.pick(logits[0, -1:])
+            t = self.sampler.pick_logits(logits[0, -1:])
         self.sampler.observe(t)
         self.stats["plain"] += 1
         if self.mtp is not None:
@@ -169,14 +175,20 @@ class GraphedMTPCycle:
     Everything that changes between cycles is device state: the pending
     (hidden, token) pairs of the MTP head (k + 1 fixed rows, the first n_prev + 1
     valid), the feed token, the cache counters (advanced by captured commit
-    kernels) and the uniforms (a pre-drawn table read through a device index).
+    kernels) and the sampler's uniform draw counter (Philox, advanced by the
+    finishing kernel, so the stream is the eager one for any number of cycles).
     The MTP head's first step always runs k + 1 rows and keeps row n_prev on the
     device; rows past it write KV entries beyond the committed position, which
     later cycles overwrite. One replay = one cycle; the host reads
     [n, token, drafts] once and updates its counter mirrors.
+
+    While the object drives the decoder's caches their device counters are
+    authoritative: eager model calls, rollbacks and MTPDecoder steps on them
+    raise until release() hands the state back. A cycle that could write past a
+    KV cache's capacity raises before it is launched.
     """
 
-    def __init__(self, dec: MTPDecoder, table_rows: int = 8192):
+    def __init__(self, dec: MTPDecoder):
         if dec.mtp is None or not dec.pend_h:
             raise _C.QvexError("GraphedMTPCycle needs an MTPDecoder with an MTP head and pending pairs")
         self.dec = dec
@@ -203,12 +215,10 @@ class GraphedMTPCycle:
         self.drafts = self.ids[0, 1:]
         self.out = torch.zeros(2 + k, dtype=torch.int32, device=dev)
         self.zero = torch.zeros(1, dtype=torch.int32, device=dev)
-        self.u_table = torch.from_numpy(dec.sampler.rng.random((table_rows, k + 1), dtype=np.float32)).to(dev)
-        self.u_idx = torch.zeros(1, dtype=torch.int32, device=dev)
         self.u_buf = torch.empty(k + 1, dtype=torch.float32, device=dev)
         # the first cycle's uniforms; each replay draws the next cycle's at its end
-        _C.call("qvex_next_uniforms", _ptr(self.u_table), self.u_table.shape[0], k + 1, _ptr(self.u_idx),
-                _ptr(self.u_buf), _stream())
+        dec.sampler.draw_into(self.u_buf)
+        self.released = False
         # device counters must hold the host values before they become authoritative
         cache.counters.sync()
         mc.counters.sync()
@@ -226,8 +236,12 @@ class GraphedMTPCycle:
         host_mtp = d.mtp_cache.counters.host.copy()
         widths = [getattr(c, "last_width", None) for c in d.cache]
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, pool=pool):
-            self._body(out)
+        d.cache.counters.capturing = d.mtp_cache.counters.capturing = True
+        try:
+            with torch.cuda.graph(g, pool=pool):
+                self._body(out)
+        finally:
+            d.cache.counters.capturing = d.mtp_cache.counters.capturing = False
         d.cache.counters.host[:] = host_main
         d.mtp_cache.counters.host[:] = host_mtp
         for c, w in zip(d.cache, widths):
@@ -260,11 +274,30 @@ class GraphedMTPCycle:
                 _ptr(self.feed), _ptr(self.n_prev), _ptr(out), _ptr(self.ids),
                 d.cache.counters.dev.data_ptr(), d.cache.counters.dev.numel(), 1,
                 mc.counters.dev.data_ptr(), mc.counters.dev.numel(), -(k - 2) if k > 1 else 0,
-                _ptr(self.u_table), self.u_table.shape[0], k + 1, _ptr(self.u_idx), _ptr(self.u_buf), _stream())
+                d.sampler.seed, d.sampler.counter(self.u_buf.device).data_ptr(), k + 1, _ptr(self.u_buf), _stream())
         d.sampler.observe_result(out)
+
+    def _check_room(self, in_flight: int = 0) -> None:
+        """Raise unless the next cycle (after `in_flight` launched, unaccounted
+        cycles of at most k + 1 tokens each) fits every KV cache: the verify writes
+        k + 1 positions from the main offset, the draft steps k + 1 and then k - 1
+        rows from the MTP offset."""
+        if self.released:
+            raise _C.QvexError("GraphedMTPCycle was released")
+        k, d = self.k, self.dec
+        ahead = in_flight * (k + 1)
+        for c in d.cache:
+            cap = getattr(c, "capacity", None)
+            if cap is not None and c.offset + ahead + k + 1 > cap:
+                raise _C.QvexError(f"KV cache full: offset {c.offset} + {ahead + k + 1} > capacity {cap} "
+                                   "(make the cache with a larger max_context)")
+        mc = d.mtp_cache
+        if mc.offset + ahead + self.n_prev_host + 1 + 2 * k > mc.capacity:
+            raise _C.QvexError(f"MTP KV cache full: offset {mc.offset} > capacity {mc.capacity} - {2 * k + 1}")
 
     def cycle(self) -> list[int]:
         """Replay one cycle; returns the emitted tokens (n accepted drafts + 1)."""
+        self._check_room()
         self.graph.replay()
         return self._account(self.out.tolist())        # the one host sync
 
@@ -284,24 +317,50 @@ class GraphedMTPCycle:
         res = []
         if n <= 0:
             return res
+        self._check_room()
         graphs[0].replay()
         evs[0].record()
         for c in range(n):
             s = c % 2
             if c + 1 < n:
+                self._check_room(in_flight=1)
                 graphs[1 - s].replay()
                 evs[1 - s].record()
             evs[s].synchronize()
             res.append(self._account(ring[s].tolist()))
         return res
 
+    def release(self) -> MTPDecoder:
+        """Hand the state back to the MTPDecoder (device counters, feed, pending
+        pairs) so eager cycle()/plain() steps, model calls and rollbacks work
+        again; this object cannot replay afterwards. Returns the decoder."""
+        if self.released:
+            return self.dec
+        torch.cuda.synchronize()
+        d = self.dec
+        for counters in (d.cache.counters, d.mtp_cache.counters):
+            counters.host[:] = counters.dev.cpu().numpy()
+            counters.graph_mode = False
+            counters.dirty = False
+        # the last replay drew the next cycle's uniforms; give that draw back so
+        # the next eager draw takes the same event
+        d.sampler.counter(self.u_buf.device).sub_(1)
+        P = self.n_prev_host + 1
+        d.pend_h = [self.pend_h[:, :P].clone()]
+        d.pend_ids = [self.pend_ids[:, :P].clone()]
+        d.feed = self.feed.clone()
+        self.released = True
+        return d
+
     def _account(self, vals) -> list[int]:
         """Host mirrors and stats of one finished cycle from its [n, token, drafts]."""
         n, tok = int(vals[0]), int(vals[1])
         d = self.dec
+        d.cache.counters.host += n + 1
         for c in d.cache:
-            c.offset += n + 1
-        d.mtp_cache.offset += self.n_prev_host + 1
+            if hasattr(c, "last_width"):
+                c.last_width = n + 1          # the verify's k + 1 snapshots, k - n rolled back
+        d.mtp_cache.counters.host[d.mtp_cache.index] += self.n_prev_host + 1
         self.n_prev_host = n
         d.cache.counters.dirty = False
         d.mtp_cache.counters.dirty = False

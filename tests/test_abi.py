@@ -101,12 +101,15 @@ def test_packed_swiglu_rejects_odd_halves():
 def test_spec_filter_argument_rules():
     buf = ctypes.create_string_buffer(1 << 20)
     p16 = (ctypes.addressof(buf) + 15) // 16 * 16
-    with pytest.raises(_C.QvexError, match="whole vocabulary"):
-        _C.call("qvex_spec_accept_filtered", p16, None, p16, p16, p16, 1.0, None, 0.0, 0, 0.9, p16, p16,
-                1, 1, 4096, p16, 1 << 19, None)
     with pytest.raises(_C.QvexError, match="top_k"):
-        _C.call("qvex_spec_accept_filtered", p16, None, p16, p16, p16, 1.0, None, 0.0, 65, 0.9, p16, p16,
+        _C.call("qvex_spec_accept_filtered", p16, None, p16, p16, p16, 1.0, None, 0.0, -1, 0.9, p16, p16,
                 1, 1, 4096, p16, 1 << 19, None)
+    with pytest.raises(_C.QvexError, match="top_p is NaN"):
+        _C.call("qvex_spec_accept_filtered", p16, None, p16, p16, p16, 1.0, None, 0.0, 0, float("nan"), p16, p16,
+                1, 1, 4096, p16, 1 << 19, None)
+    with pytest.raises(_C.QvexError, match="workspace"):       # the wide form needs its row records
+        _C.call("qvex_spec_accept_filtered", p16, None, p16, p16, p16, 1.0, None, 0.0, 0, 0.9, p16, p16,
+                1, 1, 4096, p16, 8, None)
     lib = _C.lib()
     assert lib.qvex_spec_accept_filtered_workspace_bytes(1, 1, 8192, 0, 20) > \
         lib.qvex_spec_accept_filtered_workspace_bytes(1, 1, 8192, 0, 0) == lib.qvex_spec_accept_workspace_bytes(1, 1, 8192, 0)

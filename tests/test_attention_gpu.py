@@ -1,6 +1,7 @@
 """Verify attention kernel (qvex_attention) vs a float64 causal GQA softmax
-attention times sigmoid(gate) (GPU). Tolerance: 2e-2 absolute on outputs of
-order 1 (bf16 P and output rounding)."""
+attention times sigmoid(gate) (GPU). Tolerance: 1.5e-2 absolute on outputs of
+order 1 (bf16 P and output rounding; 7.7e-3 is the largest error measured on
+MI355X)."""
 
 import numpy as np
 import pytest
@@ -60,4 +61,4 @@ def test_attention_matches_reference(L, Hq, Hkv, D, pos0, kps, spare):
     got = tof(out).reshape(L, Hq, D)
     err = np.abs(got - ref).max()
     print(f"max abs err {err:.4f}")
-    assert err < 2e-2
+    assert err < 1.5e-2

@@ -18,8 +18,10 @@ import oracle
 from qvex import kernels, synth
 from test_gdn_gpu import bf, dev_inputs, f32, to_np_bf16
 
-Y_TOL = 2e-2
-S_TOL = 2e-2
+# about twice the largest errors measured on MI355X (y 6.8e-3 at T = 200, state
+# 5.1e-3 at T = 65)
+Y_TOL = 1.4e-2
+S_TOL = 1e-2
 
 
 def rel(got, ref):

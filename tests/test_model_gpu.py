@@ -1,8 +1,9 @@
 """Verify forward, rollback and MTP decode on a small random-init model (GPU).
 
 Forward parity vs the numpy restatement of engine/model.py (oracle/model.py):
-logits within 0.15 absolute (unit-scale logits, bf16 rounding points of the
-fused kernels differ from the reference's per-op roundings). Rollback and
+logits within two bf16 steps at the largest |logit| (logit_tol; the bf16
+rounding points of the fused kernels differ from the reference's per-op
+roundings, and one step is what is measured). Rollback and
 speculative-vs-plain checks are bit-exact: every kernel computes a row the
 same way whatever the number of rows in the call.
 """
@@ -18,7 +19,6 @@ from qvex.sampler import Sampler, SamplingParams
 from qvex.speculative import decode, mtp_prefill
 
 DEV = "cuda:0"
-LOGIT_TOL = 0.15
 
 
 @pytest.fixture(scope="module")
@@ -27,6 +27,13 @@ def tiny():
     cfg = Config.tiny(layers=4, vocab=4096)
     m = random_model(cfg, seed=7, device=DEV, max_context=1024, max_width=8)
     return m
+
+
+def logit_tol(ref) -> float:
+    """Two bf16 steps at the largest |logit| of the compared rows: the logits
+    leave every path rounded to bf16, and the errors measured on MI355X are one
+    such step (0.0625 at the tiny model's logits, 0.125 at the 9B width)."""
+    return 2.0 * 2.0 ** (np.floor(np.log2(np.abs(ref).max())) - 7)
 
 
 def prompt(n, V, seed=3):
@@ -48,13 +55,13 @@ def test_prefill_and_verify_match_oracle(tiny):
     d = np.abs(f32(logits[0]) - ol).max()
     dh = np.abs(f32(hidden[0]) - oh).max() / (np.abs(oh).max() + 1e-6)
     print(f"prefill: max|dlogit|={d:.4f} rel|dhidden|={dh:.4f} argmax {int(f32(logits[0]).argmax())} vs {int(ol.argmax())}")
-    assert d < LOGIT_TOL
+    assert d <= logit_tol(ol)
     ver = prompt(4, V, seed=5)
     logits4 = tiny(torch.from_numpy(ver).reshape(1, -1), cache, last_only=False)
     ol4, _ = orc.forward(ver, last_only=False)
     d4 = np.abs(f32(logits4[0]) - ol4).max()
     print(f"verify: max|dlogit|={d4:.4f}")
-    assert d4 < LOGIT_TOL
+    assert d4 <= logit_tol(ol4)
 
 
 @pytest.mark.gpu

@@ -46,7 +46,10 @@ def bonus_law(logits, T, n=8192, **kw):
 
 
 @pytest.mark.parametrize("top_k,top_p,penalty", [(8, 1.0, 0.0), (8, 0.8, 0.0), (20, 0.95, 1.3), (1, 1.0, 0.0),
-                                                 (5, 0.5, 2.0), (64, 0.9, 0.7)])
+                                                 (5, 0.5, 2.0), (64, 0.9, 0.7),
+                                                 # wide form: top-k > 64, top-p over the whole vocabulary
+                                                 (80, 1.0, 0.0), (70, 0.8, 0.7), (0, 0.9, 0.0), (0, 0.5, 1.3),
+                                                 (96, 0.8, 0.0), (500, 0.95, 0.0)])
 def test_filtered_law_matches_reference_scores(top_k, top_p, penalty):
     g = np.random.default_rng(top_k * 10 + int(top_p * 100))
     V, T = 96, 0.7
@@ -58,20 +61,39 @@ def test_filtered_law_matches_reference_scores(top_k, top_p, penalty):
     assert set(np.flatnonzero(law)) <= set(np.flatnonzero(p > 0))
 
 
-def test_ties_at_the_cutoff_are_all_kept():
-    """bf16-like logits with many exact ties: every token equal to the k-th value stays."""
+@pytest.mark.parametrize("top_k,top_p", [(10, 1.0), (70, 1.0), (70, 0.9), (0, 0.6)])
+def test_ties_at_the_cutoff_are_all_kept(top_k, top_p):
+    """bf16-like logits with many exact ties: every token equal to the cutoff
+    value stays (list form for top_k <= 64, wide form otherwise)."""
     g = np.random.default_rng(7)
     V, T = 400, 1.0
     logits = np.round(g.standard_normal(V) * 2.0).astype(np.float32)   # integers: heavy ties
-    p = np.exp(ref_scores(logits, T, top_k=10))
+    p = np.exp(ref_scores(logits, T, top_k=top_k, top_p=top_p))
     kept = p > 0
-    assert kept.sum() > 10            # the tie really extends past k
-    law = bonus_law(logits, T, n=1 << 15, top_k=10)
+    if top_k:
+        assert kept.sum() > top_k     # the tie really extends past k
+    law = bonus_law(logits, T, n=1 << 15, top_k=top_k, top_p=top_p)
     np.testing.assert_allclose(law, p, atol=1e-3)
     assert set(np.flatnonzero(law)) == set(np.flatnonzero(kept))
 
 
-@pytest.mark.parametrize("top_k,top_p", [(6, 1.0), (12, 0.7)])
+def test_wide_cutoff_is_the_cumulative_rule():
+    """Whole-vocabulary top-p on a row with known masses: values 3, 2, 1, 0 with
+    multiplicities 1, 2, 4, 8 at T = 1 / ln 2 (masses 8, 2 x 4, 4 x 2, 8 x 1 of 32).
+    Mass above 2 is 8/32 = 0.25, above 1 is 16/32, above 0 is 24/32: top_p = 0.5
+    keeps {3, 2} (0.5 is not < 0.5), 0.51 keeps down to 1, 0.76 everything."""
+    vals = np.array([3.0] + [2.0] * 2 + [1.0] * 4 + [0.0] * 8 + [-60.0] * 1, np.float32)
+    V = vals.size
+    perm = np.random.default_rng(3).permutation(V)
+    logits = vals[perm]
+    inv_t = float(np.log(2.0))
+    for top_p, lowest in ((0.25, 3.0), (0.26, 2.0), (0.5, 2.0), (0.51, 1.0), (0.75, 1.0), (0.76, 0.0)):
+        law = bonus_law(logits, 1.0 / inv_t, n=4096, top_k=0, top_p=top_p)
+        kept = set(np.flatnonzero(law))
+        assert kept == set(np.flatnonzero(logits >= lowest)), (top_p, lowest)
+
+
+@pytest.mark.parametrize("top_k,top_p", [(6, 1.0), (12, 0.7), (0, 0.7), (30, 0.8)])
 def test_filtered_accept_probability(top_k, top_p):
     """One-hot draft d: P(accept) = p(d) of the filtered target; a filtered-out d is
     never accepted, and the first emitted token still follows p."""

@@ -27,10 +27,16 @@ def test_scores_mirror_reference(T, top_k, top_p, pen):
     np.testing.assert_allclose(got[fin], ref[fin], rtol=1e-5, atol=1e-5)
 
 
-def test_unsupported_filters_raise():
-    with pytest.raises(NotImplementedError, match="whole vocabulary"):
-        Sampler(SamplingParams(temperature=0.7, top_k=0, top_p=0.9), 1000)
-    with pytest.raises(NotImplementedError, match="top_k > 64"):
-        Sampler(SamplingParams(temperature=0.7, top_k=100, top_p=0.9), 1000)
-    Sampler(SamplingParams(temperature=0.0, top_k=0, top_p=0.9), 1000)        # greedy ignores the filters
-    Sampler(SamplingParams(), 248320)                                         # the reference's defaults
+def test_filter_settings_follow_the_reference():
+    """engine/sampler.py:44-50: top-k when 0 < top_k < V (top_k >= V or 0 means the
+    whole vocabulary is the candidate set), top-p when 0 < top_p < 1; greedy
+    sampling ignores both."""
+    s = Sampler(SamplingParams(temperature=0.7, top_k=0, top_p=0.9), 1000)
+    assert (s.top_k, s.top_p) == (0, 0.9)
+    s = Sampler(SamplingParams(temperature=0.7, top_k=100, top_p=0.9), 1000)
+    assert (s.top_k, s.top_p) == (100, 0.9)
+    s = Sampler(SamplingParams(temperature=0.7, top_k=1000, top_p=1.0), 1000)
+    assert (s.top_k, s.top_p) == (0, 1.0)
+    assert Sampler(SamplingParams(temperature=0.0, top_k=20, top_p=0.9), 1000).top_k == 0
+    s = Sampler(SamplingParams(), 248320)                                     # the reference's defaults
+    assert (s.top_k, s.top_p) == (20, 0.95)

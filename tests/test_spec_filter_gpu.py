@@ -52,6 +52,12 @@ CASES = [
     (8, 3, 30000, 0.7, 20, 0.9, 0.8, False, True),         # draft logits (q unfiltered)
     (24, 0, 248320, 0.7, 20, 0.95, 0.3, True, False),      # plain sampling (k = 0)
     (6, 3, 248320, 0.8, 64, 0.9, 0.0, True, False),        # 31 x 64 candidates: the 16-slot merge
+    # wide form: top-p over the whole vocabulary, top-k > 64
+    (12, 3, 248320, 0.7, 0, 0.9, 0.0, False, False),       # whole-vocabulary top-p
+    (8, 3, 248320, 0.6, 200, 0.95, 1.2, True, False),      # top-k 200 + top-p + penalty, bf16 ties
+    (8, 2, 248320, 1.0, 1000, 1.0, 0.0, True, False),      # top-k only, 1000 candidates
+    (6, 3, 50000, 0.7, 0, 0.5, 0.5, False, True),          # tight whole-vocabulary p, draft logits
+    (16, 4, 20000, 0.7, 20000, 0.8, 0.0, False, False),    # top_k = V: no top-k (the reference's rule)
 ]
 
 
