@@ -274,10 +274,12 @@ int qvex_spec_accept(const float* target, const float* draft, const int32_t* dra
 /* The same with the target rows filtered as Sampler.scores
  * (engine/sampler.py:30-52): presence penalty x - penalty * s(j), s(j) = 1 for
  * the tokens of `seen` (fp32 [V], 0/1, or NULL) and, in verify row i, for the
- * drafts d_0..d_{i-1}; when sampling, top-k (1..64; 0 = off) and top-p
- * (0 < top_p < 1, applied over the top-k values; top-p without top-k is not
- * implemented and returns QVEX_ENOTSUP). Greedy scores are only penalised.
- * Draft logits, when given, are not filtered. Ties at the cutoff are all kept.
+ * drafts d_0..d_{i-1}; when sampling, top-k (0 < top_k < V; 0 or >= V = off)
+ * and top-p (0 < top_p < 1, over the top-k values or, without top-k, over the
+ * whole vocabulary: engine/sampler.py:44-50). top_k <= 64 merges per-part lists;
+ * larger top_k and whole-vocabulary top-p find the cutoff by exact radix
+ * descents (csrc/spec.hip). Greedy scores are only penalised. Draft logits,
+ * when given, are not filtered. Ties at the cutoff are all kept.
  * workspace: qvex_spec_accept_filtered_workspace_bytes(S, k, V, has_draft, top_k). */
 uint64_t qvex_spec_accept_filtered_workspace_bytes(int S, int k, int V, int has_draft, int top_k);
 int qvex_spec_accept_filtered(const float* target, const float* draft, const int32_t* draft_ids,
