@@ -298,6 +298,25 @@ int qvex_spec_accept_filtered_bf16(const uint16_t* target, const uint16_t* draft
                                    int32_t* n_accept, int32_t* out_token, int S, int k, int V,
                                    void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* qvex_spec_accept_filtered_bf16 without a workspace argument and without any
+ * allocation: the workspace is a static device array of QVEX_SPEC_SCRATCH_BYTES
+ * (4 MiB) per GPU, held until the process ends, whose address is looked up
+ * once per device on the first call there. No counterpart in the reference:
+ * this is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation). Calls whose
+ * qvex_spec_accept_filtered_workspace_bytes(S, k, V, draft != NULL, top_k)
+ * exceeds the array return QVEX_EINVAL (a verify step of the 9B vocabulary
+ * needs < 100 KB). Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU (different streams, threads) race and must be ordered
+ * by the caller. Results equal qvex_spec_accept_filtered_bf16's bit for bit. */
+#define QVEX_SPEC_SCRATCH_BYTES (4u << 20)
+int qvex_spec_accept_filtered_bf16_noalloc(const uint16_t* target, const uint16_t* draft,
+                                           const int32_t* draft_ids, const float* u_accept,
+                                           const float* u_sample, float inv_temp, const float* seen,
+                                           float presence_penalty, int top_k, float top_p,
+                                           int32_t* n_accept, int32_t* out_token, int S, int k, int V,
+                                           void* stream);
+
 /* ------------------------------------------------------------------------
  * Verify-forward glue (Qwen3.5 hybrid stack, engine/model.py). bf16 storage,
  * fp32 arithmetic, one bf16 rounding per output.

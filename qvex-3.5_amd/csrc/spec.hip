@@ -54,6 +54,13 @@
 //     the 16 wave sums in wave order).
 #include "qvex_common.h"
 
+#include <mutex>
+
+// Workspace of qvex_spec_accept_filtered_bf16_noalloc: one array per GPU, at
+// an address looked up once per device (the name is a host-side stand-in, not
+// a device address).
+static __device__ __align__(256) unsigned char scratch[QVEX_SPEC_SCRATCH_BYTES];
+
 namespace {
 
 constexpr int PART = 8192;
@@ -1238,4 +1245,46 @@ extern "C" int qvex_spec_accept(const float* target, const float* draft, const i
                                 void* workspace, uint64_t workspace_bytes, void* stream) {
   return qvex_spec_accept_filtered(target, draft, draft_ids, u_accept, u_sample, inv_temp, nullptr, 0.0f, 0, 1.0f,
                                    n_accept, out_token, S, k, V, workspace, workspace_bytes, stream);
+}
+
+// Device address of `scratch` on the current device, looked up on the first
+// call there (hipGetSymbolAddress with that device current); nullptr on error.
+static void* scratch_ptr(int* err_dev) {
+  static std::mutex mu;
+  static void* ptrs[64] = {nullptr};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    *err_dev = dev;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+      *err_dev = dev;
+      return nullptr;
+    }
+    ptrs[dev] = p;
+  }
+  return ptrs[dev];
+}
+
+extern "C" int qvex_spec_accept_filtered_bf16_noalloc(const uint16_t* target, const uint16_t* draft,
+                                                      const int32_t* draft_ids, const float* u_accept,
+                                                      const float* u_sample, float inv_temp, const float* seen,
+                                                      float presence_penalty, int top_k, float top_p,
+                                                      int32_t* n_accept, int32_t* out_token, int S, int k, int V,
+                                                      void* stream) {
+  QVEX_CHECK_ARG(S >= 1 && k >= 0 && V >= 1 && top_k >= 0, "qvex_spec_accept_noalloc: S=%d k=%d V=%d top_k=%d", S, k,
+                 V, top_k);
+  const uint64_t need = qvex_spec_accept_filtered_workspace_bytes(S, k, V, draft != nullptr, top_k);
+  QVEX_CHECK_ARG(need <= QVEX_SPEC_SCRATCH_BYTES,
+                 "qvex_spec_accept_noalloc: S=%d k=%d V=%d top_k=%d need %llu workspace bytes, more than the %u-byte "
+                 "static scratch; use qvex_spec_accept_filtered_bf16 with a workspace",
+                 S, k, V, top_k, (unsigned long long)need, (unsigned)QVEX_SPEC_SCRATCH_BYTES);
+  int dev = -1;
+  void* ws = scratch_ptr(&dev);
+  if (!ws) return qvex::fail(QVEX_EHIP, "qvex_spec_accept_noalloc: no scratch address on device %d", dev);
+  return spec_accept_impl(target, draft, 1, draft_ids, u_accept, u_sample, inv_temp, seen, presence_penalty, top_k,
+                          top_p, n_accept, out_token, S, k, V, ws, QVEX_SPEC_SCRATCH_BYTES, stream);
 }

@@ -42,6 +42,7 @@ SIGNATURES: dict[str, list] = {
     "qvex_spec_accept": [P, P, P, P, P, F, P, P, I, I, I, P, U64, P],
     "qvex_spec_accept_filtered": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P, U64, P],
     "qvex_spec_accept_filtered_bf16": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P, U64, P],
+    "qvex_spec_accept_filtered_bf16_noalloc": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P],
     "qvex_mark_seen": [P, I, P, I, P, I, P],
     "qvex_embed_w4g64": [P, I, P, P, P, I, I, P, P],
     "qvex_rmsnorm": [P, LNG, P, P, LNG, I, I, F, F, P],
