@@ -470,6 +470,20 @@ int qvex_read_roof(const void* buf, uint64_t bytes, uint32_t* sink, int blocks,
 int qvex_w4g64_dequant(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int N, int K,
                        uint16_t* out, void* stream);
 
+/* Prefill products from the packed copy: y[M, N] = x[M, K] @ W^T for prompt
+ * chunks (mx.quantized_matmul in QLinear.__call__, engine/model.py:87-91, on
+ * the 512-token chunks of engine/engine.py:232-248). x bf16 [M, K] row-major
+ * (16-byte aligned), packed from qvex_w4g64_pack, y bf16 [M, N]. Each weight is
+ * dequantized in registers to bf16(s * q + b) (as qvex_w4g64_dequant) and the
+ * products accumulate in fp32 on the matrix cores; any M >= 1, K % 256 == 0. */
+int qvex_w4g64_packed_gemm(const uint16_t* x, const void* packed, uint16_t* y, int M, int N, int K,
+                           void* stream);
+/* The same on a weight packed by qvex_w4g64_pack_swiglu (fused [gate; up], N
+ * rows): y [M, N/2] = bf16(silu(g) * u) with g and u the bf16-rounded products
+ * (MLP.__call__'s _swiglu, engine/model.py:133-135, 300-302). N % 16 == 0. */
+int qvex_w4g64_packed_gemm_swiglu(const uint16_t* x, const void* packed, uint16_t* y, int M, int N, int K,
+                                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,6 +25,8 @@ SIGNATURES: dict[str, list] = {
     "qvex_qmv_w4g64_mfma": [P, P, P, P, P, I, I, I, I, I, P],
     "qvex_w4g64_pack": [P, P, P, I, I, P, U64, P],
     "qvex_w4g64_dequant": [P, P, P, I, I, P, P],
+    "qvex_w4g64_packed_gemm": [P, P, P, I, I, I, P],
+    "qvex_w4g64_packed_gemm_swiglu": [P, P, P, I, I, I, P],
     "qvex_qmv_w4g64_packed": [P, P, P, I, I, I, P],
     "qvex_qmv_w4g64_packed_tiled": [P, P, P, I, I, I, I, I, I, P],
     "qvex_qmv_w4g64_packed_resid": [P, P, I, I, I, P, P, P, P, P, P],

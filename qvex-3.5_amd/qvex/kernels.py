@@ -119,6 +119,31 @@ def dequant_w4(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, out:
     return out
 
 
+def packed_gemm(x: torch.Tensor, packed: torch.Tensor, N: int, out: torch.Tensor | None = None,
+                swiglu: bool = False) -> torch.Tensor:
+    """Prefill product y = x @ dequant(W)^T of any number of rows from pack_w4's
+    copy (qvex_w4g64_packed_gemm): weights dequantized in registers to bf16,
+    fp32 accumulation on MFMA. swiglu=True (a swiglu-packed [gate; up] weight):
+    y [M, N/2] = silu(gate) * up."""
+    _check(x, "x", torch.bfloat16)
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    M = x2.shape[0]
+    if packed.dtype != torch.uint8 or not packed.is_contiguous() or packed.device != x.device:
+        raise _C.QvexError("packed must be a contiguous uint8 tensor on the device of x")
+    if packed.numel() != int(_C.lib().qvex_w4g64_packed_bytes(N, K)):
+        raise _C.QvexError(f"packed has {packed.numel()} bytes, not the size of an N={N} K={K} pack")
+    No = N // 2 if swiglu else N
+    if out is None:
+        out = torch.empty((M, No), dtype=torch.bfloat16, device=x.device)
+    _check(out, "out", torch.bfloat16)
+    if out.numel() != M * No:
+        raise _C.QvexError(f"out must hold M x {No} = {M * No} values")
+    _C.call("qvex_w4g64_packed_gemm_swiglu" if swiglu else "qvex_w4g64_packed_gemm", _ptr(x2), _ptr(packed),
+            _ptr(out), M, N, K, _stream())
+    return out
+
+
 def quantized_matmul_packed(x: torch.Tensor, packed: torch.Tensor, N: int, out: torch.Tensor | None = None,
                             tile: tuple[int, ...] | None = None, swiglu: bool = False) -> torch.Tensor:
     """y = x @ dequant(W)^T from pack_w4's copy, x bf16 [..., K] with 1..4 rows

@@ -130,8 +130,10 @@ def load_model(model_dir: str | Path, device="cuda", max_context: int = 8192, ma
         raise _C.QvexError(f"{e}: only 4-bit group-64 embeddings are implemented (got {bits}/{gs})")
     embed = QEmbedding(sh.get(f"{e}.weight", device), _bf16(sh, f"{e}.scales", device),
                        _bf16(sh, f"{e}.biases", device), gs, bits)
-    return Qwen35(cfg, embed, layers, _bf16(sh, "model.norm.weight", device), qlin("lm_head"),
-                  max_context=max_context, max_width=max_width)
+    model = Qwen35(cfg, embed, layers, _bf16(sh, "model.norm.weight", device), qlin("lm_head"),
+                   max_context=max_context, max_width=max_width)
+    model.offload_mlx()          # one device copy of each weight: the packed one
+    return model
 
 
 def load_mtp(model: Qwen35, path: str | Path, hidden_mode: str = "pre"):
@@ -160,4 +162,6 @@ def load_mtp(model: Qwen35, path: str | Path, hidden_mode: str = "pre"):
                  "q_norm": _bf16(sh, f"{sa}.q_norm.weight", dev), "k_norm": _bf16(sh, f"{sa}.k_norm.weight", dev)},
         "mlp": {n: qlin(f"{mlp}.{n}") for n in ("gate_proj", "up_proj", "down_proj")},
     }
-    return MTPHead(model, w, gs, bits, hidden_mode)
+    head = MTPHead(model, w, gs, bits, hidden_mode)
+    head.offload_mlx()
+    return head

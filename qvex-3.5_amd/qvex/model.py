@@ -124,13 +124,12 @@ class QLinear:
     up to 3 drafts - through the MFMA kernel on it; the row bits of that kernel
     do not depend on the number of rows. Calls of 5..DENSE_MIN_ROWS-1 rows
     (verify of more drafts, short prefill tails) run it on chunks of 4 rows, so
-    their rows have the same bits too; longer calls dequantize once and use a
-    library GEMM. Without a packed copy (K not a multiple of 256) the MLX-layout
-    kernel takes chunks of 8 rows."""
+    their rows have the same bits too; longer calls (prefill) run the packed
+    MFMA GEMM (weights dequantized to bf16 in registers). Without a packed copy
+    (K not a multiple of 256) the MLX-layout kernel takes chunks of 8 rows."""
 
     PACKED_MAX_ROWS = 4
-    # calls of at least this many rows (prefill) dequantize the weight to bf16
-    # and run a library GEMM; 0 disables it
+    # calls of at least this many rows (prefill) run the packed GEMM; 0 disables it
     DENSE_MIN_ROWS = 16
 
     def __init__(self, w, scales, biases, group_size=64, bits=4, pack: bool = True, swiglu: bool = False):
@@ -150,7 +149,22 @@ class QLinear:
     def repack(self) -> None:
         """Rebuild the packed copy after the MLX-layout tensors were edited in place."""
         if self.packed is not None:
-            self.packed = kernels.pack_w4(self.w, self.scales, self.biases, swiglu=self.swiglu_packed)
+            w, s, b = self._mlx_on(self.packed.device)
+            self.packed = kernels.pack_w4(w, s, b, swiglu=self.swiglu_packed)
+
+    def offload_mlx(self) -> None:
+        """Keep the MLX-layout triplet in host memory once the packed copy exists:
+        every device path of a packed layer reads the packed copy, so the
+        weight is resident on the GPU once (the host copy serves repack() and
+        the plain product of a gate/up-interleaved weight)."""
+        if self.packed is not None and self.w.is_cuda:
+            self.w, self.scales, self.biases = self.w.cpu(), self.scales.cpu(), self.biases.cpu()
+
+    def _mlx_on(self, device):
+        """The MLX-layout triplet on `device` (a transient copy when offloaded)."""
+        if self.w.device == torch.device(device):
+            return self.w, self.scales, self.biases
+        return self.w.to(device), self.scales.to(device), self.biases.to(device)
 
     def _takes_normed(self, x, M: int) -> bool:
         return self.packed is not None and M <= self.PACKED_MAX_ROWS and NormedRows.supported(self.K)
@@ -171,6 +185,8 @@ class QLinear:
         M, I = x2.shape[0], self.N // 2
         if self.swiglu_packed and self.packed is not None and M <= self.PACKED_MAX_ROWS:
             return kernels.quantized_matmul_packed(x2, self.packed, self.N, swiglu=True)
+        if self.swiglu_packed and self.packed is not None and self.DENSE_MIN_ROWS and M >= self.DENSE_MIN_ROWS:
+            return kernels.packed_gemm(x2.contiguous(), self.packed, self.N, swiglu=True)
         if self.swiglu_packed and self._packed_chunks(M):
             h = torch.empty((M, I), dtype=torch.bfloat16, device=x.device)
             for m0 in range(0, M, self.PACKED_MAX_ROWS):
@@ -204,15 +220,15 @@ class QLinear:
                 m1 = min(M, m0 + self.PACKED_MAX_ROWS)
                 kernels.quantized_matmul_packed(x2[m0:m1], self.packed, self.N, out=o2[m0:m1])
             return out.view(*lead, self.N)
-        if self.DENSE_MIN_ROWS and M >= self.DENSE_MIN_ROWS:
-            # long (prefill) call: the weight dequantized once to bf16, then a
-            # plain 2-D library GEMM (fp32 accumulation) instead of M / 8 GEMVs
-            wd = kernels.dequant_w4(self.w, self.scales, self.biases)
-            torch.mm(x2, wd.t(), out=o2)
+        if self.packed is not None and not self.swiglu_packed and self.DENSE_MIN_ROWS and \
+                M >= self.DENSE_MIN_ROWS:
+            # long (prefill) call: the packed MFMA GEMM
+            kernels.packed_gemm(x2.contiguous(), self.packed, self.N, out=o2)
             return out.view(*lead, self.N)
+        w, sc, bi = self._mlx_on(x.device)
         for m0 in range(0, M, QMV_MAX_ROWS):
             m1 = min(M, m0 + QMV_MAX_ROWS)
-            kernels.quantized_matmul(x2[m0:m1], self.w, self.scales, self.biases, out=o2[m0:m1])
+            kernels.quantized_matmul(x2[m0:m1], w, sc, bi, out=o2[m0:m1])
         return out.view(*lead, self.N)
 
     def argmax(self, x, out: torch.Tensor) -> torch.Tensor:
@@ -731,6 +747,22 @@ class Qwen35:
                                       capacity=cap, device=dev))
         return LayerCaches(caches, counters)
 
+    def qlinears(self):
+        """Every QLinear of the stack (the shared lm_head included)."""
+        for l in self.layers:
+            m = l.mixer
+            if l.linear:
+                yield from (m.in_proj, m.out_proj)
+            else:
+                yield from (m.qkv_proj, m.o_proj)
+            yield from (l.mlp.gate_up, l.mlp.down)
+        yield self.lm_head
+
+    def offload_mlx(self) -> None:
+        """QLinear.offload_mlx for every layer: one device copy of each weight."""
+        for q in self.qlinears():
+            q.offload_mlx()
+
     def __call__(self, ids, cache, last_only=True, return_hidden=False, keep_prev=False, hidden_out=None):
         """ids: [1, L] int -> logits [1, L or 1, V] bf16 (and pre-norm hidden [1, L, H],
         written into hidden_out when given)."""
@@ -796,10 +828,12 @@ def _rand_qlinear(N, K, gen, scale, device, pack: bool = True) -> QLinear:
 
 
 def random_model(cfg: Config, seed: int = 1004, device="cuda", max_context: int = 8192,
-                 max_width: int = 8, lm_head_scale: float = 2.0) -> Qwen35:
+                 max_width: int = 8, lm_head_scale: float = 2.0, keep_mlx: bool = False) -> Qwen35:
     """Random-init model of the given shape with weights generated directly in the
     MLX 4-bit layout on the device (no checkpoint). Linear scales are chosen so a
-    unit-RMS input gives a unit-RMS output (dequantized w has variance 21.25 s^2)."""
+    unit-RMS input gives a unit-RMS output (dequantized w has variance 21.25 s^2).
+    Unless keep_mlx, each packed layer's MLX-layout triplet then moves to host
+    memory (QLinear.offload_mlx)."""
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
     H, I = cfg.hidden_size, cfg.intermediate_size
@@ -838,4 +872,7 @@ def random_model(cfg: Config, seed: int = 1004, device="cuda", max_context: int 
     e = _rand_qlinear(V, H, gen, 1.0 / math.sqrt(21.25), device, pack=False)
     embed = QEmbedding(e.w, e.scales, e.biases)
     lm_head = lin(V, H, lm_head_scale)
-    return Qwen35(cfg, embed, layers, ones(H), lm_head, max_context=max_context, max_width=max_width)
+    model = Qwen35(cfg, embed, layers, ones(H), lm_head, max_context=max_context, max_width=max_width)
+    if not keep_mlx:
+        model.offload_mlx()
+    return model

@@ -45,6 +45,15 @@ class MTPHead:
         self._zero = torch.zeros((QLinear.PACKED_MAX_ROWS, cfg.hidden_size), dtype=torch.bfloat16,
                                  device=model.norm.device)
 
+    def qlinears(self):
+        m = self.layer.mixer
+        return [self.fc, m.qkv_proj, m.o_proj, self.layer.mlp.gate_up, self.layer.mlp.down]
+
+    def offload_mlx(self) -> None:
+        """QLinear.offload_mlx for the head's own layers (the lm_head is the model's)."""
+        for q in self.qlinears():
+            q.offload_mlx()
+
     def make_cache(self, max_context: int | None = None) -> KVCache:
         cfg = self.model.cfg
         return KVCache(None, 0, n_kv=cfg.num_key_value_heads, head_dim=cfg.head_dim,
@@ -123,8 +132,9 @@ class MTPHead:
         return (logits, out.view(1, T, H)) if return_hidden else logits
 
 
-def random_mtp(model: Qwen35, seed: int = 2004) -> MTPHead:
-    """Random-init MTP head (fc 2H -> H plus one full-attention layer) in the MLX 4-bit layout."""
+def random_mtp(model: Qwen35, seed: int = 2004, keep_mlx: bool = False) -> MTPHead:
+    """Random-init MTP head (fc 2H -> H plus one full-attention layer) in the MLX
+    4-bit layout (the MLX triplets moved to host memory unless keep_mlx)."""
     cfg = model.cfg
     dev = model.norm.device
     gen = torch.Generator(device=dev)
@@ -143,4 +153,7 @@ def random_mtp(model: Qwen35, seed: int = 2004) -> MTPHead:
          "attn": {"q_proj": lin(Hq * 2 * D, H), "k_proj": lin(Hkv * D, H), "v_proj": lin(Hkv * D, H),
                   "o_proj": lin(H, Hq * D, 0.5), "q_norm": ones(D), "k_norm": ones(D)},
          "mlp": {"gate_proj": lin(I, H), "up_proj": lin(I, H), "down_proj": lin(H, I, 0.5)}}
-    return MTPHead(model, w)
+    head = MTPHead(model, w)
+    if not keep_mlx:
+        head.offload_mlx()
+    return head
