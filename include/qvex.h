@@ -298,6 +298,19 @@ int qvex_spec_accept_filtered_bf16(const uint16_t* target, const uint16_t* draft
                                    int32_t* n_accept, int32_t* out_token, int S, int k, int V,
                                    void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* Sampler.scores (engine/sampler.py:30-52) for R rows of V logits (bf16 when
+ * logits_bf16, else fp32; 16-byte aligned) into out fp32 [R, V]: the presence
+ * penalty x - penalty * seen[j] (seen fp32 [V] 0/1 or NULL; the caller marks
+ * extra_seen in it), then greedy (inv_temp <= 0): the penalised logits; else
+ * z = x * inv_temp filtered by top-k / top-p exactly as the accept entry
+ * points filter their target rows (same cutoff), and out = z - c_0 - log(S) on
+ * the kept set (c_0 the row maximum, S the kept sum of exp(z - c_0)), -inf
+ * elsewhere. workspace: qvex_sampler_scores_workspace_bytes(R, V, top_k). */
+uint64_t qvex_sampler_scores_workspace_bytes(int R, int V, int top_k);
+int qvex_sampler_scores(const void* logits, int logits_bf16, int R, int V, const float* seen,
+                        float presence_penalty, float inv_temp, int top_k, float top_p, float* out,
+                        void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* qvex_spec_accept_filtered_bf16 without a workspace argument and without any
  * allocation: the workspace is a static device array of QVEX_SPEC_SCRATCH_BYTES
  * (4 MiB) per GPU, held until the process ends, whose address is looked up

@@ -68,6 +68,8 @@ def lib() -> ctypes.CDLL:
         L.orc_philox4x32_10.restype = None
         L.orc_philox_uniforms.argtypes = [ctypes.c_uint64, ctypes.c_uint64, I, P]
         L.orc_philox_uniforms.restype = None
+        L.orc_row_filter.argtypes = [P, I, F, P, F, I, F, P]
+        L.orc_row_filter.restype = None
         L.orc_expf.argtypes = [F]
         L.orc_expf.restype = F
         for fn in ("orc_qmv_w4g64_f64", "orc_qmv_w4g64_f32", "orc_gated_delta_f64",
@@ -234,6 +236,17 @@ def philox_uniforms(seed: int, event: int, n: int) -> np.ndarray:
     """The sampler's n uniforms of draw event `event` (oracle/rng.c)."""
     out = np.empty(n, np.float32)
     lib().orc_philox_uniforms(int(seed) & (2**64 - 1), int(event), int(n), _p(out))
+    return out
+
+
+def row_filter(row, inv_temp, seen=None, presence_penalty=0.0, top_k=0, top_p=1.0):
+    """(c_0, S_p, cutoff) of one target row: the filter record of oracle/spec.c."""
+    row = np.ascontiguousarray(row, np.float32).reshape(-1)
+    if seen is not None:
+        seen = np.ascontiguousarray(seen, np.float32).reshape(-1)
+    out = np.empty(3, np.float32)
+    lib().orc_row_filter(_p(row), row.size, float(np.float32(inv_temp)), _p(seen),
+                         float(np.float32(presence_penalty)), int(top_k), float(np.float32(top_p)), _p(out))
     return out
 
 

@@ -59,6 +59,11 @@ void orc_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t ou
 /* The sampler's uniforms of draw event `event` (see rng.c): n values in [0, 1). */
 void orc_philox_uniforms(uint64_t seed, uint64_t event, int n, float* out);
 
+/* The filter record (c_0, S_p, cutoff) of one target row (see spec.c); an
+ * unfiltered row gives cutoff = -inf and (max, sum exp) from the part order. */
+void orc_row_filter(const float* row, int V, float inv_temp, const float* seen, float presence_penalty, int top_k,
+                    float top_p, float out[3]);
+
 /* exp used by the sampler on both sides (Cody-Waite reduction + Taylor, fmaf). */
 float orc_expf(float x);
 

@@ -467,6 +467,22 @@ void orc_spec_accept_filtered(const float* target, const float* draft, const int
   }
 }
 
+/* the filter record (c_0, S_p, cutoff) of one target row, as the accept and
+ * scores kernels use it (row_stats for an unfiltered sampling row) */
+void orc_row_filter(const float* row, int V, float inv_temp, const float* seen, float presence_penalty, int top_k,
+                    float top_p, float out[3]) {
+  pfilt pf = {seen, presence_penalty, NULL, 0};
+  const int tk = (top_k > 0 && top_k < V) ? top_k : 0;
+  const int use_p = top_p > 0.0f && top_p < 1.0f;
+  rowstat r;
+  if (tk >= 1 && tk <= 64) r = filtered_stats(row, V, inv_temp, &pf, tk, top_p);
+  else if (tk > 64 || use_p) r = wide_stats(row, V, inv_temp, &pf, tk, top_p);
+  else r = row_stats(row, V, inv_temp, &pf);
+  out[0] = r.m;
+  out[1] = r.s;
+  out[2] = r.cutoff;
+}
+
 void orc_spec_accept(const float* target, const float* draft, const int32_t* draft_ids,
                      const float* u_accept, const float* u_sample, float inv_temp,
                      int32_t* n_accept, int32_t* out_token, int S, int k, int V, int threads) {

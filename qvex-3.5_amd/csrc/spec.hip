@@ -1136,6 +1136,47 @@ __global__ __launch_bounds__(NT) void spec_sample_kernel(SpecArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- full-vocabulary scores (Sampler.scores)
+
+// out[row, j] for part p of the row: greedy - the penalised logit; sampling -
+// z - c_0 - log(S) on the kept set (z >= cutoff), -inf elsewhere, where
+// (c_0, S, cutoff) are the row's filter record, or for an unfiltered row
+// c_0 = max z and S = sum exp(z - c_0) combined from the part statistics in the
+// accept kernels' order (engine/sampler.py:30-52).
+__global__ __launch_bounds__(NT) void spec_scores_kernel(SpecArgs a, float* __restrict__ out) {
+  const int p = blockIdx.x, row = blockIdx.y;
+  const int t = threadIdx.x;
+  const void* src = row_ptr(a, row, 0);
+  float c0 = 0.0f, lS = 0.0f, cut = -__builtin_inff();
+  if (!a.greedy) {
+    if (a.filt) {
+      const float* fr = a.frow + (long)row * 4;
+      c0 = fr[0];
+      lS = logf(fr[1]);
+      cut = fr[2];
+    } else {
+      const float* w = a.ws + (long)row * a.P * 2;
+      float m = -__builtin_inff();
+      for (int q = 0; q < a.P; ++q) m = fmaxf(m, w[2 * q]);
+      float S = 0.0f;
+      for (int q = 0; q < a.P; ++q) S = S + w[2 * q + 1] * qx_expf(w[2 * q] - m);
+      c0 = m;
+      lS = logf(S);
+    }
+  }
+  const int base = p * PART, end = min(a.V, base + PART);
+  float* o = out + (long)row * a.V;
+  for (int j = base + t; j < end; j += NT) {
+    const float x = pen_x(a.seen, a.pen, lg(src, j, a.bf), j, nullptr, 0);
+    if (a.greedy) {
+      o[j] = x;
+    } else {
+      const float z = x * a.inv_temp;
+      o[j] = z >= cut ? (z - c0) - lS : -__builtin_inff();
+    }
+  }
+}
+
 int nparts(int V) { return (V + PART - 1) / PART; }
 
 }  // namespace
@@ -1237,6 +1278,55 @@ extern "C" int qvex_spec_accept_filtered_bf16(const uint16_t* target, const uint
                                               uint64_t workspace_bytes, void* stream) {
   return spec_accept_impl(target, draft, 1, draft_ids, u_accept, u_sample, inv_temp, seen, presence_penalty, top_k,
                           top_p, n_accept, out_token, S, k, V, workspace, workspace_bytes, stream);
+}
+
+
+extern "C" uint64_t qvex_sampler_scores_workspace_bytes(int R, int V, int top_k) {
+  return qvex_spec_accept_filtered_workspace_bytes(R, 0, V, 0, top_k);
+}
+
+extern "C" int qvex_sampler_scores(const void* logits, int logits_bf16, int R, int V, const float* seen,
+                                   float presence_penalty, float inv_temp, int top_k, float top_p, float* out,
+                                   void* workspace, uint64_t workspace_bytes, void* stream) {
+  QVEX_CHECK_ARG(logits && out && workspace, "qvex_sampler_scores: null pointer");
+  QVEX_CHECK_ARG(R >= 1 && R <= 65535 && V >= 4 && V % 4 == 0 && top_k >= 0,
+                 "qvex_sampler_scores: R=%d V=%d top_k=%d (V a positive multiple of 4)", R, V, top_k);
+  QVEX_CHECK_ARG(qvex_aligned(logits, 16), "qvex_sampler_scores: logits must be 16-byte aligned");
+  QVEX_CHECK_ARG(presence_penalty == presence_penalty && top_p == top_p, "qvex_sampler_scores: NaN argument");
+  const int greedy = !(inv_temp > 0.0f);
+  const bool use_p = top_p > 0.0f && top_p < 1.0f;
+  const int P = nparts(V);
+  const int tk = (top_k > 0 && top_k < V) ? top_k : 0;
+  const int filt = greedy ? 0 : (tk >= 1 && tk <= 64 ? 1 : ((tk > 64 || use_p) ? 2 : 0));
+  const int kf = filt == 1 ? tk : 0;
+  QVEX_CHECK_ARG(kf == 0 || P * kf <= 64 * 64, "qvex_sampler_scores: V=%d too large for top_k=%d", V, kf);
+  const uint64_t base = ws_floats(R, 1, P);
+  const uint64_t need = (base + (filt ? filter_floats(R, 0, P, kf) : 0)) * sizeof(float);
+  QVEX_CHECK_ARG(workspace_bytes >= need, "qvex_sampler_scores: workspace %llu bytes < %llu needed",
+                 (unsigned long long)workspace_bytes, (unsigned long long)need);
+  float* fws = (float*)workspace + base;
+  float* frow = fws + (kf > 0 ? (uint64_t)R * P * (kf + 1) : 0);
+  SpecArgs a{logits, nullptr, nullptr, nullptr, nullptr, inv_temp, greedy, nullptr, nullptr, (float*)workspace,
+             R, 0, V, P, 1, seen, presence_penalty, kf, use_p ? top_p : 1.0f, fws, frow, logits_bf16 ? 1 : 0,
+             filt, filt == 2 ? tk : 0};
+  hipStream_t st = (hipStream_t)stream;
+  if (!greedy) {
+    if (a.bf)
+      hipLaunchKernelGGL(spec_rowstats_kernel<true>, dim3(P, R), dim3(NT), 0, st, a);
+    else
+      hipLaunchKernelGGL(spec_rowstats_kernel<false>, dim3(P, R), dim3(NT), 0, st, a);
+    QVEX_CHECK_LAUNCH("qvex_sampler_scores/rowstats");
+    if (filt == 1) {
+      hipLaunchKernelGGL(spec_filter_kernel, dim3(R), dim3(NT), 0, st, a);
+      QVEX_CHECK_LAUNCH("qvex_sampler_scores/filter");
+    } else if (filt == 2) {
+      hipLaunchKernelGGL(spec_wide_filter_kernel, dim3(R), dim3(WT), 0, st, a);
+      QVEX_CHECK_LAUNCH("qvex_sampler_scores/wide_filter");
+    }
+  }
+  hipLaunchKernelGGL(spec_scores_kernel, dim3(P, R), dim3(NT), 0, st, a, out);
+  QVEX_CHECK_LAUNCH("qvex_sampler_scores/scores");
+  return QVEX_OK;
 }
 
 extern "C" int qvex_spec_accept(const float* target, const float* draft, const int32_t* draft_ids,

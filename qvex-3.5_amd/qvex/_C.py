@@ -45,6 +45,7 @@ SIGNATURES: dict[str, list] = {
     "qvex_spec_accept_filtered": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P, U64, P],
     "qvex_spec_accept_filtered_bf16": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P, U64, P],
     "qvex_spec_accept_filtered_bf16_noalloc": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P],
+    "qvex_sampler_scores": [P, I, I, I, P, F, F, I, F, P, P, U64, P],
     "qvex_mark_seen": [P, I, P, I, P, I, P],
     "qvex_embed_w4g64": [P, I, P, P, P, I, I, P, P],
     "qvex_rmsnorm": [P, LNG, P, P, LNG, I, I, F, F, P],
@@ -92,6 +93,8 @@ def lib() -> ctypes.CDLL:
         L.qvex_spec_accept_filtered_workspace_bytes.argtypes = [I, I, I, I, I]
         L.qvex_gdn_chunked_workspace_bytes.restype = U64
         L.qvex_gdn_chunked_workspace_bytes.argtypes = [I, I, I, I, I, I]
+        L.qvex_sampler_scores_workspace_bytes.restype = U64
+        L.qvex_sampler_scores_workspace_bytes.argtypes = [I, I, I]
         L.qvex_qmv_w4g64_argmax_workspace_bytes.restype = U64
         L.qvex_qmv_w4g64_argmax_workspace_bytes.argtypes = [I, I]
         for name, args in SIGNATURES.items():
@@ -114,4 +117,4 @@ def exported_symbols() -> list[str]:
     return ["qvex_last_error", "qvex_abi_version", "qvex_spec_accept_workspace_bytes",
             "qvex_attn_workspace_bytes", "qvex_w4g64_packed_bytes",
             "qvex_gdn_chunked_workspace_bytes", "qvex_spec_accept_filtered_workspace_bytes",
-            "qvex_qmv_w4g64_argmax_workspace_bytes", *SIGNATURES]
+            "qvex_qmv_w4g64_argmax_workspace_bytes", "qvex_sampler_scores_workspace_bytes", *SIGNATURES]

@@ -74,26 +74,32 @@ class Sampler:
         return self._ws[key]
 
     def scores(self, logits: torch.Tensor, extra_seen=None) -> torch.Tensor:
-        """Full-vocab fp32 scores as engine/sampler.py:30-52: penalised logits
-        (greedy) or filtered log-probs. A convenience mirror of the reference's
-        API; the decode path does this inside the fused kernel."""
-        z = to_f32(logits.reshape(-1)).clone()
+        """Full-vocabulary fp32 scores as engine/sampler.py:30-52 (qvex_sampler_scores):
+        penalised logits when greedy, else filtered log-probabilities (-inf outside
+        the top-k / top-p set). logits: [V] or [R, V] bf16 / fp32 on the device;
+        extra_seen: ids that count as seen for this call only. The decode path
+        does the same filtering inside its sampling kernel instead."""
+        t = as_logits(logits)
+        R = t.numel() // self.V
+        seen = None
         if self.p.presence_penalty:
-            seen = self._filter(z.device)["seen"].clone()
+            seen = self._filter(t.device)["seen"]
             if extra_seen is not None:
-                seen[torch.as_tensor(extra_seen, device=z.device).long().reshape(-1)] = 1.0
-            z = z - self.p.presence_penalty * seen
-        if self.greedy:
-            return z
-        z = z / self.p.temperature
-        cand = torch.topk(z, self.top_k).values if self.top_k else torch.sort(z, descending=True).values
-        cutoff = cand[-1]
-        if self.top_p < 1.0:
-            probs = torch.softmax(cand, dim=0)
-            keep = (torch.cumsum(probs, 0) - probs) < self.top_p
-            cutoff = torch.where(keep, cand, torch.full_like(cand, float("inf"))).min()
-        z = torch.where(z >= cutoff, z, torch.full_like(z, float("-inf")))
-        return z - torch.logsumexp(z, 0)
+                seen = seen.clone()
+                ids = torch.as_tensor(extra_seen, device=t.device).reshape(-1).to(torch.int32)
+                _C.call("qvex_mark_seen", seen.data_ptr(), self.V, ids.data_ptr(), ids.numel(), None, ids.numel(),
+                        kernels._stream())
+        key = ("scores", R)
+        if key not in self._ws:
+            n = int(_C.lib().qvex_sampler_scores_workspace_bytes(R, self.V, self.top_k))
+            self._ws[key] = torch.empty((max(n, 4) + 3) // 4, dtype=torch.float32, device=t.device)
+        ws = self._ws[key]
+        out = torch.empty(t.shape, dtype=torch.float32, device=t.device)
+        inv = float(np.float32(1.0) / np.float32(self.p.temperature)) if not self.greedy else 0.0
+        _C.call("qvex_sampler_scores", t.data_ptr(), int(t.dtype == torch.bfloat16), R, self.V,
+                seen.data_ptr() if seen is not None else None, float(self.p.presence_penalty), inv, self.top_k,
+                float(self.top_p), out.data_ptr(), ws.data_ptr(), ws.numel() * 4, kernels._stream())
+        return out
 
     def counter(self, device) -> torch.Tensor:
         """The device draw counter (one uint64 in an int64 tensor)."""

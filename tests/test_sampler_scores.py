@@ -1,6 +1,7 @@
-"""Sampler.scores (the reference-API mirror, engine/sampler.py:30-52) against the
-float64 restatement used to pin the fused kernel's oracle: same kept set, same
-log-probs to fp32 accuracy. CPU tensors, no device."""
+"""Sampler.scores (engine/sampler.py:30-52, qvex_sampler_scores on the device)
+against the float64 restatement used to pin the fused kernel's oracle: same
+kept set, same log-probs to fp32 accuracy (GPU); the filter settings follow the
+reference's rules (CPU)."""
 
 import numpy as np
 import pytest
@@ -10,17 +11,19 @@ from qvex.sampler import Sampler, SamplingParams
 from test_oracle_spec_filter import ref_scores
 
 
+@pytest.mark.gpu
 @pytest.mark.parametrize("T,top_k,top_p,pen", [(0.7, 20, 0.95, 0.0), (0.6, 10, 0.8, 1.5), (1.0, 5, 1.0, 0.0),
-                                               (0.0, 20, 0.95, 2.0)])
+                                               (0.0, 20, 0.95, 2.0), (0.7, 100, 0.9, 0.0), (0.8, 0, 0.7, 0.5)])
 def test_scores_mirror_reference(T, top_k, top_p, pen):
     g = np.random.default_rng(int(T * 10) + top_k)
-    V = 500
+    V = 512
     logits = (g.standard_normal(V) * 2.0).astype(np.float32)
     seen = (g.random(V) < 0.2).astype(np.float32)
     s = Sampler(SamplingParams(temperature=T, top_k=top_k, top_p=top_p, presence_penalty=pen), V)
     if pen:
-        s.seen = torch.from_numpy(seen)
-    got = s.scores(torch.from_numpy(logits), extra_seen=[3] if pen else None).numpy().astype(np.float64)
+        s.seen = torch.from_numpy(seen).to("cuda:0")
+    got = s.scores(torch.from_numpy(logits).to("cuda:0"),
+                   extra_seen=[3] if pen else None).cpu().numpy().astype(np.float64)
     ref = ref_scores(logits, T, seen if pen else None, pen, top_k if T > 0 else 0, top_p, extra=(3,) if pen else ())
     assert np.array_equal(np.isfinite(got), np.isfinite(ref))
     fin = np.isfinite(ref)

@@ -58,6 +58,8 @@ CASES = [
     (8, 2, 248320, 1.0, 1000, 1.0, 0.0, True, False),      # top-k only, 1000 candidates
     (6, 3, 50000, 0.7, 0, 0.5, 0.5, False, True),          # tight whole-vocabulary p, draft logits
     (16, 4, 20000, 0.7, 20000, 0.8, 0.0, False, False),    # top_k = V: no top-k (the reference's rule)
+    (8, 3, 248320, 1.5, 0, 0.9, 0.0, False, False),        # flat: tens of thousands of tokens kept
+    (4, 2, 248320, 2.0, 3000, 0.7, 0.4, True, False),      # flat, top-k 3000 then top-p, ties
 ]
 
 
@@ -113,3 +115,46 @@ def test_bf16_logits_equal_their_fp32_copies(S, k, V, T, top_k, top_p, pen, dl):
                                    *args, **kw)
     torch.cuda.synchronize()
     assert torch.equal(n1, n2) and torch.equal(tok1, tok2)
+
+
+# ---------------------------------------------------------------- Sampler.scores (engine/sampler.py:30-52)
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("V,T,top_k,top_p,pen,bf16", [
+    (248320, 0.7, 20, 0.95, 0.0, True), (248320, 0.6, 0, 0.9, 1.2, False), (50000, 1.0, 200, 1.0, 0.0, True),
+    (4096, 0.0, 20, 0.9, 0.7, False), (4096, 0.8, 0, 1.0, 0.0, False), (20000, 0.7, 64, 0.5, 0.5, True),
+    (248320, 1.5, 0, 0.9, 0.0, False), (248320, 2.0, 3000, 0.7, 0.4, True)])
+def test_scores_kept_set_and_values(V, T, top_k, top_p, pen, bf16):
+    """Sampler.scores on the device: the kept set is exactly z >= the oracle's
+    cutoff (the rule the accept kernels use); values equal z - c_0 - log(S) of
+    the oracle's record within fp32 rounding; greedy gives the penalised logits;
+    extra_seen counts for this call only."""
+    from qvex.sampler import Sampler, SamplingParams
+    g = np.random.default_rng(V + top_k)
+    logits = (g.standard_normal(V) * 3.0).astype(np.float32)
+    logits[g.integers(0, V, 3)] += 8.0
+    if bf16:
+        logits = synth.bf16_to_f32(synth.bf16_bits(logits))
+    seen = (g.random(V) < 0.05).astype(np.float32)
+    extra = g.integers(0, V, 3)
+    s = Sampler(SamplingParams(temperature=T, top_k=top_k, top_p=top_p, presence_penalty=pen), V)
+    if pen:
+        s.seen = torch.from_numpy(seen).to(DEV)
+    lt = torch.from_numpy(logits).to(DEV)
+    got = s.scores(lt.to(torch.bfloat16) if bf16 else lt, extra_seen=extra).cpu().numpy().astype(np.float64)
+    if pen:
+        assert torch.equal(s.seen.cpu(), torch.from_numpy(seen))            # extra_seen left no mark
+    sv = seen.copy()
+    sv[extra] = 1.0
+    x = logits - np.float32(pen) * sv if pen else logits
+    if T <= 0:
+        np.testing.assert_array_equal(got, x.astype(np.float64))
+        return
+    c0, S, cut = oracle.row_filter(logits, inv(T), seen=sv if pen else None, presence_penalty=pen, top_k=top_k,
+                                   top_p=top_p)
+    z = (x.astype(np.float32) * np.float32(inv(T))).astype(np.float64)
+    kept = z >= cut
+    assert np.array_equal(np.isfinite(got), kept)
+    ref = z[kept] - float(c0) - np.log(float(S))
+    assert np.abs(got[kept] - ref).max() <= 1e-5 * (1.0 + np.abs(ref).max())
+    print(f"V={V} top_k={top_k} top_p={top_p}: kept {int(kept.sum())}")
