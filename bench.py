@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """MTP speculative-decode throughput on one MI355X, plus the 4-bit qmv roofline.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload e2e|qmv]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload e2e|qmv|gdn|gdn_verify|mixer|attn|spec] [--accept-all]
 
 Workload "e2e" (default): a random-init Qwen3.5-9B-shaped model (32 layers, 24
 Gated DeltaNet + 8 gated attention, hidden 4096, MLP 12288, vocab 248320, 4-bit
@@ -24,7 +25,20 @@ Every line also carries:
   qmv_shapes: the decode cycle's other matmul shapes;
   cpu_baseline: the oracle's C restatement (OpenMP) of the cycle's quantized
     matmuls, timed on this host on one cycle's worth of shapes and scaled to
-    tokens per second with the GPU run's tokens per cycle.
+    tokens per second with the GPU run's tokens per cycle;
+  cpu_baselines: the same restatement beside each config's GPU figure
+    (config-0 GEMV, config-2 verify recurrence, config-3 accept on a sample of
+    steps), on all host threads, best of repeated runs.
+
+--accept-all is a labelled diagnostic, not the headline: greedy decoding with
+the shared lm_head zeroed, so every draft is accepted (k + 1 tokens a cycle)
+and the timed cycles take the n = k commit path at the 9B shape.
+
+The other workloads run one kernel family in a loop for rocprofv3 counter
+passes (profiles/): gdn (chunked DeltaNet prefill), gdn_verify (the config-2
+recurrence), mixer (the cycle's split DeltaNet mixer at the 9B shape), attn
+(the verify attention's q/k norm + RoPE, partial and combine at a 4352-token
+context), spec (config 3).
 """
 
 from __future__ import annotations
@@ -324,6 +338,105 @@ def cpu_baseline(cfg, k, tokens_per_cycle):
             "host_cpus": os.cpu_count(), "host_affinity": len(os.sched_getaffinity(0))}
 
 
+def _best_of(fn, reps=3):
+    best = float("inf")
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        best = min(best, time.perf_counter() - t0)
+    return best
+
+
+def cpu_baselines(k_spec=4, steps_sample=4):
+    """The oracle's C restatement beside each config's GPU figure, on all host
+    threads (best of 3): config 0 (the 12288 x 4096 GEMV, fp32 accumulate),
+    config 2 verify (T = 5 recurrence with snapshots, 32 heads of 128), config 3
+    (the fused accept on a sample of `steps_sample` of its 256 steps, scaled)."""
+    import oracle
+    from qvex import synth
+    threads = min(int(os.environ.get("OMP_NUM_THREADS", "16")), len(os.sched_getaffinity(0)))
+    out = {"cores": threads, "kind": "port"}
+    w, s, b = synth.qmv_weights(12288, 4096, tag=9)
+    x = synth.qmv_x(1, 4096, tag=9)
+    oracle.qmv_f32(x, w[:64], s[:64], b[:64], threads)
+    t = _best_of(lambda: oracle.qmv_f32(x, w, s, b, threads))
+    out["config0_gemv"] = {"us": round(t * 1e6, 1), "GB/s": round(28344320 / t / 1e9, 2)}
+    inp = synth.gdn_inputs(5, seed=9, Hk=16, Hv=32)
+    f = synth.bf16_to_f32
+    args = [f(inp[n]) for n in ("q", "k", "v", "a", "b")]
+    t = _best_of(lambda: oracle.gated_delta_f32(*args, inp["A_log"], f(inp["dt_bias"]), inp["state"], snaps=True,
+                                                 threads=threads))
+    out["config2_verify"] = {"us": round(t * 1e6, 1), "GB/s": round(12.71e6 / t / 1e9, 2)}
+    sp = synth.spec_inputs(range(steps_sample), k=k_spec, V=248320)
+    t = _best_of(lambda: oracle.spec_accept(sp["target"], sp["draft"], sp["draft_ids"], sp["u_accept"],
+                                             sp["u_sample"], float(np.float32(1.0) / np.float32(0.7)),
+                                             threads=threads), reps=2)
+    out["config3_accept"] = {"us_per_step": round(t * 1e6 / steps_sample, 1),
+                             "us_256_steps": round(t * 1e6 / steps_sample * 256, 1),
+                             "sample": f"{steps_sample} of the 256 steps (k={k_spec}, V=248320, draft logits)"}
+    return out
+
+
+# ---------------------------------------------------------------- single-kernel workloads (profiling)
+
+def mixer_verify(copies=24, iters=96):
+    """The decode cycle's split DeltaNet mixer (qvex_gdn_decode_split, 4 workgroups
+    per value head) at the 9B shape for a 4-token verify with snapshots, over
+    rotating recurrent caches (state ring + conv ring, ~19 MB each); bytes = the
+    state read + 4 snapshots written = 10 MiB per call."""
+    import torch
+    from qvex.model import Config, random_model
+    cfg = Config.qwen35_9b()
+    cfg.num_hidden_layers = 1
+    m = random_model(cfg, seed=5, device="cuda:0", max_context=256, max_width=4)
+    gdn = m.layers[0].mixer
+    caches = [m.make_cache(max_width=4) for _ in range(copies)]
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(5)
+    proj = (torch.randn((4, gdn.in_proj.N), generator=g, device="cuda:0")).to(torch.bfloat16)
+    us = _event_time(lambda i: gdn.mix_split(proj, caches[i % copies][0]), iters)
+    nbytes = 5 * 32 * 128 * 128 * 4
+    return {"kernel": "qvex_gdn_decode_split (4 blocks per head, T=4 with snapshots)", "us": round(us, 2),
+            "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1), "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            "bytes": nbytes}
+
+
+def attn_verify(L=4, pos0=4348, copies=24, iters=96, kps=128):
+    """The verify attention of one layer at the 9B shape (16 q / 4 kv heads of 256,
+    L = 4 rows at positions 4348..4351): q/k norm + RoPE + KV append, then the
+    split-K partial and combine kernels over rotating KV caches; bytes = the K
+    and V read for the 4352 keys (17.8 MB per call)."""
+    import torch
+    from qvex import _C
+    from qvex.kernels import _ptr, _stream
+    dev = torch.device("cuda:0")
+    Hq, Hkv, D, rot = 16, 4, 256, 64
+    cap = 4608
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    proj = torch.randn((L, Hq * 2 * D + 2 * Hkv * D), generator=g, device=dev).to(torch.bfloat16)
+    qn = torch.ones(D, dtype=torch.bfloat16, device=dev)
+    kc = [torch.randn((Hkv, cap, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(copies)]
+    vc = [torch.randn((Hkv, D, cap), generator=g, device=dev).to(torch.bfloat16) for _ in range(copies)]
+    pos = torch.tensor([pos0], dtype=torch.int32, device=dev)
+    q = torch.empty((L, Hq, D), dtype=torch.bfloat16, device=dev)
+    out = torch.empty((L, Hq * D), dtype=torch.bfloat16, device=dev)
+    need = int(_C.lib().qvex_attn_workspace_bytes(L, Hq, Hkv, D, pos0 + L, kps))
+    ws = torch.empty((need + 3) // 4, dtype=torch.float32, device=dev)
+
+    def step(i):
+        c = i % copies
+        _C.call("qvex_attn_qk_rope", _ptr(proj), proj.stride(0), _ptr(qn), _ptr(qn), _ptr(pos), L, Hq, Hkv, D, rot,
+                1e7, 1e-6, _ptr(q), _ptr(kc[c]), _ptr(vc[c]), cap, _stream())
+        _C.call("qvex_attention", _ptr(q), _ptr(kc[c]), _ptr(vc[c]), _ptr(pos), L, Hq, Hkv, D, cap, pos0 + L, kps,
+                _ptr(proj), proj.stride(0), _ptr(out), _ptr(ws), ws.numel() * 4, _stream())
+    us = _event_time(step, iters)
+    nbytes = 2 * Hkv * (pos0 + L) * D * 2
+    return {"kernel": "qvex_attn_qk_rope + qvex_attention (partial + combine)", "ctx": pos0 + L, "us": round(us, 2),
+            "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1), "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            "bytes": nbytes}
+
+
 # ---------------------------------------------------------------- end to end
 
 def run_e2e(args):
@@ -331,7 +444,8 @@ def run_e2e(args):
     from qvex.model import Config, random_model
     from qvex.mtp import random_mtp
     from qvex.sampler import Sampler, SamplingParams
-    from qvex.speculative import GraphedMTPCycle, MTPDecoder, mtp_prefill
+    from qvex.engine import prefill
+    from qvex.speculative import GraphedMTPCycle, MTPDecoder
     from qvex import synth
 
     cfg = Config.qwen35_9b()
@@ -346,13 +460,19 @@ def run_e2e(args):
     ids_t = torch.from_numpy(ids).reshape(1, -1).to(dev)
     cache, mcache = model.make_cache(), mtp.make_cache()
     t0 = time.perf_counter()
-    logits, hidden = model(ids_t, cache, return_hidden=True)
-    last_h = mtp_prefill(mtp, mcache, hidden, ids_t, None)
+    logits, last_h = prefill(model, ids_t, cache, mtp, mcache)      # 512-token chunks, MTP head per chunk
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t0
     log(f"prefill {args.prompt} tokens in {prefill_s:.2f}s")
+    temperature = args.temperature
+    if args.accept_all:
+        # diagnostic: greedy with every logit 0, so drafts (token 0) are always accepted
+        model.lm_head.scales.zero_()
+        model.lm_head.biases.zero_()
+        model.lm_head.repack()
+        temperature = 0.0
     # the reference's MTP benchmark samples with top_k = 20, top_p = 0.8 (bench/mtp_bench.py:39)
-    sampler = Sampler(SamplingParams(temperature=args.temperature, top_k=args.top_k, top_p=args.top_p,
+    sampler = Sampler(SamplingParams(temperature=temperature, top_k=args.top_k, top_p=args.top_p,
                                      seed=synth.SEED_E2E), cfg.vocab_size)
     stats = {}
     dec = MTPDecoder(model, sampler, cache, logits[0, -1], last_h, mtp, mcache, k=args.k, stats=stats)
@@ -393,7 +513,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="e2e", choices=["e2e", "qmv", "gdn"])
+    ap.add_argument("--workload", default="e2e", choices=["e2e", "qmv", "gdn", "gdn_verify", "mixer", "attn", "spec"])
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--k", type=int, default=3)
     ap.add_argument("--temperature", type=float, default=0.7)
@@ -404,6 +524,8 @@ def main():
     ap.add_argument("--qmv", default="config0", choices=sorted(ROOF_KERNELS),
                     help="kernel timed by --workload qmv")
     ap.add_argument("--eager", action="store_true", help="launch every kernel from Python (no HIP graph)")
+    ap.add_argument("--accept-all", action="store_true",
+                    help="diagnostic: greedy, zeroed lm_head, every draft accepted (not the headline figure)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (collectives are out of scope); "
@@ -429,6 +551,10 @@ def main():
                           "k": args.k, "prompt_tokens": args.prompt, "temperature": args.temperature,
                           "top_k": args.top_k, "top_p": args.top_p,
                           "cycles_timed": args.steps, "hip_graph": not args.eager}
+        if args.accept_all:
+            line["metric"] = "diagnostic: MTP cycle with every draft accepted (greedy, zeroed lm_head), tok/s"
+            line["config"]["temperature"] = 0.0
+            line["config"]["workload"] += "; DIAGNOSTIC accept-all (not the headline)"
         line["tokens_per_cycle"] = round(res["tokens_per_cycle"], 4)
         line["acceptance"] = round(res["acceptance"], 4)
         line["prefill_s"] = round(res["prefill_s"], 2)
@@ -436,6 +562,13 @@ def main():
         from qvex.model import Config
         cfg = Config.qwen35_9b()
         res = None
+    single = {"gdn_verify": gdn_config2_verify, "mixer": mixer_verify, "attn": attn_verify, "spec": spec_config3}
+    if args.workload in single:
+        r = single[args.workload]()
+        line.update({"value": r["GB/s"], "unit": "GB/s", "ms_per_step": r["us"] / 1e3, args.workload: r,
+                     "config": {"workload": r["kernel"]}})
+        print(json.dumps(line), flush=True)
+        return
     if args.workload == "gdn":
         # the chunked prefill kernel only (what the rocprofv3 MFMA passes under profiles/ run)
         r = gdn_config2_prefill(recurrent=False)
@@ -470,6 +603,9 @@ def main():
         log("cpu baseline")
         tpc = res["tokens_per_cycle"] if res else 1.0
         line["cpu_baseline"] = cpu_baseline(cfg, args.k, tpc)
+        if not args.no_shapes:
+            log("cpu baselines per config")
+            line["cpu_baselines"] = cpu_baselines()
     print(json.dumps(line), flush=True)
 
 
