@@ -120,6 +120,40 @@ def qmv_time(M, N, K, iters=None, tile=None, seed_tag=0, packed=False, swiglu=Fa
     return best, algo
 
 
+def read_ceiling_us(nbytes, blocks=2048, iters=200):
+    """The single-launch HBM read ceiling for a buffer of nbytes: qvex_read_roof
+    (grid-stride 16-byte loads; 2048 blocks of 256 threads = 32 waves on each of
+    the 256 CUs) replayed back to back from a HIP graph over rotating copies
+    (> 600 MB, so HBM serves them), as the products are timed. A sweep of 256 to
+    4096 blocks and 1 to 16 loads in flight per lane found this shape fastest for
+    9.4 to 57 MB."""
+    import torch
+    from qvex import kernels
+    n = nbytes // 16 * 16
+    copies = int(np.ceil(600e6 / n)) + 1
+    bufs = [torch.empty(n // 4, dtype=torch.int32, device="cuda:0").fill_(i) for i in range(copies)]
+    sink = torch.zeros(64, dtype=torch.int32, device="cuda:0")
+    kernels.read_roof(bufs[0], sink, blocks)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(iters):
+            kernels.read_roof(bufs[i % copies], sink, blocks)
+    g.replay()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e3 / iters)
+    del g, bufs
+    torch.cuda.empty_cache()
+    return best
+
+
 def read_roof_calibration(nbytes=28344320 // 16 * 16, copies=24, reps=3):
     """Stream-read `copies` distinct buffers of nbytes with qvex_read_roof: a
     kernel of known traffic, for scaling PMC byte counters (FETCH_SIZE)."""
@@ -149,10 +183,12 @@ def roofline(name):
     M, N, K, packed, prof_name, label = ROOF_KERNELS[name]
     us, algo = qmv_time(M, N, K, packed=bool(packed), swiglu=packed == "swiglu")
     ach = algo / (us * 1e-6) / 1e9
+    ceil = read_ceiling_us(int(algo))
     out = {"kernel": label, "bound": "hbm",
            "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
            "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
-           "algorithmic_bytes_per_launch": int(algo), "avg_launch_us": round(us, 3)}
+           "algorithmic_bytes_per_launch": int(algo), "avg_launch_us": round(us, 3),
+           "read_ceiling_us": round(ceil, 3), "frac_of_read_ceiling": round(ceil / us, 3)}
     # HBM bytes per launch come from rocprofv3 FETCH_SIZE/WRITE_SIZE passes of
     # `bench.py --workload qmv --qmv NAME` (calibrated on a read of known size), kept in profiles/
     prof = REPO / "profiles" / prof_name
@@ -176,8 +212,10 @@ def qmv_shapes():
               "gate_up_swiglu_m5": (5, 24576, 4096)}
     for name, (M, N, K) in shapes.items():
         us, algo = qmv_time(M, N, K, packed=True, swiglu="swiglu" in name)
+        ceil = read_ceiling_us(int(0.5625 * N * K))
         out[name] = {"us": round(us, 2), "GB/s": round(algo / (us * 1e-6) / 1e9, 1),
                      "frac": round(algo / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                     "read_ceiling_us": round(ceil, 2), "frac_of_read_ceiling": round(ceil / us, 3),
                      "kernel": "packed" if M <= 4 else "packed, chunks of 4 rows"}
     return out
 
