@@ -155,6 +155,11 @@ struct PkEpi {
 };
 
 constexpr int pk_block(int WS) { return WS >= 4 ? 64 * WS : 256; }   // WS = 16: 1024 threads
+// Waves per SIMD the register budget must allow: the lm_head-wide (2, 4)
+// double-buffered product runs ~30 k waves in many rounds and needs 4 resident
+// (at most 128 VGPRs: 84.9 against 91.8 us at M = 1 when the compiler takes 172);
+// the others run one round of waves and keep the compiler's choice.
+constexpr int pk_min_waves(int TN, int WS, int NP) { return TN == 2 && WS == 4 && NP == 0 ? 4 : 1; }
 
 // TN 16-row tiles per wave share each activation operand; WS waves of a block
 // split the sets of the same tiles (set ws, ws + WS, ...) and combine through
@@ -171,7 +176,7 @@ constexpr int pk_block(int WS) { return WS >= 4 ? 64 * WS : 256; }   // WS = 16:
 // scale of PkEpi (a mode of its own so that the other kernels keep their
 // registers). MODE 0: plain.
 template <int TN, int WS, int NP, int MODE>
-__global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk_min_waves(TN, WS, NP)))) void qmv_packed_kernel(const uint16_t* __restrict__ x,
                                                                    const uint8_t* __restrict__ packed,
                                                                    uint16_t* __restrict__ y, int M, int N, int K,
                                                                    PkEpi e) {
@@ -216,15 +221,18 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
   constexpr bool SWIGLU = MODE == 1;
   constexpr bool seg = MODE == 2;
 
-  // head-segment partials: thread i sums pair (head i / 4, row i % 4)
+  // head-segment partials: thread i sums pair (head i / 4, row i % 4).
+  // Epilogue inputs are loaded from clamped (always valid) addresses with no
+  // condition, and the entries that do not exist are dropped where the values
+  // are used: a conditional load makes the compiler wait for it at the end of
+  // the condition, before the weight loads go out.
   __shared__ __align__(16) float seg_tab[seg ? 256 : 4];
   const int H = K / 128;
   float segv[8];
   if constexpr (seg) {
-    const int sh = threadIdx.x >> 2, sr = threadIdx.x & 3;
+    const int sh = min((int)threadIdx.x >> 2, H - 1), sr = min((int)threadIdx.x & 3, M - 1);
 #pragma unroll
-    for (int b = 0; b < 8; ++b)
-      segv[b] = (b < e.seg_nb && sh < H && sr < M) ? e.seg_ss[((size_t)sr * H + sh) * e.seg_nb + b] : 0.0f;
+    for (int b = 0; b < 8; ++b) segv[b] = e.seg_ss[((size_t)sr * H + sh) * e.seg_nb + min(b, e.seg_nb - 1)];
   }
   auto seg_table = [&]() {
     if constexpr (seg) {
@@ -245,18 +253,21 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
   if (rs && ws == 0) {
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      rsp[r] = (r < M && 4 * lane < e.rs_nparts) ? load16(e.rs_parts + (size_t)r * e.rs_nparts + 4 * lane)
-                                                 : u32x4{0u, 0u, 0u, 0u};
+      rsp[r] = load16(e.rs_parts + (size_t)min(r, M - 1) * e.rs_nparts + min(4 * lane, e.rs_nparts - 4));
   }
   // the plain epilogue gives lane L row L / 16 and column L % 16 of each tile
   const int er = lane >> 4, ei = lane & 15;
+  // (loaded by every wave, with x standing in when there is no residual: under a
+  // branch the compiler converts them as soon as they arrive, which waits)
   uint16_t rsd[TN], nw[TN];
-  if (prod && ws == 0) {
+  {
+    const uint16_t* rp = prod ? e.resid : x;
+    const uint16_t* wp = prod ? e.norm_w : x;
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
-      const int n = (tile0 + t) * PK_TILE + ei;
-      nw[t] = n < N ? e.norm_w[n] : (uint16_t)0;
-      rsd[t] = (er < M && n < N) ? e.resid[(size_t)er * N + n] : (uint16_t)0;
+      const int nc = min((tile0 + t) * PK_TILE + ei, N - 1);   // columns past N and rows past M are never stored
+      nw[t] = wp[prod ? nc : 0];
+      rsd[t] = rp[prod ? (size_t)min(er, M - 1) * N + nc : 0];
     }
   }
   // consumer scale: summed as soon as the partials are in (they were requested
@@ -267,6 +278,7 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
     for (int r = 0; r < 4; ++r) {
       float v = ((__uint_as_float(rsp[r].x) + __uint_as_float(rsp[r].y)) + __uint_as_float(rsp[r].z)) +
                 __uint_as_float(rsp[r].w);
+      v = 4 * lane < e.rs_nparts ? v : 0.0f;   // lanes past the partials loaded a copy
       v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_to_lane63(v)), 63));
       rstd[r] = rsqrtf(v / (float)e.rs_dim + e.rs_eps);
     }
@@ -352,18 +364,31 @@ __global__ __launch_bounds__(pk_block(WS)) void qmv_packed_kernel(const uint16_t
   const int rot = nws > 1 ? (int)(blockIdx.x % (unsigned)nws) : 0;
   auto set_of = [&](int j) { const int jj = j + rot; return ws + (jj >= nws ? jj - nws : jj) * WS; };
   if constexpr (NP == 0) {
+    // Each step requests the next set, then computes the current one. The loop
+    // body has no branch (a branch between a request and its use lets the
+    // compiler sink the request past the compute before it, and a conditional
+    // request makes its wait counts cover both paths, so that the wait for the
+    // current set also waits for the next); the last one or two sets are
+    // computed after it. Buffer 0 holds set j at the top of the loop.
     if (nws > 0) issue(0, set_of(0));
-    if (nws > 1) issue(1, set_of(1));
     seg_table();
     if (rs && ws == 0) compute_rstd();
     int j = 0;
-    while (j < nws) {
-      if (j + 1 < nws && j != 0) issue(1, set_of(j + 1));
+    for (; j + 2 < nws; j += 2) {
+      issue(1, set_of(j + 1));
+      __builtin_amdgcn_sched_barrier(0);   // keep the request ahead of the compute
       compute(0);
-      if (j + 1 >= nws) break;
-      if (j + 2 < nws) issue(0, set_of(j + 2));
+      issue(0, set_of(j + 2));
+      __builtin_amdgcn_sched_barrier(0);
       compute(1);
-      j += 2;
+    }
+    if (j + 1 < nws) {
+      issue(1, set_of(j + 1));
+      __builtin_amdgcn_sched_barrier(0);
+      compute(0);
+      compute(1);
+    } else if (j < nws) {
+      compute(0);
     }
   } else {
 #pragma unroll
