@@ -441,9 +441,11 @@ def mixer_verify(copies=24, iters=96):
 
 def attn_verify(L=4, pos0=4348, copies=24, iters=96, kps=128):
     """The verify attention of one layer at the 9B shape (16 q / 4 kv heads of 256,
-    L = 4 rows at positions 4348..4351): q/k norm + RoPE + KV append, then the
-    split-K partial and combine kernels over rotating KV caches; bytes = the K
-    and V read for the 4352 keys (17.8 MB per call)."""
+    L = 4 rows at positions 4348..4351) over rotating KV caches: the fused decode
+    step (qvex_attention_decode: norms, RoPE and the KV append inside the split
+    kernel, then the combine), beside the two-launch path it replaces
+    (qvex_attn_qk_rope, then qvex_attention); bytes = the K and V read for the
+    4352 keys (17.8 MB per call)."""
     import torch
     from qvex import _C
     from qvex.kernels import _ptr, _stream
@@ -462,17 +464,27 @@ def attn_verify(L=4, pos0=4348, copies=24, iters=96, kps=128):
     need = int(_C.lib().qvex_attn_workspace_bytes(L, Hq, Hkv, D, pos0 + L, kps))
     ws = torch.empty((need + 3) // 4, dtype=torch.float32, device=dev)
 
-    def step(i):
+    def two_launch(i):
         c = i % copies
         _C.call("qvex_attn_qk_rope", _ptr(proj), proj.stride(0), _ptr(qn), _ptr(qn), _ptr(pos), L, Hq, Hkv, D, rot,
                 1e7, 1e-6, _ptr(q), _ptr(kc[c]), _ptr(vc[c]), cap, _stream())
-        _C.call("qvex_attention", _ptr(q), _ptr(kc[c]), _ptr(vc[c]), _ptr(pos), L, Hq, Hkv, D, cap, pos0 + L, kps,
+        _C.call("qvex_attention", _ptr(q), _ptr(kc[c]), _ptr(vc[c]), _ptr(pos), L, Hq, Hkv, D, cap, pos0 + L, pos0 + L, kps,
                 _ptr(proj), proj.stride(0), _ptr(out), _ptr(ws), ws.numel() * 4, _stream())
-    us = _event_time(step, iters)
+
+    from qvex.model import rope_table
+    tab = rope_table(rot, 1e7, cap, dev)
+
+    def fused(i):
+        c = i % copies
+        _C.call("qvex_attention_decode", _ptr(proj), proj.stride(0), _ptr(qn), _ptr(qn), _ptr(pos), L, Hq, Hkv, D,
+                rot, 1e-6, _ptr(tab), tab.shape[0], _ptr(kc[c]), _ptr(vc[c]), cap, pos0 + L, kps, _ptr(out), _ptr(ws),
+                ws.numel() * 4, _stream())
+    us2 = _event_time(two_launch, iters)
+    us = _event_time(fused, iters)
     nbytes = 2 * Hkv * (pos0 + L) * D * 2
-    return {"kernel": "qvex_attn_qk_rope + qvex_attention (partial + combine)", "ctx": pos0 + L, "us": round(us, 2),
+    return {"kernel": "qvex_attention_decode (decode partial + combine)", "ctx": pos0 + L, "us": round(us, 2),
             "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1), "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
-            "bytes": nbytes}
+            "bytes": nbytes, "two_launch_us": round(us2, 2)}
 
 
 # ---------------------------------------------------------------- end to end

@@ -395,12 +395,19 @@ int qvex_swiglu(const uint16_t* gu, uint16_t* out, int L, int I, void* stream);
 /* fp32 copy of bf16 values (Sampler.scores' astype(float32), engine/sampler.py:151). */
 int qvex_bf16_to_f32(const uint16_t* in, float* out, long n, void* stream);
 
-/* Attention input stage (engine/model.py:213-226): q and k rms-normalised per
+/* KV cache layouts (cap a multiple of 32; K and V each hold Hkv * cap * D bf16),
+ * tiled so that each wave load instruction of the attention kernels reads 1 KiB
+ * of consecutive bytes:
+ *   K: key p, dim d of kv head h at
+ *      (((h * cap/16 + p/16) * D/32 + d/32) * 64 + ((d % 32) / 8) * 16 + p % 16) * 8 + d % 8
+ *   V: (((h * cap/32 + p/32) * D + d) * 32 + p % 32
+ * (the reference keeps [B, Hkv, cap, D] arrays, engine/model.py:149-176).
+ *
+ * Attention input stage (engine/model.py:213-226): q and k rms-normalised per
  * head with q_norm / k_norm, NeoX-form RoPE on the first rot_dim dims at
  * positions *pos0 + l (pos0 a device int32), q written to q_out [L, Hq, D],
- * k appended to k_cache [Hkv, cap, D] and v to the dim-major v_cache
- * [Hkv, D, cap] at those positions (KVCache.update, engine/model.py:156-170).
- * proj row = [Hq x (q | gate) | Hkv x k | Hkv x v]. */
+ * k and v appended to the caches at those positions (KVCache.update,
+ * engine/model.py:156-170). proj row = [Hq x (q | gate) | Hkv x k | Hkv x v]. */
 int qvex_attn_qk_rope(const uint16_t* proj, long p_stride, const uint16_t* q_norm,
                       const uint16_t* k_norm, const int32_t* pos0, int L, int Hq, int Hkv, int D,
                       int rot_dim, float theta, float eps, uint16_t* q_out, uint16_t* k_cache,
@@ -411,13 +418,39 @@ int qvex_attn_qk_rope(const uint16_t* proj, long p_stride, const uint16_t* q_nor
  * rows: mx.fast.scaled_dot_product_attention + o * sigmoid(gate)
  * (engine/model.py:228-232). Split-K over keys_per_split keys per block
  * (a multiple of 128: 4 waves x 32 keys per step); max_keys bounds *pos0 + L,
- * and only the splits below *pos0 + L do work. D is 128 or 256.
- * workspace: qvex_attn_workspace_bytes(). */
+ * and only the splits below *pos0 + L do work. Splits below known_keys (keys
+ * visible on every call: max_keys for a one-off call, the position at capture
+ * for a captured graph) request their first keys before reading *pos0, the
+ * others read it first and load nothing when past it; results do not depend on
+ * known_keys. D is 128 or 256. workspace: qvex_attn_workspace_bytes(). */
 uint64_t qvex_attn_workspace_bytes(int L, int Hq, int Hkv, int D, int max_keys, int keys_per_split);
 int qvex_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                    const int32_t* pos0, int L, int Hq, int Hkv, int D, int cap, int max_keys,
-                   int keys_per_split, const uint16_t* gate, long gate_stride, uint16_t* out,
-                   void* workspace, uint64_t workspace_bytes, void* stream);
+                   int known_keys, int keys_per_split, const uint16_t* gate, long gate_stride,
+                   uint16_t* out, void* workspace, uint64_t workspace_bytes, void* stream);
+
+/* The decode / verify step of the attention block in two launches: the input
+ * stage of qvex_attn_qk_rope (q and k norms, RoPE, the cache append) folded
+ * into qvex_attention's split kernel, for L = 1..8 new tokens
+ * (engine/model.py:213-232 on the speculative verify, engine/speculative.py:86).
+ * Each split block computes its query rows and, where its keys include this
+ * call's, those keys itself; splits past *pos0 + L load nothing (a graph may be
+ * captured with max_keys = cap). rot_dim / 2 must be a multiple of D / 16.
+ * The rotation's (cos, sin) come from a table of qvex_rope_table() covering at
+ * least cap positions (the same values qvex_attn_qk_rope computes); L * rot_dim / 2
+ * must be at most 256. The norms' sums of squares run in another order than
+ * qvex_attn_qk_rope's, so cached keys can differ from its in the last bit.
+ * Workspace as qvex_attention's. */
+int qvex_attention_decode(const uint16_t* proj, long p_stride, const uint16_t* q_norm,
+                          const uint16_t* k_norm, const int32_t* pos0, int L, int Hq, int Hkv, int D,
+                          int rot_dim, float eps, const float* rope, int rope_rows, uint16_t* k_cache,
+                          uint16_t* v_cache, int cap, int max_keys, int keys_per_split, uint16_t* out,
+                          void* workspace, uint64_t workspace_bytes, void* stream);
+
+/* RoPE table for qvex_attention_decode: table[p][i] = (cos, sin) of
+ * p * theta^(-2i / rot_dim), p < rows, i < rot_dim / 2 (float pairs); the angle
+ * of mx.fast.rope(traditional=False) at position p (engine/model.py:222-225). */
+int qvex_rope_table(int rot_dim, float theta, int rows, float* table, void* stream);
 
 /* ------------------------------------------------------------------------
  * Device-side cycle bookkeeping (host side of decode(),

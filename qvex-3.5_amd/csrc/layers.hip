@@ -199,6 +199,21 @@ __global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t* __rest
     out[i] = bf16_to_f32(in[i]);
 }
 
+// KV cache layouts, tiled so that every load of the attention kernels reads
+// 1 KiB of consecutive bytes per wave instruction (cap a multiple of 32):
+//   K [Hkv][cap / 16][D / 32][64][8]: key p, dim d at block p / 16, step d / 32,
+//     lane 16 ((d % 32) / 8) + p % 16, element d % 8 -- exactly the B operand of
+//     the score MFMA (lane l: key l % 16, dims 32 step + 8 (l / 16) .. +7);
+//   V [Hkv][cap / 32][D][32]: key p, dim d at block p / 32, row d, column p % 32
+//     -- the B operand of the P.V MFMA (lane l: dim l % 16 of a 16-dim tile, keys
+//     8 (l / 16) .. +7 of a 32-key block).
+__host__ __device__ __forceinline__ size_t kt_index(int kh, int cap, int D, int p, int d) {
+  return ((((size_t)kh * (cap / 16) + p / 16) * (D / 32) + d / 32) * 64 + ((d % 32) / 8) * 16 + p % 16) * 8 + d % 8;
+}
+__host__ __device__ __forceinline__ size_t vt_index(int kh, int cap, int D, int p, int d) {
+  return (((size_t)kh * (cap / 32) + p / 32) * D + d) * 32 + p % 32;
+}
+
 // ---------------------------------------------------------------- attention: q/k norm + partial RoPE + KV append
 //
 // proj row l = [Hq x (q D | gate D) | Hkv x k D | Hkv x v D]. One wave per
@@ -256,13 +271,10 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
 #pragma unroll
     for (int i = 0; i < PER; ++i) dst[lane + 64 * i] = f32_to_bf16(x[i]);
   } else if (pos >= 0 && pos < cap) {
-    // K key-major [Hkv, cap, D]; V dim-major [Hkv, D, cap] (the P.V MFMA reads
-    // 8 consecutive keys of one dim per lane)
-    uint16_t* kd = k_cache + ((size_t)kh * cap + pos) * D;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      kd[lane + 64 * i] = f32_to_bf16(x[i]);
-      v_cache[((size_t)kh * D + lane + 64 * i) * cap + pos] = vv[i];
+      k_cache[kt_index(kh, cap, D, pos, lane + 64 * i)] = f32_to_bf16(x[i]);
+      v_cache[vt_index(kh, cap, D, pos, lane + 64 * i)] = vv[i];
     }
   }
 }
@@ -312,8 +324,8 @@ __device__ __forceinline__ att_bf16x8 as_att8(const u32x4 v) { return __builtin_
 template <int D>
 __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
-    const int32_t* __restrict__ pos0, int L, int Hq, int Hkv, int cap, int QT, int keys_per_split, float scale,
-    float* __restrict__ ws) {
+    const int32_t* __restrict__ pos0, int L, int Hq, int Hkv, int cap, int QT, int keys_per_split, int known_keys,
+    float scale, float* __restrict__ ws) {
   constexpr int KS = D / 32;     // MFMA steps over head dims
   constexpr int NT = D / 16;     // 16-dim output tiles of O
   const int kh = blockIdx.x, tile = blockIdx.y, split = blockIdx.z;
@@ -324,10 +336,11 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
   const uint16_t* kbase = k_cache + (size_t)kh * cap * D;
   const uint16_t* vbase = v_cache + (size_t)kh * D * cap;
 
-  // K rows kb + 16h + li and V columns kb + 8lg .. +7 of a 128-key window, issued
-  // together (clamped in bounds; keys past k_hi are masked out of the softmax and
-  // get P = 0). The first window does not depend on the device position, so its
-  // loads go out before the position is read.
+  // K keys kb + 16h + li and V keys kb + 8lg .. +7 of a 128-key window (tiled
+  // layouts above), issued together (keys past k_hi are masked out of the
+  // softmax and get P = 0). The first window does not depend on the device
+  // position, so its loads go out before the position is read (this kernel runs
+  // the prefill, where the grid holds only visible splits).
   // A operand: Q row li, dims step*32 + 8*lg .. +7 (the 1/sqrt(D) scale is applied
   // to the scores). Requested first: loads complete in order, so the scores can
   // start once Q and K are in while the V columns still stream
@@ -341,22 +354,29 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
   }
   u32x4 kr[2][KS], vr[NT];
   auto load_kv = [&](int kb) {
+    kb = min(kb, cap - 32);      // whole 32-key blocks in bounds (keys past k_hi are masked)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const uint16_t* kp = kbase + (size_t)min(kb + 16 * h + li, cap - 1) * D + 8 * lg;
+      const uint16_t* kp = kbase + ((size_t)(kb / 16 + h) * KS * 64 + lane) * 8;
 #pragma unroll
-      for (int s = 0; s < KS; ++s) kr[h][s] = load16(kp + 32 * s);
+      for (int s = 0; s < KS; ++s) kr[h][s] = load16(kp + (size_t)s * 512);
     }
-    const int kv0 = min(kb + 8 * lg, cap - 8);
+    const uint16_t* vp = vbase + (size_t)(kb / 32) * D * 32 + li * 32 + 8 * lg;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) vr[t] = load16(vbase + (size_t)(t * 16 + li) * cap + kv0);
+    for (int t = 0; t < NT; ++t) vr[t] = load16(vp + (size_t)t * 512);
   };
-  load_kv(k_lo + 32 * w);
+  // splits below known_keys hold visible keys on every call: their first
+  // window goes out before the position is read; the others read it first and
+  // exit without loading when their keys are past it (a captured graph spans the
+  // whole capacity)
+  const bool early = k_lo < known_keys;      // uniform over the block
+  if (early) load_kv(k_lo + 32 * w);
 
   const int p0 = *pos0;
   const int kend_tile = p0 + min(L, (tile + 1) * QT);
   const int k_hi = min(k_lo + keys_per_split, kend_tile);
   if (k_lo >= k_hi) return;      // split past the visible keys: the combine never reads it
+  if (!early) load_kv(k_lo + 32 * w);
 
   __shared__ __align__(16) uint32_t ps[4][16][20];   // per-wave P tile, bf16 pairs [row][key pair], 80-byte rows
   __shared__ float4 obv[4][NT][4][16];   // per-wave O for the merge: [wave][dim tile][row group][dim] x 4 rows
@@ -460,6 +480,368 @@ __global__ __launch_bounds__(256) void attn_mfma_partial_kernel(
   }
   __syncthreads();
   // thread (row group rg, dim d): rows 4 rg .. 4 rg + 3 of dim d, one b128 read per wave
+  for (int e = threadIdx.x; e < 4 * D; e += 256) {
+    const int rg = e / D, d = e % D, t = d >> 4, dl = d & 15;
+    float4 ov[4], fv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      ov[v] = obv[v][t][rg][dl];
+      fv[v] = *reinterpret_cast<const float4*>(&fac[v][4 * rg]);
+    }
+    const float a0 = ((ov[0].x * fv[0].x + ov[1].x * fv[1].x) + ov[2].x * fv[2].x) + ov[3].x * fv[3].x;
+    const float a1 = ((ov[0].y * fv[0].y + ov[1].y * fv[1].y) + ov[2].y * fv[2].y) + ov[3].y * fv[3].y;
+    const float a2 = ((ov[0].z * fv[0].z + ov[1].z * fv[1].z) + ov[2].z * fv[2].z) + ov[3].z * fv[3].z;
+    const float a3 = ((ov[0].w * fv[0].w + ov[1].w * fv[1].w) + ov[2].w * fv[2].w) + ov[3].w * fv[3].w;
+    float* op = wsb + 32 + (size_t)(4 * rg) * D + d;
+    op[0] = a0;
+    op[D] = a1;
+    op[2 * D] = a2;
+    op[3 * D] = a3;
+  }
+}
+
+// (cos, sin) of p * theta^(-2i/rot) for positions p < rows and i < rot / 2, as
+// qk_norm_rope_kernel evaluates them (same expressions, so the same bits):
+// table[p][i] = (cos, sin).
+__global__ __launch_bounds__(256) void rope_table_kernel(int rot, float theta, long n, float2* __restrict__ table) {
+  const long e = (long)blockIdx.x * 256 + threadIdx.x;
+  if (e >= n) return;
+  const int half = rot / 2;
+  const int p = (int)(e / half), i = (int)(e % half);
+  const float inv_freq = powf(theta, -2.0f * (float)i / (float)rot);
+  float sn, cs;
+  sincosf((float)p * inv_freq, &sn, &cs);
+  table[e] = make_float2(cs, sn);
+}
+
+// ---------------------------------------------------------------- attention: decode step, fused
+//
+// The decode / verify step (L <= 8 new tokens) as one launch plus the combine.
+// Each block (kv head, 16-row tile, split) first reads the token count, so the
+// splits past the visible keys exit before loading anything (a captured graph is
+// sized for the whole capacity), then does for itself what qk_norm_rope does:
+//   Q: its 16 rows from the projection row, RMS-normed (q_norm) and rotated, into
+//      LDS in the A-operand layout (16 threads per row, D / 16 dims each; the row
+//      sum of squares is a DPP sum over the 16 threads; rotation partners are
+//      rot / 2 dims apart, D / 16 divides rot / 2, so a partner is a lane shift);
+//   new keys p0 .. p0 + L - 1 (blocks whose split holds any): K normed (k_norm)
+//      and rotated, V copied, into LDS; the lanes whose cache keys are new take
+//      them from there, and the block of the split holding key p0 + j and of the
+//      tile (j / QT) whose rows first see it writes it to the caches (each key
+//      written once; every block computes the same bits).
+// Rounding follows qk_norm_rope: bf16(w * (x * rstd)), rotation in fp32 on
+// those values, bf16 result (the sum of squares runs in another order).
+// The key loop, softmax, merge and partials are attn_mfma_partial_kernel's.
+template <int D>
+__global__ __launch_bounds__(256) void attn_decode_kernel(
+    const int32_t* __restrict__ pos0, const uint16_t* __restrict__ proj, long p_stride,
+    const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm, uint16_t* __restrict__ k_cache,
+    uint16_t* __restrict__ v_cache, float* __restrict__ ws, const float2* __restrict__ rope, int rope_rows, int L,
+    int Hq, int Hkv, int cap, int QT, int keys_per_split, int rot, float eps, float scale) {
+  constexpr int KS = D / 32;       // MFMA steps over head dims
+  constexpr int NT = D / 16;       // 16-dim output tiles of O
+  constexpr int DPT = D / 16;      // dims per thread in the norm passes
+  constexpr int QROW = D + 8;      // bf16 per LDS row (16-byte pad: the 16 rows of an A read hit distinct banks)
+  const int kh = blockIdx.x, tile = blockIdx.y, split = blockIdx.z;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int li = lane & 15, lg = lane >> 4;
+  const int GQ = Hq / Hkv;
+  const int k_lo = split * keys_per_split;
+  const int p0 = *pos0;
+
+  // raw inputs of the norm pass, requested before the position is waited for:
+  // thread (row nr = tid / 16, slice nc = tid % 16) -> dims nc * DPT .. + DPT - 1
+  const int nr = threadIdx.x >> 4, nc = threadIdx.x & 15;
+  const int qg = nr / QT, qlq = tile * QT + nr % QT;
+  const bool qok = qg < GQ && qlq < L;
+  u32x4 qraw[DPT / 8], qwt[DPT / 8];
+  {
+    const uint16_t* src = proj + (size_t)(qok ? qlq : 0) * p_stride + (size_t)(kh * GQ + (qok ? qg : 0)) * 2 * D + nc * DPT;
+#pragma unroll
+    for (int i = 0; i < DPT / 8; ++i) {
+      qraw[i] = load16(src + 8 * i);
+      qwt[i] = load16(q_norm + nc * DPT + 8 * i);
+    }
+  }
+  // the new keys' raw K and V slices (row nr = token nr; rows past L re-read the
+  // last), loaded with no condition and before the K / V window: a later or
+  // conditional load would make the norm pass wait for the whole window
+  u32x4 kraw[DPT / 8], kwt[DPT / 8], vraw[DPT / 8];
+  {
+    const uint16_t* src = proj + (size_t)min(nr, L - 1) * p_stride + (size_t)Hq * 2 * D + (size_t)kh * D + nc * DPT;
+#pragma unroll
+    for (int i = 0; i < DPT / 8; ++i) {
+      kraw[i] = load16(src + 8 * i);
+      vraw[i] = load16(src + (size_t)Hkv * D + 8 * i);
+      kwt[i] = load16(k_norm + nc * DPT + 8 * i);
+    }
+  }
+
+  const int kend_tile = p0 + min(L, (tile + 1) * QT);
+  const int k_hi = min(k_lo + keys_per_split, kend_tile);
+  if (k_lo >= k_hi) return;      // split past the visible keys: the combine never reads it
+  const bool has_new = k_hi > max(p0, k_lo);   // this split holds keys of this call (uniform)
+  // rotation (cos, sin) of this call's tokens (the Q rows' positions are the new
+  // keys' positions) from the table, requested before the K / V window so that
+  // the norm pass waits only for them
+  // (no condition: a load under a branch is waited for at the end of the
+  // branch; the workspace stands in for the table when there is no rotation)
+  const int half = rot / 2;
+  const bool rthr = (int)threadIdx.x < L * half;
+  const float2 rcs = [&]() {
+    const int hs = max(half, 1), e = rthr ? (int)threadIdx.x : 0, j = e / hs, i = e % hs;
+    const float2* src = half > 0 ? rope + (size_t)min(p0 + j, rope_rows - 1) * half + i
+                                 : reinterpret_cast<const float2*>(ws);
+    return *src;
+  }();
+  __builtin_amdgcn_sched_barrier(0);     // the table load goes out before the K / V window
+
+  const uint16_t* kbase = k_cache + (size_t)kh * cap * D;
+  const uint16_t* vbase = v_cache + (size_t)kh * D * cap;
+  u32x4 kr[2][KS], vr[NT];
+  auto load_kv = [&](int kb) {
+    kb = min(kb, cap - 32);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint16_t* kp = kbase + ((size_t)(kb / 16 + h) * KS * 64 + lane) * 8;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) kr[h][s] = load16(kp + (size_t)s * 512);
+    }
+    const uint16_t* vp = vbase + (size_t)(kb / 32) * D * 32 + li * 32 + 8 * lg;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) vr[t] = load16(vp + (size_t)t * 512);
+  };
+  load_kv(k_lo + 32 * w);
+
+
+  // LDS: Q rows, new K / V rows and the rotation table while the keys are
+  // scored; the wave merge after the loop reuses it
+  constexpr int OBV_BYTES = 4 * NT * 4 * 16 * 16;
+  constexpr int TAB_BYTES = 2 * 8 * (D / 2) * 4;
+  constexpr int PRE_BYTES = (16 + 2 * 8) * QROW * 2 + TAB_BYTES;
+  constexpr int VT_BYTES = 2 * NT * 64 * 16;            // two waves' V operand tiles
+  constexpr int LOOP_BYTES = PRE_BYTES + VT_BYTES;
+  __shared__ __align__(16) unsigned char smem[OBV_BYTES > LOOP_BYTES ? OBV_BYTES : LOOP_BYTES];
+  uint16_t* qs = reinterpret_cast<uint16_t*>(smem);               // [16][QROW]
+  uint16_t* nk = qs + 16 * QROW;                                   // [8][QROW]
+  uint16_t* nv = nk + 8 * QROW;                                    // [8][QROW]
+  float* tab_c = reinterpret_cast<float*>(nv + 8 * QROW);          // [8][rot / 2] cos, then sin
+  float* tab_s = tab_c + 8 * (D / 2);
+  float4 (*obv)[NT][4][16] = reinterpret_cast<float4 (*)[NT][4][16]>(smem);
+  __shared__ __align__(16) uint32_t ps[4][16][20];   // per-wave P tile, bf16 pairs [row][key pair], 80-byte rows
+  __shared__ float ml[4][16][2];                      // per-wave (m, l)
+  __shared__ __align__(16) float fac[4][16];          // merge factors e^{m_w - m}
+
+  if (half > 0 && rthr) {
+    const int j = threadIdx.x / half, i = threadIdx.x % half;
+    tab_c[j * (D / 2) + i] = rcs.x;
+    tab_s[j * (D / 2) + i] = rcs.y;
+  }
+  __syncthreads();
+
+  // RMS norm + rotation of one 16-thread row slice (tok = its token's index in the call)
+  // (the row's 16 threads are lanes of one wave: the normed slices go to the
+  // row in LDS, each thread reads its rotation partner's slice back, and LDS
+  // runs in order within a wave)
+  auto norm_rope = [&](const u32x4 (&raw)[DPT / 8], const u32x4 (&wt)[DPT / 8], int tok, uint16_t* row) {
+    float x[DPT], wv[DPT];
+#pragma unroll
+    for (int i = 0; i < DPT / 8; ++i) {
+      const uint32_t r4[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+      const uint32_t w4[4] = {wt[i].x, wt[i].y, wt[i].z, wt[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        x[8 * i + 2 * j] = bf16_lo(r4[j]);
+        x[8 * i + 2 * j + 1] = bf16_hi(r4[j]);
+        wv[8 * i + 2 * j] = bf16_lo(w4[j]);
+        wv[8 * i + 2 * j + 1] = bf16_hi(w4[j]);
+      }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) ss = fmaf(x[e], x[e], ss);
+    ss = row16_sum(ss);
+    const float inv = rsqrtf(ss / (float)D + eps);
+    auto store = [&](uint16_t* dst) {
+#pragma unroll
+      for (int i = 0; i < DPT / 8; ++i) {
+        u32x4 o;
+        o.x = (uint32_t)f32_to_bf16(x[8 * i]) | ((uint32_t)f32_to_bf16(x[8 * i + 1]) << 16);
+        o.y = (uint32_t)f32_to_bf16(x[8 * i + 2]) | ((uint32_t)f32_to_bf16(x[8 * i + 3]) << 16);
+        o.z = (uint32_t)f32_to_bf16(x[8 * i + 4]) | ((uint32_t)f32_to_bf16(x[8 * i + 5]) << 16);
+        o.w = (uint32_t)f32_to_bf16(x[8 * i + 6]) | ((uint32_t)f32_to_bf16(x[8 * i + 7]) << 16);
+        *reinterpret_cast<u32x4*>(dst + 8 * i) = o;
+      }
+    };
+    const int d0 = nc * DPT;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) x[e] = bf16_to_f32(f32_to_bf16(wv[e] * (x[e] * inv)));
+    store(row + d0);
+    if (rot > 0) {
+      const int pd0 = d0 < half ? d0 + half : d0 - half;    // partner slice (half % DPT == 0)
+      const int i0 = d0 < rot ? d0 % half : 0;
+      u32x4 pr[DPT / 8];
+#pragma unroll
+      for (int i = 0; i < DPT / 8; ++i) pr[i] = *reinterpret_cast<const u32x4*>(row + (d0 < rot ? pd0 : d0) + 8 * i);
+#pragma unroll
+      for (int e = 0; e < DPT; ++e) {
+        const uint32_t pw = e % 8 < 2 ? pr[e / 8].x : e % 8 < 4 ? pr[e / 8].y : e % 8 < 6 ? pr[e / 8].z : pr[e / 8].w;
+        const float partner = (e & 1) ? bf16_hi(pw) : bf16_lo(pw);
+        const float cs = tab_c[tok * (D / 2) + i0 + e], sn = tab_s[tok * (D / 2) + i0 + e];
+        const int d = d0 + e;
+        const float r = d < half ? x[e] * cs - partner * sn : partner * sn + x[e] * cs;
+        x[e] = d < rot ? r : x[e];
+      }
+      store(row + d0);
+    }
+  };
+  if (qok) {
+    norm_rope(qraw, qwt, qlq, qs + nr * QROW);
+  } else {
+#pragma unroll
+    for (int i = 0; i < DPT / 8; ++i) *reinterpret_cast<u32x4*>(qs + nr * QROW + nc * DPT + 8 * i) = u32x4{0u, 0u, 0u, 0u};
+  }
+  if (has_new && nr < 8) {     // uniform per 16-thread row: the row16 sum stays within live lanes
+    if (nr < L) {
+      norm_rope(kraw, kwt, nr, nk + nr * QROW);
+#pragma unroll
+      for (int i = 0; i < DPT / 8; ++i) *reinterpret_cast<u32x4*>(nv + nr * QROW + nc * DPT + 8 * i) = vraw[i];
+    }
+  }
+  __syncthreads();
+
+  // the new keys to the caches: key p0 + j by the split holding it, in the tile whose rows first see it
+  if (has_new) {
+    for (int e = threadIdx.x; e < 8 * (D / 8); e += 256) {
+      const int j = e / (D / 8), c8 = (e % (D / 8)) * 8, p = p0 + j;
+      if (j < L && j / QT == tile && p >= k_lo && p < k_lo + keys_per_split && p < cap) {
+        *reinterpret_cast<u32x4*>(k_cache + kt_index(kh, cap, D, p, c8)) =
+            *reinterpret_cast<const u32x4*>(nk + j * QROW + c8);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v_cache[vt_index(kh, cap, D, p, c8 + q)] = nv[j * QROW + c8 + q];
+      }
+    }
+  }
+
+  u32x4 qa[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) qa[s] = *reinterpret_cast<const u32x4*>(qs + li * QROW + 32 * s + 8 * lg);
+
+  // the 4 rows this lane owns in accumulator layout: r = 4*lg + j
+  int rlim[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 4 * lg + j;
+    const int g = r / QT, lq = tile * QT + r % QT;
+    rlim[j] = (g < GQ && lq < L) ? p0 + lq : -1;     // last visible key, -1 = dead row
+  }
+
+  float m_r[4], l_r[4];
+  att_f32x4 o[NT];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { m_r[j] = -INFINITY; l_r[j] = 0.0f; }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) o[t] = att_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int n_it = (k_hi - k_lo + 127) / 128;          // uniform over the block
+  for (int it = 0; it < n_it; ++it) {
+    const int kb = k_lo + 128 * it + 32 * w;
+    if (it > 0) load_kv(kb);
+    if (has_new && kb + 31 >= p0 && kb < p0 + L) {     // this wave's window holds new keys (uniform per wave)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int j = kb + 16 * h + li - p0;
+        if (j >= 0 && j < L) {
+#pragma unroll
+          for (int s = 0; s < KS; ++s) kr[h][s] = *reinterpret_cast<const u32x4*>(nk + j * QROW + 32 * s + 8 * lg);
+        }
+      }
+      // V: the window's B operands through a wave-private LDS tile, the new
+      // keys' values written over theirs (at most two adjacent waves hold new
+      // keys: tiles w & 1), read back; LDS is in order within a wave
+      u32x4* vt = reinterpret_cast<u32x4*>(smem + PRE_BYTES) + (w & 1) * NT * 64;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) vt[t * 64 + lane] = vr[t];
+      uint16_t* vt16 = reinterpret_cast<uint16_t*>(vt);
+      for (int e = lane; e < L * D; e += 64) {
+        const int j = e / D, d = e % D, k = p0 + j - kb;
+        if (k >= 0 && k < 32) vt16[((d >> 4) * 64 + (k >> 3) * 16 + (d & 15)) * 8 + (k & 7)] = nv[j * QROW + d];
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) vr[t] = vt[t * 64 + lane];
+    }
+
+    att_f32x4 sc[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      att_f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_att8(qa[s]), as_att8(kr[h][s]), c, 0, 0, 0);
+      sc[h] = c;
+    }
+    float p[2][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int key = kb + 16 * h + li;
+        const bool vis = key < k_hi && key <= rlim[j];
+        sc[h][j] = vis ? sc[h][j] * scale : -INFINITY;
+        mx = fmaxf(mx, sc[h][j]);
+      }
+      mx = row16_max(mx);
+      const float mnew = fmaxf(m_r[j], mx);
+      const float corr = (mnew == -INFINITY) ? 1.0f : expf(m_r[j] - mnew);
+      float sum = 0.0f;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        p[h][j] = (sc[h][j] == -INFINITY) ? 0.0f : expf(sc[h][j] - mnew);
+        sum += p[h][j];
+      }
+      l_r[j] = l_r[j] * corr + row16_sum(sum);
+      m_r[j] = mnew;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) o[t][j] *= corr;
+    }
+    {
+      uint16_t* ps16 = reinterpret_cast<uint16_t*>(&ps[w][0][0]);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ps16[(4 * lg + j) * 40 + 16 * h + li] = f32_to_bf16(p[h][j]);
+    }
+    u32x4 pa;
+    __builtin_memcpy(&pa, &ps[w][li][4 * lg], sizeof(pa));
+#pragma unroll
+    for (int t = 0; t < NT; ++t) o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_att8(pa), as_att8(vr[t]), o[t], 0, 0, 0);
+  }
+
+  // merge the 4 waves as attn_mfma_partial_kernel does (the merge buffer reuses the Q / new-key LDS)
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = 4 * lg + j;
+    if (li == 0) { ml[w][r][0] = m_r[j]; ml[w][r][1] = l_r[j]; }
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) obv[w][t][lg][li] = make_float4(o[t][0], o[t][1], o[t][2], o[t][3]);
+  __syncthreads();
+  float* wsb = ws + (((size_t)kh * gridDim.y + tile) * gridDim.z + split) * 16 * (D + 2);
+  if (threadIdx.x < 16) {
+    const int r = threadIdx.x;
+    const float m = fmaxf(fmaxf(ml[0][r][0], ml[1][r][0]), fmaxf(ml[2][r][0], ml[3][r][0]));
+    float l = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float f = ml[v][r][0] == -INFINITY ? 0.0f : expf(ml[v][r][0] - m);
+      fac[v][r] = f;
+      l += ml[v][r][1] * f;
+    }
+    wsb[2 * r] = m;
+    wsb[2 * r + 1] = l;
+  }
+  __syncthreads();
   for (int e = threadIdx.x; e < 4 * D; e += 256) {
     const int rg = e / D, d = e % D, t = d >> 4, dl = d & 15;
     float4 ov[4], fv[4];
@@ -697,8 +1079,9 @@ extern "C" int qvex_attn_qk_rope(const uint16_t* proj, long p_stride, const uint
                                  void* stream) {
   QVEX_CHECK_ARG(proj && q_norm && k_norm && pos0 && q_out && k_cache && v_cache, "qvex_attn_qk_rope: null pointer");
   QVEX_CHECK_ARG(L >= 1 && Hq >= 1 && Hkv >= 1 && Hq % Hkv == 0 && D % 64 == 0 && D <= 512 && rot_dim >= 0 &&
-                     rot_dim <= 64 && rot_dim % 2 == 0 && cap >= 1,
-                 "qvex_attn_qk_rope: L=%d Hq=%d Hkv=%d D=%d rot=%d", L, Hq, Hkv, D, rot_dim);
+                     rot_dim <= 64 && rot_dim % 2 == 0 && cap >= 32 && cap % 32 == 0,
+                 "qvex_attn_qk_rope: L=%d Hq=%d Hkv=%d D=%d rot=%d cap=%d (cap a multiple of 32)", L, Hq, Hkv, D,
+                 rot_dim, cap);
   QVEX_CHECK_ARG(p_stride >= (long)Hq * 2 * D + 2L * Hkv * D, "qvex_attn_qk_rope: p_stride too small");
   decltype(&qk_norm_rope_kernel<1>) fn = nullptr;
   switch (D / 64) {
@@ -733,14 +1116,14 @@ extern "C" uint64_t qvex_attn_workspace_bytes(int L, int Hq, int Hkv, int D, int
 
 extern "C" int qvex_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                               const int32_t* pos0, int L, int Hq, int Hkv, int D, int cap, int max_keys,
-                              int keys_per_split, const uint16_t* gate, long gate_stride, uint16_t* out,
-                              void* workspace, uint64_t workspace_bytes, void* stream) {
+                              int known_keys, int keys_per_split, const uint16_t* gate, long gate_stride,
+                              uint16_t* out, void* workspace, uint64_t workspace_bytes, void* stream) {
   QVEX_CHECK_ARG(q && k_cache && v_cache && pos0 && gate && out && workspace, "qvex_attention: null pointer");
   QVEX_CHECK_ARG(L >= 1 && Hkv >= 1 && Hq % Hkv == 0 && Hq / Hkv <= ATT_ROWS, "qvex_attention: Hq=%d Hkv=%d", Hq, Hkv);
   QVEX_CHECK_ARG(D == 256 || D == 128, "qvex_attention: D=%d (128 or 256 supported)", D);
   QVEX_CHECK_ARG(max_keys >= 1 && max_keys <= cap && keys_per_split >= 128 && keys_per_split % 128 == 0 &&
-                     cap % 8 == 0 && cap >= 32,
-                 "qvex_attention: max_keys=%d cap=%d keys_per_split=%d (a multiple of 128; cap %% 8 == 0)", max_keys,
+                     cap % 32 == 0 && cap >= 32,
+                 "qvex_attention: max_keys=%d cap=%d keys_per_split=%d (a multiple of 128; cap %% 32 == 0)", max_keys,
                  cap, keys_per_split);
   const uint64_t need = qvex_attn_workspace_bytes(L, Hq, Hkv, D, max_keys, keys_per_split);
   QVEX_CHECK_ARG(workspace_bytes >= need, "qvex_attention: workspace %llu < %llu bytes",
@@ -755,20 +1138,86 @@ extern "C" int qvex_attention(const uint16_t* q, const uint16_t* k_cache, const 
   const dim3 pgrid(Hkv, ntile, nsplit);
   if (D == 256) {
     hipLaunchKernelGGL((attn_mfma_partial_kernel<256>), pgrid, dim3(256), 0, st, q, k_cache, v_cache, pos0, L, Hq,
-                       Hkv, cap, QT, keys_per_split, scale, (float*)workspace);
+                       Hkv, cap, QT, keys_per_split, known_keys, scale, (float*)workspace);
     QVEX_CHECK_LAUNCH("qvex_attention/partial");
     hipLaunchKernelGGL((attn_combine_kernel<256, ATT_DSPLIT>), dim3(Hkv, ntile, ATT_ROWS * ATT_DSPLIT), dim3(256), 0, st,
                        (const float*)workspace, nsplit, ntile, keys_per_split, pos0, L, Hq, Hkv, QT, gate,
                        gate_stride, out);
   } else {
     hipLaunchKernelGGL((attn_mfma_partial_kernel<128>), pgrid, dim3(256), 0, st, q, k_cache, v_cache, pos0, L, Hq,
-                       Hkv, cap, QT, keys_per_split, scale, (float*)workspace);
+                       Hkv, cap, QT, keys_per_split, known_keys, scale, (float*)workspace);
     QVEX_CHECK_LAUNCH("qvex_attention/partial");
     hipLaunchKernelGGL((attn_combine_kernel<128, ATT_DSPLIT>), dim3(Hkv, ntile, ATT_ROWS * ATT_DSPLIT), dim3(256), 0, st,
                        (const float*)workspace, nsplit, ntile, keys_per_split, pos0, L, Hq, Hkv, QT, gate,
                        gate_stride, out);
   }
   QVEX_CHECK_LAUNCH("qvex_attention/combine");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_rope_table(int rot_dim, float theta, int rows, float* table, void* stream) {
+  QVEX_CHECK_ARG(table && rot_dim >= 2 && rot_dim % 2 == 0 && rows >= 1, "qvex_rope_table: rot_dim=%d rows=%d", rot_dim,
+                 rows);
+  const long n = (long)rows * (rot_dim / 2);
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, rot_dim,
+                     theta, n, reinterpret_cast<float2*>(table));
+  QVEX_CHECK_LAUNCH("qvex_rope_table");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_attention_decode(const uint16_t* proj, long p_stride, const uint16_t* q_norm,
+                                     const uint16_t* k_norm, const int32_t* pos0, int L, int Hq, int Hkv, int D,
+                                     int rot_dim, float eps, const float* rope, int rope_rows, uint16_t* k_cache,
+                                     uint16_t* v_cache, int cap, int max_keys, int keys_per_split, uint16_t* out,
+                                     void* workspace, uint64_t workspace_bytes, void* stream) {
+  const char* fn = "qvex_attention_decode";
+  QVEX_CHECK_ARG(proj && q_norm && k_norm && pos0 && k_cache && v_cache && out && workspace && (rope || rot_dim == 0),
+                 "%s: null pointer", fn);
+  QVEX_CHECK_ARG(rot_dim == 0 || (rope_rows >= cap && qvex_aligned(rope, 8)),
+                 "%s: rope table of %d rows must cover cap=%d positions (8-byte aligned)", fn, rope_rows, cap);
+  QVEX_CHECK_ARG(L >= 1 && L <= 8 && Hkv >= 1 && Hq % Hkv == 0 && Hq / Hkv <= ATT_ROWS, "%s: L=%d (1..8) Hq=%d Hkv=%d",
+                 fn, L, Hq, Hkv);
+  QVEX_CHECK_ARG(D == 256 || D == 128, "%s: D=%d (128 or 256 supported)", fn, D);
+  QVEX_CHECK_ARG(rot_dim >= 0 && rot_dim <= D && rot_dim % 2 == 0 && (rot_dim == 0 || (rot_dim / 2) % (D / 16) == 0) &&
+                     L * (rot_dim / 2) <= 256,
+                 "%s: rot_dim=%d must be even, at most D, a multiple of 2 * D / 16 = %d, and L * rot_dim / 2 <= 256",
+                 fn, rot_dim, D / 8);
+  QVEX_CHECK_ARG(p_stride >= (long)Hq * 2 * D + 2L * Hkv * D && p_stride % 8 == 0,
+                 "%s: p_stride=%ld too small or not a multiple of 8", fn, p_stride);
+  QVEX_CHECK_ARG(qvex_aligned(proj, 16) && qvex_aligned(q_norm, 16) && qvex_aligned(k_norm, 16) &&
+                     qvex_aligned(k_cache, 16) && qvex_aligned(v_cache, 16),
+                 "%s: proj, norms and caches must be 16-byte aligned", fn);
+  QVEX_CHECK_ARG(max_keys >= 1 && max_keys <= cap && keys_per_split >= 128 && keys_per_split % 128 == 0 &&
+                     cap % 32 == 0 && cap >= 32,
+                 "%s: max_keys=%d cap=%d keys_per_split=%d (a multiple of 128; cap %% 32 == 0)", fn, max_keys, cap,
+                 keys_per_split);
+  const uint64_t need = qvex_attn_workspace_bytes(L, Hq, Hkv, D, max_keys, keys_per_split);
+  QVEX_CHECK_ARG(workspace_bytes >= need, "%s: workspace %llu < %llu bytes", fn, (unsigned long long)workspace_bytes,
+                 (unsigned long long)need);
+  const int GQ = Hq / Hkv;
+  const int QT = ATT_ROWS / GQ;
+  const int ntile = (L + QT - 1) / QT;
+  const int nsplit = (max_keys + keys_per_split - 1) / keys_per_split;
+  QVEX_CHECK_ARG(nsplit <= 65535, "%s: grid too large", fn);
+  const float scale = 1.0f / sqrtf((float)D);
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 pgrid(Hkv, ntile, nsplit);
+  if (D == 256) {
+    hipLaunchKernelGGL((attn_decode_kernel<256>), pgrid, dim3(256), 0, st, pos0, proj, p_stride, q_norm, k_norm,
+                       k_cache, v_cache, (float*)workspace, reinterpret_cast<const float2*>(rope), rope_rows, L, Hq,
+                       Hkv, cap, QT, keys_per_split, rot_dim, eps, scale);
+    QVEX_CHECK_LAUNCH("qvex_attention_decode/partial");
+    hipLaunchKernelGGL((attn_combine_kernel<256, ATT_DSPLIT>), dim3(Hkv, ntile, ATT_ROWS * ATT_DSPLIT), dim3(256), 0, st,
+                       (const float*)workspace, nsplit, ntile, keys_per_split, pos0, L, Hq, Hkv, QT, proj, p_stride, out);
+  } else {
+    hipLaunchKernelGGL((attn_decode_kernel<128>), pgrid, dim3(256), 0, st, pos0, proj, p_stride, q_norm, k_norm,
+                       k_cache, v_cache, (float*)workspace, reinterpret_cast<const float2*>(rope), rope_rows, L, Hq,
+                       Hkv, cap, QT, keys_per_split, rot_dim, eps, scale);
+    QVEX_CHECK_LAUNCH("qvex_attention_decode/partial");
+    hipLaunchKernelGGL((attn_combine_kernel<128, ATT_DSPLIT>), dim3(Hkv, ntile, ATT_ROWS * ATT_DSPLIT), dim3(256), 0, st,
+                       (const float*)workspace, nsplit, ntile, keys_per_split, pos0, L, Hq, Hkv, QT, proj, p_stride, out);
+  }
+  QVEX_CHECK_LAUNCH("qvex_attention_decode/combine");
   return QVEX_OK;
 }
 

@@ -62,7 +62,9 @@ SIGNATURES: dict[str, list] = {
     "qvex_swiglu": [P, P, I, I, P],
     "qvex_bf16_to_f32": [P, P, LNG, P],
     "qvex_attn_qk_rope": [P, LNG, P, P, P, I, I, I, I, I, F, F, P, P, P, I, P],
-    "qvex_attention": [P, P, P, P, I, I, I, I, I, I, I, P, LNG, P, P, U64, P],
+    "qvex_attention": [P, P, P, P, I, I, I, I, I, I, I, I, P, LNG, P, P, U64, P],
+    "qvex_attention_decode": [P, LNG, P, P, P, I, I, I, I, I, F, P, I, P, P, I, I, I, P, P, U64, P],
+    "qvex_rope_table": [I, F, I, P, P],
 }
 
 _lib: ctypes.CDLL | None = None

@@ -455,3 +455,30 @@ def spec_accept(target: torch.Tensor, draft: torch.Tensor | None, draft_ids: tor
             float(np.float32(top_p)), _ptr(n_accept), _ptr(out_token), S, k, V, _ptr(workspace),
             workspace.numel() * 4, _stream())
     return n_accept, out_token
+
+
+# ---------------------------------------------------------------- KV cache layouts
+
+def kv_tile_k(k: torch.Tensor) -> torch.Tensor:
+    """[Hkv, cap, D] keys -> the tiled K cache layout [Hkv, cap/16, D/32, 64, 8]
+    (key p, dim d at lane 16 ((d % 32) / 8) + p % 16 of block p / 16, step d / 32)."""
+    h, cap, D = k.shape
+    return k.reshape(h, cap // 16, 16, D // 32, 4, 8).permute(0, 1, 3, 4, 2, 5).contiguous()
+
+
+def kv_tile_v(v: torch.Tensor) -> torch.Tensor:
+    """[Hkv, cap, D] values -> the tiled V cache layout [Hkv, cap/32, D, 32]."""
+    h, cap, D = v.shape
+    return v.reshape(h, cap // 32, 32, D).permute(0, 1, 3, 2).contiguous()
+
+
+def kv_untile_k(kt: torch.Tensor) -> torch.Tensor:
+    """The tiled K cache [Hkv, cap/16, D/32, 64, 8] as [Hkv, cap, D] (a copy)."""
+    h, nb, ns = kt.shape[:3]
+    return kt.reshape(h, nb, ns, 4, 16, 8).permute(0, 1, 4, 2, 3, 5).reshape(h, nb * 16, ns * 32)
+
+
+def kv_untile_v(vt: torch.Tensor) -> torch.Tensor:
+    """The tiled V cache [Hkv, cap/32, D, 32] as [Hkv, cap, D] (a copy)."""
+    h, nb, d = vt.shape[:3]
+    return vt.permute(0, 1, 3, 2).reshape(h, nb * 32, d)

@@ -402,10 +402,33 @@ class CacheCounters:
         return c
 
 
+_ROPE_TABLES: dict = {}
+
+
+def rope_table(rot: int, theta: float, rows: int, device, capturing: bool = False) -> torch.Tensor | None:
+    """The (cos, sin) table [rows', rot/2, 2] of qvex_rope_table with rows' >=
+    rows, shared by every attention layer with the same rot and theta on a
+    device; grown (never inside a graph capture) when a larger cache appears."""
+    if rot == 0:
+        return None
+    key = (int(rot), float(theta), str(torch.device(device)))
+    t = _ROPE_TABLES.get(key)
+    if t is None or t.shape[0] < rows:
+        if capturing:
+            raise _C.QvexError(f"rope table for {rows} positions missing while a graph is captured "
+                               "(run one eager step with the cache first)")
+        t = torch.empty((int(rows), rot // 2, 2), dtype=torch.float32, device=device)
+        _C.call("qvex_rope_table", int(rot), float(theta), int(rows), _ptr(t), _stream())
+        _ROPE_TABLES[key] = t
+    return t
+
+
 class KVCache:
-    """bf16 K [Hkv, cap, D] and V [Hkv, D, cap] (dim-major, what the P.V MFMA
-    reads), preallocated (engine/model.py:149-176 grows [B, H, cap, D] arrays in
-    256-token steps instead). rollback(n) is offset -= n."""
+    """bf16 K and V of Hkv heads x cap keys x D dims in the tiled layouts the
+    attention kernels read 1 KiB at a time (K [Hkv, cap/16, D/32, 64, 8], V
+    [Hkv, cap/32, D, 32]; ``keys()`` / ``values()`` give [Hkv, cap, D] copies),
+    preallocated (engine/model.py:149-176 grows [B, H, cap, D] arrays in 256-token
+    steps instead). rollback(n) is offset -= n."""
 
     step = 256
 
@@ -416,8 +439,19 @@ class KVCache:
             index = 0
         self.counters, self.index = counters, index
         self.capacity = int(math.ceil(max(capacity, 1) / self.step) * self.step)
-        self.k = torch.zeros((n_kv, self.capacity, head_dim), dtype=torch.bfloat16, device=device)
-        self.v = torch.zeros((n_kv, head_dim, self.capacity), dtype=torch.bfloat16, device=device)
+        if head_dim % 32:
+            raise ValueError(f"KVCache: head_dim={head_dim} must be a multiple of 32")
+        cap = self.capacity
+        self.k = torch.zeros((n_kv, cap // 16, head_dim // 32, 64, 8), dtype=torch.bfloat16, device=device)
+        self.v = torch.zeros((n_kv, cap // 32, head_dim, 32), dtype=torch.bfloat16, device=device)
+
+    def keys(self) -> torch.Tensor:
+        """K as [Hkv, cap, D] (a copy)."""
+        return kernels.kv_untile_k(self.k)
+
+    def values(self) -> torch.Tensor:
+        """V as [Hkv, cap, D] (a copy)."""
+        return kernels.kv_untile_v(self.v)
 
     @property
     def offset(self) -> int:
@@ -516,6 +550,8 @@ class Attention:
 
     # keys per split of the decode / verify attention (a multiple of 128)
     decode_kps = 128
+    fused_decode = False    # qvex_attention_decode for 1..8 new tokens (slower per cycle: see its header)
+    late_splits = True      # captured: splits past the position at capture read it before loading
 
     def __init__(self, cfg: Config, p: dict):
         self.cfg = cfg
@@ -544,18 +580,29 @@ class Attention:
             raise _C.QvexError(f"KV cache full: offset {cache.offset} + {L} tokens > capacity {cache.capacity} "
                                "(make the cache with a larger max_context)")
         proj = self.qkv_proj(x)                                   # [L, H*2D + 2*Hkv*D]
-        q = torch.empty((L, H, D), dtype=torch.bfloat16, device=x.device)
         pos = cache.counters.ptr(cache.index)
-        _C.call("qvex_attn_qk_rope", _ptr(proj), proj.stride(0), _ptr(self.q_norm), _ptr(self.k_norm), pos,
-                L, H, Hkv, D, cfg.rotary_dim, float(cfg.rope_theta), float(cfg.rms_norm_eps), _ptr(q),
-                _ptr(cache.k), _ptr(cache.v), cache.capacity, _stream())
         # a captured call must work for every later context length: bound by capacity
         max_keys = cache.capacity if cache.counters.graph_mode else min(cache.capacity, cache.offset + L)
         kps = self.decode_kps if L <= 8 else 512   # keys per 4-wave block: verify spreads ~ctx/32 waves per kv head
         ws = self._workspace(L, max_keys, kps, x.device)
         o = torch.empty((L, H * D), dtype=torch.bfloat16, device=x.device)
-        _C.call("qvex_attention", _ptr(q), _ptr(cache.k), _ptr(cache.v), pos, L, H, Hkv, D, cache.capacity,
-                max_keys, kps, _ptr(proj), proj.stride(0), _ptr(o), _ptr(ws), ws.numel() * 4, _stream())
+        rot = cfg.rotary_dim
+        if self.fused_decode and L <= 8 and (rot == 0 or ((rot // 2) % (D // 16) == 0 and L * (rot // 2) <= 256)):
+            # norms, RoPE and the cache append inside the split kernel
+            tab = rope_table(rot, cfg.rope_theta, cache.capacity, x.device, cache.counters.graph_mode)
+            _C.call("qvex_attention_decode", _ptr(proj), proj.stride(0), _ptr(self.q_norm), _ptr(self.k_norm), pos,
+                    L, H, Hkv, D, rot, float(cfg.rms_norm_eps), _ptr(tab) if tab is not None else 0,
+                    tab.shape[0] if tab is not None else 0, _ptr(cache.k), _ptr(cache.v), cache.capacity, max_keys,
+                    kps, _ptr(o), _ptr(ws), ws.numel() * 4, _stream())
+        else:
+            q = torch.empty((L, H, D), dtype=torch.bfloat16, device=x.device)
+            _C.call("qvex_attn_qk_rope", _ptr(proj), proj.stride(0), _ptr(self.q_norm), _ptr(self.k_norm), pos,
+                    L, H, Hkv, D, rot, float(cfg.rope_theta), float(cfg.rms_norm_eps), _ptr(q),
+                    _ptr(cache.k), _ptr(cache.v), cache.capacity, _stream())
+            # keys below the position at capture stay visible on every replay
+            known = min(cache.offset, max_keys) if cache.counters.graph_mode and self.late_splits else max_keys
+            _C.call("qvex_attention", _ptr(q), _ptr(cache.k), _ptr(cache.v), pos, L, H, Hkv, D, cache.capacity,
+                    max_keys, known, kps, _ptr(proj), proj.stride(0), _ptr(o), _ptr(ws), ws.numel() * 4, _stream())
         cache.offset += L
         if resid is not None:
             return self.o_proj.residual(o, resid, norm_w, eps)

@@ -67,7 +67,7 @@ def test_attention_rejects_bad_split_or_dim(kps, D, err):
     buf = ctypes.create_string_buffer(1 << 12)
     p16 = (ctypes.addressof(buf) + 15) // 16 * 16
     with pytest.raises(_C.QvexError, match=err):
-        _C.call("qvex_attention", p16, p16, p16, p16, 4, 16, 4, D, 4096, 4096, kps, p16, 2 * D * 16, p16, p16,
+        _C.call("qvex_attention", p16, p16, p16, p16, 4, 16, 4, D, 4096, 4096, 4096, kps, p16, 2 * D * 16, p16, p16,
                 1 << 40, None)
 
 

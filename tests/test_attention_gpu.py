@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from qvex import _C
-from qvex.kernels import _ptr, _stream
+from qvex.kernels import _ptr, _stream, kv_tile_k, kv_tile_v
 
 DEV = "cuda:0"
 
@@ -35,18 +35,19 @@ def test_attention_matches_reference(L, Hq, Hkv, D, pos0, kps, spare):
     kc = g.standard_normal((Hkv, cap, D)).astype(np.float32)
     vc = g.standard_normal((Hkv, cap, D)).astype(np.float32)
     gate_rows = g.standard_normal((L, Hq, 2 * D)).astype(np.float32)
-    qt, kt = bf(q), bf(kc)
-    vt = bf(np.ascontiguousarray(vc.transpose(0, 2, 1)))          # dim-major V cache
+    qt, kt = bf(q), kv_tile_k(bf(kc))                              # tiled caches
+    vt = kv_tile_v(bf(vc))
     gt = bf(gate_rows.reshape(L, -1))
     pos = torch.tensor([pos0], dtype=torch.int32, device=DEV)
     out = torch.empty((L, Hq * D), dtype=torch.bfloat16, device=DEV)
     max_keys = cap if spare else pos0 + L
+    known = pos0 if spare else max_keys     # graph sizing: splits past the position read it first
     need = int(_C.lib().qvex_attn_workspace_bytes(L, Hq, Hkv, D, max_keys, kps))
     ws = torch.empty((need + 3) // 4, dtype=torch.float32, device=DEV)
-    _C.call("qvex_attention", _ptr(qt), _ptr(kt), _ptr(vt), _ptr(pos), L, Hq, Hkv, D, cap, max_keys, kps,
+    _C.call("qvex_attention", _ptr(qt), _ptr(kt), _ptr(vt), _ptr(pos), L, Hq, Hkv, D, cap, max_keys, known, kps,
             _ptr(gt), gt.stride(0), _ptr(out), _ptr(ws), ws.numel() * 4, _stream())
     torch.cuda.synchronize()
-    qf, kf, vf = tof(qt).astype(np.float64), tof(kt).astype(np.float64), vc.astype(np.float64)
+    qf, kf = tof(qt).astype(np.float64), tof(bf(kc)).astype(np.float64)
     vf = tof(bf(vc)).astype(np.float64)
     gf = tof(gt).astype(np.float64).reshape(L, Hq, 2 * D)[..., D:]
     ref = np.zeros((L, Hq, D))

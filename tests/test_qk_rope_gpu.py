@@ -14,7 +14,7 @@ import torch
 from oracle import model as om
 from oracle import round_bf16
 from qvex import _C
-from qvex.kernels import _ptr, _stream
+from qvex.kernels import _ptr, _stream, kv_untile_k, kv_untile_v
 
 DEV = "cuda:0"
 
@@ -54,8 +54,8 @@ def test_qk_rope_matches_fp64(L, Hq, Hkv, D, rot, pos0):
     eps, theta = 1e-6, 1e7
     pt, qnt, knt = bf(proj), bf(qn), bf(kn)          # held: the kernel runs after this line
     q_out = torch.empty((L, Hq, D), dtype=torch.bfloat16, device=DEV)
-    kc = torch.zeros((Hkv, cap, D), dtype=torch.bfloat16, device=DEV)
-    vc = torch.zeros((Hkv, D, cap), dtype=torch.bfloat16, device=DEV)
+    kc = torch.zeros((Hkv, cap // 16, D // 32, 64, 8), dtype=torch.bfloat16, device=DEV)   # tiled caches
+    vc = torch.zeros((Hkv, cap // 32, D, 32), dtype=torch.bfloat16, device=DEV)
     pos = torch.tensor([pos0], dtype=torch.int32, device=DEV)
     _C.call("qvex_attn_qk_rope", _ptr(pt), pt.stride(0), _ptr(qnt), _ptr(knt), _ptr(pos), L, Hq, Hkv, D, rot,
             theta, eps, _ptr(q_out), _ptr(kc), _ptr(vc), cap, _stream())
@@ -65,7 +65,7 @@ def test_qk_rope_matches_fp64(L, Hq, Hkv, D, rot, pos0):
     v = proj[:, Hq * 2 * D + Hkv * D:].reshape(L, Hkv, D)
     worst = 0.0
     for name, x, w, got in (("q", qg, qn, tof(q_out)),
-                            ("k", k, kn, tof(kc)[:, pos0:pos0 + L].transpose(1, 0, 2))):
+                            ("k", k, kn, tof(kv_untile_k(kc))[:, pos0:pos0 + L].transpose(1, 0, 2))):
         n = om.rms_norm(x, w, eps)                                   # [L, heads, D] bf16 values
         ref, pair = rope64(n.transpose(1, 0, 2), pos0, rot, theta)
         ref, pair = ref.transpose(1, 0, 2), pair.transpose(1, 0, 2)
@@ -74,5 +74,5 @@ def test_qk_rope_matches_fp64(L, Hq, Hkv, D, rot, pos0):
         err = np.abs(got[..., :rot] - ref[..., :rot]) / pair[..., :rot]
         worst = max(worst, float(err.max()))
         assert np.all(err <= 2.0 ** -7), f"{name}: rotated dims, worst {err.max():.3e} of the pair norm"
-    np.testing.assert_array_equal(tof(vc)[:, :, pos0:pos0 + L].transpose(2, 0, 1), v)
+    np.testing.assert_array_equal(tof(kv_untile_v(vc))[:, pos0:pos0 + L].transpose(1, 0, 2), v)
     print(f"L={L} D={D} rot={rot} pos={pos0}: worst rotated error {worst:.3e} of the pair norm")
