@@ -354,7 +354,11 @@ __global__ __launch_bounds__(FUSED_THREADS) void gdn_decode_fused_kernel(GdnFuse
 // and the out_proj applies the scale to each 128-column segment of its input
 // as it stages it (qvex_qmv_w4g64_packed_resid with a segment scale). The conv
 // ring and state ring are bitwise those of the other forms.
-template <int NB>
+// TT: the token count (p.T == TT, 1..FUSED_TMAX) as a compile-time constant:
+// the token loop is unrolled into one branch-free block, so one token's output
+// dot, gated-norm input and snapshot overlap the next token's state update (the
+// same operations in the same order as a loop: the same bits).
+template <int NB, int TT>
 __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArgs p, float* ss_parts) {
   constexpr int RB = DK / NB;            // rows per block
   constexpr int NTH = 16 * RB;           // threads
@@ -366,7 +370,7 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArg
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int grp = threadIdx.x >> 4, l16 = threadIdx.x & 15;
   const int dv = b * RB + grp;
-  const int T = p.T;
+  constexpr int T = TT;
   const long p0 = *p.counter;
   const int cur = (int)(((p0 % p.n_slots) + p.n_slots) % p.n_slots);
   const int rbase = (int)(((p0 % p.R) + p.R) % p.R);
@@ -394,17 +398,15 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArg
     aa_raw = p.proj[(size_t)t * p.p_stride + p.ab_off + p.Hv + hv];
     bb_raw = p.proj[(size_t)t * p.p_stride + p.ab_off + hv];
   }
-  // this row's z for every token and its norm weight (the row's lane 0 uses
-  // them), loaded unconditionally (rows past T re-read row T - 1) into one
-  // register each, so the loads go out together and are first waited for in
-  // the recurrence
+  // this row's z for every token and its norm weight, in every lane of the
+  // row (the unrolled token loop has all 16 store the row's output; the 16
+  // loads of one address are one request), rows past T re-reading row T - 1,
+  // one register each, so the loads go out together and are first waited for
+  // in the recurrence
   uint32_t zr[FUSED_TMAX];
-  uint32_t wr_raw = 0;
-  if (l16 == 0) {
-    wr_raw = p.norm_w[dv];
+  const uint32_t wr_raw = p.norm_w[dv];
 #pragma unroll
-    for (int t = 0; t < FUSED_TMAX; ++t) zr[t] = p.proj[(size_t)min(t, T - 1) * p.p_stride + p.z_off + hv * DK + dv];
-  }
+  for (int t = 0; t < FUSED_TMAX; ++t) zr[t] = p.proj[(size_t)min(t, T - 1) * p.p_stride + p.z_off + hv * DK + dv];
   // 1. conv + silu. Two kinds of task, each one wave with all of its loads
   // issued in its own iteration: a token's q and k heads (lane: channels 2l,
   // 2l+1 of both, each head normed by its own wave sum as in
@@ -504,7 +506,7 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArg
   __syncthreads();
 
   // 2. recurrence; u of this block's rows to `out`, y to LDS for the sums
-  for (int t = 0; t < T; ++t) {
+  auto token = [&](int t) {
     const float g = gb_s[0][t];
     const float beta = gb_s[1][t];
     float kk[8], qq[8];
@@ -528,27 +530,34 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArg
       o = fmaf(st[i], qq[i], o);
     }
     o = row16_allsum(o);
-    if (l16 == 0) {
+    // the row's lane 0 sum (the lanes' sums may differ in rounding) in all 16
+    // lanes, which store the same value, so the unrolled loop stays one block
+    o = __shfl(o, lane & ~15, 64);
+    {
       const float y = bf16_to_f32(f32_to_bf16(o));
       ys[t][grp] = y;
       uint32_t zb = zr[0];
 #pragma unroll
       for (int i = 1; i < FUSED_TMAX; ++i) zb = t == i ? zr[i] : zb;
-      asm volatile("" : "+v"(zb), "+v"(wr_raw));
+      uint32_t wb = wr_raw;
+      asm volatile("" : "+v"(zb), "+v"(wb));
       const float zt = bf16_to_f32((uint16_t)zb);
-      p.out[(size_t)t * p.Hv * DK + hv * DK + dv] = f32_to_bf16(silu(zt) * (bf16_to_f32((uint16_t)wr_raw) * y));
+      p.out[(size_t)t * p.Hv * DK + hv * DK + dv] = f32_to_bf16(silu(zt) * (bf16_to_f32((uint16_t)wb) * y));
     }
-    if (p.snap_every || t == T - 1) {
-      float* dstp = p.state + wrap_add(cur, (1 + t) % p.n_slots, p.n_slots) * slot_stride + row_off;
-      u32x4 o0, o1;
-      o0.x = __float_as_uint(st[0]); o0.y = __float_as_uint(st[1]);
-      o0.z = __float_as_uint(st[2]); o0.w = __float_as_uint(st[3]);
-      o1.x = __float_as_uint(st[4]); o1.y = __float_as_uint(st[5]);
-      o1.z = __float_as_uint(st[6]); o1.w = __float_as_uint(st[7]);
-      __builtin_nontemporal_store(o0, reinterpret_cast<u32x4*>(dstp));
-      __builtin_nontemporal_store(o1, reinterpret_cast<u32x4*>(dstp + 4));
-    }
-  }
+    // without per-token snapshots every token stores to the final slot (the
+    // last store wins): no branch in the unrolled form
+    const int slot = (p.snap_every ? 1 + t : T) % p.n_slots;
+    float* dstp = p.state + wrap_add(cur, slot, p.n_slots) * slot_stride + row_off;
+    u32x4 o0, o1;
+    o0.x = __float_as_uint(st[0]); o0.y = __float_as_uint(st[1]);
+    o0.z = __float_as_uint(st[2]); o0.w = __float_as_uint(st[3]);
+    o1.x = __float_as_uint(st[4]); o1.y = __float_as_uint(st[5]);
+    o1.z = __float_as_uint(st[6]); o1.w = __float_as_uint(st[7]);
+    __builtin_nontemporal_store(o0, reinterpret_cast<u32x4*>(dstp));
+    __builtin_nontemporal_store(o1, reinterpret_cast<u32x4*>(dstp + 4));
+  };
+#pragma unroll
+  for (int t = 0; t < TT; ++t) token(t);
   __syncthreads();
   // 3. per token, the sum of y^2 over this block's rows: one wave per token,
   // lane r < RB squares row r, a DPP sum over the wave
@@ -646,6 +655,26 @@ extern "C" int qvex_gdn_decode_fused(const uint16_t* proj, long p_stride, uint16
   return QVEX_OK;
 }
 
+template <int NB, int TT>
+void launch_split_t(dim3 grid, hipStream_t st, const GdnFusedArgs& p, float* ss_parts) {
+  hipLaunchKernelGGL((gdn_decode_split_kernel<NB, TT>), grid, dim3(2048 / NB), 0, st, p, ss_parts);
+}
+
+template <int NB>
+void launch_split(dim3 grid, int T, hipStream_t st, const GdnFusedArgs& p, float* ss_parts) {
+  static_assert(FUSED_TMAX == 8, "one instantiation per token count");
+  switch (T) {
+    case 1: launch_split_t<NB, 1>(grid, st, p, ss_parts); break;
+    case 2: launch_split_t<NB, 2>(grid, st, p, ss_parts); break;
+    case 3: launch_split_t<NB, 3>(grid, st, p, ss_parts); break;
+    case 4: launch_split_t<NB, 4>(grid, st, p, ss_parts); break;
+    case 5: launch_split_t<NB, 5>(grid, st, p, ss_parts); break;
+    case 6: launch_split_t<NB, 6>(grid, st, p, ss_parts); break;
+    case 7: launch_split_t<NB, 7>(grid, st, p, ss_parts); break;
+    case 8: launch_split_t<NB, 8>(grid, st, p, ss_parts); break;
+  }
+}
+
 extern "C" int qvex_gdn_decode_split(const uint16_t* proj, long p_stride, uint16_t* conv_ring, int ring_rows,
                                      const int32_t* counter, const uint16_t* conv_w, int kernel_size, int conv_dim,
                                      int key_dim, float q_scale, float k_scale, float qk_eps, const float* A_log,
@@ -682,9 +711,9 @@ extern "C" int qvex_gdn_decode_split(const uint16_t* proj, long p_stride, uint16
                  snap_every ? 1 : 0, norm_w, 0.0f, u_out, T, Hk, Hv};
   const dim3 grid(Hv * blocks_per_head);
   switch (blocks_per_head) {
-    case 2: hipLaunchKernelGGL(gdn_decode_split_kernel<2>, grid, dim3(1024), 0, (hipStream_t)stream, p, ss_parts); break;
-    case 4: hipLaunchKernelGGL(gdn_decode_split_kernel<4>, grid, dim3(512), 0, (hipStream_t)stream, p, ss_parts); break;
-    case 8: hipLaunchKernelGGL(gdn_decode_split_kernel<8>, grid, dim3(256), 0, (hipStream_t)stream, p, ss_parts); break;
+    case 2: launch_split<2>(grid, T, (hipStream_t)stream, p, ss_parts); break;
+    case 4: launch_split<4>(grid, T, (hipStream_t)stream, p, ss_parts); break;
+    case 8: launch_split<8>(grid, T, (hipStream_t)stream, p, ss_parts); break;
   }
   QVEX_CHECK_LAUNCH(fn);
   return QVEX_OK;
