@@ -82,7 +82,7 @@ uint64_t qvex_w4g64_packed_bytes(int N, int K);
 int qvex_w4g64_pack(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                     int N, int K, void* packed, uint64_t packed_bytes, void* stream);
 
-/* y[M, N] = x[M, K] @ dequant(W)^T from the packed copy, M = 1..4: the product
+/* y[M, N] = x[M, K] @ dequant(W)^T from the packed copy, M = 1..8: the product
  * of mx.quantized_matmul(x, w, scales, biases, transpose=True, group_size=64,
  * bits=4) in QLinear.__call__ (engine/model.py:87-91), on MFMA with fully
  * coalesced record loads. The tile depends on (N, K) only, so each output row

@@ -1,4 +1,4 @@
-// 4-bit group-64 skinny GEMM (M = 1..4 activation rows) on a tile-packed copy of
+// 4-bit group-64 skinny GEMM (M = 1..8 activation rows) on a tile-packed copy of
 // the MLX weights, for the verify / draft matmuls of the decode cycle.
 //
 // Reference semantics: mx.quantized_matmul(transpose=True, group_size=64, bits=4)
@@ -159,7 +159,7 @@ constexpr int pk_block(int WS) { return WS >= 4 ? 64 * WS : 256; }   // WS = 16:
 // double-buffered product runs ~30 k waves in many rounds and needs 4 resident
 // (at most 128 VGPRs: 84.9 against 91.8 us at M = 1 when the compiler takes 172);
 // the others run one round of waves and keep the compiler's choice.
-constexpr int pk_min_waves(int TN, int WS, int NP) { return TN == 2 && WS == 4 && NP == 0 ? 4 : 1; }
+constexpr int pk_min_waves(int TN, int WS, int NP, int MH) { return TN == 2 && WS == 4 && NP == 0 && MH == 1 ? 4 : 1; }
 
 // TN 16-row tiles per wave share each activation operand; WS waves of a block
 // split the sets of the same tiles (set ws, ws + WS, ...) and combine through
@@ -175,8 +175,8 @@ constexpr int pk_min_waves(int TN, int WS, int NP) { return TN == 2 && WS == 4 &
 // would) and writes bf16(silu(g) * u) to y [M, N/2]. MODE 2: the head-segment
 // scale of PkEpi (a mode of its own so that the other kernels keep their
 // registers). MODE 0: plain.
-template <int TN, int WS, int NP, int MODE>
-__global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk_min_waves(TN, WS, NP)))) void qmv_packed_kernel(const uint16_t* __restrict__ x,
+template <int TN, int WS, int NP, int MODE, int MH>
+__global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk_min_waves(TN, WS, NP, MH)))) void qmv_packed_kernel(const uint16_t* __restrict__ x,
                                                                    const uint8_t* __restrict__ packed,
                                                                    uint16_t* __restrict__ y, int M, int N, int K,
                                                                    PkEpi e) {
@@ -189,31 +189,37 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
   const int tiles = (N + PK_TILE - 1) / PK_TILE;
   const int c = lane >> 4, i16 = lane & 15;
   const int am = i16 & 3;
-  const bool part = (i16 >> 2) == c && am < M;   // A row i16 = (group slot i16/4, activation row i16%4)
+  constexpr int MR = 4 * MH;                     // activation rows: MH halves of 4
   const int tile0 = (blockIdx.x * RG + rg) * TN;
 
   // per wave: [activation row][32 chunks of 8 bf16], then 8 zero chunks that the
-  // lanes outside the block diagonal read in place of x (no predicated reads)
-  __shared__ u32x4 xslot[NWAVE][4 * 32 + 8];
+  // lanes outside the block diagonal read in place of x (no predicated reads).
+  // Half h's A row i16 = (group slot i16/4, activation row 4h + i16%4).
+  __shared__ u32x4 xslot[NWAVE][MR * 32 + 8];
   u32x4* slot = xslot[wave];
-  if (lane < 8) slot[4 * 32 + lane] = u32x4{0u, 0u, 0u, 0u};
-  const u32x4* arow = part ? slot + am * 32 + c * 8 : slot + 4 * 32;
+  if (lane < 8) slot[MR * 32 + lane] = u32x4{0u, 0u, 0u, 0u};
+  const u32x4* arow[MH];
+#pragma unroll
+  for (int h = 0; h < MH; ++h) {
+    const bool part = (i16 >> 2) == c && 4 * h + am < M;
+    arow[h] = part ? slot + (4 * h + am) * 32 + c * 8 : slot + MR * 32;
+  }
 
   const uint32_t magic = opaque_vgpr(kMagic);
   const uint32_t nib = opaque_sgpr(kNib);
   // four distinct registers (the compiler would otherwise keep one and copy it per step)
   const bf16x8_t ones = as_bf16x8(opaque_vgpr(kOnes), opaque_vgpr(kOnes), opaque_vgpr(kOnes), opaque_vgpr(kOnes));
 
-  float acc[TN][4];
+  float acc[TN][MR];
 #pragma unroll
   for (int t = 0; t < TN; ++t)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) acc[t][r] = 0.0f;
+    for (int r = 0; r < MR; ++r) acc[t][r] = 0.0f;
 
   constexpr int NB = NP > 0 ? NP : 2;
   u32x4 wb[NB][TN][2];
   uint32_t sb[NB][TN];
-  u32x4 xr[NB][2];
+  u32x4 xr[NB][2 * MH];
   int sgs[NB];
 
   // activation slice loader: lane L of load q covers row 2q + L/32, chunk L%32
@@ -221,27 +227,27 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
   constexpr bool SWIGLU = MODE == 1;
   constexpr bool seg = MODE == 2;
 
-  // head-segment partials: thread i sums pair (head i / 4, row i % 4).
+  // head-segment partials: thread i sums pair (head i / MR, row i % MR).
   // Epilogue inputs are loaded from clamped (always valid) addresses with no
   // condition, and the entries that do not exist are dropped where the values
   // are used: a conditional load makes the compiler wait for it at the end of
   // the condition, before the weight loads go out.
-  __shared__ __align__(16) float seg_tab[seg ? 256 : 4];
+  __shared__ __align__(16) float seg_tab[seg ? 64 * MR : 4];
   const int H = K / 128;
   float segv[8];
   if constexpr (seg) {
-    const int sh = min((int)threadIdx.x >> 2, H - 1), sr = min((int)threadIdx.x & 3, M - 1);
+    const int sh = min((int)threadIdx.x / MR, H - 1), sr = min((int)threadIdx.x % MR, M - 1);
 #pragma unroll
     for (int b = 0; b < 8; ++b) segv[b] = e.seg_ss[((size_t)sr * H + sh) * e.seg_nb + min(b, e.seg_nb - 1)];
   }
   auto seg_table = [&]() {
     if constexpr (seg) {
-      if ((int)threadIdx.x < 4 * H) {
+      if ((int)threadIdx.x < MR * H) {
         float v = segv[0];
 #pragma unroll
         for (int b = 1; b < 8; ++b)
           if (b < e.seg_nb) v += segv[b];
-        seg_tab[threadIdx.x] = (int)(threadIdx.x & 3) < M ? rsqrtf(v / 128.0f + e.seg_eps) : 1.0f;
+        seg_tab[threadIdx.x] = (int)(threadIdx.x % MR) < M ? rsqrtf(v / 128.0f + e.seg_eps) : 1.0f;
       }
       __syncthreads();
     }
@@ -249,17 +255,17 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
 
   // epilogue inputs, requested before the weights so their latency hides
   const bool rs = e.rs_parts != nullptr, prod = e.resid != nullptr;
-  u32x4 rsp[4];
+  u32x4 rsp[MR];
   if (rs && ws == 0) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < MR; ++r)
       rsp[r] = load16(e.rs_parts + (size_t)min(r, M - 1) * e.rs_nparts + min(4 * lane, e.rs_nparts - 4));
   }
   // the plain epilogue gives lane L row L / 16 and column L % 16 of each tile
   const int er = lane >> 4, ei = lane & 15;
   // (loaded by every wave, with x standing in when there is no residual: under a
   // branch the compiler converts them as soon as they arrive, which waits)
-  uint16_t rsd[TN], nw[TN];
+  uint16_t rsd[MH][TN], nw[TN];
   {
     const uint16_t* rp = prod ? e.resid : x;
     const uint16_t* wp = prod ? e.norm_w : x;
@@ -267,20 +273,29 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
     for (int t = 0; t < TN; ++t) {
       const int nc = min((tile0 + t) * PK_TILE + ei, N - 1);   // columns past N and rows past M are never stored
       nw[t] = wp[prod ? nc : 0];
-      rsd[t] = rp[prod ? (size_t)min(er, M - 1) * N + nc : 0];
+#pragma unroll
+      for (int h = 0; h < MH; ++h) rsd[h][t] = rp[prod ? (size_t)min(4 * h + er, M - 1) * N + nc : 0];
     }
   }
   // consumer scale: summed as soon as the partials are in (they were requested
   // first), off the tail of the kernel; a DPP sum into lane 63, read back
-  float rstd[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  // rstd[r] for the SwiGLU epilogue, rs_row[mh] = rstd[4 mh + er] for the plain
+  // one (selected as the sums complete: an index by the lane's row would make
+  // the compiler keep the array in scratch)
+  float rstd[MR], rs_row[MH];
+#pragma unroll
+  for (int r = 0; r < MR; ++r) rstd[r] = 1.0f;
+#pragma unroll
+  for (int mh = 0; mh < MH; ++mh) rs_row[mh] = 1.0f;
   auto compute_rstd = [&]() {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < MR; ++r) {
       float v = ((__uint_as_float(rsp[r].x) + __uint_as_float(rsp[r].y)) + __uint_as_float(rsp[r].z)) +
                 __uint_as_float(rsp[r].w);
       v = 4 * lane < e.rs_nparts ? v : 0.0f;   // lanes past the partials loaded a copy
       v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_to_lane63(v)), 63));
       rstd[r] = rsqrtf(v / (float)e.rs_dim + e.rs_eps);
+      rs_row[r / 4] = (r % 4) == er ? rstd[r] : rs_row[r / 4];
     }
   };
 
@@ -296,7 +311,7 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
     // rows m >= M re-read row M - 1: only the block-diagonal lanes of rows < M
     // ever read the slot, so no zero fill (and no predicated load) is needed
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < 2 * MH; ++q) {
       const int m = min(2 * q + xm0, M - 1);
       xr[buf][q] = load16(x + (size_t)m * K + (size_t)gs * PK_SET + 8 * xch);
     }
@@ -304,11 +319,15 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
   };
 
   auto compute = [&](int buf) {
-    slot[xm0 * 32 + xch] = xr[buf][0];
-    slot[(2 + xm0) * 32 + xch] = xr[buf][1];
-    f32x4_t C[TN], CX = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int t = 0; t < TN; ++t) C[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int q = 0; q < 2 * MH; ++q) slot[(2 * q + xm0) * 32 + xch] = xr[buf][q];
+    f32x4_t C[MH][TN], CX[MH];
+#pragma unroll
+    for (int mh = 0; mh < MH; ++mh) {
+      CX[mh] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int t = 0; t < TN; ++t) C[mh][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
 #pragma unroll
     for (int s = 0; s < 8; s += 2) {
       // steps s and s + 1 use adjacent words of a tile: one 64-bit shift moves
@@ -325,24 +344,30 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
                               and_or((uint32_t)(p8 >> (32 * h)), nib, magic), and_or((uint32_t)(p12 >> (32 * h)), nib, magic));
       }
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, arow[s + h]);
-        CX = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, CX, 0, 0, 0);
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int t = 0; t < TN; ++t) C[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[t][h], C[t], 0, 0, 0);
-      }
+        for (int mh = 0; mh < MH; ++mh) {   // both row halves share the dequantized weights
+          const bf16x8_t a = __builtin_bit_cast(bf16x8_t, arow[mh][s + h]);
+          CX[mh] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, CX[mh], 0, 0, 0);
+#pragma unroll
+          for (int t = 0; t < TN; ++t) C[mh][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[t][h], C[mh][t], 0, 0, 0);
+        }
     }
     if constexpr (seg) {
-      // lane (c, i16) holds group slot c: head 2 gs + c / 2 of rows 0..3
-      const float4 gt = reinterpret_cast<const float4*>(seg_tab)[2 * sgs[buf] + (c >> 1)];
-      const float g[4] = {gt.x, gt.y, gt.z, gt.w};
+      // lane (c, i16) holds group slot c: head 2 gs + c / 2 of rows 4 mh .. 4 mh + 3
 #pragma unroll
-      for (int t = 0; t < TN; ++t) {
-        const float sc = bf16_to_f32((uint16_t)(sb[buf][t] & 0xffffu));
-        const float bi = bf16_to_f32((uint16_t)(sb[buf][t] >> 16));
-        const float bo = fmaf(-128.0f, sc, bi);
+      for (int mh = 0; mh < MH; ++mh) {
+        const float4 gt = reinterpret_cast<const float4*>(seg_tab)[(2 * sgs[buf] + (c >> 1)) * MH + mh];
+        const float g[4] = {gt.x, gt.y, gt.z, gt.w};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(g[r], fmaf(sc, C[t][r], bo * CX[r]), acc[t][r]);
+        for (int t = 0; t < TN; ++t) {
+          const float sc = bf16_to_f32((uint16_t)(sb[buf][t] & 0xffffu));
+          const float bi = bf16_to_f32((uint16_t)(sb[buf][t] >> 16));
+          const float bo = fmaf(-128.0f, sc, bi);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[t][4 * mh + r] = fmaf(g[r], fmaf(sc, C[mh][t][r], bo * CX[mh][r]), acc[t][4 * mh + r]);
+        }
       }
       return;
     }
@@ -352,7 +377,10 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
       const float bi = bf16_to_f32((uint16_t)(sb[buf][t] >> 16));
       const float bo = fmaf(-128.0f, sc, bi);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(sc, C[t][r], fmaf(bo, CX[r], acc[t][r]));
+      for (int mh = 0; mh < MH; ++mh)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[t][4 * mh + r] = fmaf(sc, C[mh][t][r], fmaf(bo, CX[mh][r], acc[t][4 * mh + r]));
     }
   };
 
@@ -404,19 +432,19 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
 #pragma unroll
   for (int t = 0; t < TN; ++t)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < MR; ++r) {
       float v = acc[t][r];
       v += __shfl_xor(v, 16, 64);
       v += __shfl_xor(v, 32, 64);
       acc[t][r] = v;
     }
   if constexpr (WS > 1) {
-    __shared__ float red[NWAVE][TN][4][16];
+    __shared__ float red[NWAVE][TN][MR][16];
     if (lane < 16) {
 #pragma unroll
       for (int t = 0; t < TN; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[wave][t][r][lane] = acc[t][r];
+        for (int r = 0; r < MR; ++r) red[wave][t][r][lane] = acc[t][r];
     }
     __syncthreads();
     if (ws != 0) return;
@@ -424,7 +452,7 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
 #pragma unroll
       for (int t = 0; t < TN; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < MR; ++r) {
           float v = 0.0f;
 #pragma unroll
           for (int j = 0; j < WS; ++j) v += red[rg * WS + j][t][r][lane];
@@ -433,61 +461,65 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
     }
   }
   if constexpr (SWIGLU) {
-    // lanes 0-7 hold gate rows, lanes 8-15 the matching up rows. The TN*4*8
+    // lanes 0-7 hold gate rows, lanes 8-15 the matching up rows. The TN*MR*8
     // outputs are spread over the wave through its (now idle) LDS slot so that
-    // each lane evaluates at most TN/2 of the exp/divide pairs.
+    // each lane evaluates at most TN*MR/8 of the exp/divide pairs.
     const int half = N / 2;
-    float* ep = reinterpret_cast<float*>(slot);          // [TN][4][16] floats <= 1 KiB of the 2 KiB slot
+    float* ep = reinterpret_cast<float*>(slot);          // [TN][MR][16] floats <= 1 KiB per 4 rows of the slot
     if (lane < 16) {
 #pragma unroll
       for (int t = 0; t < TN; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) ep[(t * 4 + r) * 16 + lane] = rs ? acc[t][r] * rstd[r] : acc[t][r];
+        for (int r = 0; r < MR; ++r) ep[(t * MR + r) * 16 + lane] = rs ? acc[t][r] * rstd[r] : acc[t][r];
     }
 #pragma unroll
-    for (int o = lane; o < TN * 32; o += 64) {
-      const int t = o >> 5, r = (o >> 3) & 3, i = o & 7;
-      const float gv = bf16_to_f32(f32_to_bf16(ep[(t * 4 + r) * 16 + i]));
-      const float uv = bf16_to_f32(f32_to_bf16(ep[(t * 4 + r) * 16 + 8 + i]));
+    for (int o = lane; o < TN * 8 * MR; o += 64) {
+      const int t = o / (8 * MR), r = (o >> 3) % MR, i = o & 7;
+      const float gv = bf16_to_f32(f32_to_bf16(ep[(t * MR + r) * 16 + i]));
+      const float uv = bf16_to_f32(f32_to_bf16(ep[(t * MR + r) * 16 + 8 + i]));
       const int j = (tile0 + t) * 8 + i;
       if (j < half && r < M) y[(size_t)r * half + j] = f32_to_bf16(gv / (1.0f + expf(-gv)) * uv);
     }
   } else {
     // lanes 0-15 hold row r of tile t in acc[t][r]; spread through the wave's
-    // (idle) LDS slot so that lane L finishes row L / 16, column L % 16
-    float* ep = reinterpret_cast<float*>(slot);          // [TN][4][16] floats <= 1 KiB of the 2 KiB slot
+    // (idle) LDS slot so that lane L finishes rows L / 16 + 4 mh, column L % 16
+    float* ep = reinterpret_cast<float*>(slot);          // [TN][MR][16] floats <= 1 KiB per 4 rows of the slot
     if (lane < 16) {
 #pragma unroll
       for (int t = 0; t < TN; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) ep[(t * 4 + r) * 16 + lane] = acc[t][r];
+        for (int r = 0; r < MR; ++r) ep[(t * MR + r) * 16 + lane] = acc[t][r];
     }
-    const float rs_r = er == 0 ? rstd[0] : er == 1 ? rstd[1] : er == 2 ? rstd[2] : rstd[3];
-    if (er < M) {                       // whole 16-lane DPP rows
 #pragma unroll
-      for (int t = 0; t < TN; ++t) {
-        const int n = (tile0 + t) * PK_TILE + ei;
-        const int tile = tile0 + t;
-        const float a = ep[(t * 4 + er) * 16 + ei];
-        const uint16_t d = f32_to_bf16(rs ? a * rs_r : a);
-        if (prod) {
-          const float hv = n < N ? bf16_to_f32(f32_to_bf16(bf16_to_f32(rsd[t]) + bf16_to_f32(d))) : 0.0f;
-          const float sq = row16_allsum(hv * hv);
-          if (n < N) {
-            e.h_out[(size_t)er * N + n] = f32_to_bf16(hv);
-            e.u_out[(size_t)er * N + n] = f32_to_bf16(hv * bf16_to_f32(nw[t]));
+    for (int mh = 0; mh < MH; ++mh) {
+      const int row = 4 * mh + er;
+      const float rs_r = rs_row[mh];
+      if (row < M) {                    // whole 16-lane DPP rows
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+          const int n = (tile0 + t) * PK_TILE + ei;
+          const int tile = tile0 + t;
+          const float a = ep[(t * MR + row) * 16 + ei];
+          const uint16_t d = f32_to_bf16(rs ? a * rs_r : a);
+          if (prod) {
+            const float hv = n < N ? bf16_to_f32(f32_to_bf16(bf16_to_f32(rsd[mh][t]) + bf16_to_f32(d))) : 0.0f;
+            const float sq = row16_allsum(hv * hv);
+            if (n < N) {
+              e.h_out[(size_t)row * N + n] = f32_to_bf16(hv);
+              e.u_out[(size_t)row * N + n] = f32_to_bf16(hv * bf16_to_f32(nw[t]));
+            }
+            if (ei == 0 && tile < tiles) e.sq_parts[(size_t)row * tiles + tile] = sq;
           }
-          if (ei == 0 && tile < tiles) e.sq_parts[(size_t)er * tiles + tile] = sq;
-        }
-        if (y && n < N) y[(size_t)er * N + n] = d;
-        if (e.am_parts) {
-          // the tile's largest rounded output and its first column (whole DPP rows active)
-          const float v = n < N ? bf16_to_f32(d) : -__builtin_inff();
-          const float m = row16_allmax(v);
-          const int j = row16_allmin(n < N && v == m ? n : 0x7fffffff);
-          if (ei == 0 && tile < tiles) {
-            e.am_parts[((size_t)er * tiles + tile) * 2] = m;
-            e.am_parts[((size_t)er * tiles + tile) * 2 + 1] = __int_as_float(j);
+          if (y && n < N) y[(size_t)row * N + n] = d;
+          if (e.am_parts) {
+            // the tile's largest rounded output and its first column (whole DPP rows active)
+            const float v = n < N ? bf16_to_f32(d) : -__builtin_inff();
+            const float m = row16_allmax(v);
+            const int j = row16_allmin(n < N && v == m ? n : 0x7fffffff);
+            if (ei == 0 && tile < tiles) {
+              e.am_parts[((size_t)row * tiles + tile) * 2] = m;
+              e.am_parts[((size_t)row * tiles + tile) * 2 + 1] = __int_as_float(j);
+            }
           }
         }
       }
@@ -556,38 +588,44 @@ __global__ __launch_bounds__(256) void rms_parts_kernel(const uint16_t* __restri
 
 typedef void (*qmv_packed_fn)(const uint16_t*, const uint8_t*, uint16_t*, int, int, int, PkEpi);
 
-template <int TN, int NP, int SW>
+template <int TN, int NP, int SW, int MH>
 qmv_packed_fn pick_ws(int ws) {
   switch (ws) {
-    case 1: return NP == 0 ? qmv_packed_kernel<TN, 1, 0, SW> : nullptr;
-    case 2: return qmv_packed_kernel<TN, 2, NP, SW>;
-    case 4: return qmv_packed_kernel<TN, 4, NP, SW>;
-    case 8: return qmv_packed_kernel<TN, 8, NP, SW>;
-    case 16: return TN == 1 ? qmv_packed_kernel<1, 16, NP, SW> : nullptr;
+    case 1: return NP == 0 ? qmv_packed_kernel<TN, 1, 0, SW, MH> : nullptr;
+    case 2: return qmv_packed_kernel<TN, 2, NP, SW, MH>;
+    case 4: return qmv_packed_kernel<TN, 4, NP, SW, MH>;
+    case 8: return qmv_packed_kernel<TN, 8, NP, SW, MH>;
+    case 16: return TN == 1 ? qmv_packed_kernel<1, 16, NP, SW, MH> : nullptr;
   }
   return nullptr;
 }
 
-template <int NP, int SW>
+// 5..8 rows (MH = 2) for one or two tiles per wave (what the default tiles pick)
+template <int NP, int SW, int MH>
 qmv_packed_fn pick_tn(int tn, int ws) {
   switch (tn) {
-    case 1: return pick_ws<1, NP, SW>(ws);
-    case 2: return NP <= 4 ? pick_ws<2, (NP <= 4 ? NP : 0), SW>(ws) : nullptr;
-    case 4: return NP <= 2 ? pick_ws<4, (NP <= 2 ? NP : 0), SW>(ws) : nullptr;
+    case 1: return pick_ws<1, NP, SW, MH>(ws);
+    case 2: return NP <= 4 ? pick_ws<2, (NP <= 4 ? NP : 0), SW, MH>(ws) : nullptr;
+    case 4: return NP <= 2 && MH == 1 ? pick_ws<4, (NP <= 2 ? NP : 0), SW, 1>(ws) : nullptr;
+  }
+  return nullptr;
+}
+
+template <int SW, int MH>
+qmv_packed_fn pick_packed_np(int tn, int ws, int np) {
+  switch (np) {
+    case 0: return pick_tn<0, SW, MH>(tn, ws);
+    case 2: return pick_tn<2, SW, MH>(tn, ws);
+    case 4: return pick_tn<4, SW, MH>(tn, ws);
+    case 6: return pick_tn<6, SW, MH>(tn, ws);
+    case 8: return pick_tn<8, SW, MH>(tn, ws);
   }
   return nullptr;
 }
 
 template <int SW>
-qmv_packed_fn pick_packed(int tn, int ws, int np) {
-  switch (np) {
-    case 0: return pick_tn<0, SW>(tn, ws);
-    case 2: return pick_tn<2, SW>(tn, ws);
-    case 4: return pick_tn<4, SW>(tn, ws);
-    case 6: return pick_tn<6, SW>(tn, ws);
-    case 8: return pick_tn<8, SW>(tn, ws);
-  }
-  return nullptr;
+qmv_packed_fn pick_packed(int tn, int ws, int np, int mh) {
+  return mh == 2 ? pick_packed_np<SW, 2>(tn, ws, np) : pick_packed_np<SW, 1>(tn, ws, np);
 }
 
 // Full prefetch when a wave's sets fit: the smallest NP in {2, 4, 6, 8} holding
@@ -642,7 +680,7 @@ int launch_packed(const uint16_t* x, const uint8_t* packed, uint16_t* y, int M, 
   const char* fn_name =
       fn_name_override ? fn_name_override : swiglu ? "qvex_qmv_w4g64_packed_swiglu" : "qvex_qmv_w4g64_packed";
   QVEX_CHECK_ARG(x && packed && (y || e.resid || e.am_parts), "%s: null pointer", fn_name);
-  QVEX_CHECK_ARG(M >= 1 && M <= 4, "%s: M=%d outside 1..4", fn_name, M);
+  QVEX_CHECK_ARG(M >= 1 && M <= 8, "%s: M=%d outside 1..8", fn_name, M);
   QVEX_CHECK_ARG(N >= 1 && K >= PK_SET && K % PK_SET == 0, "%s: N=%d K=%d (K must be a positive multiple of 256)",
                  fn_name, N, K);
   QVEX_CHECK_ARG(!swiglu || (N % 16 == 0), "%s: N=%d must be a multiple of 16 (gate and up halves of N/2 rows)",
@@ -653,9 +691,13 @@ int launch_packed(const uint16_t* x, const uint8_t* packed, uint16_t* y, int M, 
   QVEX_CHECK_ARG(NP == 0 || (WS >= 2 && (K / PK_SET + WS - 1) / WS <= NP),
                  "%s: prefetch_sets=%d must be 0 or hold all ceil(K/256 / WS) = %d sets of a wave", fn_name, NP,
                  (K / PK_SET + WS - 1) / WS);
-  qmv_packed_fn fn = swiglu   ? pick_packed<1>(TN, WS, NP)
-                     : e.seg_ss ? pick_packed<2>(TN, WS, NP)
-                                : pick_packed<0>(TN, WS, NP);
+  const int MH = M > 4 ? 2 : 1;           // 5..8 rows: two halves over one read of the weights
+  QVEX_CHECK_ARG(!e.seg_ss || 4 * MH * (K / 128) <= pk_block(WS),
+                 "%s: %d rows x %d heads of segment scales exceed the block's %d threads", fn_name, 4 * MH, K / 128,
+                 pk_block(WS));
+  qmv_packed_fn fn = swiglu   ? pick_packed<1>(TN, WS, NP, MH)
+                     : e.seg_ss ? pick_packed<2>(TN, WS, NP, MH)
+                                : pick_packed<0>(TN, WS, NP, MH);
   QVEX_CHECK_ARG(fn != nullptr, "%s: unsupported tile TN=%d WS=%d prefetch_sets=%d", fn_name, TN, WS, NP);
   const int threads = pk_block(WS);
   const int tiles = (N + PK_TILE - 1) / PK_TILE;

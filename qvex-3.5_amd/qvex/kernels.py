@@ -146,7 +146,7 @@ def packed_gemm(x: torch.Tensor, packed: torch.Tensor, N: int, out: torch.Tensor
 
 def quantized_matmul_packed(x: torch.Tensor, packed: torch.Tensor, N: int, out: torch.Tensor | None = None,
                             tile: tuple[int, ...] | None = None, swiglu: bool = False) -> torch.Tensor:
-    """y = x @ dequant(W)^T from pack_w4's copy, x bf16 [..., K] with 1..4 rows
+    """y = x @ dequant(W)^T from pack_w4's copy, x bf16 [..., K] with 1..8 rows
     (the product of mx.quantized_matmul in QLinear.__call__, engine/model.py:87-91).
     tile = (tiles_per_wave, wave_ksplit[, prefetch_sets]) forces a tile and load
     pipeline (prefetch_sets 0 = two-deep, default -1 = automatic).

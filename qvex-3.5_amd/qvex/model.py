@@ -120,15 +120,15 @@ class QLinear:
 
     w: int32 [N, K/8] (uint32 words), scales, biases: bf16 [N, K/64]. When K is
     a multiple of 256 the layer also keeps the tile-packed copy (pack_w4), built
-    once here, and runs every call of 1..4 rows - decode, MTP drafts, verify of
-    up to 3 drafts - through the MFMA kernel on it; the row bits of that kernel
-    do not depend on the number of rows. Calls of 5..DENSE_MIN_ROWS-1 rows
-    (verify of more drafts, short prefill tails) run it on chunks of 4 rows, so
-    their rows have the same bits too; longer calls (prefill) run the packed
+    once here, and runs every call of 1..8 rows - decode, MTP drafts, verify of
+    up to 7 drafts - through the MFMA kernel on it (5..8 rows as two halves over
+    one read of the weights); the row bits of that kernel do not depend on the
+    number of rows. Calls of 9..DENSE_MIN_ROWS-1 rows (short prefill tails) run
+    it on chunks of 8 rows, so their rows have the same bits too; longer calls (prefill) run the packed
     MFMA GEMM (weights dequantized to bf16 in registers). Without a packed copy
     (K not a multiple of 256) the MLX-layout kernel takes chunks of 8 rows."""
 
-    PACKED_MAX_ROWS = 4
+    PACKED_MAX_ROWS = 8
     # calls of at least this many rows (prefill) run the packed GEMM; 0 disables it
     DENSE_MIN_ROWS = 16
 
@@ -140,7 +140,7 @@ class QLinear:
         self.N = w.shape[0]
         self.K = w.shape[1] * 8
         # swiglu: a fused [gate; up] weight whose packed copy carries the gate/up
-        # interleave; its 1..4-row calls go through swiglu() (SwiGLU fused in)
+        # interleave; its 1..8-row calls go through swiglu() (SwiGLU fused in)
         self.swiglu_packed = swiglu and self.N % 16 == 0
         self.packed = None
         if pack and self.K % 256 == 0:
@@ -170,7 +170,7 @@ class QLinear:
         return self.packed is not None and M <= self.PACKED_MAX_ROWS and NormedRows.supported(self.K)
 
     def _packed_chunks(self, M: int) -> bool:
-        """Rows for the packed kernel in chunks of PACKED_MAX_ROWS (M > 4, below the dense GEMM)."""
+        """Rows for the packed kernel in chunks of PACKED_MAX_ROWS (below the dense GEMM)."""
         return self.packed is not None and M < max(self.DENSE_MIN_ROWS, self.PACKED_MAX_ROWS + 1)
 
     def swiglu(self, x) -> torch.Tensor:
@@ -233,7 +233,7 @@ class QLinear:
 
     def argmax(self, x, out: torch.Tensor) -> torch.Tensor:
         """Greedy token per row of the product (first index of the largest bf16
-        output) into out int32 [M]; x a tensor or NormedRows of 1..4 rows."""
+        output) into out int32 [M]; x a tensor or NormedRows of 1..8 rows."""
         if isinstance(x, NormedRows):
             M = x.u.reshape(-1, self.K).shape[0]
             if self._takes_normed(x, M) and not self.swiglu_packed:
@@ -253,7 +253,7 @@ class QLinear:
     def residual(self, x: torch.Tensor, resid: torch.Tensor, norm_w: torch.Tensor, eps: float,
                  h_out: torch.Tensor | None = None):
         """h = resid + x W^T and the next norm of h: returns (h, NormedRows) with
-        the add and the norm's inputs in the product's epilogue (1..4 rows), or
+        the add and the norm's inputs in the product's epilogue (1..8 rows), or
         (h, normalised tensor) through add_rms_norm otherwise. h_out: where h goes."""
         x2 = x.reshape(-1, self.K)
         M = x2.shape[0]
@@ -315,7 +315,7 @@ def add_rms_norm(x, delta, w, eps, h_out=None, out=None):
 
 
 class NormedRows:
-    """rms_norm(h) * w for 1..4 rows kept unnormalised: u = bf16(h * w) and the
+    """rms_norm(h) * w for 1..8 rows kept unnormalised: u = bf16(h * w) and the
     fp32 sums of h^2 per 16 columns (written by the product that made h, or by
     rms_parts). A packed QLinear takes it as input and applies the per-row
     rsqrt(mean(h^2) + eps) to its outputs, so the norm costs no launch."""
@@ -632,7 +632,7 @@ class GatedDeltaNet:
     # calls of at least this many tokens without snapshots (prefill) use the
     # chunked recurrence (qvex_gdn_chunked); larger than any ring-snapshot width
     CHUNKED_MIN_T = 64
-    # with the norms folded (resid given, <= 4 rows) each head is split over this
+    # with the norms folded (resid given, <= 8 rows) each head is split over this
     # many workgroups (qvex_gdn_decode_split) and the gated norm's scale moves
     # into the out_proj; 0 keeps one workgroup per head
     split_blocks = 4
@@ -724,7 +724,7 @@ class GatedDeltaNet:
 
 
 class MLP:
-    """down(silu(gate(x)) * up(x)) (engine/model.py:294-302); for 1..4 rows the
+    """down(silu(gate(x)) * up(x)) (engine/model.py:294-302); for 1..8 rows the
     SwiGLU is fused into the gate/up product."""
 
     def __init__(self, p: dict):
@@ -745,7 +745,7 @@ class Layer:
         self.eps = cfg.rms_norm_eps
 
     def fused(self, h, st, cache, keep_prev, next_w, h_out=None):
-        """1..4 rows with the norms folded into the products: h the residual stream,
+        """1..8 rows with the norms folded into the products: h the residual stream,
         st its ln1 norm as NormedRows; returns the new stream (into h_out when
         given) and its norm by next_w."""
         kw = dict(resid=h, norm_w=self.ln2, eps=self.eps)
@@ -764,7 +764,7 @@ class Layer:
 class Qwen35:
     """Forward of the hybrid stack (engine/model.py:319-336) for batch 1."""
 
-    # 1..4-row calls fold every residual RMSNorm into the neighbouring products
+    # 1..8-row calls fold every residual RMSNorm into the neighbouring products
     # (QLinear.residual / NormedRows); False keeps the separate norm kernels
     fuse_norms = True
     # prompt tokens per forward call of a prefill (engine/engine.py:232-248 runs

@@ -79,8 +79,8 @@ def test_packed_bytes_and_rejections():
     assert lib.qvex_w4g64_packed_bytes(0, 256) == 0
     buf = ctypes.create_string_buffer(1 << 12)
     p16 = (ctypes.addressof(buf) + 15) // 16 * 16
-    with pytest.raises(_C.QvexError, match="outside 1..4"):
-        _C.call("qvex_qmv_w4g64_packed", p16, p16, p16, 5, 16, 256, None)
+    with pytest.raises(_C.QvexError, match="outside 1..8"):
+        _C.call("qvex_qmv_w4g64_packed", p16, p16, p16, 9, 16, 256, None)
     with pytest.raises(_C.QvexError, match="multiple of 256"):
         _C.call("qvex_qmv_w4g64_packed", p16, p16, p16, 1, 16, 320, None)
     with pytest.raises(_C.QvexError, match="unsupported tile"):
@@ -173,8 +173,8 @@ def test_gnorm_resid_argument_rules():
             _C.call("qvex_qmv_w4g64_packed_gnorm_resid", p, p, 1, 16, 256, p, nb, 1e-6, p, p, p, p, p, None)
     with pytest.raises(_C.QvexError, match="null pointer"):
         _C.call("qvex_qmv_w4g64_packed_gnorm_resid", p, p, 1, 16, 256, None, 8, 1e-6, p, p, p, p, p, None)
-    with pytest.raises(_C.QvexError, match="outside 1..4"):
-        _C.call("qvex_qmv_w4g64_packed_gnorm_resid", p, p, 5, 16, 256, p, 8, 1e-6, p, p, p, p, p, None)
+    with pytest.raises(_C.QvexError, match="outside 1..8"):
+        _C.call("qvex_qmv_w4g64_packed_gnorm_resid", p, p, 9, 16, 256, p, 8, 1e-6, p, p, p, p, p, None)
 
 
 def test_resid_norm_products_argument_rules():
@@ -182,8 +182,8 @@ def test_resid_norm_products_argument_rules():
     p = (ctypes.addressof(buf) + 15) // 16 * 16
     with pytest.raises(_C.QvexError, match="null pointer"):
         _C.call("qvex_qmv_w4g64_packed_resid", p, p, 1, 16, 256, None, p, p, p, p, None)
-    with pytest.raises(_C.QvexError, match="outside 1..4"):
-        _C.call("qvex_qmv_w4g64_packed_resid", p, p, 5, 16, 256, p, p, p, p, p, None)
+    with pytest.raises(_C.QvexError, match="outside 1..8"):
+        _C.call("qvex_qmv_w4g64_packed_resid", p, p, 9, 16, 256, p, p, p, p, p, None)
     with pytest.raises(_C.QvexError, match="ceil\\(dim/16\\)"):
         _C.call("qvex_qmv_w4g64_packed_rstd", p, p, p, 1, 16, 256, p, 255, 4096, 1e-6, 0, None)
     with pytest.raises(_C.QvexError, match="ceil\\(dim/16\\)"):

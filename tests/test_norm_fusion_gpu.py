@@ -38,7 +38,7 @@ def bf(t):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("M", [1, 2, 4, 5, 8])
 @pytest.mark.parametrize("N,K", [(4096, 12288), (512, 1024), (4096, 4096)])
 def test_producer_epilogue(M, N, K):
     w, s, b = synth.qmv_weights(N, K, seed=41, tag=N)
@@ -59,7 +59,7 @@ def test_producer_epilogue(M, N, K):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M", [1, 3, 4])
+@pytest.mark.parametrize("M", [1, 3, 4, 6, 8])
 @pytest.mark.parametrize("N,K,swiglu", [(12352, 4096, False), (24576, 4096, True), (1024, 512, False),
                                         (2048, 512, True)])
 def test_consumer_scales_rows_by_rstd(M, N, K, swiglu):

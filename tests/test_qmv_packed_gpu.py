@@ -23,8 +23,10 @@ def run_packed(x, w, s, b, tile=None):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("tile", PACKED_TILES)
-@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
 def test_packed_tiles(tile, M):
+    if M > 4 and tile[0] == 4:
+        pytest.skip("5..8 rows run one or two tiles per wave (what the default tiles pick)")
     N, K = 531, 2304                       # ragged last tile, 9 sets
     w, s, b = synth.qmv_weights(N, K, seed=31, tag=M)
     x = synth.qmv_x(M, K, seed=31, tag=M)
@@ -64,6 +66,12 @@ def test_packed_rows_bitwise_independent_of_m(N, K):
         assert np.array_equal(y1[0], y4[m]), f"row {m} differs between M=1 and M=4"
     y2 = run_packed(x4[1:3], w, s, b)
     assert np.array_equal(y2, y4[1:3])
+    # 5..8 rows (two row halves in one launch): each row as in the 4-row calls
+    x8 = np.concatenate([x4, synth.qmv_x(4, K, seed=34, tag=K)])
+    y8 = run_packed(x8, w, s, b)
+    assert np.array_equal(y8[:4], y4)
+    assert np.array_equal(y8[4:], run_packed(x8[4:], w, s, b))
+    assert np.array_equal(run_packed(x8[:5], w, s, b), y8[:5])
 
 
 @pytest.mark.gpu
@@ -79,7 +87,7 @@ def test_packed_matches_mlx_layout_kernel_closely():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 6, 8])
 @pytest.mark.parametrize("N,K", [(24576, 4096), (48, 512), (4096, 256)])
 def test_packed_swiglu_equals_product_then_swiglu(M, N, K):
     """The fused SwiGLU epilogue matches the packed product followed by qvex_swiglu
@@ -145,7 +153,7 @@ def test_prefetch_explicit_tiles(tile):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M", [1, 3, 4])
+@pytest.mark.parametrize("M", [1, 3, 4, 7])
 @pytest.mark.parametrize("N,K,ties", [(248320, 4096, False), (4096, 512, True), (531, 2304, True), (50000, 1024, False)])
 def test_argmax_epilogue_equals_argmax_of_product(M, N, K, ties):
     """qvex_qmv_w4g64_packed_argmax == the first index of the maximum of the bf16
@@ -181,8 +189,9 @@ def test_argmax_epilogue_equals_argmax_of_product(M, N, K, ties):
 @pytest.mark.parametrize("M", [5, 7, 8, 13])
 @pytest.mark.parametrize("swiglu", [False, True])
 def test_qlinear_rows_5_to_15_equal_single_row_calls(M, swiglu):
-    """QLinear runs 5..15 rows through the packed kernel in chunks of 4: every row
-    has the bits of the same row computed alone (as decode computes it)."""
+    """QLinear runs 5..15 rows through the packed kernel (5..8 in one launch, more
+    in chunks of 8): every row has the bits of the same row computed alone (as
+    decode computes it)."""
     from qvex.model import QLinear
     N, K = 1024, 2048
     w, s, b = synth.qmv_weights(N, K, seed=41, tag=M)
