@@ -114,6 +114,40 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
+template <int CTRL, int ROW_MASK = 0xf, bool BOUND_CTRL = true>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, BOUND_CTRL);
+}
+
+// Exclusive prefix sum over the block's threads of v; *total = the sum. sh: 4
+// ints. The wave's inclusive scan runs on DPP row shifts and row broadcasts.
+__device__ __forceinline__ int block_excl_scan(int v, int* sh, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+  x += dpp_i<DPP_ROW_SHR(1)>(x);
+  x += dpp_i<DPP_ROW_SHR(2)>(x);
+  x += dpp_i<DPP_ROW_SHR(4)>(x);
+  x += dpp_i<DPP_ROW_SHR(8)>(x);
+  x += dpp_i<DPP_ROW_BCAST15, 0xa, false>(x);
+  x += dpp_i<DPP_ROW_BCAST31, 0xc, false>(x);
+  __syncthreads();
+  if (lane == 63) sh[wave] = x;
+  __syncthreads();
+  int off = 0;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) off += w < wave ? sh[w] : 0;
+  *total = ((sh[0] + sh[1]) + sh[2]) + sh[3];
+  return off + x - v;
+}
+
+// Candidates kept per part and target row for the one-kernel list form: every
+// index with z above the part's k-th value (at most k - 1 <= 63, in slots
+// [0, CAND_GT)) and up to CAND_CAP - CAND_GT of the ties at it (slots after)
+constexpr int CAND_CAP = 96;
+constexpr int CAND_GT = 64;
+constexpr int CAND_IT = 16;         // slots per thread of the draw: P * CAND_CAP <= NT * CAND_IT
+constexpr int CAND_LIST_FLOATS = 42 * 65;   // the row's part lists in LDS: P (<= 42) x (top_k + 1)
+
 struct SpecArgs {
   const void* target;     // [S, k+1, V] fp32, or bf16 when bf
   const void* draft;      // [S, k, V] or nullptr, same type
@@ -135,6 +169,13 @@ struct SpecArgs {
   int bf;                 // logits are bf16 (widened exactly to fp32 on load)
   int filt;               // 0: no filter, 1: list form, 2: wide form
   int wide_k;             // wide form: top-k (0 = off)
+  // list form without draft logits (one kernel after the statistics):
+  int fast;
+  int32_t* cand;          // [S * (k+1), P, CAND_CAP] indices of z >= the part's k-th value
+  float* cand_z;          // [S * (k+1), P, CAND_CAP] their z
+  int32_t* ncand;         // [S * (k+1), P, 2] how many the part has above / at its k-th value
+  int32_t* ctr;           // [S] blocks of the step that finished their row
+  int32_t* rres;          // [S * (k+1), 2] each row's accept flag and draw
 };
 
 __device__ __forceinline__ const void* row_ptr(const SpecArgs& a, int step, int i) {
@@ -199,7 +240,7 @@ __device__ __forceinline__ void next_buf(const float (&v)[NS], float lv, int li,
 // dry (a lane must win TOPK_BUF rounds first).
 // The four sorted lists are then merged by rank: entry i of wave w lands at
 // i + #(entries of other waves that are larger, or equal and from a lower
-// wave), which is unique. wl: 4 * K floats.
+// wave), which is unique. wl: 4 * 64 floats, 16-byte aligned (wave w's list at 64 w).
 template <int NS>
 __device__ __forceinline__ void block_topk(const float (&v)[NS], int K, float* lst, float* wl) {
   float bv[TOPK_BUF];
@@ -209,7 +250,7 @@ __device__ __forceinline__ void block_topk(const float (&v)[NS], int K, float* l
   for (int r = 0; r < K; ++r) {
     const float m = wave_allmax(bv[0]);
     const unsigned long long msk = __ballot(bv[0] == m);
-    if (lane == 0) wl[wave * K + r] = m;
+    if (lane == 0) wl[wave * 64 + r] = m;
     if (lane == __ffsll(msk) - 1) {
       const float lv = bv[0];
       const int li = bi[0];
@@ -225,14 +266,19 @@ __device__ __forceinline__ void block_topk(const float (&v)[NS], int K, float* l
   }
   __syncthreads();
   if (t < 4 * K) {
-    const int w = t / K;
-    const float x = wl[t];
-    int rank = t - w * K;
+    const int w = t / K, r = t - w * K;
+    const float x = wl[w * 64 + r];
+    int rank = r;
     for (int w2 = 0; w2 < 4; ++w2) {
       if (w2 == w) continue;
-      const float* o = wl + w2 * K;
-#pragma unroll 8
-      for (int j = 0; j < K; ++j) rank += (o[j] > x || (w2 < w && o[j] == x)) ? 1 : 0;
+      const float4* o = reinterpret_cast<const float4*>(wl + w2 * 64);
+      for (int j4 = 0; j4 < (K + 3) / 4; ++j4) {   // four entries per LDS read
+        const float4 q = o[j4];
+        const float e[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          rank += (4 * j4 + i < K && (e[i] > x || (w2 < w && e[i] == x))) ? 1 : 0;
+      }
     }
     if (rank < K) lst[rank] = x;
   }
@@ -345,7 +391,7 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
   if (tgt && a.filt == 1) {
     // this part's top_k largest z and the count of its values equal to the k-th
     __shared__ float lst[64];
-    __shared__ float wl[4 * 64];
+    __shared__ __align__(16) float wl[4 * 64];
     const int K = a.top_k;
     float zz[4 * NI];
 #pragma unroll
@@ -363,6 +409,48 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
     float* L = a.fws + (((long)step * (a.k + 1) + i) * a.P + p) * (K + 1);
     if (t < K) L[t] = lst[t];
     if (t == 0) L[K] = cnt;
+    if (a.fast) {
+      // the part's indices and z above vk, then up to CAND_CAP - CAND_GT of those
+      // equal to vk, in any order (the consumer orders them): the row's kept set
+      // (z >= cutoff, cutoff >= every part's vk) lies in them unless the part
+      // holds more ties and the cutoff is vk itself
+      __shared__ int c_gt, c_eq;
+      if (t == 0) {
+        c_gt = 0;
+        c_eq = 0;
+      }
+      __syncthreads();
+      const long crow = (long)step * (a.k + 1) + i;
+      int32_t* C = a.cand + (crow * a.P + p) * CAND_CAP;
+      float* Zc = a.cand_z + (crow * a.P + p) * CAND_CAP;
+#pragma unroll
+      for (int it = 0; it < NI; ++it)
+        if (ok[it]) {
+          const int j = base + 4 * (t + NT * it);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float zv = z[it][e];
+            if (zv > vk) {
+              const int q = atomicAdd(&c_gt, 1);          // < K - 1 <= CAND_GT
+              C[q] = j + e;
+              Zc[q] = zv;
+            } else if (zv == vk) {
+              const int q = atomicAdd(&c_eq, 1);
+              if (q < CAND_CAP - CAND_GT) {
+                C[CAND_GT + q] = j + e;
+                Zc[CAND_GT + q] = zv;
+              }
+            }
+          }
+        }
+      __syncthreads();
+      if (t == 0) {
+        a.ncand[(crow * a.P + p) * 2] = c_gt;
+        a.ncand[(crow * a.P + p) * 2 + 1] = c_eq;
+      }
+      if (p == 0 && row == 0)
+        for (int q = t; q < a.S; q += NT) a.ctr[q] = 0;
+    }
   }
 }
 
@@ -375,12 +463,8 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
 // row's count of values equal to the cutoff: a part whose k-th value is the
 // cutoff contributes its tie count, any other part its list entries equal to it
 // (the cutoff is never below a part's k-th value).
-__global__ __launch_bounds__(NT) void spec_filter_kernel(SpecArgs a) {
-  __shared__ float lst[64];
-  __shared__ float wl[4 * 64];
-  __shared__ float cut_s;
-  __shared__ int neq_s;
-  const int row = blockIdx.x;           // step * (k + 1) + i
+__device__ __forceinline__ void filter_row(const SpecArgs& a, int row, float* lst, float* wl, float& cut_s,
+                                           int& neq_s) {
   const int K = a.top_k, P = a.P;
   const int n = P * K;                  // <= 16 * NT, checked by the host
   const float* L = a.fws + (long)row * P * (K + 1);
@@ -458,6 +542,14 @@ __global__ __launch_bounds__(NT) void spec_filter_kernel(SpecArgs a) {
       fr[2] = cutoff;
     }
   }
+}
+
+__global__ __launch_bounds__(NT) void spec_filter_kernel(SpecArgs a) {
+  __shared__ float lst[64];
+  __shared__ __align__(16) float wl[4 * 64];
+  __shared__ float cut_s;
+  __shared__ int neq_s;
+  filter_row(a, blockIdx.x, lst, wl, cut_s, neq_s);   // row = step * (k + 1) + i
 }
 
 // ---------------------------------------------------------------- wide filter (top-k > 64, top-p over the vocabulary)
@@ -719,6 +811,18 @@ __device__ __forceinline__ float weight(const WCtx& c, int j) {
     Sq = 1.0f;
   }
   const float t1 = ep * Sq;
+  const float t2 = eq * c.sp;
+  const float r = t1 - t2;
+  return r > 0.0f ? r : 0.0f;
+}
+
+// weight() of a one-hot draft from the element's z (the value the statistics
+// kernel stored for it: the same penalised logit times 1/T, so the same bits)
+__device__ __forceinline__ float weight_z(const WCtx& c, int j, float z) {
+  const float ep = z >= c.cutoff ? qx_expf(z - c.mp) : 0.0f;
+  if (c.mode == 1) return ep;
+  const float eq = (j == c.d) ? 1.0f : 0.0f;
+  const float t1 = ep * 1.0f;
   const float t2 = eq * c.sp;
   const float r = t1 - t2;
   return r > 0.0f ? r : 0.0f;
@@ -1136,6 +1240,364 @@ __global__ __launch_bounds__(NT) void spec_sample_kernel(SpecArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- one kernel after the statistics (list form)
+
+// The sampling walk's order (parts, then threads, then each thread's (i, e)) as
+// one integer: key = ((part * NT + thread) * NI + i) * 4 + e, so key >> 5 is the
+// thread slot, key >> 11 its wave quarter and key >> 13 the part.
+__device__ __forceinline__ int walk_key(int j) {
+  const int p = j / PART, l = j - p * PART;
+  return ((p * NT + ((l >> 2) & (NT - 1))) * NI + (l >> 10)) * 4 + (l & 3);
+}
+__device__ __forceinline__ int key_index(int key) {
+  return (key >> 13) * PART + 4 * (((key >> 5) & (NT - 1)) + NT * ((key >> 2) & (NI - 1))) + (key & 3);
+}
+
+struct SparseSh {
+  int key[NT];          // positive weights, in arrival order
+  float w[NT];
+  int skey[NT];         // the same in walk order
+  float sw[NT];
+  float ssum[NT];       // at the first entry of a thread slot: the slot's thread sum
+  int gstart[NT];       // first entry of each (part, quarter) group
+  float gsum[NT];       // the group's wave butterfly sum
+  int pstart[NT];       // first group of each part present
+  float psum[NT];       // the part's block sum
+  int scan[8];
+  int n, fb, ng, np;
+};
+
+// A row's stored candidates, requested at kernel start: thread t holds slots
+// t + NT q (unused slots hold stale values, dropped by the counts) and, for
+// t < P, part t's tie count.
+struct CandRegs {
+  int j[CAND_IT], ngt[CAND_IT], neq[CAND_IT];
+  float z[CAND_IT];
+  int part_neq;
+};
+
+__device__ __forceinline__ void load_cands(const SpecArgs& a, long crow, CandRegs& r) {
+  const int t = threadIdx.x, P = a.P;
+  const int* cn = a.ncand + crow * P * 2;
+  const int32_t* cl = a.cand + crow * P * CAND_CAP;
+  const float* cz = a.cand_z + crow * P * CAND_CAP;
+#pragma unroll
+  for (int q = 0; q < CAND_IT; ++q) {
+    const int i = min(t + NT * q, P * CAND_CAP - 1), p = i / CAND_CAP;
+    r.j[q] = cl[i];
+    r.z[q] = cz[i];
+    r.ngt[q] = cn[2 * p];
+    r.neq[q] = cn[2 * p + 1];
+  }
+  r.part_neq = cn[2 * min(t, P - 1) + 1];
+}
+
+// The draw of the fixed-order walk (spec_decide_kernel + spec_sample_kernel)
+// from the candidate lists alone. Weights outside the kept set are zero and
+// x + 0 = x exactly in fp32, so every thread sum, wave butterfly, part sum and
+// running prefix of the walk over the whole row equals the same operations over
+// the positive weights only, applied in walk order with the same tree: thread
+// sums from 0 in (i, e) order, each wave quarter through wave_bfly_sum with the
+// absent threads as zeros, parts as ((q0 + q1) + q2) + q3, then the walks.
+// lists: the row's part lists in LDS ([P][K + 1]). Returns the token, -1 when
+// no weight is positive, -2 when the lists do not hold every kept index (a
+// part with more than CAND_CAP - CAND_GT ties at a cutoff equal to its k-th
+// value) or more than NT weights are positive.
+__device__ __forceinline__ int sparse_sample(const SpecArgs& a, const WCtx& c, const CandRegs& r, const float* lists,
+                                             float u, SparseSh& L) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int K = a.top_k, P = a.P;
+  if (t == 0) {
+    L.n = 0;
+    L.fb = 0;
+  }
+  __syncthreads();
+  if (t < P && r.part_neq > CAND_CAP - CAND_GT && !(c.cutoff > lists[t * (K + 1) + K - 1])) L.fb = 1;
+#pragma unroll
+  for (int q = 0; q < CAND_IT; ++q) {
+    const int i = t + NT * q;
+    if (i < P * CAND_CAP) {
+      const int sl = i % CAND_CAP;
+      const bool stored = sl < CAND_GT ? sl < r.ngt[q] : sl - CAND_GT < r.neq[q];
+      if (stored && r.z[q] >= c.cutoff) {
+        const float w = weight_z(c, r.j[q], r.z[q]);
+        if (w > 0.0f) {
+          const int e = atomicAdd(&L.n, 1);
+          if (e < NT) {
+            L.key[e] = walk_key(r.j[q]);
+            L.w[e] = w;
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int n = L.n;
+  if (L.fb || n > NT) return -2;
+  if (n == 0) return -1;
+  if (t < n) {                          // keys are distinct: rank = position in walk order
+    const int key = L.key[t];
+    int r = 0;
+    for (int q = 0; q < n; ++q) r += L.key[q] < key ? 1 : 0;
+    L.skey[r] = key;
+    L.sw[r] = L.w[t];
+  }
+  __syncthreads();
+  bool gfirst = false;
+  if (t < n) {
+    const int key = L.skey[t];
+    if (t == 0 || (L.skey[t - 1] >> 5) != (key >> 5)) {
+      float acc = 0.0f;
+      for (int q = t; q < n && (L.skey[q] >> 5) == (key >> 5); ++q) acc = acc + L.sw[q];
+      L.ssum[t] = acc;
+    }
+    gfirst = t == 0 || (L.skey[t - 1] >> 11) != (key >> 11);
+  }
+  int ng;
+  const int gi = block_excl_scan(gfirst ? 1 : 0, L.scan, &ng);
+  if (gfirst) L.gstart[gi] = t;
+  __syncthreads();
+  for (int g = wave; g < ng; g += NT / 64) {
+    const int s0 = L.gstart[g], s1 = g + 1 < ng ? L.gstart[g + 1] : n;
+    float v = 0.0f;
+    for (int q = s0; q < s1; ++q) {
+      const int key = L.skey[q];
+      const bool first = q == 0 || (L.skey[q - 1] >> 5) != (key >> 5);
+      if (first && ((key >> 5) & 63) == lane) v = L.ssum[q];
+    }
+    v = wave_bfly_sum(v);
+    if (lane == 0) L.gsum[g] = v;
+  }
+  __syncthreads();
+  bool pfirst = false;
+  if (t < ng) pfirst = t == 0 || (L.skey[L.gstart[t - 1]] >> 13) != (L.skey[L.gstart[t]] >> 13);
+  int np;
+  const int pi = block_excl_scan(pfirst ? 1 : 0, L.scan, &np);
+  if (pfirst) {
+    const int part = L.skey[L.gstart[t]] >> 13;
+    float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
+    for (int g = t; g < ng && (L.skey[L.gstart[g]] >> 13) == part; ++g) {
+      const int q = (L.skey[L.gstart[g]] >> 11) & 3;
+      const float v = L.gsum[g];
+      b0 = q == 0 ? v : b0;
+      b1 = q == 1 ? v : b1;
+      b2 = q == 2 ? v : b2;
+      b3 = q == 3 ? v : b3;
+    }
+    L.psum[pi] = ((b0 + b1) + b2) + b3;
+    L.pstart[pi] = t;
+  }
+  __syncthreads();
+  // the walks of spec_sample_kernel, over the positive entries only
+  __shared__ int s_res;
+  if (t == 0) {
+    float Wt = 0.0f;
+    for (int q = 0; q < np; ++q) Wt = Wt + L.psum[q];
+    const float th = u * Wt;
+    float cacc = 0.0f;
+    int ps = -1;
+    for (int q = 0; q < np; ++q) {
+      const float nx = cacc + L.psum[q];
+      if (nx > th) { ps = q; break; }
+      cacc = nx;
+    }
+    bool fallback = false;
+    if (ps < 0) {                       // every present part is positive: the last one
+      ps = np - 1;
+      fallback = true;
+    }
+    const int e0 = L.gstart[L.pstart[ps]];
+    const int e1 = ps + 1 < np ? L.gstart[L.pstart[ps + 1]] : n;
+    int ts = -1;                        // entry index of the chosen slot's first entry
+    if (!fallback) {
+      for (int q = e0; q < e1; ++q) {
+        if (q != e0 && (L.skey[q - 1] >> 5) == (L.skey[q] >> 5)) continue;
+        const float nx = cacc + L.ssum[q];
+        if (nx > th) { ts = q; break; }
+        cacc = nx;
+      }
+    }
+    if (ts < 0) {                       // the last slot of the part
+      for (int q = e0; q < e1; ++q)
+        if (q == e0 || (L.skey[q - 1] >> 5) != (L.skey[q] >> 5)) ts = q;
+      fallback = true;
+    }
+    int res = -1, last = ts;
+    for (int q = ts; q < e1 && (L.skey[q] >> 5) == (L.skey[ts] >> 5); ++q) {
+      last = q;
+      if (!fallback && res < 0) {
+        cacc = cacc + L.sw[q];
+        if (cacc > th) res = q;
+      }
+    }
+    if (res < 0) res = last;            // the slot's last positive weight
+    s_res = key_index(L.skey[res]);
+  }
+  __syncthreads();
+  return s_res;
+}
+
+// The filter of spec_filter_kernel for one row in wave 0, from the row's part
+// lists in LDS (fl, [P][K + 1], P <= 64): the row's K largest values come from a
+// tournament over the lists' heads (one lane per part, one wave maximum per
+// round), the same multiset as the block merge; then the top-p cutoff, the
+// ties at it and S_p exactly as there. Results in (c0, S, cutoff).
+__device__ __forceinline__ void filter_wave(const SpecArgs& a, const float* fl, float& c0_out, float& S_out,
+                                            float& cut_out) {
+  const int lane = threadIdx.x & 63, K = a.top_k, P = a.P;
+  const float* my = fl + min(lane, P - 1) * (K + 1);
+  int ptr = 0;
+  float h = lane < P ? my[0] : -__builtin_inff();
+  float hn = lane < P && K > 1 ? my[1] : -__builtin_inff();
+  float cl = -__builtin_inff();
+  for (int r = 0; r < K; ++r) {
+    const float m = wave_allmax(h);
+    cl = lane == r ? m : cl;
+    const unsigned long long hit = __ballot(h == m);
+    if (lane == __ffsll(hit) - 1) {
+      ++ptr;
+      h = hn;
+      hn = lane < P && ptr + 1 < K ? my[ptr + 1] : -__builtin_inff();
+    }
+  }
+  const float c0 = readlane_f(cl, 0);
+  const float el = lane < K ? qx_expf(cl - c0) : 0.0f;
+  float cutoff = readlane_f(cl, K - 1);
+  if (a.top_p > 0.0f && a.top_p < 1.0f) {
+    float Ssum = 0.0f;
+    for (int q = 0; q < K; ++q) Ssum = Ssum + readlane_f(el, q);
+    const float pl = el / Ssum;
+    float run = 0.0f, mn = __builtin_inff();
+    for (int q = 0; q < K; ++q) {
+      const float pi = readlane_f(pl, q);
+      const float cq = readlane_f(cl, q);
+      const float incl = run + pi;
+      if ((incl - pi) < a.top_p && cq < mn) mn = cq;
+      run = incl;
+    }
+    cutoff = mn;
+  }
+  // ties at the cutoff: a part whose K-th value is the cutoff contributes its
+  // tie count, any other part its list entries equal to it (integer, order-free)
+  int eq = 0;
+  if (lane < P) {
+    if (my[K - 1] == cutoff) {
+      eq = (int)my[K];
+    } else {
+#pragma unroll 8
+      for (int q = 0; q < K; ++q) eq += my[q] == cutoff ? 1 : 0;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) eq += __shfl_xor(eq, o, 64);
+  const int n_gt = __popcll(__ballot(lane < K && cl > cutoff));
+  float S = 0.0f;
+  for (int q = 0; q < n_gt; ++q) S = S + readlane_f(el, q);
+  S = S + (float)eq * qx_expf(cutoff - c0);
+  c0_out = c0;
+  S_out = S;
+  cut_out = cutoff;
+}
+
+// List form without draft logits, one block per target row i of a step: the
+// row's filter, its accept test (i < k: spec_decide_kernel's rule) and its draw
+// (i < k: the residual at a rejection there, falling back to p_i when it
+// vanishes; i = k: the bonus) from the candidate lists, or from the full
+// fixed-order pass when the lists do not hold the kept set. The last block of
+// the step (a device-scope counter, zeroed by the statistics kernel) takes the
+// first rejection's draw, or the bonus.
+__global__ __launch_bounds__(NT) void spec_finish_kernel(SpecArgs a) {
+  extern __shared__ float smem[];       // fallback pass: [P][NT] thread sums, [P] part sums
+  __shared__ float fl[CAND_LIST_FLOATS];
+  __shared__ float s_c0, s_S, s_cut;
+  __shared__ int s_last;
+  __shared__ SparseSh sh;
+  __shared__ float red[4];
+  const int row = blockIdx.x, k = a.k, step = row / (k + 1), i = row - step * (k + 1);
+  const int t = threadIdx.x, K = a.top_k, P = a.P;
+  // requests first: the part lists, the candidates, the draft's logit
+  const float* L = a.fws + (long)row * P * (K + 1);
+  float lv[CAND_LIST_FLOATS / NT + 1];
+#pragma unroll
+  for (int q = 0; q < CAND_LIST_FLOATS / NT + 1; ++q) lv[q] = L[min(t + NT * q, P * (K + 1) - 1)];
+  CandRegs cr;
+  load_cands(a, row, cr);
+  const int32_t* d = a.ids + (long)step * k;
+  const int di = i < k ? d[i] : -1;
+  const bool din = i < k && !(di < 0 || di >= a.V);
+  const float xd = din ? lg(row_ptr(a, step, i), di, a.bf) : 0.0f;
+  const float ua = i < k ? a.u_acc[(long)step * k + i] : 0.0f;
+  const float u = a.u_smp[step];
+#pragma unroll
+  for (int q = 0; q < CAND_LIST_FLOATS / NT + 1; ++q)
+    if (t + NT * q < P * (K + 1)) fl[t + NT * q] = lv[q];
+  __syncthreads();
+  if (t < 64) {
+    float c0, S, cut;
+    filter_wave(a, fl, c0, S, cut);
+    if (t == 0) {
+      s_c0 = c0;
+      s_S = S;
+      s_cut = cut;
+      float* fr = a.frow + (long)row * 4;
+      fr[0] = c0;
+      fr[1] = S;
+      fr[2] = cut;
+    }
+  }
+  __syncthreads();
+  WCtx c;
+  c.inv_temp = a.inv_temp;
+  c.tp = row_ptr(a, step, i);
+  c.tq = nullptr;
+  c.bf = a.bf;
+  c.mp = s_c0;
+  c.sp = s_S;
+  c.cutoff = s_cut;
+  c.seen = a.seen;
+  c.pen = a.pen;
+  c.extra = d;
+  c.n_extra = i;
+  c.d = i < k ? di : -1;
+  c.mode = i < k ? 0 : 1;
+  c.mq = 0.0f;
+  c.sq = 1.0f;
+  int ok = 0;
+  if (din) {
+    const float zd = pen_x(a.seen, a.pen, xd, di, d, i) * a.inv_temp;
+    const float ep = zd >= c.cutoff ? qx_expf(zd - c.mp) : 0.0f;
+    const float eq = 1.0f, Sq = 1.0f;
+    const float lhs = ua * eq * c.sp;
+    const float rhs = ep * Sq;
+    ok = lhs < rhs ? 1 : 0;
+  }
+  int tok = sparse_sample(a, c, cr, fl, u, sh);
+  if (tok == -1 && c.mode == 0) {       // residual vanished: sample p_i
+    c.mode = 1;
+    tok = sparse_sample(a, c, cr, fl, u, sh);
+  }
+  while (tok == -2) {                   // the full pass in the mode reached, then p_i if needed
+    tok = sample_pass(c, a.V, P, u, smem, smem + P * NT, red);
+    if (tok < 0 && c.mode == 0) {
+      c.mode = 1;
+      tok = -2;
+    }
+  }
+  if (t == 0) {
+    a.rres[2 * row] = ok;
+    a.rres[2 * row + 1] = tok;
+    const int old = __hip_atomic_fetch_add(a.ctr + step, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == k) {
+      // every row of the step is in (their results read after the acquire)
+      int n = k;
+      for (int r = 0; r < k; ++r)
+        if (!a.rres[2 * (step * (k + 1) + r)]) { n = r; break; }
+      a.n_accept[step] = n;
+      a.out_token[step] = a.rres[2 * (step * (k + 1) + n) + 1];
+    }
+  }
+}
+
 // ---------------------------------------------------------------- full-vocabulary scores (Sampler.scores)
 
 // out[row, j] for part p of the row: greedy - the penalised logit; sampling -
@@ -1192,11 +1654,21 @@ uint64_t filter_floats(int S, int k, int P, int top_k) {
   return lists + (uint64_t)S * (k + 1) * 4;
 }
 
+// list form without draft logits: per target row and part CAND_CAP candidate
+// indices and their count, then one finished-filter counter per step
+bool cand_fits(int P) { return P * CAND_CAP <= NT * CAND_IT; }
+uint64_t cand_ints(int S, int k, int P, int top_k, int has_draft) {
+  return (top_k >= 1 && top_k <= 64 && !has_draft && cand_fits(P))
+             ? (uint64_t)S * (k + 1) * P * (2 * CAND_CAP + 2) + S + (uint64_t)S * (k + 1) * 2
+             : 0;
+}
+
 extern "C" uint64_t qvex_spec_accept_filtered_workspace_bytes(int S, int k, int V, int has_draft, int top_k) {
   if (S < 1 || k < 0 || V < 1 || top_k < 0) return 0;
   const int rps = (k + 1) + (has_draft ? k : 0);
   const int P = nparts(V);
-  return (ws_floats(S, rps, P) + filter_floats(S, k, P, top_k)) * sizeof(float);
+  const int tk = top_k < V ? top_k : 0;
+  return (ws_floats(S, rps, P) + filter_floats(S, k, P, top_k) + cand_ints(S, k, P, tk, has_draft)) * sizeof(float);
 }
 
 extern "C" uint64_t qvex_spec_accept_workspace_bytes(int S, int k, int V, int has_draft) {
@@ -1226,8 +1698,10 @@ static int spec_accept_impl(const void* target, const void* draft, int bf, const
   const int kf = filt == 1 ? tk : 0;           // list-form top-k
   QVEX_CHECK_ARG(kf == 0 || P * kf <= 64 * 64, "qvex_spec_accept: V=%d too large for top_k=%d", V, kf);
   const int rps = (k + 1) + (draft ? k : 0);
+  const bool fast = filt == 1 && !draft && cand_fits(P);
   const uint64_t base = ws_floats(S, rps, P);
-  const uint64_t need = (base + (filt ? filter_floats(S, k, P, kf) : 0)) * sizeof(float);
+  const uint64_t need =
+      (base + (filt ? filter_floats(S, k, P, kf) : 0) + (fast ? cand_ints(S, k, P, kf, 0) : 0)) * sizeof(float);
   QVEX_CHECK_ARG(workspace_bytes >= need, "qvex_spec_accept: workspace %llu bytes < %llu needed",
                  (unsigned long long)workspace_bytes, (unsigned long long)need);
   const size_t lds = ((size_t)P * NT + P + 2 * rps) * sizeof(float);
@@ -1236,15 +1710,26 @@ static int spec_accept_impl(const void* target, const void* draft, int bf, const
   QVEX_CHECK_ARG(rps <= 80, "qvex_spec_accept: k=%d too large", k);
   float* fws = (float*)workspace + base;
   float* frow = fws + (kf > 0 ? (uint64_t)S * (k + 1) * P * (kf + 1) : 0);
+  int32_t* cand = reinterpret_cast<int32_t*>(frow + (uint64_t)S * (k + 1) * 4);
+  float* cand_z = reinterpret_cast<float*>(cand + (uint64_t)S * (k + 1) * P * CAND_CAP);
+  int32_t* ncand = reinterpret_cast<int32_t*>(cand_z + (uint64_t)S * (k + 1) * P * CAND_CAP);
+  int32_t* ctr = ncand + (uint64_t)S * (k + 1) * P * 2;
+  int32_t* rres = ctr + S;
   SpecArgs a{target, draft, draft_ids, u_accept, u_sample, inv_temp, greedy, n_accept, out_token,
              (float*)workspace, S, k, V, P, rps, seen, presence_penalty, kf, use_p ? top_p : 1.0f, fws, frow, bf,
-             filt, filt == 2 ? tk : 0};
+             filt, filt == 2 ? tk : 0, fast ? 1 : 0, fast ? cand : nullptr, fast ? cand_z : nullptr,
+             fast ? ncand : nullptr, fast ? ctr : nullptr, fast ? rres : nullptr};
   hipStream_t st = (hipStream_t)stream;
   if (a.bf)
     hipLaunchKernelGGL(spec_rowstats_kernel<true>, dim3(P, S * rps), dim3(NT), 0, st, a);
   else
     hipLaunchKernelGGL(spec_rowstats_kernel<false>, dim3(P, S * rps), dim3(NT), 0, st, a);
   QVEX_CHECK_LAUNCH("qvex_spec_accept/rowstats");
+  if (fast) {
+    hipLaunchKernelGGL(spec_finish_kernel, dim3(S * (k + 1)), dim3(NT), lds, st, a);
+    QVEX_CHECK_LAUNCH("qvex_spec_accept/finish");
+    return QVEX_OK;
+  }
   if (filt == 1) {
     hipLaunchKernelGGL(spec_filter_kernel, dim3(S * (k + 1)), dim3(NT), 0, st, a);
     QVEX_CHECK_LAUNCH("qvex_spec_accept/filter");

@@ -72,6 +72,35 @@ def test_filtered_accept_bit_exact(S, k, V, T, top_k, top_p, pen, bf16, dl):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("top_k,top_p", [(20, 0.8), (1, 1.0), (64, 0.95), (5, 1.0)])
+def test_list_form_ties_bit_exact(top_k, top_p):
+    """The list form without draft logits draws from each part's stored candidates
+    (indices with z at or above the part's k-th value, at most 96 per part) and
+    falls back to the full pass when a part holds more ties at the cutoff. Rows:
+    all logits equal (every part overflows at the cutoff), three distinct values
+    (thousands of ties), values on a 0.25 grid (ties at the cutoff in some parts),
+    and ordinary rows; S = 8 steps of k = 3 drafts, V = 248,320."""
+    S, k, V = 8, 3, 248320
+    target, _, ids, ua, us, _ = make_case(S, k, V, seed=300 + top_k, bf16=True)
+    g = np.random.default_rng(301 + top_k)
+    target[0] = 1.5
+    target[1] = g.integers(0, 3, size=(k + 1, V)).astype(np.float32)
+    target[2] = np.round(g.standard_normal((k + 1, V)) * 4.0).astype(np.float32) / 4.0
+    target[3, 1:] = 0.0                          # rows after the first tied
+    ids[:4] = g.integers(0, V, size=(4, k)).astype(np.int32)
+    ua[:4] = g.random((4, k)).astype(np.float32) * 0.5
+    assert_same(*run_both(target, None, ids, ua, us, 0.7, top_k=top_k, top_p=top_p))
+
+
+@pytest.mark.gpu
+def test_list_form_cycle_shape_many_seeds():
+    """The decode cycle's call (one step, k = 3, top-k 20, top-p 0.8, T = 0.7, bf16
+    logits) over 48 seeded rows of steps, bit-exact with the oracle."""
+    target, _, ids, ua, us, _ = make_case(48, 3, 248320, seed=777, bf16=True)
+    assert_same(*run_both(target, None, ids, ua, us, 0.7, top_k=20, top_p=0.8))
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("k", [0, 3])
 def test_greedy_presence_penalty_bit_exact(k):
     target, _, ids, ua, us, seen = make_case(16, k, 248320, seed=90 + k, bf16=True)
