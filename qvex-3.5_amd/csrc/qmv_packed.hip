@@ -645,9 +645,10 @@ int packed_prefetch_depth(int K, int TN, int WS) {
 // least 2 sets per wave; at most 8 waves per tile for K >= 12288 (the MLP down:
 // 512-thread blocks, 9.3 against 9.5 us at (1,16), -9.7 us per decode cycle).
 // Measured on the 9B shapes (M = 4 / 1, us): in_proj (2,8) 9.6 / 8.9, qkv (1,8)
-// 8.4 / 7.5, o_proj (1,8) 5.2 / 4.8, gate_up (2,4) 13.3 / 12.9 (the fused
-// gate/up product takes packed_swiglu_tile), mtp fc (1,16) 7.1 / 6.4, lm_head
-// (2,4) 93.5 / 86.0.
+// 8.4 / 7.5, o_proj (1,8) 5.2 / 4.8, gate_up (2,4) 13.3 / 12.9, mtp fc (1,16)
+// 7.1 / 6.4, lm_head (2,4) 93.5 / 86.0. The fused gate/up + SwiGLU product takes
+// the same tile: (2,4) two-deep 12.2 us against 13.2 for (1,4) with all four
+// sets in flight, -24 us per decode cycle (3 of 3 alternations).
 void packed_default_tile(int N, int K, int* TN, int* WS) {
   const long tiles = (N + PK_TILE - 1) / PK_TILE;
   const int GS = K / PK_SET;
@@ -660,18 +661,6 @@ void packed_default_tile(int N, int K, int* TN, int* WS) {
   if (GS >= 48 && ws > 8) ws = 8;                        // long K (the MLP down): 512-thread blocks
   *TN = tn;
   *WS = ws;
-}
-
-// The fused gate/up product: one tile per wave below lm_head widths (all of a
-// wave's sets in flight), measured on the 9B gate/up (N = 24576, K = 4096, M = 4):
-// (1,4) 12.2 us against 12.8 for the (2,4) of packed_default_tile.
-void packed_swiglu_tile(int N, int K, int* TN, int* WS) {
-  packed_default_tile(N, K, TN, WS);
-  const long tiles = (N + PK_TILE - 1) / PK_TILE;
-  if (*TN == 2 && tiles < 4096 && K / PK_SET >= 8) {
-    *TN = 1;
-    *WS = 4;
-  }
 }
 
 int launch_packed(const uint16_t* x, const uint8_t* packed, uint16_t* y, int M, int N, int K, int TN, int WS,
@@ -761,7 +750,7 @@ extern "C" int qvex_qmv_w4g64_packed_tiled(const uint16_t* x, const void* packed
 extern "C" int qvex_qmv_w4g64_packed_swiglu(const uint16_t* x, const void* packed, uint16_t* y, int M, int N, int K,
                                             void* stream) {
   int TN = 1, WS = 1;
-  if (N >= 1 && K >= PK_SET) packed_swiglu_tile(N, K, &TN, &WS);
+  if (N >= 1 && K >= PK_SET) packed_default_tile(N, K, &TN, &WS);
   return launch_packed(x, (const uint8_t*)packed, y, M, N, K, TN, WS, true, -1, PkEpi{}, (hipStream_t)stream);
 }
 
@@ -814,7 +803,7 @@ extern "C" int qvex_qmv_w4g64_packed_rstd(const uint16_t* u, const void* packed,
                  "%s: nparts=%d must be ceil(dim/16) for dim=%d, a multiple of 4 and <= 256", fn, nparts, dim);
   QVEX_CHECK_ARG(qvex_aligned(sq_parts, 16), "%s: sq_parts must be 16-byte aligned", fn);
   int TN = 1, WS = 1;
-  if (N >= 1 && K >= PK_SET) (swiglu ? packed_swiglu_tile : packed_default_tile)(N, K, &TN, &WS);
+  if (N >= 1 && K >= PK_SET) packed_default_tile(N, K, &TN, &WS);
   PkEpi e{};
   e.rs_parts = sq_parts;
   e.rs_nparts = nparts;
