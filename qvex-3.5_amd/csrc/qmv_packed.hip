@@ -661,6 +661,13 @@ void packed_default_tile(int N, int K, int* TN, int* WS) {
   if (GS >= 48 && ws > 8) ws = 8;                        // long K (the MLP down): 512-thread blocks
   *TN = tn;
   *WS = ws;
+  // 704..1023 tiles (the DeltaNet in_proj, N = 12352): one tile per wave and 2
+  // waves per tile, 8 sets each two-deep: -5 us per decode cycle against (2,8)
+  // (5 of 5 alternations)
+  if (tn == 2 && tiles < 1024 && GS >= 8) {
+    *TN = 1;
+    *WS = 2;
+  }
 }
 
 int launch_packed(const uint16_t* x, const uint8_t* packed, uint16_t* y, int M, int N, int K, int TN, int WS,

@@ -121,6 +121,8 @@ def default_tile(N, K):
         ws = 4
     if GS >= 48 and ws > 8:
         ws = 8
+    if tn == 2 and tiles < 1024 and GS >= 8:
+        tn, ws = 1, 2
     return tn, ws
 
 
