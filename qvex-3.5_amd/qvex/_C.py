@@ -67,6 +67,10 @@ SIGNATURES: dict[str, list] = {
     "qvex_rope_table": [I, F, I, P, P],
 }
 
+# qvex_abi_version() of the library these bindings match (3: tiled K/V caches,
+# qvex_attention's known_keys)
+ABI_VERSION = 3
+
 _lib: ctypes.CDLL | None = None
 
 
@@ -85,6 +89,9 @@ def lib() -> ctypes.CDLL:
         L.qvex_last_error.argtypes = []
         L.qvex_abi_version.restype = I
         L.qvex_abi_version.argtypes = []
+        if L.qvex_abi_version() != ABI_VERSION:
+            raise QvexError(f"{LIB_PATH} has ABI version {L.qvex_abi_version()}, these bindings need "
+                            f"{ABI_VERSION}: rebuild it")
         L.qvex_spec_accept_workspace_bytes.restype = U64
         L.qvex_spec_accept_workspace_bytes.argtypes = [I, I, I, I]
         L.qvex_attn_workspace_bytes.restype = U64

@@ -35,7 +35,7 @@ def test_bindings_cover_header():
 
 
 def test_abi_version():
-    assert _C.lib().qvex_abi_version() >= 1
+    assert _C.lib().qvex_abi_version() == _C.ABI_VERSION
 
 
 @pytest.mark.parametrize("M,N,K", [(0, 16, 64), (9, 16, 64), (1, 0, 64), (1, 16, 96), (1, 16, 0)])
