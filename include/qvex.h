@@ -143,7 +143,10 @@ int qvex_qmv_w4g64_packed_gnorm_resid(const uint16_t* u, const void* packed, int
  * keeps each 16-row tile's (max, first index); a one-block-per-row kernel
  * takes the first tile holding the row maximum. With sq_parts the rows are
  * scaled as qvex_qmv_w4g64_packed_rstd does (x = u of the final norm).
- * workspace: qvex_qmv_w4g64_argmax_workspace_bytes(M, N) = M * ceil(N/16) * 8. */
+ * workspace: qvex_qmv_w4g64_argmax_workspace_bytes(M, N) = M * ceil(N/16) * 8.
+ * With out_token NULL only the product runs: the workspace then holds row r's
+ * per-tile pairs at float offset r * ceil(N/16) * 2, for qvex_mtp_input or
+ * qvex_embed_rms_parts to reduce inside their own launch. */
 uint64_t qvex_qmv_w4g64_argmax_workspace_bytes(int M, int N);
 int qvex_qmv_w4g64_packed_argmax(const uint16_t* x, const void* packed, int M, int N, int K,
                                  const float* sq_parts, int nparts, int dim, float eps,
@@ -355,6 +358,33 @@ int qvex_rmsnorm(const uint16_t* x, long x_stride, const uint16_t* w, uint16_t* 
 int qvex_rmsnorm_pair(const uint16_t* x0, long x0_stride, const uint16_t* w0, uint16_t* out0,
                       const uint16_t* x1, long x1_stride, const uint16_t* w1, uint16_t* out1,
                       long out_stride, int R, int D, float eps, void* stream);
+
+/* The MTP head's input for one draft step in one launch (MTPHead.__call__,
+ * engine/mtp.py:61-63): x_in[r, 0:H] = rms_norm(embed(tok_r)) * w_emb and
+ * x_in[r, H:2H] = rms_norm(hid[s_r]) * w_hid, bit-identical to qvex_embed_w4g64
+ * + qvex_rmsnorm_pair. tok_r = ids[r], or, for T = 1 with am_parts, the greedy
+ * token of the previous step's lm_head: the argmax of the per-tile pairs that
+ * qvex_qmv_w4g64_packed_argmax left in its workspace (out_token NULL), row
+ * *am_row (NULL: row 0), stored to *ids_out (as that call's reduction would
+ * store it). s_r = *hid_sel (device row index; NULL: r). With counters, the
+ * launch also adds *n_accept (NULL: 0) + extra to counters[0 .. ncnt) (the
+ * previous step's qvex_commit_step). Same layout rules as those calls. */
+int qvex_mtp_input(const int32_t* ids, int T, const float* am_parts, int am_tiles, const int32_t* am_row,
+                   int32_t* ids_out, const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                   int V, int H, const uint16_t* w_emb, const uint16_t* hid, long hid_stride,
+                   const int32_t* hid_sel, const uint16_t* w_hid, uint16_t* x_in, long x_stride, float eps,
+                   int32_t* counters, int ncnt, const int32_t* n_accept, int extra, void* stream);
+
+/* The verify rows' input in one launch (QEmbedding.__call__, engine/model.py:
+ * 126-130, then the first layer's input norm, engine/model.py:309-310): h_out =
+ * embed(ids), and u_out, parts as qvex_rms_parts(h_out, norm_w) writes them,
+ * bit-identical to those two calls. With am_parts, ids[am_slot] is first
+ * replaced by the argmax of the per-tile pairs of row *am_row (NULL: row 0)
+ * that qvex_qmv_w4g64_packed_argmax left in its workspace (the last draft). */
+int qvex_embed_rms_parts(int32_t* ids, int L, const float* am_parts, int am_tiles, const int32_t* am_row,
+                         int am_slot, const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                         int V, int H, const uint16_t* norm_w, uint16_t* h_out, uint16_t* u_out,
+                         float* parts, void* stream);
 
 /* h = bf16(x + delta); out = rms_norm(h) * w: the residual add and the next
  * pre-norm of Layer.__call__ (engine/model.py:313-316) in one pass. [R, D],

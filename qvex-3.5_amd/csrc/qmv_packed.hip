@@ -839,7 +839,7 @@ extern "C" int qvex_qmv_w4g64_packed_argmax(const uint16_t* x, const void* packe
                                             const float* sq_parts, int nparts, int dim, float eps, int32_t* out_token,
                                             void* workspace, uint64_t workspace_bytes, void* stream) {
   const char* fn = "qvex_qmv_w4g64_packed_argmax";
-  QVEX_CHECK_ARG(out_token && workspace, "%s: null pointer", fn);
+  QVEX_CHECK_ARG(workspace, "%s: null pointer", fn);
   QVEX_CHECK_ARG(workspace_bytes >= qvex_qmv_w4g64_argmax_workspace_bytes(M, N),
                  "%s: workspace %llu bytes < %llu", fn, (unsigned long long)workspace_bytes,
                  (unsigned long long)qvex_qmv_w4g64_argmax_workspace_bytes(M, N));
@@ -861,6 +861,7 @@ extern "C" int qvex_qmv_w4g64_packed_argmax(const uint16_t* x, const void* packe
   if (int rc = launch_packed(x, (const uint8_t*)packed, nullptr, M, N, K, TN, WS, false, -1, e,
                              (hipStream_t)stream, fn))
     return rc;
+  if (!out_token) return QVEX_OK;   // the caller reduces the per-tile pairs (qvex_mtp_input, qvex_embed_rms_parts)
   hipLaunchKernelGGL(argmax_parts_kernel, dim3(M), dim3(AM_T), 0, (hipStream_t)stream, (const float*)workspace,
                      (N + PK_TILE - 1) / PK_TILE, out_token);
   QVEX_CHECK_LAUNCH(fn);

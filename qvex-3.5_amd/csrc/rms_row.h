@@ -26,26 +26,17 @@ __device__ __forceinline__ u32x4 pack8(const float* f) {
   return v;
 }
 
-template <bool ADD>
-__device__ __forceinline__ void rms_row256(const uint16_t* __restrict__ xr, const uint16_t* __restrict__ dr,
-                                           uint16_t* __restrict__ hr, const uint16_t* __restrict__ w,
-                                           uint16_t* __restrict__ outr, int D, float eps, float scale, float* red) {
+// The normalisation of a row whose values thread t already holds as v[c][e] =
+// element 8 (t + 256 c) + e (what rms_row256 loads): y = w * (v * inv) * scale.
+__device__ __forceinline__ void rms_vals256(float (&v)[RMS_MAXC][8], const uint16_t* __restrict__ w,
+                                            uint16_t* __restrict__ outr, int D, float eps, float scale, float* red) {
   const int t = threadIdx.x;
   const bool act = t < 256;
-  float v[RMS_MAXC][8];
   float ss = 0.0f;
 #pragma unroll
   for (int c = 0; c < RMS_MAXC; ++c) {
     const int i = (t + 256 * c) * 8;
     if (act && i < D) {
-      unpack8(load16(xr + i), v[c]);
-      if constexpr (ADD) {
-        float d[8];
-        unpack8(load16(dr + i), d);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[c][e] = bf16_to_f32(f32_to_bf16(v[c][e] + d[e]));
-        *reinterpret_cast<u32x4*>(hr + i) = pack8(v[c]);
-      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss = fmaf(v[c][e], v[c][e], ss);
     }
@@ -72,6 +63,30 @@ __device__ __forceinline__ void rms_row256(const uint16_t* __restrict__ xr, cons
       *reinterpret_cast<u32x4*>(outr + i) = pack8(o);
     }
   }
+}
+
+template <bool ADD>
+__device__ __forceinline__ void rms_row256(const uint16_t* __restrict__ xr, const uint16_t* __restrict__ dr,
+                                           uint16_t* __restrict__ hr, const uint16_t* __restrict__ w,
+                                           uint16_t* __restrict__ outr, int D, float eps, float scale, float* red) {
+  const int t = threadIdx.x;
+  const bool act = t < 256;
+  float v[RMS_MAXC][8];
+#pragma unroll
+  for (int c = 0; c < RMS_MAXC; ++c) {
+    const int i = (t + 256 * c) * 8;
+    if (act && i < D) {
+      unpack8(load16(xr + i), v[c]);
+      if constexpr (ADD) {
+        float d[8];
+        unpack8(load16(dr + i), d);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[c][e] = bf16_to_f32(f32_to_bf16(v[c][e] + d[e]));
+        *reinterpret_cast<u32x4*>(hr + i) = pack8(v[c]);
+      }
+    }
+  }
+  rms_vals256(v, w, outr, D, eps, scale, red);
 }
 
 }  // namespace

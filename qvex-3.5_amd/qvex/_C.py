@@ -48,6 +48,8 @@ SIGNATURES: dict[str, list] = {
     "qvex_sampler_scores": [P, I, I, I, P, F, F, I, F, P, P, U64, P],
     "qvex_mark_seen": [P, I, P, I, P, I, P],
     "qvex_embed_w4g64": [P, I, P, P, P, I, I, P, P],
+    "qvex_mtp_input": [P, I, P, I, P, P, P, P, P, I, I, P, P, LNG, P, P, P, LNG, F, P, I, P, I, P],
+    "qvex_embed_rms_parts": [P, I, P, I, P, I, P, P, P, I, I, P, P, P, P, P],
     "qvex_rmsnorm": [P, LNG, P, P, LNG, I, I, F, F, P],
     "qvex_add_rmsnorm": [P, P, P, P, P, I, I, F, P],
     "qvex_rmsnorm_pair": [P, LNG, P, P, P, LNG, P, P, LNG, I, I, F, P],
@@ -67,9 +69,9 @@ SIGNATURES: dict[str, list] = {
     "qvex_rope_table": [I, F, I, P, P],
 }
 
-# qvex_abi_version() of the library these bindings match (3: tiled K/V caches,
-# qvex_attention's known_keys)
-ABI_VERSION = 3
+# qvex_abi_version() of the library these bindings match (4: qvex_mtp_input,
+# qvex_embed_rms_parts, the deferred reduction of qvex_qmv_w4g64_packed_argmax)
+ABI_VERSION = 4
 
 _lib: ctypes.CDLL | None = None
 

@@ -259,20 +259,23 @@ def qmv_packed_rstd(u: torch.Tensor, packed: torch.Tensor, N: int, parts: torch.
     return out
 
 
-def qmv_packed_argmax(x: torch.Tensor, packed: torch.Tensor, N: int, out: torch.Tensor,
+def qmv_packed_argmax(x: torch.Tensor, packed: torch.Tensor, N: int, out: torch.Tensor | None,
                       parts: torch.Tensor | None = None, eps: float = 0.0,
                       workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Greedy token of each row of x W^T (first index of the largest bf16-rounded
     output, as an argmax over the product's bf16 result) without writing the
     product: out int32 [M]. With parts, x is NormedRows' u (the rows are scaled
-    by rsqrt(mean(h^2) + eps) as qmv_packed_rstd does)."""
+    by rsqrt(mean(h^2) + eps) as qmv_packed_rstd does). out=None defers the
+    reduction: returns the per-tile (max, first index) pairs [M, ceil(N/16), 2]
+    (a view of the workspace) for mtp_input / embed_rms_parts to reduce."""
     K = x.shape[-1]
     x2 = x.reshape(-1, K)
     M = x2.shape[0]
     _check(x2, "x", torch.bfloat16, 2)
-    _check(out, "out", torch.int32)
-    if out.numel() != M:
-        raise _C.QvexError(f"out must hold M = {M} values")
+    if out is not None:
+        _check(out, "out", torch.int32)
+        if out.numel() != M:
+            raise _C.QvexError(f"out must hold M = {M} values")
     if packed.numel() != int(_C.lib().qvex_w4g64_packed_bytes(N, K)):
         raise _C.QvexError(f"packed has {packed.numel()} bytes, not the size of an N={N} K={K} pack")
     need = int(_C.lib().qvex_qmv_w4g64_argmax_workspace_bytes(M, N))
@@ -284,9 +287,84 @@ def qmv_packed_argmax(x: torch.Tensor, packed: torch.Tensor, N: int, out: torch.
         if parts.numel() != M * nparts:
             raise _C.QvexError(f"parts must hold M * ceil(K/16) = {M * nparts} values")
     _C.call("qvex_qmv_w4g64_packed_argmax", _ptr(x2), _ptr(packed), M, N, K,
-            _ptr(parts) if parts is not None else None, nparts, K, float(eps), _ptr(out), _ptr(workspace),
+            _ptr(parts) if parts is not None else None, nparts, K, float(eps),
+            _ptr(out) if out is not None else None, _ptr(workspace),
             workspace.numel() * workspace.element_size(), _stream())
+    if out is None:
+        tiles = (N + 15) // 16
+        return workspace.view(-1)[:M * tiles * 2].view(M, tiles, 2)
     return out
+
+
+def _argmax_src(am, am_row):
+    """(pointer, tiles, row pointer) of a deferred argmax input (qmv_packed_argmax with out=None)."""
+    if am is None:
+        return None, 0, None
+    _check(am, "am", torch.float32)
+    if am.dim() != 3 or am.shape[2] != 2 or not am.is_contiguous():
+        raise _C.QvexError("am must be the [M, tiles, 2] pairs of qmv_packed_argmax(out=None)")
+    if am_row is not None:
+        _check(am_row, "am_row", torch.int32)
+    return _ptr(am), am.shape[1], _ptr(am_row) if am_row is not None else None
+
+
+def mtp_input(emb, ids, T: int, w_emb, hid, w_hid, eps: float, x_in: torch.Tensor, hid_sel=None, am=None,
+              am_row=None, ids_out=None, counters=None, n_accept=None, extra: int = 0) -> torch.Tensor:
+    """x_in [T, 2H] = [rms_norm(embed(ids)) * w_emb | rms_norm(hid[sel]) * w_hid] in one
+    launch (engine/mtp.py:61-63); emb is the QEmbedding (4-bit, group 64). With am
+    (T = 1) the token is the argmax of row am_row (device int32, None: 0) of the
+    deferred pairs, also stored to ids_out; hid_sel: device row index of hid; with
+    counters, *n_accept + extra is added to every counter in the same launch."""
+    H = emb.H
+    if (emb.bits, emb.group_size) != (4, 64):
+        raise _C.QvexError("mtp_input needs a 4-bit group-64 embedding")
+    hid2 = hid.reshape(-1, hid.shape[-1])
+    _check(hid2, "hid", torch.bfloat16, 2)
+    _check(x_in, "x_in", torch.bfloat16, 2)
+    if x_in.shape[0] < T or x_in.shape[1] < 2 * H:
+        raise _C.QvexError(f"x_in must hold [{T}, {2 * H}]")
+    amp, tiles, rowp = _argmax_src(am, am_row)
+    if am is None:
+        _check(ids, "ids", torch.int32)
+        if not ids.is_contiguous() or ids.numel() != T:
+            raise _C.QvexError("ids must be a contiguous int32 tensor of T values")
+    elif ids_out is None:
+        raise _C.QvexError("ids_out is needed with am")
+    if hid_sel is not None:
+        _check(hid_sel, "hid_sel", torch.int32)
+    if n_accept is not None:
+        _check(n_accept, "n_accept", torch.int32)
+    if counters is not None:
+        _check(counters, "counters", torch.int32)
+    _C.call("qvex_mtp_input", _ptr(ids) if am is None else None, T, amp, tiles, rowp,
+            _ptr(ids_out) if ids_out is not None else None, _ptr(emb.w), _ptr(emb.scales), _ptr(emb.biases),
+            emb.V, H, _ptr(w_emb), _ptr(hid2), hid2.stride(0), _ptr(hid_sel) if hid_sel is not None else None,
+            _ptr(w_hid), _ptr(x_in), x_in.stride(0), float(eps),
+            _ptr(counters) if counters is not None else None, counters.numel() if counters is not None else 0,
+            _ptr(n_accept) if n_accept is not None else None, int(extra), _stream())
+    return x_in
+
+
+def embed_rms_parts(emb, ids: torch.Tensor, norm_w: torch.Tensor, am=None, am_row=None, am_slot: int = -1,
+                    h_out=None, u_out=None, parts=None):
+    """h = embed(ids) [L, H] and the first norm's folded inputs (u, parts as
+    rms_parts(h, norm_w)) in one launch; with am, ids[am_slot] is first set to the
+    argmax of row am_row of the deferred pairs (the last draft). Returns (h, u, parts)."""
+    H = emb.H
+    if (emb.bits, emb.group_size) != (4, 64):
+        raise _C.QvexError("embed_rms_parts needs a 4-bit group-64 embedding")
+    _check(ids, "ids", torch.int32)
+    if not ids.is_contiguous():
+        raise _C.QvexError("ids must be contiguous")
+    L = ids.numel()
+    dev = ids.device
+    h_out = torch.empty((L, H), dtype=torch.bfloat16, device=dev) if h_out is None else h_out
+    u_out = torch.empty((L, H), dtype=torch.bfloat16, device=dev) if u_out is None else u_out
+    parts = torch.empty((L, (H + 15) // 16), dtype=torch.float32, device=dev) if parts is None else parts
+    amp, tiles, rowp = _argmax_src(am, am_row)
+    _C.call("qvex_embed_rms_parts", _ptr(ids), L, amp, tiles, rowp, int(am_slot), _ptr(emb.w), _ptr(emb.scales),
+            _ptr(emb.biases), emb.V, H, _ptr(norm_w), _ptr(h_out), _ptr(u_out), _ptr(parts), _stream())
+    return h_out, u_out, parts
 
 
 def rms_parts(x: torch.Tensor, w: torch.Tensor, u_out: torch.Tensor | None = None,

@@ -231,9 +231,13 @@ class QLinear:
             kernels.quantized_matmul(x2[m0:m1], w, sc, bi, out=o2[m0:m1])
         return out.view(*lead, self.N)
 
-    def argmax(self, x, out: torch.Tensor) -> torch.Tensor:
+    def argmax(self, x, out: torch.Tensor | None) -> torch.Tensor:
         """Greedy token per row of the product (first index of the largest bf16
-        output) into out int32 [M]; x a tensor or NormedRows of 1..8 rows."""
+        output) into out int32 [M]; x a tensor or NormedRows of 1..8 rows. out=None
+        (NormedRows input, packed weights): the reduction is left to the next
+        launch, which takes the returned per-tile pairs [M, ceil(N/16), 2]
+        (kernels.mtp_input / embed_rms_parts); the buffer is reused by the next
+        call with the same M."""
         if isinstance(x, NormedRows):
             M = x.u.reshape(-1, self.K).shape[0]
             if self._takes_normed(x, M) and not self.swiglu_packed:
@@ -244,6 +248,8 @@ class QLinear:
                     need = int(_C.lib().qvex_qmv_w4g64_argmax_workspace_bytes(M, self.N))
                     ws = self._am_ws[M] = torch.empty((need + 3) // 4, dtype=torch.float32, device=x.device)
                 return kernels.qmv_packed_argmax(x.u, self.packed, self.N, out, x.parts, x.eps, workspace=ws)
+        if out is None:
+            raise _C.QvexError("a deferred argmax needs NormedRows input and a packed QLinear")
         from .speculative import _argmax
         logits = self(x).reshape(-1, self.N)
         for r in range(logits.shape[0]):
@@ -810,9 +816,16 @@ class Qwen35:
         for q in self.qlinears():
             q.offload_mlx()
 
-    def __call__(self, ids, cache, last_only=True, return_hidden=False, keep_prev=False, hidden_out=None):
+    def _fused_inputs(self) -> bool:
+        e = self.embed
+        return isinstance(e, QEmbedding) and (e.bits, e.group_size) == (4, 64) and e.H % 64 == 0 and e.H <= 8192
+
+    def __call__(self, ids, cache, last_only=True, return_hidden=False, keep_prev=False, hidden_out=None,
+                 in_argmax=None):
         """ids: [1, L] int -> logits [1, L or 1, V] bf16 (and pre-norm hidden [1, L, H],
-        written into hidden_out when given)."""
+        written into hidden_out when given). in_argmax = (pairs, row, slot): ids[slot]
+        is first set, on the device, to the token of the deferred lm_head argmax
+        `pairs` (QLinear.argmax with out=None), row `row` (device int32 or None)."""
         ids = torch.as_tensor(ids, device=self.norm.device).reshape(-1)
         L = ids.numel()
         counters = cache.counters
@@ -834,11 +847,26 @@ class Qwen35:
             logits = outs[-1] if last_only else torch.cat(outs, dim=1)
             return (logits, torch.cat(hs, dim=1)) if return_hidden else logits
         counters.sync()
-        x = self.embed(ids)
         eps = self.cfg.rms_norm_eps
-        if self.fuse_norms and L <= QLinear.PACKED_MAX_ROWS and NormedRows.supported(self.cfg.hidden_size):
+        fused = self.fuse_norms and L <= QLinear.PACKED_MAX_ROWS and NormedRows.supported(self.cfg.hidden_size)
+        if in_argmax is not None and not (fused and self._fused_inputs()):
+            raise _C.QvexError("in_argmax needs the fused decode path (1..8 rows, 4-bit group-64 embedding)")
+        if fused and self._fused_inputs():
+            # embedding + the first norm's inputs in one launch (and the last
+            # draft's argmax, when the caller left it to this launch)
+            am, am_row, am_slot = in_argmax if in_argmax is not None else (None, None, -1)
+            ids32 = ids if ids.dtype == torch.int32 and ids.is_contiguous() else ids.to(torch.int32).contiguous()
+            if am is not None and ids32 is not ids:
+                raise _C.QvexError("in_argmax needs ids as a contiguous int32 device tensor (the slot is written)")
+            x, u, parts = kernels.embed_rms_parts(self.embed, ids32, self.layers[0].ln1, am, am_row, am_slot)
+            st = NormedRows(u, parts, eps)
+        else:
+            x = self.embed(ids)
+            if fused:
+                st = NormedRows.of(x, self.layers[0].ln1, eps)
+        if fused:
             # decode / verify: residual adds and norms ride on the products' epilogues
-            h, st = x, NormedRows.of(x, self.layers[0].ln1, eps)
+            h = x
             for i, (layer, c) in enumerate(zip(self.layers, cache)):
                 last = i + 1 == len(self.layers)
                 nxt = self.norm if last else self.layers[i + 1].ln1

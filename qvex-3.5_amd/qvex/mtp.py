@@ -15,7 +15,7 @@ import math
 
 import torch
 
-from . import _C
+from . import _C, kernels
 from .kernels import _ptr, _stream
 from .model import (Attention, KVCache, Layer, MLP, NormedRows, QLinear, Qwen35, _rand_qlinear, add_rms_norm,
                     rms_norm)
@@ -60,7 +60,7 @@ class MTPHead:
                        capacity=max_context or self.model.max_context, device=self.model.norm.device)
 
     def __call__(self, hidden, next_ids, cache: KVCache, last_only=True, return_hidden=False, select=None,
-                 argmax_out=None):
+                 argmax_out=None, defer_argmax=False, in_argmax=None, hid_sel=None, commit=None):
         """hidden [1, T, H] (main model, pre-norm) and next_ids [1, T] -> logits
         [1, 1 or T, V] (engine/mtp.py:58-68); with return_hidden also the block
         output [1, T, H] before the final norm (what a chained draft step takes).
@@ -68,19 +68,44 @@ class MTPHead:
         the lm_head (and is returned as the hidden), chosen on the device.
         argmax_out: optional int32 [1]; the greedy draft of the (selected or last)
         row is written there by the lm_head's argmax epilogue and no logits are
-        made (logits returned as None)."""
+        made (logits returned as None).
+        Launch-saving forms of the decode cycle (4-bit group-64 embedding, "pre"
+        hidden): defer_argmax returns the lm_head's per-tile argmax pairs of the
+        last (or, with last_only False, every) row in place of logits, for the next
+        launch to reduce; in_argmax = (pairs, row, ids_out) takes the step's token
+        (T = 1) from such pairs, row `row` (device int32 or None), storing it to
+        ids_out; hid_sel: device row index of `hidden`; commit = (counters, n,
+        extra) adds *n (None: 0) + extra to the cache counters in the same launch
+        (the previous step's advance)."""
         H = self.model.cfg.hidden_size
         h = hidden.reshape(-1, H)
-        ids = torch.as_tensor(next_ids, device=h.device).reshape(-1)
-        T = ids.numel()
+        if in_argmax is not None:
+            ids, T = None, 1
+        else:
+            ids = torch.as_tensor(next_ids, device=h.device).reshape(-1)
+            T = ids.numel()
         if self.hidden_mode == "post":
             h = rms_norm(h, self.model.norm, self.eps)
         cache.counters.sync()
-        e = self.model.embed(ids)
         x_in = torch.empty((T, 2 * H), dtype=torch.bfloat16, device=h.device)
-        # [rms(embed) | rms(hidden)] in one launch
-        _C.call("qvex_rmsnorm_pair", _ptr(e), e.stride(0), _ptr(self.norm_emb), _ptr(x_in), _ptr(h), h.stride(0),
-                _ptr(self.norm_hid), _ptr(x_in) + 2 * H, x_in.stride(0), T, H, float(self.eps), _stream())
+        if self.model._fused_inputs():
+            # embedding + both input norms (+ the previous draft's argmax and the
+            # previous step's counter advance) in one launch
+            am, am_row, ids_out = in_argmax if in_argmax is not None else (None, None, None)
+            cnt, n_ptr, extra = commit if commit is not None else (None, None, 0)
+            ids32 = None
+            if ids is not None:
+                ids32 = ids if ids.dtype == torch.int32 and ids.is_contiguous() else ids.to(torch.int32).contiguous()
+            kernels.mtp_input(self.model.embed, ids32, T, self.norm_emb, h, self.norm_hid, self.eps, x_in,
+                              hid_sel=hid_sel, am=am, am_row=am_row, ids_out=ids_out,
+                              counters=cnt.dev if cnt is not None else None, n_accept=n_ptr, extra=extra)
+        else:
+            if in_argmax is not None or hid_sel is not None or commit is not None:
+                raise _C.QvexError("in_argmax / hid_sel / commit need a 4-bit group-64 embedding")
+            e = self.model.embed(ids)
+            # [rms(embed) | rms(hidden)] in one launch
+            _C.call("qvex_rmsnorm_pair", _ptr(e), e.stride(0), _ptr(self.norm_emb), _ptr(x_in), _ptr(h), h.stride(0),
+                    _ptr(self.norm_hid), _ptr(x_in) + 2 * H, x_in.stride(0), T, H, float(self.eps), _stream())
         V = self.model.cfg.vocab_size
         if self.model.fuse_norms and T <= QLinear.PACKED_MAX_ROWS and NormedRows.supported(H):
             # the block's residual norms ride on its products (Layer.fused); the
@@ -92,6 +117,9 @@ class MTPHead:
             if not isinstance(n1, NormedRows):
                 n1 = NormedRows.of(x, self.layer.ln1, self.eps)
             out, st = self.layer.fused(x, n1, cache, False, self.norm_out)
+            if defer_argmax:
+                am = self.model.lm_head.argmax(st[-1:] if last_only else st, None)
+                return (am, out.view(1, T, H)) if return_hidden else am
             if select is not None:
                 o_sel = torch.empty((1, H), dtype=torch.bfloat16, device=h.device)
                 _C.call("qvex_gather_row", _ptr(out), H, _ptr(select), T, _ptr(o_sel), H, _stream())
@@ -109,6 +137,8 @@ class MTPHead:
                 from .speculative import _argmax
                 _argmax(logits[0, -1], out=argmax_out)
             return (logits, out.view(1, T, H)) if return_hidden else logits
+        if defer_argmax:
+            raise _C.QvexError("defer_argmax needs the fused path (1..8 rows)")
         x = self.fc(x_in)
         n = rms_norm(x, self.layer.ln1, self.eps)
         hh, m = self.layer(x, cache, normed=n)

@@ -255,17 +255,37 @@ class GraphedMTPCycle:
     def _body(self, out):
         d = self.dec
         k, mtp, mc = self.k, d.mtp, d.mtp_cache
-        # greedy drafts straight from the MTP lm_head's argmax epilogue into the verify ids
-        _, h = mtp(self.pend_h, self.pend_ids, mc, return_hidden=True, select=self.n_prev,
-                   argmax_out=self.ids[0, 1:2])
-        self._commit(mc.counters, self.n_prev, 1)
-        for j in range(1, k):
-            _, h = mtp(h, self.ids[:, j:j + 1], mc, last_only=True, return_hidden=True,
-                       argmax_out=self.ids[0, j + 1:j + 2])
-            if j < k - 1:                        # the last step's advance folds into the finish
-                self._commit(mc.counters, self.zero, 1)
-        logits, _ = d.model(self.ids, d.cache, last_only=False, return_hidden=True, keep_prev=True,
-                            hidden_out=self.pend_h)
+        if d.model._fused_inputs():
+            # Each draft's argmax is reduced inside the next launch (the next
+            # step's input, or the verify's embedding), which also stores it into
+            # the verify ids; a step's counter advance rides on the next step's
+            # input launch. Step 1 takes the k + 1 pending pairs: its lm_head runs
+            # on all of them and row n_prev (the hidden of the next step too) is
+            # picked on the device.
+            am, h = mtp(self.pend_h, self.pend_ids, mc, last_only=False, return_hidden=True, defer_argmax=True)
+            sel = self.n_prev
+            commit = (mc.counters, self.n_prev, 1)
+            for j in range(1, k):
+                am, h = mtp(h, None, mc, last_only=True, return_hidden=True, defer_argmax=True,
+                            in_argmax=(am, sel, self.ids[0, j:j + 1]), hid_sel=sel, commit=commit)
+                sel = None
+                commit = (mc.counters, None, 1) if j < k - 1 else None   # the last step's advance folds into the finish
+            if commit is not None:               # k = 1: no later draft launch to carry it
+                self._commit(mc.counters, self.n_prev, 1)
+            logits, _ = d.model(self.ids, d.cache, last_only=False, return_hidden=True, keep_prev=True,
+                                hidden_out=self.pend_h, in_argmax=(am, sel, k))
+        else:
+            # greedy drafts straight from the MTP lm_head's argmax epilogue into the verify ids
+            _, h = mtp(self.pend_h, self.pend_ids, mc, return_hidden=True, select=self.n_prev,
+                       argmax_out=self.ids[0, 1:2])
+            self._commit(mc.counters, self.n_prev, 1)
+            for j in range(1, k):
+                _, h = mtp(h, self.ids[:, j:j + 1], mc, last_only=True, return_hidden=True,
+                           argmax_out=self.ids[0, j + 1:j + 2])
+                if j < k - 1:                        # the last step's advance folds into the finish
+                    self._commit(mc.counters, self.zero, 1)
+            logits, _ = d.model(self.ids, d.cache, last_only=False, return_hidden=True, keep_prev=True,
+                                hidden_out=self.pend_h)
         n, tok = d.sampler.accept_device(logits[0], self.drafts, self.u_buf)
         # verify commit (+n+1 on every main cache), the k - 1 speculative MTP
         # entries rolled back (net -(k-2) after the folded last advance), the
