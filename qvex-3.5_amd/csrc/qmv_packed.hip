@@ -175,11 +175,21 @@ constexpr int pk_min_waves(int TN, int WS, int NP, int MH) { return TN == 2 && W
 // would) and writes bf16(silu(g) * u) to y [M, N/2]. MODE 2: the head-segment
 // scale of PkEpi (a mode of its own so that the other kernels keep their
 // registers). MODE 0: plain.
+// The arguments read before the first weight loads - x, the packed weights and
+// the shape, the consumer's partials (or the segment scales) with their count,
+// the residual and the norm weight - are separate scalar arguments at the front,
+// so that they fill the 14 dwords of kernel arguments preloaded into SGPRs (16
+// user SGPRs less the argument pointer): an aggregate argument is never
+// preloaded, and a wait for its fields held every first load back by a
+// scalar-load round trip. y and PkEpi (which keeps all fields) are read later.
 template <int TN, int WS, int NP, int MODE, int MH>
 __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk_min_waves(TN, WS, NP, MH)))) void qmv_packed_kernel(const uint16_t* __restrict__ x,
-                                                                   const uint8_t* __restrict__ packed,
-                                                                   uint16_t* __restrict__ y, int M, int N, int K,
-                                                                   PkEpi e) {
+                                                                   const uint8_t* __restrict__ packed, int M,
+                                                                   int N, int K, int pre_n,
+                                                                   const float* __restrict__ pre_p,
+                                                                   const uint16_t* __restrict__ pre_resid,
+                                                                   const uint16_t* __restrict__ pre_norm_w,
+                                                                   uint16_t* __restrict__ y, PkEpi e) {
   constexpr int NWAVE = pk_block(WS) / 64;
   constexpr int RG = NWAVE / WS;
   // the wave index is uniform: in an SGPR, the tile / set / record arithmetic is scalar
@@ -235,10 +245,10 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
   __shared__ __align__(16) float seg_tab[seg ? 64 * MR : 4];
   const int H = K / 128;
   float segv[8];
-  if constexpr (seg) {
+  if constexpr (seg) {   // pre_p = e.seg_ss, pre_n = e.seg_nb
     const int sh = min((int)threadIdx.x / MR, H - 1), sr = min((int)threadIdx.x % MR, M - 1);
 #pragma unroll
-    for (int b = 0; b < 8; ++b) segv[b] = e.seg_ss[((size_t)sr * H + sh) * e.seg_nb + min(b, e.seg_nb - 1)];
+    for (int b = 0; b < 8; ++b) segv[b] = pre_p[((size_t)sr * H + sh) * pre_n + min(b, pre_n - 1)];
   }
   auto seg_table = [&]() {
     if constexpr (seg) {
@@ -246,7 +256,7 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
         float v = segv[0];
 #pragma unroll
         for (int b = 1; b < 8; ++b)
-          if (b < e.seg_nb) v += segv[b];
+          if (b < pre_n) v += segv[b];
         seg_tab[threadIdx.x] = (int)(threadIdx.x % MR) < M ? rsqrtf(v / 128.0f + e.seg_eps) : 1.0f;
       }
       __syncthreads();
@@ -254,12 +264,13 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
   };
 
   // epilogue inputs, requested before the weights so their latency hides
-  const bool rs = e.rs_parts != nullptr, prod = e.resid != nullptr;
+  // (MODE != 2: pre_p = e.rs_parts, pre_n = e.rs_nparts)
+  const bool rs = !seg && pre_p != nullptr, prod = pre_resid != nullptr;
   u32x4 rsp[MR];
   if (rs && ws == 0) {
 #pragma unroll
     for (int r = 0; r < MR; ++r)
-      rsp[r] = load16(e.rs_parts + (size_t)min(r, M - 1) * e.rs_nparts + min(4 * lane, e.rs_nparts - 4));
+      rsp[r] = load16(pre_p + (size_t)min(r, M - 1) * pre_n + min(4 * lane, pre_n - 4));
   }
   // the plain epilogue gives lane L row L / 16 and column L % 16 of each tile
   const int er = lane >> 4, ei = lane & 15;
@@ -267,8 +278,8 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
   // branch the compiler converts them as soon as they arrive, which waits)
   uint16_t rsd[MH][TN], nw[TN];
   {
-    const uint16_t* rp = prod ? e.resid : x;
-    const uint16_t* wp = prod ? e.norm_w : x;
+    const uint16_t* rp = prod ? pre_resid : x;
+    const uint16_t* wp = prod ? pre_norm_w : x;
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
       const int nc = min((tile0 + t) * PK_TILE + ei, N - 1);   // columns past N and rows past M are never stored
@@ -292,7 +303,7 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
     for (int r = 0; r < MR; ++r) {
       float v = ((__uint_as_float(rsp[r].x) + __uint_as_float(rsp[r].y)) + __uint_as_float(rsp[r].z)) +
                 __uint_as_float(rsp[r].w);
-      v = 4 * lane < e.rs_nparts ? v : 0.0f;   // lanes past the partials loaded a copy
+      v = 4 * lane < pre_n ? v : 0.0f;   // lanes past the partials loaded a copy
       v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_sum_to_lane63(v)), 63));
       rstd[r] = rsqrtf(v / (float)e.rs_dim + e.rs_eps);
       rs_row[r / 4] = (r % 4) == er ? rstd[r] : rs_row[r / 4];
@@ -586,7 +597,8 @@ __global__ __launch_bounds__(256) void rms_parts_kernel(const uint16_t* __restri
   if (i16 == 0 && tile < tiles) parts[(size_t)r * tiles + tile] = sq;
 }
 
-typedef void (*qmv_packed_fn)(const uint16_t*, const uint8_t*, uint16_t*, int, int, int, PkEpi);
+typedef void (*qmv_packed_fn)(const uint16_t*, const uint8_t*, int, int, int, int, const float*, const uint16_t*,
+                              const uint16_t*, uint16_t*, PkEpi);
 
 template <int TN, int NP, int SW, int MH>
 qmv_packed_fn pick_ws(int ws) {
@@ -699,7 +711,9 @@ int launch_packed(const uint16_t* x, const uint8_t* packed, uint16_t* y, int M, 
   const int tiles = (N + PK_TILE - 1) / PK_TILE;
   const int tiles_per_block = TN * (threads / 64 / WS);
   const int blocks = (tiles + tiles_per_block - 1) / tiles_per_block;
-  hipLaunchKernelGGL(fn, dim3(blocks), dim3(threads), 0, stream, x, packed, y, M, N, K, e);
+  const bool segm = e.seg_ss != nullptr && !swiglu;
+  hipLaunchKernelGGL(fn, dim3(blocks), dim3(threads), 0, stream, x, packed, M, N, K, segm ? e.seg_nb : e.rs_nparts,
+                     segm ? e.seg_ss : e.rs_parts, e.resid, e.norm_w, y, e);
   QVEX_CHECK_LAUNCH(fn_name);
   return QVEX_OK;
 }
