@@ -358,28 +358,43 @@ __global__ __launch_bounds__(FUSED_THREADS) void gdn_decode_fused_kernel(GdnFuse
 // the token loop is unrolled into one branch-free block, so one token's output
 // dot, gated-norm input and snapshot overlap the next token's state update (the
 // same operations in the same order as a loop: the same bits).
+// What the first loads need - the token-count pointer, the state, projection,
+// conv-ring and conv-weight pointers and the shape, small values packed in
+// pairs of 16 bits - is passed as scalar arguments ahead of the argument struct
+// (an aggregate is never preloaded into SGPRs: 14 dwords are), so the count's
+// load and the count-independent loads go out at wave start instead of after a
+// chain of waits for struct fields, the count, then more fields.
+//   dims0 = p_stride | R << 16, dims1 = n_slots | Hv << 8 | Hk << 16,
+//   dims2 = z_off | ab_off << 16, dims3 = C | key_dim << 16.
 template <int NB, int TT>
-__global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArgs p, float* ss_parts) {
+__global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(
+    const int32_t* __restrict__ counter, float* __restrict__ state_, const uint16_t* __restrict__ proj_,
+    uint16_t* __restrict__ ring_, const uint16_t* __restrict__ cw_, uint32_t dims0, uint32_t dims1, uint32_t dims2,
+    uint32_t dims3, GdnFusedArgs p, float* ss_parts) {
+  const int p_stride_ = (int)(dims0 & 0xffffu), R_ = (int)(dims0 >> 16);
+  const int n_slots_ = (int)(dims1 & 0xffu), Hv_ = (int)((dims1 >> 8) & 0xffu), Hk_ = (int)(dims1 >> 16);
+  const int z_off_ = (int)(dims2 & 0xffffu), ab_off_ = (int)(dims2 >> 16);
+  const int C_ = (int)(dims3 & 0xffffu), key_dim_ = (int)(dims3 >> 16);
   constexpr int RB = DK / NB;            // rows per block
   constexpr int NTH = 16 * RB;           // threads
   constexpr int NW = NTH / 64;           // waves
   __shared__ float qs[FUSED_TMAX][DK], ks[FUSED_TMAX][DK], vs[FUSED_TMAX][RB], ys[FUSED_TMAX][RB];
   __shared__ float gb_s[2][FUSED_TMAX];
   const int hv = blockIdx.x / NB, b = blockIdx.x % NB;
-  const int hk = hv / (p.Hv / p.Hk);
+  const int hk = hv / (Hv_ / Hk_);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int grp = threadIdx.x >> 4, l16 = threadIdx.x & 15;
   const int dv = b * RB + grp;
   constexpr int T = TT;
-  const long p0 = *p.counter;
-  const int cur = (int)(((p0 % p.n_slots) + p.n_slots) % p.n_slots);
-  const int rbase = (int)(((p0 % p.R) + p.R) % p.R);
-  const long slot_stride = (long)p.Hv * DK * DK;
+  const long p0 = *counter;
+  const int cur = (int)(((p0 % n_slots_) + n_slots_) % n_slots_);
+  const int rbase = (int)(((p0 % R_) + R_) % R_);
+  const long slot_stride = (long)Hv_ * DK * DK;
   // this block's state row first (it waits on the token count)
   const long row_off = ((long)hv * DK + dv) * DK + l16 * 8;
   float st[8];
   {
-    const float* src = p.state + cur * slot_stride + row_off;
+    const float* src = state_ + cur * slot_stride + row_off;
     const u32x4 s0 = load16(src);
     const u32x4 s1 = load16(src + 4);
     st[0] = __uint_as_float(s0.x); st[1] = __uint_as_float(s0.y);
@@ -395,8 +410,8 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArg
     const int t = threadIdx.x;
     a_log = p.A_log[hv];
     dt_raw = p.dt_bias[hv];
-    aa_raw = p.proj[(size_t)t * p.p_stride + p.ab_off + p.Hv + hv];
-    bb_raw = p.proj[(size_t)t * p.p_stride + p.ab_off + hv];
+    aa_raw = proj_[(size_t)t * p_stride_ + ab_off_ + Hv_ + hv];
+    bb_raw = proj_[(size_t)t * p_stride_ + ab_off_ + hv];
   }
   // this row's z for every token and its norm weight, in every lane of the
   // row (the unrolled token loop has all 16 store the row's output; the 16
@@ -406,7 +421,7 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArg
   uint32_t zr[FUSED_TMAX];
   const uint32_t wr_raw = p.norm_w[dv];
 #pragma unroll
-  for (int t = 0; t < FUSED_TMAX; ++t) zr[t] = p.proj[(size_t)min(t, T - 1) * p.p_stride + p.z_off + hv * DK + dv];
+  for (int t = 0; t < FUSED_TMAX; ++t) zr[t] = proj_[(size_t)min(t, T - 1) * p_stride_ + z_off_ + hv * DK + dv];
   // 1. conv + silu. Two kinds of task, each one wave with all of its loads
   // issued in its own iteration: a token's q and k heads (lane: channels 2l,
   // 2l+1 of both, each head normed by its own wave sum as in
@@ -417,7 +432,7 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArg
   constexpr int W = FUSED_KC - 1;
   constexpr int VPT = RB / 2;          // v channel pairs per token
   constexpr int VTOK = 64 / VPT;       // tokens per v task
-  const bool ring_qk = hv % (p.Hv / p.Hk) == 0 && b == 0;
+  const bool ring_qk = hv % (Hv_ / Hk_) == 0 && b == 0;
   auto conv_pair = [&](const uint32_t (&win)[FUSED_KC], const u32x4 taps, float& s0, float& s1) {
     const float w0[4] = {bf16_lo(taps.x), bf16_hi(taps.x), bf16_lo(taps.y), bf16_hi(taps.y)};
     const float w1[4] = {bf16_lo(taps.z), bf16_hi(taps.z), bf16_lo(taps.w), bf16_hi(taps.w)};
@@ -434,26 +449,26 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArg
   for (int task = wave; task < T + n_vt; task += NW) {
     if (task < T) {                       // uniform over the wave
       const int t = task;
-      const int cq = hk * DK + 2 * lane, ck = p.key_dim + hk * DK + 2 * lane;
+      const int cq = hk * DK + 2 * lane, ck = key_dim_ + hk * DK + 2 * lane;
       uint32_t wq[FUSED_KC], wk[FUSED_KC];
 #pragma unroll
       for (int j = 0; j < FUSED_KC; ++j) {
         const int r = t + j;
         if (r < W) {
-          const long rr = wrap_add(rbase, r - W, p.R);
-          wq[j] = *reinterpret_cast<const uint32_t*>(p.ring + rr * p.C + cq);
-          wk[j] = *reinterpret_cast<const uint32_t*>(p.ring + rr * p.C + ck);
+          const long rr = wrap_add(rbase, r - W, R_);
+          wq[j] = *reinterpret_cast<const uint32_t*>(ring_ + rr * C_ + cq);
+          wk[j] = *reinterpret_cast<const uint32_t*>(ring_ + rr * C_ + ck);
         } else {
-          wq[j] = *reinterpret_cast<const uint32_t*>(p.proj + (size_t)(r - W) * p.p_stride + cq);
-          wk[j] = *reinterpret_cast<const uint32_t*>(p.proj + (size_t)(r - W) * p.p_stride + ck);
+          wq[j] = *reinterpret_cast<const uint32_t*>(proj_ + (size_t)(r - W) * p_stride_ + cq);
+          wk[j] = *reinterpret_cast<const uint32_t*>(proj_ + (size_t)(r - W) * p_stride_ + ck);
         }
       }
-      const u32x4 tq = load16(p.cw + (size_t)cq * FUSED_KC);
-      const u32x4 tk = load16(p.cw + (size_t)ck * FUSED_KC);
+      const u32x4 tq = load16(cw_ + (size_t)cq * FUSED_KC);
+      const u32x4 tk = load16(cw_ + (size_t)ck * FUSED_KC);
       if (ring_qk) {
-        const long rr = wrap_add(rbase, t, p.R);
-        *reinterpret_cast<uint32_t*>(p.ring + rr * p.C + cq) = wq[W];
-        *reinterpret_cast<uint32_t*>(p.ring + rr * p.C + ck) = wk[W];
+        const long rr = wrap_add(rbase, t, R_);
+        *reinterpret_cast<uint32_t*>(ring_ + rr * C_ + cq) = wq[W];
+        *reinterpret_cast<uint32_t*>(ring_ + rr * C_ + ck) = wk[W];
       }
       float q0, q1, k0, k1;
       conv_pair(wq, tq, q0, q1);
@@ -469,21 +484,21 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArg
     } else {
       const int t = (task - T) * VTOK + lane / VPT, cp = lane % VPT;
       if (t < T) {
-        const int c0 = 2 * p.key_dim + hv * DK + b * RB + 2 * cp;
+        const int c0 = 2 * key_dim_ + hv * DK + b * RB + 2 * cp;
         uint32_t win[FUSED_KC];
 #pragma unroll
         for (int j = 0; j < FUSED_KC; ++j) {
           const int r = t + j;
           if (r < W) {
-            const long rr = wrap_add(rbase, r - W, p.R);
-            win[j] = *reinterpret_cast<const uint32_t*>(p.ring + rr * p.C + c0);
+            const long rr = wrap_add(rbase, r - W, R_);
+            win[j] = *reinterpret_cast<const uint32_t*>(ring_ + rr * C_ + c0);
           } else {
-            win[j] = *reinterpret_cast<const uint32_t*>(p.proj + (size_t)(r - W) * p.p_stride + c0);
+            win[j] = *reinterpret_cast<const uint32_t*>(proj_ + (size_t)(r - W) * p_stride_ + c0);
           }
         }
-        const u32x4 taps = load16(p.cw + (size_t)c0 * FUSED_KC);
-        const long rr = wrap_add(rbase, t, p.R);
-        *reinterpret_cast<uint32_t*>(p.ring + rr * p.C + c0) = win[W];
+        const u32x4 taps = load16(cw_ + (size_t)c0 * FUSED_KC);
+        const long rr = wrap_add(rbase, t, R_);
+        *reinterpret_cast<uint32_t*>(ring_ + rr * C_ + c0) = win[W];
         float v0, v1;
         conv_pair(win, taps, v0, v1);
         const uint32_t pv = pack_bf16x2(v0, v1);
@@ -542,12 +557,12 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArg
       uint32_t wb = wr_raw;
       asm volatile("" : "+v"(zb), "+v"(wb));
       const float zt = bf16_to_f32((uint16_t)zb);
-      p.out[(size_t)t * p.Hv * DK + hv * DK + dv] = f32_to_bf16(silu(zt) * (bf16_to_f32((uint16_t)wb) * y));
+      p.out[(size_t)t * Hv_ * DK + hv * DK + dv] = f32_to_bf16(silu(zt) * (bf16_to_f32((uint16_t)wb) * y));
     }
     // without per-token snapshots every token stores to the final slot (the
     // last store wins): no branch in the unrolled form
-    const int slot = (p.snap_every ? 1 + t : T) % p.n_slots;
-    float* dstp = p.state + wrap_add(cur, slot, p.n_slots) * slot_stride + row_off;
+    const int slot = (p.snap_every ? 1 + t : T) % n_slots_;
+    float* dstp = state_ + wrap_add(cur, slot, n_slots_) * slot_stride + row_off;
     u32x4 o0, o1;
     o0.x = __float_as_uint(st[0]); o0.y = __float_as_uint(st[1]);
     o0.z = __float_as_uint(st[2]); o0.w = __float_as_uint(st[3]);
@@ -564,7 +579,7 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(GdnFusedArg
   for (int t = wave; t < T; t += NW) {
     const float y = lane < RB ? ys[t][lane] : 0.0f;
     const float ss = wave_allsum(y * y);
-    if (lane == 0) ss_parts[((size_t)t * p.Hv + hv) * NB + b] = ss;
+    if (lane == 0) ss_parts[((size_t)t * Hv_ + hv) * NB + b] = ss;
   }
 }
 
@@ -657,7 +672,12 @@ extern "C" int qvex_gdn_decode_fused(const uint16_t* proj, long p_stride, uint16
 
 template <int NB, int TT>
 void launch_split_t(dim3 grid, hipStream_t st, const GdnFusedArgs& p, float* ss_parts) {
-  hipLaunchKernelGGL((gdn_decode_split_kernel<NB, TT>), grid, dim3(2048 / NB), 0, st, p, ss_parts);
+  const uint32_t d0 = (uint32_t)p.p_stride | ((uint32_t)p.R << 16);
+  const uint32_t d1 = (uint32_t)p.n_slots | ((uint32_t)p.Hv << 8) | ((uint32_t)p.Hk << 16);
+  const uint32_t d2 = (uint32_t)p.z_off | ((uint32_t)p.ab_off << 16);
+  const uint32_t d3 = (uint32_t)p.C | ((uint32_t)p.key_dim << 16);
+  hipLaunchKernelGGL((gdn_decode_split_kernel<NB, TT>), grid, dim3(2048 / NB), 0, st, p.counter, p.state, p.proj,
+                     p.ring, p.cw, d0, d1, d2, d3, p, ss_parts);
 }
 
 template <int NB>
@@ -706,6 +726,9 @@ extern "C" int qvex_gdn_decode_split(const uint16_t* proj, long p_stride, uint16
   QVEX_CHECK_ARG(qvex_aligned(proj, 4) && qvex_aligned(conv_ring, 4) && qvex_aligned(state_ring, 16) &&
                      qvex_aligned(conv_w, 16),
                  "%s: proj, conv_ring need 4-byte and state_ring, conv_w 16-byte alignment", fn);
+  QVEX_CHECK_ARG(p_stride < 65536 && ring_rows < 65536 && n_slots < 256 && Hv < 256 && Hk < 65536 &&
+                     z_offset < 65536 && ab_offset < 65536 && conv_dim < 65536 && key_dim < 65536,
+                 "%s: p_stride, ring_rows, offsets and dims must be below 65536 (n_slots, Hv below 256)", fn);
   GdnFusedArgs p{proj, p_stride, conv_ring, ring_rows, counter, conv_w, conv_dim, key_dim,
                  q_scale, k_scale, qk_eps, A_log, dt_bias, z_offset, ab_offset, state_ring, n_slots,
                  snap_every ? 1 : 0, norm_w, 0.0f, u_out, T, Hk, Hv};
