@@ -28,7 +28,9 @@ Every line also carries:
     tokens per second with the GPU run's tokens per cycle;
   cpu_baselines: the same restatement beside each config's GPU figure
     (config-0 GEMV, config-2 verify recurrence, config-3 accept on a sample of
-    steps), on all host threads, best of repeated runs.
+    steps), on all host threads, best of repeated runs;
+  cycle_kernels: the cycle's split DeltaNet mixer and verify attention (one
+    layer at the 9B shape, isolated, rotating caches) with their HBM fractions.
 
 --accept-all is a labelled diagnostic, not the headline: greedy decoding with
 the shared lm_head zeroed, so every draft is accepted (k + 1 tokens a cycle)
@@ -220,6 +222,31 @@ def qmv_shapes():
     return out
 
 
+def _graph_time(fn, iters, reps=5):
+    """Best-of-reps average µs per call of fn(i), i = 0..iters-1, captured once as a
+    HIP graph and replayed between HIP events (no host launch cost in the timing,
+    as in the decode cycle)."""
+    import torch
+    fn(0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(iters):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e3 / iters)
+    del g
+    return best
+
+
 def _event_time(fn, iters, reps=3):
     """Best-of-reps average µs per call of fn(i), i = 0..iters-1, between HIP events
     on the current stream (every call launches on that stream)."""
@@ -291,7 +318,7 @@ def gdn_config2_verify(T=5, Hk=16, Hv=32, D=128, copies=40):
     states = [torch.randn((1, Hv, D, D), generator=g, device=dev) * 0.02 for _ in range(copies)]
     snaps = [torch.empty((T, 1, Hv, D, D), device=dev) for _ in range(copies)]
     y = torch.empty((1, T, Hv, D), device=dev, dtype=bf)
-    us = _event_time(lambda i: kernels.gated_delta_snapshots(q, kk, v, a, b, A_log, dt, states[i % copies],
+    us = _graph_time(lambda i: kernels.gated_delta_snapshots(q, kk, v, a, b, A_log, dt, states[i % copies],
                                                               snapshots=snaps[i % copies], y=y), 4 * copies)
     nbytes = (1 + T) * Hv * D * D * 4 + 2 * T * Hk * D * 2 + 2 * T * Hv * D * 2 + 2 * T * Hv * 2
     return {"kernel": "qvex_gdn_recurrent (T=5, per-token snapshots)", "us": round(us, 2),
@@ -432,7 +459,7 @@ def mixer_verify(copies=24, iters=96):
     g = torch.Generator(device="cuda:0")
     g.manual_seed(5)
     proj = (torch.randn((4, gdn.in_proj.N), generator=g, device="cuda:0")).to(torch.bfloat16)
-    us = _event_time(lambda i: gdn.mix_split(proj, caches[i % copies][0]), iters)
+    us = _graph_time(lambda i: gdn.mix_split(proj, caches[i % copies][0]), iters)
     nbytes = 5 * 32 * 128 * 128 * 4
     return {"kernel": "qvex_gdn_decode_split (4 blocks per head, T=4 with snapshots)", "us": round(us, 2),
             "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1), "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
@@ -479,8 +506,8 @@ def attn_verify(L=4, pos0=4348, copies=24, iters=96, kps=128):
         _C.call("qvex_attention_decode", _ptr(proj), proj.stride(0), _ptr(qn), _ptr(qn), _ptr(pos), L, Hq, Hkv, D,
                 rot, 1e-6, _ptr(tab), tab.shape[0], _ptr(kc[c]), _ptr(vc[c]), cap, pos0 + L, kps, _ptr(out), _ptr(ws),
                 ws.numel() * 4, _stream())
-    us2 = _event_time(two_launch, iters)
-    us = _event_time(fused, iters)
+    us2 = _graph_time(two_launch, iters)
+    us = _graph_time(fused, iters)
     nbytes = 2 * Hkv * (pos0 + L) * D * 2
     return {"kernel": "qvex_attention_decode (decode partial + combine)", "ctx": pos0 + L, "us": round(us, 2),
             "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1), "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
@@ -649,6 +676,17 @@ def main():
         line["spec_config3"] = spec_config3()
         log("config-2 prefill (chunked GDN)")
         line["gdn_config2_prefill"] = gdn_config2_prefill()
+        log("the cycle's other hot kernels (DeltaNet mixer, verify attention)")
+        att = attn_verify()
+        gbs = att["bytes"] / (att["two_launch_us"] * 1e-6) / 1e9
+        line["cycle_kernels"] = {
+            "gdn_mixer": mixer_verify(),
+            "attention": {"kernel": "qvex_attn_qk_rope + qvex_attention (the cycle's path: q/k norm, RoPE and KV "
+                                    "append, then the split-K partial and the combine)",
+                          "ctx": att["ctx"], "us": att["two_launch_us"], "GB/s": round(gbs, 1),
+                          "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": att["bytes"],
+                          "fused_decode_us": att["us"]},
+        }
     if not args.no_cpu_baseline:
         log("cpu baseline")
         tpc = res["tokens_per_cycle"] if res else 1.0
