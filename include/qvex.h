@@ -72,6 +72,37 @@ int qvex_qmv_w4g64_mfma(const uint16_t* x, const uint32_t* w, const uint16_t* sc
                         int tiles_per_wave, int wave_ksplit, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Other widths and groups of the MLX affine layout: bits in {2,3,4,5,6,8},
+ * group_size in {32,64,128} (per-module overrides, Config.qparams at
+ * engine/model.py:68-71; mixed 4/3-bit models from quant/build.py:67-68).
+ * Each weight row is a little-endian bit stream of K codes (quant/quantize.py:
+ * 71-75): q[n, k] = bits [k*bits, (k+1)*bits) of row n's stream, w: uint32
+ * [N, K*bits/32]; scales, biases: bf16 [N, K/group_size].
+ *
+ * y[M, N] = x[M, K] @ dequant(W)^T, fp32 accumulation per 32-code chunk
+ * (sum q*x and sum x, folded with the group's scale and bias), one bf16
+ * rounding: mx.quantized_matmul(..., group_size, bits) in QLinear.__call__
+ * (engine/model.py:87-91). 1 <= M <= 8, K % group_size == 0, x and w 16-byte
+ * aligned. */
+int qvex_qmv_affine(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
+                    const uint16_t* biases, uint16_t* y, int M, int N, int K, int bits,
+                    int group_size, void* stream);
+/* out[l, :] = bf16(s * q + b) of row ids[l] (clamped to [0, V)): mx.dequantize
+ * of the gathered rows in QEmbedding.__call__ (engine/model.py:126-130).
+ * H % group_size == 0; w, out 16-byte aligned. */
+int qvex_embed_affine(const int32_t* ids, int L, const uint32_t* w, const uint16_t* scales,
+                      const uint16_t* biases, int V, int H, int bits, int group_size,
+                      uint16_t* out, void* stream);
+/* Lossless re-encoding of a bits <= 4, group 64 or 128 weight in the 4-bit
+ * group-64 layout (codes unchanged in nibbles, a group-128 scale and bias
+ * repeated for both halves): w4 uint32 [N, K/8], scales4, biases4 bf16
+ * [N, K/64]; every 4-bit group-64 entry point then computes the same
+ * products. No reference counterpart (a layout step of this library). */
+int qvex_affine_widen_w4g64(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                            int N, int K, int bits, int group_size, uint32_t* w4,
+                            uint16_t* scales4, uint16_t* biases4, void* stream);
+
+/* ------------------------------------------------------------------------
  * Tile-packed weights: the QLinear triplet (engine/model.py:83-85) re-laid
  * once, at layer construction, as records of (16 rows x 256 k): 2048 bytes of
  * 4-bit words in the order the MFMA lanes consume them (nibbles reordered so

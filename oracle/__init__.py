@@ -8,15 +8,21 @@ never as the thing being measured or shipped. The product path
 Contents:
   * liboracle.so (oracle/*.c, built by oracle/Makefile): fp64 qmv, fp64/fp32
     Gated DeltaNet recurrence, fp32-emulation speculative acceptance;
-  * numpy helpers: bf16 rounding, the MLX 4-bit pack/unpack
-    (quant/quantize.py:71-75), and a numpy layer-level restatement
-    (oracle.model) of the verify forward.
+  * numpy helpers: bf16 rounding, the MLX affine pack/unpack of any width
+    (quant/quantize.py:71-75) with its fp64 dequant and product, and a numpy
+    layer-level restatement (oracle.model) of the verify forward.
 
 Pinning (what checks each function against something other than itself) is
 listed per function below; each is exercised in tests/test_oracle.py.
   - qmv_f64: independent numpy dequant (np.unpackbits, quant/quantize.py:71-75)
     + float64 matmul; closed forms (q = 8 with b = -8s gives 0; x = e_k gives
     column k; s = 1, b = 0 gives an exact integer GEMV); golden fixtures.
+  - pack_bits / unpack_bits / dequant_f64 / qmv_affine_f64 (any width):
+    codes against a Python-integer stream (sum of q_k << bits*k, cut into
+    32-bit words), hand-worked 2-, 3- and 8-bit words, pack_w4 at 4 bits,
+    qmv_f64 (C) at 4-bit group 64, scale/bias shared within a group and a
+    zero product where every code is the bias midpoint
+    (tests/test_oracle_affine.py).
   - gated_delta_f64: matrix form S_t = g S (I - b k k^T) + b v k^T (a different
     formulation); delta-rule invariants (g = 1, b = 0 keeps S; g = 1, b = 1,
     |k| = 1 gives S k = v); T-step = T one-step calls; golden fixtures.
@@ -130,6 +136,49 @@ def dequant_w4_f64(w, scales_bits, biases_bits, K) -> np.ndarray:
     s = np.repeat(bf16_to_f32(scales_bits).astype(np.float64), 64, axis=1)
     b = np.repeat(bf16_to_f32(biases_bits).astype(np.float64), 64, axis=1)
     return s * q + b
+
+
+# ---------------------------------------------------------------- MLX affine layout, any width
+
+def pack_bits(q: np.ndarray, bits: int) -> np.ndarray:
+    """uint8 codes [N, K] -> uint32 [N, K*bits/32]: each row a little-endian bit
+    stream of `bits`-bit codes (restates quant/quantize.py:71-75)."""
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    N, K = q.shape
+    assert (K * bits) % 32 == 0
+    stream = np.unpackbits(q[..., None], axis=-1, bitorder="little")[..., :bits].reshape(N, K * bits)
+    return np.ascontiguousarray(np.packbits(stream, axis=-1, bitorder="little").view(np.uint32))
+
+
+def unpack_bits(w: np.ndarray, K: int, bits: int) -> np.ndarray:
+    """uint32 [N, K*bits/32] -> uint8 codes [N, K] (inverse of pack_bits)."""
+    w = np.ascontiguousarray(w, dtype=np.uint32)
+    N = w.shape[0]
+    stream = np.unpackbits(w.view(np.uint8), axis=-1, bitorder="little").reshape(N, K, bits)
+    pad = np.zeros((N, K, 8 - bits), np.uint8)
+    return np.packbits(np.concatenate([stream, pad], axis=-1), axis=-1, bitorder="little")[..., 0]
+
+
+def dequant_f64(w, scales_bits, biases_bits, K: int, bits: int, group_size: int) -> np.ndarray:
+    """Dense float64 [N, K] weight = s * q + b per group (mx.dequantize)."""
+    q = unpack_bits(w, K, bits).astype(np.float64)
+    s = np.repeat(bf16_to_f32(scales_bits).astype(np.float64), group_size, axis=1)
+    b = np.repeat(bf16_to_f32(biases_bits).astype(np.float64), group_size, axis=1)
+    return s * q + b
+
+
+def qmv_affine_f64(x_bits, w, scales_bits, biases_bits, bits: int, group_size: int,
+                   row_block: int = 4096) -> np.ndarray:
+    """fp64 y [M, N] = x @ dequant(W)^T for any width (mx.quantized_matmul,
+    engine/model.py:87-91), dequantizing row_block weight rows at a time."""
+    x = bf16_to_f32(np.ascontiguousarray(x_bits, dtype=np.uint16)).astype(np.float64)
+    N = w.shape[0]
+    K = x.shape[1]
+    y = np.empty((x.shape[0], N), np.float64)
+    for r0 in range(0, N, row_block):
+        r1 = min(N, r0 + row_block)
+        y[:, r0:r1] = x @ dequant_f64(w[r0:r1], scales_bits[r0:r1], biases_bits[r0:r1], K, bits, group_size).T
+    return y
 
 
 # ---------------------------------------------------------------- qmv

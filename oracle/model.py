@@ -19,7 +19,8 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import bf16_bits, bf16_to_f32, round_bf16, dequant_w4_f64, gated_delta_f64, qmv_f64
+from . import (bf16_bits, bf16_to_f32, round_bf16, dequant_f64, gated_delta_f64, qmv_affine_f64,
+               qmv_f64)
 
 
 def _np_bf16(t):
@@ -42,20 +43,32 @@ def _qweights(q):
     return w, s, b
 
 
+def _width(q):
+    return getattr(q, "bits", 4), getattr(q, "group_size", 64)
+
+
 def embed_rows(e, ids):
     """bf16(s * q + b) of the gathered rows (mx.dequantize on QEmbedding rows)."""
     w, s, b = _qweights(e)
+    bits, gs = _width(e)
     ids = np.asarray(ids, np.int64)
-    return round_bf16(dequant_w4_f64(w[ids], s[ids], b[ids], w.shape[1] * 8).astype(np.float32))
+    H = w.shape[1] * 32 // bits
+    return round_bf16(dequant_f64(w[ids], s[ids], b[ids], H, bits, gs).astype(np.float32))
 
 
 def qlinear(q, x):
     """y = bf16(x @ dequant(W)^T) (mx.quantized_matmul); x holds bf16 values.
-    The fp64 sum runs in C (one dequantized weight row at a time), so a
-    full-vocabulary lm_head needs no dense copy of the weight."""
+    4-bit group-64: the fp64 sum runs in C (one dequantized weight row at a
+    time), so a full-vocabulary lm_head needs no dense copy of the weight; other
+    widths dequantize blocks of rows in numpy."""
     w, s, b = _qweights(q)
-    x2 = np.asarray(x, np.float32).reshape(-1, w.shape[1] * 8)
-    y = qmv_f64(bf16_bits(x2), w, s, b)
+    bits, gs = _width(q)
+    K = w.shape[1] * 32 // bits
+    x2 = np.asarray(x, np.float32).reshape(-1, K)
+    if (bits, gs) == (4, 64):
+        y = qmv_f64(bf16_bits(x2), w, s, b)
+    else:
+        y = qmv_affine_f64(bf16_bits(x2), w, s, b, bits, gs)
     return round_bf16(y.astype(np.float32)).reshape(*np.shape(x)[:-1], w.shape[0])
 
 

@@ -23,6 +23,9 @@ SIGNATURES: dict[str, list] = {
     "qvex_qmv_w4g64_tiled": [P, P, P, P, P, I, I, I, I, I, P],
     "qvex_read_roof": [P, U64, P, I, P],
     "qvex_qmv_w4g64_mfma": [P, P, P, P, P, I, I, I, I, I, P],
+    "qvex_qmv_affine": [P, P, P, P, P, I, I, I, I, I, P],
+    "qvex_embed_affine": [P, I, P, P, P, I, I, I, I, P, P],
+    "qvex_affine_widen_w4g64": [P, P, P, I, I, I, I, P, P, P, P],
     "qvex_w4g64_pack": [P, P, P, I, I, P, U64, P],
     "qvex_w4g64_dequant": [P, P, P, I, I, P, P],
     "qvex_w4g64_packed_gemm": [P, P, P, I, I, I, P],
@@ -71,7 +74,7 @@ SIGNATURES: dict[str, list] = {
 
 # qvex_abi_version() of the library these bindings match (4: qvex_mtp_input,
 # qvex_embed_rms_parts, the deferred reduction of qvex_qmv_w4g64_packed_argmax)
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lib: ctypes.CDLL | None = None
 

@@ -39,13 +39,17 @@ def _check(t: torch.Tensor, name: str, dtype: torch.dtype, ndim: int | None = No
 def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
                      out: torch.Tensor | None = None, group_size: int = GROUP, bits: int = BITS,
                      tile: tuple[int, int] | None = None) -> torch.Tensor:
-    """y = x @ dequant(w)^T for MLX 4-bit group-64 weights
+    """y = x @ dequant(w)^T for MLX affine weights
     (mx.quantized_matmul(transpose=True), engine/model.py:87-91).
 
     x: bf16 [..., K] with at most 8 rows in total; w: uint32 viewed as int32
-    [N, K/8]; scales, biases: bf16 [N, K/64]. Returns bf16 [..., N]."""
-    if group_size != GROUP or bits != BITS:
-        raise _C.QvexError(f"only group_size={GROUP}, bits={BITS} is implemented")
+    [N, K*bits/32]; scales, biases: bf16 [N, K/group_size]. Returns bf16 [..., N].
+    4-bit group-64 runs qvex_qmv_w4g64 (tile optional); the other widths
+    (bits 2, 3, 5, 6, 8, groups 32 / 128) run qvex_qmv_affine."""
+    if (group_size, bits) != (GROUP, BITS):
+        if tile is not None:
+            raise _C.QvexError("explicit tiles exist for 4-bit group-64 weights only")
+        return quantized_matmul_affine(x, w, scales, biases, group_size, bits, out)
     K = x.shape[-1]
     N = w.shape[0]
     x2 = x.reshape(-1, K)
@@ -72,6 +76,75 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
         _C.call("qvex_qmv_w4g64_tiled", _ptr(x2), _ptr(w), _ptr(scales), _ptr(biases), _ptr(out),
                 M, N, K, int(tile[0]), int(tile[1]), _stream())
     return out
+
+
+def _check_affine(w, scales, biases, K: int, group_size: int, bits: int):
+    _check(w, "w", torch.int32, 2)
+    _check(scales, "scales", torch.bfloat16, 2)
+    _check(biases, "biases", torch.bfloat16, 2)
+    if group_size not in (32, 64, 128) or bits not in (2, 3, 4, 5, 6, 8):
+        raise _C.QvexError(f"unsupported quantization bits={bits} group_size={group_size} "
+                           "(bits 2, 3, 4, 5, 6, 8; groups 32, 64, 128)")
+    N = w.shape[0]
+    if K % group_size or w.shape[1] * 32 != K * bits or scales.shape != (N, K // group_size) \
+            or biases.shape != (N, K // group_size):
+        raise _C.QvexError(f"shape mismatch for {bits}-bit group-{group_size} weights of K={K}: "
+                           f"w {tuple(w.shape)} scales {tuple(scales.shape)} biases {tuple(biases.shape)}")
+
+
+def quantized_matmul_affine(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                            group_size: int, bits: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """y = x @ dequant(w)^T for any supported width (qvex_qmv_affine); x at most
+    8 rows, w int32 [N, K*bits/32], scales/biases bf16 [N, K/group_size]."""
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    M = x2.shape[0]
+    _check(x2, "x", torch.bfloat16, 2)
+    _check_affine(w, scales, biases, K, group_size, bits)
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty((*x.shape[:-1], N), dtype=torch.bfloat16, device=x.device)
+    _check(out, "out", torch.bfloat16)
+    if out.numel() != M * N:
+        raise _C.QvexError("out has the wrong size")
+    _C.call("qvex_qmv_affine", _ptr(x2), _ptr(w), _ptr(scales), _ptr(biases), _ptr(out), M, N, K, bits,
+            group_size, _stream())
+    return out
+
+
+def embed_affine(ids: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, H: int,
+                 group_size: int, bits: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16(s * q + b) of the rows ids (clamped to [0, V)) of an affine-quantized
+    table of any supported width (qvex_embed_affine)."""
+    ids1 = ids.reshape(-1).to(torch.int32).contiguous()
+    _check(ids1, "ids", torch.int32, 1)
+    _check_affine(w, scales, biases, H, group_size, bits)
+    L = ids1.numel()
+    if out is None:
+        out = torch.empty((L, H), dtype=torch.bfloat16, device=ids1.device)
+    _check(out, "out", torch.bfloat16)
+    if out.numel() != L * H:
+        raise _C.QvexError("out has the wrong size")
+    _C.call("qvex_embed_affine", _ptr(ids1), L, _ptr(w), _ptr(scales), _ptr(biases), w.shape[0], H, bits,
+            group_size, _ptr(out), _stream())
+    return out
+
+
+def widen_w4g64(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, K: int, group_size: int,
+                bits: int):
+    """The same weight in the 4-bit group-64 layout (qvex_affine_widen_w4g64):
+    bits <= 4 and group 64 or 128 re-encode losslessly. Returns (w4 int32
+    [N, K/8], scales4, biases4 bf16 [N, K/64])."""
+    _check_affine(w, scales, biases, K, group_size, bits)
+    if bits > 4 or group_size % 64:
+        raise _C.QvexError(f"{bits}-bit group-{group_size} weights do not fit the 4-bit group-64 layout")
+    N = w.shape[0]
+    w4 = torch.empty((N, K // 8), dtype=torch.int32, device=w.device)
+    s4 = torch.empty((N, K // 64), dtype=torch.bfloat16, device=w.device)
+    b4 = torch.empty_like(s4)
+    _C.call("qvex_affine_widen_w4g64", _ptr(w), _ptr(scales), _ptr(biases), N, K, bits, group_size, _ptr(w4),
+            _ptr(s4), _ptr(b4), _stream())
+    return w4, s4, b4
 
 
 def qmv_multi(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor) -> torch.Tensor:
@@ -311,13 +384,14 @@ def _argmax_src(am, am_row):
 def mtp_input(emb, ids, T: int, w_emb, hid, w_hid, eps: float, x_in: torch.Tensor, hid_sel=None, am=None,
               am_row=None, ids_out=None, counters=None, n_accept=None, extra: int = 0) -> torch.Tensor:
     """x_in [T, 2H] = [rms_norm(embed(ids)) * w_emb | rms_norm(hid[sel]) * w_hid] in one
-    launch (engine/mtp.py:61-63); emb is the QEmbedding (4-bit, group 64). With am
+    launch (engine/mtp.py:61-63); emb is a QEmbedding with a 4-bit group-64 copy. With am
     (T = 1) the token is the argmax of row am_row (device int32, None: 0) of the
     deferred pairs, also stored to ids_out; hid_sel: device row index of hid; with
     counters, *n_accept + extra is added to every counter in the same launch."""
     H = emb.H
-    if (emb.bits, emb.group_size) != (4, 64):
-        raise _C.QvexError("mtp_input needs a 4-bit group-64 embedding")
+    e4 = emb.w4g64()
+    if e4 is None:
+        raise _C.QvexError("mtp_input needs an embedding in (or widened to) the 4-bit group-64 layout")
     hid2 = hid.reshape(-1, hid.shape[-1])
     _check(hid2, "hid", torch.bfloat16, 2)
     _check(x_in, "x_in", torch.bfloat16, 2)
@@ -337,7 +411,7 @@ def mtp_input(emb, ids, T: int, w_emb, hid, w_hid, eps: float, x_in: torch.Tenso
     if counters is not None:
         _check(counters, "counters", torch.int32)
     _C.call("qvex_mtp_input", _ptr(ids) if am is None else None, T, amp, tiles, rowp,
-            _ptr(ids_out) if ids_out is not None else None, _ptr(emb.w), _ptr(emb.scales), _ptr(emb.biases),
+            _ptr(ids_out) if ids_out is not None else None, _ptr(e4[0]), _ptr(e4[1]), _ptr(e4[2]),
             emb.V, H, _ptr(w_emb), _ptr(hid2), hid2.stride(0), _ptr(hid_sel) if hid_sel is not None else None,
             _ptr(w_hid), _ptr(x_in), x_in.stride(0), float(eps),
             _ptr(counters) if counters is not None else None, counters.numel() if counters is not None else 0,
@@ -351,8 +425,9 @@ def embed_rms_parts(emb, ids: torch.Tensor, norm_w: torch.Tensor, am=None, am_ro
     rms_parts(h, norm_w)) in one launch; with am, ids[am_slot] is first set to the
     argmax of row am_row of the deferred pairs (the last draft). Returns (h, u, parts)."""
     H = emb.H
-    if (emb.bits, emb.group_size) != (4, 64):
-        raise _C.QvexError("embed_rms_parts needs a 4-bit group-64 embedding")
+    e4 = emb.w4g64()
+    if e4 is None:
+        raise _C.QvexError("embed_rms_parts needs an embedding in (or widened to) the 4-bit group-64 layout")
     _check(ids, "ids", torch.int32)
     if not ids.is_contiguous():
         raise _C.QvexError("ids must be contiguous")
@@ -362,8 +437,8 @@ def embed_rms_parts(emb, ids: torch.Tensor, norm_w: torch.Tensor, am=None, am_ro
     u_out = torch.empty((L, H), dtype=torch.bfloat16, device=dev) if u_out is None else u_out
     parts = torch.empty((L, (H + 15) // 16), dtype=torch.float32, device=dev) if parts is None else parts
     amp, tiles, rowp = _argmax_src(am, am_row)
-    _C.call("qvex_embed_rms_parts", _ptr(ids), L, amp, tiles, rowp, int(am_slot), _ptr(emb.w), _ptr(emb.scales),
-            _ptr(emb.biases), emb.V, H, _ptr(norm_w), _ptr(h_out), _ptr(u_out), _ptr(parts), _stream())
+    _C.call("qvex_embed_rms_parts", _ptr(ids), L, amp, tiles, rowp, int(am_slot), _ptr(e4[0]), _ptr(e4[1]),
+            _ptr(e4[2]), emb.V, H, _ptr(norm_w), _ptr(h_out), _ptr(u_out), _ptr(parts), _stream())
     return h_out, u_out, parts
 
 

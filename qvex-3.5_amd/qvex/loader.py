@@ -6,9 +6,9 @@ A model directory holds config.json (read by Config.from_file, which follows
 engine/model.py:39-67: `text_config` nesting, rope parameters, the
 quantization block with per-module overrides) and *.safetensors shards:
 
-* a quantized module `<name>` is `<name>.weight` uint32 [N, K/8] (eight 4-bit
-  codes per word, code j of word i at bits 4j..4j+3), `<name>.scales` and
-  `<name>.biases` bf16 [N, K/group];
+* a quantized module `<name>` is `<name>.weight` uint32 [N, K*bits/32] (each
+  row a little-endian stream of `bits`-bit codes: for 4 bits, code j of word i
+  at bits 4j..4j+3), `<name>.scales` and `<name>.biases` bf16 [N, K/group];
 * norms are bf16 [dim]; the GDN conv1d weight is bf16 [conv_dim, K, 1]
   (mx.conv1d's [out, kernel, in/groups]); A_log is read as fp32;
 * multimodal checkpoints prefix the language model's keys with
@@ -87,7 +87,10 @@ def _bf16(sh: _Shards, name: str, device) -> torch.Tensor:
 def load_model(model_dir: str | Path, device="cuda", max_context: int = 8192, max_width: int = 8) -> Qwen35:
     """The model of an MLX-format directory (engine/model.py:342-397). Raises on
     an unsanitized checkpoint that still holds MTP tensors, as the reference does,
-    and on quantization the kernels do not implement (only 4-bit group-64)."""
+    and on a quantization the kernels do not implement (bits other than 2, 3, 4,
+    5, 6, 8 or groups other than 32, 64, 128). Per-module overrides of the
+    config's quantization block (Config.qparams) apply to every linear and to
+    the embedding; fused projections must share theirs (QLinear.fuse)."""
     model_dir = Path(model_dir)
     cfg = Config.from_file(model_dir / "config.json")
     sh = _Shards(sorted(model_dir.glob("*.safetensors")))
@@ -126,8 +129,6 @@ def load_model(model_dir: str | Path, device="cuda", max_context: int = 8192, ma
 
     e = "model.embed_tokens"
     gs, bits = cfg.qparams(e)
-    if (gs, bits) != (64, 4):
-        raise _C.QvexError(f"{e}: only 4-bit group-64 embeddings are implemented (got {bits}/{gs})")
     embed = QEmbedding(sh.get(f"{e}.weight", device), _bf16(sh, f"{e}.scales", device),
                        _bf16(sh, f"{e}.biases", device), gs, bits)
     model = Qwen35(cfg, embed, layers, _bf16(sh, "model.norm.weight", device), qlin("lm_head"),

@@ -115,10 +115,33 @@ class Config:
 
 # ---------------------------------------------------------------- building blocks
 
+WIDTHS = (2, 3, 4, 5, 6, 8)      # bits of the MLX affine layouts the kernels read
+GROUPS = (32, 64, 128)
+
+
+def widens_to_w4g64(bits: int, group_size: int) -> bool:
+    """A weight of this width re-encodes losslessly as 4-bit group-64 (codes
+    fit a nibble; a 128-code group's scale and bias serve both 64-code halves)."""
+    return bits <= 4 and group_size % 64 == 0
+
+
+def _check_quant(what: str, bits: int, group_size: int):
+    if bits not in WIDTHS or group_size not in GROUPS:
+        raise _C.QvexError(f"{what}: {bits}-bit group-{group_size} quantization is not supported "
+                           f"(bits {WIDTHS}, groups {GROUPS})")
+
+
 class QLinear:
     """Affine-quantized linear layer, y = x @ dequant(W)^T (engine/model.py:80-104).
 
-    w: int32 [N, K/8] (uint32 words), scales, biases: bf16 [N, K/64]. When K is
+    w: int32 [N, K*bits/32] (uint32 words of each row's little-endian code
+    stream), scales, biases: bf16 [N, K/group_size]; bits 2, 3, 4, 5, 6, 8 and
+    groups 32, 64, 128 (Config.qparams overrides). A width that re-encodes
+    losslessly as 4-bit group-64 (bits <= 4, group 64 or 128: every 3-bit layer
+    of a mixed 4/3-bit model) is widened once, at construction, and then takes
+    every path below exactly as a 4-bit layer does; the other widths run the
+    any-width VALU product (qvex_qmv_affine) in chunks of 8 rows, without the
+    fused epilogues. For the 4-bit group-64 layout: when K is
     a multiple of 256 the layer also keeps the tile-packed copy (pack_w4), built
     once here, and runs every call of 1..8 rows - decode, MTP drafts, verify of
     up to 7 drafts - through the MFMA kernel on it (5..8 rows as two halves over
@@ -133,24 +156,31 @@ class QLinear:
     DENSE_MIN_ROWS = 16
 
     def __init__(self, w, scales, biases, group_size=64, bits=4, pack: bool = True, swiglu: bool = False):
-        if group_size != 64 or bits != 4:
-            raise _C.QvexError(f"QLinear: only 4-bit group-64 weights are implemented (got {bits}/{group_size})")
+        _check_quant("QLinear", bits, group_size)
         self.w, self.scales, self.biases = w, scales, biases
         self.group_size, self.bits = group_size, bits
         self.N = w.shape[0]
-        self.K = w.shape[1] * 8
+        self.K = w.shape[1] * 32 // bits
+        if w.shape[1] * 32 != self.K * bits or self.K % group_size:
+            raise _C.QvexError(f"QLinear: w {tuple(w.shape)} is not a {bits}-bit row of whole {group_size}-code groups")
         # swiglu: a fused [gate; up] weight whose packed copy carries the gate/up
         # interleave; its 1..8-row calls go through swiglu() (SwiGLU fused in)
         self.swiglu_packed = swiglu and self.N % 16 == 0
         self.packed = None
-        if pack and self.K % 256 == 0:
-            self.packed = kernels.pack_w4(w, scales, biases, swiglu=self.swiglu_packed)
+        if pack and self.K % 256 == 0 and widens_to_w4g64(bits, group_size):
+            self.packed = kernels.pack_w4(*self._w4g64(w, scales, biases), swiglu=self.swiglu_packed)
+
+    def _w4g64(self, w, s, b):
+        """The triplet in the 4-bit group-64 layout (widened when stored narrower)."""
+        if (self.bits, self.group_size) == (4, 64):
+            return w, s, b
+        return kernels.widen_w4g64(w, s, b, self.K, self.group_size, self.bits)
 
     def repack(self) -> None:
         """Rebuild the packed copy after the MLX-layout tensors were edited in place."""
         if self.packed is not None:
             w, s, b = self._mlx_on(self.packed.device)
-            self.packed = kernels.pack_w4(w, s, b, swiglu=self.swiglu_packed)
+            self.packed = kernels.pack_w4(*self._w4g64(w, s, b), swiglu=self.swiglu_packed)
 
     def offload_mlx(self) -> None:
         """Keep the MLX-layout triplet in host memory once the packed copy exists:
@@ -228,7 +258,8 @@ class QLinear:
         w, sc, bi = self._mlx_on(x.device)
         for m0 in range(0, M, QMV_MAX_ROWS):
             m1 = min(M, m0 + QMV_MAX_ROWS)
-            kernels.quantized_matmul(x2[m0:m1], w, sc, bi, out=o2[m0:m1])
+            kernels.quantized_matmul(x2[m0:m1], w, sc, bi, out=o2[m0:m1], group_size=self.group_size,
+                                     bits=self.bits)
         return out.view(*lead, self.N)
 
     def argmax(self, x, out: torch.Tensor | None) -> torch.Tensor:
@@ -282,20 +313,44 @@ class QLinear:
 
 
 class QEmbedding:
-    """Quantized embedding rows, dequantized on gather (engine/model.py:121-130)."""
+    """Quantized embedding rows, dequantized on gather (engine/model.py:121-130).
+
+    Any width of QLinear's layouts. A table that widens losslessly to 4-bit
+    group-64 (bits <= 4, group 64 or 128) keeps only the widened copy on the
+    device (the stored triplet moves to host memory), so the fused decode-cycle
+    inputs (qvex_mtp_input, qvex_embed_rms_parts) read it as they read a 4-bit
+    table; the other widths gather with qvex_embed_affine."""
 
     def __init__(self, w, scales, biases, group_size=64, bits=4):
+        _check_quant("QEmbedding", bits, group_size)
         self.w, self.scales, self.biases = w, scales, biases
         self.group_size, self.bits = group_size, bits
-        self.V, self.H = w.shape[0], w.shape[1] * 8
+        self.V, self.H = w.shape[0], w.shape[1] * 32 // bits
+        if w.shape[1] * 32 != self.H * bits or self.H % group_size:
+            raise _C.QvexError(f"QEmbedding: w {tuple(w.shape)} is not a {bits}-bit row of whole "
+                               f"{group_size}-code groups")
+        self._w4 = None
+        if (bits, group_size) == (4, 64):
+            self._w4 = (w, scales, biases)
+        elif widens_to_w4g64(bits, group_size) and w.is_cuda:
+            self._w4 = kernels.widen_w4g64(w, scales, biases, self.H, group_size, bits)
+            self.w, self.scales, self.biases = w.cpu(), scales.cpu(), biases.cpu()
+
+    def w4g64(self):
+        """(w, scales, biases) in the 4-bit group-64 layout on the device, or None."""
+        return self._w4
 
     def __call__(self, ids: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         ids1 = ids.reshape(-1).to(torch.int32).contiguous()
         L = ids1.numel()
         if out is None:
             out = torch.empty((L, self.H), dtype=torch.bfloat16, device=ids.device)
-        _C.call("qvex_embed_w4g64", _ptr(ids1), L, _ptr(self.w), _ptr(self.scales), _ptr(self.biases),
-                self.V, self.H, _ptr(out), _stream())
+        if self._w4 is None:
+            return kernels.embed_affine(ids1, self.w, self.scales, self.biases, self.H, self.group_size, self.bits,
+                                        out=out)
+        w, sc, bi = self._w4
+        _C.call("qvex_embed_w4g64", _ptr(ids1), L, _ptr(w), _ptr(sc), _ptr(bi), self.V, self.H, _ptr(out),
+                _stream())
         return out
 
 
@@ -816,9 +871,19 @@ class Qwen35:
         for q in self.qlinears():
             q.offload_mlx()
 
+    def all_packed(self) -> bool:
+        """Every product has the packed copy (4-bit group-64, or widened to it):
+        the condition for folding the norms into the products' epilogues; a
+        model with any other width runs the separate norm kernels."""
+        return all(q.packed is not None for q in self.qlinears())
+
+    def _deferred_argmax(self) -> bool:
+        """The decode cycle may leave each draft's argmax to the next launch."""
+        return self.fuse_norms and self.all_packed() and self._fused_inputs()
+
     def _fused_inputs(self) -> bool:
         e = self.embed
-        return isinstance(e, QEmbedding) and (e.bits, e.group_size) == (4, 64) and e.H % 64 == 0 and e.H <= 8192
+        return isinstance(e, QEmbedding) and e.w4g64() is not None and e.H % 64 == 0 and e.H <= 8192
 
     def __call__(self, ids, cache, last_only=True, return_hidden=False, keep_prev=False, hidden_out=None,
                  in_argmax=None):
@@ -848,7 +913,8 @@ class Qwen35:
             return (logits, torch.cat(hs, dim=1)) if return_hidden else logits
         counters.sync()
         eps = self.cfg.rms_norm_eps
-        fused = self.fuse_norms and L <= QLinear.PACKED_MAX_ROWS and NormedRows.supported(self.cfg.hidden_size)
+        fused = (self.fuse_norms and L <= QLinear.PACKED_MAX_ROWS and NormedRows.supported(self.cfg.hidden_size)
+                 and self.all_packed())
         if in_argmax is not None and not (fused and self._fused_inputs()):
             raise _C.QvexError("in_argmax needs the fused decode path (1..8 rows, 4-bit group-64 embedding)")
         if fused and self._fused_inputs():
@@ -891,21 +957,29 @@ class Qwen35:
 
 # ---------------------------------------------------------------- random init in the MLX layout
 
-def _rand_qlinear(N, K, gen, scale, device, pack: bool = True) -> QLinear:
-    """Random 4-bit group-64 weights: codes uniform on 0..15, scales ~ U(0.5, 1.5) * scale,
-    biases = -8 * scale (zero-mean dequantized weights)."""
-    w = torch.randint(-2**31, 2**31, (N, K // 8), generator=gen, device=device, dtype=torch.int64)
+def _rand_qlinear(N, K, gen, scale, device, pack: bool = True, group_size: int = 64, bits: int = 4) -> QLinear:
+    """Random affine weights: codes uniform on 0..2^bits-1 (uniform random stream
+    words), scales ~ U(0.5, 1.5) * scale, biases = -2^(bits-1) * scale (zero-mean
+    dequantized weights). `scale` is given for 4 bits (code variance 21.25);
+    other widths rescale it so the dequantized variance is the same."""
+    _check_quant("random weights", bits, group_size)
+    w = torch.randint(-2**31, 2**31, (N, K * bits // 32), generator=gen, device=device, dtype=torch.int64)
     w = w.to(torch.int32)
-    s = (torch.rand((N, K // 64), generator=gen, device=device) + 0.5) * scale
+    if bits != 4:
+        scale = scale * math.sqrt(21.25 / ((4 ** bits - 1) / 12))
+    s = (torch.rand((N, K // group_size), generator=gen, device=device) + 0.5) * scale
     s = s.to(torch.bfloat16)
-    b = (-8.0 * s.float()).to(torch.bfloat16)
-    return QLinear(w, s, b, pack=pack)
+    b = (-float(2 ** (bits - 1)) * s.float()).to(torch.bfloat16)
+    return QLinear(w, s, b, group_size, bits, pack=pack)
 
 
 def random_model(cfg: Config, seed: int = 1004, device="cuda", max_context: int = 8192,
                  max_width: int = 8, lm_head_scale: float = 2.0, keep_mlx: bool = False) -> Qwen35:
     """Random-init model of the given shape with weights generated directly in the
-    MLX 4-bit layout on the device (no checkpoint). Linear scales are chosen so a
+    MLX affine layout on the device (no checkpoint): 4-bit group-64 unless the
+    config's quantization overrides (Config.qparams) name another width for a
+    module (model.layers.{i}.mlp.gate_proj, ..., model.embed_tokens, lm_head).
+    Linear scales are chosen so a
     unit-RMS input gives a unit-RMS output (dequantized w has variance 21.25 s^2).
     Unless keep_mlx, each packed layer's MLX-layout triplet then moves to host
     memory (QLinear.offload_mlx)."""
@@ -913,24 +987,31 @@ def random_model(cfg: Config, seed: int = 1004, device="cuda", max_context: int 
     gen.manual_seed(seed)
     H, I = cfg.hidden_size, cfg.intermediate_size
 
-    def lin(N, K, gain=1.0):
-        return _rand_qlinear(N, K, gen, gain / math.sqrt(21.25 * K), device)
+    def lin(N, K, gain=1.0, name=""):
+        gs, bits = cfg.qparams(name)
+        return _rand_qlinear(N, K, gen, gain / math.sqrt(21.25 * K), device, group_size=gs, bits=bits)
 
     def ones(n):
         return (1.0 + 0.1 * torch.randn(n, generator=gen, device=device)).to(torch.bfloat16)
 
     layers = []
     for i in range(cfg.num_hidden_layers):
+        pre = f"model.layers.{i}"
+        mlp = f"{pre}.mlp"
         p = {"input_layernorm": ones(H), "post_attention_layernorm": ones(H),
-             "mlp": {"gate_proj": lin(I, H), "up_proj": lin(I, H), "down_proj": lin(H, I, 0.5)}}
+             "mlp": {"gate_proj": lin(I, H, name=f"{mlp}.gate_proj"), "up_proj": lin(I, H, name=f"{mlp}.up_proj"),
+                     "down_proj": lin(H, I, 0.5, f"{mlp}.down_proj")}}
         if cfg.is_linear(i):
             kd = cfg.linear_num_key_heads * cfg.linear_key_head_dim
             vd = cfg.linear_num_value_heads * cfg.linear_value_head_dim
             conv_dim = 2 * kd + vd
             hv = cfg.linear_num_value_heads
+            la = f"{pre}.linear_attn"
             p["linear_attn"] = {
-                "in_proj_qkv": lin(conv_dim, H), "in_proj_z": lin(vd, H),
-                "in_proj_b": lin(hv, H), "in_proj_a": lin(hv, H), "out_proj": lin(H, vd, 0.5),
+                "in_proj_qkv": lin(conv_dim, H, name=f"{la}.in_proj_qkv"),
+                "in_proj_z": lin(vd, H, name=f"{la}.in_proj_z"),
+                "in_proj_b": lin(hv, H, name=f"{la}.in_proj_b"), "in_proj_a": lin(hv, H, name=f"{la}.in_proj_a"),
+                "out_proj": lin(H, vd, 0.5, f"{la}.out_proj"),
                 "conv1d": (0.5 * torch.randn((conv_dim, cfg.linear_conv_kernel_dim), generator=gen,
                                              device=device)).to(torch.bfloat16),
                 "A_log": (0.5 * torch.randn(hv, generator=gen, device=device)).float(),
@@ -939,14 +1020,18 @@ def random_model(cfg: Config, seed: int = 1004, device="cuda", max_context: int 
             }
         else:
             D, Hq, Hkv = cfg.head_dim, cfg.num_attention_heads, cfg.num_key_value_heads
-            p["self_attn"] = {"q_proj": lin(Hq * 2 * D, H), "k_proj": lin(Hkv * D, H),
-                              "v_proj": lin(Hkv * D, H), "o_proj": lin(H, Hq * D, 0.5),
+            sa = f"{pre}.self_attn"
+            p["self_attn"] = {"q_proj": lin(Hq * 2 * D, H, name=f"{sa}.q_proj"),
+                              "k_proj": lin(Hkv * D, H, name=f"{sa}.k_proj"),
+                              "v_proj": lin(Hkv * D, H, name=f"{sa}.v_proj"),
+                              "o_proj": lin(H, Hq * D, 0.5, f"{sa}.o_proj"),
                               "q_norm": ones(D), "k_norm": ones(D)}
         layers.append(Layer(cfg, i, p))
     V = cfg.vocab_size
-    e = _rand_qlinear(V, H, gen, 1.0 / math.sqrt(21.25), device, pack=False)
-    embed = QEmbedding(e.w, e.scales, e.biases)
-    lm_head = lin(V, H, lm_head_scale)
+    egs, ebits = cfg.qparams("model.embed_tokens")
+    e = _rand_qlinear(V, H, gen, 1.0 / math.sqrt(21.25), device, pack=False, group_size=egs, bits=ebits)
+    embed = QEmbedding(e.w, e.scales, e.biases, egs, ebits)
+    lm_head = lin(V, H, lm_head_scale, "lm_head")
     model = Qwen35(cfg, embed, layers, ones(H), lm_head, max_context=max_context, max_width=max_width)
     if not keep_mlx:
         model.offload_mlx()

@@ -49,6 +49,11 @@ class MTPHead:
         m = self.layer.mixer
         return [self.fc, m.qkv_proj, m.o_proj, self.layer.mlp.gate_up, self.layer.mlp.down]
 
+    def all_packed(self) -> bool:
+        """The head's products and the shared lm_head all have packed copies
+        (the norms then ride on their epilogues, as in Qwen35.all_packed)."""
+        return self.model.lm_head.packed is not None and all(q.packed is not None for q in self.qlinears())
+
     def offload_mlx(self) -> None:
         """QLinear.offload_mlx for the head's own layers (the lm_head is the model's)."""
         for q in self.qlinears():
@@ -107,7 +112,8 @@ class MTPHead:
             _C.call("qvex_rmsnorm_pair", _ptr(e), e.stride(0), _ptr(self.norm_emb), _ptr(x_in), _ptr(h), h.stride(0),
                     _ptr(self.norm_hid), _ptr(x_in) + 2 * H, x_in.stride(0), T, H, float(self.eps), _stream())
         V = self.model.cfg.vocab_size
-        if self.model.fuse_norms and T <= QLinear.PACKED_MAX_ROWS and NormedRows.supported(H):
+        if (self.model.fuse_norms and T <= QLinear.PACKED_MAX_ROWS and NormedRows.supported(H)
+                and self.all_packed()):
             # the block's residual norms ride on its products (Layer.fused); the
             # first one on the fc product, as a residual add onto zero
             if self.fc_epilogue:
@@ -162,9 +168,11 @@ class MTPHead:
         return (logits, out.view(1, T, H)) if return_hidden else logits
 
 
-def random_mtp(model: Qwen35, seed: int = 2004, keep_mlx: bool = False) -> MTPHead:
+def random_mtp(model: Qwen35, seed: int = 2004, keep_mlx: bool = False, group_size: int = 64,
+               bits: int = 4) -> MTPHead:
     """Random-init MTP head (fc 2H -> H plus one full-attention layer) in the MLX
-    4-bit layout (the MLX triplets moved to host memory unless keep_mlx)."""
+    affine layout of the given width (the head file's one group_size / bits;
+    the MLX triplets moved to host memory unless keep_mlx)."""
     cfg = model.cfg
     dev = model.norm.device
     gen = torch.Generator(device=dev)
@@ -173,7 +181,7 @@ def random_mtp(model: Qwen35, seed: int = 2004, keep_mlx: bool = False) -> MTPHe
     Hq, Hkv = cfg.num_attention_heads, cfg.num_key_value_heads
 
     def lin(N, K, gain=1.0):
-        return _rand_qlinear(N, K, gen, gain / math.sqrt(21.25 * K), dev)
+        return _rand_qlinear(N, K, gen, gain / math.sqrt(21.25 * K), dev, group_size=group_size, bits=bits)
 
     def ones(n):
         return (1.0 + 0.1 * torch.randn(n, generator=gen, device=dev)).to(torch.bfloat16)
@@ -183,7 +191,7 @@ def random_mtp(model: Qwen35, seed: int = 2004, keep_mlx: bool = False) -> MTPHe
          "attn": {"q_proj": lin(Hq * 2 * D, H), "k_proj": lin(Hkv * D, H), "v_proj": lin(Hkv * D, H),
                   "o_proj": lin(H, Hq * D, 0.5), "q_norm": ones(D), "k_norm": ones(D)},
          "mlp": {"gate_proj": lin(I, H), "up_proj": lin(I, H), "down_proj": lin(H, I, 0.5)}}
-    head = MTPHead(model, w)
+    head = MTPHead(model, w, group_size, bits)
     if not keep_mlx:
         head.offload_mlx()
     return head

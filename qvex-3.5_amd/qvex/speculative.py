@@ -255,7 +255,7 @@ class GraphedMTPCycle:
     def _body(self, out):
         d = self.dec
         k, mtp, mc = self.k, d.mtp, d.mtp_cache
-        if d.model._fused_inputs():
+        if d.model._deferred_argmax() and mtp.all_packed():
             # Each draft's argmax is reduced inside the next launch (the next
             # step's input, or the verify's embedding), which also stores it into
             # the verify ids; a step's counter advance rides on the next step's
