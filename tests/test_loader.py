@@ -116,11 +116,46 @@ def test_loaded_mtp_matches_in_memory(tiny_pair):
 
 
 @pytest.mark.gpu
-def test_load_rejects_unimplemented_quantization(tmp_path):
+@pytest.mark.parametrize("override,match", [({"bits": 7}, "7-bit group-64"),
+                                            ({"group_size": 16}, "4-bit group-16"),
+                                            ({"bits": 3}, "not a 3-bit row")])
+def test_load_rejects_unimplemented_quantization(tmp_path, override, match):
+    """Widths outside bits 2-8 / groups 32-128, and tensors whose shape does not
+    fit the declared width, raise at load."""
     from qvex import _C
     from qvex.model import random_model
     from mlx_ckpt import export_model
     m = random_model(Config.tiny(layers=4, vocab=1024), seed=33, device=DEV, max_context=256)
-    export_model(m, tmp_path, shards=1, overrides={"language_model.model.layers.1.mlp.down_proj": {"bits": 8}})
-    with pytest.raises(_C.QvexError, match="4-bit group-64"):
+    export_model(m, tmp_path, shards=1, overrides={"language_model.model.layers.1.mlp.down_proj": override})
+    with pytest.raises(_C.QvexError, match=match):
         load_model(tmp_path, device=DEV)
+
+
+@pytest.mark.gpu
+def test_mixed_width_checkpoint_round_trip(tmp_path):
+    """A mixed-width model (per-module overrides, engine/model.py:68-71; the
+    reference quantizer's 4/3-bit mix plus 5/6/8-bit modules) written with its
+    config's overrides and loaded back computes the same logits bit for bit."""
+    from qvex.model import random_model
+    from mlx_ckpt import export_model
+    quant = {"model.layers.0.mlp.down_proj": {"bits": 3},
+             **{f"model.layers.1.linear_attn.{n}": {"bits": 3, "group_size": 128}
+                for n in ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a")},
+             "model.layers.2.linear_attn.out_proj": {"bits": 6, "group_size": 32},
+             "lm_head": {"bits": 8}, "model.embed_tokens": {"bits": 3}}
+    cfg = Config.tiny(layers=4, vocab=2048)
+    cfg.quant = dict(quant)
+    m = random_model(cfg, seed=34, device=DEV, max_context=256)
+    export_model(m, tmp_path, shards=2, overrides={"language_model." + k: v for k, v in quant.items()})
+    lm = load_model(tmp_path, device=DEV, max_context=256)
+    assert lm.cfg.quant == quant
+    assert (lm.layers[1].mixer.in_proj.bits, lm.layers[1].mixer.in_proj.group_size) == (3, 128)
+    assert (lm.lm_head.bits, lm.embed.bits, lm.layers[2].mixer.out_proj.bits) == (8, 3, 6)
+    ids = torch.from_numpy(np.random.default_rng(5).integers(0, 2048, 24).astype(np.int32)).reshape(1, -1).to(DEV)
+    outs = []
+    for model in (m, lm):
+        c = model.make_cache()
+        outs.append((model(ids, c, last_only=False).float(), model(ids[:, :3], c, last_only=False).float()))
+    torch.cuda.synchronize()
+    for x, y in zip(*outs):
+        assert torch.equal(x, y)
