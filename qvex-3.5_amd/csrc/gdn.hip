@@ -22,14 +22,6 @@ constexpr int DK = 128;
 constexpr int ROWS_PER_BLOCK = 16;
 constexpr int TMAX_PREFETCH = 8;
 
-__device__ __forceinline__ void load8_bf16(const uint16_t* p, float* o) {
-  const u32x4 v = load16(p);
-  o[0] = bf16_lo(v.x); o[1] = bf16_hi(v.x);
-  o[2] = bf16_lo(v.y); o[3] = bf16_hi(v.y);
-  o[4] = bf16_lo(v.z); o[5] = bf16_hi(v.z);
-  o[6] = bf16_lo(v.w); o[7] = bf16_hi(v.w);
-}
-
 struct GdnArgs {
   const uint16_t* q;
   const uint16_t* k;
@@ -75,45 +67,69 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(GdnArgs p) {
     st[4] = __uint_as_float(s1.x); st[5] = __uint_as_float(s1.y);
     st[6] = __uint_as_float(s1.z); st[7] = __uint_as_float(s1.w);
   }
-  const float A = expf(p.A_log[hv]);
-  const float dt = bf16_to_f32(p.dt_bias[hv]);
-
-  for (int t0 = 0; t0 < T; t0 += TMAX_PREFETCH) {
+  // the gate inputs as raw values, converted after the first block's token
+  // loads are out (converting here would wait for them first)
+  float a_log = p.A_log[hv];
+  uint32_t dt_raw = p.dt_bias[hv];
+  // one block of up to TMAX_PREFETCH tokens; the first is peeled out of the
+  // loop so that its loads are not held behind a loop-carried wait
+  auto block = [&](const int t0) {
     const int tn = min(TMAX_PREFETCH, T - t0);
-    float kk[TMAX_PREFETCH][8], qq[TMAX_PREFETCH][8], vv[TMAX_PREFETCH], aa[TMAX_PREFETCH], bb[TMAX_PREFETCH];
+    // every token's inputs requested at once, as raw words (tokens past tn
+    // re-read token t0 + tn - 1, never used): converting inside a per-token
+    // branch would wait for each token's loads before issuing the next's
+    u32x4 kr[TMAX_PREFETCH], qr[TMAX_PREFETCH];
+    uint16_t vr[TMAX_PREFETCH];
 #pragma unroll
     for (int j = 0; j < TMAX_PREFETCH; ++j) {
-      if (j < tn) {
-        const int t = t0 + j;
-        const long qk = (((long)bi * T + t) * p.Hk + hk) * DK + l16 * 8;
-        load8_bf16(p.k + qk, kk[j]);
-        load8_bf16(p.q + qk, qq[j]);
-        vv[j] = bf16_to_f32(p.v[(((long)bi * T + t) * p.Hv + hv) * p.Dv + dv]);
-        aa[j] = bf16_to_f32(p.a[((long)bi * T + t) * p.Hv + hv]);
-        bb[j] = bf16_to_f32(p.b[((long)bi * T + t) * p.Hv + hv]);
-      }
+      const int t = t0 + min(j, tn - 1);
+      const long qk = (((long)bi * T + t) * p.Hk + hk) * DK + l16 * 8;
+      kr[j] = load16(p.k + qk);
+      qr[j] = load16(p.q + qk);
+      vr[j] = p.v[(((long)bi * T + t) * p.Hv + hv) * p.Dv + dv];
     }
+    // the decay and beta of token t0 + l in lane l, all tokens at once (the
+    // same value in every row of the head), each token's read back with a
+    // readlane in the chain: one gate latency per block instead of one per token
+    const int tl = t0 + min(threadIdx.x & 63, tn - 1);
+    uint32_t a_raw = p.a[((long)bi * T + tl) * p.Hv + hv];
+    uint32_t b_raw = p.b[((long)bi * T + tl) * p.Hv + hv];
+    asm volatile("" : "+v"(a_log), "+v"(dt_raw));
+    const float A = expf(a_log);
+    const float dt = bf16_to_f32((uint16_t)dt_raw);
+    const float xl = bf16_to_f32((uint16_t)a_raw) + dt;
+    const float spl = xl > 20.0f ? xl : log1pf(expf(xl));
+    const float g_l = expf(-A * spl);
+    const float beta_l = 1.0f / (1.0f + expf(-bf16_to_f32((uint16_t)b_raw)));
 #pragma unroll
     for (int j = 0; j < TMAX_PREFETCH; ++j) {
       if (j < tn) {
         const int t = t0 + j;
-        const float x = aa[j] + dt;
-        const float sp = x > 20.0f ? x : log1pf(expf(x));
-        const float g = expf(-A * sp);
-        const float beta = 1.0f / (1.0f + expf(-bb[j]));
+        float kk[8], qq[8];
+        const uint32_t kw[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
+        const uint32_t qw[4] = {qr[j].x, qr[j].y, qr[j].z, qr[j].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          kk[2 * i] = bf16_lo(kw[i]);
+          kk[2 * i + 1] = bf16_hi(kw[i]);
+          qq[2 * i] = bf16_lo(qw[i]);
+          qq[2 * i + 1] = bf16_hi(qw[i]);
+        }
+        const float g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g_l), j));
+        const float beta = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(beta_l), j));
         float kv = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           st[i] *= g;
-          kv = fmaf(st[i], kk[j][i], kv);
+          kv = fmaf(st[i], kk[i], kv);
         }
         kv = row16_allsum(kv);
-        const float delta = (vv[j] - kv) * beta;
+        const float delta = (bf16_to_f32(vr[j]) - kv) * beta;
         float o = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          st[i] = fmaf(kk[j][i], delta, st[i]);
-          o = fmaf(st[i], qq[j][i], o);
+          st[i] = fmaf(kk[i], delta, st[i]);
+          o = fmaf(st[i], qq[i], o);
         }
         o = row16_allsum(o);
         if (l16 == 0) p.y[(((long)bi * T + t) * p.Hv + hv) * p.Dv + dv] = f32_to_bf16(o);
@@ -133,12 +149,16 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(GdnArgs p) {
           o0.z = __float_as_uint(st[2]); o0.w = __float_as_uint(st[3]);
           o1.x = __float_as_uint(st[4]); o1.y = __float_as_uint(st[5]);
           o1.z = __float_as_uint(st[6]); o1.w = __float_as_uint(st[7]);
-          *reinterpret_cast<u32x4*>(dst) = o0;
-          *reinterpret_cast<u32x4*>(dst + 4) = o1;
+          // nontemporal: the snapshots are read back by a later call at most
+          // once, and dirty lines left in L2 slow the next kernels' reads
+          __builtin_nontemporal_store(o0, reinterpret_cast<u32x4*>(dst));
+          __builtin_nontemporal_store(o1, reinterpret_cast<u32x4*>(dst + 4));
         }
       }
     }
-  }
+  };
+  block(0);
+  for (int t0 = TMAX_PREFETCH; t0 < T; t0 += TMAX_PREFETCH) block(t0);
 }
 
 // ---------------------------------------------------------------- fused decode layer
