@@ -67,11 +67,32 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v) {
   return v;
 }
 
-// Sum broadcast to every lane, via xor butterflies (ds_swizzle / bpermute).
-__device__ __forceinline__ float wave_allsum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+// Sum over the 16 lanes of a DPP row in every lane of it (quad swaps, then row
+// rotations by 4 and 8). The lanes pair the four quad sums differently, so they
+// can differ in the last bit: where that matters, one lane's value is used.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_allsum(float v) {
+  v += dpp_row<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_row<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_row<0x124>(v);  // row_ror 4
+  v += dpp_row<0x128>(v);  // row_ror 8
   return v;
+}
+
+// Sum over the wave broadcast to every lane (all 64 lanes active): each DPP
+// row's sum, then the four row sums read into scalars and added as
+// (r0 + r1) + (r2 + r3). Four DPP steps and four readlanes instead of six
+// dependent LDS-permute round trips of an xor butterfly.
+__device__ __forceinline__ float wave_allsum(float v) {
+  v = row16_allsum(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
 }
 
 // DPP move whose disabled or out-of-range lanes keep their own value.
@@ -95,20 +116,6 @@ __device__ __forceinline__ float wave_allmax(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_row(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-
-// Sum over the 16 lanes of a DPP row (quad swaps, then row rotations by 4 and
-// 8), the same bits in all 16 lanes.
-__device__ __forceinline__ float row16_allsum(float v) {
-  v += dpp_row<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_row<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_row<0x124>(v);  // row_ror 4
-  v += dpp_row<0x128>(v);  // row_ror 8
-  return v;
-}
 
 // ---------------------------------------------------------------- host-side error plumbing
 
