@@ -22,7 +22,8 @@ Every line also carries:
     56,754,176 per launch;
   qmv_config0: the same for the single 4-bit GEMV of 12288 x 4096 (M=1,
     28,344,320 bytes per launch);
-  qmv_shapes: the decode cycle's other matmul shapes;
+  qmv_shapes: the decode cycle's other matmul shapes, and the config-0 GEMV on
+    the packed copy QLinear runs it on;
   cpu_baseline: the oracle's C restatement (OpenMP) of the cycle's quantized
     matmuls, timed on this host on one cycle's worth of shapes and scaled to
     tokens per second with the GPU run's tokens per cycle;
@@ -204,14 +205,16 @@ def roofline(name):
 
 def qmv_shapes():
     """Config-1 shapes as the decode cycle runs them: the packed MFMA kernel for
-    1..4 rows (M=4 verify, M=1 draft / plain decode), and in chunks of 4 rows for
-    M=5 (a verify of 4 drafts: two launches, 4 + 1 rows)."""
+    1..4 rows (M=4 verify, M=1 draft / plain decode), and for M=5 (a verify of 4
+    drafts) as two row halves over one read of the weights; config0_packed_m1 is
+    the config-0 GEMV on the copy QLinear packs once at load (what a decode step
+    runs for that weight; qmv_config0 times the MLX-layout kernel)."""
     out = {}
     shapes = {"lm_head_m1": (1, 248320, 4096), "lm_head_m4": (4, 248320, 4096),
               "gate_up_swiglu_m4": (4, 24576, 4096), "down_m4": (4, 4096, 12288),
               "gdn_in_proj_m4": (4, 12352, 4096), "attn_qkv_m4": (4, 10240, 4096),
               "o_proj_m4": (4, 4096, 4096), "mtp_fc_m1": (1, 4096, 8192),
-              "gate_up_swiglu_m5": (5, 24576, 4096)}
+              "gate_up_swiglu_m5": (5, 24576, 4096), "config0_packed_m1": (1, 12288, 4096)}
     for name, (M, N, K) in shapes.items():
         us, algo = qmv_time(M, N, K, packed=True, swiglu="swiglu" in name)
         ceil = read_ceiling_us(int(0.5625 * N * K))
