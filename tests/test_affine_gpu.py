@@ -229,13 +229,20 @@ def test_mixed_model_greedy_spec_equals_plain(mix):
 
 
 @pytest.mark.gpu
-def test_mixed_model_graphed_cycle_equals_eager():
+@pytest.mark.parametrize("mix", ["widening", "non_widening"])
+def test_mixed_model_graphed_cycle_equals_eager(mix):
     """The widening mix keeps the deferred-argmax decode cycle (every product
-    packed, 3-bit embedding widened): graphed and eager cycles agree."""
+    packed, 3-bit embedding widened), the non-widening mix the cycle with the
+    separate norm kernels: graphed and eager cycles agree in both."""
     from qvex.speculative import GraphedMTPCycle
-    m = mixed_model(WIDENING, seed=31)
-    mtp = random_mtp(m, seed=37, bits=3)
-    assert m._deferred_argmax() and mtp.all_packed()
+    if mix == "widening":
+        m = mixed_model(WIDENING, seed=31)
+        mtp = random_mtp(m, seed=37, bits=3)
+        assert m._deferred_argmax() and mtp.all_packed()
+    else:
+        m = mixed_model(NON_WIDENING, seed=31)
+        mtp = random_mtp(m, seed=37, bits=6, group_size=32)
+        assert not m._deferred_argmax() and not mtp.all_packed()
     eager = start_decoder(m, mtp, 3, 0.0)
     graphed = GraphedMTPCycle(start_decoder(m, mtp, 3, 0.0))
     te, tg = [], []
