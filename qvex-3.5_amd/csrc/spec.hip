@@ -204,7 +204,7 @@ __device__ __forceinline__ float pen_x(const float* seen, float pen, float x, in
 // A thread's next NB values in (value descending, slot ascending) order after
 // (lv, li), into bv/bi (descending): strictly greater values move ahead, so an
 // earlier slot wins a tie. Empty entries are (-inf, NS).
-constexpr int TOPK_BUF = 4;
+constexpr int TOPK_BUF = 8;
 template <int NS>
 __device__ __forceinline__ void next_buf(const float (&v)[NS], float lv, int li, float (&bv)[TOPK_BUF],
                                          int (&bi)[TOPK_BUF]) {
