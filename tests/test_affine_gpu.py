@@ -151,6 +151,22 @@ def test_qlinear_any_width(bits, gs, M):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("bits,gs", [(3, 64), (4, 64), (5, 32)])
+@pytest.mark.parametrize("M", [1, 12])
+def test_qlinear_unpackable_k(bits, gs, M):
+    """K not a multiple of 256 (no packed copy): every width, 4-bit included,
+    runs its MLX-layout product in chunks of 8 rows."""
+    N, K = 200, 320
+    w, s, b, _ = weights(N, K, bits, gs, seed=5 * bits + M)
+    lin = QLinear(to_dev(w, torch.int32), to_dev(s, torch.bfloat16), to_dev(b, torch.bfloat16), gs, bits)
+    assert lin.packed is None
+    x = synth.qmv_x(M, K, seed=17, tag=M)
+    y = lin(to_dev(x, torch.bfloat16))
+    torch.cuda.synchronize()
+    check(x, w, s, b, bits, gs, bits16(y))
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("bits,gs", [(3, 64), (6, 32)])
 def test_qlinear_swiglu_any_width(bits, gs):
     """The fused gate/up product with SwiGLU: widened (packed SwiGLU kernel) or
