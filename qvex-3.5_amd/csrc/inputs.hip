@@ -49,22 +49,20 @@ __device__ int block_argmax(const float* __restrict__ parts, int tiles, float* s
   }
   const float m = wave_allmax(bv);
   int c = bv == m ? bj : 0x7fffffff;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) c = min(c, __shfl_xor(c, o, 64));
+  c = wave_allmin(c);
   if ((t & 63) == 0) {
     sh_v[t >> 6] = m;
     sh_j[t >> 6] = c;
   }
   __syncthreads();
-  if (t == 0) {
-    float v = sh_v[0];
-    int j = sh_j[0];
-    for (int w = 1; w < IN_T / 64; ++w)
-      if (sh_v[w] > v || (sh_v[w] == v && sh_j[w] < j)) {
-        v = sh_v[w];
-        j = sh_j[w];
-      }
-    sh_j[IN_T / 64] = j == 0x7fffffff ? 0 : j;
+  // the waves' (max, first index) pairs combined the same way by wave 0: the
+  // largest value, then the smallest index holding it
+  if (t < 64) {
+    const float v = t < IN_T / 64 ? sh_v[t] : -__builtin_inff();
+    const int j = t < IN_T / 64 ? sh_j[t] : 0x7fffffff;
+    const float mm = wave_allmax(v);
+    const int cc = wave_allmin(v == mm ? j : 0x7fffffff);
+    if (t == 0) sh_j[IN_T / 64] = cc == 0x7fffffff ? 0 : cc;
   }
   __syncthreads();
   return sh_j[IN_T / 64];

@@ -568,16 +568,16 @@ __global__ __launch_bounds__(AM_T) void argmax_parts_kernel(const float* __restr
   }
   const float m = wave_allmax(bv);
   int c = bv == m ? bj : 0x7fffffff;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) c = min(c, __shfl_xor(c, o, 64));
+  c = wave_allmin(c);
   if ((t & 63) == 0) { bvs[t >> 6] = m; bjs[t >> 6] = c; }
   __syncthreads();
-  if (t == 0) {
-    float v = bvs[0];
-    int j = bjs[0];
-    for (int w = 1; w < AM_T / 64; ++w)
-      if (bvs[w] > v || (bvs[w] == v && bjs[w] < j)) { v = bvs[w]; j = bjs[w]; }
-    out[r] = j == 0x7fffffff ? 0 : j;
+  // the waves' pairs by wave 0: the largest value, then the smallest index holding it
+  if (t < 64) {
+    const float v = t < AM_T / 64 ? bvs[t] : -__builtin_inff();
+    const int j = t < AM_T / 64 ? bjs[t] : 0x7fffffff;
+    const float mm = wave_allmax(v);
+    const int cc = wave_allmin(v == mm ? j : 0x7fffffff);
+    if (t == 0) out[r] = cc == 0x7fffffff ? 0 : cc;
   }
 }
 

@@ -82,6 +82,17 @@ __device__ __forceinline__ float row16_allsum(float v) {
   return v;
 }
 
+// Minimum over the wave in every lane (all 64 lanes active): each DPP row's
+// minimum, then the four row minima read into scalars (a minimum is order-free).
+__device__ __forceinline__ int wave_allmin(int v) {
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false));   // quad_perm [2,3,0,1]
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, false));  // row_ror 4
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false));  // row_ror 8
+  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
 // Sum over the wave broadcast to every lane (all 64 lanes active): each DPP
 // row's sum, then the four row sums read into scalars and added as
 // (r0 + r1) + (r2 + r3). Four DPP steps and four readlanes instead of six
