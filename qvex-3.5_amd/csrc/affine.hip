@@ -59,10 +59,13 @@ __device__ __forceinline__ void load_chunk(const uint32_t* __restrict__ p, uint3
   }
 }
 
-constexpr int AFF_R = 2;       // weight rows per wave
 constexpr int AFF_MAXM = 8;    // activation rows per launch
 
-template <int BITS>
+// AFF_R weight rows per wave share each activation chunk: 1 for one or two
+// activation rows (81 VGPRs, more waves in flight: 12.6 against 13.6 us for a
+// 5-bit 12,288 x 4,096 product at one row), 2 above (the dequantized codes serve
+// twice as many products: 25 against 28.5 us at four rows).
+template <int BITS, int AFF_R>
 __global__ __launch_bounds__(256) void qmv_affine_kernel(const uint16_t* __restrict__ x,
                                                          const uint32_t* __restrict__ w,
                                                          const uint16_t* __restrict__ scales,
@@ -232,9 +235,14 @@ bool width_ok(int bits) { return bits == 2 || bits == 3 || bits == 4 || bits == 
   }
 
 template <int BITS>
-void launch_qmv(dim3 grid, hipStream_t st, const uint16_t* x, const uint32_t* w, const uint16_t* s,
-                const uint16_t* b, uint16_t* y, int M, int N, int K, int gs) {
-  hipLaunchKernelGGL(qmv_affine_kernel<BITS>, grid, dim3(256), 0, st, x, w, s, b, y, M, N, K, gs);
+void launch_qmv(hipStream_t st, const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                uint16_t* y, int M, int N, int K, int gs) {
+  if (M <= 2)
+    hipLaunchKernelGGL((qmv_affine_kernel<BITS, 1>), dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, x, w, s, b, y,
+                       M, N, K, gs);
+  else
+    hipLaunchKernelGGL((qmv_affine_kernel<BITS, 2>), dim3((unsigned)((N + 7) / 8)), dim3(256), 0, st, x, w, s, b, y,
+                       M, N, K, gs);
 }
 
 template <int BITS>
@@ -261,8 +269,7 @@ extern "C" int qvex_qmv_affine(const uint16_t* x, const uint32_t* w, const uint1
                  "qvex_qmv_affine: M=%d N=%d K=%d (1 <= M <= 8, K a positive multiple of the group size %d)", M, N,
                  K, group_size);
   QVEX_CHECK_ARG(qvex_aligned(x, 16) && qvex_aligned(w, 16), "qvex_qmv_affine: x and w must be 16-byte aligned");
-  const unsigned blocks = (unsigned)((N + 4 * AFF_R - 1) / (4 * AFF_R));
-  AFFINE_BITS_SWITCH(bits, launch_qmv, dim3(blocks), (hipStream_t)stream, x, w, scales, biases, y, M, N, K, gs);
+  AFFINE_BITS_SWITCH(bits, launch_qmv, (hipStream_t)stream, x, w, scales, biases, y, M, N, K, gs);
   QVEX_CHECK_LAUNCH("qvex_qmv_affine");
   return QVEX_OK;
 }
