@@ -7,11 +7,19 @@
 Workload "e2e" (default): a random-init Qwen3.5-9B-shaped model (32 layers, 24
 Gated DeltaNet + 8 gated attention, hidden 4096, MLP 12288, vocab 248320, 4-bit
 group-64 MLX-layout weights) with an MTP draft head sharing the lm_head. A
-4096-token prompt of seeded uniform ids is prefilled (untimed), then W warmup
-cycles run, then exactly K timed MTP cycles (draft k=3 greedy, verify 4 tokens,
-accept at T=0.7 with top-k 20 / top-p 0.8 as the reference's MTP benchmark, roll back; the cycle is captured once as a HIP graph and
-replayed, each cycle launched before the previous cycle's result is read).
-value = tokens emitted in the timed cycles / time.
+4096-token prompt of seeded uniform ids is prefilled (untimed), then the
+speculative.decode() generator - the reference's API, iterated as its MTP
+benchmark does (bench/mtp_bench.py:49-55) - runs W warmup cycles (the first
+captures the cycle as a HIP graph) and exactly K timed MTP cycles (draft k=3
+greedy, verify 4 tokens, accept at T=0.7 with top-k 20 / top-p 0.8 as the
+reference's MTP benchmark, roll back): one graph replay and one host read per
+cycle. value = tokens emitted in the timed cycles / time.
+graphed_run: the same cycles through GraphedMTPCycle.run (each launched before
+  the previous result is read), from the same prompt and seed;
+cycle_roofline: the cycle's algorithmic HBM bytes (weights, DeltaNet states, KV)
+  at 8 TB/s against the measured cycle;
+accept_all: a labelled diagnostic, greedy with the shared lm_head zeroed, so
+  every draft is accepted (k + 1 tokens a cycle, the n = k commit path).
 
 Every line also carries:
   roofline: the dominant kernel of the cycle, the packed 4-bit MFMA qmv on the
@@ -33,9 +41,7 @@ Every line also carries:
   cycle_kernels: the cycle's split DeltaNet mixer and verify attention (one
     layer at the 9B shape, isolated, rotating caches) with their HBM fractions.
 
---accept-all is a labelled diagnostic, not the headline: greedy decoding with
-the shared lm_head zeroed, so every draft is accepted (k + 1 tokens a cycle)
-and the timed cycles take the n = k commit path at the 9B shape.
+--accept-all makes that diagnostic the line's value (labelled, not the headline).
 
 The other workloads run one kernel family in a loop for rocprofv3 counter
 passes (profiles/): gdn (chunked DeltaNet prefill), gdn_verify (the config-2
@@ -269,23 +275,22 @@ def _event_time(fn, iters, reps=3):
 
 
 def spec_config3(S=256, k=4, V=248320, temperature=0.7):
-    """Fused accept/resample over S verify steps in one launch (target ~N(0,3) plus
-    +8 spikes, draft = target + N(0,1), uniforms U(0,1)); bytes (2k+1)*V*4 per step.
-    Inputs (2.29 GB) are generated on the device; bit-exactness against the oracle
-    is what the spec tests check on the same rule."""
+    """Fused accept/resample over S verify steps in one launch on the seeded
+    config-3 inputs of synth.spec_inputs (target ~N(0,3) plus +8 spikes, draft =
+    target + N(0,1), draft ids from softmax(draft/T), uniforms U(0,1)): the same
+    bytes tests/test_spec_gpu.py checks bit for bit against the oracle for all
+    256 steps. Bytes (2k+1)*V*4 per step."""
     import torch
-    from qvex import kernels
+    from qvex import kernels, synth
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(1003)
-    target = torch.randn((S, k + 1, V), generator=g, device=dev) * 3.0
-    spikes = torch.randint(0, V, (S, k + 1, 3), generator=g, device=dev)
-    target.scatter_add_(2, spikes, torch.full(spikes.shape, 8.0, device=dev))
-    draft = target[:, :k] + torch.randn((S, k, V), generator=g, device=dev)
-    draft_ids = torch.multinomial(torch.softmax(draft.reshape(-1, V) / temperature, -1), 1,
-                                  generator=g).reshape(S, k).to(torch.int32)
-    u_acc = torch.rand((S, k), generator=g, device=dev)
-    u_smp = torch.rand((S,), generator=g, device=dev)
+    threads = min(16, len(os.sched_getaffinity(0)))
+    inp = synth.spec_inputs(range(S), k=k, V=V, temperature=temperature, threads=threads)
+    target = torch.from_numpy(inp["target"]).to(dev)
+    draft = torch.from_numpy(inp["draft"]).to(dev)
+    draft_ids = torch.from_numpy(inp["draft_ids"]).to(dev)
+    u_acc = torch.from_numpy(inp["u_accept"]).to(dev)
+    u_smp = torch.from_numpy(inp["u_sample"]).to(dev)
+    del inp
     ws = kernels.spec_workspace(S, k, V, True, dev)
     n = torch.empty(S, dtype=torch.int32, device=dev)
     tok = torch.empty(S, dtype=torch.int32, device=dev)
@@ -293,9 +298,10 @@ def spec_config3(S=256, k=4, V=248320, temperature=0.7):
                                                     n_accept=n, out_token=tok, workspace=ws), 5)
     nbytes = (2 * k + 1) * V * 4 * S
     acc = float(n.float().mean())
-    del target, draft, spikes
+    del target, draft
     torch.cuda.empty_cache()
     return {"kernel": "qvex_spec_accept (3 kernels: rowstats, decide, sample)", "steps": S, "k": k, "V": V,
+            "inputs": f"synth.spec_inputs(range({S}), k={k}) (seed {synth.SEED_SPEC}, the tested inputs)",
             "us": round(us, 1), "us_per_step": round(us / S, 3), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
             "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4), "bytes": nbytes,
             "mean_accept": round(acc, 3)}
@@ -418,8 +424,9 @@ def _best_of(fn, reps=3):
 def cpu_baselines(k_spec=4, steps_sample=4):
     """The oracle's C restatement beside each config's GPU figure, on all host
     threads (best of 3): config 0 (the 12288 x 4096 GEMV, fp32 accumulate),
-    config 2 verify (T = 5 recurrence with snapshots, 32 heads of 128), config 3
-    (the fused accept on a sample of `steps_sample` of its 256 steps, scaled)."""
+    config 2 verify (T = 5 recurrence with snapshots, 32 heads of 128), config 2
+    prefill (T = 4096, one run), config 3 (the fused accept on a sample of
+    `steps_sample` of its 256 steps, scaled)."""
     import oracle
     from qvex import synth
     threads = min(int(os.environ.get("OMP_NUM_THREADS", "16")), len(os.sched_getaffinity(0)))
@@ -435,6 +442,16 @@ def cpu_baselines(k_spec=4, steps_sample=4):
     t = _best_of(lambda: oracle.gated_delta_f32(*args, inp["A_log"], f(inp["dt_bias"]), inp["state"], snaps=True,
                                                  threads=threads))
     out["config2_verify"] = {"us": round(t * 1e6, 1), "GB/s": round(12.71e6 / t / 1e9, 2)}
+    # config-2 prefill: the recurrence of engine/kernels.py:34-63 over all 4096
+    # tokens (the chunked GPU kernel regroups the same arithmetic), run once
+    inp = synth.gdn_inputs(4096, seed=9, Hk=16, Hv=32)
+    args = [f(inp[n]) for n in ("q", "k", "v", "a", "b")]
+    t0 = time.perf_counter()
+    oracle.gated_delta_f32(*args, inp["A_log"], f(inp["dt_bias"]), inp["state"], snaps=False, threads=threads)
+    t = time.perf_counter() - t0
+    flops = 32 * (4096 // 64) * (4 * 64 * 64 * 128 * 2 + 6 * 64 * 128 * 128)
+    out["config2_prefill"] = {"us": round(t * 1e6, 1), "TFLOP/s": round(flops / t / 1e12, 4),
+                              "sample": "T = 4096, 32 value heads of 128, one run (no chunking: the recurrence)"}
     sp = synth.spec_inputs(range(steps_sample), k=k_spec, V=248320)
     t = _best_of(lambda: oracle.spec_accept(sp["target"], sp["draft"], sp["draft_ids"], sp["u_accept"],
                                              sp["u_sample"], float(np.float32(1.0) / np.float32(0.7)),
@@ -519,13 +536,88 @@ def attn_verify(L=4, pos0=4348, copies=24, iters=96, kps=128):
 
 # ---------------------------------------------------------------- end to end
 
+def cycle_bytes(model, mtp, k, ctx):
+    """Algorithmic HBM bytes of one MTP cycle (k drafts, k + 1 verify rows) at
+    context ctx: every main-model weight byte once (the verify, lm_head
+    included), the MTP head's products and the shared lm_head once per draft,
+    the DeltaNet states read once and written after each verify token, and the
+    verify attention's K and V of the ctx keys in every attention layer."""
+    cfg = model.cfg
+    w = lambda q: 0.5625 * q.N * q.K
+    main = sum(w(q) for q in model.qlinears())
+    draft = k * (sum(w(q) for q in mtp.qlinears()) + w(model.lm_head))
+    n_gdn = sum(cfg.is_linear(i) for i in range(cfg.num_hidden_layers))
+    n_att = cfg.num_hidden_layers - n_gdn
+    state = cfg.linear_num_value_heads * cfg.linear_value_head_dim * cfg.linear_key_head_dim * 4
+    gdn = n_gdn * state * (1 + (k + 1))
+    kv = n_att * 2 * cfg.num_key_value_heads * ctx * cfg.head_dim * 2
+    return {"main_weights": int(main), "drafting": int(draft), "gdn_state": int(gdn), "kv": int(kv),
+            "total": int(main + draft + gdn + kv)}
+
+
+def _pull(gen, toks, stats, cycles):
+    """Iterate the decode() generator until `cycles` cycles have run and every
+    token they emitted has been taken."""
+    while stats["cycles"] < cycles or len(toks) < stats["emitted"]:
+        toks.append(next(gen))
+
+
+def time_decode(model, mtp, caches, logits, last_h, sampler, k, warmup, steps):
+    """The reference's API as its MTP benchmark drives it (bench/mtp_bench.py:
+    49-55): iterate decode() and time the tokens of `steps` cycles after
+    `warmup` cycles (the first of which captures the cycle's HIP graph). Each
+    cycle is one graph replay and one host read of its result."""
+    import torch
+    from qvex.speculative import decode
+    cache, mcache = caches
+    stats = {}
+    gen = decode(model, sampler, cache, logits[0, -1], last_h, mtp, mcache, stats=stats, k=k)
+    toks = [next(gen)]
+    _pull(gen, toks, stats, warmup)
+    torch.cuda.synchronize()
+    n0, a0, c0, g0 = len(toks), stats["accepted"], stats["cycles"], stats["graph_cycles"]
+    t0 = time.perf_counter()
+    _pull(gen, toks, stats, warmup + steps)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    gen.close()
+    n, cycles = len(toks) - n0, stats["cycles"] - c0
+    return {"value": n / dt, "ms_per_step": dt / steps * 1e3, "tokens": n, "tokens_per_cycle": n / cycles,
+            "acceptance": (stats["accepted"] - a0) / (cycles * k), "graph_cycles": stats["graph_cycles"] - g0,
+            "captures": stats["captures"]}, toks
+
+
+def time_run(model, mtp, caches, logits, last_h, sampler, k, warmup, steps):
+    """GraphedMTPCycle.run: each cycle launched before the previous cycle's result
+    is read (two graphs alternating over pinned result slots), so the GPU never
+    waits on the host between cycles; the upper bound of the decode() figure."""
+    import torch
+    from qvex.speculative import GraphedMTPCycle, MTPDecoder
+    cache, mcache = caches
+    stats = {}
+    dec = MTPDecoder(model, sampler, cache, logits[0, -1], last_h, mtp, mcache, k=k, stats=stats)
+    g = GraphedMTPCycle(dec)
+    toks = [dec.first]
+    for part in g.run(warmup):
+        toks += part
+    torch.cuda.synchronize()
+    n0 = len(toks)
+    t0 = time.perf_counter()
+    for part in g.run(steps):
+        toks += part
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    g.release()
+    n = len(toks) - n0
+    return {"value": n / dt, "ms_per_step": dt / steps * 1e3, "tokens": n}, toks
+
+
 def run_e2e(args):
     import torch
     from qvex.model import Config, random_model
     from qvex.mtp import random_mtp
     from qvex.sampler import Sampler, SamplingParams
     from qvex.engine import prefill
-    from qvex.speculative import GraphedMTPCycle, MTPDecoder
     from qvex import synth
 
     cfg = Config.qwen35_9b()
@@ -544,48 +636,75 @@ def run_e2e(args):
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t0
     log(f"prefill {args.prompt} tokens in {prefill_s:.2f}s")
-    temperature = args.temperature
-    if args.accept_all:
+    clone = lambda: (cache.clone(), mcache.clone())                  # every measurement starts from the prompt
+
+    def sampler(temperature):
+        # the reference's MTP benchmark samples with top_k = 20, top_p = 0.8 (bench/mtp_bench.py:39)
+        return Sampler(SamplingParams(temperature=temperature, top_k=args.top_k, top_p=args.top_p,
+                                      seed=synth.SEED_E2E), cfg.vocab_size)
+
+    def zero_head():
         # diagnostic: greedy with every logit 0, so drafts (token 0) are always accepted
         model.lm_head.scales.zero_()
         model.lm_head.biases.zero_()
         model.lm_head.repack()
-        temperature = 0.0
-    # the reference's MTP benchmark samples with top_k = 20, top_p = 0.8 (bench/mtp_bench.py:39)
-    sampler = Sampler(SamplingParams(temperature=temperature, top_k=args.top_k, top_p=args.top_p,
-                                     seed=synth.SEED_E2E), cfg.vocab_size)
-    stats = {}
-    dec = MTPDecoder(model, sampler, cache, logits[0, -1], last_h, mtp, mcache, k=args.k, stats=stats)
-    runner = dec
-    if not args.eager:
-        dec.cycle()                        # one eager cycle, then capture the cycle as a HIP graph
-        t0 = time.perf_counter()
-        runner = GraphedMTPCycle(dec)
-        log(f"cycle captured as a HIP graph in {time.perf_counter() - t0:.2f}s")
+
+    extra = {}
+    if args.accept_all:
+        zero_head()
+    temperature = 0.0 if args.accept_all else args.temperature
     if args.eager:
+        from qvex.speculative import MTPDecoder
+        stats = {}
+        dec = MTPDecoder(model, sampler(temperature), cache, logits[0, -1], last_h, mtp, mcache, k=args.k,
+                         stats=stats)
         for _ in range(args.warmup):
-            runner.cycle()
+            dec.cycle()
+        torch.cuda.synchronize()
+        e0, a0, c0 = stats["emitted"], stats["accepted"], stats["cycles"]
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            dec.cycle()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        n, cycles = stats["emitted"] - e0, stats["cycles"] - c0
+        res = {"value": n / dt, "ms_per_step": dt / args.steps * 1e3, "tokens": n, "tokens_per_cycle": n / cycles,
+               "acceptance": (stats["accepted"] - a0) / (cycles * args.k)}
     else:
-        runner.run(args.warmup)            # graphed: each cycle launched before the previous result is read
-    torch.cuda.synchronize()
-    e0 = stats["emitted"]
-    a0, c0 = stats["accepted"], stats["cycles"]
-    t0 = time.perf_counter()
-    if args.eager:
-        for i in range(args.steps):
-            runner.cycle()
-            if (i + 1) % 64 == 0:
-                log(f"cycle {i + 1}/{args.steps}")
-    else:
-        runner.run(args.steps)
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    emitted = stats["emitted"] - e0
-    acc = stats["accepted"] - a0
-    cycles = stats["cycles"] - c0
-    return {"value": emitted / dt, "ms_per_step": dt / args.steps * 1e3, "tokens": emitted,
-            "tokens_per_cycle": emitted / cycles, "acceptance": acc / (cycles * args.k),
-            "prefill_s": prefill_s}, cfg
+        res, toks = time_decode(model, mtp, clone(), logits, last_h, sampler(temperature), args.k, args.warmup,
+                                args.steps)
+        log(f"decode(): {res['value']:.1f} tok/s, {res['ms_per_step']:.3f} ms per cycle")
+        run, toks_run = time_run(model, mtp, clone(), logits, last_h, sampler(temperature), args.k, args.warmup,
+                                 args.steps)
+        log(f"GraphedMTPCycle.run: {run['value']:.1f} tok/s, {run['ms_per_step']:.3f} ms per cycle")
+        extra["graphed_run"] = {"value": round(run["value"], 2), "unit": "tok/s",
+                                "ms_per_step": round(run["ms_per_step"], 3),
+                                "same_tokens_as_decode": toks_run == toks[:len(toks_run)],
+                                "decode_over_run": round(res["value"] / run["value"], 4),
+                                "how": "GraphedMTPCycle.run(K): each cycle launched before the previous result "
+                                       "is read (no host gap); same seed and prompt as the decode() figure"}
+        if not args.accept_all and not args.no_accept_all:
+            zero_head()
+            aa, _ = time_decode(model, mtp, clone(), logits, last_h, sampler(0.0), args.k, args.warmup, args.steps)
+            log(f"accept-all diagnostic: {aa['value']:.1f} tok/s, {aa['ms_per_step']:.3f} ms per cycle")
+            extra["accept_all"] = {"value": round(aa["value"], 2), "unit": "tok/s",
+                                   "ms_per_step": round(aa["ms_per_step"], 3),
+                                   "tokens_per_cycle": round(aa["tokens_per_cycle"], 4),
+                                   "acceptance": round(aa["acceptance"], 4),
+                                   "how": "DIAGNOSTIC: greedy with the shared lm_head zeroed, so every draft is "
+                                          "accepted (k + 1 tokens, the n = k commit path, every cycle); decode() "
+                                          "iterated as for the headline"}
+    ctx = args.prompt + (args.warmup + args.steps // 2) * res["tokens_per_cycle"]
+    cb = cycle_bytes(model, mtp, args.k, int(ctx))
+    ms_peak = cb["total"] / (PEAK_HBM_GBS * 1e9) * 1e3
+    extra["cycle_roofline"] = {"bound": "hbm", "bytes_per_cycle": cb["total"], "components": cb,
+                               "context": int(ctx), "ms_at_peak": round(ms_peak, 4),
+                               "ms_per_cycle": round(res["ms_per_step"], 4),
+                               "frac": round(ms_peak / res["ms_per_step"], 4),
+                               "tok_s_at_peak": round(res["tokens_per_cycle"] / ms_peak * 1e3, 1)}
+    res["prefill_s"] = prefill_s
+    res["extra"] = extra
+    return res, cfg
 
 
 def main():
@@ -606,6 +725,8 @@ def main():
     ap.add_argument("--eager", action="store_true", help="launch every kernel from Python (no HIP graph)")
     ap.add_argument("--accept-all", action="store_true",
                     help="diagnostic: greedy, zeroed lm_head, every draft accepted (not the headline figure)")
+    ap.add_argument("--no-accept-all", action="store_true",
+                    help="skip the accept-all diagnostic that follows the headline")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (collectives are out of scope); "
@@ -635,9 +756,15 @@ def main():
             line["metric"] = "diagnostic: MTP cycle with every draft accepted (greedy, zeroed lm_head), tok/s"
             line["config"]["temperature"] = 0.0
             line["config"]["workload"] += "; DIAGNOSTIC accept-all (not the headline)"
+        line["config"]["timed_through"] = "MTPDecoder.cycle() op by op (--eager)" if args.eager else \
+            "speculative.decode() generator (reference API; graph replay, one host read per cycle)"
         line["tokens_per_cycle"] = round(res["tokens_per_cycle"], 4)
         line["acceptance"] = round(res["acceptance"], 4)
         line["prefill_s"] = round(res["prefill_s"], 2)
+        for key in ("graph_cycles", "captures"):
+            if key in res:
+                line[key] = res[key]
+        line.update(res["extra"])
     else:
         from qvex.model import Config
         cfg = Config.qwen35_9b()

@@ -68,8 +68,9 @@ def generate(model: Qwen35, prompt_ids, params: SamplingParams, mtp: MTPHead | N
              mtp_mode: str = "auto", k: int = 3, stop_ids=(), forced: list[int] | None = None,
              max_tokens: int | None = None) -> GenerateResult:
     """Prefill the prompt (the model runs it in 512-token chunks), hand the last
-    hidden states to the MTP head, then draw tokens through decode() until a
-    stop id or max_tokens (engine/engine.py:280-300). `forced` is shared with the
+    hidden states to the MTP head, then draw tokens through decode() (MTP
+    cycles replayed from a captured HIP graph) until a stop id or max_tokens
+    (engine/engine.py:280-300). `forced` is shared with the
     generator: ids appended to it while iterating are emitted next, as the
     reference's reasoning budget does. A stop id counts in completion_tokens but
     is not returned. Stats keys follow the reference's (engine/engine.py:340-357)
@@ -84,8 +85,8 @@ def generate(model: Qwen35, prompt_ids, params: SamplingParams, mtp: MTPHead | N
 
     t_start = time.perf_counter()
     # room for the prompt, every emitted token and the draft/verify tokens past
-    # the last one (the reference's caches grow, engine/model.py:156-170; these
-    # are sized up front)
+    # the last one: the caches grow when they must (engine/model.py:156-170),
+    # but sized up front the captured cycle is never captured again for room
     need = ids.shape[1] + limit + 2 * k + 2
     cap = max(model.max_context, need)
     cache = model.make_cache(max_context=cap)
@@ -122,5 +123,6 @@ def generate(model: Qwen35, prompt_ids, params: SamplingParams, mtp: MTPHead | N
         "decode_tps": n / decode_s if decode_s > 0 else None,
         "mtp_cycles": spec.get("cycles", 0),
         "mtp_accepted": spec.get("accepted", 0),
+        "mtp_graph_cycles": spec.get("graph_cycles", 0),
     }
     return GenerateResult(out, finish, stats)

@@ -528,6 +528,26 @@ class KVCache:
     def rollback(self, n=1):
         self.offset -= n  # entries past offset are overwritten by the next append
 
+    def grow(self, min_capacity: int) -> bool:
+        """Enlarge the cache to hold at least min_capacity keys, rounded up to a
+        whole step (engine/model.py:156-170 grows by the same 256-token steps
+        when an update would pass the end). The keys kept so far move to the new
+        tiles; a HIP graph captured on the old buffers must be captured again.
+        Returns whether the buffers changed."""
+        self.counters._check_host_edit()
+        if min_capacity <= self.capacity:
+            return False
+        cap = int(math.ceil(min_capacity / self.step) * self.step)
+        k = torch.zeros((self.k.shape[0], cap // 16) + tuple(self.k.shape[2:]), dtype=self.k.dtype,
+                        device=self.k.device)
+        v = torch.zeros((self.v.shape[0], cap // 32) + tuple(self.v.shape[2:]), dtype=self.v.dtype,
+                        device=self.v.device)
+        # a head's tiles are consecutive and key-major: the old tiles are the new head's first ones
+        k[:, : self.k.shape[1]].copy_(self.k)
+        v[:, : self.v.shape[1]].copy_(self.v)
+        self.k, self.v, self.capacity = k, v, cap
+        return True
+
     def clone(self, counters: CacheCounters | None = None) -> "KVCache":
         """A copy of the cache (device tensors copied); counters: the cloned table
         it indexes (a new one-entry table for a standalone cache)."""
@@ -636,10 +656,10 @@ class Attention:
         cfg = self.cfg
         H, Hkv, D = self.n_heads, self.n_kv, self.head_dim
         if not cache.counters.graph_mode and cache.offset + L > cache.capacity:
-            # the kernels would drop the writes past the capacity; the reference
-            # grows its cache (engine/model.py:156-170), this one is sized up front
-            raise _C.QvexError(f"KV cache full: offset {cache.offset} + {L} tokens > capacity {cache.capacity} "
-                               "(make the cache with a larger max_context)")
+            # grown in 256-token steps as engine/model.py:156-170 does; a captured
+            # call cannot move its buffers (GraphedMTPCycle checks room before each
+            # replay, and decode() grows the caches and captures again)
+            cache.grow(cache.offset + L)
         proj = self.qkv_proj(x)                                   # [L, H*2D + 2*Hkv*D]
         pos = cache.counters.ptr(cache.index)
         # a captured call must work for every later context length: bound by capacity

@@ -96,6 +96,10 @@ class MTPDecoder:
     def can_speculate(self) -> bool:
         return self.mtp is not None and bool(self.pend_h)
 
+    def pending(self) -> int:
+        """(hidden, token) pairs not yet given to the MTP head."""
+        return sum(int(h.shape[1]) for h in self.pend_h)
+
     def _eager(self) -> None:
         if self.cache.counters.graph_mode or (self.mtp_cache is not None and self.mtp_cache.counters.graph_mode):
             raise _C.QvexError("this decoder's caches are driven by a GraphedMTPCycle; call its release() "
@@ -151,26 +155,83 @@ class MTPDecoder:
         return int(t.item())
 
 
+# a captured cycle that runs out of KV room grows the caches by at least this
+# many positions (or half their capacity) before it is captured again
+GRAPH_GROW_MIN = 2048
+
+
+def grow_kv(caches, extra: int) -> bool:
+    """Grow every KV cache among `caches` to hold `extra` positions past its
+    offset (KVCache.grow); returns whether any moved."""
+    moved = False
+    for c in caches:
+        if hasattr(c, "grow"):
+            moved |= c.grow(c.offset + extra)
+    return moved
+
+
 def decode(model: Qwen35, sampler: Sampler, cache, first_logits, last_hidden=None,
            mtp: MTPHead | None = None, mtp_cache=None,
            use_mtp: Callable[[], bool] = lambda: True, stats: dict | None = None,
-           forced: list[int] | None = None, k: int = 1):
+           forced: list[int] | None = None, k: int = 1, graph: bool = True):
     """Generator of token ids (engine/speculative.py:44-118). stats gets 'cycles',
-    'accepted' (accepted drafts), 'plain' and 'emitted'. forced: tokens emitted
-    next, in order, instead of sampled ones (plain steps only)."""
+    'accepted' (accepted drafts), 'plain' and 'emitted', plus 'graph_cycles'
+    (cycles replayed from the captured graph) and 'captures'. forced: tokens
+    emitted next, in order, instead of sampled ones (plain steps only).
+
+    With graph (the default) each MTP cycle is a replay of a GraphedMTPCycle:
+    one launch of the captured draft -> verify -> accept -> commit graph and one
+    host read of its result, the reference's one synchronisation per cycle
+    (engine/speculative.py:82-85). use_mtp() and `forced` are looked at before
+    every cycle, as the reference does: a plain or forced step releases the
+    graph (the caches go back to eager control), and the next MTP cycle
+    captures it again (10-30 ms), after one eager cycle when more than k + 1
+    (hidden, token) pairs are pending. When the next cycle would not fit a KV
+    cache, the caches grow (by GRAPH_GROW_MIN positions or half their capacity)
+    and the cycle is captured on the new buffers. The token stream is the one
+    graph=False (every cycle launched op by op from the host) emits."""
     forced = forced if forced is not None else []
     dec = MTPDecoder(model, sampler, cache, first_logits, last_hidden, mtp, mtp_cache, k, stats)
+    st = dec.stats
+    st.setdefault("graph_cycles", 0)
+    st.setdefault("captures", 0)
     yield dec.first
-    while True:
-        if dec.can_speculate() and not forced and use_mtp():
-            for t in dec.cycle():
-                yield t
-        else:
-            yield dec.plain(forced.pop(0) if forced else None)
+    g = None
+    try:
+        while True:
+            if dec.can_speculate() and not forced and use_mtp():
+                if graph:
+                    if g is None or g.released:
+                        if dec.pending() > k + 1:
+                            for t in dec.cycle():
+                                yield t
+                            continue
+                        g = GraphedMTPCycle(dec) if g is None else g.attach()
+                        st["captures"] += 1
+                    if g.room() < 1:
+                        g.release()
+                        kv = [c for c in dec.cache if hasattr(c, "grow")] + [dec.mtp_cache]
+                        grow_kv(kv, max(GRAPH_GROW_MIN, max(c.capacity for c in kv) // 2))
+                        g.attach()
+                        st["captures"] += 1
+                    emitted = g.cycle()
+                    st["graph_cycles"] += 1
+                    for t in emitted:
+                        yield t
+                else:
+                    for t in dec.cycle():
+                        yield t
+            else:
+                if g is not None and not g.released:
+                    g.release()
+                yield dec.plain(forced.pop(0) if forced else None)
+    finally:
+        if g is not None and not g.released:
+            g.release()
 
 
 class GraphedMTPCycle:
-    """The MTP cycle of MTPDecoder.cycle() captured once as a HIP graph.
+    """The MTP cycle of MTPDecoder.cycle() captured as a HIP graph.
 
     Everything that changes between cycles is device state: the pending
     (hidden, token) pairs of the MTP head (k + 1 fixed rows, the first n_prev + 1
@@ -184,49 +245,77 @@ class GraphedMTPCycle:
 
     While the object drives the decoder's caches their device counters are
     authoritative: eager model calls, rollbacks and MTPDecoder steps on them
-    raise until release() hands the state back. A cycle that could write past a
-    KV cache's capacity raises before it is launched.
+    raise until release() hands the state back; attach() takes it again (and
+    captures the cycle again). A cycle that could write past a KV cache's
+    capacity raises before it is launched (room() tells how many fit).
     """
 
     def __init__(self, dec: MTPDecoder):
         if dec.mtp is None or not dec.pend_h:
             raise _C.QvexError("GraphedMTPCycle needs an MTPDecoder with an MTP head and pending pairs")
         self.dec = dec
-        model, mtp, cache, mc, k = dec.model, dec.mtp, dec.cache, dec.mtp_cache, dec.k
+        model, k = dec.model, dec.k
         self.k = k
         dev = model.norm.device
         H = model.cfg.hidden_size
-        h_in = dec.pend_h[0] if len(dec.pend_h) == 1 else torch.cat(dec.pend_h, dim=1)
-        id_in = dec.pend_ids[0] if len(dec.pend_ids) == 1 else torch.cat(dec.pend_ids, dim=1)
-        P = h_in.shape[1]
-        if P > k + 1:
-            raise _C.QvexError(f"{P} pending pairs exceed the captured width k + 1 = {k + 1}")
         self.pend_h = torch.zeros((1, k + 1, H), dtype=torch.bfloat16, device=dev)
-        self.pend_h[:, :P] = h_in
         self.pend_ids = torch.zeros((1, k + 1), dtype=torch.int32, device=dev)
-        self.pend_ids[:, :P] = id_in.to(torch.int32)
-        self.n_prev = torch.tensor([P - 1], dtype=torch.int32, device=dev)
-        self.n_prev_host = P - 1
-        self.feed = dec.feed.to(torch.int32).reshape(1).clone()
+        self.n_prev = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.n_prev_host = 0
+        self.feed = torch.zeros(1, dtype=torch.int32, device=dev)
         # verify input [feed, d_0 .. d_{k-1}]: the drafts are written in place and
         # the finishing kernel stores the next feed in slot 0
-        self.ids = torch.empty((1, k + 1), dtype=torch.int32, device=dev)
-        self.ids[:, :1] = self.feed.view(1, 1)
+        self.ids = torch.zeros((1, k + 1), dtype=torch.int32, device=dev)
         self.drafts = self.ids[0, 1:]
         self.out = torch.zeros(2 + k, dtype=torch.int32, device=dev)
         self.zero = torch.zeros(1, dtype=torch.int32, device=dev)
         self.u_buf = torch.empty(k + 1, dtype=torch.float32, device=dev)
-        # the first cycle's uniforms; each replay draws the next cycle's at its end
-        dec.sampler.draw_into(self.u_buf)
-        self.released = False
-        # device counters must hold the host values before they become authoritative
-        cache.counters.sync()
-        mc.counters.sync()
-        torch.cuda.synchronize()
-        cache.counters.graph_mode = True
-        mc.counters.graph_mode = True
-        self.graph = self._capture(self.out)
+        self._kv = [c for c in dec.cache if hasattr(c, "capacity")]
+        self._rec = [c for c in dec.cache if hasattr(c, "last_width")]
+        self.released = True
+        self.graph = None
         self._pipe = None
+        self.attach()
+
+    def attach(self) -> "GraphedMTPCycle":
+        """Take the decoder's state (pending pairs, feed, counters) into the device
+        buffers and capture the cycle on the caches' current buffers. Called by
+        the constructor, and again after release() and eager steps (plain steps,
+        forced tokens, an eager cycle, a grown KV cache): the capture is made
+        again each time, since a grown cache has moved and attention's key
+        bound depends on the position at capture. Needs at most k + 1 pending
+        pairs (run one eager cycle first when there are more)."""
+        if not self.released:
+            return self
+        d, k = self.dec, self.k
+        if not d.pend_h:
+            raise _C.QvexError("GraphedMTPCycle needs pending (hidden, token) pairs")
+        h_in = d.pend_h[0] if len(d.pend_h) == 1 else torch.cat(d.pend_h, dim=1)
+        id_in = d.pend_ids[0] if len(d.pend_ids) == 1 else torch.cat(d.pend_ids, dim=1)
+        P = h_in.shape[1]
+        if P > k + 1:
+            raise _C.QvexError(f"{P} pending pairs exceed the captured width k + 1 = {k + 1}")
+        self.pend_h.zero_()
+        self.pend_h[:, :P] = h_in
+        self.pend_ids.zero_()
+        self.pend_ids[:, :P] = id_in.to(torch.int32)
+        self.n_prev.fill_(P - 1)
+        self.n_prev_host = P - 1
+        self.feed.copy_(d.feed.to(torch.int32).reshape(1))
+        self.ids[:, :1] = self.feed.view(1, 1)
+        # the first cycle's uniforms; each replay draws the next cycle's at its end
+        d.sampler.draw_into(self.u_buf)
+        # device counters must hold the host values before they become authoritative
+        d.cache.counters.sync()
+        d.mtp_cache.counters.sync()
+        torch.cuda.synchronize()
+        d.cache.counters.graph_mode = True
+        d.mtp_cache.counters.graph_mode = True
+        self.released = False
+        old = self.graph
+        self.graph = self._capture(self.out, pool=None if old is None else old.pool())
+        self._pipe = None
+        return self
 
     def _capture(self, out, pool=None) -> torch.cuda.CUDAGraph:
         """Capture one cycle writing its result to `out`; the host mirrors the
@@ -297,23 +386,36 @@ class GraphedMTPCycle:
                 d.sampler.seed, d.sampler.counter(self.u_buf.device).data_ptr(), k + 1, _ptr(self.u_buf), _stream())
         d.sampler.observe_result(out)
 
-    def _check_room(self, in_flight: int = 0) -> None:
-        """Raise unless the next cycle (after `in_flight` launched, unaccounted
-        cycles of at most k + 1 tokens each) fits every KV cache: the verify writes
-        k + 1 positions from the main offset, the draft steps k + 1 and then k - 1
-        rows from the MTP offset."""
+    def room(self) -> int:
+        """How many more cycles surely fit every KV cache (none in flight): each
+        verify writes k + 1 positions from the main offset and commits at most
+        k + 1; the draft steps write k + 1 rows and then k - 1 more from the MTP
+        offset (n_prev + 1 + 2k positions past it) and commit n_prev + 1 <= k + 1."""
         if self.released:
             raise _C.QvexError("GraphedMTPCycle was released")
         k, d = self.k, self.dec
-        ahead = in_flight * (k + 1)
-        for c in d.cache:
-            cap = getattr(c, "capacity", None)
-            if cap is not None and c.offset + ahead + k + 1 > cap:
-                raise _C.QvexError(f"KV cache full: offset {c.offset} + {ahead + k + 1} > capacity {cap} "
-                                   "(make the cache with a larger max_context)")
+        fit = None
+        for c in self._kv:
+            m = max(0, (c.capacity - c.offset) // (k + 1))
+            fit = m if fit is None else min(fit, m)
         mc = d.mtp_cache
-        if mc.offset + ahead + self.n_prev_host + 1 + 2 * k > mc.capacity:
-            raise _C.QvexError(f"MTP KV cache full: offset {mc.offset} > capacity {mc.capacity} - {2 * k + 1}")
+        free = mc.capacity - mc.offset
+        if free < self.n_prev_host + 1 + 2 * k:
+            m = 0
+        else:      # the first cycle as above, each later one with n_prev <= k
+            m = 1 + max(0, (free - (self.n_prev_host + 1) - (3 * k + 1)) // (k + 1) + 1)
+        return m if fit is None else min(fit, m)
+
+    def _check_room(self, n: int = 1) -> None:
+        """Raise, before anything is launched, unless n more cycles fit."""
+        r = self.room()
+        if r < n:
+            d = self.dec
+            caps = sorted({getattr(c, "capacity", 0) for c in d.cache} - {0})
+            raise _C.QvexError(f"KV cache full: {n} more cycle(s) of k + 1 = {self.k + 1} tokens need room, {r} "
+                               f"fit (main offset {d.cache[-1].offset}, capacity {caps}; MTP offset "
+                               f"{d.mtp_cache.offset}, capacity {d.mtp_cache.capacity}); release() and grow the "
+                               "caches, or make them with a larger max_context")
 
     def cycle(self) -> list[int]:
         """Replay one cycle; returns the emitted tokens (n accepted drafts + 1)."""
@@ -329,6 +431,8 @@ class GraphedMTPCycle:
         cycle only reads device state, so the token stream and the caches are
         those of n cycle() calls, and no cycle is in flight on return. Returns
         each cycle's emitted tokens."""
+        if self.released:
+            raise _C.QvexError("GraphedMTPCycle was released")
         if self._pipe is None:
             ring = torch.zeros((2, 2 + self.k), dtype=torch.int32, pin_memory=True)
             graphs = [self._capture(ring[s], pool=self.graph.pool()) for s in range(2)]
@@ -337,13 +441,14 @@ class GraphedMTPCycle:
         res = []
         if n <= 0:
             return res
-        self._check_room()
+        # room for every cycle is checked before the first launch, so no launched
+        # cycle is ever left unaccounted
+        self._check_room(n)
         graphs[0].replay()
         evs[0].record()
         for c in range(n):
             s = c % 2
             if c + 1 < n:
-                self._check_room(in_flight=1)
                 graphs[1 - s].replay()
                 evs[1 - s].record()
             evs[s].synchronize()
@@ -353,7 +458,7 @@ class GraphedMTPCycle:
     def release(self) -> MTPDecoder:
         """Hand the state back to the MTPDecoder (device counters, feed, pending
         pairs) so eager cycle()/plain() steps, model calls and rollbacks work
-        again; this object cannot replay afterwards. Returns the decoder."""
+        again; this object cannot replay until attach(). Returns the decoder."""
         if self.released:
             return self.dec
         torch.cuda.synchronize()
@@ -377,9 +482,8 @@ class GraphedMTPCycle:
         n, tok = int(vals[0]), int(vals[1])
         d = self.dec
         d.cache.counters.host += n + 1
-        for c in d.cache:
-            if hasattr(c, "last_width"):
-                c.last_width = n + 1          # the verify's k + 1 snapshots, k - n rolled back
+        for c in self._rec:
+            c.last_width = n + 1              # the verify's k + 1 snapshots, k - n rolled back
         d.mtp_cache.counters.host[d.mtp_cache.index] += self.n_prev_host + 1
         self.n_prev_host = n
         d.cache.counters.dirty = False

@@ -135,8 +135,11 @@ def spec_step(step: int, k: int, V: int, temperature: float, seed: int = SEED_SP
     return target, draft, ids, u_accept, np.float32(u_sample)
 
 
-def spec_inputs(steps, k: int = 4, V: int = VOCAB, temperature: float = 0.7, seed: int = SEED_SPEC):
-    """Stacked spec_step for the given step indices."""
+def spec_inputs(steps, k: int = 4, V: int = VOCAB, temperature: float = 0.7, seed: int = SEED_SPEC,
+                threads: int = 1):
+    """Stacked spec_step for the given step indices; with threads > 1 the steps
+    are generated concurrently (each has its own seed stream, so the bytes do
+    not depend on the thread count)."""
     steps = list(steps)
     S = len(steps)
     target = np.empty((S, k + 1, V), np.float32)
@@ -144,6 +147,15 @@ def spec_inputs(steps, k: int = 4, V: int = VOCAB, temperature: float = 0.7, see
     ids = np.empty((S, k), np.int32)
     ua = np.empty((S, k), np.float32)
     us = np.empty(S, np.float32)
-    for i, s in enumerate(steps):
-        target[i], draft[i], ids[i], ua[i], us[i] = spec_step(s, k, V, temperature, seed)
+
+    def one(i):
+        target[i], draft[i], ids[i], ua[i], us[i] = spec_step(steps[i], k, V, temperature, seed)
+
+    if threads > 1 and S > 1:
+        from concurrent.futures import ThreadPoolExecutor
+        with ThreadPoolExecutor(min(threads, S)) as ex:
+            list(ex.map(one, range(S)))
+    else:
+        for i in range(S):
+            one(i)
     return dict(target=target, draft=draft, draft_ids=ids, u_accept=ua, u_sample=us)

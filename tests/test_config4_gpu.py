@@ -139,3 +139,48 @@ def test_all_accept_cycles_graphed_equal_eager_and_plain(big):
         m.lm_head.scales.copy_(s0)
         m.lm_head.biases.copy_(b0)
         m.lm_head.repack()
+
+
+def decode_gen(big, graph, forced, flag, stats, **params):
+    from qvex.speculative import decode
+    m, mtp, cache, mc, logits, last_h = branch(big)
+    s = Sampler(SamplingParams(**params), m.cfg.vocab_size)
+    gen = decode(m, s, cache, logits[0, -1], last_h, mtp, mc, use_mtp=lambda: flag[0], stats=stats, forced=forced,
+                 k=3, graph=graph)
+    return gen, cache
+
+
+@pytest.mark.gpu
+def test_decode_graph_equals_eager_bench_sampling_forced_and_toggle(big):
+    """decode() as the reference's API drives it (engine/speculative.py:44-118,
+    bench/mtp_bench.py:49-55), at the 9B shape after the 4096-token prompt, with
+    the benchmark's sampling (T = 0.7, top-k 20, top-p 0.8): the captured-graph
+    cycles emit the op-by-op cycles' tokens, also across a forced-token
+    insertion and the MTP policy turned off and on again while iterating."""
+    params = dict(temperature=0.7, top_k=20, top_p=0.8, seed=13)
+    streams, stats, caches = [], [], []
+    for graph in (True, False):
+        forced, flag, st = [], [True], {}
+        gen, cache = decode_gen(big, graph, forced, flag, st, **params)
+        toks = []
+        for t in gen:
+            toks.append(t)
+            if len(toks) == 6:
+                forced.extend([100, 200])
+            if len(toks) == 12:
+                flag[0] = False
+            if len(toks) == 15:
+                flag[0] = True
+            if len(toks) >= 26:
+                break
+        gen.close()
+        streams.append(toks)
+        stats.append(st)
+        caches.append(cache)
+    print("graph stats", stats[0], "eager stats", stats[1])
+    assert streams[0] == streams[1]
+    assert streams[0][6:8] == [100, 200]
+    for key in ("cycles", "accepted", "plain", "emitted"):
+        assert stats[0][key] == stats[1][key], key
+    assert stats[0]["graph_cycles"] > 0 and stats[0]["captures"] >= 2 and stats[1]["graph_cycles"] == 0
+    assert [c.offset for c in caches[0]] == [c.offset for c in caches[1]]

@@ -1,5 +1,5 @@
-"""Host-side guards (CPU): a KV cache refuses a call that would pass its
-capacity (the kernels would drop those writes), caches driven by a captured
+"""Host-side guards (CPU): a KV cache grows in 256-token steps and keeps its
+keys where the kernels read them, caches driven by a captured
 cycle refuse host edits except during capture, recurrent rollback is bounded by
 the last call's width, and cache clones are independent."""
 
@@ -8,25 +8,33 @@ import pytest
 import torch
 
 from qvex import _C
-from qvex.model import Attention, CacheCounters, KVCache, LayerCaches, RecurrentCache
+from qvex.model import CacheCounters, KVCache, LayerCaches, RecurrentCache
 
 
-def attention_stub(H=2, Hkv=1, D=64):
-    att = Attention.__new__(Attention)
-    att.cfg = None
-    att.n_heads, att.n_kv, att.head_dim = H, Hkv, D
-    return att
-
-
-def test_kv_cache_refuses_to_overflow():
+def test_kv_cache_grows_in_steps_keeping_its_keys():
+    """KVCache.grow (engine/model.py:156-170 grows by 256-token steps): the
+    capacity rounds up to a step, every kept tile stays where the attention
+    kernels read it (a head's tiles are key-major), the new tiles are zero, and
+    a cache driven by a captured cycle refuses to move."""
     counters = CacheCounters(1, "cpu")
-    cache = KVCache(counters, 0, n_kv=1, head_dim=64, capacity=256, device="cpu")
-    assert cache.capacity == 256
+    cache = KVCache(counters, 0, n_kv=2, head_dim=64, capacity=256, device="cpu")
+    cache.k.copy_(torch.arange(cache.k.numel(), dtype=torch.float32).reshape(cache.k.shape))
+    cache.v.copy_(-torch.arange(cache.v.numel(), dtype=torch.float32).reshape(cache.v.shape))
+    k0, v0 = cache.k.clone(), cache.v.clone()
     cache.offset = 254
-    att = attention_stub()
-    with pytest.raises(_C.QvexError, match="KV cache full"):
-        att(torch.zeros((4, 128)), cache)
-    assert cache.offset == 254                      # nothing advanced
+    assert not cache.grow(256)
+    assert cache.grow(254 + 4)
+    assert cache.capacity == 512
+    assert cache.k.shape == (2, 512 // 16, 2, 64, 8) and cache.v.shape == (2, 512 // 32, 64, 32)
+    assert torch.equal(cache.k[:, :16], k0) and torch.equal(cache.v[:, :8], v0)
+    assert float(cache.k[:, 16:].abs().sum()) == 0.0 and float(cache.v[:, 8:].abs().sum()) == 0.0
+    assert cache.offset == 254
+    assert cache.grow(1000) and cache.capacity == 1024
+    assert torch.equal(cache.k[:, :16], k0)
+    counters.graph_mode = True
+    with pytest.raises(_C.QvexError, match="captured cycle"):
+        cache.grow(2000)
+    assert cache.capacity == 1024
 
 
 def test_graph_mode_refuses_host_edits_except_while_capturing():

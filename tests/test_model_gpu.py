@@ -315,3 +315,136 @@ def test_generate_policy_errors(tiny):
         generate(tiny, [1, 2, 3], p, None, mtp_mode="on")
     with pytest.raises(ValueError):
         generate(tiny, [1, 2, 3], p, None, mtp_mode="sometimes")
+
+
+# ---------------------------------------------------------------- decode() on the captured cycle
+
+def decode_pair(model, mtp, k, temp, seed, prompt_len=15, **params):
+    """Two decode() generators from one prefilled prompt (separate caches, same
+    sampler seed): the captured-graph one and the op-by-op one. Returns
+    ((gen, forced, flag, stats), ...) for graph=True and graph=False."""
+    from qvex.speculative import decode
+    V = model.cfg.vocab_size
+    ids = torch.from_numpy(prompt(prompt_len, V, seed=41)).reshape(1, -1).to(DEV)
+    out = []
+    for graph in (True, False):
+        cache, mc = model.make_cache(), mtp.make_cache()
+        logits, hidden = model(ids, cache, return_hidden=True)
+        last_h = mtp_prefill(mtp, mc, hidden, ids, None)
+        sp = dict(temperature=temp, top_k=0, top_p=1.0, seed=seed)
+        sp.update(params)
+        s = Sampler(SamplingParams(**sp), V)
+        forced, flag, stats = [], [True], {}
+        gen = decode(model, s, cache, logits[0, -1], last_h, mtp, mc, use_mtp=lambda f=flag: f[0], stats=stats,
+                     forced=forced, k=k, graph=graph)
+        out.append((gen, forced, flag, stats, cache, mc))
+    return out
+
+
+def drive(gen, forced, flag, n, force_at=None, off_at=None, on_at=None):
+    """Consume n tokens; at the given token counts append forced ids (a list)
+    or turn the MTP policy off / on, as a caller does between tokens."""
+    toks = []
+    for t in gen:
+        toks.append(t)
+        if force_at is not None and len(toks) == force_at[0]:
+            forced.extend(force_at[1])
+        if off_at is not None and len(toks) == off_at:
+            flag[0] = False
+        if on_at is not None and len(toks) == on_at:
+            flag[0] = True
+        if len(toks) >= n:
+            break
+    gen.close()
+    return toks
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("head", ["random", "flat"])
+def test_decode_graph_equals_eager_across_forced_and_toggle(head):
+    """decode() replays the captured cycle (graph=True, the default) and emits
+    the op-by-op cycle's tokens (graph=False), also across a forced-token
+    insertion and the MTP policy turned off and on again while iterating, with
+    the reference's MTP benchmark sampling (T = 0.7, top-k 20, top-p 0.8) plus a
+    presence penalty; the graph is released for the plain steps and captured
+    again afterwards, and closing the generator hands the caches back."""
+    m = random_model(Config.tiny(layers=4, vocab=2048), seed=71, device=DEV, max_context=1024) \
+        if head == "random" else flat_head_model(seed=72)
+    mtp = random_mtp(m, seed=73)
+    params = dict(top_k=20, top_p=0.8, presence_penalty=0.4)
+    (ga, fa, la, sa, ca, _), (ge, fe, le, se, ce, _) = decode_pair(m, mtp, 3, 0.7, 9, **params)
+    plan = dict(force_at=(7, [5, 6, 7]), off_at=15, on_at=19)
+    ta = drive(ga, fa, la, 48, **plan)
+    te = drive(ge, fe, le, 48, **plan)
+    print(head, "cycles", sa["cycles"], "accepted", sa["accepted"], "plain", sa["plain"], "graph cycles",
+          sa["graph_cycles"], "captures", sa["captures"])
+    assert ta == te
+    assert ta[7:10] == [5, 6, 7]
+    for key in ("cycles", "accepted", "plain", "emitted"):
+        assert sa[key] == se[key], key
+    assert 0 < sa["graph_cycles"] <= sa["cycles"]
+    assert se["graph_cycles"] == 0 and sa["captures"] >= 2
+    assert not ca.counters.graph_mode and [c.offset for c in ca] == [c.offset for c in ce]
+
+
+@pytest.mark.gpu
+def test_decode_graph_grows_kv_caches():
+    """A cache too small for the run: the op-by-op path grows every KV cache in
+    256-token steps as it goes (engine/model.py:156-170); the captured path
+    releases, grows and captures again. Same tokens, and the keys written
+    before a growth stay visible after it (all drafts accepted, 4 tokens a
+    cycle)."""
+    m = flat_head_model(seed=74)
+    m.max_context = 256
+    mtp = random_mtp(m, seed=75)
+    (ga, fa, la, sa, ca, mca), (ge, fe, le, se, ce, mce) = decode_pair(m, mtp, 3, 0.0, 0, prompt_len=230)
+    assert mca.capacity == 256
+    ta = drive(ga, fa, la, 120)
+    te = drive(ge, fe, le, 120)
+    assert ta == te
+    assert sa["captures"] >= 2 and sa["graph_cycles"] == sa["cycles"]
+    assert [c.offset for c in ca] == [c.offset for c in ce]
+    assert all(c.capacity >= c.offset for c in ca if hasattr(c, "capacity")) and mca.capacity > 256
+    assert min(c.capacity for c in ce if hasattr(c, "capacity")) > 256
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("head", ["random", "flat"])
+def test_graphed_run_checks_room_before_launching(head):
+    """run(n) past the caches' room raises before any launch (no cycle is left
+    in flight and unaccounted); run(room()) then fills the caches, release()
+    hands back a state from which eager cycles (growing the caches) continue the
+    stream of a decoder that ran eagerly throughout."""
+    from qvex import _C
+    from qvex.speculative import GraphedMTPCycle
+    m = random_model(Config.tiny(layers=4, vocab=2048), seed=76, device=DEV, max_context=256) \
+        if head == "random" else flat_head_model(seed=77)
+    m.max_context = 256
+    mtp = random_mtp(m, seed=78)
+    params = dict(top_k=20, top_p=0.8)
+    a = start_decoder(m, mtp, 3, 0.7, seed=4, **params)
+    b = start_decoder(m, mtp, 3, 0.7, seed=4, **params)
+    g = GraphedMTPCycle(b)
+    r = g.room()
+    assert r > 0
+    before = (b.cache.counters.dev.clone(), b.mtp_cache.counters.dev.clone(), b.stats["cycles"])
+    with pytest.raises(_C.QvexError, match="KV cache full"):
+        g.run(r + 1)
+    torch.cuda.synchronize()
+    assert torch.equal(before[0], b.cache.counters.dev) and torch.equal(before[1], b.mtp_cache.counters.dev)
+    assert b.stats["cycles"] == before[2]
+    tb = [t for part in g.run(r) for t in part]
+    with pytest.raises(_C.QvexError, match="KV cache full"):
+        g.run(g.room() + 1)
+    ta = []
+    for _ in range(r):
+        ta += a.cycle()
+    assert ta == tb
+    g.release()
+    while max(c.offset for c in a.cache) <= 300:     # past the old capacity: eager calls grow the caches
+        ta += a.cycle()
+        tb += b.cycle()
+    assert ta == tb
+    assert min(c.capacity for c in b.cache if hasattr(c, "capacity")) > 256
+    assert [c.offset for c in a.cache] == [c.offset for c in b.cache]
+    assert a.mtp_cache.offset == b.mtp_cache.offset
