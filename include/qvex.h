@@ -324,7 +324,7 @@ int qvex_spec_accept_filtered(const float* target, const float* draft, const int
 /* The same on bf16 logits as the lm_head writes them (target and draft both
  * bf16): every value widens exactly to fp32 on load, so the results equal
  * qvex_spec_accept_filtered on the fp32 copies (Sampler.scores' astype(float32),
- * engine/sampler.py:151) without making them. */
+ * engine/sampler.py:33) without making them. */
 int qvex_spec_accept_filtered_bf16(const uint16_t* target, const uint16_t* draft,
                                    const int32_t* draft_ids, const float* u_accept,
                                    const float* u_sample, float inv_temp, const float* seen,
@@ -352,8 +352,9 @@ int qvex_sampler_scores(const void* logits, int logits_bf16, int R, int V, const
  * this is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid allocation). Calls whose
  * qvex_spec_accept_filtered_workspace_bytes(S, k, V, draft != NULL, top_k)
- * exceeds the array return QVEX_EINVAL (a verify step of the 9B vocabulary
- * needs < 100 KB). Every call on a GPU shares that GPU's array: calls that
+ * exceeds the array return QVEX_EINVAL (one verify step of k = 3 drafts over
+ * the 9B vocabulary of 248,320 needs about 140 KB with top-k 20, about 33 KB
+ * unfiltered). Every call on a GPU shares that GPU's array: calls that
  * overlap on one GPU (different streams, threads) race and must be ordered
  * by the caller. Results equal qvex_spec_accept_filtered_bf16's bit for bit. */
 #define QVEX_SPEC_SCRATCH_BYTES (4u << 20)
@@ -453,7 +454,7 @@ int qvex_gated_rmsnorm(const uint16_t* y, const uint16_t* z, long z_stride, int 
  * engine/model.py:133-135, 300-302). */
 int qvex_swiglu(const uint16_t* gu, uint16_t* out, int L, int I, void* stream);
 
-/* fp32 copy of bf16 values (Sampler.scores' astype(float32), engine/sampler.py:151). */
+/* fp32 copy of bf16 values (Sampler.scores' astype(float32), engine/sampler.py:33). */
 int qvex_bf16_to_f32(const uint16_t* in, float* out, long n, void* stream);
 
 /* KV cache layouts (cap a multiple of 32; K and V each hold Hkv * cap * D bf16),

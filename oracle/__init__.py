@@ -36,13 +36,16 @@ listed per function below; each is exercised in tests/test_oracle.py.
 from __future__ import annotations
 
 import ctypes
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "liboracle.so"
+# QVEX_ORACLE_LIB names another build of the same sources (the sanitizer build
+# of `make asan`, which tests/test_oracle_asan.py runs the oracle tests on)
+LIB_PATH = Path(os.environ["QVEX_ORACLE_LIB"]) if os.environ.get("QVEX_ORACLE_LIB") else HERE / "liboracle.so"
 
 _lib = None
 

@@ -289,6 +289,84 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
+// Threshold selection of a part's K largest values (K <= 64), the same multiset
+// block_topk gives, without its K serial rounds. tau = the largest, over the
+// four waves, of the K-th largest lane maximum of a wave: the K lanes of that
+// wave whose maxima rank first hold K distinct values >= tau, so the part's
+// K-th value is >= tau and every value it keeps (and every value equal to the
+// K-th) is among the candidates {valid z >= tau}, typically K to 2K of them.
+// They are gathered in LDS and ranked (ties by index). Returns false, with
+// nothing written, when more than TK_CMAX values reach tau (rows of equal
+// values, or tau = -inf when a wave has fewer than K valid lanes); the caller
+// then runs block_topk.
+constexpr int TK_CMAX = 512;
+struct TopkSh {
+  float v[TK_CMAX];
+  int j[TK_CMAX];
+  __align__(16) float lm[NT];     // lane maxima, wave-major
+  float tau[4];
+  int scan[8];
+  int n;
+};
+
+// zz: the thread's 4 * NI values (-inf where !ok), element index of value q is
+// jb + 4 * NT * (q >> 2) + (q & 3) with jb = part base + 4 t.
+__device__ __forceinline__ bool topk_thresh(const float (&zz)[4 * NI], const bool (&ok)[NI], int jb, int K,
+                                            float* lst, TopkSh& S) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  float tm = -__builtin_inff();
+#pragma unroll
+  for (int q = 0; q < 4 * NI; ++q) tm = fmaxf(tm, zz[q]);
+  S.lm[t] = tm;
+  __syncthreads();
+  {
+    // rank of this lane's maximum within its wave (ties: lower lane first)
+    const float4* w4 = reinterpret_cast<const float4*>(S.lm + wave * 64);
+    int r = 0;
+#pragma unroll
+    for (int q4 = 0; q4 < 16; ++q4) {
+      const float4 o = w4[q4];
+      const float e[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int l2 = 4 * q4 + i;
+        r += (e[i] > tm || (e[i] == tm && l2 < lane)) ? 1 : 0;
+      }
+    }
+    if (r == K - 1) S.tau[wave] = tm;
+  }
+  __syncthreads();
+  const float tau = fmaxf(fmaxf(S.tau[0], S.tau[1]), fmaxf(S.tau[2], S.tau[3]));
+  int c = 0;
+#pragma unroll
+  for (int q = 0; q < 4 * NI; ++q) c += (ok[q >> 2] && zz[q] >= tau) ? 1 : 0;
+  int n;
+  int off = block_excl_scan(c, S.scan, &n);
+  if (n > TK_CMAX) return false;      // block-uniform
+#pragma unroll
+  for (int q = 0; q < 4 * NI; ++q)
+    if (ok[q >> 2] && zz[q] >= tau) {
+      S.v[off] = zz[q];
+      S.j[off] = jb + 4 * NT * (q >> 2) + (q & 3);
+      ++off;
+    }
+  if (t == 0) S.n = n;
+  __syncthreads();
+  for (int cc = t; cc < n; cc += NT) {
+    const float v = S.v[cc];
+    const int j = S.j[cc];
+    int r = 0;
+    for (int q = 0; q < n; ++q) {
+      const float v2 = S.v[q];
+      r += (v2 > v || (v2 == v && S.j[q] < j)) ? 1 : 0;
+    }
+    if (r < K) lst[r] = v;
+  }
+  if (t >= n && t < K) lst[t] = -__builtin_inff();   // fewer than K valid values
+  __syncthreads();
+  return true;
+}
+
 // ---------------------------------------------------------------- kernel 1: part statistics
 
 template <bool BF>
@@ -392,10 +470,58 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
     // this part's top_k largest z and the count of its values equal to the k-th
     __shared__ float lst[64];
     __shared__ __align__(16) float wl[4 * 64];
+    __shared__ TopkSh tks;
     const int K = a.top_k;
     float zz[4 * NI];
 #pragma unroll
     for (int q = 0; q < 4 * NI; ++q) zz[q] = ok[q >> 2] ? z[q >> 2][q & 3] : -__builtin_inff();
+    const bool thr = topk_thresh(zz, ok, base + 4 * t, K, lst, tks);
+    float* L = a.fws + (((long)step * (a.k + 1) + i) * a.P + p) * (K + 1);
+    const long crow = (long)step * (a.k + 1) + i;
+    if (thr) {
+      // every value equal to the K-th is a candidate: the tie count and the
+      // stored candidates come from the gathered values alone
+      const float vk = lst[K - 1];
+      const int n = tks.n;
+      int ceq = 0;
+      for (int cc = t; cc < n; cc += NT) ceq += tks.v[cc] == vk ? 1 : 0;
+      int neq_total;
+      block_excl_scan(ceq, tks.scan, &neq_total);
+      if (t < K) L[t] = lst[t];
+      if (t == 0) L[K] = (float)neq_total;
+      if (a.fast) {
+        __shared__ int c_gt2, c_eq2;
+        if (t == 0) {
+          c_gt2 = 0;
+          c_eq2 = 0;
+        }
+        __syncthreads();
+        int32_t* C = a.cand + (crow * a.P + p) * CAND_CAP;
+        float* Zc = a.cand_z + (crow * a.P + p) * CAND_CAP;
+        for (int cc = t; cc < n; cc += NT) {
+          const float zv = tks.v[cc];
+          if (zv > vk) {
+            const int q = atomicAdd(&c_gt2, 1);           // < K - 1 <= CAND_GT
+            C[q] = tks.j[cc];
+            Zc[q] = zv;
+          } else if (zv == vk) {
+            const int q = atomicAdd(&c_eq2, 1);
+            if (q < CAND_CAP - CAND_GT) {
+              C[CAND_GT + q] = tks.j[cc];
+              Zc[CAND_GT + q] = zv;
+            }
+          }
+        }
+        __syncthreads();
+        if (t == 0) {
+          a.ncand[(crow * a.P + p) * 2] = c_gt2;
+          a.ncand[(crow * a.P + p) * 2 + 1] = c_eq2;
+        }
+        if (p == 0 && row == 0)
+          for (int q = t; q < a.S; q += NT) a.ctr[q] = 0;
+      }
+      return;
+    }
     block_topk(zz, K, lst, wl);
     const float vk = lst[K - 1];
     float cnt = 0.0f;
@@ -406,7 +532,6 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
         for (int e = 0; e < 4; ++e) cnt += (z[it][e] == vk) ? 1.0f : 0.0f;
       }
     cnt = block_sum(cnt, red);
-    float* L = a.fws + (((long)step * (a.k + 1) + i) * a.P + p) * (K + 1);
     if (t < K) L[t] = lst[t];
     if (t == 0) L[K] = cnt;
     if (a.fast) {
