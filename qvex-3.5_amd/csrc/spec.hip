@@ -70,12 +70,14 @@ constexpr int NI = 8;   // float4 loads per thread per part
 // exp(x): Cody-Waite reduction x = n*ln2 + r with ln2 split in hi/lo parts,
 // degree-7 Taylor polynomial for e^r (|r| <= ln2/2) in Horner form with fmaf,
 // scaled by 2^n built in the exponent field. Returns 0 below -69 so every
-// product formed with it stays in the normal range.
+// product formed with it stays in the normal range. Branch-free: the
+// polynomial runs on the argument clamped to [-69, 88] (equal to x wherever its
+// value is used) and the out-of-range results are selected afterwards, so the
+// bits are those of the form that returns early (NaN gives 0 as there).
 __device__ __forceinline__ float qx_expf(float x) {
-  if (!(x >= -69.0f)) return 0.0f;
-  if (x > 88.0f) return __builtin_inff();
-  const float n = rintf(x * 1.44269504f);
-  float r = fmaf(n, -0.693145751953125f, x);
+  const float xc = fminf(fmaxf(x, -69.0f), 88.0f);
+  const float n = rintf(xc * 1.44269504f);
+  float r = fmaf(n, -0.693145751953125f, xc);
   r = fmaf(n, -1.428606765330187e-06f, r);
   float p = 1.0f / 5040.0f;
   p = fmaf(p, r, 1.0f / 720.0f);
@@ -86,7 +88,8 @@ __device__ __forceinline__ float qx_expf(float x) {
   p = fmaf(p, r, 1.0f);
   p = fmaf(p, r, 1.0f);
   const int e = (int)n;
-  return p * __uint_as_float((uint32_t)(e + 127) << 23);
+  const float v = p * __uint_as_float((uint32_t)(e + 127) << 23);
+  return x >= -69.0f ? (x > 88.0f ? __builtin_inff() : v) : 0.0f;
 }
 
 __device__ __forceinline__ float wave_bfly_sum(float v) {
@@ -301,8 +304,8 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
 // then runs block_topk.
 constexpr int TK_CMAX = 512;
 struct TopkSh {
-  float v[TK_CMAX];
-  int j[TK_CMAX];
+  __align__(16) float v[TK_CMAX];
+  __align__(16) int j[TK_CMAX];
   __align__(16) float lm[NT];     // lane maxima, wave-major
   float tau[4];
   int scan[8];
@@ -351,14 +354,26 @@ __device__ __forceinline__ bool topk_thresh(const float (&zz)[4 * NI], const boo
       ++off;
     }
   if (t == 0) S.n = n;
+  // pad to a multiple of 8 with entries that never rank ahead (-inf, last index)
+  if (t < 8 && n + t < TK_CMAX) {
+    S.v[n + t] = -__builtin_inff();
+    S.j[n + t] = 0x7fffffff;
+  }
   __syncthreads();
+  const int n8 = min((n + 7) & ~7, TK_CMAX);
   for (int cc = t; cc < n; cc += NT) {
     const float v = S.v[cc];
     const int j = S.j[cc];
     int r = 0;
-    for (int q = 0; q < n; ++q) {
-      const float v2 = S.v[q];
-      r += (v2 > v || (v2 == v && S.j[q] < j)) ? 1 : 0;
+    for (int q = 0; q < n8; q += 8) {     // eight entries per round of two 16-byte reads each
+      const float4 va = *reinterpret_cast<const float4*>(&S.v[q]);
+      const float4 vb = *reinterpret_cast<const float4*>(&S.v[q + 4]);
+      const int4 ja = *reinterpret_cast<const int4*>(&S.j[q]);
+      const int4 jb2 = *reinterpret_cast<const int4*>(&S.j[q + 4]);
+      const float vv[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+      const int jj[8] = {ja.x, ja.y, ja.z, ja.w, jb2.x, jb2.y, jb2.z, jb2.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r += (vv[e] > v || (vv[e] == v && jj[e] < j)) ? 1 : 0;
     }
     if (r < K) lst[r] = v;
   }
@@ -545,7 +560,6 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
         c_eq = 0;
       }
       __syncthreads();
-      const long crow = (long)step * (a.k + 1) + i;
       int32_t* C = a.cand + (crow * a.P + p) * CAND_CAP;
       float* Zc = a.cand_z + (crow * a.P + p) * CAND_CAP;
 #pragma unroll
