@@ -47,7 +47,8 @@ The other workloads run one kernel family in a loop for rocprofv3 counter
 passes (profiles/): gdn (chunked DeltaNet prefill), gdn_verify (the config-2
 recurrence), mixer (the cycle's split DeltaNet mixer at the 9B shape), attn
 (the verify attention's q/k norm + RoPE, partial and combine at a 4352-token
-context), spec (config 3).
+context), spec (config 3); readprobe prints the single-launch read ceiling by
+load path (VGPR against direct-to-LDS loads).
 """
 
 from __future__ import annotations
@@ -161,6 +162,37 @@ def read_ceiling_us(nbytes, blocks=2048, iters=200):
     del g, bufs
     torch.cuda.empty_cache()
     return best
+
+
+def read_probe_table(sizes_kib=(9216, 27648, 55296)):
+    """Single-launch read ceiling by load path: qvex_read_probe with VGPR loads
+    against gfx950's direct-to-LDS loads (global_load_lds_dwordx4), same access
+    pattern (every wave issues all its 1 KiB units before waiting), 2..16 units
+    per wave, 4 or 8 waves per block, beside qvex_read_roof's grid-stride read;
+    graphs of back-to-back launches over > 600 MB of copies. Sizes 9.4, 28.3 and
+    56.6 MB (the o_proj, config-0 and gate/up weight bytes, rounded to 128 KiB)."""
+    import torch
+    from qvex import kernels
+    dev = torch.device("cuda:0")
+    sink = torch.zeros(64, dtype=torch.int32, device=dev)
+    out = {}
+    for kib in sizes_kib:
+        nb = kib * 1024
+        copies = int(np.ceil(600e6 / nb)) + 1
+        bufs = [torch.empty(nb // 4, dtype=torch.int32, device=dev).fill_(i) for i in range(copies)]
+        res = {"grid_stride_2048": _graph_time(lambda i: kernels.read_roof(bufs[i % copies], sink, 2048), 200)}
+        for lds in (False, True):
+            for it in (2, 4, 8, 16):
+                for wpb in (4, 8):
+                    res[f"{'lds' if lds else 'vgpr'}_it{it}_w{wpb}"] = _graph_time(
+                        lambda i, it=it, lds=lds, wpb=wpb: kernels.read_probe(bufs[i % copies], sink, it, lds, wpb), 200)
+        best = {path: min(v for k, v in res.items() if k.startswith(path)) for path in ("vgpr", "lds", "grid")}
+        out[f"{nb / 1e6:.1f}MB"] = {"us": {k: round(v, 2) for k, v in res.items()},
+                                    "best_us": {k: round(v, 2) for k, v in best.items()},
+                                    "best_TB_s": {k: round(nb / v / 1e6, 2) for k, v in best.items()}}
+        del bufs
+        torch.cuda.empty_cache()
+    return out
 
 
 def read_roof_calibration(nbytes=28344320 // 16 * 16, copies=24, reps=3):
@@ -712,7 +744,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--workload", default="e2e", choices=["e2e", "qmv", "gdn", "gdn_verify", "mixer", "attn", "spec"])
+    ap.add_argument("--workload", default="e2e",
+                    choices=["e2e", "qmv", "gdn", "gdn_verify", "mixer", "attn", "spec", "readprobe"])
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--k", type=int, default=3)
     ap.add_argument("--temperature", type=float, default=0.7)
@@ -774,6 +807,14 @@ def main():
         r = single[args.workload]()
         line.update({"value": r["GB/s"], "unit": "GB/s", "ms_per_step": r["us"] / 1e3, args.workload: r,
                      "config": {"workload": r["kernel"]}})
+        print(json.dumps(line), flush=True)
+        return
+    if args.workload == "readprobe":
+        r = read_probe_table()
+        best = r["28.3MB"]["best_us"]
+        line.update({"value": round(28311552 / min(best.values()) / 1e3, 1), "unit": "GB/s",
+                     "ms_per_step": min(best.values()) / 1e3, "read_probe": r,
+                     "config": {"workload": "single-launch HBM read of 9.4 / 28.3 / 56.6 MB by load path"}})
         print(json.dumps(line), flush=True)
         return
     if args.workload == "gdn":

@@ -570,6 +570,15 @@ int qvex_mark_seen(float* seen, int V, const int32_t* ids, int max_ids, const in
 int qvex_read_roof(const void* buf, uint64_t bytes, uint32_t* sink, int blocks,
                    void* stream);
 
+/* Read-ceiling probe with a fixed access pattern and a choice of load path:
+ * waves of `waves_per_block` (4 or 8) each read `iters` (2, 4, 8 or 16) 1 KiB
+ * units, all issued before the first wait; lds = 1 lands them in LDS through
+ * global_load_lds_dwordx4, lds = 0 in VGPRs. bytes must be a multiple of
+ * 1 KiB * iters * waves_per_block. A measurement aid beside qvex_read_roof
+ * (experiments/native/qmv_spike.mm:21-32 measures its own read roof). */
+int qvex_read_probe(const void* buf, uint64_t bytes, uint32_t* sink, int iters, int lds,
+                    int waves_per_block, void* stream);
+
 /* Dense bf16 copy of an MLX 4-bit group-64 weight: out[n, k] =
  * bf16(s[n, k/64] * q[n, k] + b[n, k/64]) with the product and sum in fp32
  * (one rounding). The long (prefill) calls of QLinear (engine/model.py:87-91

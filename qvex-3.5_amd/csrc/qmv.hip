@@ -352,6 +352,41 @@ __global__ __launch_bounds__(256) void read_roof_kernel(const u32x4* __restrict_
   if (a == 0x9e3779b9u) sink[threadIdx.x & 63] = a;  // practically never taken
 }
 
+// Read-ceiling probe of one launch, two load paths with the same access
+// pattern: W waves each read ITERS 1 KiB units (unit u = wave + i * W, so the
+// waves of one step read adjacent KiB), every load issued before the first is
+// waited on; LDS = true lands the bytes in LDS with gfx950's
+// global_load_lds_dwordx4 (no VGPRs), LDS = false in VGPRs. The host sizes the
+// grid so that the buffer is exactly W * ITERS units.
+template <int ITERS, bool LDS, int WPB>
+__global__ __launch_bounds__(64 * WPB) void read_probe_kernel(const u32x4* __restrict__ buf,
+                                                              uint32_t* __restrict__ sink) {
+  __shared__ __align__(16) u32x4 ring[LDS ? WPB : 1][LDS ? ITERS : 1][64];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint64_t W = (uint64_t)gridDim.x * WPB;
+  const uint64_t gw = (uint64_t)blockIdx.x * WPB + w;
+  uint32_t a = 0;
+  if constexpr (LDS) {
+#pragma unroll
+    for (int i = 0; i < ITERS; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(buf + (gw + i * W) * 64 + lane),
+                                       (__attribute__((address_space(3))) void*)&ring[w][i][0], 16, 0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+    for (int i = 0; i < ITERS; ++i) {
+      const u32x4 v = ring[w][i][lane];
+      a ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+  } else {
+    u32x4 r[ITERS];
+#pragma unroll
+    for (int i = 0; i < ITERS; ++i) r[i] = load_nt16(buf + (gw + i * W) * 64 + lane);
+#pragma unroll
+    for (int i = 0; i < ITERS; ++i) a ^= r[i].x ^ r[i].y ^ r[i].z ^ r[i].w;
+  }
+  if (a == 0x9e3779b9u) sink[lane] = a;  // practically never taken
+}
+
 typedef void (*qmv_fn)(const uint16_t*, const uint32_t*, const uint16_t*, const uint16_t*,
                        uint16_t*, int, int);
 
@@ -527,6 +562,36 @@ extern "C" int qvex_qmv_w4g64_mfma(const uint16_t* x, const uint32_t* w, const u
                                    const uint16_t* biases, uint16_t* y, int M, int N, int K,
                                    int tiles_per_wave, int wave_ksplit, void* stream) {
   return launch_mfma(x, w, scales, biases, y, M, N, K, tiles_per_wave, wave_ksplit, (hipStream_t)stream);
+}
+
+template <int ITERS, bool LDS, int WPB>
+int launch_read_probe(const void* buf, uint64_t bytes, uint32_t* sink, hipStream_t stream) {
+  const uint64_t blocks = bytes / 1024 / ((uint64_t)ITERS * WPB);
+  hipLaunchKernelGGL((read_probe_kernel<ITERS, LDS, WPB>), dim3((unsigned)blocks), dim3(64 * WPB), 0, stream,
+                     reinterpret_cast<const u32x4*>(buf), sink);
+  QVEX_CHECK_LAUNCH("qvex_read_probe");
+  return QVEX_OK;
+}
+
+extern "C" int qvex_read_probe(const void* buf, uint64_t bytes, uint32_t* sink, int iters, int lds,
+                               int waves_per_block, void* stream) {
+  QVEX_CHECK_ARG(buf && sink && qvex_aligned(buf, 16), "qvex_read_probe: null or misaligned pointer");
+  QVEX_CHECK_ARG((iters == 2 || iters == 4 || iters == 8 || iters == 16) && (waves_per_block == 4 ||
+                 waves_per_block == 8) && (lds == 0 || lds == 1),
+                 "qvex_read_probe: iters=%d (2, 4, 8, 16), waves_per_block=%d (4, 8), lds=%d", iters, waves_per_block,
+                 lds);
+  const uint64_t unit = 1024ull * iters * waves_per_block;
+  QVEX_CHECK_ARG(bytes > 0 && bytes % unit == 0 && bytes / unit <= 0x7fffffffull,
+                 "qvex_read_probe: bytes=%llu must be a positive multiple of %llu", (unsigned long long)bytes,
+                 (unsigned long long)unit);
+  hipStream_t st = (hipStream_t)stream;
+#define QVEX_PROBE(I, Wp)                                                                        \
+  if (iters == I && waves_per_block == Wp)                                                       \
+    return lds ? launch_read_probe<I, true, Wp>(buf, bytes, sink, st) : launch_read_probe<I, false, Wp>(buf, bytes, sink, st);
+  QVEX_PROBE(2, 4) QVEX_PROBE(2, 8) QVEX_PROBE(4, 4) QVEX_PROBE(4, 8)
+  QVEX_PROBE(8, 4) QVEX_PROBE(8, 8) QVEX_PROBE(16, 4) QVEX_PROBE(16, 8)
+#undef QVEX_PROBE
+  return qvex::fail(QVEX_EINVAL, "qvex_read_probe: unreachable");
 }
 
 extern "C" int qvex_read_roof(const void* buf, uint64_t bytes, uint32_t* sink, int blocks, void* stream) {

@@ -22,6 +22,7 @@ SIGNATURES: dict[str, list] = {
     "qvex_qmv_w4g64": [P, P, P, P, P, I, I, I, P],
     "qvex_qmv_w4g64_tiled": [P, P, P, P, P, I, I, I, I, I, P],
     "qvex_read_roof": [P, U64, P, I, P],
+    "qvex_read_probe": [P, U64, P, I, I, I, P],
     "qvex_qmv_w4g64_mfma": [P, P, P, P, P, I, I, I, I, I, P],
     "qvex_qmv_affine": [P, P, P, P, P, I, I, I, I, I, P],
     "qvex_embed_affine": [P, I, P, P, P, I, I, I, I, P, P],

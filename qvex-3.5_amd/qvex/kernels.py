@@ -461,6 +461,13 @@ def read_roof(buf: torch.Tensor, sink: torch.Tensor, blocks: int = 4096) -> None
     _C.call("qvex_read_roof", _ptr(buf), nbytes, _ptr(sink), int(blocks), _stream())
 
 
+def read_probe(buf: torch.Tensor, sink: torch.Tensor, iters: int, lds: bool, waves_per_block: int = 4) -> None:
+    """Read every byte of buf with qvex_read_probe (VGPR or direct-to-LDS loads)."""
+    nbytes = buf.numel() * buf.element_size()
+    _C.call("qvex_read_probe", _ptr(buf), nbytes, _ptr(sink), int(iters), int(bool(lds)), int(waves_per_block),
+            _stream())
+
+
 # ---------------------------------------------------------------- Gated DeltaNet
 
 def _gdn_check(q, k, v, a, b, A_log, dt_bias):
