@@ -93,17 +93,28 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkArgs p) {
   const int t0 = c * CH;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, li = lane & 15, lg4 = lane >> 4;
 
-  __shared__ __align__(16) uint16_t Ks[CH * KS_LD];     // K row-major; reused for W
-  __shared__ __align__(16) uint16_t Qs[CH * KS_LD];
-  __shared__ __align__(16) uint16_t Kt[DD * KT_LD];     // K transposed [dk][t]
-  __shared__ __align__(16) uint16_t Vt[DD * KT_LD];     // V transposed [dv][t]
-  __shared__ __align__(16) float Am[CH * F_LD];
-  __shared__ __align__(16) float Tm[CH * F_LD];
-  __shared__ __align__(16) uint16_t Ps[CH * P_LD];
+  // LDS regions, each reused once its first tenant is dead, so that two blocks
+  // fit on a CU (75 KB): Q -> T (Q dies with the K K^T / Q K^T products), A -> V^T
+  // (A dies with the inverse; V waits in registers meanwhile); P goes straight
+  // to the workspace record
+  constexpr int SZ_KS = CH * KS_LD * 2, SZ_KT = DD * KT_LD * 2, SZ_F = CH * F_LD * 4;
+  constexpr int SZ_R4 = SZ_KT > SZ_F ? SZ_KT : SZ_F;
+  __shared__ __align__(16) unsigned char smem[SZ_KS + SZ_KT + SZ_KS + SZ_R4];
+  uint16_t* Ks = reinterpret_cast<uint16_t*>(smem);                       // K row-major; reused for W
+  uint16_t* Kt = reinterpret_cast<uint16_t*>(smem + SZ_KS);               // K transposed [dk][t]
+  uint16_t* Qs = reinterpret_cast<uint16_t*>(smem + SZ_KS + SZ_KT);       // Q row-major, then:
+  float* Tm = reinterpret_cast<float*>(smem + SZ_KS + SZ_KT);             //   T = (I + A)^{-1}
+  float* Am = reinterpret_cast<float*>(smem + 2 * SZ_KS + SZ_KT);         // A, then:
+  uint16_t* Vt = reinterpret_cast<uint16_t*>(smem + 2 * SZ_KS + SZ_KT);   //   V transposed [dv][t]
+  static_assert(SZ_KS == SZ_F, "Q and T share a region");
   __shared__ float lgs[CH], bet[CH], gam[CH];
   __shared__ float Xs[4][16 * 17];
+  uint8_t* rec = p.ws + (((long)bi * p.Hv + hv) * p.nchunk + c) * REC;
+  uint16_t* Pg = reinterpret_cast<uint16_t*>(rec + OFF_P);
 
-  // K, Q rows (row-major) and K, V transposed; tokens past T are zero
+  // K, Q rows (row-major) and K transposed; V kept in registers until its
+  // region is free; tokens past T are zero
+  u32x4 vreg[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int idx = tid + 256 * i;
@@ -116,16 +127,14 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkArgs p) {
       qv = load16(p.q + qk);
       vv = load16(p.v + (((long)bi * p.T + t) * p.Hv + hv) * DD + col);
     }
+    vreg[i] = vv;
     *reinterpret_cast<u32x4*>(&Ks[row * KS_LD + col]) = kv;
     *reinterpret_cast<u32x4*>(&Qs[row * KS_LD + col]) = qv;
     const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
-    const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       Kt[(col + 2 * e) * KT_LD + row] = (uint16_t)(kw[e] & 0xffffu);
       Kt[(col + 2 * e + 1) * KT_LD + row] = (uint16_t)(kw[e] >> 16);
-      Vt[(col + 2 * e) * KT_LD + row] = (uint16_t)(vw[e] & 0xffffu);
-      Vt[(col + 2 * e + 1) * KT_LD + row] = (uint16_t)(vw[e] >> 16);
     }
   }
   // gates, same formulas as the recurrent kernel; inclusive prefix sum of log g
@@ -148,7 +157,6 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkArgs p) {
     bet[lane] = be;
     gam[lane] = expf(lgv);
   }
-  for (int i = tid; i < CH * F_LD; i += 256) Tm[i] = 0.0f;
   __syncthreads();
 
   // A = beta_t e^{l_t-l_s} K K^T (s < t) and P = e^{l_t-l_s} Q K^T (s <= t); wave w = row tile
@@ -172,10 +180,12 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkArgs p) {
         const int t = 16 * rt + 4 * lg4 + r, s = 16 * ct + li;
         const float dA = (s <= t) ? expf(lgs[t] - lgs[s]) : 0.0f;
         Am[t * F_LD + s] = (s < t) ? bet[t] * dA * ckk[r] : 0.0f;
-        Ps[t * P_LD + s] = f32_to_bf16((s <= t) ? dA * cqk[r] : 0.0f);
+        Pg[t * CH + s] = f32_to_bf16((s <= t) ? dA * cqk[r] : 0.0f);
       }
     }
   }
+  __syncthreads();
+  for (int i = tid; i < CH * F_LD; i += 256) Tm[i] = 0.0f;     // Q is dead: its region becomes T
   __syncthreads();
 
   // T = (I + A)^{-1}: diagonal 16x16 blocks, wave w inverts block w (lane j = column j)
@@ -226,8 +236,21 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkArgs p) {
     __syncthreads();
   }
 
+  // A is dead: V transposed into its region
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid + 256 * i;
+    const int row = idx >> 4, col = (idx & 15) * 8;
+    const uint32_t vw[4] = {vreg[i].x, vreg[i].y, vreg[i].z, vreg[i].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      Vt[(col + 2 * e) * KT_LD + row] = (uint16_t)(vw[e] & 0xffffu);
+      Vt[(col + 2 * e + 1) * KT_LD + row] = (uint16_t)(vw[e] >> 16);
+    }
+  }
+  __syncthreads();
+
   // W = T diag(beta e^l) K -> Ks (row-major staging); U~ = T diag(beta) V -> workspace (accumulator order)
-  uint8_t* rec = p.ws + (((long)bi * p.Hv + hv) * p.nchunk + c) * REC;
   {
     const int rt = w;
     const int nks = rt >= 2 ? 2 : 1;     // T is lower triangular: token blocks past the row tile are zero
@@ -270,12 +293,6 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkArgs p) {
     const int idx = tid + 256 * i;
     const int row = idx >> 4, col = (idx & 15) * 8;
     *reinterpret_cast<u32x4*>(rec + OFF_W + (row * DD + col) * 2) = *reinterpret_cast<const u32x4*>(&Ks[row * KS_LD + col]);
-  }
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int idx = tid + 256 * i;
-    const int row = idx >> 3, col = (idx & 7) * 8;
-    *reinterpret_cast<u32x4*>(rec + OFF_P + (row * CH + col) * 2) = *reinterpret_cast<const u32x4*>(&Ps[row * P_LD + col]);
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
