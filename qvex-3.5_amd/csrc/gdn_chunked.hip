@@ -29,11 +29,16 @@
 // Results go to a workspace record per chunk in the layouts phase 2 reads.
 //
 // Phase 2, one block of NW waves per (value head, NW*16 state rows, batch):
-// each wave keeps its 16 x 128 slice of S in MFMA accumulators (fp32) for the
-// whole sequence. Per chunk the block stages W, Q, P, K^T and the gates in LDS
-// (the next chunk's copy is in flight during the current chunk's products).
-// The blocks of one head are consecutive in x, so with round-robin dispatch they
-// share an XCD and its L2.
+// each wave keeps its 16 x 128 slice of S, transposed, in MFMA accumulators
+// (fp32) for the whole sequence. Kept transposed, the state and U leave the
+// accumulators as B operands without a trip through LDS: a pair of 16-row
+// accumulator tiles is a k = 32 operand once both sides agree on the order of
+// k, and phase 1 writes W, P and K^T in that order (fragment order, below).
+// Per chunk the block stages W, Q, P, K^T and the gates in LDS, double-buffered
+// (the next chunk's copy is staged after the current chunk's products, its
+// loads in flight during them), one barrier per chunk. The blocks of one head
+// are Hv apart in the linear block order, so with round-robin dispatch over 8
+// XCDs (Hv a multiple of 8) they share an XCD and its L2.
 //
 // Operands are bf16 (the state is rounded to bf16 where it enters a product);
 // accumulation and the state itself stay fp32.
@@ -50,12 +55,12 @@ constexpr int F_LD = CH + 4;           // fp32 row stride of [64][64] matrices
 constexpr int P_LD = CH + 8;           // bf16 row stride of [64][64]
 
 // workspace record per (batch, head, chunk)
-constexpr long OFF_W = 0;              // bf16 [64][128], W row-major
+constexpr long OFF_W = 0;              // bf16 [64][128], W in fragment order
 constexpr long OFF_U = 16384;          // fp32 [4 row tiles][8 col tiles][64 lanes][4], U~ in accumulator order
-constexpr long OFF_P = 49152;          // bf16 [64][64], P row-major
-constexpr long OFF_KT = 57344;         // bf16 [128][64], K transposed
-constexpr long OFF_LG = 73728;         // fp32 [64], inclusive chunk-local log decay
-constexpr long REC = 73984;
+constexpr long OFF_P = 49152;          // bf16 [64][64], P in fragment order
+constexpr long OFF_KT = 57344;         // bf16 [128][64], K transposed, in fragment order
+constexpr long OFF_G = 73728;          // fp32 [2][64]: e^{l_t}, then e^{l_C - l_t}
+constexpr long REC = 74240;
 
 struct ChunkArgs {
   const uint16_t* q;
@@ -83,6 +88,29 @@ __device__ __forceinline__ bf16x8_t pack8(const float* v) {
 
 __device__ __forceinline__ f32x4_t mfma(bf16x8_t a, bf16x8_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// two floats to packed bf16, round to nearest even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+}
+
+// An accumulator tile pair (tiles 2m and 2m + 1 of 16 rows; lane li + 16 g
+// holds rows 4g + r of each) as the B operand of a k = 32 product, k running
+// over the pair's 32 rows in the order 4g + 0..3, 16 + 4g + 0..3.
+__device__ __forceinline__ bf16x8_t pair_operand(f32x4_t lo, f32x4_t hi) {
+  return as_bf16x8(cvt_pk(lo[0], lo[1]), cvt_pk(lo[2], lo[3]), cvt_pk(hi[0], hi[1]), cvt_pk(hi[2], hi[3]));
+}
+
+// Fragment order of a bf16 [R][K] matrix (K a multiple of 32) as the A operand
+// of those products: [R/16 row tiles][K/32 k groups][64 lanes][8], lane
+// li + 16 g holding row 16 rt + li and, of its k group, columns 4g + 0..3 then
+// 16 + 4g + 0..3 - the k order of pair_operand. Element offset of (row, k):
+__device__ __forceinline__ int frag_off(int row, int k, int nkg) {
+  const int j = k & 31;
+  return ((((row >> 4) * nkg + (k >> 5)) * 64 + (row & 15) + 16 * ((j >> 2) & 3)) << 3) + ((j >> 4) << 2) + (j & 3);
 }
 
 // ------------------------------------------------------------------ phase 1
@@ -180,7 +208,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkArgs p) {
         const int t = 16 * rt + 4 * lg4 + r, s = 16 * ct + li;
         const float dA = (s <= t) ? expf(lgs[t] - lgs[s]) : 0.0f;
         Am[t * F_LD + s] = (s < t) ? bet[t] * dA * ckk[r] : 0.0f;
-        Pg[t * CH + s] = f32_to_bf16((s <= t) ? dA * cqk[r] : 0.0f);
+        Pg[frag_off(t, s, CH / 32)] = f32_to_bf16((s <= t) ? dA * cqk[r] : 0.0f);
       }
     }
   }
@@ -288,19 +316,27 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkArgs p) {
     }
   }
   __syncthreads();
+  // W [64][128] and K^T [128][64] to the record in fragment order: 16-byte piece
+  // idx is lane idx % 64 of fragment idx / 64, gathered from two 8-byte runs
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int idx = tid + 256 * i;
-    const int row = idx >> 4, col = (idx & 15) * 8;
-    *reinterpret_cast<u32x4*>(rec + OFF_W + (row * DD + col) * 2) = *reinterpret_cast<const u32x4*>(&Ks[row * KS_LD + col]);
+    const int idx = tid + 256 * i, f = idx >> 6, fl = idx & 63;
+    const uint16_t* src = &Ks[(16 * (f >> 2) + (fl & 15)) * KS_LD + 32 * (f & 3) + 4 * (fl >> 4)];
+    const u32x2 lo = *reinterpret_cast<const u32x2*>(src), hi = *reinterpret_cast<const u32x2*>(src + 16);
+    *reinterpret_cast<u32x4*>(rec + OFF_W + (long)idx * 16) = u32x4{lo.x, lo.y, hi.x, hi.y};
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int idx = tid + 256 * i;
-    const int row = idx >> 3, col = (idx & 7) * 8;
-    *reinterpret_cast<u32x4*>(rec + OFF_KT + (row * CH + col) * 2) = *reinterpret_cast<const u32x4*>(&Kt[row * KT_LD + col]);
+    const int idx = tid + 256 * i, f = idx >> 6, fl = idx & 63;
+    const uint16_t* src = &Kt[(16 * (f >> 1) + (fl & 15)) * KT_LD + 32 * (f & 1) + 4 * (fl >> 4)];
+    const u32x2 lo = *reinterpret_cast<const u32x2*>(src), hi = *reinterpret_cast<const u32x2*>(src + 16);
+    *reinterpret_cast<u32x4*>(rec + OFF_KT + (long)idx * 16) = u32x4{lo.x, lo.y, hi.x, hi.y};
   }
-  if (tid < CH) reinterpret_cast<float*>(rec + OFF_LG)[tid] = lgs[tid];
+  if (tid < CH) {
+    float* g = reinterpret_cast<float*>(rec + OFF_G);
+    g[tid] = gam[tid];
+    g[CH + tid] = expf(lgs[CH - 1] - lgs[tid]);
+  }
 }
 
 // ------------------------------------------------------------------ phase 2
@@ -308,35 +344,37 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(ChunkArgs p) {
 template <int NW>
 __global__ __launch_bounds__(64 * NW) void gdn_chunk_scan_kernel(ChunkArgs p) {
   constexpr int NT = 64 * NW;
-  constexpr int NR = 1024 / NT;          // 16-byte chunks per thread of a [64][128] or [128][64] bf16 tile
-  constexpr int NP = 512 / NT;           // ... of the [64][64] P tile
+  constexpr int NR = 1024 / NT;          // 16-byte pieces per thread of a 16 KB tile
+  constexpr int NP = 512 / NT;           // ... of the 8 KB P tile
   const int hv = blockIdx.x, slice = blockIdx.y, bi = blockIdx.z;
   const int hk = hv / (p.Hv / p.Hk);
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, li = lane & 15, lg4 = lane >> 4;
-  const int dvt = slice * NW + w;        // this wave's 16-row tile of the state
+  const int dvt = slice * NW + w;        // this wave's 16 columns of the state
   const int dv0 = 16 * dvt;
 
-  __shared__ __align__(16) uint16_t Ws[CH * KS_LD];
-  __shared__ __align__(16) uint16_t Qs[CH * KS_LD];
-  __shared__ __align__(16) uint16_t Ps[CH * P_LD];
-  __shared__ __align__(16) uint16_t Kts[DD * KT_LD];
-  __shared__ float gam[CH], dec[CH];
-  __shared__ __align__(16) uint16_t Sb[NW][16 * KS_LD];
-  __shared__ __align__(16) uint16_t Ub[NW][16 * KT_LD];
-  __shared__ __align__(16) uint16_t DUb[NW][16 * KT_LD];
+  // operand tiles in fragment order, double-buffered: chunk c + 1 is staged
+  // while chunk c's products read the other buffer
+  __shared__ __align__(16) uint16_t Wf[2][CH * DD];
+  __shared__ __align__(16) uint16_t Qf[2][CH * DD];
+  __shared__ __align__(16) uint16_t Kf[2][DD * CH];
+  __shared__ __align__(16) uint16_t Pf[2][CH * CH];
+  __shared__ __align__(16) float gam[2][CH];
+  __shared__ __align__(16) float dec[2][CH];
 
-  // state slice S[dv0 + 4*lg4 + r][16*ct + li] in accumulator layout
-  const long s_base = (((long)bi * p.Hv + hv) * DD + dv0) * DD;
+  // the state slice, transposed, in accumulator layout: tile ct, lane li + 16 g,
+  // element r holds S[dv0 + li][16 ct + 4 g + r], so that tile pairs are the
+  // B operand of W S^T and Q S^T as they stand
+  const long s_base = (((long)bi * p.Hv + hv) * DD + dv0 + li) * DD + 4 * lg4;
   f32x4_t S[8];
 #pragma unroll
   for (int ct = 0; ct < 8; ++ct)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) S[ct][r] = p.s_in[s_base + (long)(4 * lg4 + r) * DD + 16 * ct + li];
+    for (int r = 0; r < 4; ++r) S[ct][r] = p.s_in[s_base + 16 * ct + r];
 
   const uint8_t* rec0 = p.ws + ((long)bi * p.Hv + hv) * p.nchunk * REC;
   u32x4 rW[NR], rQ[NR], rK[NR], rP[NP];
   f32x4_t rU[4];
-  float rL = 0.0f;
+  float rG = 0.0f, rD = 0.0f;
 
   auto fetch = [&](int c) {
     const uint8_t* rec = rec0 + (long)c * REC;
@@ -345,117 +383,164 @@ __global__ __launch_bounds__(64 * NW) void gdn_chunk_scan_kernel(ChunkArgs p) {
       const int idx = tid + NT * i;
       rW[i] = load16(rec + OFF_W + (long)idx * 16);
       rK[i] = load16(rec + OFF_KT + (long)idx * 16);
-      const int row = idx >> 4, col = (idx & 15) * 8;
-      const int t = c * CH + row;
-      rQ[i] = t < p.T ? load16(p.q + (((long)bi * p.T + t) * p.Hk + hk) * DD + col) : u32x4{0u, 0u, 0u, 0u};
+      // rows past T repeat row T - 1 (in bounds, no branch): they only reach
+      // output rows that are never stored
+      const int t = min(c * CH + (idx >> 4), p.T - 1);
+      rQ[i] = load16(p.q + (((long)bi * p.T + t) * p.Hk + hk) * DD + (idx & 15) * 8);
     }
 #pragma unroll
     for (int i = 0; i < NP; ++i) rP[i] = load16(rec + OFF_P + (long)(tid + NT * i) * 16);
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
       rU[rt] = *reinterpret_cast<const f32x4_t*>(rec + OFF_U + ((long)(rt * 8 + dvt) * 64 + lane) * 16);
-    if (tid < CH) rL = reinterpret_cast<const float*>(rec + OFF_LG)[tid];
+    if (tid < CH) {
+      rG = reinterpret_cast<const float*>(rec + OFF_G)[tid];
+      rD = reinterpret_cast<const float*>(rec + OFF_G)[CH + tid];
+    }
   };
-  auto stage = [&]() {
+  auto stage = [&](int b) {
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
       const int idx = tid + NT * i;
-      const int row = idx >> 4, col = (idx & 15) * 8;           // [64][128] tiles
-      *reinterpret_cast<u32x4*>(&Ws[row * KS_LD + col]) = rW[i];
-      *reinterpret_cast<u32x4*>(&Qs[row * KS_LD + col]) = rQ[i];
-      const int krow = idx >> 3, kcol = (idx & 7) * 8;          // [128][64] tile
-      *reinterpret_cast<u32x4*>(&Kts[krow * KT_LD + kcol]) = rK[i];
+      *reinterpret_cast<u32x4*>(&Wf[b][idx * 8]) = rW[i];
+      *reinterpret_cast<u32x4*>(&Kf[b][idx * 8]) = rK[i];
+      const int row = idx >> 4, col = (idx & 15) * 8;   // Q arrives row-major
+      *reinterpret_cast<u32x2*>(&Qf[b][frag_off(row, col, DD / 32)]) = u32x2{rQ[i].x, rQ[i].y};
+      *reinterpret_cast<u32x2*>(&Qf[b][frag_off(row, col + 4, DD / 32)]) = u32x2{rQ[i].z, rQ[i].w};
     }
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      const int idx = tid + NT * i;
-      const int row = idx >> 3, col = (idx & 7) * 8;
-      *reinterpret_cast<u32x4*>(&Ps[row * P_LD + col]) = rP[i];
-    }
+    for (int i = 0; i < NP; ++i) *reinterpret_cast<u32x4*>(&Pf[b][(tid + NT * i) * 8]) = rP[i];
     if (tid < CH) {                  // wave 0: chunk-local decay factors
-      const float lC = __shfl(rL, CH - 1, 64);
-      gam[tid] = expf(rL);
-      dec[tid] = expf(lC - rL);
+      gam[b][tid] = rG;
+      dec[b][tid] = rD;
     }
   };
 
   fetch(0);
+  stage(0);
+  f32x4_t U0[4] = {rU[0], rU[1], rU[2], rU[3]};
+  if (p.nchunk > 1) fetch(1);
+  __syncthreads();
   for (int c = 0; c < p.nchunk; ++c) {
-    __syncthreads();                     // every wave is done with the previous chunk's tiles
-    stage();
-    const f32x4_t U0[4] = {rU[0], rU[1], rU[2], rU[3]};
-    __syncthreads();
-    if (c + 1 < p.nchunk) fetch(c + 1);  // next chunk's loads overlap this chunk's products
+    const int b = c & 1;
+    const uint16_t* Wb = Wf[b] + lane * 8;
+    const uint16_t* Qb = Qf[b] + lane * 8;
+    const uint16_t* Kb = Kf[b] + lane * 8;
+    const uint16_t* Pb = Pf[b] + lane * 8;
 
-    // S (bf16) in B-operand layout: Sb[dv][dk]
-    uint16_t* sb = Sb[w];
+    // Operand fragments are read from LDS one step ahead of the products that
+    // use them (fa / fb alternate; sched_barrier keeps the compiler from sinking
+    // each read next to its product, which would expose every LDS latency).
+    bf16x8_t fa[8], fb[8];
 #pragma unroll
-    for (int ct = 0; ct < 8; ++ct)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sb[(4 * lg4 + r) * KS_LD + 16 * ct + li] = f32_to_bf16(S[ct][r]);
+    for (int ks = 0; ks < 4; ++ks) {
+      fa[ks] = lds8(Wb + ks * 512);
+      fa[4 + ks] = lds8(Qb + ks * 512);
+    }
     bf16x8_t bS[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) bS[ks] = lds8(&sb[li * KS_LD + 32 * ks + 8 * lg4]);
+    for (int ks = 0; ks < 4; ++ks) bS[ks] = pair_operand(S[2 * ks], S[2 * ks + 1]);
+    const float gC = gam[b][CH - 1];
+    f32x4_t d4[4];                       // e^{l_C - l_t} for this lane's tokens, by row tile
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) d4[rt] = *reinterpret_cast<const f32x4_t*>(&dec[b][16 * rt + 4 * lg4]);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // U = U~ - W S^T ;  Y = e^l (Q S^T)
+    // U = U~ - W S^T ;  Y = e^l (Q S^T); the state is scaled by e^{l_C} meanwhile
     f32x4_t U[4], Y[4];
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
+      bf16x8_t* cur = (rt & 1) ? fb : fa;
+      bf16x8_t* nxt = (rt & 1) ? fa : fb;
+      // the decay row first: LDS reads complete in order, so a read queued
+      // behind the prefetch would wait for all of it
+      const f32x4_t g4 = *reinterpret_cast<const f32x4_t*>(&gam[b][16 * rt + 4 * lg4]);
+      if (rt < 3) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          nxt[ks] = lds8(Wb + ((rt + 1) * 4 + ks) * 512);
+          nxt[4 + ks] = lds8(Qb + ((rt + 1) * 4 + ks) * 512);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) nxt[j] = lds8(Kb + j * 512);     // K^T, state tiles 0..3
+      }
       f32x4_t cw = {0.0f, 0.0f, 0.0f, 0.0f}, cq = cw;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        cw = mfma(lds8(&Ws[(16 * rt + li) * KS_LD + 32 * ks + 8 * lg4]), bS[ks], cw);
-        cq = mfma(lds8(&Qs[(16 * rt + li) * KS_LD + 32 * ks + 8 * lg4]), bS[ks], cq);
+        cw = mfma(cur[ks], bS[ks], cw);
+        cq = mfma(cur[4 + ks], bS[ks], cq);
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = 16 * rt + 4 * lg4 + r;
-        U[rt][r] = U0[rt][r] - cw[r];
-        Y[rt][r] = gam[t] * cq[r];
+      for (int ct = 2 * rt; ct < 2 * rt + 2; ++ct) S[ct] *= gC;
+      U[rt] = U0[rt] - cw;
+      Y[rt] = g4 * cq;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // U and diag(e^{l_C - l_t}) U as B operands over tokens
+    bf16x8_t bU[2], bD[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bU[ks] = pair_operand(U[2 * ks], U[2 * ks + 1]);
+      bD[ks] = pair_operand(U[2 * ks] * d4[2 * ks], U[2 * ks + 1] * d4[2 * ks + 1]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) fb[j] = lds8(Kb + (8 + j) * 512);         // K^T, state tiles 4..7
+    __builtin_amdgcn_sched_barrier(0);
+
+    // S^T = e^{l_C} S^T + K^T (D U)
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) S[ct] = mfma(fa[2 * ct + ks], bD[ks], S[ct]);
+    // P fragments (row tile, token group): (0,0) (1,0) (2,0) (2,1) (3,0) (3,1)
+    fa[0] = lds8(Pb + 0 * 512);
+    fa[1] = lds8(Pb + 2 * 512);
+#pragma unroll
+    for (int j = 2; j < 6; ++j) fa[j] = lds8(Pb + (j + 2) * 512);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ct = 4; ct < 8; ++ct)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) S[ct] = mfma(fb[2 * (ct - 4) + ks], bD[ks], S[ct]);
+
+    // Y += P U (P lower triangular: no token group 1 for the first two row tiles)
+    Y[0] = mfma(fa[0], bU[0], Y[0]);
+    Y[1] = mfma(fa[1], bU[0], Y[1]);
+    Y[2] = mfma(fa[3], bU[1], mfma(fa[2], bU[0], Y[2]));
+    Y[3] = mfma(fa[5], bU[1], mfma(fa[4], bU[0], Y[3]));
+    // Next chunk's tiles to the other buffer (its last readers finished before
+    // the previous barrier), then this chunk's outputs, then the loads two
+    // chunks ahead: the stage's wait for its loads (issued one chunk earlier)
+    // then never includes the stores, which count in the same in-order counter.
+    if (c + 1 < p.nchunk) {
+      stage(b ^ 1);
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) U0[rt] = rU[rt];
+    }
+    const bool full = (c + 1) * CH <= p.T;
+    uint16_t* yp = p.y + (((long)bi * p.T + c * CH + 4 * lg4) * p.Hv + hv) * DD + dv0 + li;
+    const long ystep = (long)p.Hv * DD;
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      const uint32_t y01 = cvt_pk(Y[rt][0], Y[rt][1]), y23 = cvt_pk(Y[rt][2], Y[rt][3]);
+      const uint16_t yv[4] = {(uint16_t)y01, (uint16_t)(y01 >> 16), (uint16_t)y23, (uint16_t)(y23 >> 16)};
+      if (full) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) yp[(16 * rt + r) * ystep] = yv[r];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (c * CH + 16 * rt + 4 * lg4 + r < p.T) yp[(16 * rt + r) * ystep] = yv[r];
       }
     }
-    // U^T and (diag(e^{l_C - l_t}) U)^T in bf16: Ub[dv][t]
-    uint16_t* ub = Ub[w];
-    uint16_t* dub = DUb[w];
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = 16 * rt + 4 * lg4 + r;
-        ub[li * KT_LD + t] = f32_to_bf16(U[rt][r]);
-        dub[li * KT_LD + t] = f32_to_bf16(U[rt][r] * dec[t]);
-      }
-    // Y += P U (P lower triangular: skip the zero token block of the first two row tiles)
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        if (ks == 0 || rt >= 2)
-          Y[rt] = mfma(lds8(&Ps[(16 * rt + li) * P_LD + 32 * ks + 8 * lg4]), lds8(&ub[li * KT_LD + 32 * ks + 8 * lg4]), Y[rt]);
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = c * CH + 16 * rt + 4 * lg4 + r;
-        if (t < p.T) p.y[(((long)bi * p.T + t) * p.Hv + hv) * DD + dv0 + li] = f32_to_bf16(Y[rt][r]);
-      }
-    // S = e^{l_C} S + (D U)^T K
-    const float gC = gam[CH - 1];
-    bf16x8_t aDU[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) aDU[ks] = lds8(&dub[li * KT_LD + 32 * ks + 8 * lg4]);
-#pragma unroll
-    for (int ct = 0; ct < 8; ++ct) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) S[ct][r] *= gC;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) S[ct] = mfma(aDU[ks], lds8(&Kts[(16 * ct + li) * KT_LD + 32 * ks + 8 * lg4]), S[ct]);
-    }
+    if (c + 2 < p.nchunk) fetch(c + 2);
+    __syncthreads();
   }
 #pragma unroll
   for (int ct = 0; ct < 8; ++ct)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) p.s_out[s_base + (long)(4 * lg4 + r) * DD + 16 * ct + li] = S[ct][r];
+    for (int r = 0; r < 4; ++r) p.s_out[s_base + 16 * ct + r] = S[ct][r];
 }
 
 constexpr int SCAN_NW = 4;
