@@ -235,6 +235,12 @@ __device__ __forceinline__ void next_buf(const float (&v)[NS], float lv, int li,
   }
 }
 
+// 1 when value e ranks ahead of v (greater, or equal and `first`), as plain bit
+// operations: the short-circuit form compiles to a branch per comparison.
+__device__ __forceinline__ int ahead(float e, float v, bool first) {
+  return (int)(e > v) | ((int)(e == v) & (int)first);
+}
+
 // The K largest of the block's values (with multiplicity) into lst[0..K-1],
 // descending; v holds the calling thread's NS values, -inf for none. Each wave
 // extracts its own K largest, one wave maximum per round (ties: lowest lane),
@@ -280,7 +286,7 @@ __device__ __forceinline__ void block_topk(const float (&v)[NS], int K, float* l
         const float e[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          rank += (4 * j4 + i < K && (e[i] > x || (w2 < w && e[i] == x))) ? 1 : 0;
+          rank += (int)(4 * j4 + i < K) & ahead(e[i], x, w2 < w);
       }
     }
     if (rank < K) lst[rank] = x;
@@ -293,15 +299,17 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
 }
 
 // Threshold selection of a part's K largest values (K <= 64), the same multiset
-// block_topk gives, without its K serial rounds. tau = the largest, over the
-// four waves, of the K-th largest lane maximum of a wave: the K lanes of that
-// wave whose maxima rank first hold K distinct values >= tau, so the part's
-// K-th value is >= tau and every value it keeps (and every value equal to the
-// K-th) is among the candidates {valid z >= tau}, typically K to 2K of them.
-// They are gathered in LDS and ranked (ties by index). Returns false, with
-// nothing written, when more than TK_CMAX values reach tau (rows of equal
-// values, or tau = -inf when a wave has fewer than K valid lanes); the caller
-// then runs block_topk.
+// block_topk gives, without its K serial rounds. tau = the K-th largest of the
+// block's 256 lane maxima (ties by lane): the K lanes whose maxima rank first
+// hold K distinct values >= tau, so the part's K-th value is >= tau and every
+// value it keeps (and every value equal to the K-th) is among the candidates
+// {valid z >= tau} - about K of them for a row of random logits (a lane holds
+// 32 of the part's values). tau comes from each wave's K largest lane maxima
+// (ranked within the wave), ranked again across the 4K of them. The candidates
+// are gathered in LDS and ranked (ties by index). Returns false, with nothing
+// written, when more than TK_CMAX values reach tau (rows of equal values, or
+// tau = -inf when fewer than K lanes hold a valid value); the caller then runs
+// block_topk.
 constexpr int TK_CMAX = 512;
 struct TopkSh {
   __align__(16) float v[TK_CMAX];
@@ -333,16 +341,29 @@ __device__ __forceinline__ bool topk_thresh(const float (&zz)[4 * NI], const boo
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int l2 = 4 * q4 + i;
-        r += (e[i] > tm || (e[i] == tm && l2 < lane)) ? 1 : 0;
+        r += ahead(e[i], tm, l2 < lane);
       }
     }
-    if (r == K - 1) S.tau[wave] = tm;
+    if (r < K) S.v[wave * K + r] = tm;    // the wave's K largest lane maxima
   }
   __syncthreads();
-  const float tau = fmaxf(fmaxf(S.tau[0], S.tau[1]), fmaxf(S.tau[2], S.tau[3]));
+  if (t < 4 * K) {                      // the K-th largest of the 4K (ties by slot)
+    const float v = S.v[t];
+    int r = 0;
+#pragma unroll 4
+    for (int q = 0; q < 4 * K; q += 4) {
+      const float4 o = *reinterpret_cast<const float4*>(&S.v[q]);
+      const float e[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r += ahead(e[i], v, q + i < t);
+    }
+    if (r == K - 1) S.tau[0] = v;
+  }
+  __syncthreads();
+  const float tau = S.tau[0];
   int c = 0;
 #pragma unroll
-  for (int q = 0; q < 4 * NI; ++q) c += (ok[q >> 2] && zz[q] >= tau) ? 1 : 0;
+  for (int q = 0; q < 4 * NI; ++q) c += (int)ok[q >> 2] & (int)(zz[q] >= tau);
   int n;
   int off = block_excl_scan(c, S.scan, &n);
   if (n > TK_CMAX) return false;      // block-uniform
@@ -365,6 +386,7 @@ __device__ __forceinline__ bool topk_thresh(const float (&zz)[4 * NI], const boo
     const float v = S.v[cc];
     const int j = S.j[cc];
     int r = 0;
+#pragma unroll 2
     for (int q = 0; q < n8; q += 8) {     // eight entries per round of two 16-byte reads each
       const float4 va = *reinterpret_cast<const float4*>(&S.v[q]);
       const float4 vb = *reinterpret_cast<const float4*>(&S.v[q + 4]);
@@ -373,7 +395,7 @@ __device__ __forceinline__ bool topk_thresh(const float (&zz)[4 * NI], const boo
       const float vv[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
       const int jj[8] = {ja.x, ja.y, ja.z, ja.w, jb2.x, jb2.y, jb2.z, jb2.w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) r += (vv[e] > v || (vv[e] == v && jj[e] < j)) ? 1 : 0;
+      for (int e = 0; e < 8; ++e) r += ahead(vv[e], v, jj[e] < j);
     }
     if (r < K) lst[r] = v;
   }
@@ -461,25 +483,30 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
   for (int it = 0; it < NI; ++it)
 #pragma unroll
     for (int e = 0; e < 4; ++e) z[it][e] = x[it][e] * a.inv_temp;
-  float m = -__builtin_inff();
+  // (m_p, S_p) of the part, which the unfiltered rules combine; the list form
+  // without draft logits (the finish kernel) takes (c_0, S_p, cutoff) from the
+  // lists alone, so its target rows skip the exponentials
+  if (!(a.fast && tgt && a.filt == 1)) {
+    float m = -__builtin_inff();
 #pragma unroll
-  for (int it = 0; it < NI; ++it)
-    if (ok[it]) {
+    for (int it = 0; it < NI; ++it)
+      if (ok[it]) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) m = fmaxf(m, z[it][e]);
+        for (int e = 0; e < 4; ++e) m = fmaxf(m, z[it][e]);
+      }
+    m = block_max(m, red);
+    float acc = 0.0f;
+#pragma unroll
+    for (int it = 0; it < NI; ++it)
+      if (ok[it]) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = acc + qx_expf(z[it][e] - m);
+      }
+    const float s = block_sum(acc, red);
+    if (t == 0) {
+      out[0] = m;
+      out[1] = s;
     }
-  m = block_max(m, red);
-  float acc = 0.0f;
-#pragma unroll
-  for (int it = 0; it < NI; ++it)
-    if (ok[it]) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc = acc + qx_expf(z[it][e] - m);
-    }
-  const float s = block_sum(acc, red);
-  if (t == 0) {
-    out[0] = m;
-    out[1] = s;
   }
   if (tgt && a.filt == 1) {
     // this part's top_k largest z and the count of its values equal to the k-th
