@@ -541,12 +541,16 @@ int qvex_cycle_finish(const int32_t* drafts, int k, const int32_t* n_accept, con
  * steps' net advance), and u_out[0:u_width) = the uniforms of draw event
  * *u_counter under u_seed (as qvex_philox_uniforms), then *u_counter += 1 (the
  * next cycle's uniforms). Null pointers skip a part; every read happens before
- * any write, so drafts may alias ids_next + 1. */
+ * any write, so drafts may alias ids_next + 1. done (optional, one int32, may
+ * be pinned host memory): set to 1 after every entry of `out` is visible
+ * system-wide, so a host that zeroes it before the launch and polls it reads
+ * the cycle's result without a stream synchronisation (the reference's one
+ * read per cycle, engine/speculative.py:82-85). */
 int qvex_cycle_finish_ex(const int32_t* drafts, int k, const int32_t* n_accept, const int32_t* token,
                          int32_t* pend_ids, int32_t* feed, int32_t* n_prev, int32_t* out,
                          int32_t* ids_next, int32_t* main_counters, int n_main, int main_extra,
                          int32_t* mtp_counters, int n_mtp, int mtp_delta, uint64_t u_seed,
-                         uint64_t* u_counter, int u_width, float* u_out, void* stream);
+                         uint64_t* u_counter, int u_width, float* u_out, int32_t* done, void* stream);
 
 /* The sampler's uniforms (the draws of engine/speculative.py:79-81 and
  * Sampler.pick's categorical, engine/sampler.py:57-58, which use MLX's

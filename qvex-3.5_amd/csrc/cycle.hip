@@ -84,7 +84,10 @@ __global__ void cycle_finish_kernel(const int32_t* __restrict__ drafts, int k, c
 // ids_next[0] = tok (the next verify's first id), main_counters[i] += n + main_extra
 // (the verify commit), mtp_counters[i] += mtp_delta (the draft steps' net
 // advance), and u_out[i] = u(*u_counter, i), ++*u_counter (the next cycle's
-// uniforms). Null pointers skip a part.
+// uniforms). Null pointers skip a part. Thread 0 writes all of `out`; with
+// `done` it then makes those writes visible system-wide (a system-scope fence)
+// and stores *done = 1, so a host that clears *done in pinned memory before the
+// launch and polls it reads a complete result without a stream synchronisation.
 __global__ void cycle_finish_ex_kernel(const int32_t* __restrict__ drafts, int k, const int32_t* __restrict__ n_ptr,
                                        const int32_t* __restrict__ tok_ptr, int32_t* __restrict__ pend_ids,
                                        int32_t* __restrict__ feed, int32_t* __restrict__ n_prev,
@@ -92,15 +95,16 @@ __global__ void cycle_finish_ex_kernel(const int32_t* __restrict__ drafts, int k
                                        int32_t* __restrict__ main_counters, int n_main, int main_extra,
                                        int32_t* __restrict__ mtp_counters, int n_mtp, int mtp_delta,
                                        uint64_t u_seed, uint64_t* __restrict__ u_counter, int width,
-                                       float* __restrict__ u_out) {
+                                       float* __restrict__ u_out, int32_t* __restrict__ done) {
   const int i = threadIdx.x;
   const int n = *n_ptr, tok = *tok_ptr;
+  __shared__ int32_t sd[256];
   int32_t d = 0;
   if (i < k) d = drafts[i];
+  if (i < k) sd[i] = d;
   const uint64_t ev = u_counter ? *u_counter : 0;
   __syncthreads();                       // every read of ids / the counter before the writes below
   if (i <= k) pend_ids[i] = i < n ? (i < k ? d : 0) : (i == n ? tok : 0);
-  if (i < k) out[2 + i] = d;
   if (main_counters)
     for (int c = i; c < n_main; c += blockDim.x) main_counters[c] += n + main_extra;
   if (mtp_counters)
@@ -112,8 +116,13 @@ __global__ void cycle_finish_ex_kernel(const int32_t* __restrict__ drafts, int k
     *n_prev = n;
     out[0] = n;
     out[1] = tok;
+    for (int j = 0; j < k; ++j) out[2 + j] = sd[j];
     if (ids_next) ids_next[0] = tok;
     if (u_counter) *u_counter = ev + 1;
+    if (done) {
+      __threadfence_system();            // out[] (this thread's writes) before the flag
+      __hip_atomic_store(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
   }
 }
 
@@ -175,7 +184,8 @@ extern "C" int qvex_cycle_finish_ex(const int32_t* drafts, int k, const int32_t*
                                     int32_t* pend_ids, int32_t* feed, int32_t* n_prev, int32_t* out,
                                     int32_t* ids_next, int32_t* main_counters, int n_main, int main_extra,
                                     int32_t* mtp_counters, int n_mtp, int mtp_delta, uint64_t u_seed,
-                                    uint64_t* u_counter, int u_width, float* u_out, void* stream) {
+                                    uint64_t* u_counter, int u_width, float* u_out, int32_t* done,
+                                    void* stream) {
   QVEX_CHECK_ARG(drafts && n_accept && token && pend_ids && feed && n_prev && out && k >= 1 && k < 255,
                  "qvex_cycle_finish_ex: bad arguments");
   QVEX_CHECK_ARG((!main_counters || n_main >= 0) && (!mtp_counters || n_mtp >= 0) &&
@@ -183,7 +193,7 @@ extern "C" int qvex_cycle_finish_ex(const int32_t* drafts, int k, const int32_t*
                  "qvex_cycle_finish_ex: bad counter or uniform arguments");
   hipLaunchKernelGGL(cycle_finish_ex_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, drafts, k, n_accept, token,
                      pend_ids, feed, n_prev, out, ids_next, main_counters, n_main, main_extra, mtp_counters, n_mtp,
-                     mtp_delta, u_seed, u_counter, u_width, u_out);
+                     mtp_delta, u_seed, u_counter, u_width, u_out, done);
   QVEX_CHECK_LAUNCH("qvex_cycle_finish_ex");
   return QVEX_OK;
 }

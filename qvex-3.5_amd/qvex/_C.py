@@ -61,7 +61,7 @@ SIGNATURES: dict[str, list] = {
     "qvex_commit_step": [P, I, P, I, P],
     "qvex_gather_row": [P, LNG, P, I, P, I, P],
     "qvex_assemble_ids": [P, P, I, P, P],
-    "qvex_cycle_finish_ex": [P, I, P, P, P, P, P, P, P, P, I, I, P, I, I, U64, P, I, P, P],
+    "qvex_cycle_finish_ex": [P, I, P, P, P, P, P, P, P, P, I, I, P, I, I, U64, P, I, P, P, P],
     "qvex_cycle_finish": [P, I, P, P, P, P, P, P, P],
     "qvex_philox_uniforms": [U64, P, I, P, P],
     "qvex_gated_rmsnorm": [P, P, LNG, I, P, P, I, I, F, P],
@@ -73,9 +73,10 @@ SIGNATURES: dict[str, list] = {
     "qvex_rope_table": [I, F, I, P, P],
 }
 
-# qvex_abi_version() of the library these bindings match (4: qvex_mtp_input,
-# qvex_embed_rms_parts, the deferred reduction of qvex_qmv_w4g64_packed_argmax)
-ABI_VERSION = 5
+# qvex_abi_version() of the library these bindings match (6: the done flag of
+# qvex_cycle_finish_ex; 4: qvex_mtp_input, qvex_embed_rms_parts, the deferred
+# reduction of qvex_qmv_w4g64_packed_argmax)
+ABI_VERSION = 6
 
 _lib: ctypes.CDLL | None = None
 

@@ -42,12 +42,40 @@ def test_device_uniforms_equal_oracle_stream():
     res = torch.zeros(k + 2, dtype=torch.int32, device=DEV)
     u = torch.empty(k + 1, dtype=torch.float32, device=DEV)
     _C.call("qvex_cycle_finish_ex", _ptr(ids) + 4, k, _ptr(n_t), _ptr(tok), _ptr(pend), _ptr(feed), _ptr(nprev),
-            _ptr(res), _ptr(ids), None, 0, 0, None, 0, 0, seed, counter.data_ptr(), k + 1, _ptr(u), _stream())
+            _ptr(res), _ptr(ids), None, 0, 0, None, 0, 0, seed, counter.data_ptr(), k + 1, _ptr(u), None, _stream())
     torch.cuda.synchronize()
     for j, out in enumerate(outs):
         np.testing.assert_array_equal(out.cpu().numpy(), oracle.philox_uniforms(seed, ev0 + j, out.numel()))
     np.testing.assert_array_equal(u.cpu().numpy(), oracle.philox_uniforms(seed, ev0 + 4, k + 1))
     assert int(counter.item()) == ev0 + 5
+
+
+@pytest.mark.gpu
+def test_cycle_finish_done_flag_in_pinned_memory():
+    """With `done`, the finishing kernel writes [n, token, drafts] into pinned
+    host memory and then sets the flag: a host polling the flag (no stream
+    synchronisation) reads the complete result, and the device-side
+    bookkeeping (pending ids, feed, n_prev, next ids) is the same as without."""
+    k = 3
+    ids = torch.tensor([7, 11, 22, 33], dtype=torch.int32, device=DEV)
+    n_t = torch.tensor([2], dtype=torch.int32, device=DEV)
+    tok = torch.tensor([99], dtype=torch.int32, device=DEV)
+    pend, feed, nprev = (torch.zeros(k + 1, dtype=torch.int32, device=DEV), torch.zeros(1, dtype=torch.int32, device=DEV),
+                         torch.zeros(1, dtype=torch.int32, device=DEV))
+    out = torch.full((k + 2,), -5, dtype=torch.int32, pin_memory=True)
+    done = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    flag = done.numpy()
+    _C.call("qvex_cycle_finish_ex", _ptr(ids) + 4, k, _ptr(n_t), _ptr(tok), _ptr(pend), _ptr(feed), _ptr(nprev),
+            out.data_ptr(), _ptr(ids), None, 0, 0, None, 0, 0, 0, None, 0, None, done.data_ptr(), _stream())
+    ev = torch.cuda.Event()
+    ev.record()
+    spins = 0
+    while flag[0] == 0:
+        spins += 1
+        assert not (spins % 1024 == 0 and ev.query() and flag[0] == 0), "done flag never set"
+    assert out.numpy().tolist() == [2, 99, 11, 22, 33]
+    torch.cuda.synchronize()
+    assert pend.tolist() == [11, 22, 99, 0] and int(feed) == 99 and int(nprev) == 2 and int(ids[0]) == 99
 
 
 @pytest.mark.gpu
