@@ -152,6 +152,15 @@ int qvex_qmv_w4g64_packed_resid(const uint16_t* x, const void* packed, int M, in
 int qvex_qmv_w4g64_packed_rstd(const uint16_t* u, const void* packed, uint16_t* y, int M, int N,
                                int K, const float* sq_parts, int nparts, int dim, float eps,
                                int swiglu, void* stream);
+/* qvex_qmv_w4g64_packed_rstd (swiglu 0) that also writes, per row r and 16-row
+ * tile j, the largest bf16 output of the tile to tile_max[r * ceil(N/16) + j]
+ * (bf16; 16-byte aligned): the verify lm_head's logits and the tile maxima
+ * qvex_spec_accept_tiles_bf16 starts from, in one launch (mx.quantized_matmul
+ * of the lm_head, engine/model.py:330-336, with the sampler's first reduction
+ * in its epilogue). */
+int qvex_qmv_w4g64_packed_rstd_tilemax(const uint16_t* u, const void* packed, uint16_t* y, int M,
+                                       int N, int K, const float* sq_parts, int nparts, int dim,
+                                       float eps, uint16_t* tile_max, void* stream);
 int qvex_rms_parts(const uint16_t* x, const uint16_t* norm_w, uint16_t* u_out, float* sq_parts,
                    int M, int D, void* stream);
 /* out_proj after the split GatedDeltaNet mixer (qvex_gdn_decode_split): the
@@ -331,6 +340,33 @@ int qvex_spec_accept_filtered_bf16(const uint16_t* target, const uint16_t* draft
                                    float presence_penalty, int top_k, float top_p,
                                    int32_t* n_accept, int32_t* out_token, int S, int k, int V,
                                    void* workspace, uint64_t workspace_bytes, void* stream);
+
+/* qvex_spec_accept_filtered_bf16 for the decode cycle's call (the verify rows'
+ * accept and draw of engine/speculative.py:74-81 with Sampler.scores'
+ * filtering, engine/sampler.py:30-52) given tile_max [S*(k+1), V/16] bf16: the
+ * largest logit of each 16-column tile of each target row, as
+ * qvex_qmv_w4g64_packed_rstd_tilemax writes it with the logits (or
+ * qvex_tile_max_bf16 computes it). Without draft logits, with no presence
+ * penalty, 1 <= top_k <= 64 when sampling, V a multiple of 128 up to 262,144,
+ * the whole call is one kernel, one block per target row: the top_k-th
+ * largest of 256 thread maxima of the tile maxima bounds the row's k-th value
+ * from below, so only the tiles whose maximum reaches it are read (a few
+ * hundred logits instead of the row); rows where too many tiles or values
+ * reach it run the two-kernel path's code inside the same block. Other calls
+ * are qvex_spec_accept_filtered_bf16's. Results are identical to that call's
+ * (no reference counterpart: this is the same interface fed by the lm_head's
+ * epilogue). workspace as there, zero-filled before its first use: the
+ * one-kernel path counts each step's finished rows in it and leaves the count
+ * at zero. */
+int qvex_spec_accept_tiles_bf16(const uint16_t* target, const uint16_t* tile_max, const int32_t* draft_ids,
+                                const float* u_accept, const float* u_sample, float inv_temp,
+                                const float* seen, float presence_penalty, int top_k, float top_p,
+                                int32_t* n_accept, int32_t* out_token, int S, int k, int V,
+                                void* workspace, uint64_t workspace_bytes, void* stream);
+/* tile_max[r][t] = the largest of x[r][16 t .. 16 t + 15] for bf16 rows x
+ * [rows, V] (bf16 out [rows, ceil(V/16)]): the tile maxima of
+ * qvex_spec_accept_tiles_bf16 for logits that no tile-maxima epilogue wrote. */
+int qvex_tile_max_bf16(const uint16_t* x, int rows, int V, uint16_t* out, void* stream);
 
 /* Sampler.scores (engine/sampler.py:30-52) for R rows of V logits (bf16 when
  * logits_bf16, else fp32; 16-byte aligned) into out fp32 [R, V]: the presence

@@ -142,6 +142,10 @@ struct PkEpi {
   // argmax (am_parts != null): per row r and 16-row tile j, the largest
   // bf16-rounded output and its first index -> am_parts[(r * tiles + j) * 2 + {0, 1}]
   float* am_parts;
+  // tile maxima (tm_out != null): per row r and 16-row tile j, the largest
+  // bf16-rounded output -> tm_out[r * tiles + j] (bf16), what the sampler's
+  // one-kernel list form starts from
+  uint16_t* tm_out;
   // head-segment scale (seg_ss != null; the gated RMSNorm before out_proj,
   // engine/model.py:285-288): x is u = bf16(silu(z) * w * y) for K / 128 <= 64
   // heads of 128 columns, and the share of the product over head h of row r is
@@ -522,15 +526,18 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
             if (ei == 0 && tile < tiles) e.sq_parts[(size_t)row * tiles + tile] = sq;
           }
           if (y && n < N) y[(size_t)row * N + n] = d;
-          if (e.am_parts) {
+          if (e.am_parts || e.tm_out) {
             // the tile's largest rounded output and its first column (whole DPP rows active)
             const float v = n < N ? bf16_to_f32(d) : -__builtin_inff();
             const float m = row16_allmax(v);
-            const int j = row16_allmin(n < N && v == m ? n : 0x7fffffff);
-            if (ei == 0 && tile < tiles) {
-              e.am_parts[((size_t)row * tiles + tile) * 2] = m;
-              e.am_parts[((size_t)row * tiles + tile) * 2 + 1] = __int_as_float(j);
+            if (e.am_parts) {
+              const int j = row16_allmin(n < N && v == m ? n : 0x7fffffff);
+              if (ei == 0 && tile < tiles) {
+                e.am_parts[((size_t)row * tiles + tile) * 2] = m;
+                e.am_parts[((size_t)row * tiles + tile) * 2 + 1] = __int_as_float(j);
+              }
             }
+            if (e.tm_out && ei == 0 && tile < tiles) e.tm_out[(size_t)row * tiles + tile] = f32_to_bf16(m);
           }
         }
       }
@@ -842,6 +849,26 @@ extern "C" int qvex_rms_parts(const uint16_t* x, const uint16_t* norm_w, uint16_
                      u_out, sq_parts, D);
   QVEX_CHECK_LAUNCH("qvex_rms_parts");
   return QVEX_OK;
+}
+
+extern "C" int qvex_qmv_w4g64_packed_rstd_tilemax(const uint16_t* u, const void* packed, uint16_t* y, int M, int N,
+                                                  int K, const float* sq_parts, int nparts, int dim, float eps,
+                                                  uint16_t* tile_max, void* stream) {
+  const char* fn = "qvex_qmv_w4g64_packed_rstd_tilemax";
+  QVEX_CHECK_ARG(sq_parts && y && tile_max, "%s: null pointer", fn);
+  QVEX_CHECK_ARG(nparts >= 1 && nparts <= 256 && nparts % 4 == 0 && dim >= 1 && nparts == (dim + PK_TILE - 1) / PK_TILE,
+                 "%s: nparts=%d must be ceil(dim/16) for dim=%d, a multiple of 4 and <= 256", fn, nparts, dim);
+  QVEX_CHECK_ARG(qvex_aligned(sq_parts, 16) && qvex_aligned(tile_max, 16),
+                 "%s: sq_parts and tile_max must be 16-byte aligned", fn);
+  int TN = 1, WS = 1;
+  if (N >= 1 && K >= PK_SET) packed_default_tile(N, K, &TN, &WS);
+  PkEpi e{};
+  e.rs_parts = sq_parts;
+  e.rs_nparts = nparts;
+  e.rs_dim = dim;
+  e.rs_eps = eps;
+  e.tm_out = tile_max;
+  return launch_packed(u, (const uint8_t*)packed, y, M, N, K, TN, WS, false, -1, e, (hipStream_t)stream, fn);
 }
 
 extern "C" uint64_t qvex_qmv_w4g64_argmax_workspace_bytes(int M, int N) {

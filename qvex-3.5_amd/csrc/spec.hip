@@ -183,8 +183,13 @@ struct SpecArgs {
 
 __device__ __forceinline__ const void* row_ptr(const SpecArgs& a, int step, int i) {
   const long es = a.bf ? 2 : 4;
-  if (i <= a.k) return (const char*)a.target + ((long)step * (a.k + 1) + i) * a.V * es;
-  return (const char*)a.draft + ((long)step * a.k + (i - a.k - 1)) * a.V * es;
+  // both pointers as opaque values: a choice between the two fields' addresses
+  // would keep the argument struct in scratch memory for an indexed load
+  const char* tp = (const char*)a.target;
+  const char* dp = (const char*)a.draft;
+  asm volatile("" : "+v"(tp), "+v"(dp));
+  if (i <= a.k) return tp + ((long)step * (a.k + 1) + i) * a.V * es;
+  return dp + ((long)step * a.k + (i - a.k - 1)) * a.V * es;
 }
 
 // Logit j of a row as fp32 (bf16 rows widen exactly).
@@ -406,12 +411,12 @@ __device__ __forceinline__ bool topk_thresh(const float (&zz)[4 * NI], const boo
 
 // ---------------------------------------------------------------- kernel 1: part statistics
 
+// Part p of row `row` (the block's work in spec_rowstats_kernel); zero_ctr:
+// this block clears the one-kernel finish counters (part 0 of row 0).
 template <bool BF>
-__global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
+__device__ __forceinline__ void rowstats_block(const SpecArgs& a, int p, int row, bool zero_ctr) {
   __shared__ float red[4];
   __shared__ int redi[4];
-  const int p = blockIdx.x;
-  const int row = blockIdx.y;
   const int step = row / a.rps, i = row % a.rps;
   const void* src = row_ptr(a, step, i);
   const int base = p * PART;
@@ -559,7 +564,7 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
           a.ncand[(crow * a.P + p) * 2] = c_gt2;
           a.ncand[(crow * a.P + p) * 2 + 1] = c_eq2;
         }
-        if (p == 0 && row == 0)
+        if (zero_ctr && p == 0 && row == 0)
           for (int q = t; q < a.S; q += NT) a.ctr[q] = 0;
       }
       return;
@@ -614,10 +619,15 @@ __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
         a.ncand[(crow * a.P + p) * 2] = c_gt;
         a.ncand[(crow * a.P + p) * 2 + 1] = c_eq;
       }
-      if (p == 0 && row == 0)
+      if (zero_ctr && p == 0 && row == 0)
         for (int q = t; q < a.S; q += NT) a.ctr[q] = 0;
     }
   }
+}
+
+template <bool BF>
+__global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
+  rowstats_block<BF>(a, blockIdx.x, blockIdx.y, true);
 }
 
 // ---------------------------------------------------------------- filter kernel (top-k / top-p)
@@ -1672,14 +1682,17 @@ __device__ __forceinline__ void filter_wave(const SpecArgs& a, const float* fl, 
 // fixed-order pass when the lists do not hold the kept set. The last block of
 // the step (a device-scope counter, zeroed by the statistics kernel) takes the
 // first rejection's draw, or the bonus.
-__global__ __launch_bounds__(NT) void spec_finish_kernel(SpecArgs a) {
-  extern __shared__ float smem[];       // fallback pass: [P][NT] thread sums, [P] part sums
+// Target row `row`'s filter, accept test and draw (the block's work in
+// spec_finish_kernel) from the statistics kernel's part lists and candidates;
+// the flag and token are returned to every thread. smem: the full pass's
+// [P][NT] thread sums and [P] part sums.
+__device__ __forceinline__ void finish_row(const SpecArgs& a, int row, float* smem, int& ok_out, int& tok_out) {
   __shared__ float fl[CAND_LIST_FLOATS];
   __shared__ float s_c0, s_S, s_cut;
-  __shared__ int s_last;
   __shared__ SparseSh sh;
   __shared__ float red[4];
-  const int row = blockIdx.x, k = a.k, step = row / (k + 1), i = row - step * (k + 1);
+  __shared__ int s_ok, s_tok;
+  const int k = a.k, step = row / (k + 1), i = row - step * (k + 1);
   const int t = threadIdx.x, K = a.top_k, P = a.P;
   // requests first: the part lists, the candidates, the draft's logit
   const float* L = a.fws + (long)row * P * (K + 1);
@@ -1750,18 +1763,496 @@ __global__ __launch_bounds__(NT) void spec_finish_kernel(SpecArgs a) {
     }
   }
   if (t == 0) {
-    a.rres[2 * row] = ok;
-    a.rres[2 * row + 1] = tok;
-    const int old = __hip_atomic_fetch_add(a.ctr + step, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == k) {
-      // every row of the step is in (their results read after the acquire)
-      int n = k;
-      for (int r = 0; r < k; ++r)
-        if (!a.rres[2 * (step * (k + 1) + r)]) { n = r; break; }
-      a.n_accept[step] = n;
-      a.out_token[step] = a.rres[2 * (step * (k + 1) + n) + 1];
+    s_ok = ok;
+    s_tok = tok;
+  }
+  __syncthreads();
+  ok_out = s_ok;
+  tok_out = s_tok;
+}
+
+// Thread 0 of each target row's block: store the row's (accept flag, draw) and
+// count the row in; the last row of the step to arrive (a device-scope
+// acquire-release counter) takes the first rejection's draw, or the bonus, and
+// puts the counter back to 0, so the counters are zero between calls.
+__device__ __forceinline__ void finish_decide(const SpecArgs& a, int row, int ok, int tok) {
+  const int k = a.k, step = row / (k + 1);
+  a.rres[2 * row] = ok;
+  a.rres[2 * row + 1] = tok;
+  const int old = __hip_atomic_fetch_add(a.ctr + step, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  if (old == k) {
+    // every row of the step is in (their results read after the acquire)
+    int n = k;
+    for (int r = 0; r < k; ++r)
+      if (!a.rres[2 * (step * (k + 1) + r)]) {
+        n = r;
+        break;
+      }
+    a.n_accept[step] = n;
+    a.out_token[step] = a.rres[2 * (step * (k + 1) + n) + 1];
+    __hip_atomic_store(a.ctr + step, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+__global__ __launch_bounds__(NT) void spec_finish_kernel(SpecArgs a) {
+  extern __shared__ float smem[];
+  int ok, tok;
+  finish_row(a, blockIdx.x, smem, ok, tok);
+  if (threadIdx.x == 0) finish_decide(a, blockIdx.x, ok, tok);
+}
+
+
+// ---------------------------------------------------------------- list form from tile maxima (one kernel)
+
+// The list form without draft logits and without a presence penalty, given
+// each target row's 16-column tile maxima (the bf16 maximum of logits
+// 16 t .. 16 t + 15, which the verify lm_head's epilogue writes): one block per
+// target row finds its top_k and every value at or above the k-th from the few
+// tiles that can hold them, instead of a pass over the row.
+//   * tau = the top_k-th largest of the block's NT thread maxima of the tile
+//     maxima (ties by thread): top_k tiles hold a value >= tau, so the row's
+//     k-th value v_k >= tau, and every logit >= v_k lies in a tile whose maximum
+//     is >= tau (z = x / T keeps the order of distinct bf16 logits);
+//   * those tiles' logits >= tau are gathered and ranked (z descending, index
+//     ascending): the first top_k are the row's k largest values, and every
+//     value equal to one of them is in the gathered set, so the ties at the
+//     cutoff are counted exactly;
+//   * the filter is filter_wave's arithmetic on those values (the same
+//     sequential sums), the accept test is spec_decide_kernel's, and the kept
+//     set (z >= cutoff) is the first n_gt + ties entries, drawn through the
+//     fixed-order walk over its positive weights (sparse_sample's sums, here in
+//     one wave: tile_walk).
+// More candidate tiles or values than fit, or more than 64 kept values, send
+// the row through the two-kernel path's code in this block (every part's
+// statistics, then finish_row). The last row of a step to finish takes the
+// decision (finish_decide).
+constexpr int TM_PER = 8;      // 16-byte loads of 8 tile maxima per thread: NT * 64 = 16384 tiles
+constexpr int TM_CT = 256;     // candidate tiles
+constexpr int TM_CE = 512;     // candidate values
+
+struct TmSh {
+  __align__(16) float lm[NT];          // thread maxima
+  __align__(16) float v4k[4 * 64];     // each wave's top_k thread maxima
+  __align__(16) float ev[TM_CE];       // candidate values (z) and indices, gathered
+  __align__(16) int ej[TM_CE];
+  __align__(16) float sv[TM_CE];       // the same ranked
+  __align__(16) int sj[TM_CE];
+  int tiles[TM_CT];
+  int scan[8];
+  float tau;
+  float f[3];                          // c_0, S_p, cutoff
+  int ok, tok, nkeep;
+  // the draw, wave 0
+  __align__(16) int wkey[64];
+  int skey[64];
+  float sw[64];
+  int slot_key[64], slot_first[64];
+  float slot_sum[64];
+  int grp_key[64], grp_first[64];
+  float grp_sum[64];
+  float part_sum[64];
+  int part_first[64];
+};
+
+// Orders a wave's LDS writes before its later reads of other lanes' entries
+// (LDS serves one wave's requests in order; this keeps the compiler from
+// moving the accesses across).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ int rl_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ float rl_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// The fixed-order walk's draw over n <= 64 positive weights in one wave: lane
+// e < n holds the e-th in walk-key order (key kv, weight wv). The sums are
+// sparse_sample's (spec_sample_kernel's with every zero weight dropped, x + 0 =
+// x): a thread slot's sum from 0 in key order; a (part, wave quarter) group's
+// sum through the full pass's xor butterfly, which with one or two non-zero
+// lanes is that lane or their sum (a + b = b + a), and with more is the
+// butterfly itself, run on the slots' lanes; a part's ((q0 + q1) + q2) + q3;
+// then the walk over parts, the chosen part's slots and the chosen slot's
+// elements with running prefixes, each the sequential fp32 chain. Slots, groups
+// and parts are found by ballots over the sorted keys. Returns the drawn index
+// in every lane.
+__device__ int tile_walk(int n, int kv, float wv, float u, TmSh& S) {
+  const int lane = threadIdx.x & 63;
+  const bool valid = lane < n;
+  const unsigned long long upto = lane == 63 ? ~0ull : ((2ull << lane) - 1ull);   // lanes <= lane
+  const int prv = lane > 0 ? lane - 1 : 0, nxl = lane < 63 ? lane + 1 : 63;
+  // slots (key >> 5)
+  const int kp = __shfl(kv, prv, 64), kn = __shfl(kv, nxl, 64);
+  const bool sfirst = valid && (lane == 0 || (kp >> 5) != (kv >> 5));
+  const bool slast = valid && (lane == n - 1 || (kn >> 5) != (kv >> 5));
+  const unsigned long long fm = __ballot(sfirst);
+  const int ns = __popcll(fm);
+  const int si = __popcll(fm & upto) - 1;                   // this entry's slot
+  const int pos = valid ? lane - (63 - __clzll(fm & upto)) : 0;
+  int maxpos = pos;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) maxpos = max(maxpos, __shfl_xor(maxpos, o, 64));
+  float run = wv;                                           // 0 + w = w
+  for (int d = 1; d <= maxpos; ++d) {                       // slots of several weights, in order
+    const float prev = __shfl(run, prv, 64);
+    run = pos == d ? prev + wv : run;
+  }
+  if (sfirst) {
+    S.slot_key[si] = kv;
+    S.slot_first[si] = lane;
+  }
+  if (slast) S.slot_sum[si] = run;
+  wave_lds_sync();
+  const bool vs = lane < ns;
+  const int sk = vs ? S.slot_key[lane] : 0x7fffffff;
+  const float ss = vs ? S.slot_sum[lane] : 0.0f;
+  const int sfl = vs ? S.slot_first[lane] : n;
+  // groups (key >> 11): consecutive slots
+  const int skp = __shfl(sk, prv, 64);
+  const bool gfirst = vs && (lane == 0 || (skp >> 11) != (sk >> 11));
+  const unsigned long long gm = __ballot(gfirst);
+  const int ng = __popcll(gm);
+  const unsigned long long gabove = gm & ~upto;
+  const int gnext = gabove ? __ffsll((long long)gabove) - 1 : ns;
+  const int m = gnext - lane;
+  const float ss1 = __shfl(ss, nxl, 64);
+  float gs = m == 1 ? ss : ss + ss1;
+  unsigned long long big = __ballot(gfirst && m >= 3);
+  while (big) {                                             // three or more slots: the butterfly itself
+    const int g0 = __ffsll((long long)big) - 1;
+    big &= big - 1;
+    const int g1 = rl_i(gnext, g0);
+    float x = 0.0f;
+    for (int q = g0; q < g1; ++q) {
+      const int L = (rl_i(sk, q) >> 5) & 63;
+      x = lane == L ? rl_f(ss, q) : x;
+    }
+    const float v = rl_f(wave_bfly_sum(x), 0);
+    gs = lane == g0 ? v : gs;
+  }
+  const int gi = __popcll(gm & upto) - 1;
+  if (gfirst) {
+    S.grp_key[gi] = sk;
+    S.grp_sum[gi] = gs;
+    S.grp_first[gi] = lane;
+  }
+  wave_lds_sync();
+  const bool vg = lane < ng;
+  const int gk = vg ? S.grp_key[lane] : 0x7fffffff;
+  const float gv = vg ? S.grp_sum[lane] : 0.0f;
+  const int gfl = vg ? S.grp_first[lane] : ns;
+  // parts (key >> 13): ((q0 + q1) + q2) + q3 over a part's (at most four) groups
+  const int gkp = __shfl(gk, prv, 64);
+  const bool pfirst = vg && (lane == 0 || (gkp >> 13) != (gk >> 13));
+  const unsigned long long pm = __ballot(pfirst);
+  const int np = __popcll(pm);
+  float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
+#pragma unroll
+  for (int dd = 0; dd < 4; ++dd) {
+    const int src = min(lane + dd, 63);
+    const int gkd = __shfl(gk, src, 64);
+    const float gvd = __shfl(gv, src, 64);
+    if (lane + dd < ng && (gkd >> 13) == (gk >> 13)) {
+      const int q = (gkd >> 11) & 3;
+      b0 = q == 0 ? gvd : b0;
+      b1 = q == 1 ? gvd : b1;
+      b2 = q == 2 ? gvd : b2;
+      b3 = q == 3 ? gvd : b3;
     }
   }
+  const int pi = __popcll(pm & upto) - 1;
+  if (pfirst) {
+    S.part_sum[pi] = ((b0 + b1) + b2) + b3;
+    S.part_first[pi] = lane;
+  }
+  wave_lds_sync();
+  const float pv = lane < np ? S.part_sum[lane] : 0.0f;
+  const int pfl = lane < np ? S.part_first[lane] : ng;
+  // the walk over parts: the running prefix, sequential from 0
+  float acc = 0.0f, pre = 0.0f;
+  for (int q = 0; q < np; ++q) {
+    acc = acc + rl_f(pv, q);
+    pre = lane == q ? acc : pre;
+  }
+  const float th = u * acc;
+  const unsigned long long hit = __ballot(lane < np && pre > th);
+  bool fallback = hit == 0ull;
+  const int ps = fallback ? np - 1 : __ffsll((long long)hit) - 1;
+  float cacc = ps > 0 ? rl_f(pre, ps - 1) : 0.0f;
+  const int gA = rl_i(pfl, ps), gB = ps + 1 < np ? rl_i(pfl, ps + 1) : ng;
+  const int sA = rl_i(gfl, gA), sB = gB < ng ? rl_i(gfl, gB) : ns;
+  int ts = -1;
+  if (!fallback) {
+    for (int q = sA; q < sB; ++q) {
+      const float nx = cacc + rl_f(ss, q);
+      if (nx > th) {
+        ts = q;
+        break;
+      }
+      cacc = nx;
+    }
+  }
+  if (ts < 0) {                                             // the part's last slot
+    ts = sB - 1;
+    fallback = true;
+  }
+  const int eA = rl_i(sfl, ts), eB = ts + 1 < ns ? rl_i(sfl, ts + 1) : n;
+  int res = -1;
+  if (!fallback) {
+    for (int e = eA; e < eB; ++e) {
+      cacc = cacc + rl_f(wv, e);
+      if (cacc > th) {
+        res = e;
+        break;
+      }
+    }
+  }
+  if (res < 0) res = eB - 1;                                // the slot's last positive weight
+  return key_index(rl_i(kv, res));
+}
+
+__global__ __launch_bounds__(NT) void spec_tiles_kernel(SpecArgs a, const uint16_t* __restrict__ tmax, int tiles) {
+  extern __shared__ float smem[];                           // the two-kernel path's full pass
+  __shared__ TmSh S;
+  const int row = blockIdx.x, k = a.k, step = row / (k + 1), i = row - step * (k + 1);
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int K = a.top_k;
+  const uint16_t* tr = tmax + (long)row * tiles;
+  const uint16_t* xr = reinterpret_cast<const uint16_t*>(row_ptr(a, step, i));
+  // requests first: the row's tile maxima (thread t: tiles 8 (t + NT q) + 0..7),
+  // the draft's logit and the uniforms
+  u32x4 tv[TM_PER];
+#pragma unroll
+  for (int q = 0; q < TM_PER; ++q) tv[q] = load16(tr + min(8 * (t + NT * q), tiles - 8));
+  const int32_t* d = a.ids + (long)step * k;
+  const int di = i < k ? d[i] : -1;
+  const bool din = i < k && !(di < 0 || di >= a.V);
+  const float xd = din ? lg(xr, di, 1) : 0.0f;
+  const float ua = i < k ? a.u_acc[(long)step * k + i] : 0.0f;
+  const float u = a.u_smp[step];
+  float tm = -__builtin_inff();
+#pragma unroll
+  for (int q = 0; q < TM_PER; ++q) {
+    const uint32_t w4[4] = {tv[q].x, tv[q].y, tv[q].z, tv[q].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = e & 1 ? bf16_hi(w4[e >> 1]) : bf16_lo(w4[e >> 1]);
+      tm = 8 * (t + NT * q) + e < tiles ? fmaxf(tm, v) : tm;
+    }
+  }
+  // tau: each wave ranks its lane maxima and keeps its top_k, then those 4 top_k are ranked
+  S.lm[t] = tm;
+  __syncthreads();
+  {
+    const float4* w4 = reinterpret_cast<const float4*>(S.lm + wave * 64);
+    int r = 0;
+#pragma unroll
+    for (int q4 = 0; q4 < 16; ++q4) {
+      const float4 o = w4[q4];
+      const float e[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r += ahead(e[j], tm, 4 * q4 + j < lane);
+    }
+    if (r < K) S.v4k[wave * K + r] = tm;
+  }
+  __syncthreads();
+  if (t < 4 * K) {
+    const float v = S.v4k[t];
+    int r = 0;
+#pragma unroll 4
+    for (int q = 0; q < 4 * K; q += 4) {
+      const float4 o = *reinterpret_cast<const float4*>(&S.v4k[q]);
+      const float e[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r += ahead(e[j], v, q + j < t);
+    }
+    if (r == K - 1) S.tau = v;
+  }
+  __syncthreads();
+  const float tau = S.tau;
+  // the tiles that can hold a value >= tau
+  int c = 0;
+#pragma unroll
+  for (int q = 0; q < TM_PER; ++q) {
+    const uint32_t w4[4] = {tv[q].x, tv[q].y, tv[q].z, tv[q].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = e & 1 ? bf16_hi(w4[e >> 1]) : bf16_lo(w4[e >> 1]);
+      c += (int)(8 * (t + NT * q) + e < tiles) & (int)(v >= tau);
+    }
+  }
+  int nt;
+  int off = block_excl_scan(c, S.scan, &nt);
+  bool fast = nt <= TM_CT;                                  // block-uniform from here on
+  if (fast) {
+#pragma unroll
+    for (int q = 0; q < TM_PER; ++q) {
+      const uint32_t w4[4] = {tv[q].x, tv[q].y, tv[q].z, tv[q].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = e & 1 ? bf16_hi(w4[e >> 1]) : bf16_lo(w4[e >> 1]);
+        const int j = 8 * (t + NT * q) + e;
+        if (j < tiles && v >= tau) S.tiles[off++] = j;
+      }
+    }
+    __syncthreads();
+    // the candidate tiles' logits, thread c taking tile c
+    float x[16];
+    int j0 = 0;
+    if (t < nt) {
+      j0 = 16 * S.tiles[t];
+      const u32x4 l0 = load16(xr + j0), l1 = load16(xr + j0 + 8);
+      const uint32_t w8[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) x[e] = e & 1 ? bf16_hi(w8[e >> 1]) : bf16_lo(w8[e >> 1]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) x[e] = -__builtin_inff();
+    }
+    int ce = 0;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) ce += (int)(t < nt) & (int)(x[e] >= tau);
+    int ne;
+    int o2 = block_excl_scan(ce, S.scan, &ne);
+    fast = ne <= TM_CE;
+    if (fast) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (t < nt && x[e] >= tau) {
+          S.ev[o2] = x[e] * a.inv_temp;
+          S.ej[o2] = j0 + e;
+          ++o2;
+        }
+      if (t < 8 && ne + t < TM_CE) {                        // padding that never ranks ahead
+        S.ev[ne + t] = -__builtin_inff();
+        S.ej[ne + t] = 0x7fffffff;
+      }
+      __syncthreads();
+      const int n8 = min((ne + 7) & ~7, TM_CE);
+      for (int cc = t; cc < ne; cc += NT) {
+        const float v = S.ev[cc];
+        const int j = S.ej[cc];
+        int r = 0;
+#pragma unroll 2
+        for (int q = 0; q < n8; q += 8) {
+          const float4 va = *reinterpret_cast<const float4*>(&S.ev[q]);
+          const float4 vb = *reinterpret_cast<const float4*>(&S.ev[q + 4]);
+          const int4 ja = *reinterpret_cast<const int4*>(&S.ej[q]);
+          const int4 jb = *reinterpret_cast<const int4*>(&S.ej[q + 4]);
+          const float vv[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+          const int jj[8] = {ja.x, ja.y, ja.z, ja.w, jb.x, jb.y, jb.z, jb.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) r += ahead(vv[e], v, jj[e] < j);
+        }
+        S.sv[r] = v;
+        S.sj[r] = j;
+      }
+      __syncthreads();
+      if (wave == 0) {
+        // filter_wave's arithmetic on the row's k largest values S.sv[0 .. K)
+        const float cl = lane < K ? S.sv[lane] : -__builtin_inff();
+        const float c0 = rl_f(cl, 0);
+        const float el = lane < K ? qx_expf(cl - c0) : 0.0f;
+        float Ssum = 0.0f, pre = 0.0f;
+        for (int q = 0; q < K; ++q) {
+          Ssum = Ssum + rl_f(el, q);
+          pre = lane == q ? Ssum : pre;
+        }
+        float cutoff = rl_f(cl, K - 1);
+        if (a.top_p > 0.0f && a.top_p < 1.0f) {
+          const float pl = el / Ssum;
+          float run = 0.0f, mn = __builtin_inff();
+          for (int q = 0; q < K; ++q) {
+            const float pq = rl_f(pl, q);
+            const float cq = rl_f(cl, q);
+            const float incl = run + pq;
+            if ((incl - pq) < a.top_p && cq < mn) mn = cq;
+            run = incl;
+          }
+          cutoff = mn;
+        }
+        int eq = 0;
+        for (int r = lane; r < ne; r += 64) eq += S.sv[r] == cutoff ? 1 : 0;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) eq += __shfl_xor(eq, o, 64);
+        const int n_gt = __popcll(__ballot(lane < K && cl > cutoff));
+        const float Sp = (n_gt > 0 ? rl_f(pre, n_gt - 1) : 0.0f) + (float)eq * qx_expf(cutoff - c0);
+        int ok = 0;
+        if (din) {
+          const float zd = xd * a.inv_temp;
+          const float ep = zd >= cutoff ? qx_expf(zd - c0) : 0.0f;
+          const float eqd = 1.0f, Sq = 1.0f;
+          const float lhs = ua * eqd * Sp;
+          const float rhs = ep * Sq;
+          ok = lhs < rhs ? 1 : 0;
+        }
+        const int nkeep = n_gt + eq;                        // the kept set: a prefix of the ranking
+        if (lane == 0) {
+          float* fr = a.frow + (long)row * 4;
+          fr[0] = c0;
+          fr[1] = Sp;
+          fr[2] = cutoff;
+          S.ok = ok;
+          S.nkeep = nkeep;
+        }
+        if (nkeep <= 64) {
+          WCtx cw;
+          cw.mp = c0;
+          cw.sp = Sp;
+          cw.cutoff = cutoff;
+          cw.d = i < k ? di : -1;
+          const int je = lane < nkeep ? S.sj[lane] : 0;
+          const float ze = lane < nkeep ? S.sv[lane] : -__builtin_inff();
+          int tok = -1;
+          for (int mode = i < k ? 0 : 1; mode <= 1; ++mode) {
+            cw.mode = mode;
+            const float w = lane < nkeep ? weight_z(cw, je, ze) : 0.0f;
+            const bool pos = w > 0.0f;
+            const int npos = __popcll(__ballot(pos));
+            if (npos == 0) continue;                        // mode 0 with no residual weight: p_i
+            const int key = pos ? walk_key(je) : 0x7fffffff;
+            S.wkey[lane] = key;
+            wave_lds_sync();
+            int r = 0;
+#pragma unroll
+            for (int q4 = 0; q4 < 16; ++q4) {
+              const int4 o = *reinterpret_cast<const int4*>(&S.wkey[4 * q4]);
+              r += (int)(o.x < key) + (int)(o.y < key) + (int)(o.z < key) + (int)(o.w < key);
+            }
+            if (pos) {
+              S.skey[r] = key;
+              S.sw[r] = w;
+            }
+            wave_lds_sync();
+            const int kv = lane < npos ? S.skey[lane] : 0x7fffffff;
+            const float wv = lane < npos ? S.sw[lane] : 0.0f;
+            tok = tile_walk(npos, kv, wv, u, S);
+            break;
+          }
+          if (lane == 0) S.tok = tok;
+        }
+      }
+      __syncthreads();
+      fast = S.nkeep <= 64;
+    }
+  }
+  int ok, tok;
+  if (fast) {
+    ok = S.ok;
+    tok = S.tok;
+  } else {
+    // the two-kernel path's work for this row, in this block: every part's
+    // statistics, then finish_row (all inlined: no call carries the arguments)
+    for (int p = 0; p < a.P; ++p) {
+      rowstats_block<true>(a, p, row, false);
+      __syncthreads();
+    }
+    finish_row(a, row, smem, ok, tok);
+  }
+  if (t == 0) finish_decide(a, row, ok, tok);
 }
 
 // ---------------------------------------------------------------- full-vocabulary scores (Sampler.scores)
@@ -1931,6 +2422,68 @@ extern "C" int qvex_spec_accept_filtered_bf16(const uint16_t* target, const uint
                           top_p, n_accept, out_token, S, k, V, workspace, workspace_bytes, stream);
 }
 
+
+extern "C" int qvex_spec_accept_tiles_bf16(const uint16_t* target, const uint16_t* tile_max, const int32_t* draft_ids,
+                                           const float* u_accept, const float* u_sample, float inv_temp,
+                                           const float* seen, float presence_penalty, int top_k, float top_p,
+                                           int32_t* n_accept, int32_t* out_token, int S, int k, int V,
+                                           void* workspace, uint64_t workspace_bytes, void* stream) {
+  const int tk = (top_k > 0 && top_k < V) ? top_k : 0;
+  const int P = nparts(V);
+  const int tiles = V / 16;
+  const bool use = tile_max && inv_temp > 0.0f && tk >= 1 && tk <= 64 && presence_penalty == 0.0f &&
+                   V % 128 == 0 && V >= 128 && tiles <= NT * 8 * TM_PER && cand_fits(P) && S >= 1 && k >= 0 &&
+                   k <= 32 && (long)S * (k + 1) <= 65535;
+  if (!use)
+    return spec_accept_impl(target, nullptr, 1, draft_ids, u_accept, u_sample, inv_temp, seen, presence_penalty,
+                            top_k, top_p, n_accept, out_token, S, k, V, workspace, workspace_bytes, stream);
+  QVEX_CHECK_ARG(target && n_accept && out_token && workspace && u_sample, "qvex_spec_accept_tiles: null pointer");
+  QVEX_CHECK_ARG(k == 0 || (draft_ids && u_accept), "qvex_spec_accept_tiles: draft_ids/u_accept required for k > 0");
+  QVEX_CHECK_ARG(qvex_aligned(target, 16) && qvex_aligned(tile_max, 16),
+                 "qvex_spec_accept_tiles: logits and tile maxima must be 16-byte aligned");
+  QVEX_CHECK_ARG(top_p == top_p, "qvex_spec_accept_tiles: top_p is NaN");
+  const bool use_p = top_p > 0.0f && top_p < 1.0f;
+  const int rps = k + 1;
+  const uint64_t base = ws_floats(S, rps, P);
+  const uint64_t need = (base + filter_floats(S, k, P, tk) + cand_ints(S, k, P, tk, 0)) * sizeof(float);
+  QVEX_CHECK_ARG(workspace_bytes >= need, "qvex_spec_accept_tiles: workspace %llu bytes < %llu needed",
+                 (unsigned long long)workspace_bytes, (unsigned long long)need);
+  const size_t lds = ((size_t)P * NT + P + 2 * rps) * sizeof(float);
+  float* fws = (float*)workspace + base;
+  float* frow = fws + (uint64_t)S * (k + 1) * P * (tk + 1);
+  int32_t* cand = reinterpret_cast<int32_t*>(frow + (uint64_t)S * (k + 1) * 4);
+  float* cand_z = reinterpret_cast<float*>(cand + (uint64_t)S * (k + 1) * P * CAND_CAP);
+  int32_t* ncand = reinterpret_cast<int32_t*>(cand_z + (uint64_t)S * (k + 1) * P * CAND_CAP);
+  int32_t* ctr = ncand + (uint64_t)S * (k + 1) * P * 2;
+  int32_t* rres = ctr + S;
+  SpecArgs a{target, nullptr, draft_ids, u_accept, u_sample, inv_temp, 0, n_accept, out_token,
+             (float*)workspace, S, k, V, P, rps, seen, 0.0f, tk, use_p ? top_p : 1.0f, fws, frow, 1,
+             1, 0, 1, cand, cand_z, ncand, ctr, rres};
+  hipLaunchKernelGGL(spec_tiles_kernel, dim3(S * rps), dim3(NT), lds, (hipStream_t)stream, a, tile_max, tiles);
+  QVEX_CHECK_LAUNCH("qvex_spec_accept_tiles");
+  return QVEX_OK;
+}
+
+// tile_max[r][t] = the largest of x[r][16 t .. 16 t + 15] (bf16; -inf for no value)
+__global__ void tile_max_kernel(const uint16_t* __restrict__ x, int rows, int V, uint16_t* __restrict__ out) {
+  const int tiles = (V + 15) / 16;
+  const long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= (long)rows * tiles) return;
+  const int r = (int)(g / tiles), tt = (int)(g - (long)r * tiles);
+  const uint16_t* xr = x + (long)r * V + 16 * tt;
+  float m = -__builtin_inff();
+  for (int e = 0; e < 16 && 16 * tt + e < V; ++e) m = fmaxf(m, bf16_to_f32(xr[e]));
+  out[g] = f32_to_bf16(m);
+}
+
+extern "C" int qvex_tile_max_bf16(const uint16_t* x, int rows, int V, uint16_t* out, void* stream) {
+  QVEX_CHECK_ARG(x && out && rows >= 1 && V >= 1, "qvex_tile_max_bf16: bad arguments (rows=%d V=%d)", rows, V);
+  const long n = (long)rows * ((V + 15) / 16);
+  hipLaunchKernelGGL(tile_max_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, x, rows,
+                     V, out);
+  QVEX_CHECK_LAUNCH("qvex_tile_max_bf16");
+  return QVEX_OK;
+}
 
 extern "C" uint64_t qvex_sampler_scores_workspace_bytes(int R, int V, int top_k) {
   return qvex_spec_accept_filtered_workspace_bytes(R, 0, V, 0, top_k);

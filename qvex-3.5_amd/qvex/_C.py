@@ -35,6 +35,7 @@ SIGNATURES: dict[str, list] = {
     "qvex_qmv_w4g64_packed_tiled": [P, P, P, I, I, I, I, I, I, P],
     "qvex_qmv_w4g64_packed_resid": [P, P, I, I, I, P, P, P, P, P, P],
     "qvex_qmv_w4g64_packed_rstd": [P, P, P, I, I, I, P, I, I, F, I, P],
+    "qvex_qmv_w4g64_packed_rstd_tilemax": [P, P, P, I, I, I, P, I, I, F, P, P],
     "qvex_qmv_w4g64_packed_gnorm_resid": [P, P, I, I, I, P, I, F, P, P, P, P, P, P],
     "qvex_rms_parts": [P, P, P, P, I, I, P],
     "qvex_qmv_w4g64_packed_argmax": [P, P, I, I, I, P, I, I, F, P, P, U64, P],
@@ -48,6 +49,8 @@ SIGNATURES: dict[str, list] = {
     "qvex_spec_accept": [P, P, P, P, P, F, P, P, I, I, I, P, U64, P],
     "qvex_spec_accept_filtered": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P, U64, P],
     "qvex_spec_accept_filtered_bf16": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P, U64, P],
+    "qvex_spec_accept_tiles_bf16": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P, U64, P],
+    "qvex_tile_max_bf16": [P, I, I, P, P],
     "qvex_spec_accept_filtered_bf16_noalloc": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P],
     "qvex_sampler_scores": [P, I, I, I, P, F, F, I, F, P, P, U64, P],
     "qvex_mark_seen": [P, I, P, I, P, I, P],

@@ -311,9 +311,12 @@ def qmv_packed_gnorm_resid(u: torch.Tensor, ss_parts: torch.Tensor, packed: torc
 
 
 def qmv_packed_rstd(u: torch.Tensor, packed: torch.Tensor, N: int, parts: torch.Tensor, eps: float,
-                    out: torch.Tensor | None = None, swiglu: bool = False) -> torch.Tensor:
+                    out: torch.Tensor | None = None, swiglu: bool = False,
+                    tile_max: torch.Tensor | None = None) -> torch.Tensor:
     """quantized_matmul_packed of rms_norm(h) given as u = bf16(h * w) and the
-    per-16-column sums of h^2 (qmv_packed_resid / rms_parts); swiglu as there."""
+    per-16-column sums of h^2 (qmv_packed_resid / rms_parts); swiglu as there.
+    tile_max (bf16 [M, ceil(N/16)], not with swiglu): also each 16-column tile's
+    largest output, for spec_accept's one-kernel list form."""
     K = u.shape[-1]
     u2 = u.reshape(-1, K)
     M = u2.shape[0]
@@ -327,6 +330,15 @@ def qmv_packed_rstd(u: torch.Tensor, packed: torch.Tensor, N: int, parts: torch.
     NO = N // 2 if swiglu else N
     out = torch.empty((M, NO), dtype=torch.bfloat16, device=u.device) if out is None else out
     _check(out, "out", torch.bfloat16)
+    if tile_max is not None:
+        if swiglu:
+            raise _C.QvexError("tile maxima are written by the plain product only")
+        _check(tile_max, "tile_max", torch.bfloat16)
+        if tile_max.numel() != M * ((N + 15) // 16):
+            raise _C.QvexError(f"tile_max must hold M * ceil(N/16) = {M * ((N + 15) // 16)} values")
+        _C.call("qvex_qmv_w4g64_packed_rstd_tilemax", _ptr(u2), _ptr(packed), _ptr(out), M, N, K, _ptr(parts),
+                nparts, K, float(eps), _ptr(tile_max), _stream())
+        return out
     _C.call("qvex_qmv_w4g64_packed_rstd", _ptr(u2), _ptr(packed), _ptr(out), M, N, K, _ptr(parts), nparts, K,
             float(eps), int(bool(swiglu)), _stream())
     return out
@@ -561,15 +573,35 @@ def gated_delta_chunked(q, k, v, a, b, A_log, dt_bias, state, state_out=None, y=
 
 
 def spec_workspace(S: int, k: int, V: int, has_draft: bool, device, top_k: int = 0) -> torch.Tensor:
+    """Sampler workspace, zero-filled: the one-kernel list form (tile maxima)
+    needs its step counters at zero before the first call (every call leaves
+    them at zero)."""
     n = int(_C.lib().qvex_spec_accept_filtered_workspace_bytes(S, k, V, int(has_draft), int(top_k)))
-    return torch.empty((max(n, 4) + 3) // 4, dtype=torch.float32, device=device)
+    return torch.zeros((max(n, 4) + 3) // 4, dtype=torch.float32, device=device)
+
+
+def tile_max(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Each 16-column tile's largest value of bf16 logits [..., V] -> bf16
+    [rows, ceil(V/16)] (what the lm_head's tile-maxima epilogue writes)."""
+    _check(logits, "logits", torch.bfloat16)
+    V = logits.shape[-1]
+    rows = logits.numel() // V
+    tiles = (V + 15) // 16
+    if out is None:
+        out = torch.empty((rows, tiles), dtype=torch.bfloat16, device=logits.device)
+    _check(out, "out", torch.bfloat16)
+    if out.numel() != rows * tiles:
+        raise _C.QvexError(f"out must hold rows * ceil(V/16) = {rows * tiles} values")
+    _C.call("qvex_tile_max_bf16", _ptr(logits), rows, V, _ptr(out), _stream())
+    return out
 
 
 def spec_accept(target: torch.Tensor, draft: torch.Tensor | None, draft_ids: torch.Tensor,
                 u_accept: torch.Tensor, u_sample: torch.Tensor, temperature: float,
                 n_accept: torch.Tensor | None = None, out_token: torch.Tensor | None = None,
                 workspace: torch.Tensor | None = None, seen: torch.Tensor | None = None,
-                presence_penalty: float = 0.0, top_k: int = 0, top_p: float = 1.0):
+                presence_penalty: float = 0.0, top_k: int = 0, top_p: float = 1.0,
+                tile_max: torch.Tensor | None = None):
     """Fused accept / residual-resample / bonus sampling for S verify steps.
 
     target fp32 or bf16 [S,k+1,V]; draft [S,k,V] of the same dtype or None (greedy
@@ -580,6 +612,11 @@ def spec_accept(target: torch.Tensor, draft: torch.Tensor | None, draft_ids: tor
     The target rows are scored as Sampler.scores (engine/sampler.py:30-52):
     presence penalty over `seen` (fp32 [V], 0/1) plus the drafts before each row,
     then top-k (0..64, 0 = off) and top-p (needs top-k) when sampling.
+    tile_max: bf16 [S*(k+1), ceil(V/16)], each target row's 16-column tile maxima
+    (qmv_packed_rstd's epilogue or tile_max()); with bf16 logits, no draft
+    logits and no presence penalty the list form (1 <= top_k <= 64) then runs as
+    one kernel that reads only the tiles that can hold the top-k (the same
+    results as without it).
     Returns (n_accept int32 [S], out_token int32 [S]) on the device."""
     bf = target.dtype == torch.bfloat16
     ldt = torch.bfloat16 if bf else torch.float32
@@ -608,6 +645,17 @@ def spec_accept(target: torch.Tensor, draft: torch.Tensor | None, draft_ids: tor
             raise _C.QvexError(f"seen must hold V={V} values")
     if workspace is None:
         workspace = spec_workspace(S, k, V, draft is not None, dev, top_k)
+    if tile_max is not None:
+        if not bf or draft is not None:
+            raise _C.QvexError("tile maxima go with bf16 target logits and no draft logits")
+        _check(tile_max, "tile_max", torch.bfloat16)
+        if tile_max.numel() != S * k1 * ((V + 15) // 16):
+            raise _C.QvexError(f"tile_max must hold S*(k+1)*ceil(V/16) = {S * k1 * ((V + 15) // 16)} values")
+        _C.call("qvex_spec_accept_tiles_bf16", _ptr(target), _ptr(tile_max), _ptr(draft_ids), _ptr(u_accept),
+                _ptr(u_sample), inv_temp, _ptr(seen) if seen is not None else None,
+                float(np.float32(presence_penalty)), int(top_k), float(np.float32(top_p)), _ptr(n_accept),
+                _ptr(out_token), S, k, V, _ptr(workspace), workspace.numel() * 4, _stream())
+        return n_accept, out_token
     _C.call("qvex_spec_accept_filtered_bf16" if bf else "qvex_spec_accept_filtered", _ptr(target),
             _ptr(draft) if draft is not None else None,
             _ptr(draft_ids), _ptr(u_accept), _ptr(u_sample), inv_temp,

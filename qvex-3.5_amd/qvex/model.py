@@ -262,6 +262,20 @@ class QLinear:
                                      bits=self.bits)
         return out.view(*lead, self.N)
 
+    def with_tile_max(self, x, tile_max: torch.Tensor) -> torch.Tensor:
+        """self(x) that also writes each output row's 16-column tile maxima into
+        tile_max (bf16 [M, ceil(N/16)]) for Sampler.accept_device: in the
+        product's epilogue for NormedRows input on packed weights (1..8 rows),
+        else by a pass over the result."""
+        if isinstance(x, NormedRows):
+            M = x.u.reshape(-1, self.K).shape[0]
+            if not self.swiglu_packed and self._takes_normed(x, M):
+                o = kernels.qmv_packed_rstd(x.u, self.packed, self.N, x.parts, x.eps, tile_max=tile_max)
+                return o.view(*x.u.shape[:-1], self.N)
+        y = self(x)
+        kernels.tile_max(y.reshape(-1, self.N), out=tile_max)
+        return y
+
     def argmax(self, x, out: torch.Tensor | None) -> torch.Tensor:
         """Greedy token per row of the product (first index of the largest bf16
         output) into out int32 [M]; x a tensor or NormedRows of 1..8 rows. out=None
@@ -906,11 +920,13 @@ class Qwen35:
         return isinstance(e, QEmbedding) and e.w4g64() is not None and e.H % 64 == 0 and e.H <= 8192
 
     def __call__(self, ids, cache, last_only=True, return_hidden=False, keep_prev=False, hidden_out=None,
-                 in_argmax=None):
+                 in_argmax=None, tile_max_out=None):
         """ids: [1, L] int -> logits [1, L or 1, V] bf16 (and pre-norm hidden [1, L, H],
         written into hidden_out when given). in_argmax = (pairs, row, slot): ids[slot]
         is first set, on the device, to the token of the deferred lm_head argmax
-        `pairs` (QLinear.argmax with out=None), row `row` (device int32 or None)."""
+        `pairs` (QLinear.argmax with out=None), row `row` (device int32 or None).
+        tile_max_out: bf16 [rows, ceil(V/16)] for the logits rows' 16-column tile
+        maxima (QLinear.with_tile_max), which Sampler.accept_device takes."""
         ids = torch.as_tensor(ids, device=self.norm.device).reshape(-1)
         L = ids.numel()
         counters = cache.counters
@@ -957,7 +973,9 @@ class Qwen35:
                 last = i + 1 == len(self.layers)
                 nxt = self.norm if last else self.layers[i + 1].ln1
                 h, st = layer.fused(h, st, c, keep_prev, nxt, h_out=hidden_out if last else None)
-            logits = self.lm_head(st[-1:] if last_only else st).view(1, -1, self.cfg.vocab_size)
+            xs = st[-1:] if last_only else st
+            logits = (self.lm_head(xs) if tile_max_out is None else self.lm_head.with_tile_max(xs, tile_max_out))
+            logits = logits.view(1, -1, self.cfg.vocab_size)
             return (logits, h.view(1, L, -1)) if return_hidden else logits
         n = rms_norm(x, self.layers[0].ln1, eps)
         for i, (layer, c) in enumerate(zip(self.layers, cache)):
@@ -970,7 +988,7 @@ class Qwen35:
             hidden = hidden_out
         if last_only:
             n = n[-1:]
-        logits = self.lm_head(n)
+        logits = self.lm_head(n) if tile_max_out is None else self.lm_head.with_tile_max(n, tile_max_out)
         logits = logits.view(1, -1, self.cfg.vocab_size)
         return (logits, hidden.view(1, L, -1)) if return_hidden else logits
 

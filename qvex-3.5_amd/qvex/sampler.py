@@ -133,15 +133,19 @@ class Sampler:
                                    u[k:].contiguous(), self.p.temperature,
                                    workspace=self._workspace(1, k, d is not None, t.device), **self._filter(t.device))
 
-    def accept_device(self, target: torch.Tensor, draft_ids: torch.Tensor, u: torch.Tensor):
+    def accept_device(self, target: torch.Tensor, draft_ids: torch.Tensor, u: torch.Tensor,
+                      tile_max: torch.Tensor | None = None):
         """accept() with the k + 1 uniforms given as a device fp32 [k+1] tensor
         (no host RNG, so the call can be captured in a graph). bf16 logits are
-        read in place."""
+        read in place. tile_max: the rows' 16-column tile maxima (the lm_head's
+        epilogue, Qwen35(..., tile_max_out=...)), which lets the filtered accept
+        run as one kernel over the few tiles that hold the top-k (same results)."""
         t = as_logits(target).reshape(1, -1, self.V)
         k = t.shape[1] - 1
+        use_tm = tile_max is not None and t.dtype == torch.bfloat16
         return kernels.spec_accept(t, None, draft_ids.reshape(1, k), u[:k].reshape(1, k), u[k:],
                                    self.p.temperature, workspace=self._workspace(1, k, False, t.device),
-                                   **self._filter(t.device))
+                                   tile_max=tile_max if use_tm else None, **self._filter(t.device))
 
     def pick(self, scores: torch.Tensor) -> torch.Tensor:
         """One token per row of scores [R, V] as made by scores() (engine/sampler.py:

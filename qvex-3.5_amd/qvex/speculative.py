@@ -275,6 +275,9 @@ class GraphedMTPCycle:
         self._out_np, self._done_np = self.out.numpy(), self.done.numpy()
         self.zero = torch.zeros(1, dtype=torch.int32, device=dev)
         self.u_buf = torch.empty(k + 1, dtype=torch.float32, device=dev)
+        # the verify logits' 16-column tile maxima, written by the lm_head's epilogue
+        # for the sampler's one-kernel list form
+        self.tile_max = torch.empty((k + 1, (model.cfg.vocab_size + 15) // 16), dtype=torch.bfloat16, device=dev)
         self._kv = [c for c in dec.cache if hasattr(c, "capacity")]
         self._rec = [c for c in dec.cache if hasattr(c, "last_width")]
         self.released = True
@@ -368,7 +371,7 @@ class GraphedMTPCycle:
             if commit is not None:               # k = 1: no later draft launch to carry it
                 self._commit(mc.counters, self.n_prev, 1)
             logits, _ = d.model(self.ids, d.cache, last_only=False, return_hidden=True, keep_prev=True,
-                                hidden_out=self.pend_h, in_argmax=(am, sel, k))
+                                hidden_out=self.pend_h, in_argmax=(am, sel, k), tile_max_out=self.tile_max)
         else:
             # greedy drafts straight from the MTP lm_head's argmax epilogue into the verify ids
             _, h = mtp(self.pend_h, self.pend_ids, mc, return_hidden=True, select=self.n_prev,
@@ -380,8 +383,8 @@ class GraphedMTPCycle:
                 if j < k - 1:                        # the last step's advance folds into the finish
                     self._commit(mc.counters, self.zero, 1)
             logits, _ = d.model(self.ids, d.cache, last_only=False, return_hidden=True, keep_prev=True,
-                                hidden_out=self.pend_h)
-        n, tok = d.sampler.accept_device(logits[0], self.drafts, self.u_buf)
+                                hidden_out=self.pend_h, tile_max_out=self.tile_max)
+        n, tok = d.sampler.accept_device(logits[0], self.drafts, self.u_buf, tile_max=self.tile_max)
         # verify commit (+n+1 on every main cache), the k - 1 speculative MTP
         # entries rolled back (net -(k-2) after the folded last advance), the
         # next feed and the next cycle's uniforms

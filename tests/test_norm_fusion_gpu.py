@@ -94,6 +94,32 @@ def test_consumer_scales_rows_by_rstd(M, N, K, swiglu):
     assert (err <= bound + 1e-6).all(), f"max excess {float((err - bound).max())}"
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 4, 8])
+@pytest.mark.parametrize("N,K", [(248320, 4096), (1040, 512), (12352, 4096)])
+def test_tile_max_epilogue(M, N, K):
+    """The product with the tile-maxima epilogue writes the same logits bit for
+    bit and, per row and 16-column tile, exactly their maximum (checked against
+    numpy on the written logits and against the separate tile_max pass)."""
+    w, s, b = synth.qmv_weights(N, K, seed=43, tag=N)
+    g = torch.Generator().manual_seed(11 * M + K)
+    hrow = (torch.randn(M, K, generator=g) * 3).to(torch.bfloat16).to(DEV)
+    nw = (1 + 0.1 * torch.randn(K, generator=g)).to(torch.bfloat16).to(DEV)
+    st = NormedRows.of(hrow, nw, EPS)
+    packed = kernels.pack_w4(to_dev(w, torch.int32), to_dev(s, torch.bfloat16), to_dev(b, torch.bfloat16))
+    y0 = kernels.qmv_packed_rstd(st.u, packed, N, st.parts, EPS)
+    tm = torch.full((M, (N + 15) // 16), float("nan"), dtype=torch.bfloat16, device=DEV)
+    y1 = kernels.qmv_packed_rstd(st.u, packed, N, st.parts, EPS, tile_max=tm)
+    tm2 = kernels.tile_max(y1)
+    torch.cuda.synchronize()
+    assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
+    yn = y1.float().cpu().numpy()
+    pad = (-N) % 16
+    ref = np.pad(yn, ((0, 0), (0, pad)), constant_values=-np.inf).reshape(M, -1, 16).max(-1)
+    assert np.array_equal(tm.float().cpu().numpy(), ref)
+    assert torch.equal(tm.view(torch.int16), tm2.view(torch.int16))
+
+
 @pytest.fixture(scope="module")
 def tiny():
     cfg = Config.tiny(layers=4, vocab=4096)

@@ -93,6 +93,123 @@ def test_list_form_ties_bit_exact(top_k, top_p):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("top_k,top_p", [(20, 0.8), (32, 1.0), (7, 0.95)])
+def test_list_form_clustered_kept_set(top_k, top_p):
+    """Kept tokens packed into few walk slots and groups, bit-exact with the
+    oracle: the largest logits at indices 0..39 (part 0, wave quarter 0: ten
+    thread slots of four elements, so one part holds the whole kept set, slots
+    hold several weights and one group holds many slots), a step with them
+    spread over two quarters of one part, and a step with ties across parts;
+    S = 6 steps of k = 7 drafts (two rows per wave of the finish kernel)."""
+    S, k, V = 6, 7, 248320
+    target, _, ids, ua, us, _ = make_case(S, k, V, seed=500 + top_k, bf16=True)
+    g = np.random.default_rng(501 + top_k)
+    base = synth.bf16_to_f32(synth.bf16_bits(40.0 + 2.0 * g.standard_normal((S, k + 1, 40)).astype(np.float32)))
+    target[0, :, :40] = base[0]
+    target[1, :, 256:276] = base[1, :, :20]                  # quarter 1 of part 0
+    target[1, :, 1024:1044] = base[1, :, 20:40]              # quarter 0 again, next i
+    target[2, :, ::8192] = 40.0                              # one tie in every part
+    target[3, :, :64] = 40.0                                 # 64 equal maxima in one part
+    ids[:4] = g.integers(0, 40, size=(4, k)).astype(np.int32)
+    ua[:4] = g.random((4, k)).astype(np.float32) * 0.3
+    assert_same(*run_both(target, None, ids, ua, us, 0.7, top_k=top_k, top_p=top_p))
+
+
+def run_tiles(target, ids, ua, us, T, **kw):
+    """spec_accept through the one-kernel list form (tile maxima of bf16 target
+    rows), against the oracle on the same inputs."""
+    t = torch.from_numpy(target).to(DEV).to(torch.bfloat16)
+    S, k1, V = target.shape
+    tm = kernels.tile_max(t.reshape(S * k1, V))
+    n, tok = kernels.spec_accept(t, None, torch.from_numpy(ids).to(DEV), torch.from_numpy(ua).to(DEV),
+                                 torch.from_numpy(us).to(DEV), T, tile_max=tm, **kw)
+    torch.cuda.synchronize()
+    n_o, tok_o = oracle.spec_accept(target, None, ids, ua, us, inv(T), threads=16, **kw)
+    return n.cpu().numpy(), tok.cpu().numpy(), n_o, tok_o
+
+
+TILE_CASES = [
+    # S, k, V, T, top_k, top_p, penalty
+    (12, 3, 248320, 0.7, 20, 0.8, 0.0),          # the decode cycle's call
+    (12, 3, 248320, 0.7, 20, 0.95, 0.0),
+    (16, 2, 50048, 1.0, 8, 1.0, 0.0),            # top-k only, ties at the k-th value
+    (16, 4, 20096, 0.7, 64, 0.5, 0.0),           # wide k, tight p
+    (16, 1, 8192, 0.9, 1, 1.0, 0.0),             # top-1
+    (8, 7, 248320, 0.6, 32, 0.9, 0.0),           # k = 7
+    (24, 0, 248320, 0.7, 20, 0.95, 0.0),         # plain sampling (k = 0)
+    (6, 3, 248320, 0.8, 64, 0.9, 0.0),
+    (12, 3, 248320, 0.6, 20, 0.95, 1.2),         # presence penalty: the two-kernel path
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("S,k,V,T,top_k,top_p,pen", TILE_CASES)
+def test_tiles_form_bit_exact(S, k, V, T, top_k, top_p, pen):
+    target, _, ids, ua, us, seen = make_case(S, k, V, seed=S * 13 + k + top_k, bf16=True)
+    kw = dict(top_k=top_k, top_p=top_p)
+    if pen:
+        kw.update(seen=seen, presence_penalty=pen)
+        t = torch.from_numpy(target).to(DEV).to(torch.bfloat16)
+        tm = kernels.tile_max(t.reshape(-1, V))
+        n, tok = kernels.spec_accept(t, None, torch.from_numpy(ids).to(DEV), torch.from_numpy(ua).to(DEV),
+                                     torch.from_numpy(us).to(DEV), T, tile_max=tm, seen=torch.from_numpy(seen).to(DEV),
+                                     presence_penalty=pen, top_k=top_k, top_p=top_p)
+        torch.cuda.synchronize()
+        n_o, tok_o = oracle.spec_accept(target, None, ids, ua, us, inv(T), threads=16, seen=seen,
+                                        presence_penalty=pen, top_k=top_k, top_p=top_p)
+        assert_same(n.cpu().numpy(), tok.cpu().numpy(), n_o, tok_o)
+        return
+    assert_same(*run_tiles(target, ids, ua, us, T, **kw))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("top_k,top_p", [(20, 0.8), (1, 1.0), (64, 0.95), (5, 1.0), (32, 1.0)])
+def test_tiles_form_ties_and_clusters(top_k, top_p):
+    """The one-kernel list form on rows that leave its fast path (all logits
+    equal, three distinct values: too many candidate tiles or values, so the
+    block runs the two-kernel path's code; a 0.25 grid: ties at the cutoff), on
+    kept sets packed into few walk slots and groups (the largest logits at
+    indices 0..39, or in two quarters of one part; one tie in every part; 64
+    equal maxima in one part), and on ordinary rows; S = 10, k = 3, bit-exact
+    with the oracle."""
+    S, k, V = 10, 3, 248320
+    target, _, ids, ua, us, _ = make_case(S, k, V, seed=700 + top_k, bf16=True)
+    g = np.random.default_rng(701 + top_k)
+    target[0] = 1.5
+    target[1] = g.integers(0, 3, size=(k + 1, V)).astype(np.float32)
+    target[2] = np.round(g.standard_normal((k + 1, V)) * 4.0).astype(np.float32) / 4.0
+    target[3, 1:] = 0.0
+    base = synth.bf16_to_f32(synth.bf16_bits(40.0 + 2.0 * g.standard_normal((k + 1, 40)).astype(np.float32)))
+    target[4, :, :40] = base
+    target[5, :, 256:276] = base[:, :20]
+    target[5, :, 1024:1044] = base[:, 20:40]
+    target[6, :, ::8192] = 40.0
+    target[7, :, :64] = 40.0
+    ids[:8] = g.integers(0, 40, size=(8, k)).astype(np.int32)
+    ua[:8] = g.random((8, k)).astype(np.float32) * 0.3
+    assert_same(*run_tiles(target, ids, ua, us, 0.7, top_k=top_k, top_p=top_p))
+
+
+@pytest.mark.gpu
+def test_tiles_form_counters_stay_zero():
+    """The one-kernel form counts each step's finished rows in the workspace and
+    leaves the count at zero: many calls on one workspace, alternating with the
+    two-kernel path on the same workspace, all bit-exact."""
+    S, k, V = 4, 3, 248320
+    ws = kernels.spec_workspace(S, k, V, False, DEV, 20)
+    for rep in range(6):
+        target, _, ids, ua, us, _ = make_case(S, k, V, seed=900 + rep, bf16=True)
+        t = torch.from_numpy(target).to(DEV).to(torch.bfloat16)
+        tm = kernels.tile_max(t.reshape(-1, V)) if rep % 2 == 0 else None
+        n, tok = kernels.spec_accept(t, None, torch.from_numpy(ids).to(DEV), torch.from_numpy(ua).to(DEV),
+                                     torch.from_numpy(us).to(DEV), 0.7, workspace=ws, tile_max=tm, top_k=20,
+                                     top_p=0.8)
+        torch.cuda.synchronize()
+        n_o, tok_o = oracle.spec_accept(target, None, ids, ua, us, inv(0.7), threads=16, top_k=20, top_p=0.8)
+        assert_same(n.cpu().numpy(), tok.cpu().numpy(), n_o, tok_o)
+
+
+@pytest.mark.gpu
 def test_list_form_cycle_shape_many_seeds():
     """The decode cycle's call (one step, k = 3, top-k 20, top-p 0.8, T = 0.7, bf16
     logits) over 48 seeded rows of steps, bit-exact with the oracle."""
