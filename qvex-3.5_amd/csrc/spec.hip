@@ -179,6 +179,10 @@ struct SpecArgs {
   int32_t* ncand;         // [S * (k+1), P, 2] how many the part has above / at its k-th value
   int32_t* ctr;           // [S] blocks of the step that finished their row
   int32_t* rres;          // [S * (k+1), 2] each row's accept flag and draw
+  // after the one-kernel list form (tile maxima): [S * (k+1)], 1 for a row it
+  // left to the statistics and finish kernels, which then skip every other row
+  // (and leave the step counters to the arrivals); nullptr otherwise
+  const int32_t* gate;
 };
 
 __device__ __forceinline__ const void* row_ptr(const SpecArgs& a, int step, int i) {
@@ -627,7 +631,8 @@ __device__ __forceinline__ void rowstats_block(const SpecArgs& a, int p, int row
 
 template <bool BF>
 __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
-  rowstats_block<BF>(a, blockIdx.x, blockIdx.y, true);
+  if (a.gate && !a.gate[blockIdx.y]) return;                // a row the one-kernel form finished
+  rowstats_block<BF>(a, blockIdx.x, blockIdx.y, a.gate == nullptr);
 }
 
 // ---------------------------------------------------------------- filter kernel (top-k / top-p)
@@ -1796,6 +1801,7 @@ __device__ __forceinline__ void finish_decide(const SpecArgs& a, int row, int ok
 
 __global__ __launch_bounds__(NT) void spec_finish_kernel(SpecArgs a) {
   extern __shared__ float smem[];
+  if (a.gate && !a.gate[blockIdx.x]) return;                // a row the one-kernel form finished
   int ok, tok;
   finish_row(a, blockIdx.x, smem, ok, tok);
   if (threadIdx.x == 0) finish_decide(a, blockIdx.x, ok, tok);
@@ -1831,15 +1837,14 @@ constexpr int TM_CT = 256;     // candidate tiles
 constexpr int TM_CE = 512;     // candidate values
 
 struct TmSh {
-  __align__(16) float lm[NT];          // thread maxima
-  __align__(16) float v4k[4 * 64];     // each wave's top_k thread maxima
   __align__(16) float ev[TM_CE];       // candidate values (z) and indices, gathered
   __align__(16) int ej[TM_CE];
   __align__(16) float sv[TM_CE];       // the same ranked
   __align__(16) int sj[TM_CE];
+  __align__(16) uint32_t ek[TM_CE];     // candidates' rank keys
   int tiles[TM_CT];
   int scan[8];
-  float tau;
+  uint32_t tauw[4];
   float f[3];                          // c_0, S_p, cutoff
   int ok, tok, nkeep;
   // the draw, wave 0
@@ -1866,6 +1871,31 @@ __device__ __forceinline__ void wave_lds_sync() {
 __device__ __forceinline__ int rl_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
 __device__ __forceinline__ float rl_f(float v, int l) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// 16-bit key of the bf16 in the low half of h with the order of the values
+// (negative values flipped, positive ones above them), NaN mapped to 0, below
+// every value
+__device__ __forceinline__ uint32_t bf16_key(uint32_t h) {
+  h &= 0xffffu;
+  const uint32_t neg = (uint32_t)((int32_t)(h << 16) >> 31);
+  const uint32_t kk = (h ^ (neg | 0x8000u)) & 0xffffu;
+  uint32_t d = 0x7f80u - (h & 0x7fffu);                   // negative: exponent all ones, mantissa non-zero
+  asm("" : "+v"(d));
+  return kk & ((d >> 31) - 1u);
+}
+// a >= b and a > b for keys below 2^31, as 0/1 from the sign of a difference
+// (the empty asm keeps the compiler from turning it back into a compare, whose
+// lane masks it would keep in scalar registers)
+__device__ __forceinline__ int key_ge(uint32_t a, uint32_t b) {
+  uint32_t d = a - b;
+  asm("" : "+v"(d));
+  return (int)((d >> 31) ^ 1u);
+}
+__device__ __forceinline__ int key_gt(uint32_t a, uint32_t b) {
+  uint32_t d = b - a;
+  asm("" : "+v"(d));
+  return (int)(d >> 31);
 }
 
 // The fixed-order walk's draw over n <= 64 positive weights in one wave: lane
@@ -2014,8 +2044,8 @@ __device__ int tile_walk(int n, int kv, float wv, float u, TmSh& S) {
   return key_index(rl_i(kv, res));
 }
 
-__global__ __launch_bounds__(NT) void spec_tiles_kernel(SpecArgs a, const uint16_t* __restrict__ tmax, int tiles) {
-  extern __shared__ float smem[];                           // the two-kernel path's full pass
+__global__ __launch_bounds__(NT) void spec_tiles_kernel(SpecArgs a, int32_t* __restrict__ gate,
+                                                      const uint16_t* __restrict__ tmax, int tiles) {
   __shared__ TmSh S;
   const int row = blockIdx.x, k = a.k, step = row / (k + 1), i = row - step * (k + 1);
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -2033,122 +2063,112 @@ __global__ __launch_bounds__(NT) void spec_tiles_kernel(SpecArgs a, const uint16
   const float xd = din ? lg(xr, di, 1) : 0.0f;
   const float ua = i < k ? a.u_acc[(long)step * k + i] : 0.0f;
   const float u = a.u_smp[step];
-  float tm = -__builtin_inff();
+  // every comparison below is on 16-bit order keys of the bf16 values (the
+  // order of the floats, NaN lowest), counted with integer arithmetic: no
+  // compare masks, so nothing spills
+  // the thread's 64 tile keys (0 for tiles past the row), computed once, and
+  // the largest of each group of 8 (one load)
+  uint32_t tk[8 * TM_PER], gk[TM_PER];
+  uint32_t mk = 0;                                          // the thread's largest tile key
 #pragma unroll
   for (int q = 0; q < TM_PER; ++q) {
     const uint32_t w4[4] = {tv[q].x, tv[q].y, tv[q].z, tv[q].w};
+    gk[q] = 0;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float v = e & 1 ? bf16_hi(w4[e >> 1]) : bf16_lo(w4[e >> 1]);
-      tm = 8 * (t + NT * q) + e < tiles ? fmaxf(tm, v) : tm;
+      uint32_t dj = (uint32_t)(8 * (t + NT * q) + e) - (uint32_t)tiles;       // negative: j < tiles
+      asm("" : "+v"(dj));
+      tk[8 * q + e] = bf16_key(w4[e >> 1] >> (16 * (e & 1))) & (0u - (dj >> 31));
+      gk[q] = max(gk[q], tk[8 * q + e]);
     }
+    mk = max(mk, gk[q]);
   }
-  // tau: each wave ranks its lane maxima and keeps its top_k, then those 4 top_k are ranked
-  S.lm[t] = tm;
-  __syncthreads();
+  // tau: each wave's top_k-th largest thread key (ties by thread), by a bit
+  // descent over ballots; top_k threads of that wave hold a tile key >= it, so
+  // the row's k-th value is at least the largest of the four
   {
-    const float4* w4 = reinterpret_cast<const float4*>(S.lm + wave * 64);
-    int r = 0;
-#pragma unroll
-    for (int q4 = 0; q4 < 16; ++q4) {
-      const float4 o = w4[q4];
-      const float e[4] = {o.x, o.y, o.z, o.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) r += ahead(e[j], tm, 4 * q4 + j < lane);
+    const uint32_t uk = (mk << 8) | (uint32_t)(255 - t);
+    uint32_t x = 0;
+    for (int b = 23; b >= 0; --b) {
+      const uint32_t y = x | (1u << b);
+      x = __popcll(__ballot(uk >= y)) >= K ? y : x;
     }
-    if (r < K) S.v4k[wave * K + r] = tm;
+    if (lane == 0) S.tauw[wave] = x >> 8;
   }
   __syncthreads();
-  if (t < 4 * K) {
-    const float v = S.v4k[t];
-    int r = 0;
-#pragma unroll 4
-    for (int q = 0; q < 4 * K; q += 4) {
-      const float4 o = *reinterpret_cast<const float4*>(&S.v4k[q]);
-      const float e[4] = {o.x, o.y, o.z, o.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) r += ahead(e[j], v, q + j < t);
-    }
-    if (r == K - 1) S.tau = v;
-  }
-  __syncthreads();
-  const float tau = S.tau;
+  // key 0 (no tile, or NaN) never counts
+  const uint32_t tau = max(max(max(S.tauw[0], S.tauw[1]), max(S.tauw[2], S.tauw[3])), 1u);
   // the tiles that can hold a value >= tau
+  // (groups whose largest key is below tau are skipped whole: usually all)
   int c = 0;
 #pragma unroll
-  for (int q = 0; q < TM_PER; ++q) {
-    const uint32_t w4[4] = {tv[q].x, tv[q].y, tv[q].z, tv[q].w};
+  for (int q = 0; q < TM_PER; ++q)
+    if (gk[q] >= tau) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float v = e & 1 ? bf16_hi(w4[e >> 1]) : bf16_lo(w4[e >> 1]);
-      c += (int)(8 * (t + NT * q) + e < tiles) & (int)(v >= tau);
+      for (int e = 0; e < 8; ++e) c += key_ge(tk[8 * q + e], tau);
     }
-  }
   int nt;
   int off = block_excl_scan(c, S.scan, &nt);
   bool fast = nt <= TM_CT;                                  // block-uniform from here on
   if (fast) {
 #pragma unroll
-    for (int q = 0; q < TM_PER; ++q) {
-      const uint32_t w4[4] = {tv[q].x, tv[q].y, tv[q].z, tv[q].w};
+    for (int q = 0; q < TM_PER; ++q)
+      if (gk[q] >= tau) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float v = e & 1 ? bf16_hi(w4[e >> 1]) : bf16_lo(w4[e >> 1]);
-        const int j = 8 * (t + NT * q) + e;
-        if (j < tiles && v >= tau) S.tiles[off++] = j;
+        for (int e = 0; e < 8; ++e)
+          if (tk[8 * q + e] >= tau) S.tiles[off++] = 8 * (t + NT * q) + e;
       }
-    }
     __syncthreads();
     // the candidate tiles' logits, thread c taking tile c
-    float x[16];
+    uint32_t w8[8];
     int j0 = 0;
     if (t < nt) {
       j0 = 16 * S.tiles[t];
       const u32x4 l0 = load16(xr + j0), l1 = load16(xr + j0 + 8);
-      const uint32_t w8[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
-#pragma unroll
-      for (int e = 0; e < 16; ++e) x[e] = e & 1 ? bf16_hi(w8[e >> 1]) : bf16_lo(w8[e >> 1]);
+      w8[0] = l0.x; w8[1] = l0.y; w8[2] = l0.z; w8[3] = l0.w;
+      w8[4] = l1.x; w8[5] = l1.y; w8[6] = l1.z; w8[7] = l1.w;
     } else {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) x[e] = -__builtin_inff();
+      for (int e = 0; e < 8; ++e) w8[e] = 0xffffffffu;         // NaN: key 0
     }
     int ce = 0;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) ce += (int)(t < nt) & (int)(x[e] >= tau);
+    for (int e = 0; e < 16; ++e) ce += key_ge(bf16_key(w8[e >> 1] >> (16 * (e & 1))), tau);
     int ne;
     int o2 = block_excl_scan(ce, S.scan, &ne);
     fast = ne <= TM_CE;
     if (fast) {
+      if (ce > 0) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        if (t < nt && x[e] >= tau) {
-          S.ev[o2] = x[e] * a.inv_temp;
-          S.ej[o2] = j0 + e;
-          ++o2;
+        for (int e = 0; e < 16; ++e) {
+          const uint32_t kk = bf16_key(w8[e >> 1] >> (16 * (e & 1)));
+          if (kk >= tau) {
+            const float xv = e & 1 ? bf16_hi(w8[e >> 1]) : bf16_lo(w8[e >> 1]);
+            S.ev[o2] = xv * a.inv_temp;
+            S.ej[o2] = j0 + e;
+            S.ek[o2] = (kk << 15) | (uint32_t)(0x7fff - o2);   // unique, < 2^31: order of z, then slot
+            ++o2;
+          }
         }
-      if (t < 8 && ne + t < TM_CE) {                        // padding that never ranks ahead
-        S.ev[ne + t] = -__builtin_inff();
-        S.ej[ne + t] = 0x7fffffff;
       }
+      if (t < 8 && ne + t < TM_CE) S.ek[ne + t] = 0;          // padding: below every key
       __syncthreads();
+      // rank by key: the number of candidates with a larger key (z descending;
+      // equal values in slot order, which no later step depends on)
       const int n8 = min((ne + 7) & ~7, TM_CE);
       for (int cc = t; cc < ne; cc += NT) {
-        const float v = S.ev[cc];
-        const int j = S.ej[cc];
+        const uint32_t mykey = S.ek[cc];
         int r = 0;
 #pragma unroll 2
         for (int q = 0; q < n8; q += 8) {
-          const float4 va = *reinterpret_cast<const float4*>(&S.ev[q]);
-          const float4 vb = *reinterpret_cast<const float4*>(&S.ev[q + 4]);
-          const int4 ja = *reinterpret_cast<const int4*>(&S.ej[q]);
-          const int4 jb = *reinterpret_cast<const int4*>(&S.ej[q + 4]);
-          const float vv[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
-          const int jj[8] = {ja.x, ja.y, ja.z, ja.w, jb.x, jb.y, jb.z, jb.w};
-#pragma unroll
-          for (int e = 0; e < 8; ++e) r += ahead(vv[e], v, jj[e] < j);
+          const int4 ka = *reinterpret_cast<const int4*>(&S.ek[q]);
+          const int4 kb = *reinterpret_cast<const int4*>(&S.ek[q + 4]);
+          r += key_gt((uint32_t)ka.x, mykey) + key_gt((uint32_t)ka.y, mykey) + key_gt((uint32_t)ka.z, mykey) +
+               key_gt((uint32_t)ka.w, mykey) + key_gt((uint32_t)kb.x, mykey) + key_gt((uint32_t)kb.y, mykey) +
+               key_gt((uint32_t)kb.z, mykey) + key_gt((uint32_t)kb.w, mykey);
         }
-        S.sv[r] = v;
-        S.sj[r] = j;
+        S.sv[r] = S.ev[cc];
+        S.sj[r] = S.ej[cc];
       }
       __syncthreads();
       if (wave == 0) {
@@ -2175,9 +2195,10 @@ __global__ __launch_bounds__(NT) void spec_tiles_kernel(SpecArgs a, const uint16
           cutoff = mn;
         }
         int eq = 0;
-        for (int r = lane; r < ne; r += 64) eq += S.sv[r] == cutoff ? 1 : 0;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) eq += __shfl_xor(eq, o, 64);
+        for (int r0 = 0; r0 < ne; r0 += 64) {
+          const float v = r0 + lane < ne ? S.sv[r0 + lane] : -__builtin_inff();
+          eq += __popcll(__ballot(v == cutoff));
+        }
         const int n_gt = __popcll(__ballot(lane < K && cl > cutoff));
         const float Sp = (n_gt > 0 ? rl_f(pre, n_gt - 1) : 0.0f) + (float)eq * qx_expf(cutoff - c0);
         int ok = 0;
@@ -2239,20 +2260,12 @@ __global__ __launch_bounds__(NT) void spec_tiles_kernel(SpecArgs a, const uint16
       fast = S.nkeep <= 64;
     }
   }
-  int ok, tok;
-  if (fast) {
-    ok = S.ok;
-    tok = S.tok;
-  } else {
-    // the two-kernel path's work for this row, in this block: every part's
-    // statistics, then finish_row (all inlined: no call carries the arguments)
-    for (int p = 0; p < a.P; ++p) {
-      rowstats_block<true>(a, p, row, false);
-      __syncthreads();
-    }
-    finish_row(a, row, smem, ok, tok);
+  // a row the fast path cannot finish (more candidates than it holds, or a
+  // kept set over 64) is left to the statistics and finish kernels that follow
+  if (t == 0) {
+    gate[row] = fast ? 0 : 1;
+    if (fast) finish_decide(a, row, S.ok, S.tok);
   }
-  if (t == 0) finish_decide(a, row, ok, tok);
 }
 
 // ---------------------------------------------------------------- full-vocabulary scores (Sampler.scores)
@@ -2312,11 +2325,12 @@ uint64_t filter_floats(int S, int k, int P, int top_k) {
 }
 
 // list form without draft logits: per target row and part CAND_CAP candidate
-// indices and their count, then one finished-filter counter per step
+// indices and their count, then one finished-filter counter per step, each
+// row's (accept flag, draw) and its one-kernel gate
 bool cand_fits(int P) { return P * CAND_CAP <= NT * CAND_IT; }
 uint64_t cand_ints(int S, int k, int P, int top_k, int has_draft) {
   return (top_k >= 1 && top_k <= 64 && !has_draft && cand_fits(P))
-             ? (uint64_t)S * (k + 1) * P * (2 * CAND_CAP + 2) + S + (uint64_t)S * (k + 1) * 2
+             ? (uint64_t)S * (k + 1) * P * (2 * CAND_CAP + 2) + S + (uint64_t)S * (k + 1) * 3
              : 0;
 }
 
@@ -2456,11 +2470,20 @@ extern "C" int qvex_spec_accept_tiles_bf16(const uint16_t* target, const uint16_
   int32_t* ncand = reinterpret_cast<int32_t*>(cand_z + (uint64_t)S * (k + 1) * P * CAND_CAP);
   int32_t* ctr = ncand + (uint64_t)S * (k + 1) * P * 2;
   int32_t* rres = ctr + S;
+  int32_t* gate = rres + (uint64_t)S * (k + 1) * 2;
   SpecArgs a{target, nullptr, draft_ids, u_accept, u_sample, inv_temp, 0, n_accept, out_token,
              (float*)workspace, S, k, V, P, rps, seen, 0.0f, tk, use_p ? top_p : 1.0f, fws, frow, 1,
-             1, 0, 1, cand, cand_z, ncand, ctr, rres};
-  hipLaunchKernelGGL(spec_tiles_kernel, dim3(S * rps), dim3(NT), lds, (hipStream_t)stream, a, tile_max, tiles);
+             1, 0, 1, cand, cand_z, ncand, ctr, rres, nullptr};
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(spec_tiles_kernel, dim3(S * rps), dim3(NT), 0, st, a, gate, tile_max, tiles);
   QVEX_CHECK_LAUNCH("qvex_spec_accept_tiles");
+  // the rows it left: the two-kernel list form, gated to them (blocks of the
+  // other rows return at once)
+  a.gate = gate;
+  hipLaunchKernelGGL(spec_rowstats_kernel<true>, dim3(P, S * rps), dim3(NT), 0, st, a);
+  QVEX_CHECK_LAUNCH("qvex_spec_accept_tiles/rowstats");
+  hipLaunchKernelGGL(spec_finish_kernel, dim3(S * rps), dim3(NT), lds, st, a);
+  QVEX_CHECK_LAUNCH("qvex_spec_accept_tiles/finish");
   return QVEX_OK;
 }
 
