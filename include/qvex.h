@@ -351,14 +351,13 @@ int qvex_spec_accept_filtered_bf16(const uint16_t* target, const uint16_t* draft
  * one kernel with one block per target row does the work: the top_k-th
  * largest of 256 thread maxima of the tile maxima bounds the row's k-th value
  * from below, so only the tiles whose maximum reaches it are read (a few
- * hundred logits instead of the row). Rows where too many tiles or values
- * reach it are left to the two-kernel path's statistics and finish kernels,
- * launched after it in the same call and gated to those rows (their other
- * blocks return at once). Other calls are qvex_spec_accept_filtered_bf16's.
- * Results are identical to that call's (no reference counterpart: this is the
- * same interface fed by the lm_head's epilogue). workspace as there
- * (qvex_spec_accept_filtered_workspace_bytes), zero-filled before its first
- * use: the call counts each step's finished rows in it and leaves the count
+ * hundred logits instead of the row); rows where too many tiles or values
+ * reach it run the two-kernel path's work inside the same block. Other calls
+ * are qvex_spec_accept_filtered_bf16's. Results are identical to that call's
+ * (no reference counterpart: this is the same interface fed by the lm_head's
+ * epilogue). workspace as there (qvex_spec_accept_filtered_workspace_bytes),
+ * zero-filled before its first use (and outside any graph capture that uses
+ * it): the call counts each step's finished rows in it and leaves the count
  * at zero. */
 int qvex_spec_accept_tiles_bf16(const uint16_t* target, const uint16_t* tile_max, const int32_t* draft_ids,
                                 const float* u_accept, const float* u_sample, float inv_temp,

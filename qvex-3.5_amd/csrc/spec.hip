@@ -179,10 +179,6 @@ struct SpecArgs {
   int32_t* ncand;         // [S * (k+1), P, 2] how many the part has above / at its k-th value
   int32_t* ctr;           // [S] blocks of the step that finished their row
   int32_t* rres;          // [S * (k+1), 2] each row's accept flag and draw
-  // after the one-kernel list form (tile maxima): [S * (k+1)], 1 for a row it
-  // left to the statistics and finish kernels, which then skip every other row
-  // (and leave the step counters to the arrivals); nullptr otherwise
-  const int32_t* gate;
 };
 
 __device__ __forceinline__ const void* row_ptr(const SpecArgs& a, int step, int i) {
@@ -631,8 +627,7 @@ __device__ __forceinline__ void rowstats_block(const SpecArgs& a, int p, int row
 
 template <bool BF>
 __global__ __launch_bounds__(NT) void spec_rowstats_kernel(SpecArgs a) {
-  if (a.gate && !a.gate[blockIdx.y]) return;                // a row the one-kernel form finished
-  rowstats_block<BF>(a, blockIdx.x, blockIdx.y, a.gate == nullptr);
+  rowstats_block<BF>(a, blockIdx.x, blockIdx.y, true);
 }
 
 // ---------------------------------------------------------------- filter kernel (top-k / top-p)
@@ -1801,7 +1796,6 @@ __device__ __forceinline__ void finish_decide(const SpecArgs& a, int row, int ok
 
 __global__ __launch_bounds__(NT) void spec_finish_kernel(SpecArgs a) {
   extern __shared__ float smem[];
-  if (a.gate && !a.gate[blockIdx.x]) return;                // a row the one-kernel form finished
   int ok, tok;
   finish_row(a, blockIdx.x, smem, ok, tok);
   if (threadIdx.x == 0) finish_decide(a, blockIdx.x, ok, tok);
@@ -2044,8 +2038,22 @@ __device__ int tile_walk(int n, int kv, float wv, float u, TmSh& S) {
   return key_index(rl_i(kv, res));
 }
 
-__global__ __launch_bounds__(NT) void spec_tiles_kernel(SpecArgs a, int32_t* __restrict__ gate,
-                                                      const uint16_t* __restrict__ tmax, int tiles) {
+// A row the one-kernel form's fast path cannot finish, in its block: every
+// part's statistics, then the finish (the two-kernel path's code). Outlined, so
+// that the fast path keeps its own register allocation; the arguments travel by
+// value and the result comes back as (ok, tok).
+__device__ __noinline__ int2 tiles_full_row(SpecArgs a, int row) {
+  extern __shared__ float smem[];
+  for (int p = 0; p < a.P; ++p) {
+    rowstats_block<true>(a, p, row, false);
+    __syncthreads();
+  }
+  int ok, tok;
+  finish_row(a, row, smem, ok, tok);
+  return make_int2(ok, tok);
+}
+
+__global__ __launch_bounds__(NT) void spec_tiles_kernel(SpecArgs a, const uint16_t* __restrict__ tmax, int tiles) {
   __shared__ TmSh S;
   const int row = blockIdx.x, k = a.k, step = row / (k + 1), i = row - step * (k + 1);
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -2261,11 +2269,17 @@ __global__ __launch_bounds__(NT) void spec_tiles_kernel(SpecArgs a, int32_t* __r
     }
   }
   // a row the fast path cannot finish (more candidates than it holds, or a
-  // kept set over 64) is left to the statistics and finish kernels that follow
-  if (t == 0) {
-    gate[row] = fast ? 0 : 1;
-    if (fast) finish_decide(a, row, S.ok, S.tok);
+  // kept set over 64) runs the two-kernel path's work in this block
+  int ok, tok;
+  if (fast) {
+    ok = S.ok;
+    tok = S.tok;
+  } else {
+    const int2 r = tiles_full_row(a, row);
+    ok = r.x;
+    tok = r.y;
   }
+  if (t == 0) finish_decide(a, row, ok, tok);
 }
 
 // ---------------------------------------------------------------- full-vocabulary scores (Sampler.scores)
@@ -2325,12 +2339,12 @@ uint64_t filter_floats(int S, int k, int P, int top_k) {
 }
 
 // list form without draft logits: per target row and part CAND_CAP candidate
-// indices and their count, then one finished-filter counter per step, each
-// row's (accept flag, draw) and its one-kernel gate
+// indices and their count, then one finished-filter counter per step and each
+// row's (accept flag, draw)
 bool cand_fits(int P) { return P * CAND_CAP <= NT * CAND_IT; }
 uint64_t cand_ints(int S, int k, int P, int top_k, int has_draft) {
   return (top_k >= 1 && top_k <= 64 && !has_draft && cand_fits(P))
-             ? (uint64_t)S * (k + 1) * P * (2 * CAND_CAP + 2) + S + (uint64_t)S * (k + 1) * 3
+             ? (uint64_t)S * (k + 1) * P * (2 * CAND_CAP + 2) + S + (uint64_t)S * (k + 1) * 2
              : 0;
 }
 
@@ -2470,20 +2484,11 @@ extern "C" int qvex_spec_accept_tiles_bf16(const uint16_t* target, const uint16_
   int32_t* ncand = reinterpret_cast<int32_t*>(cand_z + (uint64_t)S * (k + 1) * P * CAND_CAP);
   int32_t* ctr = ncand + (uint64_t)S * (k + 1) * P * 2;
   int32_t* rres = ctr + S;
-  int32_t* gate = rres + (uint64_t)S * (k + 1) * 2;
   SpecArgs a{target, nullptr, draft_ids, u_accept, u_sample, inv_temp, 0, n_accept, out_token,
              (float*)workspace, S, k, V, P, rps, seen, 0.0f, tk, use_p ? top_p : 1.0f, fws, frow, 1,
-             1, 0, 1, cand, cand_z, ncand, ctr, rres, nullptr};
-  hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(spec_tiles_kernel, dim3(S * rps), dim3(NT), 0, st, a, gate, tile_max, tiles);
+             1, 0, 1, cand, cand_z, ncand, ctr, rres};
+  hipLaunchKernelGGL(spec_tiles_kernel, dim3(S * rps), dim3(NT), lds, (hipStream_t)stream, a, tile_max, tiles);
   QVEX_CHECK_LAUNCH("qvex_spec_accept_tiles");
-  // the rows it left: the two-kernel list form, gated to them (blocks of the
-  // other rows return at once)
-  a.gate = gate;
-  hipLaunchKernelGGL(spec_rowstats_kernel<true>, dim3(P, S * rps), dim3(NT), 0, st, a);
-  QVEX_CHECK_LAUNCH("qvex_spec_accept_tiles/rowstats");
-  hipLaunchKernelGGL(spec_finish_kernel, dim3(S * rps), dim3(NT), lds, st, a);
-  QVEX_CHECK_LAUNCH("qvex_spec_accept_tiles/finish");
   return QVEX_OK;
 }
 

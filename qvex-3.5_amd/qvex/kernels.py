@@ -575,7 +575,12 @@ def gated_delta_chunked(q, k, v, a, b, A_log, dt_bias, state, state_out=None, y=
 def spec_workspace(S: int, k: int, V: int, has_draft: bool, device, top_k: int = 0) -> torch.Tensor:
     """Sampler workspace, zero-filled: the one-kernel list form (tile maxima)
     needs its step counters at zero before the first call (every call leaves
-    them at zero)."""
+    them at zero). Refused while a graph is being captured on the current
+    stream: the zero fill would only be recorded, so a graph captured later on
+    the same workspace would start from whatever the memory held."""
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        raise _C.QvexError("spec_workspace: make the sampler workspace before the graph capture "
+                           "(Sampler.prepare_accept), not inside it")
     n = int(_C.lib().qvex_spec_accept_filtered_workspace_bytes(S, k, V, int(has_draft), int(top_k)))
     return torch.zeros((max(n, 4) + 3) // 4, dtype=torch.float32, device=device)
 

@@ -62,9 +62,23 @@ class Sampler:
 
     def _filter(self, device) -> dict:
         if self.p.presence_penalty and self.seen is None:
+            if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+                # a mask made inside a capture would be cleared on every replay
+                raise _C.QvexError("Sampler: the presence mask must exist before a graph capture "
+                                   "(Sampler.prepare_accept)")
             self.seen = torch.zeros(self.V, dtype=torch.float32, device=device)
         return dict(seen=self.seen if self.p.presence_penalty else None,
                     presence_penalty=float(self.p.presence_penalty), top_k=self.top_k, top_p=self.top_p)
+
+    def prepare_accept(self, k: int, device) -> None:
+        """Make the device buffers that accept_device() uses for k drafts (the
+        presence mask, the workspace, the draw counter) now, zero-filled: inside
+        a graph capture their fill would only be recorded (each replay of that
+        graph would clear them, and other graphs captured on them would start
+        from whatever the memory held)."""
+        self._filter(device)
+        self._workspace(1, k, False, device)
+        self.counter(device)
 
     def _workspace(self, S, k, has_draft, device, top_k=None):
         tk = self.top_k if top_k is None else top_k
@@ -104,6 +118,9 @@ class Sampler:
     def counter(self, device) -> torch.Tensor:
         """The device draw counter (one uint64 in an int64 tensor)."""
         if self.u_counter is None:
+            if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+                # a counter made inside a capture would restart on every replay
+                raise _C.QvexError("Sampler: the draw counter must exist before a graph capture")
             self.u_counter = torch.zeros(1, dtype=torch.int64, device=device)
         return self.u_counter
 

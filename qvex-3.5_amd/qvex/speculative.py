@@ -313,6 +313,9 @@ class GraphedMTPCycle:
         self.ids[:, :1] = self.feed.view(1, 1)
         # the first cycle's uniforms; each replay draws the next cycle's at its end
         d.sampler.draw_into(self.u_buf)
+        # the sampler's buffers exist, zero-filled, before any capture: the graphs
+        # of run() are captured later on them and replayed without this one
+        d.sampler.prepare_accept(k, self.u_buf.device)
         # device counters must hold the host values before they become authoritative
         d.cache.counters.sync()
         d.mtp_cache.counters.sync()

@@ -408,21 +408,14 @@ def test_decode_graph_grows_kv_caches():
     assert min(c.capacity for c in ce if hasattr(c, "capacity")) > 256
 
 
-# Two runs of this test faulted the GPU (an illegal memory access during the
-# pipelined replays of run(), the box lost): the flat head with an earlier build
-# of the one-kernel sampler, and the random head with a later one. In both the
-# tiny vocabulary (2048) sends every verify row of the captured cycle past the
-# one-kernel sampler's fast path, which then finished the row inside the same
-# kernel; no out-of-bounds access has been found in it, so the cause is not
-# shown. That in-kernel path is gone (such rows now go to the two-kernel
-# statistics and finish kernels, gated to them), and until a cause is shown
-# this case stays off the GPU.
-GRAPHED_RUN_SKIP = pytest.mark.skip(reason="faulted the GPU twice (pipelined graphed run at vocab 2048 with the "
-                                           "one-kernel sampler); cause not shown, case kept off the GPU")
-
-
+# Regression: this test once faulted the GPU (both heads, in different runs).
+# The sampler's workspace was first made inside the capture of the decoder's
+# graph, so its zero fill was only recorded there; run() replays two graphs
+# captured later, the step counters of the one-kernel sampler started from stale
+# memory, no row decided, and the finishing kernel advanced the caches by an
+# uninitialised accept count. The buffers are now made before any capture
+# (Sampler.prepare_accept) and refused inside one.
 @pytest.mark.gpu
-@GRAPHED_RUN_SKIP
 @pytest.mark.parametrize("head", ["random", "flat"])
 def test_graphed_run_checks_room_before_launching(head):
     """run(n) past the caches' room raises before any launch (no cycle is left

@@ -146,3 +146,27 @@ def test_release_then_eager_equals_eager_throughout():
     assert ta == tb
     assert [c.offset for c in a.cache] == [c.offset for c in b.cache]
     assert torch.equal(a.sampler.seen, b.sampler.seen)
+
+
+@pytest.mark.gpu
+def test_sampler_buffers_made_before_capture():
+    """The presence mask, the workspace and the draw counter are made (zero-filled)
+    by prepare_accept outside a capture; inside one they are refused, since the
+    zero fill would only be recorded and a graph captured later on the same
+    buffers would start from stale memory."""
+    V = 2048
+    s = Sampler(SamplingParams(temperature=0.7, top_k=20, top_p=0.8, presence_penalty=0.3, seed=1), V)
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(_C.QvexError, match="before a graph capture"):
+        with torch.cuda.graph(g):
+            s.prepare_accept(3, torch.device(DEV))
+    s.prepare_accept(3, torch.device(DEV))
+    ws = s._workspace(1, 3, False, torch.device(DEV))
+    torch.cuda.synchronize()
+    assert int(ws.abs().sum().item()) == 0 and int(s.seen.sum().item()) == 0
+    assert int(s.counter(torch.device(DEV)).item()) == 0
+    g2 = torch.cuda.CUDAGraph()
+    with pytest.raises(_C.QvexError, match="before the graph capture"):
+        with torch.cuda.graph(g2):
+            from qvex import kernels
+            kernels.spec_workspace(1, 3, V, False, torch.device(DEV), 20)
