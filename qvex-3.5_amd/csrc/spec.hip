@@ -1836,9 +1836,10 @@ struct TmSh {
   __align__(16) float sv[TM_CE];       // the same ranked
   __align__(16) int sj[TM_CE];
   __align__(16) uint32_t ek[TM_CE];     // candidates' rank keys
-  int tiles[TM_CT];
+  int tiles[TM_CT];                    // candidate tiles, wave w's in [64 w, 64 w + 64)
   int scan[8];
   uint32_t tauw[4];
+  int wcnt[4];                         // each wave's candidate tiles
   float f[3];                          // c_0, S_p, cutoff
   int ok, tok, nkeep;
   // the draw, wave 0
@@ -2042,7 +2043,7 @@ __device__ int tile_walk(int n, int kv, float wv, float u, TmSh& S) {
 // part's statistics, then the finish (the two-kernel path's code). Outlined, so
 // that the fast path keeps its own register allocation; the arguments travel by
 // value and the result comes back as (ok, tok).
-__device__ __noinline__ int2 tiles_full_row(SpecArgs a, int row) {
+__device__ __noinline__ int2 tiles_full_row(const SpecArgs& a, int row) {
   extern __shared__ float smem[];
   for (int p = 0; p < a.P; ++p) {
     rowstats_block<true>(a, p, row, false);
@@ -2053,18 +2054,35 @@ __device__ __noinline__ int2 tiles_full_row(SpecArgs a, int row) {
   return make_int2(ok, tok);
 }
 
-__global__ __launch_bounds__(NT) void spec_tiles_kernel(SpecArgs a, const uint16_t* __restrict__ tmax, int tiles) {
+// The tile maxima's pointer and count come first, as scalar arguments: the
+// first 14 dwords of scalar kernel arguments arrive preloaded in SGPRs (an
+// aggregate never does), so the row's tile-maxima loads go out at wave start
+// instead of after a round trip for the argument struct. The kernel-argument
+// segment then holds them and the struct as this mirror does.
+struct TilesKernArgs {
+  const uint16_t* tmax;
+  int tiles;
+  SpecArgs a;
+};
+constexpr size_t TILES_ARGS_OFFSET = offsetof(TilesKernArgs, a);
+static_assert(TILES_ARGS_OFFSET == 16, "kernel-argument layout of spec_tiles_kernel");
+
+__global__ __launch_bounds__(NT) void spec_tiles_kernel(const uint16_t* __restrict__ tmax, int tiles, SpecArgs a) {
   __shared__ TmSh S;
-  const int row = blockIdx.x, k = a.k, step = row / (k + 1), i = row - step * (k + 1);
+  const int row = blockIdx.x;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int K = a.top_k;
-  const uint16_t* tr = tmax + (long)row * tiles;
-  const uint16_t* xr = reinterpret_cast<const uint16_t*>(row_ptr(a, step, i));
   // requests first: the row's tile maxima (thread t: tiles 8 (t + NT q) + 0..7),
-  // the draft's logit and the uniforms
+  // from the preloaded arguments alone (nothing may be scheduled ahead of them,
+  // or they would wait for the argument struct's loads), then the draft's logit
+  // and the uniforms
+  const uint16_t* tr = tmax + (long)row * tiles;
   u32x4 tv[TM_PER];
 #pragma unroll
   for (int q = 0; q < TM_PER; ++q) tv[q] = load16(tr + min(8 * (t + NT * q), tiles - 8));
+  __builtin_amdgcn_sched_barrier(0);
+  const int k = a.k, step = row / (k + 1), i = row - step * (k + 1);
+  const int K = a.top_k;
+  const uint16_t* xr = reinterpret_cast<const uint16_t*>(row_ptr(a, step, i));
   const int32_t* d = a.ids + (long)step * k;
   const int di = i < k ? d[i] : -1;
   const bool din = i < k && !(di < 0 || di >= a.V);
@@ -2106,32 +2124,36 @@ __global__ __launch_bounds__(NT) void spec_tiles_kernel(SpecArgs a, const uint16
   __syncthreads();
   // key 0 (no tile, or NaN) never counts
   const uint32_t tau = max(max(max(S.tauw[0], S.tauw[1]), max(S.tauw[2], S.tauw[3])), 1u);
-  // the tiles that can hold a value >= tau
-  // (groups whose largest key is below tau are skipped whole: usually all)
-  int c = 0;
+  // the tiles that can hold a value >= tau, gathered per wave into its own 64
+  // slots of S.tiles by ballots: every branch below is on a wave-wide mask
+  // (uniform), and a group of 8 tiles whose largest key is below tau in every
+  // lane costs one ballot (usually all of them)
+  int wc = 0;                                               // uniform over the wave
+  const unsigned long long below = (1ull << lane) - 1ull;
 #pragma unroll
-  for (int q = 0; q < TM_PER; ++q)
-    if (gk[q] >= tau) {
+  for (int q = 0; q < TM_PER; ++q) {
+    if (__ballot(gk[q] >= tau)) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) c += key_ge(tk[8 * q + e], tau);
-    }
-  int nt;
-  int off = block_excl_scan(c, S.scan, &nt);
-  bool fast = nt <= TM_CT;                                  // block-uniform from here on
-  if (fast) {
-#pragma unroll
-    for (int q = 0; q < TM_PER; ++q)
-      if (gk[q] >= tau) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (tk[8 * q + e] >= tau) S.tiles[off++] = 8 * (t + NT * q) + e;
+      for (int e = 0; e < 8; ++e) {
+        const unsigned long long m = __ballot(tk[8 * q + e] >= tau);
+        if (m) {
+          const int pos = wc + __popcll(m & below);
+          if (((m >> lane) & 1ull) && pos < 64) S.tiles[64 * wave + pos] = 8 * (t + NT * q) + e;
+          wc += __popcll(m);
+        }
       }
-    __syncthreads();
-    // the candidate tiles' logits, thread c taking tile c
+    }
+  }
+  if (lane == 0) S.wcnt[wave] = wc;
+  __syncthreads();
+  const int wc0 = S.wcnt[0], wc1 = S.wcnt[1], wc2 = S.wcnt[2], wc3 = S.wcnt[3];
+  bool fast = max(max(wc0, wc1), max(wc2, wc3)) <= 64;     // block-uniform from here on
+  if (fast) {
+    // the candidate tiles' logits, lane c of wave w taking the wave's tile c
     uint32_t w8[8];
     int j0 = 0;
-    if (t < nt) {
-      j0 = 16 * S.tiles[t];
+    if (lane < S.wcnt[wave]) {
+      j0 = 16 * S.tiles[64 * wave + lane];
       const u32x4 l0 = load16(xr + j0), l1 = load16(xr + j0 + 8);
       w8[0] = l0.x; w8[1] = l0.y; w8[2] = l0.z; w8[3] = l0.w;
       w8[4] = l1.x; w8[5] = l1.y; w8[6] = l1.z; w8[7] = l1.w;
@@ -2275,7 +2297,12 @@ __global__ __launch_bounds__(NT) void spec_tiles_kernel(SpecArgs a, const uint16
     ok = S.ok;
     tok = S.tok;
   } else {
-    const int2 r = tiles_full_row(a, row);
+    // the arguments as they lie in the kernel-argument segment: a reference to
+    // the parameter itself would make the kernel copy all of it to scratch
+    // memory before its first loads
+    const SpecArgs* ap =
+        (const SpecArgs*)((const char*)__builtin_amdgcn_kernarg_segment_ptr() + TILES_ARGS_OFFSET);
+    const int2 r = tiles_full_row(*ap, row);
     ok = r.x;
     tok = r.y;
   }
@@ -2487,7 +2514,7 @@ extern "C" int qvex_spec_accept_tiles_bf16(const uint16_t* target, const uint16_
   SpecArgs a{target, nullptr, draft_ids, u_accept, u_sample, inv_temp, 0, n_accept, out_token,
              (float*)workspace, S, k, V, P, rps, seen, 0.0f, tk, use_p ? top_p : 1.0f, fws, frow, 1,
              1, 0, 1, cand, cand_z, ncand, ctr, rres};
-  hipLaunchKernelGGL(spec_tiles_kernel, dim3(S * rps), dim3(NT), lds, (hipStream_t)stream, a, tile_max, tiles);
+  hipLaunchKernelGGL(spec_tiles_kernel, dim3(S * rps), dim3(NT), lds, (hipStream_t)stream, tile_max, tiles, a);
   QVEX_CHECK_LAUNCH("qvex_spec_accept_tiles");
   return QVEX_OK;
 }
