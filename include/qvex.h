@@ -364,6 +364,25 @@ int qvex_spec_accept_tiles_bf16(const uint16_t* target, const uint16_t* tile_max
                                 const float* seen, float presence_penalty, int top_k, float top_p,
                                 int32_t* n_accept, int32_t* out_token, int S, int k, int V,
                                 void* workspace, uint64_t workspace_bytes, void* stream);
+/* 1 when qvex_spec_accept_tiles_bf16 runs its one-kernel form for a call with
+ * these arguments (and tile maxima), else 0 (no reference counterpart: the
+ * dispatch test of the entry above, for callers that choose before a graph
+ * capture). */
+int qvex_spec_accept_tiles_applies(int S, int k, int V, float inv_temp, int top_k, float presence_penalty);
+/* The one-kernel form of qvex_spec_accept_tiles_bf16 without the step
+ * decision: each target row r leaves rows[2 r] = its accept flag (rows r < k;
+ * 0 for the bonus row k) and rows[2 r + 1] = its draw (the residual draw at a rejection,
+ * the bonus draw for row k) in rows [S * (k+1)][2] int32; the step's (n, token)
+ * is the first row with flag 0 and its draw, as qvex_cycle_finish_ex decides it
+ * from rows (the accept loop of engine/speculative.py:74-81). Only for calls
+ * where qvex_spec_accept_tiles_applies is 1 (else QVEX_EINVAL); the workspace
+ * needs no zero fill (no counter is used). No reference counterpart: it splits
+ * the reference's accept loop between two launches of the decode cycle. */
+int qvex_spec_accept_tiles_rows_bf16(const uint16_t* target, const uint16_t* tile_max, const int32_t* draft_ids,
+                                     const float* u_accept, const float* u_sample, float inv_temp,
+                                     const float* seen, float presence_penalty, int top_k, float top_p,
+                                     int32_t* rows, int S, int k, int V, void* workspace,
+                                     uint64_t workspace_bytes, void* stream);
 /* tile_max[r][t] = the largest of x[r][16 t .. 16 t + 15] for bf16 rows x
  * [rows, V] (bf16 out [rows, ceil(V/16)]): the tile maxima of
  * qvex_spec_accept_tiles_bf16 for logits that no tile-maxima epilogue wrote. */
@@ -582,12 +601,17 @@ int qvex_cycle_finish(const int32_t* drafts, int k, const int32_t* n_accept, con
  * be pinned host memory): set to 1 after every entry of `out` is visible
  * system-wide, so a host that zeroes it before the launch and polls it reads
  * the cycle's result without a stream synchronisation (the reference's one
- * read per cycle, engine/speculative.py:82-85). */
+ * read per cycle, engine/speculative.py:82-85). rows (optional, [k + 1][2]
+ * int32, as qvex_spec_accept_tiles_rows_bf16 leaves them): when given,
+ * n_accept and token are not read (may be NULL) and the step is decided here,
+ * as decode() does with the verify's accept flags (engine/speculative.py:74-81):
+ * n = the first r < k whose flag is 0 (k when none), token = row n's draw. */
 int qvex_cycle_finish_ex(const int32_t* drafts, int k, const int32_t* n_accept, const int32_t* token,
                          int32_t* pend_ids, int32_t* feed, int32_t* n_prev, int32_t* out,
                          int32_t* ids_next, int32_t* main_counters, int n_main, int main_extra,
                          int32_t* mtp_counters, int n_mtp, int mtp_delta, uint64_t u_seed,
-                         uint64_t* u_counter, int u_width, float* u_out, int32_t* done, void* stream);
+                         uint64_t* u_counter, int u_width, float* u_out, int32_t* done,
+                         const int32_t* rows, void* stream);
 
 /* The sampler's uniforms (the draws of engine/speculative.py:79-81 and
  * Sampler.pick's categorical, engine/sampler.py:57-58, which use MLX's

@@ -95,9 +95,24 @@ __global__ void cycle_finish_ex_kernel(const int32_t* __restrict__ drafts, int k
                                        int32_t* __restrict__ main_counters, int n_main, int main_extra,
                                        int32_t* __restrict__ mtp_counters, int n_mtp, int mtp_delta,
                                        uint64_t u_seed, uint64_t* __restrict__ u_counter, int width,
-                                       float* __restrict__ u_out, int32_t* __restrict__ done) {
+                                       float* __restrict__ u_out, int32_t* __restrict__ done,
+                                       const int32_t* __restrict__ rows) {
   const int i = threadIdx.x;
-  const int n = *n_ptr, tok = *tok_ptr;
+  int n, tok;
+  if (rows) {
+    // the verify rows' (accept flag, draw): the first rejected draft's draw, or
+    // the bonus row's when all k are accepted
+    n = k;
+    for (int r = 0; r < k; ++r)
+      if (!rows[2 * r]) {
+        n = r;
+        break;
+      }
+    tok = rows[2 * n + 1];
+  } else {
+    n = *n_ptr;
+    tok = *tok_ptr;
+  }
   __shared__ int32_t sd[256];
   int32_t d = 0;
   if (i < k) d = drafts[i];
@@ -185,15 +200,15 @@ extern "C" int qvex_cycle_finish_ex(const int32_t* drafts, int k, const int32_t*
                                     int32_t* ids_next, int32_t* main_counters, int n_main, int main_extra,
                                     int32_t* mtp_counters, int n_mtp, int mtp_delta, uint64_t u_seed,
                                     uint64_t* u_counter, int u_width, float* u_out, int32_t* done,
-                                    void* stream) {
-  QVEX_CHECK_ARG(drafts && n_accept && token && pend_ids && feed && n_prev && out && k >= 1 && k < 255,
+                                    const int32_t* rows, void* stream) {
+  QVEX_CHECK_ARG(drafts && (rows || (n_accept && token)) && pend_ids && feed && n_prev && out && k >= 1 && k < 255,
                  "qvex_cycle_finish_ex: bad arguments");
   QVEX_CHECK_ARG((!main_counters || n_main >= 0) && (!mtp_counters || n_mtp >= 0) &&
                      (!u_out || (u_counter && u_width >= 1 && u_width <= 256)),
                  "qvex_cycle_finish_ex: bad counter or uniform arguments");
   hipLaunchKernelGGL(cycle_finish_ex_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, drafts, k, n_accept, token,
                      pend_ids, feed, n_prev, out, ids_next, main_counters, n_main, main_extra, mtp_counters, n_mtp,
-                     mtp_delta, u_seed, u_counter, u_width, u_out, done);
+                     mtp_delta, u_seed, u_counter, u_width, u_out, done, rows);
   QVEX_CHECK_LAUNCH("qvex_cycle_finish_ex");
   return QVEX_OK;
 }

@@ -179,6 +179,7 @@ struct SpecArgs {
   int32_t* ncand;         // [S * (k+1), P, 2] how many the part has above / at its k-th value
   int32_t* ctr;           // [S] blocks of the step that finished their row
   int32_t* rres;          // [S * (k+1), 2] each row's accept flag and draw
+  int rows_only;          // one-kernel form: leave (flag, draw) per row in rres; no step decision
 };
 
 __device__ __forceinline__ const void* row_ptr(const SpecArgs& a, int step, int i) {
@@ -2306,7 +2307,14 @@ __global__ __launch_bounds__(NT) void spec_tiles_kernel(const uint16_t* __restri
     ok = r.x;
     tok = r.y;
   }
-  if (t == 0) finish_decide(a, row, ok, tok);
+  if (t == 0) {
+    if (a.rows_only) {
+      a.rres[2 * row] = ok;
+      a.rres[2 * row + 1] = tok;
+    } else {
+      finish_decide(a, row, ok, tok);
+    }
+  }
 }
 
 // ---------------------------------------------------------------- full-vocabulary scores (Sampler.scores)
@@ -2478,21 +2486,33 @@ extern "C" int qvex_spec_accept_filtered_bf16(const uint16_t* target, const uint
 }
 
 
-extern "C" int qvex_spec_accept_tiles_bf16(const uint16_t* target, const uint16_t* tile_max, const int32_t* draft_ids,
-                                           const float* u_accept, const float* u_sample, float inv_temp,
-                                           const float* seen, float presence_penalty, int top_k, float top_p,
-                                           int32_t* n_accept, int32_t* out_token, int S, int k, int V,
-                                           void* workspace, uint64_t workspace_bytes, void* stream) {
+// Whether the one-kernel list form runs for a call with these arguments (tile
+// maxima given): bf16 logits without draft logits, sampling with 1 <= top_k <= 64
+// and no presence penalty, V a multiple of 128 whose tiles and parts fit.
+static bool tiles_form_applies(int S, int k, int V, float inv_temp, int top_k, float presence_penalty) {
+  const int tk = (top_k > 0 && top_k < V) ? top_k : 0;
+  return inv_temp > 0.0f && tk >= 1 && tk <= 64 && presence_penalty == 0.0f && V % 128 == 0 && V >= 128 &&
+         V / 16 <= NT * 8 * TM_PER && cand_fits(nparts(V)) && S >= 1 && k >= 0 && k <= 32 &&
+         (long)S * (k + 1) <= 65535;
+}
+
+extern "C" int qvex_spec_accept_tiles_applies(int S, int k, int V, float inv_temp, int top_k,
+                                              float presence_penalty) {
+  return tiles_form_applies(S, k, V, inv_temp, top_k, presence_penalty) ? 1 : 0;
+}
+
+// The one-kernel list form. rows == nullptr: the last row of each step decides
+// (n_accept, out_token); otherwise each row leaves its (accept flag, draw) in
+// rows [S * (k+1)][2] and nothing decides.
+static int spec_tiles_launch(const uint16_t* target, const uint16_t* tile_max, const int32_t* draft_ids,
+                             const float* u_accept, const float* u_sample, float inv_temp, const float* seen,
+                             int top_k, float top_p, int32_t* n_accept, int32_t* out_token, int32_t* rows, int S,
+                             int k, int V, void* workspace, uint64_t workspace_bytes, void* stream) {
   const int tk = (top_k > 0 && top_k < V) ? top_k : 0;
   const int P = nparts(V);
   const int tiles = V / 16;
-  const bool use = tile_max && inv_temp > 0.0f && tk >= 1 && tk <= 64 && presence_penalty == 0.0f &&
-                   V % 128 == 0 && V >= 128 && tiles <= NT * 8 * TM_PER && cand_fits(P) && S >= 1 && k >= 0 &&
-                   k <= 32 && (long)S * (k + 1) <= 65535;
-  if (!use)
-    return spec_accept_impl(target, nullptr, 1, draft_ids, u_accept, u_sample, inv_temp, seen, presence_penalty,
-                            top_k, top_p, n_accept, out_token, S, k, V, workspace, workspace_bytes, stream);
-  QVEX_CHECK_ARG(target && n_accept && out_token && workspace && u_sample, "qvex_spec_accept_tiles: null pointer");
+  QVEX_CHECK_ARG(target && workspace && u_sample && (rows || (n_accept && out_token)),
+                 "qvex_spec_accept_tiles: null pointer");
   QVEX_CHECK_ARG(k == 0 || (draft_ids && u_accept), "qvex_spec_accept_tiles: draft_ids/u_accept required for k > 0");
   QVEX_CHECK_ARG(qvex_aligned(target, 16) && qvex_aligned(tile_max, 16),
                  "qvex_spec_accept_tiles: logits and tile maxima must be 16-byte aligned");
@@ -2510,13 +2530,39 @@ extern "C" int qvex_spec_accept_tiles_bf16(const uint16_t* target, const uint16_
   float* cand_z = reinterpret_cast<float*>(cand + (uint64_t)S * (k + 1) * P * CAND_CAP);
   int32_t* ncand = reinterpret_cast<int32_t*>(cand_z + (uint64_t)S * (k + 1) * P * CAND_CAP);
   int32_t* ctr = ncand + (uint64_t)S * (k + 1) * P * 2;
-  int32_t* rres = ctr + S;
+  int32_t* rres = rows ? rows : ctr + S;
   SpecArgs a{target, nullptr, draft_ids, u_accept, u_sample, inv_temp, 0, n_accept, out_token,
              (float*)workspace, S, k, V, P, rps, seen, 0.0f, tk, use_p ? top_p : 1.0f, fws, frow, 1,
-             1, 0, 1, cand, cand_z, ncand, ctr, rres};
+             1, 0, 1, cand, cand_z, ncand, ctr, rres, rows ? 1 : 0};
   hipLaunchKernelGGL(spec_tiles_kernel, dim3(S * rps), dim3(NT), lds, (hipStream_t)stream, tile_max, tiles, a);
   QVEX_CHECK_LAUNCH("qvex_spec_accept_tiles");
   return QVEX_OK;
+}
+
+extern "C" int qvex_spec_accept_tiles_bf16(const uint16_t* target, const uint16_t* tile_max, const int32_t* draft_ids,
+                                           const float* u_accept, const float* u_sample, float inv_temp,
+                                           const float* seen, float presence_penalty, int top_k, float top_p,
+                                           int32_t* n_accept, int32_t* out_token, int S, int k, int V,
+                                           void* workspace, uint64_t workspace_bytes, void* stream) {
+  if (!tile_max || !tiles_form_applies(S, k, V, inv_temp, top_k, presence_penalty))
+    return spec_accept_impl(target, nullptr, 1, draft_ids, u_accept, u_sample, inv_temp, seen, presence_penalty,
+                            top_k, top_p, n_accept, out_token, S, k, V, workspace, workspace_bytes, stream);
+  return spec_tiles_launch(target, tile_max, draft_ids, u_accept, u_sample, inv_temp, seen, top_k, top_p, n_accept,
+                           out_token, nullptr, S, k, V, workspace, workspace_bytes, stream);
+}
+
+extern "C" int qvex_spec_accept_tiles_rows_bf16(const uint16_t* target, const uint16_t* tile_max,
+                                                const int32_t* draft_ids, const float* u_accept,
+                                                const float* u_sample, float inv_temp, const float* seen,
+                                                float presence_penalty, int top_k, float top_p, int32_t* rows, int S,
+                                                int k, int V, void* workspace, uint64_t workspace_bytes,
+                                                void* stream) {
+  QVEX_CHECK_ARG(tile_max && rows, "qvex_spec_accept_tiles_rows: tile_max and rows are required");
+  QVEX_CHECK_ARG(tiles_form_applies(S, k, V, inv_temp, top_k, presence_penalty),
+                 "qvex_spec_accept_tiles_rows: the one-kernel form does not apply to this call (see "
+                 "qvex_spec_accept_tiles_applies)");
+  return spec_tiles_launch(target, tile_max, draft_ids, u_accept, u_sample, inv_temp, seen, top_k, top_p, nullptr,
+                           nullptr, rows, S, k, V, workspace, workspace_bytes, stream);
 }
 
 // tile_max[r][t] = the largest of x[r][16 t .. 16 t + 15] (bf16; -inf for no value)

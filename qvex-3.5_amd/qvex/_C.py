@@ -50,6 +50,7 @@ SIGNATURES: dict[str, list] = {
     "qvex_spec_accept_filtered": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P, U64, P],
     "qvex_spec_accept_filtered_bf16": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P, U64, P],
     "qvex_spec_accept_tiles_bf16": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P, U64, P],
+    "qvex_spec_accept_tiles_rows_bf16": [P, P, P, P, P, F, P, F, I, F, P, I, I, I, P, U64, P],
     "qvex_tile_max_bf16": [P, I, I, P, P],
     "qvex_spec_accept_filtered_bf16_noalloc": [P, P, P, P, P, F, P, F, I, F, P, P, I, I, I, P],
     "qvex_sampler_scores": [P, I, I, I, P, F, F, I, F, P, P, U64, P],
@@ -64,7 +65,7 @@ SIGNATURES: dict[str, list] = {
     "qvex_commit_step": [P, I, P, I, P],
     "qvex_gather_row": [P, LNG, P, I, P, I, P],
     "qvex_assemble_ids": [P, P, I, P, P],
-    "qvex_cycle_finish_ex": [P, I, P, P, P, P, P, P, P, P, I, I, P, I, I, U64, P, I, P, P, P],
+    "qvex_cycle_finish_ex": [P, I, P, P, P, P, P, P, P, P, I, I, P, I, I, U64, P, I, P, P, P, P],
     "qvex_cycle_finish": [P, I, P, P, P, P, P, P, P],
     "qvex_philox_uniforms": [U64, P, I, P, P],
     "qvex_gated_rmsnorm": [P, P, LNG, I, P, P, I, I, F, P],
@@ -76,10 +77,10 @@ SIGNATURES: dict[str, list] = {
     "qvex_rope_table": [I, F, I, P, P],
 }
 
-# qvex_abi_version() of the library these bindings match (6: the done flag of
-# qvex_cycle_finish_ex; 4: qvex_mtp_input, qvex_embed_rms_parts, the deferred
+# qvex_abi_version() of the library these bindings match (7: the rows argument
+# of qvex_cycle_finish_ex; 6: the done flag of qvex_cycle_finish_ex; 4: qvex_mtp_input, qvex_embed_rms_parts, the deferred
 # reduction of qvex_qmv_w4g64_packed_argmax)
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lib: ctypes.CDLL | None = None
 
@@ -116,6 +117,8 @@ def lib() -> ctypes.CDLL:
         L.qvex_sampler_scores_workspace_bytes.argtypes = [I, I, I]
         L.qvex_qmv_w4g64_argmax_workspace_bytes.restype = U64
         L.qvex_qmv_w4g64_argmax_workspace_bytes.argtypes = [I, I]
+        L.qvex_spec_accept_tiles_applies.restype = I          # 1 / 0, not a status
+        L.qvex_spec_accept_tiles_applies.argtypes = [I, I, I, F, I, F]
         for name, args in SIGNATURES.items():
             fn = getattr(L, name)
             fn.argtypes = args
@@ -136,4 +139,5 @@ def exported_symbols() -> list[str]:
     return ["qvex_last_error", "qvex_abi_version", "qvex_spec_accept_workspace_bytes",
             "qvex_attn_workspace_bytes", "qvex_w4g64_packed_bytes",
             "qvex_gdn_chunked_workspace_bytes", "qvex_spec_accept_filtered_workspace_bytes",
-            "qvex_qmv_w4g64_argmax_workspace_bytes", "qvex_sampler_scores_workspace_bytes", *SIGNATURES]
+            "qvex_qmv_w4g64_argmax_workspace_bytes", "qvex_sampler_scores_workspace_bytes",
+            "qvex_spec_accept_tiles_applies", *SIGNATURES]

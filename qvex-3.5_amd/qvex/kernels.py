@@ -670,6 +670,58 @@ def spec_accept(target: torch.Tensor, draft: torch.Tensor | None, draft_ids: tor
     return n_accept, out_token
 
 
+def _inv_temp(temperature: float) -> float:
+    import numpy as np
+    return float(np.float32(1.0) / np.float32(temperature)) if temperature > 0 else 0.0
+
+
+def tiles_rows_apply(S: int, k: int, V: int, temperature: float, top_k: int, presence_penalty: float) -> bool:
+    """Whether spec_accept_rows (the one-kernel form from tile maxima) serves a
+    call with these arguments: bf16 logits, no draft logits, sampling with
+    1 <= top_k <= 64, no presence penalty, V a multiple of 128 that fits."""
+    import numpy as np
+    return bool(_C.lib().qvex_spec_accept_tiles_applies(S, k, V, _inv_temp(temperature), int(top_k),
+                                                        float(np.float32(presence_penalty))))
+
+
+def spec_accept_rows(target: torch.Tensor, draft_ids: torch.Tensor, u_accept: torch.Tensor, u_sample: torch.Tensor,
+                     temperature: float, tile_max: torch.Tensor, rows: torch.Tensor | None = None,
+                     workspace: torch.Tensor | None = None, seen: torch.Tensor | None = None,
+                     presence_penalty: float = 0.0, top_k: int = 0, top_p: float = 1.0) -> torch.Tensor:
+    """spec_accept's one-kernel form without the step decision: each target row
+    leaves (accept flag, draw) in rows int32 [S*(k+1), 2] (the flag of row k, the
+    bonus row, is 0 and unused); a step's (n, token) is its first row with flag
+    0 among rows 0..k-1 (else row k) and that row's draw, which the decode
+    cycle's finishing kernel takes (cycle_finish_ex with rows). Only where
+    tiles_rows_apply holds; bf16 target [S,k+1,V] with its tile maxima."""
+    import numpy as np
+    _check(target, "target", torch.bfloat16, 3)
+    S, k1, V = target.shape
+    k = k1 - 1
+    _check(draft_ids, "draft_ids", torch.int32)
+    _check(u_accept, "u_accept", torch.float32)
+    _check(u_sample, "u_sample", torch.float32)
+    if draft_ids.numel() != S * k or u_accept.numel() != S * k or u_sample.numel() != S:
+        raise _C.QvexError("draft_ids/u_accept must hold S*k values and u_sample S values")
+    _check(tile_max, "tile_max", torch.bfloat16)
+    if tile_max.numel() != S * k1 * ((V + 15) // 16):
+        raise _C.QvexError(f"tile_max must hold S*(k+1)*ceil(V/16) = {S * k1 * ((V + 15) // 16)} values")
+    if not tiles_rows_apply(S, k, V, temperature, top_k, presence_penalty):
+        raise _C.QvexError("spec_accept_rows: the one-kernel form does not apply to this call")
+    if rows is None:
+        rows = torch.empty((S * k1, 2), dtype=torch.int32, device=target.device)
+    _check(rows, "rows", torch.int32)
+    if rows.numel() != 2 * S * k1:
+        raise _C.QvexError(f"rows must hold 2*S*(k+1) = {2 * S * k1} values")
+    if workspace is None:
+        workspace = spec_workspace(S, k, V, False, target.device, top_k)
+    _C.call("qvex_spec_accept_tiles_rows_bf16", _ptr(target), _ptr(tile_max), _ptr(draft_ids), _ptr(u_accept),
+            _ptr(u_sample), _inv_temp(temperature), _ptr(seen) if seen is not None else None,
+            float(np.float32(presence_penalty)), int(top_k), float(np.float32(top_p)), _ptr(rows), S, k, V,
+            _ptr(workspace), workspace.numel() * 4, _stream())
+    return rows
+
+
 # ---------------------------------------------------------------- KV cache layouts
 
 def kv_tile_k(k: torch.Tensor) -> torch.Tensor:

@@ -164,6 +164,23 @@ class Sampler:
                                    self.p.temperature, workspace=self._workspace(1, k, False, t.device),
                                    tile_max=tile_max if use_tm else None, **self._filter(t.device))
 
+    def accept_rows_device(self, target: torch.Tensor, draft_ids: torch.Tensor, u: torch.Tensor,
+                           tile_max: torch.Tensor, rows: torch.Tensor | None = None):
+        """accept_device() without the step decision, when its one-kernel form
+        applies (bf16 logits, top-k 1..64, no penalty): each of the k + 1 rows
+        leaves (accept flag, draw) in rows [k+1, 2] for the decode cycle's
+        finishing kernel to decide; returns rows, or None when the form does not
+        apply (then use accept_device)."""
+        t = as_logits(target).reshape(1, -1, self.V)
+        k = t.shape[1] - 1
+        f = self._filter(t.device)
+        if t.dtype != torch.bfloat16 or not kernels.tiles_rows_apply(1, k, self.V, self.p.temperature,
+                                                                     f["top_k"], f["presence_penalty"]):
+            return None
+        return kernels.spec_accept_rows(t, draft_ids.reshape(1, k), u[:k].reshape(1, k), u[k:],
+                                        self.p.temperature, tile_max, rows=rows,
+                                        workspace=self._workspace(1, k, False, t.device), **f)
+
     def pick(self, scores: torch.Tensor) -> torch.Tensor:
         """One token per row of scores [R, V] as made by scores() (engine/sampler.py:
         57-58): argmax when greedy, else a categorical draw with probabilities

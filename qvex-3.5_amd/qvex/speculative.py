@@ -278,6 +278,9 @@ class GraphedMTPCycle:
         # the verify logits' 16-column tile maxima, written by the lm_head's epilogue
         # for the sampler's one-kernel list form
         self.tile_max = torch.empty((k + 1, (model.cfg.vocab_size + 15) // 16), dtype=torch.bfloat16, device=dev)
+        # the verify rows' (accept flag, draw) when the sampler's one-kernel form
+        # applies: the finishing kernel decides the step from them
+        self.rows = torch.zeros((k + 1, 2), dtype=torch.int32, device=dev)
         self._kv = [c for c in dec.cache if hasattr(c, "capacity")]
         self._rec = [c for c in dec.cache if hasattr(c, "last_width")]
         self.released = True
@@ -387,16 +390,22 @@ class GraphedMTPCycle:
                     self._commit(mc.counters, self.zero, 1)
             logits, _ = d.model(self.ids, d.cache, last_only=False, return_hidden=True, keep_prev=True,
                                 hidden_out=self.pend_h, tile_max_out=self.tile_max)
-        n, tok = d.sampler.accept_device(logits[0], self.drafts, self.u_buf, tile_max=self.tile_max)
+        rows = d.sampler.accept_rows_device(logits[0], self.drafts, self.u_buf, self.tile_max, rows=self.rows)
+        if rows is None:
+            n, tok = d.sampler.accept_device(logits[0], self.drafts, self.u_buf, tile_max=self.tile_max)
+            n_p, tok_p, rows_p = _ptr(n), _ptr(tok), None
+        else:
+            n_p = tok_p = None
+            rows_p = _ptr(rows)
         # verify commit (+n+1 on every main cache), the k - 1 speculative MTP
         # entries rolled back (net -(k-2) after the folded last advance), the
         # next feed and the next cycle's uniforms
-        _C.call("qvex_cycle_finish_ex", _ptr(self.drafts), k, _ptr(n), _ptr(tok), _ptr(self.pend_ids),
+        _C.call("qvex_cycle_finish_ex", _ptr(self.drafts), k, n_p, tok_p, _ptr(self.pend_ids),
                 _ptr(self.feed), _ptr(self.n_prev), _ptr(out), _ptr(self.ids),
                 d.cache.counters.dev.data_ptr(), d.cache.counters.dev.numel(), 1,
                 mc.counters.dev.data_ptr(), mc.counters.dev.numel(), -(k - 2) if k > 1 else 0,
                 d.sampler.seed, d.sampler.counter(self.u_buf.device).data_ptr(), k + 1, _ptr(self.u_buf),
-                None if done is None else done.data_ptr(), _stream())
+                None if done is None else done.data_ptr(), rows_p, _stream())
         d.sampler.observe_result(out)
 
     def room(self) -> int:

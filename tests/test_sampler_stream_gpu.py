@@ -42,7 +42,8 @@ def test_device_uniforms_equal_oracle_stream():
     res = torch.zeros(k + 2, dtype=torch.int32, device=DEV)
     u = torch.empty(k + 1, dtype=torch.float32, device=DEV)
     _C.call("qvex_cycle_finish_ex", _ptr(ids) + 4, k, _ptr(n_t), _ptr(tok), _ptr(pend), _ptr(feed), _ptr(nprev),
-            _ptr(res), _ptr(ids), None, 0, 0, None, 0, 0, seed, counter.data_ptr(), k + 1, _ptr(u), None, _stream())
+            _ptr(res), _ptr(ids), None, 0, 0, None, 0, 0, seed, counter.data_ptr(), k + 1, _ptr(u), None, None,
+            _stream())
     torch.cuda.synchronize()
     for j, out in enumerate(outs):
         np.testing.assert_array_equal(out.cpu().numpy(), oracle.philox_uniforms(seed, ev0 + j, out.numel()))
@@ -66,7 +67,7 @@ def test_cycle_finish_done_flag_in_pinned_memory():
     done = torch.zeros(1, dtype=torch.int32, pin_memory=True)
     flag = done.numpy()
     _C.call("qvex_cycle_finish_ex", _ptr(ids) + 4, k, _ptr(n_t), _ptr(tok), _ptr(pend), _ptr(feed), _ptr(nprev),
-            out.data_ptr(), _ptr(ids), None, 0, 0, None, 0, 0, 0, None, 0, None, done.data_ptr(), _stream())
+            out.data_ptr(), _ptr(ids), None, 0, 0, None, 0, 0, 0, None, 0, None, done.data_ptr(), None, _stream())
     ev = torch.cuda.Event()
     ev.record()
     spins = 0
@@ -76,6 +77,33 @@ def test_cycle_finish_done_flag_in_pinned_memory():
     assert out.numpy().tolist() == [2, 99, 11, 22, 33]
     torch.cuda.synchronize()
     assert pend.tolist() == [11, 22, 99, 0] and int(feed) == 99 and int(nprev) == 2 and int(ids[0]) == 99
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("flags,n_want", [([1, 1, 1, 0], 3), ([1, 0, 1, 0], 1), ([0, 1, 1, 0], 0)])
+def test_cycle_finish_decides_from_rows(flags, n_want):
+    """With rows (each verify row's accept flag and draw), the finishing kernel
+    takes the first rejection's draw (or the bonus row's) and does the same
+    bookkeeping as when given (n, token)."""
+    k = 3
+    draws = [101, 202, 303, 404]
+    rows = torch.tensor([[f, d] for f, d in zip(flags, draws)], dtype=torch.int32, device=DEV)
+    outs = []
+    for use_rows in (True, False):
+        ids = torch.tensor([7, 11, 22, 33], dtype=torch.int32, device=DEV)
+        n_t = torch.tensor([n_want], dtype=torch.int32, device=DEV)
+        tok = torch.tensor([draws[n_want]], dtype=torch.int32, device=DEV)
+        pend, feed, nprev = (torch.zeros(k + 1, dtype=torch.int32, device=DEV),
+                             torch.zeros(1, dtype=torch.int32, device=DEV), torch.zeros(1, dtype=torch.int32, device=DEV))
+        ctr = torch.tensor([5, 9], dtype=torch.int32, device=DEV)
+        res = torch.zeros(k + 2, dtype=torch.int32, device=DEV)
+        _C.call("qvex_cycle_finish_ex", _ptr(ids) + 4, k, None if use_rows else _ptr(n_t),
+                None if use_rows else _ptr(tok), _ptr(pend), _ptr(feed), _ptr(nprev), _ptr(res), _ptr(ids),
+                _ptr(ctr), 2, 1, None, 0, 0, 0, None, 0, None, None, _ptr(rows) if use_rows else None, _stream())
+        torch.cuda.synchronize()
+        outs.append([t.cpu().tolist() for t in (res, pend, feed, nprev, ids, ctr)])
+    assert outs[0] == outs[1]
+    assert outs[0][0][:2] == [n_want, draws[n_want]] and outs[0][5] == [5 + n_want + 1, 9 + n_want + 1]
 
 
 @pytest.mark.gpu

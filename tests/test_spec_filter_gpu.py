@@ -190,6 +190,52 @@ def test_tiles_form_ties_and_clusters(top_k, top_p):
     assert_same(*run_tiles(target, ids, ua, us, 0.7, top_k=top_k, top_p=top_p))
 
 
+def decide_rows(rows, S, k):
+    """A step's (n, token) from its rows' (accept flag, draw), as the decode
+    loop decides (engine/speculative.py:74-81): the first rejected draft's draw,
+    or the bonus row's when all k are accepted."""
+    rows = rows.reshape(S, k + 1, 2)
+    n = np.full(S, k, dtype=np.int32)
+    for s in range(S):
+        for r in range(k):
+            if rows[s, r, 0] == 0:
+                n[s] = r
+                break
+    return n, rows[np.arange(S), n, 1].astype(np.int32)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("S,k,V,T,top_k,top_p,pen", [c for c in TILE_CASES if c[6] == 0.0])
+def test_tiles_rows_form_bit_exact(S, k, V, T, top_k, top_p, pen):
+    """The one-kernel form without the step decision (spec_accept_rows, what the
+    decode cycle runs): deciding each step from its rows gives the oracle's
+    (n, token), and rows on which ties force the in-block slow path do too."""
+    target, _, ids, ua, us, _ = make_case(S, k, V, seed=S * 17 + k + top_k, bf16=True)
+    if S >= 3 and V >= 8192:
+        target[0] = 1.5                                   # all equal: the slow path
+        target[1, :, :64] = 40.0                          # 64 equal maxima
+    t = torch.from_numpy(target).to(DEV).to(torch.bfloat16)
+    tm = kernels.tile_max(t.reshape(-1, V))
+    assert kernels.tiles_rows_apply(S, k, V, T, top_k, 0.0)
+    rows = kernels.spec_accept_rows(t, torch.from_numpy(ids).to(DEV), torch.from_numpy(ua).to(DEV),
+                                    torch.from_numpy(us).to(DEV), T, tm, top_k=top_k, top_p=top_p)
+    torch.cuda.synchronize()
+    n, tok = decide_rows(rows.cpu().numpy(), S, k)
+    n_o, tok_o = oracle.spec_accept(target, None, ids, ua, us, inv(T), threads=16, top_k=top_k, top_p=top_p)
+    assert_same(n, tok, n_o, tok_o)
+
+
+def test_tiles_rows_apply_conditions():
+    """The one-kernel form serves bf16 sampling with 1 <= top_k <= 64, no
+    penalty and V a multiple of 128 (the C-ABI query, no GPU call)."""
+    assert kernels.tiles_rows_apply(1, 3, 248320, 0.7, 20, 0.0)
+    assert not kernels.tiles_rows_apply(1, 3, 248320, 0.7, 20, 0.3)     # penalty
+    assert not kernels.tiles_rows_apply(1, 3, 248320, 0.0, 20, 0.0)     # greedy
+    assert not kernels.tiles_rows_apply(1, 3, 248320, 0.7, 0, 0.0)      # no top-k
+    assert not kernels.tiles_rows_apply(1, 3, 248320, 0.7, 65, 0.0)     # wide top-k
+    assert not kernels.tiles_rows_apply(1, 3, 248328, 0.7, 20, 0.0)     # V % 128
+
+
 @pytest.mark.gpu
 def test_tiles_form_counters_stay_zero():
     """The one-kernel form counts each step's finished rows in the workspace and
