@@ -98,32 +98,43 @@ __global__ void cycle_finish_ex_kernel(const int32_t* __restrict__ drafts, int k
                                        float* __restrict__ u_out, int32_t* __restrict__ done,
                                        const int32_t* __restrict__ rows) {
   const int i = threadIdx.x;
+  // every read first, in one round trip (the counters' new values need only n)
+  __shared__ int32_t sd[256];
+  __shared__ int32_t srow[512];            // rows: 2 (k + 1) <= 512
+  int32_t d = 0;
+  if (i < k) d = drafts[i];
+  if (i < k) sd[i] = d;
+  if (rows && i < 2 * (k + 1)) srow[i] = rows[i];
+  if (rows && i + 256 < 2 * (k + 1)) srow[i + 256] = rows[i + 256];
+  const int32_t cm = (main_counters && i < n_main) ? main_counters[i] : 0;
+  const int32_t ct = (mtp_counters && i < n_mtp) ? mtp_counters[i] : 0;
+  const uint64_t ev = u_counter ? *u_counter : 0;
+  const int n_given = rows ? 0 : *n_ptr, tok_given = rows ? 0 : *tok_ptr;
+  __syncthreads();                       // every read of ids / the counter before the writes below
   int n, tok;
   if (rows) {
     // the verify rows' (accept flag, draw): the first rejected draft's draw, or
     // the bonus row's when all k are accepted
     n = k;
     for (int r = 0; r < k; ++r)
-      if (!rows[2 * r]) {
+      if (!srow[2 * r]) {
         n = r;
         break;
       }
-    tok = rows[2 * n + 1];
+    tok = srow[2 * n + 1];
   } else {
-    n = *n_ptr;
-    tok = *tok_ptr;
+    n = n_given;
+    tok = tok_given;
   }
-  __shared__ int32_t sd[256];
-  int32_t d = 0;
-  if (i < k) d = drafts[i];
-  if (i < k) sd[i] = d;
-  const uint64_t ev = u_counter ? *u_counter : 0;
-  __syncthreads();                       // every read of ids / the counter before the writes below
   if (i <= k) pend_ids[i] = i < n ? (i < k ? d : 0) : (i == n ? tok : 0);
-  if (main_counters)
-    for (int c = i; c < n_main; c += blockDim.x) main_counters[c] += n + main_extra;
-  if (mtp_counters)
-    for (int c = i; c < n_mtp; c += blockDim.x) mtp_counters[c] += mtp_delta;
+  if (main_counters) {
+    if (i < n_main) main_counters[i] = cm + n + main_extra;
+    for (int c = i + (int)blockDim.x; c < n_main; c += blockDim.x) main_counters[c] += n + main_extra;
+  }
+  if (mtp_counters) {
+    if (i < n_mtp) mtp_counters[i] = ct + mtp_delta;
+    for (int c = i + (int)blockDim.x; c < n_mtp; c += blockDim.x) mtp_counters[c] += mtp_delta;
+  }
   if (u_out && i < width) u_out[i] = philox_uniform(u_seed, ev, i);
   __syncthreads();
   if (i == 0) {
