@@ -572,17 +572,20 @@ def gated_delta_chunked(q, k, v, a, b, A_log, dt_bias, state, state_out=None, y=
     return y, state_out
 
 
-def spec_workspace(S: int, k: int, V: int, has_draft: bool, device, top_k: int = 0) -> torch.Tensor:
-    """Sampler workspace, zero-filled: the one-kernel list form (tile maxima)
-    needs its step counters at zero before the first call (every call leaves
-    them at zero). Refused while a graph is being captured on the current
-    stream: the zero fill would only be recorded, so a graph captured later on
-    the same workspace would start from whatever the memory held."""
-    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+def spec_workspace(S: int, k: int, V: int, has_draft: bool, device, top_k: int = 0,
+                   zeroed: bool = True) -> torch.Tensor:
+    """Sampler workspace. zeroed: filled with zeros, as the one-kernel list form
+    (spec_accept with tile maxima) needs it: it counts each step's finished rows
+    there and relies on the count starting at zero (every call leaves it at
+    zero); the other forms need no fill. A zero-filled workspace is refused
+    while a graph is being captured on the current stream: the fill would only
+    be recorded, so a graph captured later on the same workspace would start
+    from whatever the memory held."""
+    if zeroed and torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
         raise _C.QvexError("spec_workspace: make the sampler workspace before the graph capture "
                            "(Sampler.prepare_accept), not inside it")
     n = int(_C.lib().qvex_spec_accept_filtered_workspace_bytes(S, k, V, int(has_draft), int(top_k)))
-    return torch.zeros((max(n, 4) + 3) // 4, dtype=torch.float32, device=device)
+    return (torch.zeros if zeroed else torch.empty)((max(n, 4) + 3) // 4, dtype=torch.float32, device=device)
 
 
 def tile_max(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -648,8 +651,8 @@ def spec_accept(target: torch.Tensor, draft: torch.Tensor | None, draft_ids: tor
         _check(seen, "seen", torch.float32)
         if seen.numel() != V:
             raise _C.QvexError(f"seen must hold V={V} values")
-    if workspace is None:
-        workspace = spec_workspace(S, k, V, draft is not None, dev, top_k)
+    if workspace is None:   # zero-filled only for the one-kernel form's step counters
+        workspace = spec_workspace(S, k, V, draft is not None, dev, top_k, zeroed=tile_max is not None)
     if tile_max is not None:
         if not bf or draft is not None:
             raise _C.QvexError("tile maxima go with bf16 target logits and no draft logits")
@@ -713,8 +716,8 @@ def spec_accept_rows(target: torch.Tensor, draft_ids: torch.Tensor, u_accept: to
     _check(rows, "rows", torch.int32)
     if rows.numel() != 2 * S * k1:
         raise _C.QvexError(f"rows must hold 2*S*(k+1) = {2 * S * k1} values")
-    if workspace is None:
-        workspace = spec_workspace(S, k, V, False, target.device, top_k)
+    if workspace is None:   # no counter in this form: no fill needed
+        workspace = spec_workspace(S, k, V, False, target.device, top_k, zeroed=False)
     _C.call("qvex_spec_accept_tiles_rows_bf16", _ptr(target), _ptr(tile_max), _ptr(draft_ids), _ptr(u_accept),
             _ptr(u_sample), _inv_temp(temperature), _ptr(seen) if seen is not None else None,
             float(np.float32(presence_penalty)), int(top_k), float(np.float32(top_p)), _ptr(rows), S, k, V,
