@@ -177,6 +177,32 @@ def test_graphed_cycle_equals_eager(k, head):
 
 
 @pytest.mark.gpu
+def test_graphed_cycle_with_fused_decode_attention():
+    """With the fused decode attention switched on (q/k norms, RoPE and the KV
+    append inside the split kernel; off by default), the captured cycle needs
+    its RoPE table before the capture: attach() makes it, and the graphed
+    cycles emit the eager cycles' tokens (sampling, top-k / top-p)."""
+    from qvex.model import Attention
+    from qvex.speculative import GraphedMTPCycle
+    m = random_model(Config.tiny(layers=4, vocab=2048), seed=14, device=DEV, max_context=1024)
+    mtp = random_mtp(m, seed=15)
+    was = Attention.fused_decode
+    Attention.fused_decode = True
+    try:
+        params = dict(top_k=20, top_p=0.8)
+        eager = start_decoder(m, mtp, 3, 0.7, seed=6, **params)
+        graphed = GraphedMTPCycle(start_decoder(m, mtp, 3, 0.7, seed=6, **params))
+        te, tg = [], []
+        for _ in range(8):
+            te += eager.cycle()
+            tg += graphed.cycle()
+        assert te == tg
+        assert [c.offset for c in eager.cache] == [c.offset for c in graphed.dec.cache]
+    finally:
+        Attention.fused_decode = was
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("n", [0, 1, 2, 3])
 def test_cycle_finish_bookkeeping(n):
     from qvex import _C
