@@ -433,15 +433,11 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(
     aa_raw = proj_[(size_t)t * p_stride_ + ab_off_ + Hv_ + hv];
     bb_raw = proj_[(size_t)t * p_stride_ + ab_off_ + hv];
   }
-  // this row's z for every token and its norm weight, in every lane of the
-  // row (the unrolled token loop has all 16 store the row's output; the 16
-  // loads of one address are one request), rows past T re-reading row T - 1,
-  // one register each, so the loads go out together and are first waited for
-  // in the recurrence
-  uint32_t zr[FUSED_TMAX];
+  // lane t of a row: the row's z of token t (lanes past T re-read token T - 1)
+  // and its norm weight, both first waited for after the recurrence, where
+  // lane t writes token t's output
+  const uint32_t z_own = proj_[(size_t)min(l16, T - 1) * p_stride_ + z_off_ + hv * DK + dv];
   const uint32_t wr_raw = p.norm_w[dv];
-#pragma unroll
-  for (int t = 0; t < FUSED_TMAX; ++t) zr[t] = proj_[(size_t)min(t, T - 1) * p_stride_ + z_off_ + hv * DK + dv];
   // 1. conv + silu. Two kinds of task, each one wave with all of its loads
   // issued in its own iteration: a token's q and k heads (lane: channels 2l,
   // 2l+1 of both, each head normed by its own wave sum as in
@@ -540,7 +536,18 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(
   }
   __syncthreads();
 
-  // 2. recurrence; u of this block's rows to `out`, y to LDS for the sums
+  // 2. recurrence; u of this block's rows to `out`, y to LDS for the sums.
+  // Each token's snapshot address, computed once in scalar registers (without
+  // per-token snapshots every token stores to the final slot: the last store
+  // wins, no branch in the unrolled form).
+  float* snap[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    int s = cur + (p.snap_every ? 1 + t : T);
+    while (s >= n_slots_) s -= n_slots_;
+    snap[t] = state_ + s * slot_stride + row_off;
+  }
+  float ot[TT];
   auto token = [&](int t) {
     const float g = gb_s[0][t];
     const float beta = gb_s[1][t];
@@ -564,35 +571,34 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(
       st[i] = fmaf(kk[i], delta, st[i]);
       o = fmaf(st[i], qq[i], o);
     }
-    o = row16_allsum(o);
-    // the row's lane 0 sum (the lanes' sums may differ in rounding) in all 16
-    // lanes, which store the same value, so the unrolled loop stays one block
-    o = __shfl(o, lane & ~15, 64);
-    {
-      const float y = bf16_to_f32(f32_to_bf16(o));
-      ys[t][grp] = y;
-      uint32_t zb = zr[0];
-#pragma unroll
-      for (int i = 1; i < FUSED_TMAX; ++i) zb = t == i ? zr[i] : zb;
-      uint32_t wb = wr_raw;
-      asm volatile("" : "+v"(zb), "+v"(wb));
-      const float zt = bf16_to_f32((uint16_t)zb);
-      p.out[(size_t)t * Hv_ * DK + hv * DK + dv] = f32_to_bf16(silu(zt) * (bf16_to_f32((uint16_t)wb) * y));
-    }
-    // without per-token snapshots every token stores to the final slot (the
-    // last store wins): no branch in the unrolled form
-    const int slot = (p.snap_every ? 1 + t : T) % n_slots_;
-    float* dstp = state_ + wrap_add(cur, slot, n_slots_) * slot_stride + row_off;
+    ot[t] = row16_allsum(o);
     u32x4 o0, o1;
     o0.x = __float_as_uint(st[0]); o0.y = __float_as_uint(st[1]);
     o0.z = __float_as_uint(st[2]); o0.w = __float_as_uint(st[3]);
     o1.x = __float_as_uint(st[4]); o1.y = __float_as_uint(st[5]);
     o1.z = __float_as_uint(st[6]); o1.w = __float_as_uint(st[7]);
-    __builtin_nontemporal_store(o0, reinterpret_cast<u32x4*>(dstp));
-    __builtin_nontemporal_store(o1, reinterpret_cast<u32x4*>(dstp + 4));
+    __builtin_nontemporal_store(o0, reinterpret_cast<u32x4*>(snap[t]));
+    __builtin_nontemporal_store(o1, reinterpret_cast<u32x4*>(snap[t] + 4));
   };
 #pragma unroll
   for (int t = 0; t < TT; ++t) token(t);
+  // the outputs, one lane per token: lane t of a row takes lane 0's sum of
+  // token t (the lanes' sums may differ in the last bit) by a row shift, then
+  // rounds it, gates it and stores it: once per (row, token) instead of in all
+  // 16 lanes inside the state chain
+  float orow = ot[0];
+#pragma unroll
+  for (int t = 1; t < TT; ++t) {
+    const float sh = row_shr_n(ot[t], t);
+    orow = l16 == t ? sh : orow;
+  }
+  if (l16 < T) {
+    const int t = l16;
+    const float y = bf16_to_f32(f32_to_bf16(orow));
+    ys[t][grp] = y;
+    const float zt = bf16_to_f32((uint16_t)z_own);
+    p.out[(size_t)t * Hv_ * DK + hv * DK + dv] = f32_to_bf16(silu(zt) * (bf16_to_f32((uint16_t)wr_raw) * y));
+  }
   __syncthreads();
   // 3. per token, the sum of y^2 over this block's rows: one wave per token,
   // lane r < RB squares row r, a DPP sum over the wave

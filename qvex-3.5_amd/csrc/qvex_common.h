@@ -82,6 +82,22 @@ __device__ __forceinline__ float row16_allsum(float v) {
   return v;
 }
 
+// Lane i of each DPP row gets lane i - n of the same row (n in 0..8, a
+// constant after unrolling; lanes i < n read 0).
+__device__ __forceinline__ float row_shr_n(float v, int n) {
+  switch (n) {
+    case 1: return dpp_row<DPP_ROW_SHR(1)>(v);
+    case 2: return dpp_row<DPP_ROW_SHR(2)>(v);
+    case 3: return dpp_row<DPP_ROW_SHR(3)>(v);
+    case 4: return dpp_row<DPP_ROW_SHR(4)>(v);
+    case 5: return dpp_row<DPP_ROW_SHR(5)>(v);
+    case 6: return dpp_row<DPP_ROW_SHR(6)>(v);
+    case 7: return dpp_row<DPP_ROW_SHR(7)>(v);
+    case 8: return dpp_row<DPP_ROW_SHR(8)>(v);
+    default: return v;
+  }
+}
+
 // Minimum over the wave in every lane (all 64 lanes active): each DPP row's
 // minimum, then the four row minima read into scalars (a minimum is order-free).
 __device__ __forceinline__ int wave_allmin(int v) {
