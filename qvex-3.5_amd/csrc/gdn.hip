@@ -422,12 +422,17 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(
     st[4] = __uint_as_float(s1.x); st[5] = __uint_as_float(s1.y);
     st[6] = __uint_as_float(s1.z); st[7] = __uint_as_float(s1.w);
   }
-  // the token's decay and beta inputs (threads t < T), converted after the conv
-  // tasks so that no wave waits on them before issuing its conv loads
+  // the tokens' decay and beta inputs: lanes t < T of the first wave without a
+  // conv task below (the last wave when every wave has one), so that their
+  // transcendentals do not lengthen a conv task's wave; converted after the
+  // conv tasks so that no wave waits on them before issuing its conv loads
+  constexpr int GATE_WAVE = T + (T + 2 * 64 / RB - 1) / (2 * 64 / RB) < NW ? T + (T + 2 * 64 / RB - 1) / (2 * 64 / RB)
+                                                                            : NW - 1;
+  const bool gate_lane = wave == GATE_WAVE && lane < T;
   float a_log = 0.0f;
   uint32_t dt_raw = 0, aa_raw = 0, bb_raw = 0;
-  if (threadIdx.x < T) {
-    const int t = threadIdx.x;
+  if (gate_lane) {
+    const int t = lane;
     a_log = p.A_log[hv];
     dt_raw = p.dt_bias[hv];
     aa_raw = proj_[(size_t)t * p_stride_ + ab_off_ + Hv_ + hv];
@@ -462,6 +467,7 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(
     s1 = silu(acc1);
   };
   const int n_vt = (T + VTOK - 1) / VTOK;
+  static_assert(VTOK == 2 * 64 / RB, "gate wave placement assumes this v-task width");
   for (int task = wave; task < T + n_vt; task += NW) {
     if (task < T) {                       // uniform over the wave
       const int t = task;
@@ -523,8 +529,8 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(
       }
     }
   }
-  if (threadIdx.x < T) {
-    const int t = threadIdx.x;
+  if (gate_lane) {
+    const int t = lane;
     // empty asm: keeps the compiler from hoisting these conversions (and the
     // wait for their loads) back above the conv tasks
     asm volatile("" : "+v"(a_log), "+v"(dt_raw), "+v"(aa_raw), "+v"(bb_raw));
