@@ -497,8 +497,8 @@ def cpu_baselines(k_spec=4, steps_sample=4):
 # ---------------------------------------------------------------- single-kernel workloads (profiling)
 
 def mixer_verify(copies=24, iters=96):
-    """The decode cycle's split DeltaNet mixer (qvex_gdn_decode_split, 4 workgroups
-    per value head) at the 9B shape for a 4-token verify with snapshots, over
+    """The decode cycle's split DeltaNet mixer (qvex_gdn_decode_split, the model's
+    workgroups per value head) at the 9B shape for a 4-token verify with snapshots, over
     rotating recurrent caches (state ring + conv ring, ~19 MB each); bytes = the
     state read + 4 snapshots written = 10 MiB per call."""
     import torch
@@ -513,7 +513,8 @@ def mixer_verify(copies=24, iters=96):
     proj = (torch.randn((4, gdn.in_proj.N), generator=g, device="cuda:0")).to(torch.bfloat16)
     us = _graph_time(lambda i: gdn.mix_split(proj, caches[i % copies][0]), iters)
     nbytes = 5 * 32 * 128 * 128 * 4
-    return {"kernel": "qvex_gdn_decode_split (4 blocks per head, T=4 with snapshots)", "us": round(us, 2),
+    return {"kernel": f"qvex_gdn_decode_split ({gdn.split_blocks} blocks per head, T=4 with snapshots)",
+            "us": round(us, 2),
             "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1), "frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
             "bytes": nbytes}
 

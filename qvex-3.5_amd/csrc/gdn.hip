@@ -386,8 +386,14 @@ __global__ __launch_bounds__(FUSED_THREADS) void gdn_decode_fused_kernel(GdnFuse
 // chain of waits for struct fields, the count, then more fields.
 //   dims0 = p_stride | R << 16, dims1 = n_slots | Hv << 8 | Hk << 16,
 //   dims2 = z_off | ab_off << 16, dims3 = C | key_dim << 16.
+// Blocks have at least 8 waves: with 8 blocks per head the 4 waves past the
+// 16 state rows only run conv tasks (a 4-token verify's T + 1 tasks stay one
+// round), while the state rows get one wave per SIMD.
+template <int NB>
+constexpr int split_threads() { return 16 * (DK / NB) < 512 ? 512 : 16 * (DK / NB); }
+
 template <int NB, int TT>
-__global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(
+__global__ __launch_bounds__(split_threads<NB>()) void gdn_decode_split_kernel(
     const int32_t* __restrict__ counter, float* __restrict__ state_, const uint16_t* __restrict__ proj_,
     uint16_t* __restrict__ ring_, const uint16_t* __restrict__ cw_, uint32_t dims0, uint32_t dims1, uint32_t dims2,
     uint32_t dims3, GdnFusedArgs p, float* ss_parts) {
@@ -396,15 +402,16 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(
   const int z_off_ = (int)(dims2 & 0xffffu), ab_off_ = (int)(dims2 >> 16);
   const int C_ = (int)(dims3 & 0xffffu), key_dim_ = (int)(dims3 >> 16);
   constexpr int RB = DK / NB;            // rows per block
-  constexpr int NTH = 16 * RB;           // threads
-  constexpr int NW = NTH / 64;           // waves
+  constexpr int NREC = 16 * RB;          // threads on state rows (the first NREC / 64 waves)
+  constexpr int NW = split_threads<NB>() / 64;   // waves
   __shared__ float qs[FUSED_TMAX][DK], ks[FUSED_TMAX][DK], vs[FUSED_TMAX][RB], ys[FUSED_TMAX][RB];
   __shared__ float gb_s[2][FUSED_TMAX];
   const int hv = blockIdx.x / NB, b = blockIdx.x % NB;
   const int hk = hv / (Hv_ / Hk_);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int grp = threadIdx.x >> 4, l16 = threadIdx.x & 15;
-  const int dv = b * RB + grp;
+  const bool rec = threadIdx.x < NREC;   // uniform per wave
+  const int dv = b * RB + (rec ? grp : 0);   // conv-only waves: a valid row, never used
   constexpr int T = TT;
   const long p0 = *counter;
   const int cur = (int)(((p0 % n_slots_) + n_slots_) % n_slots_);
@@ -412,8 +419,8 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(
   const long slot_stride = (long)Hv_ * DK * DK;
   // this block's state row first (it waits on the token count)
   const long row_off = ((long)hv * DK + dv) * DK + l16 * 8;
-  float st[8];
-  {
+  float st[8] = {};
+  if (rec) {
     const float* src = state_ + cur * slot_stride + row_off;
     const u32x4 s0 = load16(src);
     const u32x4 s1 = load16(src + 4);
@@ -553,57 +560,59 @@ __global__ __launch_bounds__(2048 / NB) void gdn_decode_split_kernel(
     while (s >= n_slots_) s -= n_slots_;
     snap[t] = state_ + s * slot_stride + row_off;
   }
-  float ot[TT];
-  auto token = [&](int t) {
-    const float g = gb_s[0][t];
-    const float beta = gb_s[1][t];
-    float kk[8], qq[8];
+  if (rec) {
+    float ot[TT];
+    auto token = [&](int t) {
+      const float g = gb_s[0][t];
+      const float beta = gb_s[1][t];
+      float kk[8], qq[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      kk[i] = ks[t][l16 * 8 + i];
-      qq[i] = qs[t][l16 * 8 + i];
+      for (int i = 0; i < 8; ++i) {
+        kk[i] = ks[t][l16 * 8 + i];
+        qq[i] = qs[t][l16 * 8 + i];
+      }
+      float kv = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        st[i] *= g;
+        kv = fmaf(st[i], kk[i], kv);
+      }
+      kv = row16_allsum(kv);
+      const float delta = (vs[t][grp] - kv) * beta;
+      float o = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        st[i] = fmaf(kk[i], delta, st[i]);
+        o = fmaf(st[i], qq[i], o);
+      }
+      ot[t] = row16_allsum(o);
+      u32x4 o0, o1;
+      o0.x = __float_as_uint(st[0]); o0.y = __float_as_uint(st[1]);
+      o0.z = __float_as_uint(st[2]); o0.w = __float_as_uint(st[3]);
+      o1.x = __float_as_uint(st[4]); o1.y = __float_as_uint(st[5]);
+      o1.z = __float_as_uint(st[6]); o1.w = __float_as_uint(st[7]);
+      __builtin_nontemporal_store(o0, reinterpret_cast<u32x4*>(snap[t]));
+      __builtin_nontemporal_store(o1, reinterpret_cast<u32x4*>(snap[t] + 4));
+    };
+#pragma unroll
+    for (int t = 0; t < TT; ++t) token(t);
+    // the outputs, one lane per token: lane t of a row takes lane 0's sum of
+    // token t (the lanes' sums may differ in the last bit) by a row shift, then
+    // rounds it, gates it and stores it: once per (row, token) instead of in all
+    // 16 lanes inside the state chain
+    float orow = ot[0];
+#pragma unroll
+    for (int t = 1; t < TT; ++t) {
+      const float sh = row_shr_n(ot[t], t);
+      orow = l16 == t ? sh : orow;
     }
-    float kv = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      st[i] *= g;
-      kv = fmaf(st[i], kk[i], kv);
+    if (l16 < T) {
+      const int t = l16;
+      const float y = bf16_to_f32(f32_to_bf16(orow));
+      ys[t][grp] = y;
+      const float zt = bf16_to_f32((uint16_t)z_own);
+      p.out[(size_t)t * Hv_ * DK + hv * DK + dv] = f32_to_bf16(silu(zt) * (bf16_to_f32((uint16_t)wr_raw) * y));
     }
-    kv = row16_allsum(kv);
-    const float delta = (vs[t][grp] - kv) * beta;
-    float o = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      st[i] = fmaf(kk[i], delta, st[i]);
-      o = fmaf(st[i], qq[i], o);
-    }
-    ot[t] = row16_allsum(o);
-    u32x4 o0, o1;
-    o0.x = __float_as_uint(st[0]); o0.y = __float_as_uint(st[1]);
-    o0.z = __float_as_uint(st[2]); o0.w = __float_as_uint(st[3]);
-    o1.x = __float_as_uint(st[4]); o1.y = __float_as_uint(st[5]);
-    o1.z = __float_as_uint(st[6]); o1.w = __float_as_uint(st[7]);
-    __builtin_nontemporal_store(o0, reinterpret_cast<u32x4*>(snap[t]));
-    __builtin_nontemporal_store(o1, reinterpret_cast<u32x4*>(snap[t] + 4));
-  };
-#pragma unroll
-  for (int t = 0; t < TT; ++t) token(t);
-  // the outputs, one lane per token: lane t of a row takes lane 0's sum of
-  // token t (the lanes' sums may differ in the last bit) by a row shift, then
-  // rounds it, gates it and stores it: once per (row, token) instead of in all
-  // 16 lanes inside the state chain
-  float orow = ot[0];
-#pragma unroll
-  for (int t = 1; t < TT; ++t) {
-    const float sh = row_shr_n(ot[t], t);
-    orow = l16 == t ? sh : orow;
-  }
-  if (l16 < T) {
-    const int t = l16;
-    const float y = bf16_to_f32(f32_to_bf16(orow));
-    ys[t][grp] = y;
-    const float zt = bf16_to_f32((uint16_t)z_own);
-    p.out[(size_t)t * Hv_ * DK + hv * DK + dv] = f32_to_bf16(silu(zt) * (bf16_to_f32((uint16_t)wr_raw) * y));
   }
   __syncthreads();
   // 3. per token, the sum of y^2 over this block's rows: one wave per token,
@@ -708,7 +717,7 @@ void launch_split_t(dim3 grid, hipStream_t st, const GdnFusedArgs& p, float* ss_
   const uint32_t d1 = (uint32_t)p.n_slots | ((uint32_t)p.Hv << 8) | ((uint32_t)p.Hk << 16);
   const uint32_t d2 = (uint32_t)p.z_off | ((uint32_t)p.ab_off << 16);
   const uint32_t d3 = (uint32_t)p.C | ((uint32_t)p.key_dim << 16);
-  hipLaunchKernelGGL((gdn_decode_split_kernel<NB, TT>), grid, dim3(2048 / NB), 0, st, p.counter, p.state, p.proj,
+  hipLaunchKernelGGL((gdn_decode_split_kernel<NB, TT>), grid, dim3(split_threads<NB>()), 0, st, p.counter, p.state, p.proj,
                      p.ring, p.cw, d0, d1, d2, d3, p, ss_parts);
 }
 
