@@ -547,7 +547,7 @@ def attn_verify(L=4, pos0=4348, copies=24, iters=96, kps=128):
     def two_launch(i):
         c = i % copies
         _C.call("qvex_attn_qk_rope", _ptr(proj), proj.stride(0), _ptr(qn), _ptr(qn), _ptr(pos), L, Hq, Hkv, D, rot,
-                1e7, 1e-6, _ptr(q), _ptr(kc[c]), _ptr(vc[c]), cap, _stream())
+                1e7, 1e-6, _ptr(q), _ptr(kc[c]), _ptr(vc[c]), cap, _ptr(tab), tab.shape[0], _stream())
         _C.call("qvex_attention", _ptr(q), _ptr(kc[c]), _ptr(vc[c]), _ptr(pos), L, Hq, Hkv, D, cap, pos0 + L, pos0 + L, kps,
                 _ptr(proj), proj.stride(0), _ptr(out), _ptr(ws), ws.numel() * 4, _stream())
 

@@ -525,11 +525,14 @@ int qvex_bf16_to_f32(const uint16_t* in, float* out, long n, void* stream);
  * head with q_norm / k_norm, NeoX-form RoPE on the first rot_dim dims at
  * positions *pos0 + l (pos0 a device int32), q written to q_out [L, Hq, D],
  * k and v appended to the caches at those positions (KVCache.update,
- * engine/model.py:156-170). proj row = [Hq x (q | gate) | Hkv x k | Hkv x v]. */
+ * engine/model.py:156-170). proj row = [Hq x (q | gate) | Hkv x k | Hkv x v].
+ * rope: NULL, or a qvex_rope_table() of rope_rows positions for rot_dim and
+ * theta, whose (cos, sin) pairs are then loaded instead of evaluated (the same
+ * values, so the same results; positions past rope_rows are evaluated). */
 int qvex_attn_qk_rope(const uint16_t* proj, long p_stride, const uint16_t* q_norm,
                       const uint16_t* k_norm, const int32_t* pos0, int L, int Hq, int Hkv, int D,
                       int rot_dim, float theta, float eps, uint16_t* q_out, uint16_t* k_cache,
-                      uint16_t* v_cache, int cap, void* stream);
+                      uint16_t* v_cache, int cap, const float* rope, int rope_rows, void* stream);
 
 /* Causal GQA attention of L queries over the cache (query l sees keys
  * 0 .. *pos0 + l), scale 1/sqrt(D), output times sigmoid(gate) from the q_proj
@@ -565,7 +568,7 @@ int qvex_attention_decode(const uint16_t* proj, long p_stride, const uint16_t* q
                           uint16_t* v_cache, int cap, int max_keys, int keys_per_split, uint16_t* out,
                           void* workspace, uint64_t workspace_bytes, void* stream);
 
-/* RoPE table for qvex_attention_decode: table[p][i] = (cos, sin) of
+/* RoPE table for qvex_attn_qk_rope and qvex_attention_decode: table[p][i] = (cos, sin) of
  * p * theta^(-2i / rot_dim), p < rows, i < rot_dim / 2 (float pairs); the angle
  * of mx.fast.rope(traditional=False) at position p (engine/model.py:222-225). */
 int qvex_rope_table(int rot_dim, float theta, int rows, float* table, void* stream);

@@ -26,4 +26,4 @@ int fail(int code, const char* fmt, ...) {
 
 extern "C" const char* qvex_last_error(void) { return qvex::g_err; }
 
-extern "C" int qvex_abi_version(void) { return 7; }
+extern "C" int qvex_abi_version(void) { return 8; }

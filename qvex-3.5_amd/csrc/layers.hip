@@ -222,15 +222,23 @@ __host__ __device__ __forceinline__ size_t vt_index(int kh, int cap, int D, int 
 // pos * theta^(-2i/rot); dims >= rot pass through. pos = *pos0 + l.
 // PER = D / 64 elements per lane, a template parameter so that every load of the
 // wave (row, norm weights, the V row) is issued before the first is waited on.
+// With a table of rope_table_kernel (rows >= pos + 1) the lane's (cos, sin) is
+// loaded as soon as the position arrives, alongside the row, instead of being
+// evaluated after the norm (powf and sincosf of a large angle: ~1 us of the
+// wave's ~2 us); the table holds the same values, so the results are the same.
 template <int PER>
 __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
     const uint16_t* __restrict__ proj, long p_stride, const uint16_t* __restrict__ q_norm,
     const uint16_t* __restrict__ k_norm, const int32_t* __restrict__ pos0, int Hq, int Hkv, int D,
     int rot, float theta, float eps, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
-    uint16_t* __restrict__ v_cache, int cap) {
+    uint16_t* __restrict__ v_cache, int cap, const float2* __restrict__ rope, int rope_rows) {
   const int l = blockIdx.x, h = blockIdx.y;  // h < Hq: query head; else kv head h - Hq
   const int lane = threadIdx.x;
   const int pos = *pos0 + l;
+  const int half = rot / 2;
+  const bool tab = rope != nullptr && pos >= 0 && pos < rope_rows;   // uniform over the wave
+  float2 cs_tab = make_float2(1.0f, 0.0f);
+  if (tab && lane < rot) cs_tab = rope[(size_t)pos * half + lane % half];
   const bool isq = h < Hq;
   const int kh = h - Hq;
   const uint16_t* src = isq ? proj + (size_t)l * p_stride + (size_t)h * 2 * D
@@ -255,14 +263,18 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
   // rotary part lives in element slot 0 (lane < 64 <= rot requires rot <= 64);
   // lane i < half pairs with lane i + half (an explicit index: an xor by half
   // pairs the right lanes only when half is a power of two)
-  const int half = rot / 2;
   if (rot > 0) {
     const float partner = __shfl(x[0], lane < half ? lane + half : lane - half, 64);
     if (lane < rot) {
-      const int i = lane % half;
-      const float inv_freq = powf(theta, -2.0f * (float)i / (float)rot);
       float sn, cs;
-      sincosf((float)pos * inv_freq, &sn, &cs);
+      if (tab) {
+        cs = cs_tab.x;
+        sn = cs_tab.y;
+      } else {
+        const int i = lane % half;
+        const float inv_freq = powf(theta, -2.0f * (float)i / (float)rot);
+        sincosf((float)pos * inv_freq, &sn, &cs);
+      }
       x[0] = lane < half ? x[0] * cs - partner * sn : partner * sn + x[0] * cs;
     }
   }
@@ -1076,13 +1088,15 @@ extern "C" int qvex_bf16_to_f32(const uint16_t* in, float* out, long n, void* st
 extern "C" int qvex_attn_qk_rope(const uint16_t* proj, long p_stride, const uint16_t* q_norm, const uint16_t* k_norm,
                                  const int32_t* pos0, int L, int Hq, int Hkv, int D, int rot_dim, float theta,
                                  float eps, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, int cap,
-                                 void* stream) {
+                                 const float* rope, int rope_rows, void* stream) {
   QVEX_CHECK_ARG(proj && q_norm && k_norm && pos0 && q_out && k_cache && v_cache, "qvex_attn_qk_rope: null pointer");
   QVEX_CHECK_ARG(L >= 1 && Hq >= 1 && Hkv >= 1 && Hq % Hkv == 0 && D % 64 == 0 && D <= 512 && rot_dim >= 0 &&
                      rot_dim <= 64 && rot_dim % 2 == 0 && cap >= 32 && cap % 32 == 0,
                  "qvex_attn_qk_rope: L=%d Hq=%d Hkv=%d D=%d rot=%d cap=%d (cap a multiple of 32)", L, Hq, Hkv, D,
                  rot_dim, cap);
   QVEX_CHECK_ARG(p_stride >= (long)Hq * 2 * D + 2L * Hkv * D, "qvex_attn_qk_rope: p_stride too small");
+  QVEX_CHECK_ARG(rope_rows >= 0 && (rope == nullptr || qvex_aligned(rope, 8)),
+                 "qvex_attn_qk_rope: rope_rows=%d (the table 8-byte aligned)", rope_rows);
   decltype(&qk_norm_rope_kernel<1>) fn = nullptr;
   switch (D / 64) {
     case 1: fn = qk_norm_rope_kernel<1>; break;
@@ -1095,7 +1109,8 @@ extern "C" int qvex_attn_qk_rope(const uint16_t* proj, long p_stride, const uint
     case 8: fn = qk_norm_rope_kernel<8>; break;
   }
   hipLaunchKernelGGL(fn, dim3(L, Hq + Hkv), dim3(64), 0, (hipStream_t)stream, proj, p_stride, q_norm, k_norm, pos0,
-                     Hq, Hkv, D, rot_dim, theta, eps, q_out, k_cache, v_cache, cap);
+                     Hq, Hkv, D, rot_dim, theta, eps, q_out, k_cache, v_cache, cap,
+                     reinterpret_cast<const float2*>(rope), rope ? rope_rows : 0);
   QVEX_CHECK_LAUNCH("qvex_attn_qk_rope");
   return QVEX_OK;
 }

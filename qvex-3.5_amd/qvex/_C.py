@@ -71,16 +71,16 @@ SIGNATURES: dict[str, list] = {
     "qvex_gated_rmsnorm": [P, P, LNG, I, P, P, I, I, F, P],
     "qvex_swiglu": [P, P, I, I, P],
     "qvex_bf16_to_f32": [P, P, LNG, P],
-    "qvex_attn_qk_rope": [P, LNG, P, P, P, I, I, I, I, I, F, F, P, P, P, I, P],
+    "qvex_attn_qk_rope": [P, LNG, P, P, P, I, I, I, I, I, F, F, P, P, P, I, P, I, P],
     "qvex_attention": [P, P, P, P, I, I, I, I, I, I, I, I, P, LNG, P, P, U64, P],
     "qvex_attention_decode": [P, LNG, P, P, P, I, I, I, I, I, F, P, I, P, P, I, I, I, P, P, U64, P],
     "qvex_rope_table": [I, F, I, P, P],
 }
 
-# qvex_abi_version() of the library these bindings match (7: the rows argument
-# of qvex_cycle_finish_ex; 6: the done flag of qvex_cycle_finish_ex; 4: qvex_mtp_input, qvex_embed_rms_parts, the deferred
+# qvex_abi_version() of the library these bindings match (8: the RoPE table of
+# qvex_attn_qk_rope; 7: the rows argument of qvex_cycle_finish_ex; 6: the done flag of qvex_cycle_finish_ex; 4: qvex_mtp_input, qvex_embed_rms_parts, the deferred
 # reduction of qvex_qmv_w4g64_packed_argmax)
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lib: ctypes.CDLL | None = None
 

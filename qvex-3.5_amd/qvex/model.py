@@ -691,9 +691,21 @@ class Attention:
                     kps, _ptr(o), _ptr(ws), ws.numel() * 4, _stream())
         else:
             q = torch.empty((L, H, D), dtype=torch.bfloat16, device=x.device)
+            # the rotation's (cos, sin) from the shared table covering the cache; a
+            # call under graph capture never makes one (decode() makes it before
+            # capturing) and without it the kernel evaluates the same angles
+            tab = None
+            if rot:
+                key = (int(rot), float(cfg.rope_theta), str(torch.device(x.device)))
+                have = _ROPE_TABLES.get(key)
+                if torch.cuda.is_current_stream_capturing():
+                    tab = have if have is not None and have.shape[0] >= cache.capacity else None
+                else:
+                    tab = rope_table(rot, cfg.rope_theta, cache.capacity, x.device)
             _C.call("qvex_attn_qk_rope", _ptr(proj), proj.stride(0), _ptr(self.q_norm), _ptr(self.k_norm), pos,
                     L, H, Hkv, D, rot, float(cfg.rope_theta), float(cfg.rms_norm_eps), _ptr(q),
-                    _ptr(cache.k), _ptr(cache.v), cache.capacity, _stream())
+                    _ptr(cache.k), _ptr(cache.v), cache.capacity, _ptr(tab) if tab is not None else 0,
+                    tab.shape[0] if tab is not None else 0, _stream())
             # keys below the position at capture stay visible on every replay
             known = min(cache.offset, max_keys) if cache.counters.graph_mode and self.late_splits else max_keys
             _C.call("qvex_attention", _ptr(q), _ptr(cache.k), _ptr(cache.v), pos, L, H, Hkv, D, cache.capacity,

@@ -20,7 +20,7 @@ import torch
 
 from . import _C
 from .kernels import _ptr, _stream
-from .model import Attention, Qwen35, rope_table
+from .model import Qwen35, rope_table
 from .mtp import MTPHead
 from .sampler import Sampler
 
@@ -319,11 +319,10 @@ class GraphedMTPCycle:
         # the sampler's buffers exist, zero-filled, before any capture: the graphs
         # of run() are captured later on them and replayed without this one
         d.sampler.prepare_accept(k, self.u_buf.device)
-        # so does the RoPE table of the fused decode attention, when it is on
-        if Attention.fused_decode:
-            cfg = d.model.cfg
-            caps = [c.capacity for c in self._kv] + [getattr(d.mtp_cache, "capacity", 0)]
-            rope_table(cfg.rotary_dim, cfg.rope_theta, max(caps), self.u_buf.device)
+        # so does the attention's RoPE table (cos, sin per position), for every cache
+        cfg = d.model.cfg
+        caps = [c.capacity for c in self._kv] + [getattr(d.mtp_cache, "capacity", 0)]
+        rope_table(cfg.rotary_dim, cfg.rope_theta, max(caps), self.u_buf.device)
         # device counters must hold the host values before they become authoritative
         d.cache.counters.sync()
         d.mtp_cache.counters.sync()

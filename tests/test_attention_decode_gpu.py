@@ -94,7 +94,7 @@ def test_attention_decode(L, Hq, Hkv, D, rot, pos0, spare):
     out2 = torch.empty((L, Hq * D), dtype=torch.bfloat16, device=DEV)
     ws2 = workspace(L, Hq, Hkv, D, max_keys, kps)
     _C.call("qvex_attn_qk_rope", _ptr(pt), pt.stride(0), _ptr(qnt), _ptr(knt), _ptr(pos), L, Hq, Hkv, D, rot,
-            theta, eps, _ptr(q2), _ptr(kc2), _ptr(vc2), cap, _stream())
+            theta, eps, _ptr(q2), _ptr(kc2), _ptr(vc2), cap, 0, 0, _stream())
     _C.call("qvex_attention", _ptr(q2), _ptr(kc2), _ptr(vc2), _ptr(pos), L, Hq, Hkv, D, cap, max_keys, max_keys, kps,
             _ptr(pt), pt.stride(0), _ptr(out2), _ptr(ws2), ws2.numel() * 4, _stream())
     torch.cuda.synchronize()
