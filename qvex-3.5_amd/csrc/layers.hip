@@ -957,14 +957,19 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
   if (j == 0) { gm[grp] = m; gl[grp] = l; }
   *reinterpret_cast<float4*>(&part[grp][4 * j]) = o;
   __syncthreads();
-  if (tid < DSL) {
+  if (tid < DSL) {   // wave 0 (DSL <= 64)
     float mx = gm[0];
 #pragma unroll
     for (int q = 1; q < NG; ++q) mx = fmaxf(mx, gm[q]);
+    // group q's factor evaluated once, in lane q, and read back per group
+    // (the same value every lane computed before: one exp per lane, not NG)
+    static_assert(NG <= DSL && DSL <= 64, "lane q of the active lanes holds group q's factor");
+    const float gq = tid < NG ? gm[tid] : -INFINITY;
+    const float fl = gq == -INFINITY ? 0.0f : expf(gq - mx);
     float acc = 0.0f, lt = 0.0f;
 #pragma unroll
     for (int q = 0; q < NG; ++q) {
-      const float f = gm[q] == -INFINITY ? 0.0f : expf(gm[q] - mx);
+      const float f = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fl), q));
       acc = fmaf(part[q][tid], f, acc);
       lt = fmaf(gl[q], f, lt);
     }
