@@ -75,14 +75,26 @@ __device__ __forceinline__ void embed_row_regs(int id, const uint32_t* __restric
                                                u32x4 (&packed)[RMS_MAXC]) {
   const int t = threadIdx.x;
   const int KW = H / 8, G = H / 64;
+  // every chunk's words, scales and biases requested first (chunks past the row
+  // re-read chunk 0, never used), then dequantized: loads used inside their own
+  // chunk's branch would each be waited for there, one round trip per chunk
+  uint32_t wq[RMS_MAXC], sq[RMS_MAXC], bq[RMS_MAXC];
+  if (t < 256) {
+#pragma unroll
+    for (int c = 0; c < RMS_MAXC; ++c) {
+      const int wi = t + 256 * c, wc = wi < KW ? wi : 0;
+      wq[c] = w[(size_t)id * KW + wc];
+      sq[c] = sc[(size_t)id * G + wc / 8];
+      bq[c] = bi[(size_t)id * G + wc / 8];
+    }
+  }
 #pragma unroll
   for (int c = 0; c < RMS_MAXC; ++c) {
     const int wi = t + 256 * c;
     if (t < 256 && wi < KW) {
-      const uint32_t word = w[(size_t)id * KW + wi];
-      const int g = wi / 8;
-      const float s = bf16_to_f32(sc[(size_t)id * G + g]);
-      const float b = bf16_to_f32(bi[(size_t)id * G + g]);
+      const uint32_t word = wq[c];
+      const float s = bf16_to_f32((uint16_t)sq[c]);
+      const float b = bf16_to_f32((uint16_t)bq[c]);
       uint32_t pk[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -179,11 +191,23 @@ __global__ __launch_bounds__(IN_T) void embed_parts_kernel(int32_t* __restrict__
   // rms_parts_kernel's layout: column n on lane n % 16 of a DPP row
   const uint16_t* rb = reinterpret_cast<const uint16_t*>(rowbuf);
   const int tiles = H / 16;
-  for (int n = t; n < H; n += IN_T) {
-    const float hv = bf16_to_f32(rb[n]);
-    const float sq = row16_allsum(hv * hv);
-    u_out[(size_t)row * H + n] = f32_to_bf16(hv * bf16_to_f32(norm_w[n]));
-    if ((n & 15) == 0) parts[(size_t)row * tiles + n / 16] = sq;
+  // the norm weights of this thread's columns requested together, before the loop
+  // (H <= 8192: at most 8 per thread; columns past H re-read column 0, never used)
+  uint16_t nw[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int n = t + IN_T * q;
+    nw[q] = norm_w[n < H ? n : 0];
+  }
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int n = t + IN_T * q;
+    if (n < H) {
+      const float hv = bf16_to_f32(rb[n]);
+      const float sq = row16_allsum(hv * hv);
+      u_out[(size_t)row * H + n] = f32_to_bf16(hv * bf16_to_f32(nw[q]));
+      if ((n & 15) == 0) parts[(size_t)row * tiles + n / 16] = sq;
+    }
   }
 }
 

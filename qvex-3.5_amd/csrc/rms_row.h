@@ -32,6 +32,17 @@ __device__ __forceinline__ void rms_vals256(float (&v)[RMS_MAXC][8], const uint1
                                             uint16_t* __restrict__ outr, int D, float eps, float scale, float* red) {
   const int t = threadIdx.x;
   const bool act = t < 256;
+  // the weight chunks requested before the reduction (chunks past D re-read
+  // chunk 0, never used): loaded where they are used, each chunk would wait
+  // for its own round trip after the barrier
+  u32x4 wq[RMS_MAXC];
+  if (w && act) {
+#pragma unroll
+    for (int c = 0; c < RMS_MAXC; ++c) {
+      const int i = (t + 256 * c) * 8;
+      wq[c] = load16(w + (i < D ? i : 0));
+    }
+  }
   float ss = 0.0f;
 #pragma unroll
   for (int c = 0; c < RMS_MAXC; ++c) {
@@ -53,7 +64,7 @@ __device__ __forceinline__ void rms_vals256(float (&v)[RMS_MAXC][8], const uint1
       float o[8];
       if (w) {
         float wf[8];
-        unpack8(load16(w + i), wf);
+        unpack8(wq[c], wf);
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = wf[e] * (v[c][e] * inv) * scale;
       } else {
@@ -72,14 +83,26 @@ __device__ __forceinline__ void rms_row256(const uint16_t* __restrict__ xr, cons
   const int t = threadIdx.x;
   const bool act = t < 256;
   float v[RMS_MAXC][8];
+  // every chunk's loads first (chunks past D re-read chunk 0, never used), then
+  // the arithmetic: a load used inside its own chunk's branch is waited for
+  // there, one round trip per chunk
+  u32x4 xq[RMS_MAXC], dq[RMS_MAXC];
+  if (act) {
+#pragma unroll
+    for (int c = 0; c < RMS_MAXC; ++c) {
+      const int i = (t + 256 * c) * 8, ic = i < D ? i : 0;
+      xq[c] = load16(xr + ic);
+      if constexpr (ADD) dq[c] = load16(dr + ic);
+    }
+  }
 #pragma unroll
   for (int c = 0; c < RMS_MAXC; ++c) {
     const int i = (t + 256 * c) * 8;
     if (act && i < D) {
-      unpack8(load16(xr + i), v[c]);
+      unpack8(xq[c], v[c]);
       if constexpr (ADD) {
         float d[8];
-        unpack8(load16(dr + i), d);
+        unpack8(dq[c], d);
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[c][e] = bf16_to_f32(f32_to_bf16(v[c][e] + d[e]));
         *reinterpret_cast<u32x4*>(hr + i) = pack8(v[c]);
