@@ -413,7 +413,11 @@ __global__ __launch_bounds__(pk_block(WS)) __attribute__((amdgpu_waves_per_eu(pk
     // request makes its wait counts cover both paths, so that the wait for the
     // current set also waits for the next); the last one or two sets are
     // computed after it. Buffer 0 holds set j at the top of the loop.
-    if (nws > 0) issue(0, set_of(0));
+    // unconditional (a wave without sets re-reads the last one, never used), so
+    // that the folded norm's wait below counts only its own, earlier loads: a
+    // conditional request made it wait for this set as well, before the next
+    // set was requested
+    issue(0, nws > 0 ? set_of(0) : GS - 1);
     seg_table();
     if (rs && ws == 0) compute_rstd();
     int j = 0;
